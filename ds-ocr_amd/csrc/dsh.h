@@ -1,0 +1,144 @@
+// dsh.h — device helpers shared by the gfx950 kernels of the ds-ocr INT8 MoE decode path.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define DSH_WAVE 64
+
+// ---------------------------------------------------------------- scalar semantics
+
+__device__ __forceinline__ float dsh_bf16_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
+__device__ __forceinline__ float dsh_bf16lo(uint32_t packed) { return __uint_as_float(packed << 16); }
+__device__ __forceinline__ float dsh_bf16hi(uint32_t packed) { return __uint_as_float(packed & 0xFFFF0000u); }
+
+// Schraudolph fast exp of ds_kernels.h:296-302, as the reference build evaluates it: the affine map
+// is one fused multiply-add (GCC contracts 12102203*x + 1064866805), the float->uint32 conversion
+// goes through a signed integer (the scalar x86 code), so a negative result wraps instead of
+// saturating. The fmaf here is an explicit fused op, independent of contraction flags.
+__device__ __forceinline__ float dsh_fast_expf(float x) {
+  if (x < -88.0f) return 0.0f;
+  if (x > 88.0f) return 1e38f;
+  float v = __builtin_fmaf(12102203.0f, x, 1064866805.0f);
+  uint32_t i = (v != v) ? 0u : (uint32_t)(int32_t)v;
+  return __uint_as_float(i);
+}
+
+// ds_swiglu_direct element (ds_kernels.c:1771): (g / (1 + fe(-g))) * u. Division is IEEE
+// correctly rounded (hipcc default), matching the x86 divss.
+__device__ __forceinline__ float dsh_swiglu(float g, float u) { return (g / (1.0f + dsh_fast_expf(-g))) * u; }
+
+// ds_bf16_truncate_array element (ds_kernels.c:2484-2490): round-half-up on the bit pattern.
+__device__ __forceinline__ float dsh_bf16_round_half_up(float f) {
+  return __uint_as_float((__float_as_uint(f) + 0x8000u) & 0xFFFF0000u);
+}
+
+// ---------------------------------------------------------------- wave helpers
+
+template <int CTRL>
+__device__ __forceinline__ float dsh_dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each aligned group of 16 lanes (one DPP row); every lane of the row gets the sum.
+__device__ __forceinline__ float dsh_row16_sum(float v) {
+  v += dsh_dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dsh_dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dsh_dpp<0x141>(v);  // row_half_mirror
+  v += dsh_dpp<0x140>(v);  // row_mirror
+  return v;
+}
+
+// Sum over each aligned group of 8 lanes; every lane of the group gets the sum.
+__device__ __forceinline__ float dsh_row8_sum(float v) {
+  v += dsh_dpp<0xB1>(v);
+  v += dsh_dpp<0x4E>(v);
+  v += dsh_dpp<0x141>(v);
+  return v;
+}
+
+// Sum over each aligned group of 4 lanes.
+__device__ __forceinline__ float dsh_row4_sum(float v) {
+  v += dsh_dpp<0xB1>(v);
+  v += dsh_dpp<0x4E>(v);
+  return v;
+}
+
+__device__ __forceinline__ float dsh_wave_sum(float v) {
+  v = dsh_row16_sum(v);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+__device__ __forceinline__ float dsh_wave_max(float v) {
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// ---------------------------------------------------------------- INT8 code helpers
+
+// Stored codes are int8 q = u - 128 (ds_quantize.c:45); as bytes that is u ^ 0x80, so one XOR per
+// dword recovers u and one conversion per byte (v_cvt_f32_ubyteN) gives it exactly as a float.
+__device__ __forceinline__ void dsh_u8x4_to_f32(uint32_t w, float &a, float &b, float &c, float &d) {
+  uint32_t u = w ^ 0x80808080u;
+  a = (float)(u & 0xFFu);  // selected as v_cvt_f32_ubyte0..3
+  b = (float)((u >> 8) & 0xFFu);
+  c = (float)((u >> 16) & 0xFFu);
+  d = (float)(u >> 24);
+}
+
+// dot += Σ u_j * x_j over 16 codes in one 128-bit word.
+__device__ __forceinline__ float dsh_dot16_u8(u32x4 w, const float *x, float acc) {
+#pragma unroll
+  for (int d = 0; d < 4; d++) {
+    float a, b, c, e;
+    dsh_u8x4_to_f32(w[d], a, b, c, e);
+    acc = __builtin_fmaf(a, x[4 * d + 0], acc);
+    acc = __builtin_fmaf(b, x[4 * d + 1], acc);
+    acc = __builtin_fmaf(c, x[4 * d + 2], acc);
+    acc = __builtin_fmaf(e, x[4 * d + 3], acc);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ u32x4 dsh_load_nt(const void *p) {
+  return __builtin_nontemporal_load((const u32x4 *)p);
+}
+
+__device__ __forceinline__ f32x4 dsh_load_f4(const float *p) { return *(const f32x4 *)p; }
+
+// ---------------------------------------------------------------- argmax key
+
+// Orderable key for (value, index): larger value wins, then smaller index. Only values strictly
+// greater than -1e30 and not NaN can win (ds_kernels_avx.c:159-160 initial best_val = -1e30 with
+// strict '>'); key 0 means "no candidate". -0 and +0 compare equal in the reference, so both map
+// to the +0 key and the index decides.
+__device__ __forceinline__ unsigned long long dsh_argmax_key(float v, int idx) {
+  if (!(v > -1e30f)) return 0ull;
+  uint32_t u = __float_as_uint(v);
+  if ((u << 1) == 0u) u = 0u;
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
+}
+__device__ __forceinline__ int dsh_key_index(unsigned long long k) {
+  return k == 0ull ? 0 : (int)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
+}
+__device__ __forceinline__ float dsh_key_value(unsigned long long k) {
+  if (k == 0ull) return -1e30f;
+  uint32_t u = (uint32_t)(k >> 32);
+  u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
+  return __uint_as_float(u);
+}
+__device__ __forceinline__ unsigned long long dsh_umax64(unsigned long long a, unsigned long long b) {
+  return a > b ? a : b;
+}
+__device__ __forceinline__ unsigned long long dsh_wave_max_u64(unsigned long long v) {
+  for (int o = 32; o >= 1; o >>= 1) {
+    unsigned long long w = __shfl_xor(v, o);
+    v = dsh_umax64(v, w);
+  }
+  return v;
+}

@@ -1,0 +1,96 @@
+// k_core.h — launcher entry points of the gfx950 kernels (C linkage, device pointers, one stream).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define DSH_ROUTE_DECODE 0 /* bf16 router, fast-exp softmax over all experts, top-k, no renorm */
+#define DSH_ROUTE_CFG 1    /* f32 router, top-k on raw scores, expf softmax over the k (renorm) */
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+hipError_t dsh_launch_quantize_bf16(const uint16_t *W, int8_t *q, float *scale, float *offset, int out_dim, int in_dim,
+                                    hipStream_t s);
+hipError_t dsh_launch_quantize_f32(const float *W, int8_t *q, float *scale, float *offset, int out_dim, int in_dim,
+                                   hipStream_t s);
+/* Quantizes into a code array and an interleaved (scale, offset) array. */
+hipError_t dsh_launch_quantize_bf16_so(const uint16_t *W, int8_t *q, float *so, int out_dim, int in_dim, hipStream_t s);
+/* work: >= 2*1024 + 2 doubles; work[0] = Σ(w-deq)^2, work[1] = Σw^2. */
+hipError_t dsh_launch_quant_rms(const int8_t *q, const float *scale, const float *offset, const uint16_t *W,
+                                int out_dim, int in_dim, double *work, hipStream_t s);
+hipError_t dsh_launch_gemm_bf16w(const float *X, const uint16_t *W, float *Y, int M, int K, int N, hipStream_t s);
+hipError_t dsh_launch_fill_normal_bf16(uint16_t *dst, size_t n, uint64_t seed, float std_, hipStream_t s);
+hipError_t dsh_launch_fill_normal_f32(float *dst, size_t n, uint64_t seed, float mean, float std_, hipStream_t s);
+hipError_t dsh_launch_dequantize(const int8_t *q, const float *scale, const float *offset, float *out, int out_dim,
+                                 int in_dim, hipStream_t s);
+hipError_t dsh_launch_int8_matvec(const int8_t *q, const float *scale, const float *offset, const float *x, float *y,
+                                  int in_dim, int row_start, int nrows, hipStream_t s);
+hipError_t dsh_launch_swiglu(float *out, const float *g, const float *u, size_t n, hipStream_t s);
+hipError_t dsh_launch_bf16_trunc(float *a, size_t n, hipStream_t s);
+hipError_t dsh_launch_vec_add(float *dst, const float *a, const float *b, int n, hipStream_t s);
+hipError_t dsh_launch_expert_combine(float *out, const float *eo, const float *w, int top_k, int hidden,
+                                     hipStream_t s);
+hipError_t dsh_launch_split_swiglu(float *h, const float *gu, int inter, int bf16sim, hipStream_t s);
+hipError_t dsh_launch_bf16_matvec_avx(const uint16_t *W, const float *x, const float *bias, float *y, int in_dim,
+                                      int out_dim, int nthreads, hipStream_t s);
+int dsh_argmax_avx_blocks(int out_dim);
+hipError_t dsh_launch_argmax_avx(const uint16_t *W, const float *x, unsigned long long *cand, float *logits,
+                                 int in_dim, int out_dim, int nthreads, int *out_idx, float *out_val, hipStream_t s);
+hipError_t dsh_launch_argmax_avx_partial(const uint16_t *W, const float *x, unsigned long long *cand, float *logits,
+                                         int in_dim, int out_dim, int chunk, hipStream_t s);
+/* lg, lg2: [out_dim] scratch; excl: device ids. */
+hipError_t dsh_launch_argmax_excluding(const uint16_t *W, const float *x, unsigned long long *cand, float *lg,
+                                       float *lg2, int in_dim, int out_dim, int nthreads, const int *excl, int n_excl,
+                                       int *out_idx, hipStream_t s);
+hipError_t dsh_launch_bf16_dot_row(const uint16_t *W, const float *x, int in_dim, int row, float *out, hipStream_t s);
+hipError_t dsh_launch_linear_f32_exact(const float *W, const float *x, float *y, int in_dim, int out_dim,
+                                       hipStream_t s);
+hipError_t dsh_launch_topk(const float *scores, int n, int k, int mode, int *idx, float *w, hipStream_t s);
+
+/* ---- decode MoE layer (k_moe.hip) ---- */
+typedef struct {
+  const int8_t *gu_q;   /* [E][2I][H] routed gate_up codes (gate rows, then up rows, per expert) */
+  const float *gu_so;   /* [E][2I] (scale, offset) */
+  const int8_t *dn_q;   /* [E][H][I] routed down codes */
+  const float *dn_so;   /* [E][H] */
+  const int8_t *sgu_q;  /* [2SI][H] shared gate_up */
+  const float *sgu_so;  /* [2SI] */
+  const int8_t *sdn_q;  /* [H][SI] shared down */
+  const float *sdn_so;  /* [H] */
+  const float *router_f32;     /* [E][H] */
+  const uint16_t *router_bf16; /* [E][H] */
+  int H, I, E, K, SI;
+} dsh_layer_t;
+
+/* Work buffers of one decode layer. */
+typedef struct {
+  float *scores; /* [E] router scores */
+  int *idx;      /* [K] selected experts */
+  float *w;      /* [K] routing weights */
+  float *h;      /* [K*I + SI] SwiGLU outputs (routed slots, then shared) */
+} dsh_layer_work_t;
+
+/* Shapes the fused decode kernels support (otherwise the per-op path is used). */
+int dsh_moe_fast_shape(int H, int I, int E, int K, int SI);
+
+/* x_in + step_stride * (*step) is the layer input when step != NULL (device step counter). */
+hipError_t dsh_launch_moe_scores(const dsh_layer_t *L, const float *x_in, const int *step, int step_stride,
+                                 int route_mode, int nthreads, float *scores, hipStream_t s);
+hipError_t dsh_launch_moe_gate_up(const dsh_layer_t *L, const float *x_in, const int *step, int step_stride,
+                                  int route_mode, int bf16sim, const dsh_layer_work_t *wk, hipStream_t s);
+/* x_out = (residual ? x_in : 0) + MoE(x_in). x_out may alias x_in. */
+hipError_t dsh_launch_moe_down(const dsh_layer_t *L, const float *x_in, const int *step, int step_stride,
+                               float *x_out, int residual, int bf16sim, const dsh_layer_work_t *wk, hipStream_t s);
+
+/* LM-head argmax: per-block (max, lowest index) candidates, then a final reduction that writes
+ * tokens[*step] (tokens[0] when step is NULL) and advances *step. The fast partial kernel needs
+ * in_dim % 32 == 0, 16-byte aligned rows, and every row in the 2-accumulator order. */
+int dsh_lm_argmax_blocks(int vocab);
+hipError_t dsh_launch_lm_argmax_partial(const uint16_t *W, const float *x, int in_dim, int vocab,
+                                        unsigned long long *cand, hipStream_t s);
+hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int *tokens, int *step, hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,798 @@
+// k_core.hip — gfx950 kernels behind the per-function C API of ds_quantize.h / ds_kernels.h.
+//
+// Each kernel states the reference arithmetic it reproduces (reference = vislee/ds-ocr C sources).
+// Bit-exact kernels reproduce the reference's operation order; the others keep its formula and are
+// held to 1e-3 relative error.
+#include "dsh.h"
+#include "k_core.h"
+#include "dsh_avx.h"
+
+// ============================================================================ quantizer
+// ds_quantize.c:29-47 (int8_quantize_row) per row, one wave per row.
+// min/max keep the reference's first-occurrence semantics under '<' / '>' (so -0 vs +0 ties resolve
+// to the lowest column, NaN never enters); scale = (max-min)/255 clamped to 1e-10, inv = 1/scale,
+// code = clamp(roundf((w-min)*inv), 0, 255) - 128 with roundf = half away from zero.
+
+struct MinMax {
+  float mn, mx;
+  int imn, imx;
+};
+
+__device__ __forceinline__ void mm_take(MinMax &m, float v, int c) {
+  if (v < m.mn) { m.mn = v; m.imn = c; }
+  if (v > m.mx) { m.mx = v; m.imx = c; }
+}
+
+__device__ __forceinline__ void mm_merge(MinMax &a, float omn, int oimn, float omx, int oimx) {
+  if (omn < a.mn || (omn == a.mn && oimn < a.imn)) { a.mn = omn; a.imn = oimn; }
+  if (omx > a.mx || (omx == a.mx && oimx < a.imx)) { a.mx = omx; a.imx = oimx; }
+}
+
+__device__ __forceinline__ int8_t quant_code(float v, float mn, float inv) {
+  float r = roundf((v - mn) * inv);
+  int t = (r != r) ? 0 : (int)fminf(fmaxf(r, -1.0f), 256.0f);
+  t = t < 0 ? 0 : (t > 255 ? 255 : t);
+  return (int8_t)(t - 128);
+}
+
+template <typename T>
+__device__ __forceinline__ float load_w(const T *p, size_t i);
+template <>
+__device__ __forceinline__ float load_w<uint16_t>(const uint16_t *p, size_t i) { return dsh_bf16_to_f32(p[i]); }
+template <>
+__device__ __forceinline__ float load_w<float>(const float *p, size_t i) { return p[i]; }
+
+template <typename T>
+__global__ void __launch_bounds__(256) k_quantize_rows(const T *__restrict__ W, int8_t *__restrict__ q,
+                                                       float *__restrict__ scale, float *__restrict__ offset,
+                                                       int so_stride, int out_dim, int in_dim) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= out_dim) return;
+  const T *w = W + (size_t)row * in_dim;
+  MinMax m{1e30f, -1e30f, 0x7FFFFFFF, 0x7FFFFFFF};
+  for (int c = lane; c < in_dim; c += 64) mm_take(m, load_w(w, c), c);
+  for (int o = 32; o >= 1; o >>= 1) {
+    float omn = __shfl_xor(m.mn, o), omx = __shfl_xor(m.mx, o);
+    int oimn = __shfl_xor(m.imn, o), oimx = __shfl_xor(m.imx, o);
+    mm_merge(m, omn, oimn, omx, oimx);
+  }
+  float range = m.mx - m.mn;
+  float sc = range / 255.0f;
+  if (sc < 1e-10f) sc = 1e-10f;
+  float inv = 1.0f / sc;
+  if (lane == 0) {
+    scale[(size_t)row * so_stride] = sc;
+    offset[(size_t)row * so_stride] = m.mn;
+  }
+  int8_t *qr = q + (size_t)row * in_dim;
+  for (int c = lane; c < in_dim; c += 64) qr[c] = quant_code(load_w(w, c), m.mn, inv);
+}
+
+// ds_quantize.c:115-125: out = scale*(q+128) + off, contracted by GCC to one fused multiply-add.
+__global__ void k_dequantize(const int8_t *__restrict__ q, const float *__restrict__ scale,
+                             const float *__restrict__ offset, float *__restrict__ out, int out_dim, int in_dim) {
+  size_t n = (size_t)out_dim * in_dim;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    int r = (int)(i / in_dim);
+    out[i] = __builtin_fmaf(scale[r], (float)((int)q[i] + 128), offset[r]);
+  }
+}
+
+// ============================================================================ INT8 matvec
+// y[r - row_start] = scale*Σ(q+128)x + off*Σx (ds_quantize.c:154-170), epilogue fma(scale, dot, off*xs)
+// as the reference build evaluates it. Summation order is the GPU's (16-byte chunks, DPP tree).
+// LPR lanes per row, each lane walks 16-byte chunks ch = sub, sub+LPR, ...
+template <int LPR>
+__global__ void __launch_bounds__(256) k_int8_matvec16(const int8_t *__restrict__ q, const float *__restrict__ scale,
+                                                       const float *__restrict__ offset, const float *__restrict__ x,
+                                                       float *__restrict__ y, int in_dim, int row_start, int nrows) {
+  constexpr int RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63;
+  const int sub = lane % LPR;
+  const int rr = blockIdx.x * (4 * RPW) + (threadIdx.x >> 6) * RPW + lane / LPR;
+  const bool active = rr < nrows;
+  const int r = row_start + (active ? rr : 0);
+  const int C = in_dim >> 4;
+  const int8_t *qr = q + (size_t)r * in_dim;
+  float dot = 0.0f, xs = 0.0f;
+  if (active) {
+    for (int ch = sub; ch < C; ch += LPR) {
+      u32x4 w = dsh_load_nt(qr + 16 * ch);
+      float xv[16];
+#pragma unroll
+      for (int d = 0; d < 4; d++) {
+        f32x4 t = dsh_load_f4(x + 16 * ch + 4 * d);
+        xv[4 * d] = t[0];
+        xv[4 * d + 1] = t[1];
+        xv[4 * d + 2] = t[2];
+        xv[4 * d + 3] = t[3];
+      }
+      dot = dsh_dot16_u8(w, xv, dot);
+      float s = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 16; k++) s += xv[k];
+      xs += s;
+    }
+  }
+  if (LPR == 16) {
+    dot = dsh_row16_sum(dot);
+    xs = dsh_row16_sum(xs);
+  } else if (LPR == 8) {
+    dot = dsh_row8_sum(dot);
+    xs = dsh_row8_sum(xs);
+  } else if (LPR == 4) {
+    dot = dsh_row4_sum(dot);
+    xs = dsh_row4_sum(xs);
+  }
+  if (active && sub == 0) y[rr] = __builtin_fmaf(scale[r], dot, offset[r] * xs);
+}
+
+// Any in_dim: one wave per row, byte loads.
+__global__ void __launch_bounds__(256) k_int8_matvec_any(const int8_t *__restrict__ q, const float *__restrict__ scale,
+                                                         const float *__restrict__ offset, const float *__restrict__ x,
+                                                         float *__restrict__ y, int in_dim, int row_start, int nrows) {
+  const int lane = threadIdx.x & 63;
+  const int rr = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (rr >= nrows) return;
+  const int r = row_start + rr;
+  const int8_t *qr = q + (size_t)r * in_dim;
+  float dot = 0.0f, xs = 0.0f;
+  for (int c = lane; c < in_dim; c += 64) {
+    float xv = x[c];
+    dot = __builtin_fmaf((float)((int)qr[c] + 128), xv, dot);
+    xs += xv;
+  }
+  dot = dsh_wave_sum(dot);
+  xs = dsh_wave_sum(xs);
+  if (lane == 0) y[rr] = __builtin_fmaf(scale[r], dot, offset[r] * xs);
+}
+
+// ============================================================================ elementwise
+// ds_swiglu_direct (ds_kernels.c:1739-1789), fast-exp branch, for seq rows of inter.
+__global__ void k_swiglu(float *__restrict__ out, const float *__restrict__ g, const float *__restrict__ u, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    out[i] = dsh_swiglu(g[i], u[i]);
+}
+
+__global__ void k_bf16_trunc(float *__restrict__ a, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    a[i] = dsh_bf16_round_half_up(a[i]);
+}
+
+__global__ void k_vec_add(float *__restrict__ dst, const float *__restrict__ a, const float *__restrict__ b, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) dst[i] = a[i] + b[i];
+}
+
+// ds_expert_combine (ds_kernels.c:359-371): out = 0; out[i] = fma(w_k, e_k[i], out[i]) for k in order.
+__global__ void k_expert_combine(float *__restrict__ out, const float *__restrict__ eo, const float *__restrict__ w,
+                                 int top_k, int hidden) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x) {
+    float acc = 0.0f;
+    for (int k = 0; k < top_k; k++) acc = __builtin_fmaf(w[k], eo[(size_t)k * hidden + i], acc);
+    out[i] = acc;
+  }
+}
+
+// Split of a fused [2*inter] gate_up vector + optional truncation + SwiGLU (ds_quantize.c:308-318).
+__global__ void k_split_swiglu(float *__restrict__ h, const float *__restrict__ gu, int inter, int bf16sim) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < inter; i += gridDim.x * blockDim.x) {
+    float g = gu[i], u = gu[inter + i];
+    if (bf16sim) {
+      g = dsh_bf16_round_half_up(g);
+      u = dsh_bf16_round_half_up(u);
+    }
+    float v = dsh_swiglu(g, u);
+    h[i] = bf16sim ? dsh_bf16_round_half_up(v) : v;
+  }
+}
+
+// Stages x (in_dim floats) into LDS.
+__device__ __forceinline__ void stage_x(float *xs, const float *x, int in_dim) {
+  for (int i = threadIdx.x; i < in_dim; i += blockDim.x) xs[i] = x[i];
+  __syncthreads();
+}
+
+// y = W x for rows [0, out_dim), 64 rows per 256-thread block.
+template <bool ALIGNED>
+__global__ void __launch_bounds__(256) k_bf16_matvec_avx(const uint16_t *__restrict__ W, const float *__restrict__ x,
+                                                         const float *__restrict__ bias, float *__restrict__ y,
+                                                         int in_dim, int out_dim, int chunk) {
+  extern __shared__ float xs_lds[];
+  stage_x(xs_lds, x, in_dim);
+  const int L = threadIdx.x & 3;
+  const int r = blockIdx.x * 64 + (threadIdx.x >> 2);
+  if (r >= out_dim) return;  // whole 4-lane groups exit together
+  int path = row_path(r, out_dim, chunk, false);
+  float v = avx_row<ALIGNED>(W + (size_t)r * in_dim, xs_lds, in_dim, L, path == DSH_ROW_SINGLE, true,
+                             bias ? bias[r] : 0.0f, path != DSH_ROW_GROUP4);
+  if (L == 0) y[r] = v;
+}
+
+// Per-row logits in argmax order plus per-block (max, lowest index) candidates.
+template <bool ALIGNED>
+__global__ void __launch_bounds__(256) k_argmax_avx(const uint16_t *__restrict__ W, const float *__restrict__ x,
+                                                    unsigned long long *__restrict__ cand, float *__restrict__ logits,
+                                                    int in_dim, int out_dim, int chunk) {
+  extern __shared__ float xs_lds[];
+  __shared__ unsigned long long wbest[4];
+  stage_x(xs_lds, x, in_dim);
+  const int L = threadIdx.x & 3;
+  const int r = blockIdx.x * 64 + (threadIdx.x >> 2);
+  unsigned long long key = 0ull;
+  if (r < out_dim) {
+    bool single = row_path(r, out_dim, chunk, true) == DSH_ROW_SINGLE;
+    float v = avx_row<ALIGNED>(W + (size_t)r * in_dim, xs_lds, in_dim, L, single, false, 0.0f, true);
+    if (L == 0) {
+      key = dsh_argmax_key(v, r);
+      if (logits) logits[r] = v;
+    }
+  }
+  key = dsh_wave_max_u64(key);
+  if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = key;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long b = wbest[0];
+    for (int i = 1; i < 4; i++) b = dsh_umax64(b, wbest[i]);
+    cand[blockIdx.x] = b;
+  }
+}
+
+// Reduces n candidate keys to one index (and value).
+__global__ void __launch_bounds__(256) k_argmax_final(const unsigned long long *__restrict__ cand, int n,
+                                                      int *__restrict__ out_idx, float *__restrict__ out_val) {
+  __shared__ unsigned long long wbest[4];
+  unsigned long long b = 0ull;
+  for (int i = threadIdx.x; i < n; i += 256) b = dsh_umax64(b, cand[i]);
+  b = dsh_wave_max_u64(b);
+  if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = b;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < 4; i++) wbest[0] = dsh_umax64(wbest[0], wbest[i]);
+    *out_idx = dsh_key_index(wbest[0]);
+    if (out_val) *out_val = dsh_key_value(wbest[0]);
+  }
+}
+
+// ds_bf16_dot_row non-NEON branch (ds_kernels.c:1000-1008): one sequential fused chain.
+__global__ void k_bf16_dot_row(const uint16_t *__restrict__ W, const float *__restrict__ x, int in_dim, int row,
+                               float *__restrict__ out) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  const uint16_t *w = W + (size_t)row * in_dim;
+  float s = 0.0f;
+  for (int k = 0; k < in_dim; k++) s = __builtin_fmaf(dsh_bf16_to_f32(w[k]), x[k], s);
+  *out = s;
+}
+
+// ============================================================================ f32 linear (router)
+// ds_linear without BLAS, seq = 1 (ds_kernels.c:639-652) as GCC 11 -O3 compiles it for AVX-512:
+// rounded products of the leading multiple of 16 (and then of 8) added in index order, fused tail.
+// One lane per output row; bit-exact with that build.
+__global__ void k_linear_f32_exact(const float *__restrict__ W, const float *__restrict__ x, float *__restrict__ y,
+                                   int in_dim, int out_dim) {
+  int o = blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= out_dim) return;
+  const float *w = W + (size_t)o * in_dim;
+  float s = 0.0f;
+  int i = 0;
+  if (in_dim >= 16) {
+    int m = in_dim & ~15;
+    for (; i < m; i++) s = __fadd_rn(s, __fmul_rn(x[i], w[i]));
+  }
+  if (in_dim - i >= 8) {
+    int m = i + 8;
+    for (; i < m; i++) s = __fadd_rn(s, __fmul_rn(x[i], w[i]));
+  }
+  for (; i < in_dim; i++) s = __builtin_fmaf(x[i], w[i], s);
+  y[o] = s;
+}
+
+// ============================================================================ top-k
+// Wave-level routing helpers. All per-expert state lives in lanes (lane e = expert e, n <= 64);
+// the selections of round t live in lane t. Sequential sums use readlane in index order so they
+// round exactly like the reference's loops.
+
+// ds_moe_top_k (ds_kernels.c:193-243): selection on raw scores (strict '>', lowest index on ties,
+// -1e30 floor), then expf softmax over the selected k (renormalised).
+__device__ void topk_cfg_wave(const float *scores, int n, int k, int *idx, float *w) {
+  const int lane = threadIdx.x & 63;
+  float s = lane < n ? scores[lane] : 0.0f;
+  bool taken = false;
+  int my_sel = 0;
+  float my_ss = 0.0f;
+  int ns = 0;
+  for (int t = 0; t < k; t++) {
+    unsigned long long key = (lane < n && !taken) ? dsh_argmax_key(s, lane) : 0ull;
+    key = dsh_wave_max_u64(key);
+    if (key == 0ull) continue;  // nothing strictly above -1e30 left
+    int e = dsh_key_index(key);
+    if (lane == e) taken = true;
+    if (lane == ns) {
+      my_sel = e;
+      my_ss = dsh_key_value(key);
+    }
+    ns++;
+  }
+  float mx = -1e30f;
+  for (int j = 0; j < ns; j++) {
+    float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_ss), j));
+    if (v > mx) mx = v;
+  }
+  float ev = lane < ns ? expf(my_ss - mx) : 0.0f;
+  float sum = 0.0f;
+  for (int j = 0; j < ns; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j));
+  float inv = 1.0f / sum;
+  if (lane < k) {
+    idx[lane] = lane < ns ? my_sel : 0;
+    w[lane] = lane < ns ? ev * inv : 0.0f;
+  }
+}
+
+// moe_forward inline routing (ds_moe_decoder.c:157-183): fast-exp softmax over all n experts
+// (max, sequential sum, one reciprocal), then top-k of the probabilities with strict '>' and the
+// lowest index on ties; weights are the probabilities (no renormalisation). idx = -1 when no
+// probability exceeds -1e30 (all-NaN input).
+__device__ void topk_decode_wave(const float *scores, int n, int k, int *idx, float *w) {
+  const int lane = threadIdx.x & 63;
+  float s = lane < n ? scores[lane] : 0.0f;
+  // max with '>' from -1e30: NaN never wins; equals the max over non-NaN values floored at -1e30.
+  float m = (lane < n && s > -1e30f) ? s : -1e30f;
+  m = dsh_wave_max(m);
+  float p = lane < n ? dsh_fast_expf(s - m) : 0.0f;
+  float sum = 0.0f;
+  for (int e = 0; e < n; e++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), e));
+  float inv = 1.0f / sum;
+  p = p * inv;
+  bool taken = false;
+  int my_sel = -1;
+  float my_w = -1e30f;
+  for (int t = 0; t < k; t++) {
+    unsigned long long key = (lane < n && !taken) ? dsh_argmax_key(p, lane) : 0ull;
+    key = dsh_wave_max_u64(key);
+    int e = key == 0ull ? -1 : dsh_key_index(key);
+    if (lane == e) taken = true;
+    if (lane == t) {
+      my_sel = e;
+      my_w = key == 0ull ? -1e30f : dsh_key_value(key);
+    }
+  }
+  if (lane < k) {
+    idx[lane] = my_sel;
+    w[lane] = my_w;
+  }
+}
+
+__global__ void __launch_bounds__(64) k_topk(const float *__restrict__ scores, int n, int k, int mode,
+                                             int *__restrict__ idx, float *__restrict__ w) {
+  if (mode == DSH_ROUTE_CFG)
+    topk_cfg_wave(scores, n, k, idx, w);
+  else
+    topk_decode_wave(scores, n, k, idx, w);
+}
+
+// ============================================================================ argmax with exclusions
+// ds_argmax_matvec_bf16_excluding (ds_kernels.c:1020-1099) on precomputed logits. lg: logits in the
+// order of the reference's own chunking (one chunk for 1 thread, ceil(n/T) rows otherwise); lg2
+// (single-thread branch only): logits in the order of the 8192-row rescan.
+#define EXCL_MAX_CHUNKS 1024
+
+__device__ bool excl_has(const int *excl, int n, int id) {
+  for (int i = 0; i < n; i++)
+    if (excl[i] == id) return true;
+  return false;
+}
+
+// Per-chunk argmax as ds_argmax_bf16_range_avx returns it: (best, val) with best = start and
+// val = -1e30 when no logit exceeds -1e30. Block-wide; result valid in every thread.
+__device__ void chunk_best(const float *lg, int s, int e, int *idx, float *val, unsigned long long *wb) {
+  unsigned long long k = 0ull;
+  for (int r = s + (int)threadIdx.x; r < e; r += 256) k = dsh_umax64(k, dsh_argmax_key(lg[r], r));
+  k = dsh_wave_max_u64(k);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) wb[threadIdx.x >> 6] = k;
+  __syncthreads();
+  k = dsh_umax64(dsh_umax64(wb[0], wb[1]), dsh_umax64(wb[2], wb[3]));
+  *idx = k == 0ull ? s : dsh_key_index(k);
+  *val = dsh_key_value(k);
+}
+
+__global__ void __launch_bounds__(256) k_argmax_excl_select(const float *__restrict__ lg, const float *__restrict__ lg2,
+                                                            int out_dim, int nthreads, const int *__restrict__ excl,
+                                                            int n_excl, int *__restrict__ out) {
+  __shared__ unsigned long long wb[4];
+  __shared__ int cb[EXCL_MAX_CHUNKS];
+  __shared__ float cv[EXCL_MAX_CHUNKS];
+  const int T = nthreads > 1 ? nthreads : 1;
+  const int chunk = dsh_chunk_len(out_dim, nthreads);
+  for (int t = 0; t < T; t++) {
+    int s = t * chunk, e = min(s + chunk, out_dim);
+    int bi;
+    float bv;
+    if (s < e) {
+      chunk_best(lg, s, e, &bi, &bv, wb);
+    } else {
+      bi = 0;
+      bv = -1e30f;
+    }
+    if (threadIdx.x == 0) {
+      cb[t] = bi;
+      cv[t] = bv;
+    }
+  }
+  int nres = 0;
+  if (T == 1) {
+    nres = (out_dim + 8191) / 8192;
+    for (int c = 0; c < nres; c++) {
+      int s = c * 8192, e = min(s + 8192, out_dim);
+      int bi;
+      float bv;
+      chunk_best(lg2, s, e, &bi, &bv, wb);
+      if (threadIdx.x == 0) {
+        cb[T + c] = bi;
+        cv[T + c] = bv;
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  int best = cb[0];
+  float best_val = cv[0];
+  for (int t = 1; t < T; t++)
+    if (cv[t] > best_val) {
+      best_val = cv[t];
+      best = cb[t];
+    }
+  int result = best;
+  if (excl_has(excl, n_excl, best)) {
+    if (T == 1) {
+      int sb = 0;
+      float sv = -1e30f;
+      for (int c = 0; c < nres; c++) {
+        if (excl_has(excl, n_excl, cb[1 + c])) continue;
+        if (cv[1 + c] > sv) {
+          sv = cv[1 + c];
+          sb = cb[1 + c];
+        }
+      }
+      result = sb;
+    } else {
+      bool found = false;
+      int sb = -1;
+      float sv = -1e30f;
+      for (int t = 0; t < T; t++) {
+        if (excl_has(excl, n_excl, cb[t])) continue;
+        if (!found || cv[t] > sv) {
+          sv = cv[t];
+          sb = cb[t];
+          found = true;
+        }
+      }
+      if (found) result = sb;
+    }
+  }
+  *out = result;
+}
+
+// ============================================================================ quantization RMS
+// ds_quantize.c:127-144: Σ(w - deq)^2 and Σ w^2 accumulated in double (deq as ds_int4_dequantize_f32).
+__global__ void __launch_bounds__(256) k_quant_rms(const int8_t *__restrict__ q, const float *__restrict__ scale,
+                                                   const float *__restrict__ offset, const uint16_t *__restrict__ W,
+                                                   int out_dim, int in_dim, double *__restrict__ partial) {
+  __shared__ double sa[256], sb[256];
+  size_t n = (size_t)out_dim * in_dim;
+  double a = 0.0, b = 0.0;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    int r = (int)(i / in_dim);
+    float deq = __builtin_fmaf(scale[r], (float)((int)q[i] + 128), offset[r]);
+    float orig = dsh_bf16_to_f32(W[i]);
+    float d = orig - deq;
+    a += (double)(d * d);
+    b += (double)(orig * orig);
+  }
+  sa[threadIdx.x] = a;
+  sb[threadIdx.x] = b;
+  __syncthreads();
+  for (int o = 128; o >= 1; o >>= 1) {
+    if (threadIdx.x < o) {
+      sa[threadIdx.x] += sa[threadIdx.x + o];
+      sb[threadIdx.x] += sb[threadIdx.x + o];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    partial[2 * blockIdx.x] = sa[0];
+    partial[2 * blockIdx.x + 1] = sb[0];
+  }
+}
+
+__global__ void __launch_bounds__(256) k_sum_pairs_f64(const double *__restrict__ partial, int n,
+                                                       double *__restrict__ out) {
+  __shared__ double sa[256], sb[256];
+  double a = 0.0, b = 0.0;
+  for (int i = threadIdx.x; i < n; i += 256) {
+    a += partial[2 * i];
+    b += partial[2 * i + 1];
+  }
+  sa[threadIdx.x] = a;
+  sb[threadIdx.x] = b;
+  __syncthreads();
+  for (int o = 128; o >= 1; o >>= 1) {
+    if (threadIdx.x < o) {
+      sa[threadIdx.x] += sa[threadIdx.x + o];
+      sb[threadIdx.x] += sb[threadIdx.x + o];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    out[0] = sa[0];
+    out[1] = sb[0];
+  }
+}
+
+// ============================================================================ f32 GEMM, bf16 weights
+// Y[M,N] = X[M,K] * W[N,K]^T with W widened from bf16 (ds_linear_nobias_bf16, seq_len > 1: the
+// reference converts W to f32 and calls sgemm, ds_kernels.c:917-927). 64x64 tile, 16-wide K steps.
+__global__ void __launch_bounds__(256) k_gemm_bf16w(const float *__restrict__ X, const uint16_t *__restrict__ W,
+                                                    float *__restrict__ Y, int M, int K, int N) {
+  __shared__ float xs[16][65], ws[16][65];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    for (int i = threadIdx.x; i < 16 * 64; i += 256) {
+      int kk = i & 15, rr = i >> 4;
+      int m = m0 + rr, nn = n0 + rr, k = k0 + kk;
+      xs[kk][rr] = (m < M && k < K) ? X[(size_t)m * K + k] : 0.0f;
+      ws[kk][rr] = (nn < N && k < K) ? dsh_bf16_to_f32(W[(size_t)nn * K + k]) : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; kk++) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        a[i] = xs[kk][ty * 4 + i];
+        b[i] = ws[kk][tx * 4 + i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      int m = m0 + ty * 4 + i, nn = n0 + tx * 4 + j;
+      if (m < M && nn < N) Y[(size_t)m * N + nn] = acc[i][j];
+    }
+}
+
+// ============================================================================ synthetic data
+// Counter-based: pair p draws two SplitMix64 outputs of (seed, p) and maps them through Box–Muller.
+__device__ __forceinline__ uint64_t dsh_splitmix(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+template <typename T>
+__device__ __forceinline__ T to_out(float v);
+template <>
+__device__ __forceinline__ float to_out<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ uint16_t to_out<uint16_t>(float v) {
+  uint32_t u = __float_as_uint(v);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+template <typename T>
+__global__ void k_fill_normal(T *__restrict__ dst, size_t n, uint64_t seed, float mean, float std_) {
+  size_t pairs = (n + 1) / 2;
+  for (size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x; p < pairs; p += (size_t)gridDim.x * blockDim.x) {
+    uint64_t a = dsh_splitmix(seed * 0x632BE59BD9B4E019ull + 2 * p);
+    uint64_t b = dsh_splitmix(seed * 0x632BE59BD9B4E019ull + 2 * p + 1);
+    float u1 = ((float)(a >> 40) + 1.0f) * (1.0f / 16777216.0f);
+    float u2 = (float)(b >> 40) * (1.0f / 16777216.0f);
+    float r = sqrtf(-2.0f * logf(u1));
+    float sn, cs;
+    sincosf(6.283185307f * u2, &sn, &cs);
+    dst[2 * p] = to_out<T>(mean + std_ * r * cs);
+    if (2 * p + 1 < n) dst[2 * p + 1] = to_out<T>(mean + std_ * r * sn);
+  }
+}
+
+// ============================================================================ launchers
+
+#define LAUNCH_CHECK() (hipGetLastError())
+
+extern "C" {
+
+hipError_t dsh_launch_quantize_bf16(const uint16_t *W, int8_t *q, float *scale, float *offset, int out_dim, int in_dim,
+                                    hipStream_t s) {
+  k_quantize_rows<uint16_t><<<(out_dim + 3) / 4, 256, 0, s>>>(W, q, scale, offset, 1, out_dim, in_dim);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_quantize_f32(const float *W, int8_t *q, float *scale, float *offset, int out_dim, int in_dim,
+                                   hipStream_t s) {
+  k_quantize_rows<float><<<(out_dim + 3) / 4, 256, 0, s>>>(W, q, scale, offset, 1, out_dim, in_dim);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_quantize_bf16_so(const uint16_t *W, int8_t *q, float *so, int out_dim, int in_dim, hipStream_t s) {
+  k_quantize_rows<uint16_t><<<(out_dim + 3) / 4, 256, 0, s>>>(W, q, so, so + 1, 2, out_dim, in_dim);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_quant_rms(const int8_t *q, const float *scale, const float *offset, const uint16_t *W,
+                                int out_dim, int in_dim, double *work, hipStream_t s) {
+  k_quant_rms<<<1024, 256, 0, s>>>(q, scale, offset, W, out_dim, in_dim, work + 2);
+  hipError_t e = LAUNCH_CHECK();
+  if (e != hipSuccess) return e;
+  k_sum_pairs_f64<<<1, 256, 0, s>>>(work + 2, 1024, work);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_gemm_bf16w(const float *X, const uint16_t *W, float *Y, int M, int K, int N, hipStream_t s) {
+  dim3 grid((N + 63) / 64, (M + 63) / 64);
+  k_gemm_bf16w<<<grid, 256, 0, s>>>(X, W, Y, M, K, N);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_fill_normal_bf16(uint16_t *dst, size_t n, uint64_t seed, float std_, hipStream_t s) {
+  size_t pairs = (n + 1) / 2;
+  int blocks = (int)((pairs + 255) / 256);
+  if (blocks > 65536) blocks = 65536;
+  k_fill_normal<uint16_t><<<blocks, 256, 0, s>>>(dst, n, seed, 0.0f, std_);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_fill_normal_f32(float *dst, size_t n, uint64_t seed, float mean, float std_, hipStream_t s) {
+  size_t pairs = (n + 1) / 2;
+  int blocks = (int)((pairs + 255) / 256);
+  if (blocks > 65536) blocks = 65536;
+  k_fill_normal<float><<<blocks, 256, 0, s>>>(dst, n, seed, mean, std_);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_dequantize(const int8_t *q, const float *scale, const float *offset, float *out, int out_dim,
+                                 int in_dim, hipStream_t s) {
+  size_t n = (size_t)out_dim * in_dim;
+  int blocks = (int)((n + 255) / 256);
+  if (blocks > 8192) blocks = 8192;
+  k_dequantize<<<blocks, 256, 0, s>>>(q, scale, offset, out, out_dim, in_dim);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_int8_matvec(const int8_t *q, const float *scale, const float *offset, const float *x, float *y,
+                                  int in_dim, int row_start, int nrows, hipStream_t s) {
+  if (nrows <= 0) return hipSuccess;
+  int C = in_dim / 16;
+  bool aligned = (in_dim % 16 == 0) && (((uintptr_t)q & 15) == 0) && (((uintptr_t)x & 15) == 0);
+  if (aligned && C >= 64) {
+    k_int8_matvec16<16><<<(nrows + 15) / 16, 256, 0, s>>>(q, scale, offset, x, y, in_dim, row_start, nrows);
+  } else if (aligned && C >= 16) {
+    k_int8_matvec16<8><<<(nrows + 31) / 32, 256, 0, s>>>(q, scale, offset, x, y, in_dim, row_start, nrows);
+  } else if (aligned) {
+    k_int8_matvec16<4><<<(nrows + 63) / 64, 256, 0, s>>>(q, scale, offset, x, y, in_dim, row_start, nrows);
+  } else {
+    k_int8_matvec_any<<<(nrows + 3) / 4, 256, 0, s>>>(q, scale, offset, x, y, in_dim, row_start, nrows);
+  }
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_swiglu(float *out, const float *g, const float *u, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  int blocks = (int)((n + 255) / 256);
+  if (blocks > 4096) blocks = 4096;
+  k_swiglu<<<blocks, 256, 0, s>>>(out, g, u, n);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_bf16_trunc(float *a, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  int blocks = (int)((n + 255) / 256);
+  if (blocks > 4096) blocks = 4096;
+  k_bf16_trunc<<<blocks, 256, 0, s>>>(a, n);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_vec_add(float *dst, const float *a, const float *b, int n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  int blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  k_vec_add<<<blocks, 256, 0, s>>>(dst, a, b, n);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_expert_combine(float *out, const float *eo, const float *w, int top_k, int hidden,
+                                     hipStream_t s) {
+  if (hidden <= 0) return hipSuccess;
+  k_expert_combine<<<(hidden + 255) / 256, 256, 0, s>>>(out, eo, w, top_k, hidden);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_split_swiglu(float *h, const float *gu, int inter, int bf16sim, hipStream_t s) {
+  if (inter <= 0) return hipSuccess;
+  k_split_swiglu<<<(inter + 255) / 256, 256, 0, s>>>(h, gu, inter, bf16sim);
+  return LAUNCH_CHECK();
+}
+
+static bool bf16_aligned(const uint16_t *W, int in_dim) { return (in_dim % 8 == 0) && (((uintptr_t)W & 15) == 0); }
+
+hipError_t dsh_launch_bf16_matvec_avx(const uint16_t *W, const float *x, const float *bias, float *y, int in_dim,
+                                      int out_dim, int nthreads, hipStream_t s) {
+  if (out_dim <= 0) return hipSuccess;
+  size_t lds = (size_t)in_dim * sizeof(float);
+  if (lds > 64 * 1024) return hipErrorInvalidValue;
+  int blocks = (out_dim + 63) / 64;
+  int chunk = dsh_chunk_len(out_dim, nthreads);
+  if (bf16_aligned(W, in_dim))
+    k_bf16_matvec_avx<true><<<blocks, 256, lds, s>>>(W, x, bias, y, in_dim, out_dim, chunk);
+  else
+    k_bf16_matvec_avx<false><<<blocks, 256, lds, s>>>(W, x, bias, y, in_dim, out_dim, chunk);
+  return LAUNCH_CHECK();
+}
+
+int dsh_argmax_avx_blocks(int out_dim) { return (out_dim + 63) / 64; }
+
+hipError_t dsh_launch_argmax_avx_partial(const uint16_t *W, const float *x, unsigned long long *cand, float *logits,
+                                         int in_dim, int out_dim, int chunk, hipStream_t s) {
+  if (out_dim <= 0) return hipSuccess;
+  size_t lds = (size_t)in_dim * sizeof(float);
+  if (lds > 64 * 1024) return hipErrorInvalidValue;
+  int blocks = dsh_argmax_avx_blocks(out_dim);
+  if (bf16_aligned(W, in_dim))
+    k_argmax_avx<true><<<blocks, 256, lds, s>>>(W, x, cand, logits, in_dim, out_dim, chunk);
+  else
+    k_argmax_avx<false><<<blocks, 256, lds, s>>>(W, x, cand, logits, in_dim, out_dim, chunk);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_argmax_avx(const uint16_t *W, const float *x, unsigned long long *cand, float *logits,
+                                 int in_dim, int out_dim, int nthreads, int *out_idx, float *out_val, hipStream_t s) {
+  if (out_dim <= 0) return hipSuccess;
+  hipError_t e = dsh_launch_argmax_avx_partial(W, x, cand, logits, in_dim, out_dim, dsh_chunk_len(out_dim, nthreads), s);
+  if (e != hipSuccess) return e;
+  k_argmax_final<<<1, 256, 0, s>>>(cand, dsh_argmax_avx_blocks(out_dim), out_idx, out_val);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_argmax_excluding(const uint16_t *W, const float *x, unsigned long long *cand, float *lg,
+                                       float *lg2, int in_dim, int out_dim, int nthreads, const int *excl, int n_excl,
+                                       int *out_idx, hipStream_t s) {
+  if (out_dim <= 0) return hipSuccess;
+  // chunk slots: up to 16 thread chunks, then (one thread) the rescan's 8192-row chunks after slot 0
+  if (nthreads > 16 || 1 + (out_dim + 8191) / 8192 > EXCL_MAX_CHUNKS) return hipErrorInvalidValue;
+  int chunk = dsh_chunk_len(out_dim, nthreads);
+  hipError_t e = dsh_launch_argmax_avx_partial(W, x, cand, lg, in_dim, out_dim, chunk, s);
+  if (e == hipSuccess && nthreads <= 1) e = dsh_launch_argmax_avx_partial(W, x, cand, lg2, in_dim, out_dim, 8192, s);
+  if (e != hipSuccess) return e;
+  k_argmax_excl_select<<<1, 256, 0, s>>>(lg, lg2, out_dim, nthreads, excl, n_excl, out_idx);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_bf16_dot_row(const uint16_t *W, const float *x, int in_dim, int row, float *out, hipStream_t s) {
+  k_bf16_dot_row<<<1, 64, 0, s>>>(W, x, in_dim, row, out);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_linear_f32_exact(const float *W, const float *x, float *y, int in_dim, int out_dim,
+                                       hipStream_t s) {
+  if (out_dim <= 0) return hipSuccess;
+  k_linear_f32_exact<<<(out_dim + 63) / 64, 64, 0, s>>>(W, x, y, in_dim, out_dim);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_topk(const float *scores, int n, int k, int mode, int *idx, float *w, hipStream_t s) {
+  if (n <= 0 || n > 64 || k <= 0 || k > n) return hipErrorInvalidValue;
+  k_topk<<<1, 64, 0, s>>>(scores, n, k, mode, idx, w);
+  return LAUNCH_CHECK();
+}
+
+}  // extern "C"

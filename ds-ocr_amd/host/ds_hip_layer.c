@@ -1,0 +1,532 @@
+/* ds_hip_layer.c — device-resident MoE layers and the decode stack (ds_hip.h).
+ *
+ * Layer arena (one hipMalloc per MoE layer, every region 256-byte aligned):
+ *   routed gate_up codes [E][2I][H] | routed down codes [E][H][I] | shared gate_up [2SI][H] |
+ *   shared down [H][SI] | (scale, offset) pairs for each of those row sets | router f32 [E][H] |
+ *   router bf16 [E][H] | work: scores[E], idx[K], w[K], h[K*I+SI], x[H]
+ * Expert e's rows sit at a fixed offset, so the kernels index experts from the device-side top-k
+ * without any host round trip. The reference allocates every block separately
+ * (ds_quantize.c:57-59) and gathers experts through ds_dec_layer_t.experts_int4[64].
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "dsr.h"
+#include "ds_hip.h"
+#include "ds_kernels.h"
+
+struct ds_hip_layer {
+  int H, I, E, K, SI;
+  void *arena;
+  size_t bytes;
+  dsh_layer_t d;          /* device pointers into the arena */
+  dsh_layer_work_t wk;    /* work buffers (in the arena) */
+  float *xtmp;            /* [H] */
+  int have_f32, have_bf16;
+};
+
+static size_t al(size_t n) { return (n + 255) & ~(size_t)255; }
+
+ds_hip_layer_t *ds_hip_layer_create(int hidden, int inter, int n_experts, int top_k, int shared_inter) {
+  if (dsr_init()) return NULL;
+  if (hidden <= 0 || inter <= 0 || n_experts <= 0 || top_k <= 0 || shared_inter <= 0 || n_experts > 64 ||
+      top_k > n_experts) {
+    dsr_failf("ds_hip_layer_create: invalid shape H=%d I=%d E=%d K=%d SI=%d", hidden, inter, n_experts, top_k,
+              shared_inter);
+    return NULL;
+  }
+  if (!dsh_moe_fast_shape(hidden, inter, n_experts, top_k, shared_inter)) {
+    dsr_failf("ds_hip_layer_create: shape H=%d I=%d E=%d K=%d SI=%d not supported by the fused decode kernels "
+              "(need H %% 16 == 0, I %% 128 == 0, SI %% I == 0, K + SI/I == 8)",
+              hidden, inter, n_experts, top_k, shared_inter);
+    return NULL;
+  }
+  ds_hip_layer_t *L = (ds_hip_layer_t *)calloc(1, sizeof *L);
+  if (!L) return NULL;
+  size_t H = hidden, I = inter, E = n_experts, K = top_k, SI = shared_inter;
+  size_t off[16], n = 0, k = 0;
+#define REGION(bytes) (off[k++] = n, n += al(bytes))
+  REGION(E * 2 * I * H);          /* 0 gu_q */
+  REGION(E * H * I);              /* 1 dn_q */
+  REGION(2 * SI * H);             /* 2 sgu_q */
+  REGION(H * SI);                 /* 3 sdn_q */
+  REGION(E * 2 * I * 8);          /* 4 gu_so */
+  REGION(E * H * 8);              /* 5 dn_so */
+  REGION(2 * SI * 8);             /* 6 sgu_so */
+  REGION(H * 8);                  /* 7 sdn_so */
+  REGION(E * H * 4);              /* 8 router f32 */
+  REGION(E * H * 2);              /* 9 router bf16 */
+  REGION(E * 4);                  /* 10 scores */
+  REGION(K * 4);                  /* 11 idx */
+  REGION(K * 4);                  /* 12 w */
+  REGION((K * I + SI) * 4);       /* 13 h */
+  REGION(H * 4);                  /* 14 xtmp */
+#undef REGION
+  hipError_t e = hipMalloc(&L->arena, n);
+  if (e != hipSuccess) {
+    dsr_fail("layer arena allocation", e);
+    free(L);
+    return NULL;
+  }
+  hipMemsetAsync(L->arena, 0, n, dsr_stream);
+  char *b = (char *)L->arena;
+  L->bytes = n;
+  L->H = hidden;
+  L->I = inter;
+  L->E = n_experts;
+  L->K = top_k;
+  L->SI = shared_inter;
+  L->d.gu_q = (const int8_t *)(b + off[0]);
+  L->d.dn_q = (const int8_t *)(b + off[1]);
+  L->d.sgu_q = (const int8_t *)(b + off[2]);
+  L->d.sdn_q = (const int8_t *)(b + off[3]);
+  L->d.gu_so = (const float *)(b + off[4]);
+  L->d.dn_so = (const float *)(b + off[5]);
+  L->d.sgu_so = (const float *)(b + off[6]);
+  L->d.sdn_so = (const float *)(b + off[7]);
+  L->d.router_f32 = (const float *)(b + off[8]);
+  L->d.router_bf16 = (const uint16_t *)(b + off[9]);
+  L->d.H = hidden;
+  L->d.I = inter;
+  L->d.E = n_experts;
+  L->d.K = top_k;
+  L->d.SI = shared_inter;
+  L->wk.scores = (float *)(b + off[10]);
+  L->wk.idx = (int *)(b + off[11]);
+  L->wk.w = (float *)(b + off[12]);
+  L->wk.h = (float *)(b + off[13]);
+  L->xtmp = (float *)(b + off[14]);
+  return L;
+}
+
+void ds_hip_layer_destroy(ds_hip_layer_t *L) {
+  if (!L) return;
+  hipStreamSynchronize(dsr_stream);
+  hipFree(L->arena);
+  free(L);
+}
+
+size_t ds_hip_layer_bytes(const ds_hip_layer_t *L) { return L ? L->bytes : 0; }
+
+int ds_hip_layer_set_router(ds_hip_layer_t *L, const float *router_f32, const uint16_t *router_bf16) {
+  if (!L) return dsr_failf("ds_hip_layer_set_router: NULL layer");
+  size_t n = (size_t)L->E * L->H;
+  if (router_f32) {
+    if (dsr_h2d((void *)L->d.router_f32, router_f32, n * 4)) return -1;
+    L->have_f32 = 1;
+  }
+  if (router_bf16) {
+    if (dsr_h2d((void *)L->d.router_bf16, router_bf16, n * 2)) return -1;
+    L->have_bf16 = 1;
+  }
+  DSR_TRY(hipStreamSynchronize(dsr_stream), "set router");
+  return 0;
+}
+
+int ds_hip_layer_set_router_dev(ds_hip_layer_t *L, const float *router_f32_dev, const uint16_t *router_bf16_dev) {
+  if (!L) return dsr_failf("ds_hip_layer_set_router_dev: NULL layer");
+  size_t n = (size_t)L->E * L->H;
+  if (router_f32_dev) {
+    DSR_TRY(hipMemcpyAsync((void *)L->d.router_f32, router_f32_dev, n * 4, hipMemcpyDeviceToDevice, dsr_stream),
+            "router copy");
+    L->have_f32 = 1;
+  }
+  if (router_bf16_dev) {
+    DSR_TRY(hipMemcpyAsync((void *)L->d.router_bf16, router_bf16_dev, n * 2, hipMemcpyDeviceToDevice, dsr_stream),
+            "router copy");
+    L->have_bf16 = 1;
+  }
+  return 0;
+}
+
+/* Device destinations of expert e's rows (e == -1: shared). */
+static int expert_dst(const ds_hip_layer_t *L, int e, int8_t **gq, float **gso, int8_t **dq, float **dso, int *I) {
+  size_t H = L->H;
+  if (e == -1) {
+    *I = L->SI;
+    *gq = (int8_t *)L->d.sgu_q;
+    *gso = (float *)L->d.sgu_so;
+    *dq = (int8_t *)L->d.sdn_q;
+    *dso = (float *)L->d.sdn_so;
+    return 0;
+  }
+  if (e < 0 || e >= L->E) return dsr_failf("expert index %d outside [-1, %d)", e, L->E);
+  size_t In = L->I;
+  *I = L->I;
+  *gq = (int8_t *)L->d.gu_q + (size_t)e * 2 * In * H;
+  *gso = (float *)L->d.gu_so + (size_t)e * 2 * In * 2;
+  *dq = (int8_t *)L->d.dn_q + (size_t)e * H * In;
+  *dso = (float *)L->d.dn_so + (size_t)e * H * 2;
+  return 0;
+}
+
+static int upload_block(int8_t *q, float *so, const ds_int4_block_t *b, int out_dim, int in_dim) {
+  if (!b || !b->qweight || !b->scale || !b->offset || b->out_dim != out_dim || b->in_dim != in_dim)
+    return dsr_failf("ds_hip_layer_set_expert: block shape %dx%d, expected %dx%d", b ? b->out_dim : -1,
+                     b ? b->in_dim : -1, out_dim, in_dim);
+  float *pairs = (float *)malloc((size_t)out_dim * 8);
+  if (!pairs) return dsr_failf("host allocation failed");
+  for (int r = 0; r < out_dim; r++) {
+    pairs[2 * r] = b->scale[r];
+    pairs[2 * r + 1] = b->offset[r];
+  }
+  int rc = dsr_h2d(q, b->qweight, (size_t)out_dim * in_dim) || dsr_h2d(so, pairs, (size_t)out_dim * 8);
+  if (!rc) rc = hipStreamSynchronize(dsr_stream) != hipSuccess;
+  free(pairs);
+  return rc ? -1 : 0;
+}
+
+int ds_hip_layer_set_expert(ds_hip_layer_t *L, int e, const ds_int4_block_t *gate_up, const ds_int4_block_t *down) {
+  if (!L) return dsr_failf("ds_hip_layer_set_expert: NULL layer");
+  int8_t *gq, *dq;
+  float *gso, *dso;
+  int I;
+  if (expert_dst(L, e, &gq, &gso, &dq, &dso, &I)) return -1;
+  if (upload_block(gq, gso, gate_up, 2 * I, L->H)) return -1;
+  return upload_block(dq, dso, down, L->H, I);
+}
+
+int ds_hip_layer_quantize_expert(ds_hip_layer_t *L, int e, const uint16_t *gate_up_bf16_dev,
+                                 const uint16_t *down_bf16_dev) {
+  if (!L || !gate_up_bf16_dev || !down_bf16_dev) return dsr_failf("ds_hip_layer_quantize_expert: NULL argument");
+  int8_t *gq, *dq;
+  float *gso, *dso;
+  int I;
+  if (expert_dst(L, e, &gq, &gso, &dq, &dso, &I)) return -1;
+  hipError_t err = dsh_launch_quantize_bf16_so(gate_up_bf16_dev, gq, gso, 2 * I, L->H, dsr_stream);
+  if (err == hipSuccess) err = dsh_launch_quantize_bf16_so(down_bf16_dev, dq, dso, L->H, I, dsr_stream);
+  if (err != hipSuccess) return dsr_fail("quantize expert", err);
+  return 0;
+}
+
+static int export_block(int8_t *q, float *sc, float *of, const int8_t *dq, const float *dso, int out_dim, int in_dim) {
+  if (q && dsr_d2h(q, dq, (size_t)out_dim * in_dim)) return -1;
+  if (sc || of) {
+    float *pairs = (float *)malloc((size_t)out_dim * 8);
+    if (!pairs) return dsr_failf("host allocation failed");
+    if (dsr_d2h(pairs, dso, (size_t)out_dim * 8)) {
+      free(pairs);
+      return -1;
+    }
+    for (int r = 0; r < out_dim; r++) {
+      if (sc) sc[r] = pairs[2 * r];
+      if (of) of[r] = pairs[2 * r + 1];
+    }
+    free(pairs);
+  }
+  return 0;
+}
+
+int ds_hip_layer_export_expert(const ds_hip_layer_t *L, int e, int8_t *gu_q, float *gu_scale, float *gu_offset,
+                               int8_t *dn_q, float *dn_scale, float *dn_offset) {
+  if (!L) return dsr_failf("ds_hip_layer_export_expert: NULL layer");
+  int8_t *gq, *dq;
+  float *gso, *dso;
+  int I;
+  if (expert_dst(L, e, &gq, &gso, &dq, &dso, &I)) return -1;
+  if (export_block(gu_q, gu_scale, gu_offset, gq, gso, 2 * I, L->H)) return -1;
+  return export_block(dn_q, dn_scale, dn_offset, dq, dso, L->H, I);
+}
+
+static int check_router(const ds_hip_layer_t *L, int route_mode) {
+  if (route_mode == DS_HIP_ROUTE_CFG && !L->have_f32) return dsr_failf("layer has no f32 router (route_mode CFG)");
+  if (route_mode == DS_HIP_ROUTE_DECODE && !L->have_bf16)
+    return dsr_failf("layer has no bf16 router (route_mode DECODE)");
+  if (route_mode != DS_HIP_ROUTE_CFG && route_mode != DS_HIP_ROUTE_DECODE)
+    return dsr_failf("unknown route_mode %d", route_mode);
+  return 0;
+}
+
+/* The three kernels of one layer. x_in (+ *step * stride) -> x_out. */
+static hipError_t layer_enqueue(const ds_hip_layer_t *L, const dsh_layer_work_t *wk, const float *x_in,
+                                const int *step, int stride, float *x_out, int route_mode, int residual, int bf16sim) {
+  hipError_t e = dsh_launch_moe_scores(&L->d, x_in, step, stride, route_mode, dsr_threads(), wk->scores, dsr_stream);
+  if (e == hipSuccess) e = dsh_launch_moe_gate_up(&L->d, x_in, step, stride, route_mode, bf16sim, wk, dsr_stream);
+  if (e == hipSuccess) e = dsh_launch_moe_down(&L->d, x_in, step, stride, x_out, residual, bf16sim, wk, dsr_stream);
+  return e;
+}
+
+int ds_hip_layer_forward(ds_hip_layer_t *L, float *out_dev, const float *x_dev, int route_mode, int residual,
+                         int *idx_dev, float *w_dev) {
+  if (!L || !out_dev || !x_dev) return dsr_failf("ds_hip_layer_forward: NULL argument");
+  if (check_router(L, route_mode)) return -1;
+  int bf16sim = ds_bf16_simulate_python;
+  hipError_t e = layer_enqueue(L, &L->wk, x_dev, NULL, 0, out_dev, route_mode, residual, bf16sim);
+  if (e != hipSuccess) return dsr_fail("layer kernels", e);
+  if (idx_dev)
+    DSR_TRY(hipMemcpyAsync(idx_dev, L->wk.idx, (size_t)L->K * 4, hipMemcpyDeviceToDevice, dsr_stream), "idx copy");
+  if (w_dev)
+    DSR_TRY(hipMemcpyAsync(w_dev, L->wk.w, (size_t)L->K * 4, hipMemcpyDeviceToDevice, dsr_stream), "w copy");
+  return 0;
+}
+
+/* ================================================================ decode stack */
+
+struct ds_hip_stack {
+  ds_hip_layer_t **layers;
+  int n_layers;
+  const uint16_t *lm;
+  int vocab, H;
+  int route_mode, bf16sim;
+  int lm_fast;
+  void *work;              /* step counter, x buffer, candidates */
+  int *step;
+  float *xbuf;
+  unsigned long long *cand;
+  int ncand;
+  const float *xs;
+  int stride;
+  int *tokens;
+  hipGraph_t graph;
+  hipGraphExec_t exec;
+  int bound;
+};
+
+ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers, const uint16_t *lm_head_dev,
+                                    int vocab, int route_mode) {
+  if (dsr_init()) return NULL;
+  if (!layers || n_layers <= 0 || !lm_head_dev || vocab <= 0) {
+    dsr_failf("ds_hip_stack_create: invalid arguments");
+    return NULL;
+  }
+  int H = layers[0]->H;
+  for (int l = 0; l < n_layers; l++) {
+    if (!layers[l] || layers[l]->H != H) {
+      dsr_failf("ds_hip_stack_create: layer %d missing or hidden size differs", l);
+      return NULL;
+    }
+    if (check_router(layers[l], route_mode)) return NULL;
+  }
+  ds_hip_stack_t *S = (ds_hip_stack_t *)calloc(1, sizeof *S);
+  if (!S) return NULL;
+  S->layers = (ds_hip_layer_t **)malloc(sizeof(ds_hip_layer_t *) * (size_t)n_layers);
+  memcpy(S->layers, layers, sizeof(ds_hip_layer_t *) * (size_t)n_layers);
+  S->n_layers = n_layers;
+  S->lm = lm_head_dev;
+  S->vocab = vocab;
+  S->H = H;
+  S->route_mode = route_mode;
+  S->bf16sim = ds_bf16_simulate_python;
+  /* Fast LM-head kernel: in_dim % 32 == 0, aligned rows, every reference row chunk a multiple of 4
+   * rows (then every row uses the 2-accumulator order). */
+  int chunk = vocab;
+  int T = dsr_threads();
+  if (T > 1) chunk = (vocab + T - 1) / T;
+  int ok4 = 1;
+  for (int s = 0; s < vocab; s += chunk) {
+    int len = vocab - s < chunk ? vocab - s : chunk;
+    if (len % 4) ok4 = 0;
+  }
+  S->lm_fast = (H % 32 == 0) && (((uintptr_t)lm_head_dev & 15) == 0) && ok4;
+  S->ncand = S->lm_fast ? dsh_lm_argmax_blocks(vocab) : dsh_argmax_avx_blocks(vocab);
+  size_t bytes = 256 + al((size_t)H * 4) + al((size_t)S->ncand * 8);
+  hipError_t e = hipMalloc(&S->work, bytes);
+  if (e != hipSuccess) {
+    dsr_fail("stack allocation", e);
+    free(S->layers);
+    free(S);
+    return NULL;
+  }
+  hipMemsetAsync(S->work, 0, bytes, dsr_stream);
+  S->step = (int *)S->work;
+  S->xbuf = (float *)((char *)S->work + 256);
+  S->cand = (unsigned long long *)((char *)S->work + 256 + al((size_t)H * 4));
+  return S;
+}
+
+void ds_hip_stack_destroy(ds_hip_stack_t *S) {
+  if (!S) return;
+  hipStreamSynchronize(dsr_stream);
+  if (S->exec) hipGraphExecDestroy(S->exec);
+  if (S->graph) hipGraphDestroy(S->graph);
+  hipFree(S->work);
+  free(S->layers);
+  free(S);
+}
+
+size_t ds_hip_stack_bytes_per_step(const ds_hip_stack_t *S) {
+  if (!S) return 0;
+  size_t per_layer = 0;
+  const ds_hip_layer_t *L = S->layers[0];
+  size_t H = L->H, I = L->I, K = L->K, SI = L->SI, E = L->E;
+  per_layer += K * (2 * I * H + 2 * I * 8) + K * (H * I + H * 8); /* routed experts */
+  per_layer += 2 * SI * H + 2 * SI * 8 + H * SI + H * 8;          /* shared expert */
+  per_layer += E * H * (S->route_mode == DS_HIP_ROUTE_CFG ? 4 : 2); /* router */
+  return per_layer * (size_t)S->n_layers + (size_t)S->vocab * S->H * 2;
+}
+
+/* One decode step; slot_events (optional) gets an event after every kernel. */
+static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
+  hipError_t e = hipSuccess;
+  int n = 0;
+  if (ev) e = hipEventRecord(ev[n++], dsr_stream);
+  for (int l = 0; l < S->n_layers && e == hipSuccess; l++) {
+    const ds_hip_layer_t *L = S->layers[l];
+    const dsh_layer_work_t *wk = &S->layers[0]->wk;
+    const float *xin = l == 0 ? S->xs : S->xbuf;
+    const int *st = l == 0 ? S->step : NULL;
+    int stride = l == 0 ? S->stride : 0;
+    e = dsh_launch_moe_scores(&L->d, xin, st, stride, S->route_mode, dsr_threads(), wk->scores, dsr_stream);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+    if (e == hipSuccess) e = dsh_launch_moe_gate_up(&L->d, xin, st, stride, S->route_mode, S->bf16sim, wk, dsr_stream);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+    if (e == hipSuccess)
+      e = dsh_launch_moe_down(&L->d, xin, st, stride, S->xbuf, 1, S->bf16sim, wk, dsr_stream);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+  }
+  if (e != hipSuccess) return e;
+  if (S->lm_fast) {
+    e = dsh_launch_lm_argmax_partial(S->lm, S->xbuf, S->H, S->vocab, S->cand, dsr_stream);
+  } else {
+    e = dsh_launch_argmax_avx_partial(S->lm, S->xbuf, S->cand, NULL, S->H, S->vocab,
+                                      S->vocab > 0 && dsr_threads() > 1 ? (S->vocab + dsr_threads() - 1) / dsr_threads()
+                                                                        : S->vocab,
+                                      dsr_stream);
+  }
+  if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+  if (e == hipSuccess) e = dsh_launch_lm_argmax_final(S->cand, S->ncand, S->tokens, S->step, dsr_stream);
+  if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+  return e;
+}
+
+int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int *tokens_dev) {
+  if (!S || !xs_dev || !tokens_dev || stride < 0) return dsr_failf("ds_hip_stack_bind: invalid arguments");
+  if (S->exec) {
+    hipGraphExecDestroy(S->exec);
+    S->exec = NULL;
+  }
+  if (S->graph) {
+    hipGraphDestroy(S->graph);
+    S->graph = NULL;
+  }
+  S->xs = xs_dev;
+  S->stride = stride;
+  S->tokens = tokens_dev;
+  DSR_TRY(hipStreamSynchronize(dsr_stream), "bind");
+  DSR_TRY(hipStreamBeginCapture(dsr_stream, hipStreamCaptureModeThreadLocal), "graph capture begin");
+  hipError_t e = step_enqueue(S, NULL);
+  hipGraph_t g = NULL;
+  hipError_t e2 = hipStreamEndCapture(dsr_stream, &g);
+  if (e != hipSuccess) {
+    if (g) hipGraphDestroy(g);
+    return dsr_fail("graph capture", e);
+  }
+  if (e2 != hipSuccess) return dsr_fail("graph capture end", e2);
+  S->graph = g;
+  DSR_TRY(hipGraphInstantiate(&S->exec, g, NULL, NULL, 0), "graph instantiate");
+  S->bound = 1;
+  return ds_hip_stack_reset(S);
+}
+
+int ds_hip_stack_reset(ds_hip_stack_t *S) {
+  if (!S) return -1;
+  DSR_TRY(hipMemsetAsync(S->step, 0, sizeof(int), dsr_stream), "reset step");
+  return 0;
+}
+
+int ds_hip_stack_run(ds_hip_stack_t *S, int n_steps) {
+  if (!S || !S->bound) return dsr_failf("ds_hip_stack_run: stack not bound");
+  for (int i = 0; i < n_steps; i++) DSR_TRY(hipGraphLaunch(S->exec, dsr_stream), "graph launch");
+  return 0;
+}
+
+int ds_hip_stack_run_eager(ds_hip_stack_t *S, int n_steps) {
+  if (!S || !S->bound) return dsr_failf("ds_hip_stack_run_eager: stack not bound");
+  for (int i = 0; i < n_steps; i++) {
+    hipError_t e = step_enqueue(S, NULL);
+    if (e != hipSuccess) return dsr_fail("decode step", e);
+  }
+  return 0;
+}
+
+int ds_hip_stack_hidden(ds_hip_stack_t *S, float *x_host) {
+  if (!S || !x_host) return -1;
+  return dsr_d2h(x_host, S->xbuf, (size_t)S->H * 4);
+}
+
+int ds_hip_time_stack(ds_hip_stack_t *S, int n_steps, float *ms) {
+  if (!S || !S->bound || !ms) return dsr_failf("ds_hip_time_stack: invalid arguments");
+  hipEvent_t a, b;
+  DSR_TRY(hipEventCreate(&a), "event");
+  DSR_TRY(hipEventCreate(&b), "event");
+  int rc = 0;
+  if (hipEventRecord(a, dsr_stream) != hipSuccess || ds_hip_stack_run(S, n_steps) ||
+      hipEventRecord(b, dsr_stream) != hipSuccess || hipEventSynchronize(b) != hipSuccess ||
+      hipEventElapsedTime(ms, a, b) != hipSuccess)
+    rc = dsr_failf("ds_hip_time_stack: timing failed");
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  return rc;
+}
+
+int ds_hip_profile_stack(ds_hip_stack_t *S, int n_steps, float *ms_out) {
+  if (!S || !S->bound || !ms_out || n_steps <= 0) return dsr_failf("ds_hip_profile_stack: invalid arguments");
+  int nk = 3 * S->n_layers + 2;
+  hipEvent_t *ev = (hipEvent_t *)calloc((size_t)(nk + 1), sizeof(hipEvent_t));
+  double *acc = (double *)calloc((size_t)nk, sizeof(double));
+  int rc = 0;
+  for (int i = 0; i <= nk; i++)
+    if (hipEventCreate(&ev[i]) != hipSuccess) rc = -1;
+  for (int s = 0; s < n_steps && rc == 0; s++) {
+    if (step_enqueue(S, ev) != hipSuccess || hipEventSynchronize(ev[nk]) != hipSuccess) {
+      rc = -1;
+      break;
+    }
+    for (int i = 0; i < nk; i++) {
+      float m = 0;
+      hipEventElapsedTime(&m, ev[i], ev[i + 1]);
+      acc[i] += m;
+    }
+  }
+  for (int i = 0; i < nk; i++) ms_out[i] = (float)(acc[i] / n_steps);
+  for (int i = 0; i <= nk; i++)
+    if (ev[i]) hipEventDestroy(ev[i]);
+  free(ev);
+  free(acc);
+  return rc ? dsr_failf("ds_hip_profile_stack failed") : 0;
+}
+
+/* ================================================================ device-pointer kernels */
+
+int ds_hip_quantize_bf16(int8_t *q_dev, float *scale_dev, float *offset_dev, const uint16_t *W_dev, int out_dim,
+                         int in_dim) {
+  if (dsr_init()) return -1;
+  if (!q_dev || !scale_dev || !offset_dev || !W_dev || out_dim <= 0 || in_dim <= 0)
+    return dsr_failf("ds_hip_quantize_bf16: invalid arguments");
+  DSR_TRY(dsh_launch_quantize_bf16(W_dev, q_dev, scale_dev, offset_dev, out_dim, in_dim, dsr_stream), "quantize");
+  return 0;
+}
+
+int ds_hip_int8_matvec(float *y_dev, const float *x_dev, const int8_t *q_dev, const float *scale_dev,
+                       const float *offset_dev, int in_dim, int row_start, int nrows) {
+  if (dsr_init()) return -1;
+  if (!y_dev || !x_dev || !q_dev || !scale_dev || !offset_dev || in_dim <= 0 || row_start < 0 || nrows < 0)
+    return dsr_failf("ds_hip_int8_matvec: invalid arguments");
+  DSR_TRY(dsh_launch_int8_matvec(q_dev, scale_dev, offset_dev, x_dev, y_dev, in_dim, row_start, nrows, dsr_stream),
+          "int8 matvec");
+  return 0;
+}
+
+int ds_hip_argmax_bf16(int *idx_dev, const float *x_dev, const uint16_t *W_dev, int in_dim, int out_dim) {
+  if (dsr_init()) return -1;
+  if (!idx_dev || !x_dev || !W_dev || in_dim <= 0 || out_dim <= 0)
+    return dsr_failf("ds_hip_argmax_bf16: invalid arguments");
+  int nb = dsh_argmax_avx_blocks(out_dim);
+  unsigned long long *cand = (unsigned long long *)dsr_scratch(DSR_SLOT_C, (size_t)nb * 8);
+  if (!cand) return -1;
+  DSR_TRY(dsh_launch_argmax_avx(W_dev, x_dev, cand, NULL, in_dim, out_dim, dsr_threads(), idx_dev, NULL, dsr_stream),
+          "argmax");
+  return 0;
+}
+
+int ds_hip_fill_normal_bf16(uint16_t *dst_dev, size_t n, uint64_t seed, float std_) {
+  if (dsr_init()) return -1;
+  DSR_TRY(dsh_launch_fill_normal_bf16(dst_dev, n, seed, std_, dsr_stream), "fill normal");
+  return 0;
+}
+
+int ds_hip_fill_normal_f32(float *dst_dev, size_t n, uint64_t seed, float mean, float std_) {
+  if (dsr_init()) return -1;
+  DSR_TRY(dsh_launch_fill_normal_f32(dst_dev, n, seed, mean, std_, dsr_stream), "fill normal");
+  return 0;
+}

@@ -1,0 +1,53 @@
+/* dsr.h — internal host runtime of libds_ocr_hip (C): device, stream, errors, staging, registry. */
+#ifndef DSR_H
+#define DSR_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../csrc/k_core.h"
+#include "ds_quantize.h"
+
+extern hipStream_t dsr_stream;
+
+/* Initialises device 0 and the library stream once. Returns 0, or -1 (message printed). */
+int dsr_init(void);
+/* Records and prints a failure; returns -1. */
+int dsr_fail(const char *what, hipError_t e);
+int dsr_failf(const char *fmt, ...);
+#define DSR_TRY(call, what)                          \
+  do {                                               \
+    hipError_t dsr_e_ = (call);                      \
+    if (dsr_e_ != hipSuccess) return dsr_fail((what), dsr_e_); \
+  } while (0)
+
+/* Grow-only device staging buffer per slot (not thread-safe, like the reference API). */
+enum { DSR_SLOT_X, DSR_SLOT_Y, DSR_SLOT_A, DSR_SLOT_B, DSR_SLOT_C, DSR_SLOT_D, DSR_SLOT_IDX, DSR_NSLOTS };
+void *dsr_scratch(int slot, size_t bytes);
+
+int dsr_h2d(void *dst, const void *src, size_t n);
+int dsr_d2h(void *dst, const void *src, size_t n); /* synchronises the stream */
+
+/* Device copy of an INT8 block, uploaded on first use (keyed by the qweight host pointer plus a
+ * sampled fingerprint of the host arrays, so a reused host address is detected). */
+typedef struct {
+  int8_t *q;
+  float *scale;
+  float *offset;
+  int out_dim, in_dim;
+} dsr_dblock_t;
+int dsr_block_device(const ds_int4_block_t *b, dsr_dblock_t *out);
+/* Allocates and registers device arrays for a block the device is about to produce; after the host
+ * arrays are filled, dsr_block_adopt() records their fingerprint. */
+int dsr_block_new(const ds_int4_block_t *b, dsr_dblock_t *out);
+int dsr_block_adopt(const ds_int4_block_t *b, int8_t *q, float *scale, float *offset);
+void dsr_block_forget(const void *qweight);
+
+/* Device copy of a host weight array (bf16 / f32), uploaded on first use, same keying. */
+const void *dsr_weight_device(const void *host, size_t bytes);
+
+/* Emulated reference CPU thread count (ds_set_threads). */
+int dsr_threads(void);
+
+#endif

@@ -1,0 +1,344 @@
+/* runtime.c — device/stream bring-up, error reporting, staging buffers and the host->device weight
+ * registry of libds_ocr_hip. The registry plays the role of the Metal backend's
+ * ds_metal_register_expert_block (reference ds_metal.m:244-258): weights are uploaded once and
+ * stay resident. */
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "dsr.h"
+#include "ds_hip.h"
+#include "ds_kernels.h"
+
+/* Mode globals; the reference defines them in ds_ocr.c:26-27, which wins when linked. */
+__attribute__((weak)) int ds_verbose = 0;
+__attribute__((weak)) int ds_bf16_simulate_python = 0;
+
+hipStream_t dsr_stream = NULL;
+static int g_init = 0; /* 0 = not tried, 1 = ok, -1 = failed */
+static char g_err[512] = "";
+static int g_threads = 1;
+
+int dsr_failf(const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  fprintf(stderr, "ds_ocr_hip: %s\n", g_err);
+  return -1;
+}
+
+int dsr_fail(const char *what, hipError_t e) { return dsr_failf("%s: %s", what, hipGetErrorString(e)); }
+
+const char *ds_hip_last_error(void) { return g_err; }
+
+int dsr_init(void) {
+  if (g_init == 1) return 0;
+  if (g_init == -1) return dsr_failf("HIP device unavailable (initialisation failed earlier)");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n < 1) {
+    g_init = -1;
+    return dsr_failf("no HIP device: %s", e != hipSuccess ? hipGetErrorString(e) : "device count is 0");
+  }
+  e = hipSetDevice(0);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&dsr_stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    g_init = -1;
+    return dsr_fail("HIP init", e);
+  }
+  g_init = 1;
+  return 0;
+}
+
+int ds_hip_init(void) { return dsr_init(); }
+
+/* ---------------------------------------------------------------- staging */
+
+static void *g_slot[DSR_NSLOTS];
+static size_t g_slot_cap[DSR_NSLOTS];
+
+void *dsr_scratch(int slot, size_t bytes) {
+  if (bytes == 0) bytes = 16;
+  if (bytes <= g_slot_cap[slot]) return g_slot[slot];
+  if (g_slot[slot]) {
+    hipStreamSynchronize(dsr_stream);
+    hipFree(g_slot[slot]);
+    g_slot[slot] = NULL;
+    g_slot_cap[slot] = 0;
+  }
+  size_t cap = bytes < 65536 ? 65536 : bytes + bytes / 4;
+  void *p = NULL;
+  hipError_t e = hipMalloc(&p, cap);
+  if (e != hipSuccess) {
+    dsr_fail("staging allocation", e);
+    return NULL;
+  }
+  g_slot[slot] = p;
+  g_slot_cap[slot] = cap;
+  return p;
+}
+
+int dsr_h2d(void *dst, const void *src, size_t n) {
+  if (n == 0) return 0;
+  DSR_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, dsr_stream), "copy to device");
+  return 0;
+}
+
+int dsr_d2h(void *dst, const void *src, size_t n) {
+  if (n) DSR_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, dsr_stream), "copy to host");
+  DSR_TRY(hipStreamSynchronize(dsr_stream), "stream synchronize");
+  return 0;
+}
+
+/* ---------------------------------------------------------------- registry */
+
+static uint64_t fnv(uint64_t h, const void *p, size_t n) {
+  const unsigned char *b = (const unsigned char *)p;
+  for (size_t i = 0; i < n; i++) h = (h ^ b[i]) * 1099511628211ull;
+  return h;
+}
+
+/* Hash of the length, the first and last 256 bytes and 64 evenly spaced 8-byte samples. */
+static uint64_t fingerprint(const void *p, size_t n) {
+  const unsigned char *b = (const unsigned char *)p;
+  uint64_t h = fnv(1469598103934665603ull, &n, sizeof n);
+  if (n <= 1024) return fnv(h, b, n);
+  h = fnv(h, b, 256);
+  h = fnv(h, b + n - 256, 256);
+  for (int i = 0; i < 64; i++) {
+    size_t off = (n - 8) / 64 * (size_t)i;
+    h = fnv(h, b + off, 8);
+  }
+  return h;
+}
+
+typedef struct {
+  const void *key;
+  uint64_t fp;
+  size_t bytes;
+  void *dev; /* weights: the copy; blocks: q (scale, offset follow in sdev/odev) */
+  float *sdev, *odev;
+  int out_dim, in_dim;
+  int is_block;
+} entry_t;
+
+static entry_t *g_ent = NULL;
+static int g_nent = 0, g_cap = 0;
+
+static entry_t *find(const void *key, int is_block) {
+  for (int i = 0; i < g_nent; i++)
+    if (g_ent[i].key == key && g_ent[i].is_block == is_block) return &g_ent[i];
+  return NULL;
+}
+
+static void drop(entry_t *e) {
+  hipStreamSynchronize(dsr_stream);
+  if (e->dev) hipFree(e->dev);
+  *e = g_ent[--g_nent];
+}
+
+static entry_t *add(void) {
+  if (g_nent == g_cap) {
+    int nc = g_cap ? 2 * g_cap : 64;
+    entry_t *ne = (entry_t *)realloc(g_ent, (size_t)nc * sizeof(entry_t));
+    if (!ne) return NULL;
+    g_ent = ne;
+    g_cap = nc;
+  }
+  entry_t *e = &g_ent[g_nent++];
+  memset(e, 0, sizeof *e);
+  return e;
+}
+
+static uint64_t block_fp(const ds_int4_block_t *b) {
+  size_t nq = (size_t)b->out_dim * b->in_dim;
+  uint64_t h = fingerprint(b->qweight, nq);
+  h = fnv(h, b->scale, (size_t)b->out_dim * 4);
+  h = fnv(h, b->offset, (size_t)b->out_dim * 4);
+  h = fnv(h, &b->out_dim, sizeof(int));
+  return fnv(h, &b->in_dim, sizeof(int));
+}
+
+/* One allocation per block: codes, then scales, then offsets (each 256-byte aligned). */
+static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+static int block_alloc(entry_t *e, int out_dim, int in_dim) {
+  size_t nq = al256((size_t)out_dim * in_dim), ns = al256((size_t)out_dim * 4);
+  void *p = NULL;
+  DSR_TRY(hipMalloc(&p, nq + 2 * ns), "block allocation");
+  e->dev = p;
+  e->sdev = (float *)((char *)p + nq);
+  e->odev = (float *)((char *)p + nq + ns);
+  e->out_dim = out_dim;
+  e->in_dim = in_dim;
+  e->is_block = 1;
+  return 0;
+}
+
+int dsr_block_device(const ds_int4_block_t *b, dsr_dblock_t *out) {
+  if (dsr_init()) return -1;
+  uint64_t fp = block_fp(b);
+  entry_t *e = find(b->qweight, 1);
+  if (e && (e->fp != fp || e->out_dim != b->out_dim || e->in_dim != b->in_dim)) {
+    drop(e);
+    e = NULL;
+  }
+  if (!e) {
+    e = add();
+    if (!e) return dsr_failf("registry allocation failed");
+    if (block_alloc(e, b->out_dim, b->in_dim)) {
+      g_nent--;
+      return -1;
+    }
+    e->key = b->qweight;
+    e->fp = fp;
+    if (dsr_h2d(e->dev, b->qweight, (size_t)b->out_dim * b->in_dim) ||
+        dsr_h2d(e->sdev, b->scale, (size_t)b->out_dim * 4) || dsr_h2d(e->odev, b->offset, (size_t)b->out_dim * 4)) {
+      drop(e);
+      return -1;
+    }
+  }
+  out->q = (int8_t *)e->dev;
+  out->scale = e->sdev;
+  out->offset = e->odev;
+  out->out_dim = e->out_dim;
+  out->in_dim = e->in_dim;
+  return 0;
+}
+
+/* Allocates the device arrays of a block about to be produced on the device. */
+int dsr_block_new(const ds_int4_block_t *b, dsr_dblock_t *out) {
+  if (dsr_init()) return -1;
+  entry_t *e = find(b->qweight, 1);
+  if (e) drop(e);
+  e = add();
+  if (!e) return dsr_failf("registry allocation failed");
+  if (block_alloc(e, b->out_dim, b->in_dim)) {
+    g_nent--;
+    return -1;
+  }
+  e->key = b->qweight;
+  out->q = (int8_t *)e->dev;
+  out->scale = e->sdev;
+  out->offset = e->odev;
+  out->out_dim = b->out_dim;
+  out->in_dim = b->in_dim;
+  return 0;
+}
+
+/* Seals a block produced by dsr_block_new once its host arrays hold the same values. */
+int dsr_block_adopt(const ds_int4_block_t *b, int8_t *q, float *scale, float *offset) {
+  (void)q;
+  (void)scale;
+  (void)offset;
+  entry_t *e = find(b->qweight, 1);
+  if (!e) return dsr_failf("internal: block not registered");
+  e->fp = block_fp(b);
+  return 0;
+}
+
+void dsr_block_forget(const void *qweight) {
+  if (!qweight) return;
+  entry_t *e = find(qweight, 1);
+  if (e) drop(e);
+}
+
+const void *dsr_weight_device(const void *host, size_t bytes) {
+  if (dsr_init()) return NULL;
+  uint64_t fp = fingerprint(host, bytes);
+  entry_t *e = find(host, 0);
+  if (e && (e->fp != fp || e->bytes != bytes)) {
+    drop(e);
+    e = NULL;
+  }
+  if (e) return e->dev;
+  e = add();
+  if (!e) {
+    dsr_failf("registry allocation failed");
+    return NULL;
+  }
+  void *p = NULL;
+  hipError_t err = hipMalloc(&p, bytes ? bytes : 16);
+  if (err != hipSuccess) {
+    g_nent--;
+    dsr_fail("weight allocation", err);
+    return NULL;
+  }
+  e->key = host;
+  e->fp = fp;
+  e->bytes = bytes;
+  e->dev = p;
+  if (dsr_h2d(p, host, bytes)) {
+    drop(e);
+    return NULL;
+  }
+  return p;
+}
+
+/* ---------------------------------------------------------------- threads */
+
+/* ds_kernels.c:517-543: clamp to [1, 16]. */
+void ds_set_threads(int n) {
+  if (n < 1) n = 1;
+  if (n > 16) n = 16;
+  g_threads = n;
+}
+int ds_get_threads(void) { return g_threads; }
+int dsr_threads(void) { return g_threads; }
+
+#include <unistd.h>
+int ds_get_num_cpus(void) {
+  long n = sysconf(_SC_NPROCESSORS_ONLN);
+  return n > 0 ? (int)n : 1;
+}
+
+void ds_dispatch_ensure_init(void) { (void)dsr_init(); }
+
+void ds_parallel_for(ds_parallel_fn_t fn, void *arg) {
+  if (fn) fn(0, 1, arg);
+}
+
+/* ---------------------------------------------------------------- public memory helpers */
+
+void *ds_hip_malloc(size_t bytes) {
+  if (dsr_init()) return NULL;
+  void *p = NULL;
+  hipError_t e = hipMalloc(&p, bytes ? bytes : 16);
+  if (e != hipSuccess) {
+    dsr_fail("ds_hip_malloc", e);
+    return NULL;
+  }
+  return p;
+}
+
+void ds_hip_free(void *p) {
+  if (!p || g_init != 1) return;
+  hipStreamSynchronize(dsr_stream);
+  hipFree(p);
+}
+
+int ds_hip_memcpy_h2d(void *dst, const void *src, size_t n) {
+  if (dsr_init()) return -1;
+  if (dsr_h2d(dst, src, n)) return -1;
+  DSR_TRY(hipStreamSynchronize(dsr_stream), "synchronize");
+  return 0;
+}
+
+int ds_hip_memcpy_d2h(void *dst, const void *src, size_t n) {
+  if (dsr_init()) return -1;
+  return dsr_d2h(dst, src, n);
+}
+
+int ds_hip_memcpy_d2d(void *dst, const void *src, size_t n) {
+  if (dsr_init()) return -1;
+  if (n) DSR_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, dsr_stream), "device copy");
+  return 0;
+}
+
+int ds_hip_sync(void) {
+  if (dsr_init()) return -1;
+  DSR_TRY(hipStreamSynchronize(dsr_stream), "synchronize");
+  return 0;
+}

@@ -1,0 +1,111 @@
+/*
+ * ds_hip.h — device-resident extension of the ds-ocr MoE decode API (MI355X / gfx950).
+ *
+ * The per-function API of ds_quantize.h / ds_kernels.h takes host pointers and synchronises on
+ * every call, like the reference. A decode step at batch 1 moves ~640 MB in ~100 us on MI355X, so
+ * the fast path keeps weights and activations in HBM: a layer handle owns one contiguous arena per
+ * MoE layer (all experts' codes, scales/offsets, routers), and a stack handle runs all MoE layers
+ * plus the argmax LM head as one captured HIP graph per decode step. This has no counterpart in the
+ * reference (whose MoE block, ds_moe_decoder.c:131-333 moe_forward, is a static function); it is
+ * the additive C-ABI entry the integration calls instead of the per-expert functions.
+ *
+ * Conventions: functions returning int return 0 on success and -1 on failure, with the message in
+ * ds_hip_last_error() (also printed to stderr). "_dev" pointers are device pointers. All work is
+ * ordered on the library's single stream; ds_hip_sync() waits for it.
+ */
+#ifndef DS_HIP_H
+#define DS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ds_quantize.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------- runtime ---------------- */
+int ds_hip_init(void);
+const char *ds_hip_last_error(void);
+void *ds_hip_malloc(size_t bytes);
+void ds_hip_free(void *p_dev);
+int ds_hip_memcpy_h2d(void *dst_dev, const void *src, size_t bytes);
+int ds_hip_memcpy_d2h(void *dst, const void *src_dev, size_t bytes);
+int ds_hip_memcpy_d2d(void *dst_dev, const void *src_dev, size_t bytes);
+int ds_hip_sync(void);
+/* Seeded synthetic data generated on the device (counter-based SplitMix64 + Box–Muller). */
+int ds_hip_fill_normal_bf16(uint16_t *dst_dev, size_t n, uint64_t seed, float std_);
+int ds_hip_fill_normal_f32(float *dst_dev, size_t n, uint64_t seed, float mean, float std_);
+
+/* ---------------- device-pointer kernels ---------------- */
+int ds_hip_quantize_bf16(int8_t *q_dev, float *scale_dev, float *offset_dev, const uint16_t *W_dev, int out_dim,
+                         int in_dim);
+int ds_hip_int8_matvec(float *y_dev, const float *x_dev, const int8_t *q_dev, const float *scale_dev,
+                       const float *offset_dev, int in_dim, int row_start, int nrows);
+/* Argmax of W x (bf16 W [out_dim, in_dim]) in the reference's order for ds_get_threads() threads;
+ * writes the index to *idx_dev. */
+int ds_hip_argmax_bf16(int *idx_dev, const float *x_dev, const uint16_t *W_dev, int in_dim, int out_dim);
+
+/* ---------------- device-resident MoE layer ---------------- */
+enum { DS_HIP_ROUTE_DECODE = 0, DS_HIP_ROUTE_CFG = 1 };
+/* DS_HIP_ROUTE_DECODE: the reference decode router (bf16 weights, fast-exp softmax over all
+ *   experts, top-k, weights = probabilities; ds_moe_decoder.c:145-183).
+ * DS_HIP_ROUTE_CFG: f32 router + ds_moe_top_k (top-k on raw scores, softmax over the k). */
+
+typedef struct ds_hip_layer ds_hip_layer_t;
+
+/* shared_inter = n_shared * inter (the shared experts' fused gate_up is [2*shared_inter, hidden]). */
+ds_hip_layer_t *ds_hip_layer_create(int hidden, int inter, int n_experts, int top_k, int shared_inter);
+void ds_hip_layer_destroy(ds_hip_layer_t *L);
+size_t ds_hip_layer_bytes(const ds_hip_layer_t *L);
+/* Host router weights [n_experts, hidden]; either may be NULL. */
+int ds_hip_layer_set_router(ds_hip_layer_t *L, const float *router_f32, const uint16_t *router_bf16);
+/* Router weights already on the device (copied into the arena). */
+int ds_hip_layer_set_router_dev(ds_hip_layer_t *L, const float *router_f32_dev, const uint16_t *router_bf16_dev);
+/* Copies host INT8 blocks into the arena. e in [0, n_experts) or -1 for the shared expert.
+ * gate_up is [2*I, hidden] (gate rows then up rows), down is [hidden, I]. */
+int ds_hip_layer_set_expert(ds_hip_layer_t *L, int e, const ds_int4_block_t *gate_up, const ds_int4_block_t *down);
+/* Quantizes device BF16 weights straight into the arena (bit-identical to ds_int4_quantize_bf16). */
+int ds_hip_layer_quantize_expert(ds_hip_layer_t *L, int e, const uint16_t *gate_up_bf16_dev,
+                                 const uint16_t *down_bf16_dev);
+/* Copies an expert's codes/scales/offsets back to host arrays (any pointer may be NULL). */
+int ds_hip_layer_export_expert(const ds_hip_layer_t *L, int e, int8_t *gu_q, float *gu_scale, float *gu_offset,
+                               int8_t *dn_q, float *dn_scale, float *dn_offset);
+/* out_dev[hidden] = (residual ? x : 0) + MoE(x_dev). idx_dev/w_dev (optional, [top_k]) receive the
+ * routing. bf16sim follows ds_bf16_simulate_python. Asynchronous. out_dev may equal x_dev. */
+int ds_hip_layer_forward(ds_hip_layer_t *L, float *out_dev, const float *x_dev, int route_mode, int residual,
+                         int *idx_dev, float *w_dev);
+
+/* ---------------- decode stack: n MoE layers + argmax LM head ---------------- */
+typedef struct ds_hip_stack ds_hip_stack_t;
+
+/* lm_head_dev: bf16 [vocab, hidden] on the device (borrowed). Layers are borrowed. */
+ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers, const uint16_t *lm_head_dev,
+                                    int vocab, int route_mode);
+void ds_hip_stack_destroy(ds_hip_stack_t *S);
+/* Step s reads its input hidden state from xs_dev + s*stride (stride 0: always xs_dev) and writes
+ * its token to tokens_dev[s]; s is a device counter advanced by every step. Captures the graph. */
+int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int *tokens_dev);
+int ds_hip_stack_reset(ds_hip_stack_t *S);
+/* Launches n_steps decode steps (one graph launch each), asynchronously. */
+int ds_hip_stack_run(ds_hip_stack_t *S, int n_steps);
+/* Same steps launched kernel by kernel, without the graph. */
+int ds_hip_stack_run_eager(ds_hip_stack_t *S, int n_steps);
+/* Final hidden state (after the last MoE layer) of the most recent step, to the host. */
+int ds_hip_stack_hidden(ds_hip_stack_t *S, float *x_host);
+size_t ds_hip_stack_bytes_per_step(const ds_hip_stack_t *S);
+
+/* ---------------- timing (HIP events on the library stream) ---------------- */
+/* Wall time of n_steps graph launches. */
+int ds_hip_time_stack(ds_hip_stack_t *S, int n_steps, float *ms);
+/* Per-kernel durations over n_steps eager steps, events around every kernel. ms_out receives
+ * 3*n_layers + 2 averages: for each layer scores, gate_up, down; then the LM-head partial and
+ * final kernels. */
+int ds_hip_profile_stack(ds_hip_stack_t *S, int n_steps, float *ms_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DS_HIP_H */
