@@ -17,6 +17,20 @@ i8p = np.ctypeslib.ndpointer(dtype=np.int8, flags="C_CONTIGUOUS")
 i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
 
 
+class _Optional:
+    """ctypes argument type: a contiguous ndarray of one dtype, or None (NULL)."""
+
+    def __init__(self, nd):
+        self.nd = nd
+
+    def from_param(self, obj):
+        return None if obj is None else self.nd.from_param(obj)
+
+
+f32p_opt = _Optional(f32p)
+i32p_opt = _Optional(i32p)
+
+
 class OrBlock(C.Structure):
     _fields_ = [("q", C.c_void_p), ("scale", C.c_void_p), ("offset", C.c_void_p),
                 ("out_dim", C.c_int), ("in_dim", C.c_int)]
@@ -57,7 +71,8 @@ def _load_oracle():
         "or_expert_int8": (None, [f32p, f32p, C.POINTER(OrBlock), C.POINTER(OrBlock), C.c_int, C.c_int, C.c_int]),
         "or_expert_bf16": (None, [f32p, f32p, u16p, u16p, C.c_int, C.c_int, C.c_int, C.c_int]),
         "or_expert_combine": (None, [f32p, f32p, f32p, C.c_int, C.c_int]),
-        "or_moe_layer_decode": (None, [f32p, f32p, C.POINTER(OrLayer), C.c_int, C.c_int, C.c_int, i32p, f32p]),
+        "or_moe_layer_decode": (None, [f32p, f32p, C.POINTER(OrLayer), C.c_int, C.c_int, C.c_int, i32p_opt,
+                                       f32p_opt]),
         "or_prefill_route": (None, [i32p, f32p, f32p, C.c_int, C.POINTER(OrLayer), C.c_int]),
         "or_prefill_moe_f64": (None, [f64p, f32p, C.c_int, C.POINTER(OrLayer), i32p, f32p]),
     }
@@ -107,7 +122,7 @@ def ref(variant="v4"):
         "ref_layer_sizeof": (C.c_size_t, []),
         "ref_layer_init": (None, [vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp]),
         "ref_layer_set_expert": (None, [vp, C.c_int, i8p, f32p, f32p, i8p, f32p, f32p]),
-        "ref_moe_layer": (None, [f32p, f32p, vp, C.c_int, i32p, f32p]),
+        "ref_moe_layer": (None, [f32p, f32p, vp, C.c_int, i32p_opt, f32p_opt]),
         "ref_decode_steps": (C.c_double, [vp, C.c_int, u16p, C.c_int, f32p, C.c_int, C.c_int, i32p]),
         "ref_decode_hidden": (None, [f32p, vp, C.c_int, f32p, C.c_int]),
         "ds_set_threads": (None, [C.c_int]),
