@@ -55,13 +55,6 @@ def make_layer(dev, seed, gu, dn, rf, rb):
     return h
 
 
-def kernel_names():
-    names = []
-    for l in range(LAYERS):
-        names += [f"L{l}.scores", f"L{l}.gate_up", f"L{l}.down"]
-    return names + ["lm_head.argmax", "lm_head.final"]
-
-
 def host_layers(dev, handles, rf_host, rb_host):
     """Copies the device layers' INT8 blocks to the host (for the reference CPU baseline)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -177,17 +170,17 @@ def main():
 
     # per-kernel durations (eager launches with HIP events around every kernel)
     dev.check(L.ds_hip_stack_reset(S), "reset")
-    names = kernel_names()
-    per = np.zeros(len(names), np.float32)
+    nk = L.ds_hip_stack_kernel_count(S)
+    names = [L.ds_hip_stack_kernel_name(S, i).decode() for i in range(nk)]
+    per = np.zeros(nk, np.float32)
     dev.check(L.ds_hip_profile_stack(S, min(args.profile_steps, n_inputs), per), "profile")
     kinds = {}
-    for n_, v in zip(names, per):
-        k = n_.split(".", 1)[1]
+    for k, v in zip(names, per):
         kinds.setdefault(k, []).append(float(v))
     kernel_ms = {k: {"avg_ms": round(float(np.mean(v)), 5), "launches_per_step": len(v),
                      "ms_per_step": round(float(np.sum(v)), 5)} for k, v in kinds.items()}
     lm_bytes = VOCAB * H * 2
-    lm_ms = kernel_ms["argmax"]["avg_ms"]
+    lm_ms = kernel_ms["lm_head.argmax"]["avg_ms"]
     lm_gbs = lm_bytes / (lm_ms * 1e-3) / 1e9
     step_gbs = bytes_per_step / (ms_per_step * 1e-3) / 1e9
 
@@ -222,7 +215,7 @@ def main():
         "hbm": {"bytes_per_step": int(bytes_per_step), "achieved_gbs": round(step_gbs, 1),
                 "frac_of_peak": round(step_gbs / PEAK_HBM_GBS, 4), "peak_gbs": PEAK_HBM_GBS,
                 "wall_s_timed_region": round(wall, 4)},
-        "roofline": {"kernel": "k_lm_argmax (LM-head argmax, the largest kernel)", "bound": "hbm",
+        "roofline": {"kernel": "k_dec_lm_argmax (LM-head argmax, the largest kernel)", "bound": "hbm",
                      "achieved": round(lm_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(lm_gbs / PEAK_HBM_GBS, 4), "traffic": None,
                      "bytes_per_launch": lm_bytes, "avg_ms": lm_ms},

@@ -71,25 +71,27 @@ typedef struct {
   float *h;      /* [K*I + SI] SwiGLU outputs (routed slots, then shared) */
 } dsh_layer_work_t;
 
-/* Shapes the fused decode kernels support (otherwise the per-op path is used). */
-int dsh_moe_fast_shape(int H, int I, int E, int K, int SI);
-
-/* x_in + step_stride * (*step) is the layer input when step != NULL (device step counter). */
-hipError_t dsh_launch_moe_scores(const dsh_layer_t *L, const float *x_in, const int *step, int step_stride,
-                                 int route_mode, int nthreads, float *scores, hipStream_t s);
-hipError_t dsh_launch_moe_gate_up(const dsh_layer_t *L, const float *x_in, const int *step, int step_stride,
-                                  int route_mode, int bf16sim, const dsh_layer_work_t *wk, hipStream_t s);
-/* x_out = (residual ? x_in : 0) + MoE(x_in). x_out may alias x_in. */
-hipError_t dsh_launch_moe_down(const dsh_layer_t *L, const float *x_in, const int *step, int step_stride,
-                               float *x_out, int residual, int bf16sim, const dsh_layer_work_t *wk, hipStream_t s);
-
-/* LM-head argmax: per-block (max, lowest index) candidates, then a final reduction that writes
- * tokens[*step] (tokens[0] when step is NULL) and advances *step. The fast partial kernel needs
- * in_dim % 32 == 0, 16-byte aligned rows, and every row in the 2-accumulator order. */
-int dsh_lm_argmax_blocks(int vocab);
-hipError_t dsh_launch_lm_argmax_partial(const uint16_t *W, const float *x, int in_dim, int vocab,
-                                        unsigned long long *cand, hipStream_t s);
+/* Final reduction of per-block argmax candidates: writes tokens[*step] (tokens[0] when step is
+ * NULL) and advances *step. */
 hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int *tokens, int *step, hipStream_t s);
+
+/* ---- latency-oriented decode kernels (k_dec.hip) ---- */
+int dsh_dec_supported(int H, int I, int E, int K, int SI);
+int dsh_dec_partials(int H); /* partial score rows written per layer in CFG mode */
+hipError_t dsh_launch_dec_partial_scores(const float *Wr, const float *x_in, const int *step, int stride, int H, int E,
+                                         float *partials, hipStream_t s);
+hipError_t dsh_launch_dec_scores_bf16(const uint16_t *Wr, const float *x_in, const int *step, int stride, int H, int E,
+                                      int nthreads, float *partials, hipStream_t s);
+hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const int *step, int stride,
+                                  const float *partials, int np, int route_mode, int bf16sim,
+                                  const dsh_layer_work_t *wk, hipStream_t s);
+hipError_t dsh_launch_dec_down(const dsh_layer_t *L, const float *x_in, const int *step, int stride, float *x_out,
+                               int residual, int bf16sim, const dsh_layer_work_t *wk, const float *Wr_next,
+                               int E_next, float *partials_next, hipStream_t s);
+int dsh_dec_lm_blocks(int vocab);
+int dsh_dec_lm_supported(int in_dim);
+hipError_t dsh_launch_dec_lm_argmax(const uint16_t *W, const float *x, int in_dim, int vocab,
+                                    unsigned long long *cand, hipStream_t s);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,543 @@
+// k_dec.hip — latency-oriented decode kernels (batch 1) for the device-resident MoE layer and stack.
+//
+// Per MoE layer two kernels run back to back on one stream:
+//   gate_up : routing (reduction of router partial scores, softmax/top-k) + fused gate_up INT8
+//             dequant-matvec + SwiGLU for the top-k routed experts and the shared expert
+//             (ds_moe_decoder.c:145-183 routing, ds_quantize.c:301-318 first half of the expert)
+//   down    : down INT8 dequant-matvec of every selected expert and the shared expert, combine in
+//             top-k order, shared add, residual (ds_quantize.c:319-320, ds_kernels.c:359-371,
+//             ds_moe_decoder.c:278, :468); it also emits the next layer's router partial scores
+//             (scores are linear in x, so Wr·x = Σ_blocks Wr[:, rows]·x[rows]).
+// The first layer's partial scores come from a small kernel; in DECODE routing mode (bf16 router in
+// the reference's exact AVX-512 order) a scores kernel writes the full scores as a single partial.
+//
+// Every load phase is branch-free with all of its loads issued before the first use, so each
+// kernel costs one memory round trip plus its transfer time.
+#include "dsh_avx.h"
+#include "k_core.h"
+
+__device__ __forceinline__ float2 so_pair(const float *so, size_t i) { return ((const float2 *)so)[i]; }
+
+__device__ __forceinline__ const float *at_step(const float *x, const int *step, int stride) {
+  return step ? x + (size_t)(*step) * stride : x;
+}
+
+__device__ __forceinline__ void load_f16x(const float *p, float *o) {
+#pragma unroll
+  for (int d = 0; d < 4; d++) {
+    f32x4 t = *(const f32x4 *)(p + 4 * d);
+    o[4 * d] = t[0];
+    o[4 * d + 1] = t[1];
+    o[4 * d + 2] = t[2];
+    o[4 * d + 3] = t[3];
+  }
+}
+
+// ============================================================================ routing in a block
+// All four waves reduce the NP partial score vectors (fixed order: wave w sums rows w, w+4, ...,
+// then the four sums are added in wave order), then wave 0 routes. Writes s_idx/s_w in LDS.
+template <int NW>
+__device__ void block_route(const float *__restrict__ partials, int np, int E, int K, int mode, int *s_idx,
+                            float *s_w, float (*s_red)[64]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float acc = 0.0f;
+  if (lane < E) {
+    int b = wave;
+    // batches of 8 loads issued together
+    for (; b + 7 * NW < np; b += 8 * NW) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = partials[(size_t)(b + j * NW) * 64 + lane];
+#pragma unroll
+      for (int j = 0; j < 8; j++) acc += v[j];
+    }
+    for (; b < np; b += NW) acc += partials[(size_t)b * 64 + lane];
+  }
+  s_red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    float s = s_red[0][lane];
+#pragma unroll
+    for (int w = 1; w < NW; w++) s += s_red[w][lane];
+    // route (same semantics as k_core.hip's helpers), lane e holds expert e's score
+    bool taken = false;
+    if (mode == DSH_ROUTE_CFG) {
+      int my_sel = 0, ns = 0;
+      float my_ss = 0.0f;
+      for (int t = 0; t < K; t++) {
+        unsigned long long key = (lane < E && !taken) ? dsh_argmax_key(s, lane) : 0ull;
+        key = dsh_wave_max_u64(key);
+        if (key == 0ull) continue;
+        int e = dsh_key_index(key);
+        if (lane == e) taken = true;
+        if (lane == ns) {
+          my_sel = e;
+          my_ss = dsh_key_value(key);
+        }
+        ns++;
+      }
+      float mx = -1e30f;
+      for (int j = 0; j < ns; j++) {
+        float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_ss), j));
+        if (v > mx) mx = v;
+      }
+      float ev = lane < ns ? expf(my_ss - mx) : 0.0f;
+      float sum = 0.0f;
+      for (int j = 0; j < ns; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j));
+      float inv = 1.0f / sum;
+      if (lane < K) {
+        s_idx[lane] = lane < ns ? my_sel : 0;
+        s_w[lane] = lane < ns ? ev * inv : 0.0f;
+      }
+    } else {
+      float m = (lane < E && s > -1e30f) ? s : -1e30f;
+      m = dsh_wave_max(m);
+      float p = lane < E ? dsh_fast_expf(s - m) : 0.0f;
+      float sum = 0.0f;
+      for (int e = 0; e < E; e++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), e));
+      float inv = 1.0f / sum;
+      p = p * inv;
+      int my_sel = -1;
+      float my_w = -1e30f;
+      for (int t = 0; t < K; t++) {
+        unsigned long long key = (lane < E && !taken) ? dsh_argmax_key(p, lane) : 0ull;
+        key = dsh_wave_max_u64(key);
+        int e = key == 0ull ? -1 : dsh_key_index(key);
+        if (lane == e) taken = true;
+        if (lane == t) {
+          my_sel = e;
+          my_w = key == 0ull ? -1e30f : dsh_key_value(key);
+        }
+      }
+      if (lane < K) {
+        s_idx[lane] = my_sel;
+        s_w[lane] = my_w;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// ============================================================================ partial scores
+// partials[b][e] = Σ_{r in rows of block b} Wr[e][r] * x[r] for R consecutive rows per block
+// (f32 router, CFG mode); the row order inside a block is sequential.
+template <int R>
+__global__ void __launch_bounds__(64) k_dec_partial_scores(const float *__restrict__ Wr, const float *__restrict__ x_in,
+                                                           const int *__restrict__ step, int stride, int H, int E,
+                                                           float *__restrict__ partials) {
+  const float *x = at_step(x_in, step, stride);
+  const int lane = threadIdx.x, r0 = blockIdx.x * R;
+  float p = 0.0f;
+  if (lane < E) {
+    float w[R], xv[R];
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+      w[j] = Wr[(size_t)lane * H + r0 + j];
+      xv[j] = x[r0 + j];
+    }
+#pragma unroll
+    for (int j = 0; j < R; j++) p = __builtin_fmaf(w[j], xv[j], p);
+  }
+  partials[(size_t)blockIdx.x * 64 + lane] = lane < E ? p : 0.0f;
+}
+
+// DECODE mode: full scores in the reference's AVX-512 order, written as the single partial.
+__global__ void __launch_bounds__(64) k_dec_scores_bf16(const uint16_t *__restrict__ Wr, const float *__restrict__ x_in,
+                                                        const int *__restrict__ step, int stride, int H, int E,
+                                                        int chunk, float *__restrict__ partials) {
+  extern __shared__ float xs[];
+  const float *x = at_step(x_in, step, stride);
+  for (int i = threadIdx.x; i < H; i += 64) xs[i] = x[i];
+  __syncthreads();
+  const int L = threadIdx.x & 3;
+  const int e = blockIdx.x * 16 + (threadIdx.x >> 2);
+  if (e >= E) return;
+  int path = row_path(e, E, chunk, false);
+  float v = avx_row<true>(Wr + (size_t)e * H, xs, H, L, path == DSH_ROW_SINGLE, true, 0.0f, path != DSH_ROW_GROUP4);
+  if (L == 0) partials[e] = v;
+}
+
+// ============================================================================ gate_up + SwiGLU
+// 16 units per 256-thread block (4 per wave, 16 lanes per unit). Unit u < SI: shared expert row
+// pair (u, SI+u); u >= SI: routed slot k = (u-SI)/I, intermediate i. Lane sub of a unit reads the
+// 16-byte chunks sub + 16m (m < CPL) of both rows. Requires H == 256*CPL.
+template <int CPL>
+__global__ void __launch_bounds__(256) k_dec_gate_up(dsh_layer_t L, const float *__restrict__ x_in,
+                                                     const int *__restrict__ step, int stride,
+                                                     const float *__restrict__ partials, int np, int mode, int bf16sim,
+                                                     dsh_layer_work_t wk) {
+  __shared__ int s_idx[64];
+  __shared__ float s_w[64];
+  __shared__ float s_red[4][64];
+  const float *x = at_step(x_in, step, stride);
+  const int H = L.H, I = L.I, K = L.K, SI = L.SI;
+  const int lane = threadIdx.x & 63, sub = lane & 15;
+  const int unit0 = blockIdx.x * 16;
+  const int u = unit0 + (threadIdx.x >> 4);
+  const bool shared_block = unit0 + 15 < SI;
+
+  // x chunks (independent of routing)
+  float xv[CPL][16];
+#pragma unroll
+  for (int m = 0; m < CPL; m++) load_f16x(x + 16 * (sub + 16 * m), xv[m]);
+
+  const int8_t *grow, *urow;
+  float2 sog, sou;
+  int hpos;
+  bool live = true;
+  if (shared_block) {
+    grow = L.sgu_q + (size_t)u * H;
+    urow = L.sgu_q + (size_t)(SI + u) * H;
+    hpos = K * I + u;
+  } else {
+    block_route<4>(partials, np, L.E, K, mode, s_idx, s_w, s_red);
+    if (unit0 <= SI && SI < unit0 + 16 && threadIdx.x < K) {  // this block publishes the routing
+      wk.idx[threadIdx.x] = s_idx[threadIdx.x];
+      wk.w[threadIdx.x] = s_w[threadIdx.x];
+    }
+    int r = u - SI;
+    int total_routed = K * I;
+    live = r < total_routed;
+    r = live ? r : 0;
+    int k = r / I, i = r - k * I;
+    int e = s_idx[k];
+    hpos = r;
+    if (e < 0) {
+      live = false;
+      e = 0;
+      if (sub == 0 && u - SI < total_routed) wk.h[hpos] = 0.0f;
+    }
+    size_t base = (size_t)e * 2 * I;
+    grow = L.gu_q + (base + i) * H;
+    urow = L.gu_q + (base + I + i) * H;
+    if (u - SI >= total_routed) return;
+  }
+  u32x4 wg[CPL], wu[CPL];
+#pragma unroll
+  for (int m = 0; m < CPL; m++) {
+    wg[m] = dsh_load_nt(grow + 16 * (sub + 16 * m));
+    wu[m] = dsh_load_nt(urow + 16 * (sub + 16 * m));
+  }
+  if (shared_block) {
+    sog = so_pair(L.sgu_so, u);
+    sou = so_pair(L.sgu_so, SI + u);
+  } else {
+    int r = u - SI, k = r / I, i = r - k * I;
+    int e = max(s_idx[k], 0);
+    size_t base = (size_t)e * 2 * I;
+    sog = so_pair(L.gu_so, base + i);
+    sou = so_pair(L.gu_so, base + I + i);
+  }
+  float xpart = 0.0f;
+#pragma unroll
+  for (int m = 0; m < CPL; m++) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) s += xv[m][j];
+    xpart += s;
+  }
+  float dg = 0.0f, du = 0.0f;
+#pragma unroll
+  for (int m = 0; m < CPL; m++) {
+    dg = dsh_dot16_u8(wg[m], xv[m], dg);
+    du = dsh_dot16_u8(wu[m], xv[m], du);
+  }
+  const float xsum = dsh_row16_sum(xpart);
+  dg = dsh_row16_sum(dg);
+  du = dsh_row16_sum(du);
+  if (sub == 0 && live) {
+    float g = __builtin_fmaf(sog.x, dg, sog.y * xsum);
+    float up = __builtin_fmaf(sou.x, du, sou.y * xsum);
+    if (bf16sim) {
+      g = dsh_bf16_round_half_up(g);
+      up = dsh_bf16_round_half_up(up);
+    }
+    float hv = dsh_swiglu(g, up);
+    if (bf16sim) hv = dsh_bf16_round_half_up(hv);
+    wk.h[hpos] = hv;
+  }
+}
+
+// ============================================================================ down + combine
+// One 512-thread block per R output rows; wave s (0..7) owns segment s: routed slot s for s < K,
+// else the shared expert's I-wide column block s-K. Lane j < I/16 holds the 16 h values of chunk j
+// in registers and streams chunk j of each of its R rows (one 16-byte load per row, all issued
+// together). Per row the wave sums its lanes; wave 0 then combines the 8 segments per row in the
+// reference's order and, when Wr_next is given, writes this block's partial router scores for the
+// next layer. Requires I % 16 == 0, I/16 <= 64, K + SI/I == 8, H % R == 0.
+template <int R>
+__global__ void __launch_bounds__(512) k_dec_down(dsh_layer_t L, const float *__restrict__ x_in,
+                                                  const int *__restrict__ step, int stride, float *__restrict__ x_out,
+                                                  int residual, int bf16sim, dsh_layer_work_t wk,
+                                                  const float *__restrict__ Wr_next, int E_next,
+                                                  float *__restrict__ partials_next) {
+  __shared__ float s_val[8][R];
+  __shared__ float s_hs[8];
+  __shared__ float s_x[R];
+  const float *x = at_step(x_in, step, stride);
+  const int H = L.H, I = L.I, K = L.K, SI = L.SI;
+  const int lane = threadIdx.x & 63, seg = threadIdx.x >> 6;
+  const int CI = I >> 4;
+  const int r0 = blockIdx.x * R;
+  const bool lane_on = lane < CI;
+  const int ch = lane_on ? lane : 0;
+
+  // next layer's router columns for these rows (independent of everything else)
+  float wr[R];
+  if (Wr_next && seg == 0 && lane < E_next) {
+#pragma unroll
+    for (int j = 0; j < R; j++) wr[j] = Wr_next[(size_t)lane * H + r0 + j];
+  }
+  int e = -2;
+  const int8_t *wbase;
+  size_t so_base;
+  int row_stride;
+  if (seg < K) {
+    e = wk.idx[seg];
+    int ee = e < 0 ? 0 : e;
+    wbase = L.dn_q + (size_t)ee * H * I;
+    so_base = (size_t)ee * H;
+    row_stride = I;
+  } else {
+    wbase = L.sdn_q + (size_t)(seg - K) * I;
+    so_base = 0;
+    row_stride = SI;
+  }
+  // weights of the R rows, then this lane's h chunk
+  u32x4 wv[R];
+#pragma unroll
+  for (int j = 0; j < R; j++) wv[j] = dsh_load_nt(wbase + (size_t)(r0 + j) * row_stride + 16 * ch);
+  const int hbase = seg < K ? seg * I : K * I + (seg - K) * I;
+  float hv[16];
+  load_f16x(wk.h + hbase + 16 * ch, hv);
+  float2 so = make_float2(0.0f, 0.0f);
+  if (lane < R) so = so_pair(seg < K ? L.dn_so : L.sdn_so, so_base + r0 + lane);
+
+  float hp = 0.0f;
+  if (lane_on) {
+#pragma unroll
+    for (int j = 0; j < 16; j++) hp += hv[j];
+  }
+  const float hs = dsh_wave_sum(hp);
+  float dots[R];
+#pragma unroll
+  for (int j = 0; j < R; j++) dots[j] = lane_on ? dsh_dot16_u8(wv[j], hv, 0.0f) : 0.0f;
+#pragma unroll
+  for (int j = 0; j < R; j++) dots[j] = dsh_wave_sum(dots[j]);
+  // lane j (< R) holds row j's dot and its (scale, offset)
+  float mine = 0.0f;
+#pragma unroll
+  for (int j = 0; j < R; j++)
+    if (lane == j) mine = dots[j];
+  if (lane < R) {
+    float v;
+    if (seg < K)
+      v = e >= 0 ? __builtin_fmaf(so.x, mine, so.y * hs) : 0.0f;  // e_k = scale*dot + off*Σh
+    else
+      v = mine;  // shared: raw dot, combined below with its sibling block
+    s_val[seg][lane] = v;
+  }
+  if (lane == 0) s_hs[seg] = hs;
+  __syncthreads();
+  if (seg == 0) {
+    float outv = 0.0f;
+    if (lane < R) {
+      const int r = r0 + lane;
+      for (int k = 0; k < K; k++) {
+        float v = s_val[k][lane];
+        if (bf16sim) v = dsh_bf16_round_half_up(v);
+        outv = __builtin_fmaf(wk.w[k], v, outv);
+      }
+      float sdot = 0.0f, shs = 0.0f;
+      for (int k = K; k < 8; k++) {
+        sdot += s_val[k][lane];
+        shs += s_hs[k];
+      }
+      float2 sso = so_pair(L.sdn_so, r);
+      float sh = __builtin_fmaf(sso.x, sdot, sso.y * shs);
+      if (bf16sim) sh = dsh_bf16_round_half_up(sh);
+      outv = outv + sh;
+      float xo = residual ? x[r] + outv : outv;
+      x_out[r] = xo;
+      s_x[lane] = xo;
+    }
+    if (Wr_next) {
+      // wave-local: lanes < R wrote s_x; make it visible to the other lanes of this wave
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      float p = 0.0f;
+      if (lane < E_next) {
+#pragma unroll
+        for (int j = 0; j < R; j++) p = __builtin_fmaf(wr[j], s_x[j], p);
+      }
+      partials_next[(size_t)blockIdx.x * 64 + lane] = lane < E_next ? p : 0.0f;
+    }
+  }
+}
+
+// ============================================================================ LM-head argmax
+// Bit-exact 2-accumulator AVX-512 order (see dsh_avx.h) for every row; 4 lanes per row group,
+// R rows per group walked in lockstep, a ring of D load stages in flight. T = in_dim/32 steps,
+// T % D == 0. Each block writes its (max, lowest index) key.
+template <int R, int D>
+__global__ void __launch_bounds__(256) k_dec_lm_argmax(const uint16_t *__restrict__ W, const float *__restrict__ x,
+                                                       int in_dim, int vocab, unsigned long long *__restrict__ cand) {
+  extern __shared__ float xs[];
+  __shared__ unsigned long long wbest[4];
+  for (int i = threadIdx.x; i < in_dim; i += 256) xs[i] = x[i];
+  __syncthreads();
+  const int L = threadIdx.x & 3;
+  const int g = threadIdx.x >> 2;
+  const int rbase = blockIdx.x * (64 * R) + g;
+  const uint16_t *wp[R];
+  bool ok[R];
+#pragma unroll
+  for (int j = 0; j < R; j++) {
+    int r = rbase + j * 64;
+    ok[j] = r < vocab;
+    wp[j] = W + (size_t)(ok[j] ? r : 0) * in_dim + 8 * L;
+  }
+  float acc[R][8];
+#pragma unroll
+  for (int j = 0; j < R; j++)
+#pragma unroll
+    for (int c = 0; c < 8; c++) acc[j][c] = 0.0f;
+  const int T = in_dim >> 5;
+  u32x4 ring[D][R];
+#pragma unroll
+  for (int s = 0; s < D; s++)
+#pragma unroll
+    for (int j = 0; j < R; j++) ring[s][j] = dsh_load_nt(wp[j] + 32 * s);
+  for (int t0 = 0; t0 < T; t0 += D) {
+#pragma unroll
+    for (int s = 0; s < D; s++) {
+      const int t = t0 + s;
+      const float *xp = xs + 32 * t + 8 * L;
+      f32x4 x0 = *(const f32x4 *)xp, x1 = *(const f32x4 *)(xp + 4);
+      float xf[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+      for (int j = 0; j < R; j++)
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+          acc[j][2 * d] = __builtin_fmaf(dsh_bf16lo(ring[s][j][d]), xf[2 * d], acc[j][2 * d]);
+          acc[j][2 * d + 1] = __builtin_fmaf(dsh_bf16hi(ring[s][j][d]), xf[2 * d + 1], acc[j][2 * d + 1]);
+        }
+      const int tn = min(t + D, T - 1);  // refill; the last D refills re-read the final chunk
+#pragma unroll
+      for (int j = 0; j < R; j++) ring[s][j] = dsh_load_nt(wp[j] + 32 * tn);
+    }
+  }
+  unsigned long long key = 0ull;
+#pragma unroll
+  for (int j = 0; j < R; j++) {
+    float A[8], T3[8], T6[4];
+#pragma unroll
+    for (int c = 0; c < 8; c++) A[c] = acc[j][c] + __shfl_down(acc[j][c], 2, 4);
+#pragma unroll
+    for (int c = 0; c < 8; c++) T3[c] = __shfl_down(A[c], 1, 4) + A[c];
+#pragma unroll
+    for (int c = 0; c < 4; c++) T6[c] = T3[4 + c] + T3[c];
+    float v = (T6[0] + T6[2]) + (T6[1] + T6[3]);
+    if (L == 0 && ok[j]) key = dsh_umax64(key, dsh_argmax_key(v, rbase + j * 64));
+  }
+  key = dsh_wave_max_u64(key);
+  if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = key;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long b = wbest[0];
+    for (int i = 1; i < 4; i++) b = dsh_umax64(b, wbest[i]);
+    cand[blockIdx.x] = b;
+  }
+}
+
+// Final reduction of the candidates; writes tokens[*step] (or tokens[0]) and advances *step.
+__global__ void __launch_bounds__(256) k_lm_argmax_final(const unsigned long long *__restrict__ cand, int n,
+                                                         int *__restrict__ tokens, int *__restrict__ step) {
+  __shared__ unsigned long long wbest[4];
+  unsigned long long b = 0ull;
+  for (int i = threadIdx.x; i < n; i += 256) b = dsh_umax64(b, cand[i]);
+  b = dsh_wave_max_u64(b);
+  if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = b;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < 4; i++) wbest[0] = dsh_umax64(wbest[0], wbest[i]);
+    int s = step ? *step : 0;
+    tokens[s] = dsh_key_index(wbest[0]);
+    if (step) *step = s + 1;
+  }
+}
+
+// ============================================================================ launchers
+#define DEC_R 8
+#define LM_R2 2
+#define LM_D2 8
+
+extern "C" {
+
+int dsh_dec_supported(int H, int I, int E, int K, int SI) {
+  if (H % 256 || H / 256 > 8) return 0;           // gate_up: H == 256*CPL
+  if (I % 16 || I / 16 > 64 || SI % I) return 0;  // down: one chunk per lane
+  if (K + SI / I != 8 || H % DEC_R) return 0;
+  if (E > 64 || K > E) return 0;
+  return 1;
+}
+
+int dsh_dec_partials(int H) { return H / DEC_R; }
+
+hipError_t dsh_launch_dec_partial_scores(const float *Wr, const float *x_in, const int *step, int stride, int H, int E,
+                                         float *partials, hipStream_t s) {
+  k_dec_partial_scores<DEC_R><<<H / DEC_R, 64, 0, s>>>(Wr, x_in, step, stride, H, E, partials);
+  return hipGetLastError();
+}
+
+hipError_t dsh_launch_dec_scores_bf16(const uint16_t *Wr, const float *x_in, const int *step, int stride, int H, int E,
+                                      int nthreads, float *partials, hipStream_t s) {
+  k_dec_scores_bf16<<<(E + 15) / 16, 64, (size_t)H * 4, s>>>(Wr, x_in, step, stride, H, E,
+                                                              dsh_chunk_len(E, nthreads), partials);
+  return hipGetLastError();
+}
+
+hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const int *step, int stride,
+                                  const float *partials, int np, int route_mode, int bf16sim,
+                                  const dsh_layer_work_t *wk, hipStream_t s) {
+  int total = L->K * L->I + L->SI;
+  int blocks = (total + 15) / 16;
+#define GU(N)                                                                                                  \
+  case N:                                                                                                      \
+    k_dec_gate_up<N><<<blocks, 256, 0, s>>>(*L, x_in, step, stride, partials, np, route_mode, bf16sim, *wk);   \
+    break;
+  switch (L->H / 256) {
+    GU(1) GU(2) GU(3) GU(4) GU(5) GU(6) GU(7) GU(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef GU
+  return hipGetLastError();
+}
+
+hipError_t dsh_launch_dec_down(const dsh_layer_t *L, const float *x_in, const int *step, int stride, float *x_out,
+                               int residual, int bf16sim, const dsh_layer_work_t *wk, const float *Wr_next,
+                               int E_next, float *partials_next, hipStream_t s) {
+  k_dec_down<DEC_R><<<L->H / DEC_R, 512, 0, s>>>(*L, x_in, step, stride, x_out, residual, bf16sim, *wk, Wr_next,
+                                                 E_next, partials_next);
+  return hipGetLastError();
+}
+
+int dsh_dec_lm_blocks(int vocab) { return (vocab + 64 * LM_R2 - 1) / (64 * LM_R2); }
+
+int dsh_dec_lm_supported(int in_dim) { return in_dim % (32 * LM_D2) == 0 && in_dim * 4 <= 64 * 1024; }
+
+hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int *tokens, int *step, hipStream_t s) {
+  k_lm_argmax_final<<<1, 256, 0, s>>>(cand, n, tokens, step);
+  return hipGetLastError();
+}
+
+hipError_t dsh_launch_dec_lm_argmax(const uint16_t *W, const float *x, int in_dim, int vocab,
+                                    unsigned long long *cand, hipStream_t s) {
+  if (!dsh_dec_lm_supported(in_dim) || ((uintptr_t)W & 15)) return hipErrorInvalidValue;
+  k_dec_lm_argmax<LM_R2, LM_D2><<<dsh_dec_lm_blocks(vocab), 256, (size_t)in_dim * 4, s>>>(W, x, in_dim, vocab, cand);
+  return hipGetLastError();
+}
+
+}  // extern "C"

@@ -21,7 +21,8 @@ struct ds_hip_layer {
   size_t bytes;
   dsh_layer_t d;          /* device pointers into the arena */
   dsh_layer_work_t wk;    /* work buffers (in the arena) */
-  float *xtmp;            /* [H] */
+  float *partials;        /* [H/8][64] router partial scores */
+  int np;                 /* number of partial rows in CFG mode */
   int have_f32, have_bf16;
 };
 
@@ -35,9 +36,9 @@ ds_hip_layer_t *ds_hip_layer_create(int hidden, int inter, int n_experts, int to
               shared_inter);
     return NULL;
   }
-  if (!dsh_moe_fast_shape(hidden, inter, n_experts, top_k, shared_inter)) {
+  if (!dsh_dec_supported(hidden, inter, n_experts, top_k, shared_inter)) {
     dsr_failf("ds_hip_layer_create: shape H=%d I=%d E=%d K=%d SI=%d not supported by the fused decode kernels "
-              "(need H %% 16 == 0, I %% 128 == 0, SI %% I == 0, K + SI/I == 8)",
+              "(need H %% 256 == 0 and H <= 2048, I %% 16 == 0 and I <= 1024, SI %% I == 0, K + SI/I == 8)",
               hidden, inter, n_experts, top_k, shared_inter);
     return NULL;
   }
@@ -60,7 +61,7 @@ ds_hip_layer_t *ds_hip_layer_create(int hidden, int inter, int n_experts, int to
   REGION(K * 4);                  /* 11 idx */
   REGION(K * 4);                  /* 12 w */
   REGION((K * I + SI) * 4);       /* 13 h */
-  REGION(H * 4);                  /* 14 xtmp */
+  REGION((H / 8) * 64 * 4);       /* 14 router partial scores */
 #undef REGION
   hipError_t e = hipMalloc(&L->arena, n);
   if (e != hipSuccess) {
@@ -95,7 +96,8 @@ ds_hip_layer_t *ds_hip_layer_create(int hidden, int inter, int n_experts, int to
   L->wk.idx = (int *)(b + off[11]);
   L->wk.w = (float *)(b + off[12]);
   L->wk.h = (float *)(b + off[13]);
-  L->xtmp = (float *)(b + off[14]);
+  L->partials = (float *)(b + off[14]);
+  L->np = dsh_dec_partials(hidden);
   return L;
 }
 
@@ -237,12 +239,39 @@ static int check_router(const ds_hip_layer_t *L, int route_mode) {
   return 0;
 }
 
-/* The three kernels of one layer. x_in (+ *step * stride) -> x_out. */
-static hipError_t layer_enqueue(const ds_hip_layer_t *L, const dsh_layer_work_t *wk, const float *x_in,
-                                const int *step, int stride, float *x_out, int route_mode, int residual, int bf16sim) {
-  hipError_t e = dsh_launch_moe_scores(&L->d, x_in, step, stride, route_mode, dsr_threads(), wk->scores, dsr_stream);
-  if (e == hipSuccess) e = dsh_launch_moe_gate_up(&L->d, x_in, step, stride, route_mode, bf16sim, wk, dsr_stream);
-  if (e == hipSuccess) e = dsh_launch_moe_down(&L->d, x_in, step, stride, x_out, residual, bf16sim, wk, dsr_stream);
+/* Router partial scores of layer L for input x (CFG: f32 partials; DECODE: exact full scores as
+ * one partial). Returns the number of partial rows through *np. */
+static hipError_t scores_enqueue(const ds_hip_layer_t *L, const float *x_in, const int *step, int stride,
+                                 int route_mode, float *partials, int *np) {
+  if (route_mode == DS_HIP_ROUTE_CFG) {
+    *np = L->np;
+    return dsh_launch_dec_partial_scores(L->d.router_f32, x_in, step, stride, L->H, L->E, partials, dsr_stream);
+  }
+  *np = 1;
+  return dsh_launch_dec_scores_bf16(L->d.router_bf16, x_in, step, stride, L->H, L->E, dsr_threads(), partials,
+                                    dsr_stream);
+}
+
+/* One layer: [scores], gate_up, down. In CFG mode with next != NULL, down also writes the partial
+ * scores of layer "next" and the next layer's scores kernel is skipped by the caller. */
+static hipError_t layer_enqueue(const ds_hip_layer_t *L, const dsh_layer_work_t *wk, float *partials,
+                                int have_scores, int np, const float *x_in, const int *step, int stride, float *x_out,
+                                int route_mode, int residual, int bf16sim, const ds_hip_layer_t *next,
+                                hipEvent_t *ev, int *nev) {
+  hipError_t e = hipSuccess;
+  if (!have_scores) {
+    e = scores_enqueue(L, x_in, step, stride, route_mode, partials, &np);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+  }
+  if (e == hipSuccess)
+    e = dsh_launch_dec_gate_up(&L->d, x_in, step, stride, partials, np, route_mode, bf16sim, wk, dsr_stream);
+  if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+  int chain = next && route_mode == DS_HIP_ROUTE_CFG;
+  if (e == hipSuccess)
+    e = dsh_launch_dec_down(&L->d, x_in, step, stride, x_out, residual, bf16sim, wk,
+                            chain ? next->d.router_f32 : NULL, chain ? next->E : 0, chain ? partials : NULL,
+                            dsr_stream);
+  if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
   return e;
 }
 
@@ -251,7 +280,8 @@ int ds_hip_layer_forward(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
   if (!L || !out_dev || !x_dev) return dsr_failf("ds_hip_layer_forward: NULL argument");
   if (check_router(L, route_mode)) return -1;
   int bf16sim = ds_bf16_simulate_python;
-  hipError_t e = layer_enqueue(L, &L->wk, x_dev, NULL, 0, out_dev, route_mode, residual, bf16sim);
+  hipError_t e = layer_enqueue(L, &L->wk, L->partials, 0, 0, x_dev, NULL, 0, out_dev, route_mode, residual, bf16sim,
+                               NULL, NULL, NULL);
   if (e != hipSuccess) return dsr_fail("layer kernels", e);
   if (idx_dev)
     DSR_TRY(hipMemcpyAsync(idx_dev, L->wk.idx, (size_t)L->K * 4, hipMemcpyDeviceToDevice, dsr_stream), "idx copy");
@@ -317,8 +347,8 @@ ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers,
     int len = vocab - s < chunk ? vocab - s : chunk;
     if (len % 4) ok4 = 0;
   }
-  S->lm_fast = (H % 32 == 0) && (((uintptr_t)lm_head_dev & 15) == 0) && ok4;
-  S->ncand = S->lm_fast ? dsh_lm_argmax_blocks(vocab) : dsh_argmax_avx_blocks(vocab);
+  S->lm_fast = dsh_dec_lm_supported(H) && (((uintptr_t)lm_head_dev & 15) == 0) && ok4;
+  S->ncand = S->lm_fast ? dsh_dec_lm_blocks(vocab) : dsh_argmax_avx_blocks(vocab);
   size_t bytes = 256 + al((size_t)H * 4) + al((size_t)S->ncand * 8);
   hipError_t e = hipMalloc(&S->work, bytes);
   if (e != hipSuccess) {
@@ -355,33 +385,41 @@ size_t ds_hip_stack_bytes_per_step(const ds_hip_stack_t *S) {
   return per_layer * (size_t)S->n_layers + (size_t)S->vocab * S->H * 2;
 }
 
-/* One decode step; slot_events (optional) gets an event after every kernel. */
+/* Kernels launched per decode step (for profiling). */
+static int stack_kernel_count(const ds_hip_stack_t *S) {
+  int per_layer = S->route_mode == DS_HIP_ROUTE_CFG ? 2 : 3;
+  return (S->route_mode == DS_HIP_ROUTE_CFG ? 1 : 0) + per_layer * S->n_layers + 2;
+}
+
+/* One decode step; ev (optional) receives an event before the first kernel and after each one. */
 static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
   hipError_t e = hipSuccess;
   int n = 0;
+  ds_hip_layer_t *L0 = S->layers[0];
+  float *partials = L0->partials;
+  const dsh_layer_work_t *wk = &L0->wk;
+  int np = 0;
   if (ev) e = hipEventRecord(ev[n++], dsr_stream);
+  if (e == hipSuccess && S->route_mode == DS_HIP_ROUTE_CFG) {
+    e = scores_enqueue(L0, S->xs, S->step, S->stride, S->route_mode, partials, &np);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+  }
   for (int l = 0; l < S->n_layers && e == hipSuccess; l++) {
     const ds_hip_layer_t *L = S->layers[l];
-    const dsh_layer_work_t *wk = &S->layers[0]->wk;
     const float *xin = l == 0 ? S->xs : S->xbuf;
     const int *st = l == 0 ? S->step : NULL;
     int stride = l == 0 ? S->stride : 0;
-    e = dsh_launch_moe_scores(&L->d, xin, st, stride, S->route_mode, dsr_threads(), wk->scores, dsr_stream);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
-    if (e == hipSuccess) e = dsh_launch_moe_gate_up(&L->d, xin, st, stride, S->route_mode, S->bf16sim, wk, dsr_stream);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
-    if (e == hipSuccess)
-      e = dsh_launch_moe_down(&L->d, xin, st, stride, S->xbuf, 1, S->bf16sim, wk, dsr_stream);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+    const ds_hip_layer_t *next = l + 1 < S->n_layers ? S->layers[l + 1] : NULL;
+    e = layer_enqueue(L, wk, partials, S->route_mode == DS_HIP_ROUTE_CFG, L->np, xin, st, stride, S->xbuf,
+                      S->route_mode, 1, S->bf16sim, next, ev, &n);
   }
   if (e != hipSuccess) return e;
   if (S->lm_fast) {
-    e = dsh_launch_lm_argmax_partial(S->lm, S->xbuf, S->H, S->vocab, S->cand, dsr_stream);
+    e = dsh_launch_dec_lm_argmax(S->lm, S->xbuf, S->H, S->vocab, S->cand, dsr_stream);
   } else {
+    int T = dsr_threads();
     e = dsh_launch_argmax_avx_partial(S->lm, S->xbuf, S->cand, NULL, S->H, S->vocab,
-                                      S->vocab > 0 && dsr_threads() > 1 ? (S->vocab + dsr_threads() - 1) / dsr_threads()
-                                                                        : S->vocab,
-                                      dsr_stream);
+                                      T > 1 ? (S->vocab + T - 1) / T : S->vocab, dsr_stream);
   }
   if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
   if (e == hipSuccess) e = dsh_launch_lm_argmax_final(S->cand, S->ncand, S->tokens, S->step, dsr_stream);
@@ -459,9 +497,24 @@ int ds_hip_time_stack(ds_hip_stack_t *S, int n_steps, float *ms) {
   return rc;
 }
 
+int ds_hip_stack_kernel_count(const ds_hip_stack_t *S) { return S ? stack_kernel_count(S) : 0; }
+
+const char *ds_hip_stack_kernel_name(const ds_hip_stack_t *S, int i) {
+  if (!S || i < 0 || i >= stack_kernel_count(S)) return NULL;
+  int nk = stack_kernel_count(S);
+  if (i == nk - 2) return "lm_head.argmax";
+  if (i == nk - 1) return "lm_head.final";
+  if (S->route_mode == DS_HIP_ROUTE_CFG) {
+    if (i == 0) return "scores";
+    return (i - 1) % 2 == 0 ? "gate_up" : "down";
+  }
+  static const char *names[3] = {"scores", "gate_up", "down"};
+  return names[i % 3];
+}
+
 int ds_hip_profile_stack(ds_hip_stack_t *S, int n_steps, float *ms_out) {
   if (!S || !S->bound || !ms_out || n_steps <= 0) return dsr_failf("ds_hip_profile_stack: invalid arguments");
-  int nk = 3 * S->n_layers + 2;
+  int nk = stack_kernel_count(S);
   hipEvent_t *ev = (hipEvent_t *)calloc((size_t)(nk + 1), sizeof(hipEvent_t));
   double *acc = (double *)calloc((size_t)nk, sizeof(double));
   int rc = 0;

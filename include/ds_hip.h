@@ -99,9 +99,12 @@ size_t ds_hip_stack_bytes_per_step(const ds_hip_stack_t *S);
 /* ---------------- timing (HIP events on the library stream) ---------------- */
 /* Wall time of n_steps graph launches. */
 int ds_hip_time_stack(ds_hip_stack_t *S, int n_steps, float *ms);
-/* Per-kernel durations over n_steps eager steps, events around every kernel. ms_out receives
- * 3*n_layers + 2 averages: for each layer scores, gate_up, down; then the LM-head partial and
- * final kernels. */
+/* Kernels one decode step launches, and the kind of kernel i ("scores", "gate_up", "down",
+ * "lm_head.argmax", "lm_head.final"). */
+int ds_hip_stack_kernel_count(const ds_hip_stack_t *S);
+const char *ds_hip_stack_kernel_name(const ds_hip_stack_t *S, int i);
+/* Per-kernel durations over n_steps eager steps, HIP events around every kernel; ms_out receives
+ * ds_hip_stack_kernel_count(S) averages in launch order. */
 int ds_hip_profile_stack(ds_hip_stack_t *S, int n_steps, float *ms_out);
 
 #ifdef __cplusplus
