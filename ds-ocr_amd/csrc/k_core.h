@@ -90,6 +90,9 @@ hipError_t dsh_launch_dec_down(const dsh_layer_t *L, const float *x_in, const in
                                int E_next, float *partials_next, hipStream_t s);
 int dsh_dec_lm_blocks(int vocab);
 int dsh_dec_lm_supported(int in_dim);
+int dsh_dec_lm_eligible(const void *W, int in_dim, int vocab, int nthreads);
+hipError_t dsh_launch_dec_lm_argmax_depth(const uint16_t *W, const float *x, int in_dim, int vocab,
+                                          unsigned long long *cand, int depth, hipStream_t s);
 hipError_t dsh_launch_dec_lm_argmax(const uint16_t *W, const float *x, int in_dim, int vocab,
                                     unsigned long long *cand, hipStream_t s);
 

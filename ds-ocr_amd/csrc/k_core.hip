@@ -757,6 +757,13 @@ hipError_t dsh_launch_argmax_avx_partial(const uint16_t *W, const float *x, unsi
 hipError_t dsh_launch_argmax_avx(const uint16_t *W, const float *x, unsigned long long *cand, float *logits,
                                  int in_dim, int out_dim, int nthreads, int *out_idx, float *out_val, hipStream_t s) {
   if (out_dim <= 0) return hipSuccess;
+  if (!logits && dsh_dec_lm_eligible(W, in_dim, out_dim, nthreads)) {
+    // full-line streaming kernel (k_dec.hip); its candidate count is at most dsh_argmax_avx_blocks
+    hipError_t e = dsh_launch_dec_lm_argmax(W, x, in_dim, out_dim, cand, s);
+    if (e != hipSuccess) return e;
+    k_argmax_final<<<1, 256, 0, s>>>(cand, dsh_dec_lm_blocks(out_dim), out_idx, out_val);
+    return LAUNCH_CHECK();
+  }
   hipError_t e = dsh_launch_argmax_avx_partial(W, x, cand, logits, in_dim, out_dim, dsh_chunk_len(out_dim, nthreads), s);
   if (e != hipSuccess) return e;
   k_argmax_final<<<1, 256, 0, s>>>(cand, dsh_argmax_avx_blocks(out_dim), out_idx, out_val);

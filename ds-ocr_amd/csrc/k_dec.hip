@@ -377,72 +377,89 @@ __global__ void __launch_bounds__(512) k_dec_down(dsh_layer_t L, const float *__
 }
 
 // ============================================================================ LM-head argmax
-// Bit-exact 2-accumulator AVX-512 order (see dsh_avx.h) for every row; 4 lanes per row group,
-// R rows per group walked in lockstep, a ring of D load stages in flight. T = in_dim/32 steps,
-// T % D == 0. Each block writes its (max, lowest index) key.
-template <int R, int D>
-__global__ void __launch_bounds__(256) k_dec_lm_argmax(const uint16_t *__restrict__ W, const float *__restrict__ x,
+// One row per lane, bit-exact 2-accumulator AVX-512 order (ds_kernels_avx.c:162-245, 4-row group
+// path; the stack only takes this kernel when every row of the reference's thread chunks is on that
+// path). A wave owns 64 consecutive rows. For each 128-byte line t of its rows (64 elements: two
+// AVX iterations, chains 0..31 twice) it issues 8 loads in which 8 adjacent lanes read one row's
+// full line, stores the 64 x 128 B tile in a wave-private LDS buffer (row pitch 144 B, so the
+// 16-byte reads of 64 different rows are bank-conflict free), and each lane then reads its own row
+// and accumulates its 32 chains in registers; x is uniform across the wave (scalar loads). A ring of
+// D lines of loads is kept in flight. Requires in_dim % 64 == 0. Each block writes its
+// (max, lowest index) key.
+template <int D>
+__global__ void __launch_bounds__(256) k_dec_lm_argmax(const uint16_t *W, const float *__restrict__ x,
                                                        int in_dim, int vocab, unsigned long long *__restrict__ cand) {
-  extern __shared__ float xs[];
+  constexpr int PITCH = 144;
+  __shared__ __attribute__((aligned(16))) uint8_t tile[4][64 * PITCH];
   __shared__ unsigned long long wbest[4];
-  for (int i = threadIdx.x; i < in_dim; i += 256) xs[i] = x[i];
-  __syncthreads();
-  const int L = threadIdx.x & 3;
-  const int g = threadIdx.x >> 2;
-  const int rbase = blockIdx.x * (64 * R) + g;
-  const uint16_t *wp[R];
-  bool ok[R];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r0 = (blockIdx.x * 4 + wave) * 64;
+  const size_t row_bytes = (size_t)in_dim * 2;
+  const int lrow = lane >> 3, piece = lane & 7;
+  const uint8_t *src[8];
 #pragma unroll
-  for (int j = 0; j < R; j++) {
-    int r = rbase + j * 64;
-    ok[j] = r < vocab;
-    wp[j] = W + (size_t)(ok[j] ? r : 0) * in_dim + 8 * L;
+  for (int j = 0; j < 8; j++) {
+    int r = min(r0 + 8 * j + lrow, vocab - 1);
+    src[j] = (const uint8_t *)W + (size_t)r * row_bytes + 16 * piece;
   }
-  float acc[R][8];
+  uint8_t *wtile = tile[wave];
+  float acc[32];
 #pragma unroll
-  for (int j = 0; j < R; j++)
+  for (int c = 0; c < 32; c++) acc[c] = 0.0f;
+  const int NT = in_dim >> 6;  // a multiple of D (launcher)
+  u32x4 ring[D][8];
+  // issue order = stage order, so that waiting for stage s leaves the later stages in flight (W is
+  // deliberately not __restrict__: the memory clobber then keeps these loads in place)
 #pragma unroll
-    for (int c = 0; c < 8; c++) acc[j][c] = 0.0f;
-  const int T = in_dim >> 5;
-  u32x4 ring[D][R];
+  for (int s = 0; s < D; s++) {
 #pragma unroll
-  for (int s = 0; s < D; s++)
-#pragma unroll
-    for (int j = 0; j < R; j++) ring[s][j] = dsh_load_nt(wp[j] + 32 * s);
-  for (int t0 = 0; t0 < T; t0 += D) {
+    for (int j = 0; j < 8; j++) ring[s][j] = dsh_load_nt(src[j] + 128 * s);
+    asm volatile("" ::: "memory");
+  }
+  for (int t0 = 0; t0 < NT; t0 += D) {
 #pragma unroll
     for (int s = 0; s < D; s++) {
       const int t = t0 + s;
-      const float *xp = xs + 32 * t + 8 * L;
-      f32x4 x0 = *(const f32x4 *)xp, x1 = *(const f32x4 *)(xp + 4);
-      float xf[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
 #pragma unroll
-      for (int j = 0; j < R; j++)
+      for (int j = 0; j < 8; j++) *(u32x4 *)(wtile + (8 * j + lrow) * PITCH + 16 * piece) = ring[s][j];
+      const int tn = min(t + D, NT - 1);  // refill; the last D refills re-read the final line
+#pragma unroll
+      for (int j = 0; j < 8; j++) ring[s][j] = dsh_load_nt(src[j] + 128 * tn);
+      // the tile is wave-private and LDS executes a wave's operations in order: these fences only
+      // keep the compiler from moving the reads above the writes (and the next writes above them)
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const uint8_t *mine = wtile + lane * PITCH;
+      const float *xt = x + 64 * t;
+#pragma unroll
+      for (int p = 0; p < 8; p++) {
+        u32x4 v = *(const u32x4 *)(mine + 16 * p);
+        const int c0 = (8 * p) & 31;
 #pragma unroll
         for (int d = 0; d < 4; d++) {
-          acc[j][2 * d] = __builtin_fmaf(dsh_bf16lo(ring[s][j][d]), xf[2 * d], acc[j][2 * d]);
-          acc[j][2 * d + 1] = __builtin_fmaf(dsh_bf16hi(ring[s][j][d]), xf[2 * d + 1], acc[j][2 * d + 1]);
+          acc[c0 + 2 * d] = __builtin_fmaf(dsh_bf16lo(v[d]), xt[8 * p + 2 * d], acc[c0 + 2 * d]);
+          acc[c0 + 2 * d + 1] = __builtin_fmaf(dsh_bf16hi(v[d]), xt[8 * p + 2 * d + 1], acc[c0 + 2 * d + 1]);
         }
-      const int tn = min(t + D, T - 1);  // refill; the last D refills re-read the final chunk
-#pragma unroll
-      for (int j = 0; j < R; j++) ring[s][j] = dsh_load_nt(wp[j] + 32 * tn);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
-  unsigned long long key = 0ull;
+  // _mm512_reduce_add_ps(a0 + a1) as GCC 11 expands it (see dsh_avx.h)
+  float A[16], T3[8], T6[4];
 #pragma unroll
-  for (int j = 0; j < R; j++) {
-    float A[8], T3[8], T6[4];
+  for (int i = 0; i < 16; i++) A[i] = acc[i] + acc[16 + i];
 #pragma unroll
-    for (int c = 0; c < 8; c++) A[c] = acc[j][c] + __shfl_down(acc[j][c], 2, 4);
+  for (int i = 0; i < 8; i++) T3[i] = A[8 + i] + A[i];
 #pragma unroll
-    for (int c = 0; c < 8; c++) T3[c] = __shfl_down(A[c], 1, 4) + A[c];
-#pragma unroll
-    for (int c = 0; c < 4; c++) T6[c] = T3[4 + c] + T3[c];
-    float v = (T6[0] + T6[2]) + (T6[1] + T6[3]);
-    if (L == 0 && ok[j]) key = dsh_umax64(key, dsh_argmax_key(v, rbase + j * 64));
-  }
+  for (int i = 0; i < 4; i++) T6[i] = T3[4 + i] + T3[i];
+  const float v = (T6[0] + T6[2]) + (T6[1] + T6[3]);
+  const int row = r0 + lane;
+  unsigned long long key = row < vocab ? dsh_argmax_key(v, row) : 0ull;
   key = dsh_wave_max_u64(key);
-  if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = key;
+  if (lane == 0) wbest[wave] = key;
   __syncthreads();
   if (threadIdx.x == 0) {
     unsigned long long b = wbest[0];
@@ -470,8 +487,7 @@ __global__ void __launch_bounds__(256) k_lm_argmax_final(const unsigned long lon
 
 // ============================================================================ launchers
 #define DEC_R 8
-#define LM_R2 2
-#define LM_D2 8
+#define LM_D 1
 
 extern "C" {
 
@@ -524,20 +540,52 @@ hipError_t dsh_launch_dec_down(const dsh_layer_t *L, const float *x_in, const in
   return hipGetLastError();
 }
 
-int dsh_dec_lm_blocks(int vocab) { return (vocab + 64 * LM_R2 - 1) / (64 * LM_R2); }
+int dsh_dec_lm_blocks(int vocab) { return (vocab + 255) / 256; }
 
-int dsh_dec_lm_supported(int in_dim) { return in_dim % (32 * LM_D2) == 0 && in_dim * 4 <= 64 * 1024; }
+int dsh_dec_lm_supported(int in_dim) { return in_dim > 0 && in_dim % 64 == 0; }
+
+// The one-row-per-lane kernel computes every row in the 4-row-group order; the reference takes
+// that order only for rows inside a whole group of 4 of its thread's chunk.
+int dsh_dec_lm_eligible(const void *W, int in_dim, int vocab, int nthreads) {
+  if (!dsh_dec_lm_supported(in_dim) || ((uintptr_t)W & 15) || vocab <= 0) return 0;
+  const int chunk = dsh_chunk_len(vocab, nthreads);
+  for (int s0 = 0; s0 < vocab; s0 += chunk)
+    if (min(chunk, vocab - s0) % 4) return 0;
+  return 1;
+}
 
 hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int *tokens, int *step, hipStream_t s) {
   k_lm_argmax_final<<<1, 256, 0, s>>>(cand, n, tokens, step);
   return hipGetLastError();
 }
 
+// depth: lines of loads in flight per lane (1, 2 or 4; must divide in_dim/64).
+hipError_t dsh_launch_dec_lm_argmax_depth(const uint16_t *W, const float *x, int in_dim, int vocab,
+                                          unsigned long long *cand, int depth, hipStream_t s) {
+  if (!dsh_dec_lm_supported(in_dim) || ((uintptr_t)W & 15) || vocab <= 0) return hipErrorInvalidValue;
+  if ((in_dim / 64) % depth) return hipErrorInvalidValue;
+  const int nb = dsh_dec_lm_blocks(vocab);
+  switch (depth) {
+    case 1:
+      k_dec_lm_argmax<1><<<nb, 256, 0, s>>>(W, x, in_dim, vocab, cand);
+      break;
+    case 2:
+      k_dec_lm_argmax<2><<<nb, 256, 0, s>>>(W, x, in_dim, vocab, cand);
+      break;
+    case 4:
+      k_dec_lm_argmax<4><<<nb, 256, 0, s>>>(W, x, in_dim, vocab, cand);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t dsh_launch_dec_lm_argmax(const uint16_t *W, const float *x, int in_dim, int vocab,
                                     unsigned long long *cand, hipStream_t s) {
-  if (!dsh_dec_lm_supported(in_dim) || ((uintptr_t)W & 15)) return hipErrorInvalidValue;
-  k_dec_lm_argmax<LM_R2, LM_D2><<<dsh_dec_lm_blocks(vocab), 256, (size_t)in_dim * 4, s>>>(W, x, in_dim, vocab, cand);
-  return hipGetLastError();
+  const int nt = in_dim / 64;
+  const int depth = nt % LM_D == 0 ? LM_D : (nt % 2 == 0 ? 2 : 1);
+  return dsh_launch_dec_lm_argmax_depth(W, x, in_dim, vocab, cand, depth, s);
 }
 
 }  // extern "C"

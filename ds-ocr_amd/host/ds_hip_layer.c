@@ -337,17 +337,7 @@ ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers,
   S->H = H;
   S->route_mode = route_mode;
   S->bf16sim = ds_bf16_simulate_python;
-  /* Fast LM-head kernel: in_dim % 32 == 0, aligned rows, every reference row chunk a multiple of 4
-   * rows (then every row uses the 2-accumulator order). */
-  int chunk = vocab;
-  int T = dsr_threads();
-  if (T > 1) chunk = (vocab + T - 1) / T;
-  int ok4 = 1;
-  for (int s = 0; s < vocab; s += chunk) {
-    int len = vocab - s < chunk ? vocab - s : chunk;
-    if (len % 4) ok4 = 0;
-  }
-  S->lm_fast = dsh_dec_lm_supported(H) && (((uintptr_t)lm_head_dev & 15) == 0) && ok4;
+  S->lm_fast = dsh_dec_lm_eligible(lm_head_dev, H, vocab, dsr_threads());
   S->ncand = S->lm_fast ? dsh_dec_lm_blocks(vocab) : dsh_argmax_avx_blocks(vocab);
   size_t bytes = 256 + al((size_t)H * 4) + al((size_t)S->ncand * 8);
   hipError_t e = hipMalloc(&S->work, bytes);

@@ -2,10 +2,12 @@
  * registry of libds_ocr_hip. The registry plays the role of the Metal backend's
  * ds_metal_register_expert_block (reference ds_metal.m:244-258): weights are uploaded once and
  * stay resident. */
+#include <pthread.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 #include "dsr.h"
 #include "ds_hip.h"
@@ -100,17 +102,65 @@ static uint64_t fnv(uint64_t h, const void *p, size_t n) {
   return h;
 }
 
-/* Hash of the length, the first and last 256 bytes and 64 evenly spaced 8-byte samples. */
+/* Content hash of every byte: four lanes of the xxHash64 round (acc = rotl(acc + w*P2, 31) * P1)
+ * over 32-byte stripes, the tail through FNV-1a. Any change of a cached host array is seen, also
+ * when a new array reuses a freed one's address; arrays of 32 MiB and more are hashed in parallel
+ * slices. */
+#define XXP1 11400714785092567791ull
+#define XXP2 14029467366897019727ull
+static uint64_t rotl64(uint64_t v, int r) { return (v << r) | (v >> (64 - r)); }
+
+static uint64_t hash_slice(const unsigned char *b, size_t n, uint64_t seed) {
+  uint64_t v[4] = {seed + XXP1 + XXP2, seed + XXP2, seed, seed - XXP1};
+  size_t i = 0;
+  for (; i + 32 <= n; i += 32) {
+    for (int l = 0; l < 4; l++) {
+      uint64_t w;
+      memcpy(&w, b + i + 8 * l, 8);
+      v[l] = rotl64(v[l] + w * XXP2, 31) * XXP1;
+    }
+  }
+  uint64_t h = rotl64(v[0], 1) + rotl64(v[1], 7) + rotl64(v[2], 12) + rotl64(v[3], 18);
+  return fnv(h ^ (uint64_t)n, b + i, n - i);
+}
+
+typedef struct {
+  const unsigned char *b;
+  size_t n;
+  uint64_t h;
+} slice_t;
+
+static void *hash_worker(void *arg) {
+  slice_t *s = (slice_t *)arg;
+  s->h = hash_slice(s->b, s->n, 0x9E3779B97F4A7C15ull);
+  return NULL;
+}
+
 static uint64_t fingerprint(const void *p, size_t n) {
   const unsigned char *b = (const unsigned char *)p;
   uint64_t h = fnv(1469598103934665603ull, &n, sizeof n);
-  if (n <= 1024) return fnv(h, b, n);
-  h = fnv(h, b, 256);
-  h = fnv(h, b + n - 256, 256);
-  for (int i = 0; i < 64; i++) {
-    size_t off = (n - 8) / 64 * (size_t)i;
-    h = fnv(h, b + off, 8);
+  enum { MAXS = 8 };
+  long ncpu = sysconf(_SC_NPROCESSORS_ONLN);
+  int ns = n >= ((size_t)32 << 20) ? (int)(ncpu < MAXS ? (ncpu < 1 ? 1 : ncpu) : MAXS) : 1;
+  slice_t sl[MAXS];
+  pthread_t th[MAXS];
+  int started[MAXS] = {0};
+  size_t per = ((n / (size_t)ns) + 31) & ~(size_t)31;
+  for (int i = 0; i < ns; i++) {
+    size_t s0 = per * (size_t)i < n ? per * (size_t)i : n;
+    size_t s1 = i == ns - 1 ? n : (per * (size_t)(i + 1) < n ? per * (size_t)(i + 1) : n);
+    sl[i].b = b + s0;
+    sl[i].n = s1 - s0;
+    if (i > 0 && pthread_create(&th[i], NULL, hash_worker, &sl[i]) == 0) started[i] = 1;
   }
+  hash_worker(&sl[0]);
+  for (int i = 1; i < ns; i++) {
+    if (started[i])
+      pthread_join(th[i], NULL);
+    else
+      hash_worker(&sl[i]);
+  }
+  for (int i = 0; i < ns; i++) h = fnv(h, &sl[i].h, sizeof sl[i].h);
   return h;
 }
 
@@ -155,8 +205,8 @@ static entry_t *add(void) {
 static uint64_t block_fp(const ds_int4_block_t *b) {
   size_t nq = (size_t)b->out_dim * b->in_dim;
   uint64_t h = fingerprint(b->qweight, nq);
-  h = fnv(h, b->scale, (size_t)b->out_dim * 4);
-  h = fnv(h, b->offset, (size_t)b->out_dim * 4);
+  h = fnv(h, &(uint64_t){fingerprint(b->scale, (size_t)b->out_dim * 4)}, 8);
+  h = fnv(h, &(uint64_t){fingerprint(b->offset, (size_t)b->out_dim * 4)}, 8);
   h = fnv(h, &b->out_dim, sizeof(int));
   return fnv(h, &b->in_dim, sizeof(int));
 }
@@ -288,7 +338,6 @@ void ds_set_threads(int n) {
 int ds_get_threads(void) { return g_threads; }
 int dsr_threads(void) { return g_threads; }
 
-#include <unistd.h>
 int ds_get_num_cpus(void) {
   long n = sysconf(_SC_NPROCESSORS_ONLN);
   return n > 0 ? (int)n : 1;
