@@ -34,32 +34,35 @@ __device__ __forceinline__ void load_f16x(const float *p, float *o) {
 }
 
 // ============================================================================ routing in a block
-// All four waves reduce the NP partial score vectors (fixed order: wave w sums rows w, w+4, ...,
-// then the four sums are added in wave order), then wave 0 routes. Writes s_idx/s_w in LDS.
-template <int NW>
-__device__ void block_route(const float *__restrict__ partials, int np, int E, int K, int mode, int *s_idx,
-                            float *s_w, float (*s_red)[64]) {
+// Routing of one MoE layer from the NP partial score vectors, done by every block that needs it:
+// route_load issues the ROUTE_BATCH partial loads of each wave (rows wave, wave+4, ...; at most
+// 4 * ROUTE_BATCH partials, checked by dsh_dec_supported), route_reduce sums them in that order
+// and stores the wave sums, and
+// route_select (wave 0) adds the four wave sums in wave order and selects the experts
+// (same semantics as k_core.hip's top-k helpers). Results in s_idx/s_w (LDS), visible after the
+// next barrier.
+#define ROUTE_BATCH 40
+
+__device__ __forceinline__ void route_load(const float *partials, int np, float *v) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int j = 0; j < ROUTE_BATCH; j++) v[j] = partials[(size_t)min(wave + 4 * j, np - 1) * 64 + lane];
+}
+
+__device__ __forceinline__ void route_reduce(int np, int E, const float *v, float (*s_red)[64]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float acc = 0.0f;
-  if (lane < E) {
-    int b = wave;
-    // batches of 8 loads issued together
-    for (; b + 7 * NW < np; b += 8 * NW) {
-      float v[8];
 #pragma unroll
-      for (int j = 0; j < 8; j++) v[j] = partials[(size_t)(b + j * NW) * 64 + lane];
-#pragma unroll
-      for (int j = 0; j < 8; j++) acc += v[j];
-    }
-    for (; b < np; b += NW) acc += partials[(size_t)b * 64 + lane];
-  }
-  s_red[wave][lane] = acc;
-  __syncthreads();
-  if (wave == 0) {
-    float s = s_red[0][lane];
-#pragma unroll
-    for (int w = 1; w < NW; w++) s += s_red[w][lane];
-    // route (same semantics as k_core.hip's helpers), lane e holds expert e's score
+  for (int j = 0; j < ROUTE_BATCH; j++)
+    if (wave + 4 * j < np) acc += v[j];
+  s_red[wave][lane] = lane < E ? acc : 0.0f;
+}
+
+// Wave 0 only, after a barrier that made s_red visible.
+__device__ __forceinline__ void route_select(int E, int K, int mode, int *s_idx, float *s_w, float (*s_red)[64]) {
+  const int lane = threadIdx.x & 63;
+  {
+    const float s = ((s_red[0][lane] + s_red[1][lane]) + s_red[2][lane]) + s_red[3][lane];
     bool taken = false;
     if (mode == DSH_ROUTE_CFG) {
       int my_sel = 0, ns = 0;
@@ -115,7 +118,6 @@ __device__ void block_route(const float *__restrict__ partials, int np, int E, i
       }
     }
   }
-  __syncthreads();
 }
 
 // ============================================================================ partial scores
@@ -158,103 +160,118 @@ __global__ void __launch_bounds__(64) k_dec_scores_bf16(const uint16_t *__restri
 }
 
 // ============================================================================ gate_up + SwiGLU
-// 16 units per 256-thread block (4 per wave, 16 lanes per unit). Unit u < SI: shared expert row
-// pair (u, SI+u); u >= SI: routed slot k = (u-SI)/I, intermediate i. Lane sub of a unit reads the
-// 16-byte chunks sub + 16m (m < CPL) of both rows. Requires H == 256*CPL.
+// A unit is one row pair (gate row, up row) handled by 16 lanes; lane sub reads the 16-byte chunks
+// sub + 16m (m < CPL) of both rows (H == 256*CPL). Block b, wave w: lanes 0-15 take shared-expert
+// unit 4b+w (rows u and SI+u), lanes 16-63 take routed units 12b+3w+0..2 of the K*I routed ones
+// (slot k = u/I, intermediate i = u%I). Every lane issues the same loads in the same order: x,
+// the routing partials and the shared rows first (lanes 16-63 repeat lanes 0-15's shared addresses,
+// which the wave's load coalesces), the routed rows after the routing (lanes 0-15 repeat lanes
+// 16-31's). With no load or store under a branch, every wait covers exactly the loads it needs.
+// x is staged once per block in LDS; all stores happen at the end. The empty asm statements keep
+// the compiler from reordering the three load groups (x and partials are not __restrict__ so
+// that they cannot be moved across them).
 template <int CPL>
-__global__ void __launch_bounds__(256) k_dec_gate_up(dsh_layer_t L, const float *__restrict__ x_in,
-                                                     const int *__restrict__ step, int stride,
-                                                     const float *__restrict__ partials, int np, int mode, int bf16sim,
+__global__ void __launch_bounds__(256) k_dec_gate_up(dsh_layer_t L, const float *x_in, const int *__restrict__ step,
+                                                     int stride, const float *partials, int np, int mode, int bf16sim,
                                                      dsh_layer_work_t wk) {
+  constexpr int XV = (64 * CPL + 255) / 256;  // 16-byte pieces of x per thread
   __shared__ int s_idx[64];
   __shared__ float s_w[64];
   __shared__ float s_red[4][64];
+  __shared__ __attribute__((aligned(16))) float s_x[256 * CPL];
   const float *x = at_step(x_in, step, stride);
   const int H = L.H, I = L.I, K = L.K, SI = L.SI;
-  const int lane = threadIdx.x & 63, sub = lane & 15;
-  const int unit0 = blockIdx.x * 16;
-  const int u = unit0 + (threadIdx.x >> 4);
-  const bool shared_block = unit0 + 15 < SI;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane & 15, grp = lane >> 4;
+  const int KI = K * I;
 
-  // x chunks (independent of routing)
-  float xv[CPL][16];
+  f32x4 xr[XV];
 #pragma unroll
-  for (int m = 0; m < CPL; m++) load_f16x(x + 16 * (sub + 16 * m), xv[m]);
-
-  const int8_t *grow, *urow;
-  float2 sog, sou;
-  int hpos;
-  bool live = true;
-  if (shared_block) {
-    grow = L.sgu_q + (size_t)u * H;
-    urow = L.sgu_q + (size_t)(SI + u) * H;
-    hpos = K * I + u;
-  } else {
-    block_route<4>(partials, np, L.E, K, mode, s_idx, s_w, s_red);
-    if (unit0 <= SI && SI < unit0 + 16 && threadIdx.x < K) {  // this block publishes the routing
-      wk.idx[threadIdx.x] = s_idx[threadIdx.x];
-      wk.w[threadIdx.x] = s_w[threadIdx.x];
+  for (int j = 0; j < XV; j++) xr[j] = ((const f32x4 *)x)[min((int)threadIdx.x + 256 * j, 64 * CPL - 1)];
+  asm volatile("" ::: "memory");  // keeps the issue order: x, partials, shared rows
+  float pv[ROUTE_BATCH];
+  route_load(partials, np, pv);
+  asm volatile("" ::: "memory");
+  const int su = blockIdx.x * 4 + wave;
+  const int suc = su < SI ? su : 0;
+  u32x4 sg[CPL], sup[CPL];
+  {
+    const int8_t *grow = L.sgu_q + (size_t)suc * H;
+    const int8_t *urow = L.sgu_q + (size_t)(SI + suc) * H;
+#pragma unroll
+    for (int m = 0; m < CPL; m++) {
+      sg[m] = dsh_load_nt(grow + 16 * (sub + 16 * m));
+      sup[m] = dsh_load_nt(urow + 16 * (sub + 16 * m));
     }
-    int r = u - SI;
-    int total_routed = K * I;
-    live = r < total_routed;
-    r = live ? r : 0;
-    int k = r / I, i = r - k * I;
-    int e = s_idx[k];
-    hpos = r;
-    if (e < 0) {
-      live = false;
-      e = 0;
-      if (sub == 0 && u - SI < total_routed) wk.h[hpos] = 0.0f;
-    }
-    size_t base = (size_t)e * 2 * I;
-    grow = L.gu_q + (base + i) * H;
-    urow = L.gu_q + (base + I + i) * H;
-    if (u - SI >= total_routed) return;
   }
-  u32x4 wg[CPL], wu[CPL];
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int j = 0; j < XV; j++) {
+    const int t = min((int)threadIdx.x + 256 * j, 64 * CPL - 1);  // duplicate stores of the same value
+    ((f32x4 *)s_x)[t] = xr[j];
+  }
+  route_reduce(np, L.E, pv, s_red);
+  __syncthreads();  // s_red, s_x
+  if (wave == 0) route_select(L.E, K, mode, s_idx, s_w, s_red);
+  __syncthreads();  // s_idx, s_w
+
+  const int ru = blockIdx.x * 12 + wave * 3 + max(grp - 1, 0);
+  const int r = ru < KI ? ru : 0;
+  const int k = r / I, i = r - k * I;
+  const int e = s_idx[k];
+  const size_t base = (size_t)max(e, 0) * 2 * I;
+  u32x4 rg[CPL], rup[CPL];
+  {
+    const int8_t *grow = L.gu_q + (base + i) * H;
+    const int8_t *urow = L.gu_q + (base + I + i) * H;
+#pragma unroll
+    for (int m = 0; m < CPL; m++) {
+      rg[m] = dsh_load_nt(grow + 16 * (sub + 16 * m));
+      rup[m] = dsh_load_nt(urow + 16 * (sub + 16 * m));
+    }
+  }
+  const bool is_shared = grp == 0;
+  const float2 sog = is_shared ? so_pair(L.sgu_so, suc) : so_pair(L.gu_so, base + i);
+  const float2 sou = is_shared ? so_pair(L.sgu_so, SI + suc) : so_pair(L.gu_so, base + I + i);
+  float xpart = 0.0f, dg = 0.0f, du = 0.0f;
 #pragma unroll
   for (int m = 0; m < CPL; m++) {
-    wg[m] = dsh_load_nt(grow + 16 * (sub + 16 * m));
-    wu[m] = dsh_load_nt(urow + 16 * (sub + 16 * m));
-  }
-  if (shared_block) {
-    sog = so_pair(L.sgu_so, u);
-    sou = so_pair(L.sgu_so, SI + u);
-  } else {
-    int r = u - SI, k = r / I, i = r - k * I;
-    int e = max(s_idx[k], 0);
-    size_t base = (size_t)e * 2 * I;
-    sog = so_pair(L.gu_so, base + i);
-    sou = so_pair(L.gu_so, base + I + i);
-  }
-  float xpart = 0.0f;
-#pragma unroll
-  for (int m = 0; m < CPL; m++) {
+    float xv[16];
+    load_f16x(s_x + 16 * (sub + 16 * m), xv);
     float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 16; j++) s += xv[m][j];
+    for (int j = 0; j < 16; j++) s += xv[j];
     xpart += s;
-  }
-  float dg = 0.0f, du = 0.0f;
+    u32x4 wg, wu;
 #pragma unroll
-  for (int m = 0; m < CPL; m++) {
-    dg = dsh_dot16_u8(wg[m], xv[m], dg);
-    du = dsh_dot16_u8(wu[m], xv[m], du);
+    for (int d = 0; d < 4; d++) {
+      wg[d] = is_shared ? sg[m][d] : rg[m][d];
+      wu[d] = is_shared ? sup[m][d] : rup[m][d];
+    }
+    dg = dsh_dot16_u8(wg, xv, dg);
+    du = dsh_dot16_u8(wu, xv, du);
   }
   const float xsum = dsh_row16_sum(xpart);
   dg = dsh_row16_sum(dg);
   du = dsh_row16_sum(du);
-  if (sub == 0 && live) {
-    float g = __builtin_fmaf(sog.x, dg, sog.y * xsum);
-    float up = __builtin_fmaf(sou.x, du, sou.y * xsum);
-    if (bf16sim) {
-      g = dsh_bf16_round_half_up(g);
-      up = dsh_bf16_round_half_up(up);
+  float g = __builtin_fmaf(sog.x, dg, sog.y * xsum);
+  float up = __builtin_fmaf(sou.x, du, sou.y * xsum);
+  if (bf16sim) {
+    g = dsh_bf16_round_half_up(g);
+    up = dsh_bf16_round_half_up(up);
+  }
+  float hv = dsh_swiglu(g, up);
+  if (bf16sim) hv = dsh_bf16_round_half_up(hv);
+  // stores: shared unit (KI + su), routed unit r (0 when DECODE routing left slot k empty)
+  if (sub == 0) {
+    if (is_shared) {
+      if (su < SI) wk.h[KI + su] = hv;
+    } else if (ru < KI) {
+      wk.h[r] = e >= 0 ? hv : 0.0f;
     }
-    float hv = dsh_swiglu(g, up);
-    if (bf16sim) hv = dsh_bf16_round_half_up(hv);
-    wk.h[hpos] = hv;
+  }
+  if (blockIdx.x == 0 && threadIdx.x < K) {  // block 0 publishes the routing
+    wk.idx[threadIdx.x] = s_idx[threadIdx.x];
+    wk.w[threadIdx.x] = s_w[threadIdx.x];
   }
 }
 
@@ -486,7 +503,8 @@ __global__ void __launch_bounds__(256) k_lm_argmax_final(const unsigned long lon
 }
 
 // ============================================================================ launchers
-#define DEC_R 8
+// Rows per down block (and per router partial): keeps the partial count within 4 * ROUTE_BATCH.
+static inline int dec_rows(int H) { return H <= 32 * ROUTE_BATCH ? 8 : 16; }
 #define LM_D 1
 
 extern "C" {
@@ -494,16 +512,19 @@ extern "C" {
 int dsh_dec_supported(int H, int I, int E, int K, int SI) {
   if (H % 256 || H / 256 > 8) return 0;           // gate_up: H == 256*CPL
   if (I % 16 || I / 16 > 64 || SI % I) return 0;  // down: one chunk per lane
-  if (K + SI / I != 8 || H % DEC_R) return 0;
+  if (K + SI / I != 8 || H % dec_rows(H) || H / dec_rows(H) > 4 * ROUTE_BATCH) return 0;
   if (E > 64 || K > E) return 0;
   return 1;
 }
 
-int dsh_dec_partials(int H) { return H / DEC_R; }
+int dsh_dec_partials(int H) { return H / dec_rows(H); }
 
 hipError_t dsh_launch_dec_partial_scores(const float *Wr, const float *x_in, const int *step, int stride, int H, int E,
                                          float *partials, hipStream_t s) {
-  k_dec_partial_scores<DEC_R><<<H / DEC_R, 64, 0, s>>>(Wr, x_in, step, stride, H, E, partials);
+  if (dec_rows(H) == 8)
+    k_dec_partial_scores<8><<<H / 8, 64, 0, s>>>(Wr, x_in, step, stride, H, E, partials);
+  else
+    k_dec_partial_scores<16><<<H / 16, 64, 0, s>>>(Wr, x_in, step, stride, H, E, partials);
   return hipGetLastError();
 }
 
@@ -517,8 +538,8 @@ hipError_t dsh_launch_dec_scores_bf16(const uint16_t *Wr, const float *x_in, con
 hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const int *step, int stride,
                                   const float *partials, int np, int route_mode, int bf16sim,
                                   const dsh_layer_work_t *wk, hipStream_t s) {
-  int total = L->K * L->I + L->SI;
-  int blocks = (total + 15) / 16;
+  const int ki = L->K * L->I;
+  const int blocks = max((L->SI + 3) / 4, (ki + 11) / 12);
 #define GU(N)                                                                                                  \
   case N:                                                                                                      \
     k_dec_gate_up<N><<<blocks, 256, 0, s>>>(*L, x_in, step, stride, partials, np, route_mode, bf16sim, *wk);   \
@@ -535,8 +556,12 @@ hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const
 hipError_t dsh_launch_dec_down(const dsh_layer_t *L, const float *x_in, const int *step, int stride, float *x_out,
                                int residual, int bf16sim, const dsh_layer_work_t *wk, const float *Wr_next,
                                int E_next, float *partials_next, hipStream_t s) {
-  k_dec_down<DEC_R><<<L->H / DEC_R, 512, 0, s>>>(*L, x_in, step, stride, x_out, residual, bf16sim, *wk, Wr_next,
-                                                 E_next, partials_next);
+  if (dec_rows(L->H) == 8)
+    k_dec_down<8><<<L->H / 8, 512, 0, s>>>(*L, x_in, step, stride, x_out, residual, bf16sim, *wk, Wr_next, E_next,
+                                           partials_next);
+  else
+    k_dec_down<16><<<L->H / 16, 512, 0, s>>>(*L, x_in, step, stride, x_out, residual, bf16sim, *wk, Wr_next, E_next,
+                                             partials_next);
   return hipGetLastError();
 }
 
