@@ -66,16 +66,23 @@ __device__ __forceinline__ float dsh_row4_sum(float v) {
   return v;
 }
 
+__device__ __forceinline__ float dsh_readlane(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Sum over the wave, (r0 + r1) + (r2 + r3) of the four 16-lane row sums; the result is uniform.
+// Row sums by DPP, rows combined through readlane (no LDS permutes on the critical path).
 __device__ __forceinline__ float dsh_wave_sum(float v) {
   v = dsh_row16_sum(v);
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  return (dsh_readlane(v, 0) + dsh_readlane(v, 16)) + (dsh_readlane(v, 32) + dsh_readlane(v, 48));
 }
 
 __device__ __forceinline__ float dsh_wave_max(float v) {
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+  v = fmaxf(v, dsh_dpp<0xB1>(v));
+  v = fmaxf(v, dsh_dpp<0x4E>(v));
+  v = fmaxf(v, dsh_dpp<0x141>(v));
+  v = fmaxf(v, dsh_dpp<0x140>(v));
+  return fmaxf(fmaxf(dsh_readlane(v, 0), dsh_readlane(v, 16)), fmaxf(dsh_readlane(v, 32), dsh_readlane(v, 48)));
 }
 
 // ---------------------------------------------------------------- INT8 code helpers
@@ -135,10 +142,24 @@ __device__ __forceinline__ float dsh_key_value(unsigned long long k) {
 __device__ __forceinline__ unsigned long long dsh_umax64(unsigned long long a, unsigned long long b) {
   return a > b ? a : b;
 }
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dsh_dpp64(unsigned long long v) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, CTRL, 0xF, 0xF, false);
+  hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, CTRL, 0xF, 0xF, false);
+  return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long dsh_readlane64(unsigned long long v, int lane) {
+  uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+  return ((unsigned long long)hi << 32) | lo;
+}
+// Maximum over the wave (uniform result): DPP within each 16-lane row, readlane across rows.
 __device__ __forceinline__ unsigned long long dsh_wave_max_u64(unsigned long long v) {
-  for (int o = 32; o >= 1; o >>= 1) {
-    unsigned long long w = __shfl_xor(v, o);
-    v = dsh_umax64(v, w);
-  }
-  return v;
+  v = dsh_umax64(v, dsh_dpp64<0xB1>(v));
+  v = dsh_umax64(v, dsh_dpp64<0x4E>(v));
+  v = dsh_umax64(v, dsh_dpp64<0x141>(v));
+  v = dsh_umax64(v, dsh_dpp64<0x140>(v));
+  return dsh_umax64(dsh_umax64(dsh_readlane64(v, 0), dsh_readlane64(v, 16)),
+                    dsh_umax64(dsh_readlane64(v, 32), dsh_readlane64(v, 48)));
 }
