@@ -142,6 +142,58 @@ __device__ __forceinline__ float dsh_key_value(unsigned long long k) {
 __device__ __forceinline__ unsigned long long dsh_umax64(unsigned long long a, unsigned long long b) {
   return a > b ? a : b;
 }
+// Transposed butterfly sums of V per-lane values over the wave (V = 8 or 16). Each exchange halves
+// the values a lane carries: lanes whose partner bit is 0 keep the lower half of the pairs (j, j+V/2)
+// and lanes with the bit set the upper half (v_permlane32_swap for lane bit 5, v_permlane16_swap for
+// bit 4, a DPP row rotation or mirror with a select for bits 3 (and 2)); the last lane bits are
+// summed by DPP. On return lane l holds the sum of value l >> (6 - log2 V), i.e. value j sits in
+// lanes j*64/V .. j*64/V + 64/V - 1, all with the same bits.
+__device__ __forceinline__ void dsh_pl32_add(float *v, int half) {
+  for (int j = 0; j < half; j++) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[j + half]), false, false);
+    v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+__device__ __forceinline__ void dsh_pl16_add(float *v, int half) {
+  for (int j = 0; j < half; j++) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[j]), __float_as_uint(v[j + half]), false, false);
+    v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+// lanes with bit B keep value "hi", the others "lo"; the partner (CTRL) has the opposite bit B
+template <int CTRL>
+__device__ __forceinline__ float dsh_halve(float lo, float hi, bool bit) {
+  const float keep = bit ? hi : lo, send = bit ? lo : hi;
+  return keep + dsh_dpp<CTRL>(send);
+}
+__device__ __forceinline__ float dsh_wave_tsum8(const float *in) {
+  const int lane = threadIdx.x & 63;
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) v[j] = in[j];
+  dsh_pl32_add(v, 4);
+  dsh_pl16_add(v, 2);
+  float z = dsh_halve<0x128>(v[0], v[1], lane & 8);  // row_ror:8 pairs lane l with l ^ 8
+  z += dsh_dpp<0x141>(z);                            // row_half_mirror
+  z += dsh_dpp<0x4E>(z);
+  z += dsh_dpp<0xB1>(z);
+  return z;
+}
+__device__ __forceinline__ float dsh_wave_tsum16(const float *in) {
+  const int lane = threadIdx.x & 63;
+  float v[16];
+#pragma unroll
+  for (int j = 0; j < 16; j++) v[j] = in[j];
+  dsh_pl32_add(v, 8);
+  dsh_pl16_add(v, 4);
+  float y0 = dsh_halve<0x128>(v[0], v[2], lane & 8);
+  float y1 = dsh_halve<0x128>(v[1], v[3], lane & 8);
+  float z = dsh_halve<0x141>(y0, y1, lane & 4);  // row_half_mirror pairs l with 7 - l (bit 2 flipped)
+  z += dsh_dpp<0x4E>(z);
+  z += dsh_dpp<0xB1>(z);
+  return z;
+}
+
 template <int CTRL>
 __device__ __forceinline__ unsigned long long dsh_dpp64(unsigned long long v) {
   uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);

@@ -168,18 +168,13 @@ __global__ void __launch_bounds__(64) k_dec_scores_bf16(const uint16_t *__restri
 // which the wave's load coalesces), the routed rows after the routing (lanes 0-15 repeat lanes
 // 16-31's). With no load or store under a branch, every wait covers exactly the loads it needs.
 // x is staged once per block in LDS; all stores happen at the end. The empty asm statements keep
-// the compiler from reordering the three load groups (x and partials are not __restrict__ so
-// that they cannot be moved across them).
+// the compiler from reordering the three load groups (x and partials are not __restrict__ so that
+// they cannot be moved across them).
 template <int CPL>
-__global__ void __launch_bounds__(256) k_dec_gate_up(dsh_layer_t L, const float *x_in, const int *__restrict__ step,
-                                                     int stride, const float *partials, int np, int mode, int bf16sim,
-                                                     dsh_layer_work_t wk) {
+__device__ __forceinline__ void gate_up_body(const dsh_layer_t &L, const float *x, const float *partials, int np,
+                                             int mode, int bf16sim, const dsh_layer_work_t &wk, int blk, int *s_idx,
+                                             float *s_w, float (*s_red)[64], float *s_x) {
   constexpr int XV = (64 * CPL + 255) / 256;  // 16-byte pieces of x per thread
-  __shared__ int s_idx[64];
-  __shared__ float s_w[64];
-  __shared__ float s_red[4][64];
-  __shared__ __attribute__((aligned(16))) float s_x[256 * CPL];
-  const float *x = at_step(x_in, step, stride);
   const int H = L.H, I = L.I, K = L.K, SI = L.SI;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane & 15, grp = lane >> 4;
   const int KI = K * I;
@@ -191,7 +186,7 @@ __global__ void __launch_bounds__(256) k_dec_gate_up(dsh_layer_t L, const float 
   float pv[ROUTE_BATCH];
   route_load(partials, np, pv);
   asm volatile("" ::: "memory");
-  const int su = blockIdx.x * 4 + wave;
+  const int su = blk * 4 + wave;
   const int suc = su < SI ? su : 0;
   u32x4 sg[CPL], sup[CPL];
   {
@@ -214,7 +209,7 @@ __global__ void __launch_bounds__(256) k_dec_gate_up(dsh_layer_t L, const float 
   if (wave == 0) route_select(L.E, K, mode, s_idx, s_w, s_red);
   __syncthreads();  // s_idx, s_w
 
-  const int ru = blockIdx.x * 12 + wave * 3 + max(grp - 1, 0);
+  const int ru = blk * 12 + wave * 3 + max(grp - 1, 0);
   const int r = ru < KI ? ru : 0;
   const int k = r / I, i = r - k * I;
   const int e = s_idx[k];
@@ -263,31 +258,51 @@ __global__ void __launch_bounds__(256) k_dec_gate_up(dsh_layer_t L, const float 
   if (bf16sim) hv = dsh_bf16_round_half_up(hv);
   // stores: shared unit (KI + su), routed unit r (0 when DECODE routing left slot k empty)
   if (sub == 0) {
+    float *dst = nullptr;
+    float val = hv;
     if (is_shared) {
-      if (su < SI) wk.h[KI + su] = hv;
+      if (su < SI) dst = wk.h + KI + su;
     } else if (ru < KI) {
-      wk.h[r] = e >= 0 ? hv : 0.0f;
+      dst = wk.h + r;
+      val = e >= 0 ? hv : 0.0f;
     }
+    if (dst) *dst = val;
   }
-  if (blockIdx.x == 0 && threadIdx.x < K) {  // block 0 publishes the routing
+  if (blk == 0 && threadIdx.x < K) {  // block 0 publishes the routing (read by the host API)
     wk.idx[threadIdx.x] = s_idx[threadIdx.x];
     wk.w[threadIdx.x] = s_w[threadIdx.x];
   }
 }
 
+template <int CPL>
+__global__ void __launch_bounds__(256) k_dec_gate_up(dsh_layer_t L, const float *x_in, const int *__restrict__ step,
+                                                     int stride, const float *partials, int np, int mode, int bf16sim,
+                                                     dsh_layer_work_t wk) {
+  __shared__ int s_idx[64];
+  __shared__ float s_w[64];
+  __shared__ float s_red[4][64];
+  __shared__ __attribute__((aligned(16))) float s_x[256 * CPL];
+  gate_up_body<CPL>(L, at_step(x_in, step, stride), partials, np, mode, bf16sim, wk, blockIdx.x, s_idx, s_w, s_red,
+                    s_x);
+}
+
 // ============================================================================ down + combine
-// One 512-thread block per R output rows; wave s (0..7) owns segment s: routed slot s for s < K,
-// else the shared expert's I-wide column block s-K. Lane j < I/16 holds the 16 h values of chunk j
-// in registers and streams chunk j of each of its R rows (one 16-byte load per row, all issued
-// together). Per row the wave sums its lanes; wave 0 then combines the 8 segments per row in the
-// reference's order and, when Wr_next is given, writes this block's partial router scores for the
-// next layer. Requires I % 16 == 0, I/16 <= 64, K + SI/I == 8, H % R == 0.
+// One 512-thread block per R output rows (R = 8 or 16); wave s (0..7) owns segment s: routed slot s
+// for s < K (expert idx[s]), else the shared expert's I-wide column block s-K. Lane c < I/16 holds
+// the 16 h values of chunk c in registers and streams chunk c of each of its R rows (one 16-byte
+// load per row, all issued together). The R row dots of a wave are summed over its lanes by one
+// transposed butterfly (row j lands in lanes j*64/R..), Σh by a wave sum; wave 0 then combines the 8
+// segments per row in the reference's order (routed slots in top-k order with their weights, then
+// the shared expert), adds the residual and, when Wr_next is given, writes this block's partial
+// router scores for the next layer. Requires I % 16 == 0, I/16 <= 64, K + SI/I == 8, H % R == 0.
 template <int R>
 __global__ void __launch_bounds__(512) k_dec_down(dsh_layer_t L, const float *__restrict__ x_in,
                                                   const int *__restrict__ step, int stride, float *__restrict__ x_out,
                                                   int residual, int bf16sim, dsh_layer_work_t wk,
                                                   const float *__restrict__ Wr_next, int E_next,
                                                   float *__restrict__ partials_next) {
+  static_assert(R == 8 || R == 16, "row butterfly for 8 or 16 rows");
+  constexpr int LPR = 64 / R;  // lanes holding one row's sum
   __shared__ float s_val[8][R];
   __shared__ float s_hs[8];
   __shared__ float s_x[R];
@@ -298,6 +313,7 @@ __global__ void __launch_bounds__(512) k_dec_down(dsh_layer_t L, const float *__
   const int r0 = blockIdx.x * R;
   const bool lane_on = lane < CI;
   const int ch = lane_on ? lane : 0;
+  const int myrow = lane / LPR;  // the row whose sum this lane holds after the butterfly
 
   // next layer's router columns for these rows (independent of everything else)
   float wr[R];
@@ -327,8 +343,7 @@ __global__ void __launch_bounds__(512) k_dec_down(dsh_layer_t L, const float *__
   const int hbase = seg < K ? seg * I : K * I + (seg - K) * I;
   float hv[16];
   load_f16x(wk.h + hbase + 16 * ch, hv);
-  float2 so = make_float2(0.0f, 0.0f);
-  if (lane < R) so = so_pair(seg < K ? L.dn_so : L.sdn_so, so_base + r0 + lane);
+  const float2 so = so_pair(seg < K ? L.dn_so : L.sdn_so, so_base + r0 + myrow);
 
   float hp = 0.0f;
   if (lane_on) {
@@ -339,20 +354,14 @@ __global__ void __launch_bounds__(512) k_dec_down(dsh_layer_t L, const float *__
   float dots[R];
 #pragma unroll
   for (int j = 0; j < R; j++) dots[j] = lane_on ? dsh_dot16_u8(wv[j], hv, 0.0f) : 0.0f;
-#pragma unroll
-  for (int j = 0; j < R; j++) dots[j] = dsh_wave_sum(dots[j]);
-  // lane j (< R) holds row j's dot and its (scale, offset)
-  float mine = 0.0f;
-#pragma unroll
-  for (int j = 0; j < R; j++)
-    if (lane == j) mine = dots[j];
-  if (lane < R) {
+  const float mine = R == 8 ? dsh_wave_tsum8(dots) : dsh_wave_tsum16(dots);
+  if (lane % LPR == 0) {
     float v;
     if (seg < K)
       v = e >= 0 ? __builtin_fmaf(so.x, mine, so.y * hs) : 0.0f;  // e_k = scale*dot + off*Σh
     else
-      v = mine;  // shared: raw dot, combined below with its sibling block
-    s_val[seg][lane] = v;
+      v = mine;  // shared: raw dot, combined below with its sibling segments
+    s_val[seg][myrow] = v;
   }
   if (lane == 0) s_hs[seg] = hs;
   __syncthreads();
@@ -535,11 +544,14 @@ hipError_t dsh_launch_dec_scores_bf16(const uint16_t *Wr, const float *x_in, con
   return hipGetLastError();
 }
 
+static int dec_gate_up_blocks(const dsh_layer_t *L) {
+  return max((L->SI + 3) / 4, (L->K * L->I + 11) / 12);
+}
+
 hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const int *step, int stride,
                                   const float *partials, int np, int route_mode, int bf16sim,
                                   const dsh_layer_work_t *wk, hipStream_t s) {
-  const int ki = L->K * L->I;
-  const int blocks = max((L->SI + 3) / 4, (ki + 11) / 12);
+  const int blocks = dec_gate_up_blocks(L);
 #define GU(N)                                                                                                  \
   case N:                                                                                                      \
     k_dec_gate_up<N><<<blocks, 256, 0, s>>>(*L, x_in, step, stride, partials, np, route_mode, bf16sim, *wk);   \

@@ -299,11 +299,13 @@ struct ds_hip_stack {
   int vocab, H;
   int route_mode, bf16sim;
   int lm_fast;
-  void *work;              /* step counter, x buffer, candidates */
+  void *work;              /* step counter, x buffer, candidates, partials */
+  size_t work_bytes;
   int *step;
   float *xbuf;
   unsigned long long *cand;
   int ncand;
+  float *partials[2];      /* router partial scores, by layer parity */
   const float *xs;
   int stride;
   int *tokens;
@@ -339,7 +341,9 @@ ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers,
   S->bf16sim = ds_bf16_simulate_python;
   S->lm_fast = dsh_dec_lm_eligible(lm_head_dev, H, vocab, dsr_threads());
   S->ncand = S->lm_fast ? dsh_dec_lm_blocks(vocab) : dsh_argmax_avx_blocks(vocab);
-  size_t bytes = 256 + al((size_t)H * 4) + al((size_t)S->ncand * 8);
+  const size_t np_bytes = al((size_t)layers[0]->np * 64 * 4);
+  size_t off_x = 256, off_c = off_x + al((size_t)H * 4), off_p = off_c + al((size_t)S->ncand * 8);
+  size_t bytes = off_p + 2 * np_bytes;
   hipError_t e = hipMalloc(&S->work, bytes);
   if (e != hipSuccess) {
     dsr_fail("stack allocation", e);
@@ -347,10 +351,13 @@ ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers,
     free(S);
     return NULL;
   }
+  S->work_bytes = bytes;
   hipMemsetAsync(S->work, 0, bytes, dsr_stream);
   S->step = (int *)S->work;
-  S->xbuf = (float *)((char *)S->work + 256);
-  S->cand = (unsigned long long *)((char *)S->work + 256 + al((size_t)H * 4));
+  S->xbuf = (float *)((char *)S->work + off_x);
+  S->cand = (unsigned long long *)((char *)S->work + off_c);
+  S->partials[0] = (float *)((char *)S->work + off_p);
+  S->partials[1] = (float *)((char *)S->work + off_p + np_bytes);
   return S;
 }
 
@@ -376,32 +383,41 @@ size_t ds_hip_stack_bytes_per_step(const ds_hip_stack_t *S) {
 }
 
 /* Kernels launched per decode step (for profiling). */
+/* Kernels per step: CFG routing: the first layer's partial scores, then gate_up and down per layer;
+ * DECODE routing: scores, gate_up and down per layer. Then the LM head (2 kernels). */
 static int stack_kernel_count(const ds_hip_stack_t *S) {
-  int per_layer = S->route_mode == DS_HIP_ROUTE_CFG ? 2 : 3;
-  return (S->route_mode == DS_HIP_ROUTE_CFG ? 1 : 0) + per_layer * S->n_layers + 2;
+  int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
+  return (cfg ? 1 : S->n_layers) + 2 * S->n_layers + 2;
 }
 
-/* One decode step; ev (optional) receives an event before the first kernel and after each one. */
+/* One decode step; ev (optional) receives an event before the first kernel and after each one.
+ * Layer l reads router partials from partials[l & 1]; in CFG mode its down kernel writes layer
+ * l+1's into partials[(l + 1) & 1]. */
 static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
   hipError_t e = hipSuccess;
   int n = 0;
-  ds_hip_layer_t *L0 = S->layers[0];
-  float *partials = L0->partials;
-  const dsh_layer_work_t *wk = &L0->wk;
-  int np = 0;
+  const int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
+  const dsh_layer_work_t *wk = &S->layers[0]->wk;
   if (ev) e = hipEventRecord(ev[n++], dsr_stream);
-  if (e == hipSuccess && S->route_mode == DS_HIP_ROUTE_CFG) {
-    e = scores_enqueue(L0, S->xs, S->step, S->stride, S->route_mode, partials, &np);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
-  }
   for (int l = 0; l < S->n_layers && e == hipSuccess; l++) {
     const ds_hip_layer_t *L = S->layers[l];
     const float *xin = l == 0 ? S->xs : S->xbuf;
     const int *st = l == 0 ? S->step : NULL;
     int stride = l == 0 ? S->stride : 0;
-    const ds_hip_layer_t *next = l + 1 < S->n_layers ? S->layers[l + 1] : NULL;
-    e = layer_enqueue(L, wk, partials, S->route_mode == DS_HIP_ROUTE_CFG, L->np, xin, st, stride, S->xbuf,
-                      S->route_mode, 1, S->bf16sim, next, ev, &n);
+    float *pin = S->partials[l & 1], *pout = S->partials[(l + 1) & 1];
+    int np = L->np;
+    if (!cfg || l == 0) {
+      e = scores_enqueue(L, xin, st, stride, S->route_mode, pin, &np);
+      if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+      if (e != hipSuccess) break;
+    }
+    const ds_hip_layer_t *next = cfg && l + 1 < S->n_layers ? S->layers[l + 1] : NULL;
+    e = dsh_launch_dec_gate_up(&L->d, xin, st, stride, pin, np, S->route_mode, S->bf16sim, wk, dsr_stream);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+    if (e == hipSuccess)
+      e = dsh_launch_dec_down(&L->d, xin, st, stride, S->xbuf, 1, S->bf16sim, wk, next ? next->d.router_f32 : NULL,
+                              next ? next->E : 0, next ? pout : NULL, dsr_stream);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
   }
   if (e != hipSuccess) return e;
   if (S->lm_fast) {
@@ -446,9 +462,10 @@ int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int *t
   return ds_hip_stack_reset(S);
 }
 
+/* Zeroes the step counter (and the work buffers with it). */
 int ds_hip_stack_reset(ds_hip_stack_t *S) {
   if (!S) return -1;
-  DSR_TRY(hipMemsetAsync(S->step, 0, sizeof(int), dsr_stream), "reset step");
+  DSR_TRY(hipMemsetAsync(S->work, 0, S->work_bytes, dsr_stream), "reset stack");
   return 0;
 }
 
@@ -494,12 +511,12 @@ const char *ds_hip_stack_kernel_name(const ds_hip_stack_t *S, int i) {
   int nk = stack_kernel_count(S);
   if (i == nk - 2) return "lm_head.argmax";
   if (i == nk - 1) return "lm_head.final";
-  if (S->route_mode == DS_HIP_ROUTE_CFG) {
-    if (i == 0) return "scores";
-    return (i - 1) % 2 == 0 ? "gate_up" : "down";
-  }
-  static const char *names[3] = {"scores", "gate_up", "down"};
-  return names[i % 3];
+  const int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
+  if (cfg && i == 0) return "scores";
+  const int per = cfg ? 2 : 3; /* kernels per layer */
+  const int j = (cfg ? i - 1 : i) % per;
+  if (!cfg && j == 0) return "scores";
+  return j == per - 2 ? "gate_up" : "down";
 }
 
 int ds_hip_profile_stack(ds_hip_stack_t *S, int n_steps, float *ms_out) {
