@@ -91,6 +91,7 @@ SIGNATURES = {
     "ds_hip_stack_hidden": (C.c_int, [vp, f32p]),
     "ds_hip_stack_bytes_per_step": (C.c_size_t, [vp]),
     "ds_hip_time_stack": (C.c_int, [vp, C.c_int, C.POINTER(C.c_float)]),
+    "ds_hip_time_lm_head": (C.c_int, [vp, C.c_int, C.POINTER(C.c_float)]),
     "ds_hip_stack_kernel_count": (C.c_int, [vp]),
     "ds_hip_stack_kernel_name": (C.c_char_p, [vp, C.c_int]),
     "ds_hip_profile_stack": (C.c_int, [vp, C.c_int, f32p]),

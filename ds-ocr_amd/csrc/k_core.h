@@ -59,6 +59,7 @@ typedef struct {
   const int8_t *sdn_q;  /* [H][SI] shared down */
   const float *sdn_so;  /* [H] */
   const float *router_f32;     /* [E][H] */
+  const float *router_f32_t;   /* [H][E]: the same f32 router transposed (partial scores read rows) */
   const uint16_t *router_bf16; /* [E][H] */
   int H, I, E, K, SI;
 } dsh_layer_t;
@@ -78,7 +79,8 @@ hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int
 /* ---- latency-oriented decode kernels (k_dec.hip) ---- */
 int dsh_dec_supported(int H, int I, int E, int K, int SI);
 int dsh_dec_partials(int H); /* partial score rows written per layer in CFG mode */
-hipError_t dsh_launch_dec_partial_scores(const float *Wr, const float *x_in, const int *step, int stride, int H, int E,
+hipError_t dsh_launch_transpose_f32(const float *src, float *dst, int rows, int cols, hipStream_t s);
+hipError_t dsh_launch_dec_partial_scores(const float *WrT, const float *x_in, const int *step, int stride, int H, int E,
                                          float *partials, hipStream_t s);
 hipError_t dsh_launch_dec_scores_bf16(const uint16_t *Wr, const float *x_in, const int *step, int stride, int H, int E,
                                       int nthreads, float *partials, hipStream_t s);
@@ -86,7 +88,7 @@ hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const
                                   const float *partials, int np, int route_mode, int bf16sim,
                                   const dsh_layer_work_t *wk, hipStream_t s);
 hipError_t dsh_launch_dec_down(const dsh_layer_t *L, const float *x_in, const int *step, int stride, float *x_out,
-                               int residual, int bf16sim, const dsh_layer_work_t *wk, const float *Wr_next,
+                               int residual, int bf16sim, const dsh_layer_work_t *wk, const float *WrT_next,
                                int E_next, float *partials_next, hipStream_t s);
 int dsh_dec_lm_blocks(int vocab);
 int dsh_dec_lm_supported(int in_dim);

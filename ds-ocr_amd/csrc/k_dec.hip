@@ -122,9 +122,10 @@ __device__ __forceinline__ void route_select(int E, int K, int mode, int *s_idx,
 
 // ============================================================================ partial scores
 // partials[b][e] = Σ_{r in rows of block b} Wr[e][r] * x[r] for R consecutive rows per block
-// (f32 router, CFG mode); the row order inside a block is sequential.
+// (f32 router, CFG mode); the row order inside a block is sequential. WrT is the router
+// transposed ([H][E]), so a block reads R contiguous rows of E floats.
 template <int R>
-__global__ void __launch_bounds__(64) k_dec_partial_scores(const float *__restrict__ Wr, const float *__restrict__ x_in,
+__global__ void __launch_bounds__(64) k_dec_partial_scores(const float *__restrict__ WrT, const float *__restrict__ x_in,
                                                            const int *__restrict__ step, int stride, int H, int E,
                                                            float *__restrict__ partials) {
   const float *x = at_step(x_in, step, stride);
@@ -134,13 +135,26 @@ __global__ void __launch_bounds__(64) k_dec_partial_scores(const float *__restri
     float w[R], xv[R];
 #pragma unroll
     for (int j = 0; j < R; j++) {
-      w[j] = Wr[(size_t)lane * H + r0 + j];
+      w[j] = WrT[(size_t)(r0 + j) * E + lane];
       xv[j] = x[r0 + j];
     }
 #pragma unroll
     for (int j = 0; j < R; j++) p = __builtin_fmaf(w[j], xv[j], p);
   }
   partials[(size_t)blockIdx.x * 64 + lane] = lane < E ? p : 0.0f;
+}
+
+// dst[c][r] = src[r][c] for a rows x cols f32 matrix (32x32 tiles through LDS).
+__global__ void __launch_bounds__(256) k_transpose_f32(const float *__restrict__ src, float *__restrict__ dst, int rows,
+                                                       int cols) {
+  __shared__ float t[32][33];
+  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int i = ty; i < 32; i += 8)
+    if (r0 + i < rows && c0 + tx < cols) t[i][tx] = src[(size_t)(r0 + i) * cols + c0 + tx];
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8)
+    if (c0 + i < cols && r0 + tx < rows) dst[(size_t)(c0 + i) * rows + r0 + tx] = t[tx][i];
 }
 
 // DECODE mode: full scores in the reference's AVX-512 order, written as the single partial.
@@ -293,13 +307,14 @@ __global__ void __launch_bounds__(256) k_dec_gate_up(dsh_layer_t L, const float 
 // load per row, all issued together). The R row dots of a wave are summed over its lanes by one
 // transposed butterfly (row j lands in lanes j*64/R..), Σh by a wave sum; wave 0 then combines the 8
 // segments per row in the reference's order (routed slots in top-k order with their weights, then
-// the shared expert), adds the residual and, when Wr_next is given, writes this block's partial
+// the shared expert), adds the residual and, when WrT_next (the next layer's f32 router, transposed
+// to [H][E]) is given, writes this block's partial
 // router scores for the next layer. Requires I % 16 == 0, I/16 <= 64, K + SI/I == 8, H % R == 0.
 template <int R>
 __global__ void __launch_bounds__(512) k_dec_down(dsh_layer_t L, const float *__restrict__ x_in,
                                                   const int *__restrict__ step, int stride, float *__restrict__ x_out,
                                                   int residual, int bf16sim, dsh_layer_work_t wk,
-                                                  const float *__restrict__ Wr_next, int E_next,
+                                                  const float *__restrict__ WrT_next, int E_next,
                                                   float *__restrict__ partials_next) {
   static_assert(R == 8 || R == 16, "row butterfly for 8 or 16 rows");
   constexpr int LPR = 64 / R;  // lanes holding one row's sum
@@ -317,9 +332,9 @@ __global__ void __launch_bounds__(512) k_dec_down(dsh_layer_t L, const float *__
 
   // next layer's router columns for these rows (independent of everything else)
   float wr[R];
-  if (Wr_next && seg == 0 && lane < E_next) {
+  if (WrT_next && seg == 0 && lane < E_next) {
 #pragma unroll
-    for (int j = 0; j < R; j++) wr[j] = Wr_next[(size_t)lane * H + r0 + j];
+    for (int j = 0; j < R; j++) wr[j] = WrT_next[(size_t)(r0 + j) * E_next + lane];
   }
   int e = -2;
   const int8_t *wbase;
@@ -387,7 +402,7 @@ __global__ void __launch_bounds__(512) k_dec_down(dsh_layer_t L, const float *__
       x_out[r] = xo;
       s_x[lane] = xo;
     }
-    if (Wr_next) {
+    if (WrT_next) {
       // wave-local: lanes < R wrote s_x; make it visible to the other lanes of this wave
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -429,6 +444,7 @@ __global__ void __launch_bounds__(256) k_dec_lm_argmax(const uint16_t *W, const 
     src[j] = (const uint8_t *)W + (size_t)r * row_bytes + 16 * piece;
   }
   uint8_t *wtile = tile[wave];
+  const uint8_t *xdummy = (const uint8_t *)x + 16 * (lane % (in_dim / 4));  // in bounds: in_dim*4 bytes
   float acc[32];
 #pragma unroll
   for (int c = 0; c < 32; c++) acc[c] = 0.0f;
@@ -448,9 +464,11 @@ __global__ void __launch_bounds__(256) k_dec_lm_argmax(const uint16_t *W, const 
       const int t = t0 + s;
 #pragma unroll
       for (int j = 0; j < 8; j++) *(u32x4 *)(wtile + (8 * j + lrow) * PITCH + 16 * piece) = ring[s][j];
-      const int tn = min(t + D, NT - 1);  // refill; the last D refills re-read the final line
+      // refill; past the last line the refill reads x instead (a few L2-resident bytes), so no line
+      // of W is fetched twice
+      const bool more = t + D < NT;
 #pragma unroll
-      for (int j = 0; j < 8; j++) ring[s][j] = dsh_load_nt(src[j] + 128 * tn);
+      for (int j = 0; j < 8; j++) ring[s][j] = dsh_load_nt(more ? src[j] + 128 * (t + D) : xdummy);
       // the tile is wave-private and LDS executes a wave's operations in order: these fences only
       // keep the compiler from moving the reads above the writes (and the next writes above them)
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -528,12 +546,17 @@ int dsh_dec_supported(int H, int I, int E, int K, int SI) {
 
 int dsh_dec_partials(int H) { return H / dec_rows(H); }
 
-hipError_t dsh_launch_dec_partial_scores(const float *Wr, const float *x_in, const int *step, int stride, int H, int E,
+hipError_t dsh_launch_transpose_f32(const float *src, float *dst, int rows, int cols, hipStream_t s) {
+  k_transpose_f32<<<dim3((cols + 31) / 32, (rows + 31) / 32), 256, 0, s>>>(src, dst, rows, cols);
+  return hipGetLastError();
+}
+
+hipError_t dsh_launch_dec_partial_scores(const float *WrT, const float *x_in, const int *step, int stride, int H, int E,
                                          float *partials, hipStream_t s) {
   if (dec_rows(H) == 8)
-    k_dec_partial_scores<8><<<H / 8, 64, 0, s>>>(Wr, x_in, step, stride, H, E, partials);
+    k_dec_partial_scores<8><<<H / 8, 64, 0, s>>>(WrT, x_in, step, stride, H, E, partials);
   else
-    k_dec_partial_scores<16><<<H / 16, 64, 0, s>>>(Wr, x_in, step, stride, H, E, partials);
+    k_dec_partial_scores<16><<<H / 16, 64, 0, s>>>(WrT, x_in, step, stride, H, E, partials);
   return hipGetLastError();
 }
 
@@ -566,13 +589,13 @@ hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const
 }
 
 hipError_t dsh_launch_dec_down(const dsh_layer_t *L, const float *x_in, const int *step, int stride, float *x_out,
-                               int residual, int bf16sim, const dsh_layer_work_t *wk, const float *Wr_next,
+                               int residual, int bf16sim, const dsh_layer_work_t *wk, const float *WrT_next,
                                int E_next, float *partials_next, hipStream_t s) {
   if (dec_rows(L->H) == 8)
-    k_dec_down<8><<<L->H / 8, 512, 0, s>>>(*L, x_in, step, stride, x_out, residual, bf16sim, *wk, Wr_next, E_next,
+    k_dec_down<8><<<L->H / 8, 512, 0, s>>>(*L, x_in, step, stride, x_out, residual, bf16sim, *wk, WrT_next, E_next,
                                            partials_next);
   else
-    k_dec_down<16><<<L->H / 16, 512, 0, s>>>(*L, x_in, step, stride, x_out, residual, bf16sim, *wk, Wr_next, E_next,
+    k_dec_down<16><<<L->H / 16, 512, 0, s>>>(*L, x_in, step, stride, x_out, residual, bf16sim, *wk, WrT_next, E_next,
                                              partials_next);
   return hipGetLastError();
 }

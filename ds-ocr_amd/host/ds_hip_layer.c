@@ -62,6 +62,7 @@ ds_hip_layer_t *ds_hip_layer_create(int hidden, int inter, int n_experts, int to
   REGION(K * 4);                  /* 12 w */
   REGION((K * I + SI) * 4);       /* 13 h */
   REGION((H / 8) * 64 * 4);       /* 14 router partial scores */
+  REGION(E * H * 4);              /* 15 router f32, transposed [H][E] */
 #undef REGION
   hipError_t e = hipMalloc(&L->arena, n);
   if (e != hipSuccess) {
@@ -87,6 +88,7 @@ ds_hip_layer_t *ds_hip_layer_create(int hidden, int inter, int n_experts, int to
   L->d.sdn_so = (const float *)(b + off[7]);
   L->d.router_f32 = (const float *)(b + off[8]);
   L->d.router_bf16 = (const uint16_t *)(b + off[9]);
+  L->d.router_f32_t = (const float *)(b + off[15]);
   L->d.H = hidden;
   L->d.I = inter;
   L->d.E = n_experts;
@@ -115,6 +117,8 @@ int ds_hip_layer_set_router(ds_hip_layer_t *L, const float *router_f32, const ui
   size_t n = (size_t)L->E * L->H;
   if (router_f32) {
     if (dsr_h2d((void *)L->d.router_f32, router_f32, n * 4)) return -1;
+    DSR_TRY(dsh_launch_transpose_f32(L->d.router_f32, (float *)L->d.router_f32_t, L->E, L->H, dsr_stream),
+            "router transpose");
     L->have_f32 = 1;
   }
   if (router_bf16) {
@@ -131,6 +135,8 @@ int ds_hip_layer_set_router_dev(ds_hip_layer_t *L, const float *router_f32_dev, 
   if (router_f32_dev) {
     DSR_TRY(hipMemcpyAsync((void *)L->d.router_f32, router_f32_dev, n * 4, hipMemcpyDeviceToDevice, dsr_stream),
             "router copy");
+    DSR_TRY(dsh_launch_transpose_f32(L->d.router_f32, (float *)L->d.router_f32_t, L->E, L->H, dsr_stream),
+            "router transpose");
     L->have_f32 = 1;
   }
   if (router_bf16_dev) {
@@ -245,7 +251,7 @@ static hipError_t scores_enqueue(const ds_hip_layer_t *L, const float *x_in, con
                                  int route_mode, float *partials, int *np) {
   if (route_mode == DS_HIP_ROUTE_CFG) {
     *np = L->np;
-    return dsh_launch_dec_partial_scores(L->d.router_f32, x_in, step, stride, L->H, L->E, partials, dsr_stream);
+    return dsh_launch_dec_partial_scores(L->d.router_f32_t, x_in, step, stride, L->H, L->E, partials, dsr_stream);
   }
   *np = 1;
   return dsh_launch_dec_scores_bf16(L->d.router_bf16, x_in, step, stride, L->H, L->E, dsr_threads(), partials,
@@ -269,7 +275,7 @@ static hipError_t layer_enqueue(const ds_hip_layer_t *L, const dsh_layer_work_t 
   int chain = next && route_mode == DS_HIP_ROUTE_CFG;
   if (e == hipSuccess)
     e = dsh_launch_dec_down(&L->d, x_in, step, stride, x_out, residual, bf16sim, wk,
-                            chain ? next->d.router_f32 : NULL, chain ? next->E : 0, chain ? partials : NULL,
+                            chain ? next->d.router_f32_t : NULL, chain ? next->E : 0, chain ? partials : NULL,
                             dsr_stream);
   if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
   return e;
@@ -415,7 +421,7 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
     e = dsh_launch_dec_gate_up(&L->d, xin, st, stride, pin, np, S->route_mode, S->bf16sim, wk, dsr_stream);
     if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
     if (e == hipSuccess)
-      e = dsh_launch_dec_down(&L->d, xin, st, stride, S->xbuf, 1, S->bf16sim, wk, next ? next->d.router_f32 : NULL,
+      e = dsh_launch_dec_down(&L->d, xin, st, stride, S->xbuf, 1, S->bf16sim, wk, next ? next->d.router_f32_t : NULL,
                               next ? next->E : 0, next ? pout : NULL, dsr_stream);
     if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
   }
@@ -499,6 +505,34 @@ int ds_hip_time_stack(ds_hip_stack_t *S, int n_steps, float *ms) {
       hipEventRecord(b, dsr_stream) != hipSuccess || hipEventSynchronize(b) != hipSuccess ||
       hipEventElapsedTime(ms, a, b) != hipSuccess)
     rc = dsr_failf("ds_hip_time_stack: timing failed");
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  return rc;
+}
+
+/* LM-head argmax kernel alone on the stack's current hidden state: n launches back to back
+ * between two events (kernel time plus the launch gaps). */
+int ds_hip_time_lm_head(ds_hip_stack_t *S, int n, float *ms) {
+  if (!S || !S->bound || !ms || n <= 0) return dsr_failf("ds_hip_time_lm_head: invalid arguments");
+  hipEvent_t a, b;
+  DSR_TRY(hipEventCreate(&a), "event");
+  DSR_TRY(hipEventCreate(&b), "event");
+  int rc = 0;
+  hipError_t e = hipEventRecord(a, dsr_stream);
+  for (int i = 0; i < n && e == hipSuccess; i++) {
+    if (S->lm_fast) {
+      e = dsh_launch_dec_lm_argmax(S->lm, S->xbuf, S->H, S->vocab, S->cand, dsr_stream);
+    } else {
+      int T = dsr_threads();
+      e = dsh_launch_argmax_avx_partial(S->lm, S->xbuf, S->cand, NULL, S->H, S->vocab,
+                                        T > 1 ? (S->vocab + T - 1) / T : S->vocab, dsr_stream);
+    }
+  }
+  if (e == hipSuccess) e = hipEventRecord(b, dsr_stream);
+  if (e == hipSuccess) e = hipEventSynchronize(b);
+  if (e == hipSuccess) e = hipEventElapsedTime(ms, a, b);
+  if (e != hipSuccess) rc = dsr_fail("ds_hip_time_lm_head", e);
+  else *ms /= (float)n;
   hipEventDestroy(a);
   hipEventDestroy(b);
   return rc;

@@ -99,6 +99,9 @@ size_t ds_hip_stack_bytes_per_step(const ds_hip_stack_t *S);
 /* ---------------- timing (HIP events on the library stream) ---------------- */
 /* Wall time of n_steps graph launches. */
 int ds_hip_time_stack(ds_hip_stack_t *S, int n_steps, float *ms);
+/* Average time of the LM-head argmax kernel over n back-to-back launches on the stack's current
+ * hidden state (no token written; includes the launch gaps). */
+int ds_hip_time_lm_head(ds_hip_stack_t *S, int n, float *ms);
 /* Kernels one decode step launches, and the kind of kernel i ("scores", "gate_up", "down",
  * "lm_head.argmax", "lm_head.final"). */
 int ds_hip_stack_kernel_count(const ds_hip_stack_t *S);
