@@ -72,6 +72,13 @@ typedef struct {
   float *h;      /* [K*I + SI] SwiGLU outputs (routed slots, then shared) */
 } dsh_layer_work_t;
 
+/* ---- prefill MoE block (k_prefill.hip) ---- */
+int dsh_pf_supported(const dsh_layer_t *L);
+size_t dsh_pf_workspace_bytes(const dsh_layer_t *L, int T);
+/* out[T][H] = (residual ? X : 0) + MoE(X); ws: dsh_pf_workspace_bytes(L, T) device bytes. */
+hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int route_mode, int nthreads, int residual,
+                              int bf16sim, float *out, void *ws, int *idx_out, float *w_out, hipStream_t s);
+
 /* Final reduction of per-block argmax candidates: writes tokens[*step] (tokens[0] when step is
  * NULL) and advances *step. */
 hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int *tokens, int *step, hipStream_t s);

@@ -296,6 +296,24 @@ int ds_hip_layer_forward(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
   return 0;
 }
 
+/* Prefill MoE block (ds_moe_decoder.c:629-809) for T tokens already on the device. The workspace
+ * (activations split to bf16, routing, the expert-sorted pair list, h and per-pair outputs; about
+ * 65 KB per token at DeepSeek-OCR's shape) is a library staging buffer that grows to the largest T. */
+int ds_hip_layer_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, int T, int route_mode, int residual,
+                         int *idx_dev, float *w_dev) {
+  if (!L || !out_dev || !x_dev || T <= 0) return dsr_failf("ds_hip_layer_prefill: invalid arguments");
+  if (check_router(L, route_mode)) return -1;
+  if (!dsh_pf_supported(&L->d))
+    return dsr_failf("ds_hip_layer_prefill: shape H=%d I=%d SI=%d not supported (needs H %% 256 == 0, I and SI %% 128 == 0)",
+                     L->H, L->I, L->SI);
+  void *ws = dsr_scratch(DSR_SLOT_PF, dsh_pf_workspace_bytes(&L->d, T));
+  if (!ws) return -1;
+  hipError_t e = dsh_launch_prefill(&L->d, x_dev, T, route_mode, dsr_threads(), residual, ds_bf16_simulate_python,
+                                    out_dev, ws, idx_dev, w_dev, dsr_stream);
+  if (e != hipSuccess) return dsr_fail("prefill kernels", e);
+  return 0;
+}
+
 /* ================================================================ decode stack */
 
 struct ds_hip_stack {

@@ -23,7 +23,7 @@ int dsr_failf(const char *fmt, ...);
   } while (0)
 
 /* Grow-only device staging buffer per slot (not thread-safe, like the reference API). */
-enum { DSR_SLOT_X, DSR_SLOT_Y, DSR_SLOT_A, DSR_SLOT_B, DSR_SLOT_C, DSR_SLOT_D, DSR_SLOT_IDX, DSR_NSLOTS };
+enum { DSR_SLOT_X, DSR_SLOT_Y, DSR_SLOT_A, DSR_SLOT_B, DSR_SLOT_C, DSR_SLOT_D, DSR_SLOT_IDX, DSR_SLOT_PF, DSR_NSLOTS };
 void *dsr_scratch(int slot, size_t bytes);
 
 int dsr_h2d(void *dst, const void *src, size_t n);

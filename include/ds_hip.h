@@ -77,6 +77,14 @@ int ds_hip_layer_export_expert(const ds_hip_layer_t *L, int e, int8_t *gu_q, flo
 int ds_hip_layer_forward(ds_hip_layer_t *L, float *out_dev, const float *x_dev, int route_mode, int residual,
                          int *idx_dev, float *w_dev);
 
+/* Prefill MoE block for T tokens (ds_moe_decoder.c:629-809, on this layer's INT8 blocks):
+ * out_dev[T][hidden] = (residual ? x : 0) + MoE(x_dev[T][hidden]). Routing per token as
+ * ds_hip_layer_forward (route_mode), experts as an expert-sorted grouped GEMM on bf16 MFMA, routed
+ * outputs added in ascending expert order, then the shared expert. idx_dev/w_dev (optional,
+ * [T][top_k]) receive the routing. Asynchronous; out_dev must not alias x_dev. */
+int ds_hip_layer_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, int T, int route_mode, int residual,
+                         int *idx_dev, float *w_dev);
+
 /* ---------------- decode stack: n MoE layers + argmax LM head ---------------- */
 typedef struct ds_hip_stack ds_hip_stack_t;
 

@@ -1,0 +1,147 @@
+"""GPU parity of the prefill MoE block (ds_hip_layer_prefill; reference block ds_moe_decoder.c:629-809
+run on this layer's INT8 experts) against the oracle.
+
+Routing: DECODE mode (bf16 router) is compared bit for bit with the reference arithmetic of the
+decode router (the AVX-512-order bf16 scores, or_bf16_matvec_avx512, then the fast-exp softmax and
+top-k, or_softmax_topk_decode). CFG mode (f32 router) sums the scores in a different f32 order than
+or_linear_f32, so its experts are compared with or_prefill_route except where the f64 scores of the
+k-th and (k+1)-th experts are within 1e-5 of each other, and its weights within 1e-5.
+Outputs: the GPU's own routing is fed to the f64 brute force (or_prefill_moe_f64) and the block
+output must be within max|a-b|/max|b| <= 1e-3.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+from test_gpu_moe import export_layer, make_device_layer, rel_err, upload_layer
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def gpu_prefill(dev, h, X, mode, residual=0, K=6):
+    L = dev.load()
+    T = X.shape[0]
+    xd = dev.DeviceBuffer.from_array(X)
+    od = dev.DeviceBuffer(X.nbytes)
+    idd = dev.DeviceBuffer(4 * T * K)
+    wd = dev.DeviceBuffer(4 * T * K)
+    dev.check(L.ds_hip_layer_prefill(h, od.ptr, xd.ptr, T, mode, residual, idd.ptr, wd.ptr), "prefill")
+    dev.check(L.ds_hip_sync(), "sync")
+    return (od.to_array(np.float32).reshape(X.shape), idd.to_array(np.int32).reshape(T, K),
+            wd.to_array(np.float32).reshape(T, K))
+
+
+def check_routing(B, lay, X, idx, w, mode):
+    T, K, E, H = X.shape[0], lay.top_k, lay.n_experts, lay.hidden
+    if mode == 0:
+        for t in range(T):
+            sc = np.empty(E, np.float32)
+            B.oracle().or_bf16_matvec_avx512(sc, X[t], lay.router_bf16, H, E, 1)
+            ri, rw = np.empty(K, np.int32), np.empty(K, np.float32)
+            B.oracle().or_softmax_topk_decode(ri, rw, sc, E, K)
+            assert np.array_equal(ri, idx[t]), (t, ri, idx[t])
+            assert np.array_equal(rw.view(np.uint32), w[t].view(np.uint32)), t
+        return
+    ri, rw = np.empty((T, K), np.int32), np.empty((T, K), np.float32)
+    B.oracle().or_prefill_route(ri, rw, X, T, C.byref(lay.or_layer()), mode)
+    s64 = X.astype(np.float64) @ lay.router_f32.astype(np.float64).reshape(E, H).T
+    ties = 0
+    for t in range(T):
+        if np.array_equal(ri[t], idx[t]):
+            assert np.allclose(rw[t], w[t], rtol=1e-5, atol=1e-7), t
+            continue
+        order = np.sort(s64[t])[::-1]
+        assert order[K - 1] - order[K] < 1e-5 * max(abs(order[0]), 1e-30), (t, ri[t], idx[t])
+        ties += 1
+    assert ties <= max(1, T // 50)
+
+
+@pytest.mark.parametrize("T", [1, 5, 64, 130])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_prefill_small_layer(dev, B, mode, T):
+    L = dev.load()
+    lay = B.make_moe_layer(61, hidden=256, inter=128, n_experts=16)
+    h = upload_layer(dev, lay)
+    try:
+        X = np.stack([B.normal_f32(256, 5000 + t) for t in range(T)])
+        out, idx, w = gpu_prefill(dev, h, X, mode)
+        check_routing(B, lay, X, idx, w, mode)
+        ref = np.empty((T, 256), np.float64)
+        B.oracle().or_prefill_moe_f64(ref, X, T, C.byref(lay.or_layer()), idx, w)
+        err = rel_err(out, ref)
+        print(f"prefill small mode={mode} T={T}: max rel err {err:.2e}")
+        assert err < TOL
+    finally:
+        L.ds_hip_layer_destroy(h)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_prefill_one_token_equals_decode(dev, B, mode):
+    """One token through the prefill block routes exactly like the decode layer and gives the same
+    output within the two paths' f32 rounding."""
+    from test_gpu_moe import layer_forward
+    L = dev.load()
+    lay = B.make_moe_layer(62, hidden=256, inter=128, n_experts=16)
+    h = upload_layer(dev, lay)
+    try:
+        x = B.normal_f32(256, 6001)
+        out, idx, w = gpu_prefill(dev, h, x[None, :], mode)
+        dout, didx, dw = layer_forward(dev, h, x, mode)
+        assert np.array_equal(idx[0], didx) and np.array_equal(w[0].view(np.uint32), dw.view(np.uint32))
+        err = rel_err(out[0], dout)
+        print(f"one-token prefill vs decode mode={mode}: {err:.2e}")
+        assert err < 1e-4
+    finally:
+        L.ds_hip_layer_destroy(h)
+
+
+def test_prefill_residual(dev, B):
+    L = dev.load()
+    lay = B.make_moe_layer(63, hidden=256, inter=128, n_experts=16)
+    h = upload_layer(dev, lay)
+    try:
+        X = np.stack([B.normal_f32(256, 7000 + t) for t in range(9)])
+        o0, i0, w0 = gpu_prefill(dev, h, X, 1, residual=0)
+        o1, i1, w1 = gpu_prefill(dev, h, X, 1, residual=1)
+        assert np.array_equal(i0, i1)
+        assert np.array_equal((X + o0).view(np.uint32), o1.view(np.uint32))
+    finally:
+        L.ds_hip_layer_destroy(h)
+
+
+def test_prefill_rejects_unsupported_shape(dev, B):
+    L = dev.load()
+    lay = B.make_moe_layer(64, hidden=256, inter=64, n_experts=16, n_shared=2)
+    h = upload_layer(dev, lay)
+    try:
+        X = np.stack([B.normal_f32(256, 8000 + t) for t in range(2)])
+        xd = dev.DeviceBuffer.from_array(X)
+        od = dev.DeviceBuffer(X.nbytes)
+        assert L.ds_hip_layer_prefill(h, od.ptr, xd.ptr, 2, 1, 0, None, None) != 0
+        assert b"not supported" in L.ds_hip_last_error()
+    finally:
+        L.ds_hip_layer_destroy(h)
+
+
+def test_prefill_config3(dev, B):
+    """Config 3: 662 tokens through one config-2 layer (f32 router, renormalised top-6). Routing is
+    checked for every token, the block output against the f64 oracle on 24 sampled tokens."""
+    L = dev.load()
+    T, H = 662, 1280
+    h, rf, rb = make_device_layer(dev, 300)
+    try:
+        X = np.stack([B.normal_f32(H, 9000 + t) for t in range(T)])
+        out, idx, w = gpu_prefill(dev, h, X, 1)
+        lay = export_layer(dev, B, h, rf, rb)
+        check_routing(B, lay, X, idx, w, 1)
+        rows = np.linspace(0, T - 1, 24).astype(int)
+        Xs = np.ascontiguousarray(X[rows])
+        ref = np.empty((len(rows), H), np.float64)
+        B.oracle().or_prefill_moe_f64(ref, Xs, len(rows), C.byref(lay.or_layer()),
+                                     np.ascontiguousarray(idx[rows]), np.ascontiguousarray(w[rows]))
+        err = rel_err(out[rows], ref)
+        print(f"config-3 prefill (T={T}): max rel err {err:.2e} on {len(rows)} tokens")
+        assert err < TOL
+    finally:
+        L.ds_hip_layer_destroy(h)
