@@ -132,6 +132,8 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prefill-tokens", type=int, default=662, help="config-3 prefill measurement (0: skip)")
+    ap.add_argument("--prefill-reps", type=int, default=20)
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (HBM counter calibration)")
     args = ap.parse_args()
@@ -201,6 +203,30 @@ def main():
     lm_gbs = lm_bytes / (lm_ms * 1e-3) / 1e9
     step_gbs = bytes_per_step / (ms_per_step * 1e-3) / 1e9
 
+    # prefill (config 3): 662 seeded tokens through one config-2 layer (the first decode layer)
+    prefill = None
+    if args.prefill_tokens > 0:
+        T = args.prefill_tokens
+        xp = dev.DeviceBuffer(T * H * 4)
+        dev.check(L.ds_hip_fill_normal_f32(xp.ptr, T * H, 662, 0.0, 1.0), "fill")
+        op = dev.DeviceBuffer(T * H * 4)
+        pt = C.c_float(0)
+        dev.check(L.ds_hip_time_prefill(handles[0], op.ptr, xp.ptr, T, route, args.prefill_reps, C.byref(pt)),
+                  "prefill timing")
+        us = pt.value * 1e3
+        # algorithmic work: K routed + shared experts per token (2 flops per weight element) and
+        # the router; the MFMAs run each product twice (hi and lo halves of the activations)
+        flops = T * (K * 2 * (2 * I * H + H * I) + 2 * (2 * SI * H + H * SI) + 2 * E * H)
+        wbytes = E * (2 * I * H + 2 * I * 8 + H * I + H * 8) + 2 * SI * H + 2 * SI * 8 + H * SI + H * 8
+        prefill = {"config": "config 3: 662 tokens x 1280 through one config-2 layer", "tokens": T,
+                   "us": round(us, 2), "tok_per_s": round(T / (us * 1e-6), 1),
+                   "algorithmic_tflops": round(flops / (us * 1e-6) / 1e12, 2),
+                   "mfma_frac_of_bf16_peak": round(flops / (us * 1e-6) / 2.5e15, 4),
+                   "weight_bytes": wbytes, "weight_gbs": round(wbytes / (us * 1e-6) / 1e9, 1),
+                   "note": "MFMA work is 2x the algorithmic flops (bf16 hi/lo activation split)"}
+        xp.close()
+        op.close()
+
     xs_host = xs.to_array(np.float32).reshape(n_inputs, H)[args.warmup:].copy()
     cpu = None
     if not args.no_cpu:
@@ -238,6 +264,7 @@ def main():
                      "bytes_per_launch": lm_bytes, "avg_ms": round(lm_ms, 5),
                      "avg_ms_note": "50 back-to-back launches between HIP events on the library stream"},
         "kernels": kernel_ms,
+        "prefill": prefill,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -9,10 +9,10 @@
 // row's scale and offset exactly as the decode path does: y = scale · Σu·a + offset · Σa.
 //
 // Kernels (one launch each, all sizes fixed by T, so a graph can hold them):
-//   k_pf_split   X → Xhi, Xlo (bf16), Σx per token
-//   k_pf_route   router scores in the decode path's order + top-k per token → idx, w
-//   k_pf_plan    per-expert counts and offsets, the GEMM work list (expert, 64-row chunk)
-//   k_pf_scatter expert-sorted (token, slot) pairs, tokens in increasing order per expert
+//   k_pf_scores  router scores in the decode path's order, as four partial sums per token
+//   k_pf_select  per token: X → Xhi, Xlo (bf16), Σx; expert selection → idx, w
+//   k_pf_plan    expert-sorted (token, slot) pairs (stable: tokens in increasing order per expert),
+//                per-expert offsets and the GEMM work items (expert, up-to-PF_MT-row chunk)
 //   k_pf_gate_up grouped GEMM + SwiGLU → H (bf16 hi/lo) for routed pairs and for the shared expert
 //   k_pf_down    grouped GEMM → Y (f32) per routed pair and per token for the shared expert
 //   k_pf_combine out[t] = (residual ? x : 0) + (Σ_k w_k·Y_k in ascending expert order + Y_shared)
@@ -21,12 +21,15 @@
 #include "k_core.h"
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
-#define PF_MT 64   // tokens (rows of A) per work item
+#define PF_MT 64    // rows of A per work item: one or two MFMA sub-tiles of 32 rows
 #define PF_GU_N 128 // gate_up: intermediate units per block (128 gate + 128 up weight rows)
 #define PF_DN_N 256 // down: output rows per block
+#define PF_TB 8     // tokens per DECODE-mode scores block
+#define PF_PLAN_LDS 8192  // (token, slot) entries the plan kernel caches in LDS
 
 struct pf_item {
   int seg;   // expert 0..E-1, or E for the shared expert
@@ -56,372 +59,637 @@ __device__ __forceinline__ bf16x8 ld_bf16x8(const __bf16 *p) { return *(const bf
 // D[m][n] of a 32x32 MFMA tile held by lane l, register j: n = l % 32, m = 8*(j/4) + 4*(l/32) + j%4
 __device__ __forceinline__ int mfma_row(int lane, int j) { return 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3); }
 
-// ---------------------------------------------------------------------------------- split
-// One wave per token: hi/lo bf16 split of x and Σx (lanes sum strided elements, then a wave sum).
-__global__ void __launch_bounds__(256) k_pf_split(const float *__restrict__ X, int T, int H, __bf16 *__restrict__ Xhi,
-                                                  __bf16 *__restrict__ Xlo, float *__restrict__ xsum) {
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (t >= T) return;
-  const float *x = X + (size_t)t * H;
+// ---------------------------------------------------------------------------------- routing
+// Router scores in the decode path's order, kept as four partial sums per token and expert:
+// ps[t][v][e] = Σ_jb p[v + 4·jb] added sequentially from 0, where p[b] = Σ_j WrT[R·b+j][e]·x[R·b+j]
+// is a chain of fused multiply-adds over j (the decode path's partials and per-wave sums, wave v
+// taking partials v, v+4, ...); k_pf_select adds them as ((ps0 + ps1) + ps2) + ps3 (route_select).
+// CFG (f32 router): block = (PF_SC_TOK tokens, residue v); the residue's router rows and the tokens'
+// matching x values are staged in LDS PF_SC_JB partials at a time; wave w runs tokens 4w..4w+3,
+// lane = expert.
+#define PF_SC_TOK 16
+#define PF_SC_JB 20
+template <int R>
+__global__ void __launch_bounds__(256) k_pf_scores_cfg(const float *__restrict__ WrT, const float *__restrict__ X,
+                                                       int T, int H, int E, float *__restrict__ ps) {
+  __shared__ __attribute__((aligned(16))) float wv[PF_SC_JB][R][64];
+  __shared__ __attribute__((aligned(16))) float xv[PF_SC_TOK][PF_SC_JB][R];
+  constexpr int NW = PF_SC_JB * R * 64 / 256;            // router values per thread per pass
+  constexpr int NX = PF_SC_TOK * PF_SC_JB * (R / 4);      // x float4s per pass
+  constexpr int NXT = (NX + 255) / 256;
+  const int v = blockIdx.y, t0 = blockIdx.x * PF_SC_TOK;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nbv = (H / R - v + 3) / 4;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int jb0 = 0; jb0 < nbv; jb0 += PF_SC_JB) {
+    const int nj = min(PF_SC_JB, nbv - jb0);
+    // every load of the pass in flight at once (partials past the last repeat it, unused)
+    float wr_[NW];
+    f32x4 xr_[NXT];
+#pragma unroll
+    for (int k = 0; k < NW; k++) {
+      const int i = threadIdx.x + 256 * k;
+      const int row = i >> 6, e = i & 63;
+      const int jj = row / R, j = row - jj * R;
+      const int b = v + 4 * min(jb0 + jj, nbv - 1);
+      const float val = WrT[(size_t)(R * b + j) * E + min(e, E - 1)];  // branch-free load
+      wr_[k] = e < E ? val : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < NXT; k++) {
+      const int i = min((int)threadIdx.x + 256 * k, NX - 1);
+      const int tb = i / (PF_SC_JB * (R / 4)), rem = i - tb * (PF_SC_JB * (R / 4));
+      const int jj = rem / (R / 4), q = rem - jj * (R / 4);
+      const int t = min(t0 + tb, T - 1);
+      const int b = v + 4 * min(jb0 + jj, nbv - 1);
+      xr_[k] = *(const f32x4 *)(X + (size_t)t * H + R * b + 4 * q);
+    }
+    __syncthreads();  // the previous pass's reads are done
+#pragma unroll
+    for (int k = 0; k < NW; k++) {
+      const int i = threadIdx.x + 256 * k;
+      (&wv[0][0][0])[i] = wr_[k];
+    }
+#pragma unroll
+    for (int k = 0; k < NXT; k++) {
+      const int i = threadIdx.x + 256 * k;
+      if (i < NX) ((f32x4 *)&xv[0][0][0])[i] = xr_[k];
+    }
+    __syncthreads();
+    for (int jj = 0; jj < nj; jj++) {
+      float wr[R];
+#pragma unroll
+      for (int j = 0; j < R; j++) wr[j] = wv[jj][j][lane];
+#pragma unroll
+      for (int tk = 0; tk < 4; tk++) {
+        const f32x4 *x4 = (const f32x4 *)xv[4 * wave + tk][jj];
+        float p = 0.0f;
+#pragma unroll
+        for (int q = 0; q < R / 4; q++) {
+          const f32x4 xq = x4[q];
+#pragma unroll
+          for (int i = 0; i < 4; i++) p = __builtin_fmaf(wr[4 * q + i], xq[i], p);
+        }
+        acc[tk] += p;
+      }
+    }
+  }
+#pragma unroll
+  for (int tk = 0; tk < 4; tk++) {
+    const int t = t0 + 4 * wave + tk;
+    if (t < T) ps[((size_t)t * 4 + v) * 64 + lane] = lane < E ? acc[tk] : 0.0f;
+  }
+}
+
+// DECODE (bf16 router in the reference's AVX-512 order, as k_dec_scores_bf16): one block per PF_TB
+// tokens, 64 groups of 4 lanes, group g computes expert g's score; the full score is partial 0, the
+// other three are zero (0 + ... keeps it).
+__global__ void __launch_bounds__(256) k_pf_scores_bf16(const uint16_t *__restrict__ Wr, const float *__restrict__ X,
+                                                        int T, int H, int E, int nthreads, float *__restrict__ ps) {
+  extern __shared__ __attribute__((aligned(16))) float xs[];  // [PF_TB][H]
+  const int t0 = blockIdx.x * PF_TB, nt = min(PF_TB, T - t0);
+  for (int i = threadIdx.x; i < nt * H; i += 256) xs[i] = X[(size_t)t0 * H + i];
+  __syncthreads();
+  const int Lq = threadIdx.x & 3, g = threadIdx.x >> 2;
+  const int chunk = dsh_chunk_len(E, nthreads);
+  const int path = g < E ? row_path(g, E, chunk, false) : DSH_ROW_SINGLE;
+  for (int tb = 0; tb < nt; tb++) {
+    float v = 0.0f;
+    if (g < E)
+      v = avx_row<true>(Wr + (size_t)g * H, xs + (size_t)tb * H, H, Lq, path == DSH_ROW_SINGLE, true, 0.0f,
+                        path != DSH_ROW_GROUP4);
+    if (Lq == 0) {
+      float *o = ps + (size_t)(t0 + tb) * 4 * 64;
+      o[g] = g < E ? v : 0.0f;
+      o[64 + g] = 0.0f;
+      o[128 + g] = 0.0f;
+      o[192 + g] = 0.0f;
+    }
+  }
+}
+
+// One wave per token: the bf16 hi/lo split of x and Σx, then the expert selection from the four
+// partial score rows (route_select: CFG top-k on raw scores + softmax over the k; DECODE fast-exp
+// softmax over all experts + top-k).
+#define PF_SEL_U 8  // x float4 loads per lane in flight
+template <int MODE>
+__global__ void __launch_bounds__(256) k_pf_select(const float *__restrict__ X, int T, int H, int E, int K,
+                                                   const float *__restrict__ ps, __bf16 *__restrict__ Xhi,
+                                                   __bf16 *__restrict__ Xlo, float *__restrict__ xsum,
+                                                   int *__restrict__ idx, float *__restrict__ w) {
+  __shared__ float s_red[4][4][64];
+  __shared__ int s_idx[4][64];
+  __shared__ float s_w[4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;  // no block-wide barriers below
+#pragma unroll
+  for (int r = 0; r < 4; r++) s_red[wave][r][lane] = ps[((size_t)t * 4 + r) * 64 + lane];
+  const f32x4 *src = (const f32x4 *)(X + (size_t)t * H);
   float s = 0.0f;
-  for (int c = lane; c < H; c += 64) {
-    const float v = x[c];
-    const __bf16 hi = (__bf16)v;
-    Xhi[(size_t)t * H + c] = hi;
-    Xlo[(size_t)t * H + c] = (__bf16)(v - (float)hi);
-    s += v;
+  for (int c0 = 0; c0 < H / 4; c0 += 64 * PF_SEL_U) {
+    f32x4 xv[PF_SEL_U];
+#pragma unroll
+    for (int u = 0; u < PF_SEL_U; u++) xv[u] = src[min(c0 + 64 * u + lane, H / 4 - 1)];
+#pragma unroll
+    for (int u = 0; u < PF_SEL_U; u++) {
+      const int c = c0 + 64 * u + lane;
+      if (c >= H / 4) continue;
+      const f32x4 v = xv[u];
+      bf16x4 hi, lo;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        hi[i] = (__bf16)v[i];
+        lo[i] = (__bf16)(v[i] - (float)hi[i]);
+      }
+      *(bf16x4 *)(Xhi + (size_t)t * H + 4 * c) = hi;
+      *(bf16x4 *)(Xlo + (size_t)t * H + 4 * c) = lo;
+      s += (v[0] + v[1]) + (v[2] + v[3]);
+    }
   }
   s = dsh_wave_sum(s);
   if (lane == 0) xsum[t] = s;
-}
-
-// ---------------------------------------------------------------------------------- routing
-// One 256-thread block per token. CFG: the f32 router as the decode path sums it (partials of 8
-// rows Σ_j WrT[r0+j][e]·x[r0+j]; wave w adds partials w, w+4, ... in order; the four wave sums are
-// added in wave order), top-k on raw scores, softmax over the k. DECODE: the bf16 router in the
-// reference's AVX-512 order (as k_dec_scores_bf16), fast-exp softmax over all experts, top-k.
-template <int MODE>
-__global__ void __launch_bounds__(256) k_pf_route(dsh_layer_t L, const float *__restrict__ X, int nthreads,
-                                                  int *__restrict__ idx, float *__restrict__ w) {
-  extern __shared__ float xs[];
-  __shared__ int s_idx[64];
-  __shared__ float s_w[64];
-  __shared__ float s_red[4][64];
-  const int t = blockIdx.x, H = L.H, E = L.E, K = L.K;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int i = threadIdx.x; i < H; i += 256) xs[i] = X[(size_t)t * H + i];
-  __syncthreads();
-  if (MODE == DSH_ROUTE_CFG) {
-    float acc = 0.0f;
-    if (lane < E) {
-      for (int b = wave; b < H / 8; b += 4) {
-        float p = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; j++) p = __builtin_fmaf(L.router_f32_t[(size_t)(8 * b + j) * E + lane], xs[8 * b + j], p);
-        acc += p;
-      }
-    }
-    s_red[wave][lane] = lane < E ? acc : 0.0f;
-  } else {
-    // 64 groups of 4 lanes: group g computes expert g's score in the AVX-512 order
-    const int Lq = threadIdx.x & 3, g = threadIdx.x >> 2;
-    const int chunk = dsh_chunk_len(E, nthreads);
-    float v = 0.0f;
-    if (g < E) {
-      const int path = row_path(g, E, chunk, false);
-      v = avx_row<true>(L.router_bf16 + (size_t)g * H, xs, H, Lq, path == DSH_ROW_SINGLE, true, 0.0f,
-                        path != DSH_ROW_GROUP4);
-    }
-    // the full score goes to s_red[0][g]; the other wave rows are zero (0 + ... keeps the value)
-    if (Lq == 0) s_red[0][g] = g < E ? v : 0.0f;
-    if (threadIdx.x < 192) s_red[1 + threadIdx.x / 64][threadIdx.x & 63] = 0.0f;
-  }
-  __syncthreads();
-  if (wave == 0) route_select(E, K, MODE, s_idx, s_w, s_red);
-  __syncthreads();
-  if (threadIdx.x < K) {
-    idx[(size_t)t * K + threadIdx.x] = s_idx[threadIdx.x];
-    w[(size_t)t * K + threadIdx.x] = s_w[threadIdx.x];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  route_select(E, K, MODE, s_idx[wave], s_w[wave], s_red[wave]);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (lane < K) {
+    idx[(size_t)t * K + lane] = s_idx[wave][lane];
+    w[(size_t)t * K + lane] = s_w[wave][lane];
   }
 }
 
 // ---------------------------------------------------------------------------------- plan
-// One block: counts per expert (slots with no expert, idx < 0, are skipped), exclusive offsets,
-// and the work list: each expert's pairs in chunks of PF_MT, then the shared expert's T tokens.
-__global__ void __launch_bounds__(256) k_pf_plan(const int *__restrict__ idx, int T, int K, int E,
-                                                 int *__restrict__ seg_off, pf_item *__restrict__ items,
-                                                 int *__restrict__ n_items) {
-  __shared__ int cnt[64];
-  if (threadIdx.x < 64) cnt[threadIdx.x] = 0;
+// One 1024-thread block. Wave v owns a contiguous range of the T·K (token, slot) entries. Per-wave
+// expert counts give each expert's segment offset and each wave's start inside it, so a pair's
+// position is (segment offset) + (pairs of the expert in earlier waves) + (earlier pairs of the
+// expert in this wave): expert segments hold their tokens in increasing order. Within a wave, 64
+// entries at a time, the entries routed to the same expert are found with 7 ballots over the
+// expert's bits. Entries with no expert (idx < 0 or >= E) get pos_of = -1.
+// Work items: each expert's pairs in chunks of PF_MT (items 0 .. n_routed-1), then the shared
+// expert's T tokens in chunks of PF_MT; counts = {n_routed, n_shared}.
+__global__ void __launch_bounds__(1024) k_pf_plan(const int *__restrict__ idx, int T, int K, int E,
+                                                  int *__restrict__ seg_off, pf_item *__restrict__ items,
+                                                  int *__restrict__ counts, int *__restrict__ pair_tok,
+                                                  int *__restrict__ pos_of) {
+  __shared__ int cnt[16][64];
+  __shared__ int run[16][64];
+  __shared__ int cache[PF_PLAN_LDS];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int TK = T * K;
+  const bool cached = TK <= PF_PLAN_LDS;
+  const int per = (TK + 15) / 16;
+  const int lo = min(wave * per, TK), hi = min(lo + per, TK);
+  cnt[wave][lane] = 0;
   __syncthreads();
-  for (int i = threadIdx.x; i < T * K; i += 256) {
-    const int e = idx[i];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int off = 0, ni = 0;
-    for (int e = 0; e < E; e++) {
-      seg_off[e] = off;
-      for (int m0 = 0; m0 < cnt[e]; m0 += PF_MT) items[ni++] = pf_item{e, m0, min(PF_MT, cnt[e] - m0), off};
-      off += cnt[e];
+  for (int base = lo; base < hi; base += 64 * 8) {  // 8 loads per lane in flight
+    int ev[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) ev[u] = idx[min(base + 64 * u + lane, hi - 1)];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int i = base + 64 * u + lane;
+      if (i >= hi) continue;
+      if (cached) cache[i] = ev[u];
+      if (ev[u] >= 0 && ev[u] < E) atomicAdd(&cnt[wave][ev[u]], 1);
     }
-    seg_off[E] = off;
-    for (int m0 = 0; m0 < T; m0 += PF_MT) items[ni++] = pf_item{E, m0, min(PF_MT, T - m0), 0};
-    *n_items = ni;
   }
-}
-
-// One wave per expert: walks the (token, slot) entries in token order and appends those routed
-// to its expert (ballot + prefix count), so each expert's tokens are in increasing order.
-__global__ void __launch_bounds__(256) k_pf_scatter(const int *__restrict__ idx, int T, int K, int E,
-                                                    const int *__restrict__ seg_off, int *__restrict__ pair_tok,
-                                                    int *__restrict__ pos_of) {
-  const int e = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (e >= E) return;
-  int pos = seg_off[e];
-  for (int base = 0; base < T * K; base += 64) {
+  __syncthreads();
+  if (wave == 0) {  // lane = expert
+    int c = 0;
+    for (int v = 0; v < 16; v++) {
+      run[v][lane] = c;
+      c += lane < E ? cnt[v][lane] : 0;
+    }
+    int incl = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(incl, d);
+      if (lane >= d) incl += o;
+    }
+    const int off = incl - c;
+    for (int v = 0; v < 16; v++) run[v][lane] += off;
+    if (lane < E) seg_off[lane] = off;
+    const int total = __shfl(incl, 63);
+    if (lane == 0) seg_off[E] = total;
+    const int nch = (c + PF_MT - 1) / PF_MT;
+    int ich = nch;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(ich, d);
+      if (lane >= d) ich += o;
+    }
+    const int nr = __shfl(ich, 63);
+    ich -= nch;
+    for (int j = 0; j < nch; j++) items[ich + j] = pf_item{lane, j * PF_MT, min(PF_MT, c - j * PF_MT), off};
+    const int ns = (T + PF_MT - 1) / PF_MT;
+    for (int j = lane; j < ns; j += 64) items[nr + j] = pf_item{E, j * PF_MT, min(PF_MT, T - j * PF_MT), 0};
+    if (lane == 0) {
+      counts[0] = nr;
+      counts[1] = ns;
+    }
+  }
+  __syncthreads();
+  for (int base = lo; base < hi; base += 64) {
     const int i = base + lane;
-    const bool mine = i < T * K && idx[i] == e;
-    const unsigned long long m = __ballot(mine);
-    if (mine) {
-      const int p = pos + __popcll(m & ((1ull << lane) - 1ull));
-      pair_tok[p] = i / K;
+    const int e = i < hi ? (cached ? cache[i] : idx[i]) : -1;
+    const bool valid = e >= 0 && e < E;
+    const int key = valid ? e : 127;
+    unsigned long long same = ~0ull;
+#pragma unroll
+    for (int b = 0; b < 7; b++) {
+      const bool bit = (key >> b) & 1;
+      const unsigned long long m = __ballot(bit);
+      same &= bit ? m : ~m;
+    }
+    const int rank = __popcll(same & ((1ull << lane) - 1ull));
+    const int p = valid ? run[wave][e] + rank : -1;
+    __builtin_amdgcn_wave_barrier();
+    if (valid && rank == 0) run[wave][e] = p + __popcll(same);
+    __builtin_amdgcn_wave_barrier();
+    if (i < hi) {
+      if (valid) pair_tok[p] = i / K;
       pos_of[i] = p;
     }
-    pos += __popcll(m);
   }
 }
 
-// ---------------------------------------------------------------------------------- gate_up
-// Block (work item, n-tile): 64 rows of A (the item's tokens) x 128 intermediate units. Wave w
-// owns units i0 + 32w .. +31 of both the gate rows and the up rows, so SwiGLU pairs sit in the same
-// lane and register. K (= H) runs in blocks of 32 columns: lane half h = lane/32 reads 16 bytes of
-// a weight row at columns k0 + 16h .. +15 and the matching 16 activations of its A row as two
-// MFMA k-slices (any permutation of k applied to both operands leaves the product unchanged).
-template <bool SHARED>
-__device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item &it, int nt, const __bf16 *Xhi,
-                                             const __bf16 *Xlo, const float *xsum, const int *pair_tok,
-                                             int bf16sim, __bf16 *Hhi, __bf16 *Hlo) {
-  const int H = L.H;
-  const int Iseg = SHARED ? L.SI : L.I;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, l32 = lane & 31;
-  const int unit = nt * PF_GU_N + wave * 32 + l32;  // this lane's B column (intermediate unit)
-  const int8_t *wq = SHARED ? L.sgu_q : L.gu_q + (size_t)it.seg * 2 * L.I * H;
-  const float *wso = SHARED ? L.sgu_so : L.gu_so + (size_t)it.seg * 2 * L.I * 2;
-  const int8_t *grow = wq + (size_t)unit * H;
-  const int8_t *urow = wq + (size_t)(Iseg + unit) * H;
-  // A rows of the two 32-row halves of the chunk (rows past mcnt repeat row 0: loaded, never stored)
-  int tok[2];
-#pragma unroll
-  for (int ms = 0; ms < 2; ms++) {
-    const int r = ms * 32 + l32;
-    const int rr = r < it.mcnt ? r : 0;
-    tok[ms] = SHARED ? it.m0 + rr : pair_tok[it.pos0 + it.m0 + rr];
+// ---------------------------------------------------------------------------------- grouped GEMM
+// Work tiles: the shared expert's first (n-tile major, its items adjacent, so the items that read
+// the same weight rows run together), then each routed item's n-tiles in turn (an item's tiles
+// share its A rows). Physical block b runs logical tile (b % 8)·C + b / 8 with C = ceil(tiles / 8):
+// blocks are handed to the 8 XCDs in turn, so each XCD gets a contiguous run of tiles and its L2
+// serves the shared reads.
+__device__ __forceinline__ bool pf_tile(const int *counts, int ntS, int ntR, int &item, int &nt) {
+  const int nr = counts[0], ns = counts[1];
+  const int nshared = ns * ntS, total = nshared + nr * ntR;
+  const int C = (total + 7) / 8;
+  const int b = blockIdx.x;
+  if (b >= 8 * C) return false;
+  const int lg = (b & 7) * C + (b >> 3);
+  if (lg >= total) return false;
+  if (lg < nshared) {
+    nt = lg / ns;
+    item = nr + (lg - nt * ns);
+  } else {
+    const int j = lg - nshared;
+    item = j / ntR;
+    nt = j - item * ntR;
   }
-  f32x16 acc[2][2];
+  return true;
+}
+
+// One block computes C[NSUB·32 A rows][4 waves x 2 tiles x 32 weight rows] = A · B^T over K columns:
+// A = activations split to bf16 (hi, lo), B = INT8 weight rows (codes → bf16 in registers).
+// K runs in stages of PF_KS = 128 columns, one 128-byte line of each weight row:
+// - weights: each wave streams its own 64 rows; per stage 8 loads in which 8 adjacent lanes read one
+//   row's full line (full lines keep HBM at its streaming rate), held in a PF_D-stage register ring
+//   and written to the wave's own LDS tile (pitch 144 B) when the stage begins;
+// - A: the block's rows are copied in 64-column half-stages (each thread 2 x 16 bytes of hi and of lo
+//   of one row, two half-stages ahead in registers) into a double-buffered LDS tile (pitch 144 B);
+// - per 32-column block, lane half h takes columns 16h..16h+15 as two MFMA k-slices of 8 (the same
+//   permutation of k for A and B leaves the product unchanged): one 16-byte LDS read gives a lane its
+//   16 codes of a weight row, one 16-byte read its 8 values of an A row.
+// One barrier per half-stage. The load order is the same in every stage and the first group of
+// PF_D stages is peeled, so the wait counts the compiler derives keep PF_D stages of weight lines in
+// flight. Stages past the last (K rounded up to PF_D stages) load a valid line and skip the math.
+// A rows past the item's count repeat a valid row; their results are never stored.
+#define PF_KS 128
+#define PF_D 2
+#define PF_AP 72   // A tile pitch in bf16 (144 bytes)
+#define PF_BP 144  // weight tile pitch in bytes
+
+struct pf_smem {
+  __bf16 A[2][2][PF_MT][PF_AP];   // [half-stage parity][hi, lo][row][column]
+  unsigned char B[4][64][PF_BP];  // per wave: its 64 weight rows x the stage's 128 codes
+  float hsum[4][2][32];           // down: Σh of the block's A rows (per wave, per 32-row sub-tile)
+};
+
+template <int NSUB, bool HSUM>
+__device__ __forceinline__ void pf_mainloop(const __bf16 *Ahi, const __bf16 *Alo, size_t arow, int K,
+                                            const int8_t *brow0, const int8_t *brow1, f32x16 (&acc)[NSUB][2],
+                                            float (&hsum)[NSUB], pf_smem &sm) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, l32 = lane & 31;
+  const int crow = threadIdx.x >> 2, cch = threadIdx.x & 3;
+  const int nk = K / PF_KS, nkp = (nk + PF_D - 1) / PF_D * PF_D, nh = 2 * nk;
 #pragma unroll
-  for (int ms = 0; ms < 2; ms++)
+  for (int ms = 0; ms < NSUB; ms++) {
+    hsum[ms] = 0.0f;
 #pragma unroll
     for (int q = 0; q < 2; q++)
 #pragma unroll
       for (int j = 0; j < 16; j++) acc[ms][q][j] = 0.0f;
-  for (int k0 = 0; k0 < H; k0 += 32) {
-    const int kc = k0 + 16 * half;
-    const u32x4 gb = *(const u32x4 *)(grow + kc), ub = *(const u32x4 *)(urow + kc);
-    bf16x8 ahi[2][2], alo[2][2];
+  }
+  // The weight addresses take a zero offset from an asm that depends on the A row, so the
+  // prologue's weight loads are issued after the row index is known, in the loop's order.
+  int zero = 0;
+  asm volatile("" : "+v"(zero) : "v"((int)arow));
+  const size_t K8 = (size_t)8 * K;
+  const int8_t *p0 = brow0 + zero + (size_t)(lane >> 3) * K + 16 * (lane & 7);
+  const int8_t *p1 = brow1 + zero + (size_t)(lane >> 3) * K + 16 * (lane & 7);
+  u32x4 bR[PF_D][8];
+  bf16x8 aR[2][4];  // [half-stage parity][hi cols c, hi cols c+32, lo c, lo c+32]
+  auto load_b = [&](u32x4(&dst)[8], int k) {
 #pragma unroll
-    for (int ms = 0; ms < 2; ms++)
+    for (int i = 0; i < 8; i++) dst[i] = *(const u32x4 *)((i < 4 ? p0 : p1) + (i & 3) * K8 + (size_t)k * PF_KS);
+  };
+  auto load_a = [&](bf16x8(&dst)[4], int hs) {
+    const size_t o = arow + (size_t)hs * 64 + 8 * cch;
+    dst[0] = ld_bf16x8(Ahi + o);
+    dst[1] = ld_bf16x8(Ahi + o + 32);
+    dst[2] = ld_bf16x8(Alo + o);
+    dst[3] = ld_bf16x8(Alo + o + 32);
+  };
 #pragma unroll
-      for (int s = 0; s < 2; s++) {
-        ahi[ms][s] = ld_bf16x8(Xhi + (size_t)tok[ms] * H + kc + 8 * s);
-        alo[ms][s] = ld_bf16x8(Xlo + (size_t)tok[ms] * H + kc + 8 * s);
-      }
+  for (int s = 0; s < PF_D; s++) {
+    load_b(bR[s], min(s, nk - 1));
+    asm volatile("" ::: "memory");
+  }
+  load_a(aR[0], 0);
+  asm volatile("" ::: "memory");
+  load_a(aR[1], min(1, nh - 1));
+  asm volatile("" ::: "memory");
+
+  auto group = [&](int kb0) {
 #pragma unroll
-    for (int s = 0; s < 2; s++) {
-      const bf16x8 bg = codes_to_bf16(u32x2{gb[2 * s], gb[2 * s + 1]});
-      const bf16x8 bu = codes_to_bf16(u32x2{ub[2 * s], ub[2 * s + 1]});
+    for (int s = 0; s < PF_D; s++) {
+      const int k = kb0 + s;
+      // the stage's weight lines → the wave's tile (the wave's reads of the previous stage are
+      // done: a wave's LDS operations complete in order)
 #pragma unroll
-      for (int ms = 0; ms < 2; ms++) {
-        acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ahi[ms][s], bg, acc[ms][0], 0, 0, 0);
-        acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(alo[ms][s], bg, acc[ms][0], 0, 0, 0);
-        acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ahi[ms][s], bu, acc[ms][1], 0, 0, 0);
-        acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(alo[ms][s], bu, acc[ms][1], 0, 0, 0);
+      for (int i = 0; i < 8; i++) *(u32x4 *)&sm.B[wave][8 * i + (lane >> 3)][16 * (lane & 7)] = bR[s][i];
+      load_b(bR[s], min(k + PF_D, nk - 1));
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int a = 0; a < 2; a++) {
+        *(bf16x8 *)&sm.A[a][0][crow][8 * cch] = aR[a][0];
+        *(bf16x8 *)&sm.A[a][0][crow][8 * cch + 32] = aR[a][1];
+        *(bf16x8 *)&sm.A[a][1][crow][8 * cch] = aR[a][2];
+        *(bf16x8 *)&sm.A[a][1][crow][8 * cch + 32] = aR[a][3];
+        load_a(aR[a], min(2 * k + a + 2, nh - 1));
+        asm volatile("" ::: "memory");
+        __syncthreads();
+        if (k < nk) {
+#pragma unroll
+          for (int s2 = 0; s2 < 2; s2++) {
+            const int cb = 32 * (2 * a + s2) + 16 * half;
+            const u32x4 b0 = *(const u32x4 *)&sm.B[wave][l32][cb];
+            const u32x4 b1 = *(const u32x4 *)&sm.B[wave][32 + l32][cb];
+            bf16x8 c0[2], c1[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+              c0[u] = codes_to_bf16(u32x2{b0[2 * u], b0[2 * u + 1]});
+              c1[u] = codes_to_bf16(u32x2{b1[2 * u], b1[2 * u + 1]});
+            }
+#pragma unroll
+            for (int ms = 0; ms < NSUB; ms++)
+#pragma unroll
+              for (int u = 0; u < 2; u++) {
+                const int ac = 32 * s2 + 16 * half + 8 * u;
+                const bf16x8 ah = *(const bf16x8 *)&sm.A[a][0][32 * ms + l32][ac];
+                const bf16x8 al = *(const bf16x8 *)&sm.A[a][1][32 * ms + l32][ac];
+                if (HSUM) {
+#pragma unroll
+                  for (int i = 0; i < 8; i++) hsum[ms] += (float)ah[i] + (float)al[i];
+                }
+                acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, c0[u], acc[ms][0], 0, 0, 0);
+                acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, c0[u], acc[ms][0], 0, 0, 0);
+                acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, c1[u], acc[ms][1], 0, 0, 0);
+                acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, c1[u], acc[ms][1], 0, 0, 0);
+              }
+          }
+        }
       }
     }
-  }
+  };
+  group(0);
+  for (int kb0 = PF_D; kb0 < nkp; kb0 += PF_D) group(kb0);
+}
+
+// gate_up: block = (work item, n-tile): the item's A rows (tokens) x 128 intermediate units; wave w
+// owns units i0 + 32w .. +31, tile 0 = their gate rows, tile 1 = their up rows, so the SwiGLU pairs
+// sit in the same lane and register.
+template <bool SHARED, int NSUB>
+__device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item &it, int nt, const __bf16 *Xhi,
+                                             const __bf16 *Xlo, const float *xsum, const int *pair_tok,
+                                             int bf16sim, __bf16 *Hhi, __bf16 *Hlo, float *hpart,
+                                             pf_smem &sm) {
+  const int H = L.H;
+  const int Iseg = SHARED ? L.SI : L.I, ntK = Iseg / PF_GU_N;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l32 = lane & 31;
+  const int u0 = nt * PF_GU_N + wave * 32, unit = u0 + l32;
+  const int8_t *wq = SHARED ? L.sgu_q : L.gu_q + (size_t)it.seg * 2 * L.I * H;
+  const float *wso = SHARED ? L.sgu_so : L.gu_so + (size_t)it.seg * 2 * L.I * 2;
+  const int r = threadIdx.x >> 2;
+  const int rr = r < it.mcnt ? r : 0;
+  const size_t arow = (size_t)(SHARED ? it.m0 + rr : pair_tok[it.pos0 + it.m0 + rr]) * H;
+  f32x16 acc[NSUB][2];
+  float hs[NSUB];
+  pf_mainloop<NSUB, false>(Xhi, Xlo, arow, H, wq + (size_t)u0 * H, wq + (size_t)(Iseg + u0) * H, acc, hs, sm);
   const float2 sog = ((const float2 *)wso)[unit], sou = ((const float2 *)wso)[Iseg + unit];
+  const size_t rbase = SHARED ? (size_t)it.m0 : (size_t)(it.pos0 + it.m0);
+  // The tile's h values (as the down GEMM sees them, hi + lo) also go to LDS for the row sums
+  // Σh over the block's 128 units, which the down epilogue needs for the offset term.
+  float(*red)[64][33] = (float(*)[64][33]) & sm.A[0][0][0][0];
+  __syncthreads();  // every wave is done with the main loop's tiles
 #pragma unroll
-  for (int ms = 0; ms < 2; ms++)
+  for (int ms = 0; ms < NSUB; ms++)
 #pragma unroll
     for (int j = 0; j < 16; j++) {
-      const int r = ms * 32 + mfma_row(lane, j);
-      if (r >= it.mcnt) continue;
-      const int t = SHARED ? it.m0 + r : pair_tok[it.pos0 + it.m0 + r];
-      const float xs = xsum[t];
-      float g = __builtin_fmaf(sog.x, acc[ms][0][j], sog.y * xs);
-      float up = __builtin_fmaf(sou.x, acc[ms][1][j], sou.y * xs);
-      if (bf16sim) {
-        g = dsh_bf16_round_half_up(g);
-        up = dsh_bf16_round_half_up(up);
+      const int m = ms * 32 + mfma_row(lane, j);
+      float hsum_v = 0.0f;
+      if (m < it.mcnt) {
+        const int t = SHARED ? it.m0 + m : pair_tok[it.pos0 + it.m0 + m];
+        const float xs = xsum[t];
+        float g = __builtin_fmaf(sog.x, acc[ms][0][j], sog.y * xs);
+        float up = __builtin_fmaf(sou.x, acc[ms][1][j], sou.y * xs);
+        if (bf16sim) {
+          g = dsh_bf16_round_half_up(g);
+          up = dsh_bf16_round_half_up(up);
+        }
+        float hv = dsh_swiglu(g, up);
+        if (bf16sim) hv = dsh_bf16_round_half_up(hv);
+        const size_t row = rbase + m;
+        const __bf16 hi = (__bf16)hv, lo = (__bf16)(hv - (float)hi);
+        Hhi[row * Iseg + unit] = hi;
+        Hlo[row * Iseg + unit] = lo;
+        hsum_v = (float)hi + (float)lo;
       }
-      float hv = dsh_swiglu(g, up);
-      if (bf16sim) hv = dsh_bf16_round_half_up(hv);
-      const size_t row = SHARED ? (size_t)(it.m0 + r) : (size_t)(it.pos0 + it.m0 + r);
-      const __bf16 hi = (__bf16)hv;
-      Hhi[row * Iseg + unit] = hi;
-      Hlo[row * Iseg + unit] = (__bf16)(hv - (float)hi);
+      red[wave][m][l32] = hsum_v;
     }
-}
-
-__global__ void __launch_bounds__(256) k_pf_gate_up(dsh_layer_t L, const pf_item *__restrict__ items,
-                                                    const int *__restrict__ n_items, const __bf16 *__restrict__ Xhi,
-                                                    const __bf16 *__restrict__ Xlo, const float *__restrict__ xsum,
-                                                    const int *__restrict__ pair_tok, int bf16sim,
-                                                    __bf16 *__restrict__ Hhi, __bf16 *__restrict__ Hlo,
-                                                    __bf16 *__restrict__ Shi, __bf16 *__restrict__ Slo) {
-  if ((int)blockIdx.x >= *n_items) return;
-  const pf_item it = items[blockIdx.x];
-  const int nt = blockIdx.y;
-  if (it.seg == L.E) {
-    if (nt * PF_GU_N >= L.SI) return;
-    gate_up_tile<true>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Shi, Slo);
-  } else {
-    if (nt * PF_GU_N >= L.I) return;
-    gate_up_tile<false>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Hhi, Hlo);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float part = 0.0f;  // lane = row: its sum over the wave's 32 units, in unit order
+  if (lane < 32 * NSUB) {
+#pragma unroll 8
+    for (int u = 0; u < 32; u++) part += red[wave][lane][u];
+  }
+  sm.hsum[wave][lane >> 5][lane & 31] = part;
+  __syncthreads();
+  if (threadIdx.x < it.mcnt) {
+    const int m = threadIdx.x;
+    const float tot = ((sm.hsum[0][m >> 5][m & 31] + sm.hsum[1][m >> 5][m & 31]) + sm.hsum[2][m >> 5][m & 31]) +
+                      sm.hsum[3][m >> 5][m & 31];
+    hpart[(rbase + m) * ntK + nt] = tot;
   }
 }
 
-// ---------------------------------------------------------------------------------- down
-// Block (work item, n-tile): 64 rows of A (h of the item's pairs, or of tokens for the shared
-// expert) x 256 output rows. Wave w owns output rows n0 + 64w .. +63 (two 32-column MFMA tiles).
-// Σh of each A row is summed from hi + lo along the K loop (lanes l and l+32 hold the two column
-// halves of a row) and combined across the halves at the end.
 template <bool SHARED>
+__device__ __forceinline__ void gate_up_dispatch(const dsh_layer_t &L, const pf_item &it, int nt, const __bf16 *Xhi,
+                                                 const __bf16 *Xlo, const float *xsum, const int *pair_tok,
+                                                 int bf16sim, __bf16 *Hhi, __bf16 *Hlo, float *hpart,
+                                                 pf_smem &sm) {
+  if (it.mcnt <= 32)
+    gate_up_tile<SHARED, 1>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Hhi, Hlo, hpart, sm);
+  else
+    gate_up_tile<SHARED, 2>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Hhi, Hlo, hpart, sm);
+}
+
+__global__ void __launch_bounds__(256, 2) k_pf_gate_up(dsh_layer_t L, const pf_item *__restrict__ items,
+                                                       const int *__restrict__ counts, const __bf16 *Xhi,
+                                                       const __bf16 *Xlo, const float *__restrict__ xsum,
+                                                       const int *__restrict__ pair_tok, int bf16sim,
+                                                       __bf16 *__restrict__ Hhi, __bf16 *__restrict__ Hlo,
+                                                       __bf16 *__restrict__ Shi, __bf16 *__restrict__ Slo,
+                                                       float *__restrict__ hpr, float *__restrict__ hps) {
+  __shared__ __attribute__((aligned(16))) pf_smem sm;
+  int item, nt;
+  if (!pf_tile(counts, L.SI / PF_GU_N, L.I / PF_GU_N, item, nt)) return;
+  const pf_item it = items[item];
+  if (it.seg == L.E)
+    gate_up_dispatch<true>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Shi, Slo, hps, sm);
+  else
+    gate_up_dispatch<false>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Hhi, Hlo, hpr, sm);
+}
+
+// down: block = (work item, n-tile): the item's A rows (h of its pairs, or of tokens for the shared
+// expert) x 256 output rows; wave w owns rows n0 + 64w .. +63 as two 32-row tiles. Σh of each A row
+// is the sum, in n-tile order, of the per-n-tile row sums the gate_up epilogue wrote.
+template <bool SHARED, int NSUB>
 __device__ __forceinline__ void down_tile(const dsh_layer_t &L, const pf_item &it, int nt, const __bf16 *Hhi,
-                                          const __bf16 *Hlo, float *Y) {
+                                          const __bf16 *Hlo, const float *hpart, float *Y, pf_smem &sm) {
   const int H = L.H;
-  const int Kd = SHARED ? L.SI : L.I;
+  const int Kd = SHARED ? L.SI : L.I, ntK = Kd / PF_GU_N;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, l32 = lane & 31;
   const int8_t *wq = SHARED ? L.sdn_q : L.dn_q + (size_t)it.seg * H * L.I;
   const float *wso = SHARED ? L.sdn_so : L.dn_so + (size_t)it.seg * H * 2;
-  int nrow[2];
-  const int8_t *brow[2];
-#pragma unroll
-  for (int q = 0; q < 2; q++) {
-    nrow[q] = nt * PF_DN_N + wave * 64 + q * 32 + l32;
-    brow[q] = wq + (size_t)nrow[q] * Kd;
-  }
-  size_t arow[2];
-#pragma unroll
-  for (int ms = 0; ms < 2; ms++) {
-    const int r = ms * 32 + l32;
-    const int rr = r < it.mcnt ? r : 0;
-    arow[ms] = SHARED ? (size_t)(it.m0 + rr) : (size_t)(it.pos0 + it.m0 + rr);
-  }
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int ms = 0; ms < 2; ms++)
-#pragma unroll
-    for (int q = 0; q < 2; q++)
-#pragma unroll
-      for (int j = 0; j < 16; j++) acc[ms][q][j] = 0.0f;
-  float hsum[2] = {0.0f, 0.0f};
-  for (int k0 = 0; k0 < Kd; k0 += 32) {
-    const int kc = k0 + 16 * half;
-    u32x4 braw[2];
-#pragma unroll
-    for (int q = 0; q < 2; q++) braw[q] = *(const u32x4 *)(brow[q] + kc);
-    bf16x8 ahi[2][2], alo[2][2];
-#pragma unroll
-    for (int ms = 0; ms < 2; ms++)
-#pragma unroll
-      for (int s = 0; s < 2; s++) {
-        ahi[ms][s] = ld_bf16x8(Hhi + arow[ms] * Kd + kc + 8 * s);
-        alo[ms][s] = ld_bf16x8(Hlo + arow[ms] * Kd + kc + 8 * s);
-      }
-#pragma unroll
-    for (int ms = 0; ms < 2; ms++)
-#pragma unroll
-      for (int s = 0; s < 2; s++)
-#pragma unroll
-        for (int i = 0; i < 8; i++) hsum[ms] += (float)ahi[ms][s][i] + (float)alo[ms][s][i];
-#pragma unroll
-    for (int s = 0; s < 2; s++) {
-      bf16x8 b[2];
-#pragma unroll
-      for (int q = 0; q < 2; q++) b[q] = codes_to_bf16(u32x2{braw[q][2 * s], braw[q][2 * s + 1]});
-#pragma unroll
-      for (int ms = 0; ms < 2; ms++)
-#pragma unroll
-        for (int q = 0; q < 2; q++) {
-          acc[ms][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ahi[ms][s], b[q], acc[ms][q], 0, 0, 0);
-          acc[ms][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(alo[ms][s], b[q], acc[ms][q], 0, 0, 0);
-        }
+  const int nw = nt * PF_DN_N + wave * 64, n0 = nw + l32;
+  const size_t rbase = SHARED ? (size_t)it.m0 : (size_t)(it.pos0 + it.m0);
+  const int r = threadIdx.x >> 2;
+  const size_t arow = (rbase + (r < it.mcnt ? r : 0)) * Kd;
+  f32x16 acc[NSUB][2];
+  float hsum[NSUB];
+  pf_mainloop<NSUB, false>(Hhi, Hlo, arow, Kd, wq + (size_t)nw * Kd, wq + (size_t)(nw + 32) * Kd, acc, hsum, sm);
+  {  // lane = row of the block: Σh from the gate_up partials (each wave for itself)
+    float hs = 0.0f;
+    if (lane < it.mcnt) {
+      const float *hp = hpart + (rbase + lane) * ntK;
+      for (int k = 0; k < ntK; k++) hs += hp[k];
     }
-  }
-  // Σh of row l32 (+32 ms): lanes l and l+32 hold the two column halves
-  __shared__ float s_hsum[4][2][32];
-#pragma unroll
-  for (int ms = 0; ms < 2; ms++) {
-    const float other = __shfl_xor(hsum[ms], 32);
-    if (half == 0) s_hsum[wave][ms][l32] = hsum[ms] + other;
+    sm.hsum[wave][half][l32] = hs;
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
   for (int q = 0; q < 2; q++) {
-    const float2 so = ((const float2 *)wso)[nrow[q]];
+    const float2 so = ((const float2 *)wso)[n0 + 32 * q];
 #pragma unroll
-    for (int ms = 0; ms < 2; ms++)
+    for (int ms = 0; ms < NSUB; ms++)
 #pragma unroll
       for (int j = 0; j < 16; j++) {
-        const int r = ms * 32 + mfma_row(lane, j);
-        if (r >= it.mcnt) continue;
-        const float hs = s_hsum[wave][ms][mfma_row(lane, j)];
-        const size_t row = SHARED ? (size_t)(it.m0 + r) : (size_t)(it.pos0 + it.m0 + r);
-        Y[row * H + nrow[q]] = __builtin_fmaf(so.x, acc[ms][q][j], so.y * hs);
+        const int m = ms * 32 + mfma_row(lane, j);
+        if (m >= it.mcnt) continue;
+        const float hs = sm.hsum[wave][ms][mfma_row(lane, j)];
+        Y[(rbase + m) * H + n0 + 32 * q] = __builtin_fmaf(so.x, acc[ms][q][j], so.y * hs);
       }
   }
 }
 
-__global__ void __launch_bounds__(256) k_pf_down(dsh_layer_t L, const pf_item *__restrict__ items,
-                                                 const int *__restrict__ n_items, const __bf16 *__restrict__ Hhi,
-                                                 const __bf16 *__restrict__ Hlo, const __bf16 *__restrict__ Shi,
-                                                 const __bf16 *__restrict__ Slo, float *__restrict__ Y,
-                                                 float *__restrict__ Ysh) {
-  if ((int)blockIdx.x >= *n_items) return;
-  const pf_item it = items[blockIdx.x];
-  const int nt = blockIdx.y;
-  if (it.seg == L.E)
-    down_tile<true>(L, it, nt, Shi, Slo, Ysh);
+template <bool SHARED>
+__device__ __forceinline__ void down_dispatch(const dsh_layer_t &L, const pf_item &it, int nt, const __bf16 *Hhi,
+                                              const __bf16 *Hlo, const float *hpart, float *Y, pf_smem &sm) {
+  if (it.mcnt <= 32)
+    down_tile<SHARED, 1>(L, it, nt, Hhi, Hlo, hpart, Y, sm);
   else
-    down_tile<false>(L, it, nt, Hhi, Hlo, Y);
+    down_tile<SHARED, 2>(L, it, nt, Hhi, Hlo, hpart, Y, sm);
+}
+
+__global__ void __launch_bounds__(256, 2) k_pf_down(dsh_layer_t L, const pf_item *__restrict__ items,
+                                                    const int *__restrict__ counts, const __bf16 *Hhi,
+                                                    const __bf16 *Hlo, const __bf16 *Shi, const __bf16 *Slo,
+                                                    const float *__restrict__ hpr, const float *__restrict__ hps,
+                                                    float *__restrict__ Y, float *__restrict__ Ysh) {
+  __shared__ __attribute__((aligned(16))) pf_smem sm;
+  int item, nt;
+  if (!pf_tile(counts, L.H / PF_DN_N, L.H / PF_DN_N, item, nt)) return;
+  const pf_item it = items[item];
+  if (it.seg == L.E)
+    down_dispatch<true>(L, it, nt, Shi, Slo, hps, Ysh, sm);
+  else
+    down_dispatch<false>(L, it, nt, Hhi, Hlo, hpr, Y, sm);
 }
 
 // ---------------------------------------------------------------------------------- combine
 // One block per token: routed slots in ascending expert order (the reference's scatter-add order,
-// ds_moe_decoder.c:781-795), weights w_k, then the shared output and the residual.
+// ds_moe_decoder.c:781-795; equal experts keep slot order), weights w_k, then the shared output
+// and the residual.
 __global__ void __launch_bounds__(256) k_pf_combine(const float *__restrict__ X, const int *__restrict__ idx,
                                                     const float *__restrict__ w, const int *__restrict__ pos_of,
                                                     const float *__restrict__ Y, const float *__restrict__ Ysh,
                                                     int H, int K, int residual, int bf16sim, float *__restrict__ out) {
   __shared__ int s_pos[64];
   __shared__ float s_w[64];
-  __shared__ int e_sorted[64];
   __shared__ int s_n;
   const int t = blockIdx.x;
-  if (threadIdx.x == 0) {
-    int n = 0;
-    for (int k = 0; k < K; k++) {
-      const int e = idx[(size_t)t * K + k];
-      if (e < 0) continue;
-      int j = n++;
-      while (j > 0 && e_sorted[j - 1] > e) {
-        e_sorted[j] = e_sorted[j - 1];
-        s_pos[j] = s_pos[j - 1];
-        s_w[j] = s_w[j - 1];
-        j--;
-      }
-      e_sorted[j] = e;
-      s_pos[j] = pos_of[(size_t)t * K + k];
-      s_w[j] = w[(size_t)t * K + k];
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int e = lane < K ? idx[(size_t)t * K + lane] : -1;
+    const int pos = lane < K ? pos_of[(size_t)t * K + lane] : -1;
+    const float wt = lane < K ? w[(size_t)t * K + lane] : 0.0f;
+    const bool valid = e >= 0 && pos >= 0;
+    int rank = 0;
+    for (int j = 0; j < K; j++) {
+      const int ej = __shfl(e, j), pj = __shfl(pos, j);
+      if (ej >= 0 && pj >= 0 && (ej < e || (ej == e && j < lane))) rank++;
     }
-    s_n = n;
+    if (valid) {
+      s_pos[rank] = pos;
+      s_w[rank] = wt;
+    }
+    const int n = __popcll(__ballot(valid));
+    if (lane == 0) s_n = n;
   }
   __syncthreads();
-  for (int c = threadIdx.x; c < H; c += 256) {
-    float routed = 0.0f;
-    for (int j = 0; j < s_n; j++) {
-      float v = Y[(size_t)s_pos[j] * H + c];
-      if (bf16sim) v = dsh_bf16_round_half_up(v);
-      routed = __builtin_fmaf(s_w[j], v, routed);
+  const int n = s_n;
+  for (int c = threadIdx.x; c < H / 4; c += 256) {
+    f32x4 routed = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < n; j++) {
+      f32x4 v = ((const f32x4 *)(Y + (size_t)s_pos[j] * H))[c];
+      const float wj = s_w[j];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        if (bf16sim) v[i] = dsh_bf16_round_half_up(v[i]);
+        routed[i] = __builtin_fmaf(wj, v[i], routed[i]);
+      }
     }
-    float sh = Ysh[(size_t)t * H + c];
-    if (bf16sim) sh = dsh_bf16_round_half_up(sh);
-    const float o = routed + sh;
-    out[(size_t)t * H + c] = residual ? X[(size_t)t * H + c] + o : o;
+    f32x4 sh = ((const f32x4 *)(Ysh + (size_t)t * H))[c];
+    f32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      if (bf16sim) sh[i] = dsh_bf16_round_half_up(sh[i]);
+      o[i] = routed[i] + sh[i];
+    }
+    if (residual) {
+      const f32x4 x = ((const f32x4 *)(X + (size_t)t * H))[c];
+#pragma unroll
+      for (int i = 0; i < 4; i++) o[i] = x[i] + o[i];
+    }
+    ((f32x4 *)(out + (size_t)t * H))[c] = o;
   }
 }
 
@@ -432,17 +700,24 @@ struct pf_ws {
   float *xsum;
   int *idx;
   float *w;
-  int *seg_off, *n_items;
+  int *seg_off, *counts;
   pf_item *items;
   int *pair_tok, *pos_of;
   __bf16 *Hhi, *Hlo, *Shi, *Slo;
   float *Y, *Ysh;
+  float *ps;        // [T][4][64] partial router scores
+  float *hpr, *hps; // Σh partials per (row, gate_up n-tile): routed [TK][I/128], shared [T][SI/128]
 };
 
 size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-int pf_max_items(const dsh_layer_t *L, int T) {
-  return (T * L->K + PF_MT - 1) / PF_MT + L->E + (T + PF_MT - 1) / PF_MT;
+int pf_max_routed_items(const dsh_layer_t *L, int T) { return (T * L->K + PF_MT - 1) / PF_MT + L->E; }
+int pf_shared_items(int T) { return (T + PF_MT - 1) / PF_MT; }
+
+// Blocks of a GEMM launch: every tile of the largest possible work list, rounded up to 8.
+int pf_grid(const dsh_layer_t *L, int T, int ntS, int ntR) {
+  const int n = pf_shared_items(T) * ntS + pf_max_routed_items(L, T) * ntR;
+  return (n + 7) & ~7;
 }
 
 // Carves the workspace; returns its size (ws may be NULL to size it).
@@ -461,8 +736,8 @@ size_t pf_carve(const dsh_layer_t *L, int T, void *base, pf_ws *w) {
   TAKE(idx, int, TK);
   TAKE(w, float, TK);
   TAKE(seg_off, int, E + 1);
-  TAKE(n_items, int, 1);
-  TAKE(items, pf_item, pf_max_items(L, T));
+  TAKE(counts, int, 2);
+  TAKE(items, pf_item, pf_max_routed_items(L, T) + pf_shared_items(T));
   TAKE(pair_tok, int, TK);
   TAKE(pos_of, int, TK);
   TAKE(Hhi, __bf16, TK * I);
@@ -471,6 +746,9 @@ size_t pf_carve(const dsh_layer_t *L, int T, void *base, pf_ws *w) {
   TAKE(Slo, __bf16, T * SI);
   TAKE(Y, float, TK * H);
   TAKE(Ysh, float, T * H);
+  TAKE(ps, float, (size_t)T * 4 * 64);
+  TAKE(hpr, float, TK * (I / PF_GU_N));
+  TAKE(hps, float, (size_t)T * (SI / PF_GU_N));
 #undef TAKE
   return off;
 }
@@ -480,7 +758,9 @@ extern "C" {
 
 int dsh_pf_supported(const dsh_layer_t *L) {
   if (L->H % PF_DN_N || L->I % PF_GU_N || L->SI % PF_GU_N) return 0;
+  if (L->H % PF_KS || L->I % PF_KS || L->SI % PF_KS) return 0;
   if (L->E > 64 || L->K > 64 || L->K > L->E) return 0;
+  if ((size_t)PF_TB * L->H * sizeof(float) > 96 * 1024) return 0;  // DECODE scores: x rows in LDS
   return 1;
 }
 
@@ -493,17 +773,26 @@ hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int r
   pf_ws w;
   pf_carve(L, T, ws, &w);
   const int H = L->H, K = L->K, E = L->E;
-  k_pf_split<<<(T + 3) / 4, 256, 0, s>>>(X, T, H, w.Xhi, w.Xlo, w.xsum);
-  if (route_mode == DSH_ROUTE_CFG)
-    k_pf_route<DSH_ROUTE_CFG><<<T, 256, (size_t)H * 4, s>>>(*L, X, nthreads, w.idx, w.w);
-  else
-    k_pf_route<DSH_ROUTE_DECODE><<<T, 256, (size_t)H * 4, s>>>(*L, X, nthreads, w.idx, w.w);
-  k_pf_plan<<<1, 256, 0, s>>>(w.idx, T, K, E, w.seg_off, w.items, w.n_items);
-  k_pf_scatter<<<(E + 3) / 4, 256, 0, s>>>(w.idx, T, K, E, w.seg_off, w.pair_tok, w.pos_of);
-  const int mi = pf_max_items(L, T);
-  k_pf_gate_up<<<dim3(mi, max(L->I, L->SI) / PF_GU_N), 256, 0, s>>>(*L, w.items, w.n_items, w.Xhi, w.Xlo, w.xsum,
-                                                                   w.pair_tok, bf16sim, w.Hhi, w.Hlo, w.Shi, w.Slo);
-  k_pf_down<<<dim3(mi, H / PF_DN_N), 256, 0, s>>>(*L, w.items, w.n_items, w.Hhi, w.Hlo, w.Shi, w.Slo, w.Y, w.Ysh);
+  // CFG partial sums over the same row blocks as the decode path (8 rows, 16 past 1280 columns)
+  const int R = H / dsh_dec_partials(H);
+  if (route_mode == DSH_ROUTE_CFG) {
+    const dim3 g((T + PF_SC_TOK - 1) / PF_SC_TOK, 4);
+    if (R == 16)
+      k_pf_scores_cfg<16><<<g, 256, 0, s>>>(L->router_f32_t, X, T, H, E, w.ps);
+    else
+      k_pf_scores_cfg<8><<<g, 256, 0, s>>>(L->router_f32_t, X, T, H, E, w.ps);
+    k_pf_select<DSH_ROUTE_CFG><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, w.Xhi, w.Xlo, w.xsum, w.idx, w.w);
+  } else {
+    k_pf_scores_bf16<<<(T + PF_TB - 1) / PF_TB, 256, (size_t)PF_TB * H * sizeof(float), s>>>(
+        L->router_bf16, X, T, H, E, nthreads, w.ps);
+    k_pf_select<DSH_ROUTE_DECODE><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, w.Xhi, w.Xlo, w.xsum, w.idx,
+                                                                w.w);
+  }
+  k_pf_plan<<<1, 1024, 0, s>>>(w.idx, T, K, E, w.seg_off, w.items, w.counts, w.pair_tok, w.pos_of);
+  k_pf_gate_up<<<pf_grid(L, T, L->SI / PF_GU_N, L->I / PF_GU_N), 256, 0, s>>>(
+      *L, w.items, w.counts, w.Xhi, w.Xlo, w.xsum, w.pair_tok, bf16sim, w.Hhi, w.Hlo, w.Shi, w.Slo, w.hpr, w.hps);
+  k_pf_down<<<pf_grid(L, T, H / PF_DN_N, H / PF_DN_N), 256, 0, s>>>(*L, w.items, w.counts, w.Hhi, w.Hlo, w.Shi,
+                                                                     w.Slo, w.hpr, w.hps, w.Y, w.Ysh);
   k_pf_combine<<<T, 256, 0, s>>>(X, w.idx, w.w, w.pos_of, w.Y, w.Ysh, H, K, residual, bf16sim, out);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess && idx_out)

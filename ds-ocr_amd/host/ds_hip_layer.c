@@ -24,6 +24,12 @@ struct ds_hip_layer {
   float *partials;        /* [H/8][64] router partial scores */
   int np;                 /* number of partial rows in CFG mode */
   int have_f32, have_bf16;
+  /* prefill: the launch sequence as a graph, reused while the call's pointers and sizes repeat */
+  hipGraphExec_t pf_exec;
+  struct pf_key {
+    const void *out, *x, *ws, *idx, *w;
+    int T, mode, residual, bf16sim, threads;
+  } pf_key;
 };
 
 static size_t al(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -106,6 +112,7 @@ ds_hip_layer_t *ds_hip_layer_create(int hidden, int inter, int n_experts, int to
 void ds_hip_layer_destroy(ds_hip_layer_t *L) {
   if (!L) return;
   hipStreamSynchronize(dsr_stream);
+  if (L->pf_exec) hipGraphExecDestroy(L->pf_exec);
   hipFree(L->arena);
   free(L);
 }
@@ -308,10 +315,62 @@ int ds_hip_layer_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
                      L->H, L->I, L->SI);
   void *ws = dsr_scratch(DSR_SLOT_PF, dsh_pf_workspace_bytes(&L->d, T));
   if (!ws) return -1;
-  hipError_t e = dsh_launch_prefill(&L->d, x_dev, T, route_mode, dsr_threads(), residual, ds_bf16_simulate_python,
-                                    out_dev, ws, idx_dev, w_dev, dsr_stream);
-  if (e != hipSuccess) return dsr_fail("prefill kernels", e);
+  struct pf_key key;
+  memset(&key, 0, sizeof key);
+  key.out = out_dev;
+  key.x = x_dev;
+  key.ws = ws;
+  key.idx = idx_dev;
+  key.w = w_dev;
+  key.T = T;
+  key.mode = route_mode;
+  key.residual = residual;
+  key.bf16sim = ds_bf16_simulate_python;
+  key.threads = dsr_threads();
+  if (!L->pf_exec || memcmp(&key, &L->pf_key, sizeof key) != 0) {
+    /* the seven kernels (and the idx/w copies) captured once, then one graph launch per call */
+    if (L->pf_exec) {
+      hipGraphExecDestroy(L->pf_exec);
+      L->pf_exec = NULL;
+    }
+    DSR_TRY(hipStreamBeginCapture(dsr_stream, hipStreamCaptureModeThreadLocal), "prefill capture begin");
+    hipError_t e = dsh_launch_prefill(&L->d, x_dev, T, route_mode, key.threads, residual, key.bf16sim, out_dev, ws,
+                                      idx_dev, w_dev, dsr_stream);
+    hipGraph_t g = NULL;
+    hipError_t ec = hipStreamEndCapture(dsr_stream, &g);
+    if (e != hipSuccess || ec != hipSuccess || !g) {
+      if (g) hipGraphDestroy(g);
+      return dsr_fail("prefill kernels", e != hipSuccess ? e : ec);
+    }
+    e = hipGraphInstantiate(&L->pf_exec, g, NULL, NULL, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) {
+      L->pf_exec = NULL;
+      return dsr_fail("prefill graph instantiate", e);
+    }
+    L->pf_key = key;
+  }
+  DSR_TRY(hipGraphLaunch(L->pf_exec, dsr_stream), "prefill graph launch");
   return 0;
+}
+
+/* Average device time of n back-to-back prefill calls (HIP events on the library stream). */
+int ds_hip_time_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, int T, int route_mode, int n, float *ms) {
+  if (!ms || n <= 0) return dsr_failf("ds_hip_time_prefill: invalid arguments");
+  if (ds_hip_layer_prefill(L, out_dev, x_dev, T, route_mode, 0, NULL, NULL)) return -1; /* sizes the workspace */
+  hipEvent_t a, b;
+  DSR_TRY(hipEventCreate(&a), "event");
+  DSR_TRY(hipEventCreate(&b), "event");
+  int rc = 0;
+  if (hipEventRecord(a, dsr_stream) != hipSuccess) rc = -1;
+  for (int i = 0; i < n && rc == 0; i++) rc = ds_hip_layer_prefill(L, out_dev, x_dev, T, route_mode, 0, NULL, NULL);
+  if (rc == 0 && (hipEventRecord(b, dsr_stream) != hipSuccess || hipEventSynchronize(b) != hipSuccess ||
+                  hipEventElapsedTime(ms, a, b) != hipSuccess))
+    rc = dsr_failf("ds_hip_time_prefill: timing failed");
+  if (rc == 0) *ms /= (float)n;
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  return rc;
 }
 
 /* ================================================================ decode stack */

@@ -85,6 +85,9 @@ int ds_hip_layer_forward(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
 int ds_hip_layer_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, int T, int route_mode, int residual,
                          int *idx_dev, float *w_dev);
 
+/* Average device time (ms) of n back-to-back ds_hip_layer_prefill calls (no residual). */
+int ds_hip_time_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, int T, int route_mode, int n, float *ms);
+
 /* ---------------- decode stack: n MoE layers + argmax LM head ---------------- */
 typedef struct ds_hip_stack ds_hip_stack_t;
 
