@@ -3,10 +3,10 @@
 // down projection and a deterministic combine (ds_moe_decoder.c:629-809 is the reference block; it
 // runs sgemm on bf16 weights, this build runs the same layer's INT8 blocks).
 //
-// Numerics. Codes u = q + 128 (0..255) are exact in bf16. Each f32 activation a is split into
-// hi = bf16(a) and lo = bf16(a - hi), so a = hi + lo to about 2^-17 relative, and
-// Σ u·a = Σ u·hi + Σ u·lo is accumulated by the MFMA in f32 (products exact). The epilogue folds the
-// row's scale and offset exactly as the decode path does: y = scale · Σu·a + offset · Σa.
+// Numerics. The stored codes q = u - 128 (-128..127) are exact in bf16. Each f32 activation a is
+// split into hi = bf16(a) and lo = bf16(a - hi), so a = hi + lo to about 2^-17 relative, and
+// Σ q·a = Σ q·hi + Σ q·lo is accumulated by the MFMA in f32 (products exact). The epilogue folds the
+// row's scale and offset: y = scale·Σu·a + offset·Σa = scale·Σq·a + (offset + 128·scale)·Σa.
 //
 // Kernels (one launch each, all sizes fixed by T, so a graph can hold them):
 //   k_pf_scores  router scores in the decode path's order, as four partial sums per token
@@ -22,6 +22,8 @@
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
@@ -39,19 +41,20 @@ struct pf_item {
 };
 
 // ---------------------------------------------------------------------------------- helpers
+__device__ __forceinline__ unsigned pk_bf16(float x, float y) {
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{x, y}, bf16x2));
+}
+
+// 8 stored codes q (signed bytes, q = u - 128) → 8 exact bf16 values (one sign-extending byte
+// conversion per code and one pack per pair)
 __device__ __forceinline__ bf16x8 codes_to_bf16(u32x2 v) {
-  // stored codes are q = u - 128; u = byte ^ 0x80 is exact in bf16
-  const uint32_t a = v[0] ^ 0x80808080u, b = v[1] ^ 0x80808080u;
-  bf16x8 r;
-  r[0] = (__bf16)(float)(a & 0xFF);
-  r[1] = (__bf16)(float)((a >> 8) & 0xFF);
-  r[2] = (__bf16)(float)((a >> 16) & 0xFF);
-  r[3] = (__bf16)(float)(a >> 24);
-  r[4] = (__bf16)(float)(b & 0xFF);
-  r[5] = (__bf16)(float)((b >> 8) & 0xFF);
-  r[6] = (__bf16)(float)((b >> 16) & 0xFF);
-  r[7] = (__bf16)(float)(b >> 24);
-  return r;
+  const int a = (int)v[0], b = (int)v[1];
+  u32x4 r;
+  r[0] = pk_bf16((float)((a << 24) >> 24), (float)((a << 16) >> 24));
+  r[1] = pk_bf16((float)((a << 8) >> 24), (float)(a >> 24));
+  r[2] = pk_bf16((float)((b << 24) >> 24), (float)((b << 16) >> 24));
+  r[3] = pk_bf16((float)((b << 8) >> 24), (float)(b >> 24));
+  return __builtin_bit_cast(bf16x8, r);
 }
 
 __device__ __forceinline__ bf16x8 ld_bf16x8(const __bf16 *p) { return *(const bf16x8 *)p; }
@@ -230,10 +233,12 @@ __global__ void __launch_bounds__(256) k_pf_select(const float *__restrict__ X, 
 // entries at a time, the entries routed to the same expert are found with 7 ballots over the
 // expert's bits. Entries with no expert (idx < 0 or >= E) get pos_of = -1.
 // Work items: each expert's pairs in chunks of PF_MT (items 0 .. n_routed-1), then the shared
-// expert's T tokens in chunks of PF_MT; counts = {n_routed, n_shared}.
-__global__ void __launch_bounds__(1024) k_pf_plan(const int *__restrict__ idx, int T, int K, int E,
-                                                  int *__restrict__ seg_off, pf_item *__restrict__ items,
-                                                  int *__restrict__ counts, int *__restrict__ pair_tok,
+// expert's T tokens in chunks of PF_MT; counts = {n_routed, n_shared}; and the routed GEMM tile
+// lists of both projections.
+__global__ void __launch_bounds__(1024) k_pf_plan(const int *__restrict__ idx, int T, int K, int E, int nt_gu,
+                                                  int nt_dn, int *__restrict__ seg_off, pf_item *__restrict__ items,
+                                                  int *__restrict__ counts, int *__restrict__ tiles_gu,
+                                                  int *__restrict__ tiles_dn, int *__restrict__ pair_tok,
                                                   int *__restrict__ pos_of) {
   __shared__ int cnt[16][64];
   __shared__ int run[16][64];
@@ -285,6 +290,12 @@ __global__ void __launch_bounds__(1024) k_pf_plan(const int *__restrict__ idx, i
     const int nr = __shfl(ich, 63);
     ich -= nch;
     for (int j = 0; j < nch; j++) items[ich + j] = pf_item{lane, j * PF_MT, min(PF_MT, c - j * PF_MT), off};
+    // routed GEMM tiles, expert by expert: n-tile major, the expert's chunks adjacent, so the
+    // blocks that stream the same weight rows run side by side (item << 8 | n-tile)
+    for (int nt = 0; nt < nt_gu; nt++)
+      for (int j = 0; j < nch; j++) tiles_gu[ich * nt_gu + nt * nch + j] = ((ich + j) << 8) | nt;
+    for (int nt = 0; nt < nt_dn; nt++)
+      for (int j = 0; j < nch; j++) tiles_dn[ich * nt_dn + nt * nch + j] = ((ich + j) << 8) | nt;
     const int ns = (T + PF_MT - 1) / PF_MT;
     for (int j = lane; j < ns; j += 64) items[nr + j] = pf_item{E, j * PF_MT, min(PF_MT, T - j * PF_MT), 0};
     if (lane == 0) {
@@ -318,12 +329,12 @@ __global__ void __launch_bounds__(1024) k_pf_plan(const int *__restrict__ idx, i
 }
 
 // ---------------------------------------------------------------------------------- grouped GEMM
-// Work tiles: the shared expert's first (n-tile major, its items adjacent, so the items that read
-// the same weight rows run together), then each routed item's n-tiles in turn (an item's tiles
-// share its A rows). Physical block b runs logical tile (b % 8)·C + b / 8 with C = ceil(tiles / 8):
-// blocks are handed to the 8 XCDs in turn, so each XCD gets a contiguous run of tiles and its L2
-// serves the shared reads.
-__device__ __forceinline__ bool pf_tile(const int *counts, int ntS, int ntR, int &item, int &nt) {
+// Work tiles: the shared expert's first (n-tile major, its items adjacent), then the routed tiles in
+// the plan's order (per expert: n-tile major, chunks adjacent): blocks that read the same weight rows
+// are neighbours. Physical block b runs logical tile (b % 8)·C + b / 8 with C = ceil(tiles / 8):
+// blocks are handed to the 8 XCDs in turn, so each XCD gets a contiguous run of tiles and
+// neighbouring tiles share that XCD's L2.
+__device__ __forceinline__ bool pf_tile(const int *counts, const int *tiles, int ntS, int ntR, int &item, int &nt) {
   const int nr = counts[0], ns = counts[1];
   const int nshared = ns * ntS, total = nshared + nr * ntR;
   const int C = (total + 7) / 8;
@@ -335,9 +346,9 @@ __device__ __forceinline__ bool pf_tile(const int *counts, int ntS, int ntR, int
     nt = lg / ns;
     item = nr + (lg - nt * ns);
   } else {
-    const int j = lg - nshared;
-    item = j / ntR;
-    nt = j - item * ntR;
+    const int t = tiles[lg - nshared];
+    item = t >> 8;
+    nt = t & 255;
   }
   return true;
 }
@@ -347,61 +358,76 @@ __device__ __forceinline__ bool pf_tile(const int *counts, int ntS, int ntR, int
 // K runs in stages of PF_KS = 128 columns, one 128-byte line of each weight row:
 // - weights: each wave streams its own 64 rows; per stage 8 loads in which 8 adjacent lanes read one
 //   row's full line (full lines keep HBM at its streaming rate), held in a PF_D-stage register ring
-//   and written to the wave's own LDS tile (pitch 144 B) when the stage begins;
-// - A: the block's rows are copied in 64-column half-stages (each thread 2 x 16 bytes of hi and of lo
-//   of one row, two half-stages ahead in registers) into a double-buffered LDS tile (pitch 144 B);
+//   and written to the wave's own LDS tile when the stage begins;
+// - A: the block's rows are copied in 64-column half-stages (8 adjacent lanes read one row's 128
+//   bytes of hi or lo; two half-stages ahead in registers) into a double-buffered LDS tile;
+// - both LDS tiles have 128-byte rows whose 16-byte chunks are XOR-swizzled by pf_swz(row), so the
+//   full-row writes and the MFMA reads (16 lanes, 16 rows, one chunk) are free of bank conflicts;
 // - per 32-column block, lane half h takes columns 16h..16h+15 as two MFMA k-slices of 8 (the same
 //   permutation of k for A and B leaves the product unchanged): one 16-byte LDS read gives a lane its
 //   16 codes of a weight row, one 16-byte read its 8 values of an A row.
 // One barrier per half-stage. The load order is the same in every stage and the first group of
-// PF_D stages is peeled, so the wait counts the compiler derives keep PF_D stages of weight lines in
-// flight. Stages past the last (K rounded up to PF_D stages) load a valid line and skip the math.
-// A rows past the item's count repeat a valid row; their results are never stored.
+// PF_D stages is peeled, so the wait counts the compiler derives keep the rings full. Stages past
+// the last (K rounded up to PF_D stages) load a valid line and skip the math. A rows past the item's
+// count repeat a valid row; their results are never stored.
 #define PF_KS 128
-#define PF_D 2
-#define PF_AP 72   // A tile pitch in bf16 (144 bytes)
-#define PF_BP 144  // weight tile pitch in bytes
+#ifndef PF_D
+#define PF_D 1   // weight-line stages in flight per wave
+#endif
+#ifndef PF_OCC
+#define PF_OCC 2  // GEMM blocks per CU the register budget is sized for
+#endif
 
 struct pf_smem {
-  __bf16 A[2][2][PF_MT][PF_AP];   // [half-stage parity][hi, lo][row][column]
-  unsigned char B[4][64][PF_BP];  // per wave: its 64 weight rows x the stage's 128 codes
-  float hsum[4][2][32];           // down: Σh of the block's A rows (per wave, per 32-row sub-tile)
+  union {
+    struct {
+      __bf16 A[2][2][PF_MT][64];      // [half-stage parity][hi, lo][row][column, swizzled]
+      unsigned char B[4][64][PF_KS];  // per wave: its 64 weight rows x the stage's codes, swizzled
+    } t;
+    float red[4][64][33];  // gate_up epilogue: h values per wave for the row sums
+  } u;
+  float hsum[4][2][32];  // Σh of the block's A rows (per wave, per 32-row sub-tile)
+  float xs[PF_MT];       // gate_up: Σx of the block's A rows (their tokens)
 };
 
-template <int NSUB, bool HSUM>
-__device__ __forceinline__ void pf_mainloop(const __bf16 *Ahi, const __bf16 *Alo, size_t arow, int K,
+// 16-byte chunk c of LDS row r sits at chunk c ^ pf_swz(r): 16 consecutive rows map one chunk to 16
+// distinct bank groups, and two consecutive rows fill 256 contiguous bytes
+__device__ __forceinline__ int pf_swz(int r) { return (r ^ (r >> 3)) & 7; }
+
+template <int NSUB>
+__device__ __forceinline__ void pf_mainloop(const __bf16 *Ahi, const __bf16 *Alo, const size_t *arow, int K,
                                             const int8_t *brow0, const int8_t *brow1, f32x16 (&acc)[NSUB][2],
-                                            float (&hsum)[NSUB], pf_smem &sm) {
+                                            pf_smem &sm) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, l32 = lane & 31;
-  const int crow = threadIdx.x >> 2, cch = threadIdx.x & 3;
+  const int ar = threadIdx.x >> 3, ac = threadIdx.x & 7;  // A copy: rows ar and ar + 32, chunk ac
   const int nk = K / PF_KS, nkp = (nk + PF_D - 1) / PF_D * PF_D, nh = 2 * nk;
 #pragma unroll
-  for (int ms = 0; ms < NSUB; ms++) {
-    hsum[ms] = 0.0f;
+  for (int ms = 0; ms < NSUB; ms++)
 #pragma unroll
     for (int q = 0; q < 2; q++)
 #pragma unroll
       for (int j = 0; j < 16; j++) acc[ms][q][j] = 0.0f;
-  }
-  // The weight addresses take a zero offset from an asm that depends on the A row, so the
-  // prologue's weight loads are issued after the row index is known, in the loop's order.
+  // The weight addresses take a zero offset from an asm that depends on the A rows, so the
+  // prologue's weight loads are issued after the row indices are known, in the loop's order.
   int zero = 0;
-  asm volatile("" : "+v"(zero) : "v"((int)arow));
+  asm volatile("" : "+v"(zero) : "v"((int)arow[0]), "v"((int)arow[1]));
   const size_t K8 = (size_t)8 * K;
-  const int8_t *p0 = brow0 + zero + (size_t)(lane >> 3) * K + 16 * (lane & 7);
-  const int8_t *p1 = brow1 + zero + (size_t)(lane >> 3) * K + 16 * (lane & 7);
+  const int brow = lane >> 3, bch = lane & 7;
+  const int8_t *p0 = brow0 + zero + (size_t)brow * K + 16 * bch;
+  const int8_t *p1 = brow1 + zero + (size_t)brow * K + 16 * bch;
+  const int aw0 = 8 * (ac ^ pf_swz(ar)), aw1 = 8 * (ac ^ pf_swz(ar + 32));
   u32x4 bR[PF_D][8];
-  bf16x8 aR[2][4];  // [half-stage parity][hi cols c, hi cols c+32, lo c, lo c+32]
+  bf16x8 aR[2][4];  // [half-stage parity][hi row ar, hi row ar+32, lo row ar, lo row ar+32]
   auto load_b = [&](u32x4(&dst)[8], int k) {
 #pragma unroll
     for (int i = 0; i < 8; i++) dst[i] = *(const u32x4 *)((i < 4 ? p0 : p1) + (i & 3) * K8 + (size_t)k * PF_KS);
   };
   auto load_a = [&](bf16x8(&dst)[4], int hs) {
-    const size_t o = arow + (size_t)hs * 64 + 8 * cch;
-    dst[0] = ld_bf16x8(Ahi + o);
-    dst[1] = ld_bf16x8(Ahi + o + 32);
-    dst[2] = ld_bf16x8(Alo + o);
-    dst[3] = ld_bf16x8(Alo + o + 32);
+    const size_t o = (size_t)hs * 64 + 8 * ac;
+    dst[0] = ld_bf16x8(Ahi + arow[0] + o);
+    dst[1] = ld_bf16x8(Ahi + arow[1] + o);
+    dst[2] = ld_bf16x8(Alo + arow[0] + o);
+    dst[3] = ld_bf16x8(Alo + arow[1] + o);
   };
 #pragma unroll
   for (int s = 0; s < PF_D; s++) {
@@ -420,45 +446,63 @@ __device__ __forceinline__ void pf_mainloop(const __bf16 *Ahi, const __bf16 *Alo
       // the stage's weight lines → the wave's tile (the wave's reads of the previous stage are
       // done: a wave's LDS operations complete in order)
 #pragma unroll
-      for (int i = 0; i < 8; i++) *(u32x4 *)&sm.B[wave][8 * i + (lane >> 3)][16 * (lane & 7)] = bR[s][i];
+      for (int i = 0; i < 8; i++) {
+        const int r = 8 * i + brow;
+        *(u32x4 *)&sm.u.t.B[wave][r][16 * (bch ^ pf_swz(r))] = bR[s][i];
+      }
       load_b(bR[s], min(k + PF_D, nk - 1));
       asm volatile("" ::: "memory");
 #pragma unroll
       for (int a = 0; a < 2; a++) {
-        *(bf16x8 *)&sm.A[a][0][crow][8 * cch] = aR[a][0];
-        *(bf16x8 *)&sm.A[a][0][crow][8 * cch + 32] = aR[a][1];
-        *(bf16x8 *)&sm.A[a][1][crow][8 * cch] = aR[a][2];
-        *(bf16x8 *)&sm.A[a][1][crow][8 * cch + 32] = aR[a][3];
+        *(bf16x8 *)&sm.u.t.A[a][0][ar][aw0] = aR[a][0];
+        *(bf16x8 *)&sm.u.t.A[a][0][ar + 32][aw1] = aR[a][1];
+        *(bf16x8 *)&sm.u.t.A[a][1][ar][aw0] = aR[a][2];
+        *(bf16x8 *)&sm.u.t.A[a][1][ar + 32][aw1] = aR[a][3];
         load_a(aR[a], min(2 * k + a + 2, nh - 1));
         asm volatile("" ::: "memory");
         __syncthreads();
         if (k < nk) {
+          // Fragment reads run ahead of the math: the weight chunks of both 32-column blocks and
+          // the A fragments of the first are read at once; each A fragment of the second block is
+          // read as soon as the matching fragment of the first has been used (a rolling window of
+          // registers), so LDS latency is exposed once per half-stage rather than once per MFMA.
+          u32x4 bf[2][2];
+          bf16x8 af[NSUB][2][2];  // [sub-tile][k-slice][hi, lo]
+          auto read_a = [&](int s2, int ms, int u) {
+            const int m = 32 * ms + l32;
+            const int ch = 4 * s2 + 2 * half + u;  // A chunk (8 columns) within the half-stage
+            af[ms][u][0] = *(const bf16x8 *)&sm.u.t.A[a][0][m][8 * (ch ^ pf_swz(m))];
+            af[ms][u][1] = *(const bf16x8 *)&sm.u.t.A[a][1][m][8 * (ch ^ pf_swz(m))];
+          };
 #pragma unroll
           for (int s2 = 0; s2 < 2; s2++) {
-            const int cb = 32 * (2 * a + s2) + 16 * half;
-            const u32x4 b0 = *(const u32x4 *)&sm.B[wave][l32][cb];
-            const u32x4 b1 = *(const u32x4 *)&sm.B[wave][32 + l32][cb];
+            const int cb = 2 * (2 * a + s2) + half;  // weight chunk of this lane half
+            bf[s2][0] = *(const u32x4 *)&sm.u.t.B[wave][l32][16 * (cb ^ pf_swz(l32))];
+            bf[s2][1] = *(const u32x4 *)&sm.u.t.B[wave][32 + l32][16 * (cb ^ pf_swz(32 + l32))];
+          }
+#pragma unroll
+          for (int ms = 0; ms < NSUB; ms++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) read_a(0, ms, u);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int s2 = 0; s2 < 2; s2++) {
             bf16x8 c0[2], c1[2];
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-              c0[u] = codes_to_bf16(u32x2{b0[2 * u], b0[2 * u + 1]});
-              c1[u] = codes_to_bf16(u32x2{b1[2 * u], b1[2 * u + 1]});
+              c0[u] = codes_to_bf16(u32x2{bf[s2][0][2 * u], bf[s2][0][2 * u + 1]});
+              c1[u] = codes_to_bf16(u32x2{bf[s2][1][2 * u], bf[s2][1][2 * u + 1]});
             }
 #pragma unroll
             for (int ms = 0; ms < NSUB; ms++)
 #pragma unroll
               for (int u = 0; u < 2; u++) {
-                const int ac = 32 * s2 + 16 * half + 8 * u;
-                const bf16x8 ah = *(const bf16x8 *)&sm.A[a][0][32 * ms + l32][ac];
-                const bf16x8 al = *(const bf16x8 *)&sm.A[a][1][32 * ms + l32][ac];
-                if (HSUM) {
-#pragma unroll
-                  for (int i = 0; i < 8; i++) hsum[ms] += (float)ah[i] + (float)al[i];
-                }
-                acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, c0[u], acc[ms][0], 0, 0, 0);
-                acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, c0[u], acc[ms][0], 0, 0, 0);
-                acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, c1[u], acc[ms][1], 0, 0, 0);
-                acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, c1[u], acc[ms][1], 0, 0, 0);
+                acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ms][u][0], c0[u], acc[ms][0], 0, 0, 0);
+                acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ms][u][0], c1[u], acc[ms][1], 0, 0, 0);
+                acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ms][u][1], c0[u], acc[ms][0], 0, 0, 0);
+                acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ms][u][1], c1[u], acc[ms][1], 0, 0, 0);
+                if (s2 == 0) read_a(1, ms, u);
+                __builtin_amdgcn_sched_barrier(0);
               }
           }
         }
@@ -483,17 +527,31 @@ __device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item
   const int u0 = nt * PF_GU_N + wave * 32, unit = u0 + l32;
   const int8_t *wq = SHARED ? L.sgu_q : L.gu_q + (size_t)it.seg * 2 * L.I * H;
   const float *wso = SHARED ? L.sgu_so : L.gu_so + (size_t)it.seg * 2 * L.I * 2;
-  const int r = threadIdx.x >> 2;
-  const int rr = r < it.mcnt ? r : 0;
-  const size_t arow = (size_t)(SHARED ? it.m0 + rr : pair_tok[it.pos0 + it.m0 + rr]) * H;
+  size_t arow[2];
+  int tok[2];
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    const int r = (threadIdx.x >> 3) + 32 * c;
+    const int rr = r < it.mcnt ? r : 0;
+    tok[c] = SHARED ? it.m0 + rr : pair_tok[it.pos0 + it.m0 + rr];
+    arow[c] = (size_t)tok[c] * H;
+  }
+  // the rows' Σx for the epilogue, staged in LDS (visible after the main loop's first barrier)
+  if ((threadIdx.x & 7) == 0) {
+    const float x0 = xsum[tok[0]], x1 = xsum[tok[1]];
+    sm.xs[threadIdx.x >> 3] = x0;
+    sm.xs[(threadIdx.x >> 3) + 32] = x1;
+  }
   f32x16 acc[NSUB][2];
-  float hs[NSUB];
-  pf_mainloop<NSUB, false>(Xhi, Xlo, arow, H, wq + (size_t)u0 * H, wq + (size_t)(Iseg + u0) * H, acc, hs, sm);
-  const float2 sog = ((const float2 *)wso)[unit], sou = ((const float2 *)wso)[Iseg + unit];
+  pf_mainloop<NSUB>(Xhi, Xlo, arow, H, wq + (size_t)u0 * H, wq + (size_t)(Iseg + u0) * H, acc, sm);
+  // signed codes: offset + 128·scale multiplies Σa
+  float2 sog = ((const float2 *)wso)[unit], sou = ((const float2 *)wso)[Iseg + unit];
+  sog.y = __builtin_fmaf(128.0f, sog.x, sog.y);
+  sou.y = __builtin_fmaf(128.0f, sou.x, sou.y);
   const size_t rbase = SHARED ? (size_t)it.m0 : (size_t)(it.pos0 + it.m0);
   // The tile's h values (as the down GEMM sees them, hi + lo) also go to LDS for the row sums
   // Σh over the block's 128 units, which the down epilogue needs for the offset term.
-  float(*red)[64][33] = (float(*)[64][33]) & sm.A[0][0][0][0];
+  float(*red)[64][33] = sm.u.red;
   __syncthreads();  // every wave is done with the main loop's tiles
 #pragma unroll
   for (int ms = 0; ms < NSUB; ms++)
@@ -502,8 +560,7 @@ __device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item
       const int m = ms * 32 + mfma_row(lane, j);
       float hsum_v = 0.0f;
       if (m < it.mcnt) {
-        const int t = SHARED ? it.m0 + m : pair_tok[it.pos0 + it.m0 + m];
-        const float xs = xsum[t];
+        const float xs = sm.xs[m];
         float g = __builtin_fmaf(sog.x, acc[ms][0][j], sog.y * xs);
         float up = __builtin_fmaf(sou.x, acc[ms][1][j], sou.y * xs);
         if (bf16sim) {
@@ -549,16 +606,17 @@ __device__ __forceinline__ void gate_up_dispatch(const dsh_layer_t &L, const pf_
     gate_up_tile<SHARED, 2>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Hhi, Hlo, hpart, sm);
 }
 
-__global__ void __launch_bounds__(256, 2) k_pf_gate_up(dsh_layer_t L, const pf_item *__restrict__ items,
+__global__ void __launch_bounds__(256, PF_OCC) k_pf_gate_up(dsh_layer_t L, const pf_item *__restrict__ items,
                                                        const int *__restrict__ counts, const __bf16 *Xhi,
                                                        const __bf16 *Xlo, const float *__restrict__ xsum,
                                                        const int *__restrict__ pair_tok, int bf16sim,
                                                        __bf16 *__restrict__ Hhi, __bf16 *__restrict__ Hlo,
                                                        __bf16 *__restrict__ Shi, __bf16 *__restrict__ Slo,
-                                                       float *__restrict__ hpr, float *__restrict__ hps) {
+                                                       float *__restrict__ hpr, float *__restrict__ hps,
+                                                       const int *__restrict__ tiles) {
   __shared__ __attribute__((aligned(16))) pf_smem sm;
   int item, nt;
-  if (!pf_tile(counts, L.SI / PF_GU_N, L.I / PF_GU_N, item, nt)) return;
+  if (!pf_tile(counts, tiles, L.SI / PF_GU_N, L.I / PF_GU_N, item, nt)) return;
   const pf_item it = items[item];
   if (it.seg == L.E)
     gate_up_dispatch<true>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Shi, Slo, hps, sm);
@@ -579,11 +637,14 @@ __device__ __forceinline__ void down_tile(const dsh_layer_t &L, const pf_item &i
   const float *wso = SHARED ? L.sdn_so : L.dn_so + (size_t)it.seg * H * 2;
   const int nw = nt * PF_DN_N + wave * 64, n0 = nw + l32;
   const size_t rbase = SHARED ? (size_t)it.m0 : (size_t)(it.pos0 + it.m0);
-  const int r = threadIdx.x >> 2;
-  const size_t arow = (rbase + (r < it.mcnt ? r : 0)) * Kd;
+  size_t arow[2];
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    const int r = (threadIdx.x >> 3) + 32 * c;
+    arow[c] = (rbase + (r < it.mcnt ? r : 0)) * Kd;
+  }
   f32x16 acc[NSUB][2];
-  float hsum[NSUB];
-  pf_mainloop<NSUB, false>(Hhi, Hlo, arow, Kd, wq + (size_t)nw * Kd, wq + (size_t)(nw + 32) * Kd, acc, hsum, sm);
+  pf_mainloop<NSUB>(Hhi, Hlo, arow, Kd, wq + (size_t)nw * Kd, wq + (size_t)(nw + 32) * Kd, acc, sm);
   {  // lane = row of the block: Σh from the gate_up partials (each wave for itself)
     float hs = 0.0f;
     if (lane < it.mcnt) {
@@ -597,7 +658,8 @@ __device__ __forceinline__ void down_tile(const dsh_layer_t &L, const pf_item &i
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
   for (int q = 0; q < 2; q++) {
-    const float2 so = ((const float2 *)wso)[n0 + 32 * q];
+    float2 so = ((const float2 *)wso)[n0 + 32 * q];
+    so.y = __builtin_fmaf(128.0f, so.x, so.y);  // signed codes: offset + 128·scale multiplies Σh
 #pragma unroll
     for (int ms = 0; ms < NSUB; ms++)
 #pragma unroll
@@ -619,14 +681,15 @@ __device__ __forceinline__ void down_dispatch(const dsh_layer_t &L, const pf_ite
     down_tile<SHARED, 2>(L, it, nt, Hhi, Hlo, hpart, Y, sm);
 }
 
-__global__ void __launch_bounds__(256, 2) k_pf_down(dsh_layer_t L, const pf_item *__restrict__ items,
+__global__ void __launch_bounds__(256, PF_OCC) k_pf_down(dsh_layer_t L, const pf_item *__restrict__ items,
                                                     const int *__restrict__ counts, const __bf16 *Hhi,
                                                     const __bf16 *Hlo, const __bf16 *Shi, const __bf16 *Slo,
                                                     const float *__restrict__ hpr, const float *__restrict__ hps,
-                                                    float *__restrict__ Y, float *__restrict__ Ysh) {
+                                                    float *__restrict__ Y, float *__restrict__ Ysh,
+                                                    const int *__restrict__ tiles) {
   __shared__ __attribute__((aligned(16))) pf_smem sm;
   int item, nt;
-  if (!pf_tile(counts, L.H / PF_DN_N, L.H / PF_DN_N, item, nt)) return;
+  if (!pf_tile(counts, tiles, L.H / PF_DN_N, L.H / PF_DN_N, item, nt)) return;
   const pf_item it = items[item];
   if (it.seg == L.E)
     down_dispatch<true>(L, it, nt, Shi, Slo, hps, Ysh, sm);
@@ -707,6 +770,7 @@ struct pf_ws {
   float *Y, *Ysh;
   float *ps;        // [T][4][64] partial router scores
   float *hpr, *hps; // Σh partials per (row, gate_up n-tile): routed [TK][I/128], shared [T][SI/128]
+  int *tiles_gu, *tiles_dn;  // routed GEMM tiles (item << 8 | n-tile) in launch order
 };
 
 size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -749,6 +813,8 @@ size_t pf_carve(const dsh_layer_t *L, int T, void *base, pf_ws *w) {
   TAKE(ps, float, (size_t)T * 4 * 64);
   TAKE(hpr, float, TK * (I / PF_GU_N));
   TAKE(hps, float, (size_t)T * (SI / PF_GU_N));
+  TAKE(tiles_gu, int, (size_t)pf_max_routed_items(L, T) * (I / PF_GU_N));
+  TAKE(tiles_dn, int, (size_t)pf_max_routed_items(L, T) * (H / PF_DN_N));
 #undef TAKE
   return off;
 }
@@ -788,11 +854,13 @@ hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int r
     k_pf_select<DSH_ROUTE_DECODE><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, w.Xhi, w.Xlo, w.xsum, w.idx,
                                                                 w.w);
   }
-  k_pf_plan<<<1, 1024, 0, s>>>(w.idx, T, K, E, w.seg_off, w.items, w.counts, w.pair_tok, w.pos_of);
+  k_pf_plan<<<1, 1024, 0, s>>>(w.idx, T, K, E, L->I / PF_GU_N, H / PF_DN_N, w.seg_off, w.items, w.counts,
+                               w.tiles_gu, w.tiles_dn, w.pair_tok, w.pos_of);
   k_pf_gate_up<<<pf_grid(L, T, L->SI / PF_GU_N, L->I / PF_GU_N), 256, 0, s>>>(
-      *L, w.items, w.counts, w.Xhi, w.Xlo, w.xsum, w.pair_tok, bf16sim, w.Hhi, w.Hlo, w.Shi, w.Slo, w.hpr, w.hps);
+      *L, w.items, w.counts, w.Xhi, w.Xlo, w.xsum, w.pair_tok, bf16sim, w.Hhi, w.Hlo, w.Shi, w.Slo, w.hpr, w.hps,
+      w.tiles_gu);
   k_pf_down<<<pf_grid(L, T, H / PF_DN_N, H / PF_DN_N), 256, 0, s>>>(*L, w.items, w.counts, w.Hhi, w.Hlo, w.Shi,
-                                                                     w.Slo, w.hpr, w.hps, w.Y, w.Ysh);
+                                                                     w.Slo, w.hpr, w.hps, w.Y, w.Ysh, w.tiles_dn);
   k_pf_combine<<<T, 256, 0, s>>>(X, w.idx, w.w, w.pos_of, w.Y, w.Ysh, H, K, residual, bf16sim, out);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess && idx_out)
