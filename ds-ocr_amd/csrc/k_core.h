@@ -75,6 +75,13 @@ typedef struct {
 /* ---- prefill MoE block (k_prefill.hip) ---- */
 int dsh_pf_supported(const dsh_layer_t *L);
 size_t dsh_pf_workspace_bytes(const dsh_layer_t *L, int T);
+/* Outside stream capture: sizes the fused GEMM grid and checks (once) that its blocks cover every
+ * XCD. force: 1 / 0 selects the fused or the two-kernel path, -1 the check's choice, -2 keeps the
+ * current choice. */
+hipError_t dsh_pf_init(int force);
+int dsh_pf_fused(void);
+/* 1 if a fused launch's bounded wait expired (its output is then not valid), 0 if not; synchronous. */
+int dsh_pf_wait_error(const void *ws, const dsh_layer_t *L, int T);
 /* out[T][H] = (residual ? X : 0) + MoE(X); ws: dsh_pf_workspace_bytes(L, T) device bytes. */
 hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int route_mode, int nthreads, int residual,
                               int bf16sim, float *out, void *ws, int *idx_out, float *w_out, hipStream_t s);

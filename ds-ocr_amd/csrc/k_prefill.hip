@@ -32,6 +32,21 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 #define PF_DN_N 256 // down: output rows per block
 #define PF_TB 8     // tokens per DECODE-mode scores block
 #define PF_PLAN_LDS 8192  // (token, slot) entries the plan kernel caches in LDS
+#define PF_NQ 8           // work queues of the fused GEMM kernel: one per XCD
+#define PF_DN_TILE 0x80000000u  // tile word: down tile flag | item << 8 | n-tile
+
+// Work queues of the fused GEMM kernel (k_pf_moe), built by the plan kernel.
+struct pf_queues {
+  int *tiles;    // [PF_NQ][cap] tile words in claim order
+  int *count;    // [PF_NQ] tiles per queue
+  int *next;     // [PF_NQ] claim counters (zeroed by the plan)
+  int *gu_done;  // [items] finished gate_up tiles per item (zeroed by the plan)
+  int *err;      // set when a bounded wait expires (zeroed by the plan)
+  int cap;
+  int ngu_r, ngu_s, ndn;      // n-tiles: gate_up routed / shared, down
+  int nk_gu, nk_dr, nk_ds;    // 128-column stages: gate_up, routed down, shared down
+  int enable;
+};
 
 struct pf_item {
   int seg;   // expert 0..E-1, or E for the shared expert
@@ -239,8 +254,10 @@ __global__ void __launch_bounds__(1024) k_pf_plan(const int *__restrict__ idx, i
                                                   int nt_dn, int *__restrict__ seg_off, pf_item *__restrict__ items,
                                                   int *__restrict__ counts, int *__restrict__ tiles_gu,
                                                   int *__restrict__ tiles_dn, int *__restrict__ pair_tok,
-                                                  int *__restrict__ pos_of) {
+                                                  int *__restrict__ pos_of, pf_queues Q) {
   __shared__ int cnt[16][64];
+  __shared__ int s_nch[64], s_ich[64];
+  __shared__ int s_nr;
   __shared__ int run[16][64];
   __shared__ int cache[PF_PLAN_LDS];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -301,6 +318,50 @@ __global__ void __launch_bounds__(1024) k_pf_plan(const int *__restrict__ idx, i
     if (lane == 0) {
       counts[0] = nr;
       counts[1] = ns;
+      s_nr = nr;
+    }
+    s_nch[lane] = lane < E ? nch : 0;
+    s_ich[lane] = ich;
+  }
+  if (threadIdx.x == 0) *Q.err = 0;
+  __syncthreads();
+  if (Q.enable) {
+    // Queue units are the work items: the routed items (cost cost_r in 128-column weight stages)
+    // and the shared-expert items (cost_s). Items are ranked by cost, costlier kind first, then
+    // by item number, and dealt to the queues in snake order (rank 16k + j goes to queue j for
+    // j < 8, to queue 15 - j otherwise), so no queue holds more than ceil(items / PF_NQ) of them.
+    // Each queue lists all its gate_up tiles (item by item, n-tiles adjacent: they share the item's
+    // A rows), then its down tiles, in rank order. Ranks and offsets have closed forms.
+    const int ns = (T + PF_MT - 1) / PF_MT, nr = s_nr, nu = nr + ns;
+    const int cost_s = Q.ngu_s * Q.nk_gu + Q.ndn * Q.nk_ds, cost_r = Q.ngu_r * Q.nk_gu + Q.ndn * Q.nk_dr;
+    const bool sh_first = cost_s > cost_r;
+    const int s0 = sh_first ? 0 : nr, s1 = s0 + ns;  // rank range of the shared items
+    // units of queue q among ranks [0, lim)
+    auto cnt = [](int q, int lim) {
+      const int r = lim & (2 * PF_NQ - 1);
+      return 2 * (lim / (2 * PF_NQ)) + (r > q) + (r > 2 * PF_NQ - 1 - q);
+    };
+    // gate_up tiles of queue q among ranks [0, lim)
+    auto gtiles = [&](int q, int lim) {
+      const int sh = cnt(q, min(lim, s1)) - cnt(q, min(lim, s0));
+      return sh * Q.ngu_s + (cnt(q, lim) - sh) * Q.ngu_r;
+    };
+    if (threadIdx.x < PF_NQ) {
+      const int q = threadIdx.x;
+      Q.count[q] = gtiles(q, nu) + cnt(q, nu) * Q.ndn;
+      Q.next[q] = 0;
+    }
+    for (int u = threadIdx.x; u < nu; u += 1024) {
+      Q.gu_done[u] = 0;
+      const bool shared = u >= nr;
+      const int rank = sh_first ? (shared ? u - nr : ns + u) : u;
+      const int pos = rank & (2 * PF_NQ - 1);
+      const int q = pos < PF_NQ ? pos : 2 * PF_NQ - 1 - pos;
+      const int gu0 = gtiles(q, rank), dn0 = gtiles(q, nu) + cnt(q, rank) * Q.ndn;
+      int *qt = Q.tiles + (size_t)q * Q.cap;
+      const int ngu = shared ? Q.ngu_s : Q.ngu_r;
+      for (int nt = 0; nt < ngu; nt++) qt[gu0 + nt] = (u << 8) | nt;
+      for (int nt = 0; nt < Q.ndn; nt++) qt[dn0 + nt] = (int)(PF_DN_TILE | (u << 8) | nt);
     }
   }
   __syncthreads();
@@ -462,47 +523,29 @@ __device__ __forceinline__ void pf_mainloop(const __bf16 *Ahi, const __bf16 *Alo
         asm volatile("" ::: "memory");
         __syncthreads();
         if (k < nk) {
-          // Fragment reads run ahead of the math: the weight chunks of both 32-column blocks and
-          // the A fragments of the first are read at once; each A fragment of the second block is
-          // read as soon as the matching fragment of the first has been used (a rolling window of
-          // registers), so LDS latency is exposed once per half-stage rather than once per MFMA.
-          u32x4 bf[2][2];
-          bf16x8 af[NSUB][2][2];  // [sub-tile][k-slice][hi, lo]
-          auto read_a = [&](int s2, int ms, int u) {
-            const int m = 32 * ms + l32;
-            const int ch = 4 * s2 + 2 * half + u;  // A chunk (8 columns) within the half-stage
-            af[ms][u][0] = *(const bf16x8 *)&sm.u.t.A[a][0][m][8 * (ch ^ pf_swz(m))];
-            af[ms][u][1] = *(const bf16x8 *)&sm.u.t.A[a][1][m][8 * (ch ^ pf_swz(m))];
-          };
 #pragma unroll
           for (int s2 = 0; s2 < 2; s2++) {
             const int cb = 2 * (2 * a + s2) + half;  // weight chunk of this lane half
-            bf[s2][0] = *(const u32x4 *)&sm.u.t.B[wave][l32][16 * (cb ^ pf_swz(l32))];
-            bf[s2][1] = *(const u32x4 *)&sm.u.t.B[wave][32 + l32][16 * (cb ^ pf_swz(32 + l32))];
-          }
-#pragma unroll
-          for (int ms = 0; ms < NSUB; ms++)
-#pragma unroll
-            for (int u = 0; u < 2; u++) read_a(0, ms, u);
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int s2 = 0; s2 < 2; s2++) {
+            const u32x4 b0 = *(const u32x4 *)&sm.u.t.B[wave][l32][16 * (cb ^ pf_swz(l32))];
+            const u32x4 b1 = *(const u32x4 *)&sm.u.t.B[wave][32 + l32][16 * (cb ^ pf_swz(32 + l32))];
             bf16x8 c0[2], c1[2];
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-              c0[u] = codes_to_bf16(u32x2{bf[s2][0][2 * u], bf[s2][0][2 * u + 1]});
-              c1[u] = codes_to_bf16(u32x2{bf[s2][1][2 * u], bf[s2][1][2 * u + 1]});
+              c0[u] = codes_to_bf16(u32x2{b0[2 * u], b0[2 * u + 1]});
+              c1[u] = codes_to_bf16(u32x2{b1[2 * u], b1[2 * u + 1]});
             }
 #pragma unroll
             for (int ms = 0; ms < NSUB; ms++)
 #pragma unroll
               for (int u = 0; u < 2; u++) {
-                acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ms][u][0], c0[u], acc[ms][0], 0, 0, 0);
-                acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ms][u][0], c1[u], acc[ms][1], 0, 0, 0);
-                acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ms][u][1], c0[u], acc[ms][0], 0, 0, 0);
-                acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ms][u][1], c1[u], acc[ms][1], 0, 0, 0);
-                if (s2 == 0) read_a(1, ms, u);
-                __builtin_amdgcn_sched_barrier(0);
+                const int m = 32 * ms + l32;
+                const int ch = 4 * s2 + 2 * half + u;  // A chunk (8 columns) within the half-stage
+                const bf16x8 ah = *(const bf16x8 *)&sm.u.t.A[a][0][m][8 * (ch ^ pf_swz(m))];
+                const bf16x8 al = *(const bf16x8 *)&sm.u.t.A[a][1][m][8 * (ch ^ pf_swz(m))];
+                acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, c0[u], acc[ms][0], 0, 0, 0);
+                acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, c1[u], acc[ms][1], 0, 0, 0);
+                acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, c0[u], acc[ms][0], 0, 0, 0);
+                acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, c1[u], acc[ms][1], 0, 0, 0);
               }
           }
         }
@@ -551,6 +594,9 @@ __device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item
   const size_t rbase = SHARED ? (size_t)it.m0 : (size_t)(it.pos0 + it.m0);
   // The tile's h values (as the down GEMM sees them, hi + lo) also go to LDS for the row sums
   // Σh over the block's 128 units, which the down epilogue needs for the offset term.
+  // The tile's h values go to LDS (per wave: 64 rows x its 32 units), from where each lane stores
+  // 16-byte runs of 8 units (hi and lo) and sums a row for Σh (over the block's 128 units, for the
+  // down epilogue's offset term; summed as the down GEMM sees the values, hi + lo).
   float(*red)[64][33] = sm.u.red;
   __syncthreads();  // every wave is done with the main loop's tiles
 #pragma unroll
@@ -558,7 +604,7 @@ __device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item
 #pragma unroll
     for (int j = 0; j < 16; j++) {
       const int m = ms * 32 + mfma_row(lane, j);
-      float hsum_v = 0.0f;
+      float hv = 0.0f;
       if (m < it.mcnt) {
         const float xs = sm.xs[m];
         float g = __builtin_fmaf(sog.x, acc[ms][0][j], sog.y * xs);
@@ -567,23 +613,40 @@ __device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item
           g = dsh_bf16_round_half_up(g);
           up = dsh_bf16_round_half_up(up);
         }
-        float hv = dsh_swiglu(g, up);
+        hv = dsh_swiglu(g, up);
         if (bf16sim) hv = dsh_bf16_round_half_up(hv);
-        const size_t row = rbase + m;
-        const __bf16 hi = (__bf16)hv, lo = (__bf16)(hv - (float)hi);
-        Hhi[row * Iseg + unit] = hi;
-        Hlo[row * Iseg + unit] = lo;
-        hsum_v = (float)hi + (float)lo;
       }
-      red[wave][m][l32] = hsum_v;
+      red[wave][m][l32] = hv;
     }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  {  // stores: lane → rows (lane / 4) + 16k, units 8·(lane % 4) .. +7 of the wave's 32
+    const int g8 = 8 * (lane & 3);
+#pragma unroll
+    for (int k = 0; k < 2 * NSUB; k++) {
+      const int m = (lane >> 2) + 16 * k;
+      if (m >= it.mcnt) continue;
+      bf16x8 hi8, lo8;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const float hv = red[wave][m][g8 + i];
+        hi8[i] = (__bf16)hv;
+        lo8[i] = (__bf16)(hv - (float)hi8[i]);
+      }
+      const size_t o = (rbase + m) * Iseg + u0 + g8;
+      *(bf16x8 *)(Hhi + o) = hi8;
+      *(bf16x8 *)(Hlo + o) = lo8;
+    }
+  }
   float part = 0.0f;  // lane = row: its sum over the wave's 32 units, in unit order
   if (lane < 32 * NSUB) {
 #pragma unroll 8
-    for (int u = 0; u < 32; u++) part += red[wave][lane][u];
+    for (int u = 0; u < 32; u++) {
+      const float hv = red[wave][lane][u];
+      const __bf16 hi = (__bf16)hv;
+      part += (float)hi + (float)(__bf16)(hv - (float)hi);
+    }
   }
   sm.hsum[wave][lane >> 5][lane & 31] = part;
   __syncthreads();
@@ -648,8 +711,10 @@ __device__ __forceinline__ void down_tile(const dsh_layer_t &L, const pf_item &i
   {  // lane = row of the block: Σh from the gate_up partials (each wave for itself)
     float hs = 0.0f;
     if (lane < it.mcnt) {
+      // agent-scope atomic loads read the partials at L2 (in the fused kernel other CUs of this
+      // XCD wrote them, and lines of this CU's L1 may mix them with older data)
       const float *hp = hpart + (rbase + lane) * ntK;
-      for (int k = 0; k < ntK; k++) hs += hp[k];
+      for (int k = 0; k < ntK; k++) hs += __hip_atomic_load(hp + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     sm.hsum[wave][half][l32] = hs;
   }
@@ -695,6 +760,74 @@ __global__ void __launch_bounds__(256, PF_OCC) k_pf_down(dsh_layer_t L, const pf
     down_dispatch<true>(L, it, nt, Shi, Slo, hps, Ysh, sm);
   else
     down_dispatch<false>(L, it, nt, Hhi, Hlo, hpr, Y, sm);
+}
+
+// Fused grouped GEMM: one launch runs every gate_up and down tile, one tile per block. A block
+// serves the work queue of its own XCD (hardware XCC id) and claims the queue's next tile; the
+// grid holds more blocks per XCD than any queue has tiles, and blocks that find their queue empty
+// exit. A queue lists all its gate_up tiles, then its down tiles; a down tile needs all gate_up
+// tiles of its item, which sit earlier in the same queue: they were claimed by blocks that run
+// (blocks are dispatched in order, so they are resident or done) and wait on nothing, so the
+// down block's bounded wait always ends. As gate_up tiles finish, down tiles start in their place
+// (no tail between the two projections). Coherence is XCD-local: a gate_up block drains its stores
+// to the XCD's L2 (vmcnt(0) in every thread, then a barrier) before one thread bumps the item's
+// counter with an L2 atomic; the down block reads the counter at L2, and the h rows it then loads
+// were written by this XCD (each 128-byte line by one block) and never read here before. Claim
+// counters and item counters are zeroed by the plan kernel.
+#define PF_SPIN_MAX (1 << 22)
+#define PF_PROBE 4096  // blocks of the XCD placement check
+__global__ void __launch_bounds__(256, PF_OCC) k_pf_moe(dsh_layer_t L, const pf_item *__restrict__ items,
+                                                    pf_queues Q, const __bf16 *Xhi, const __bf16 *Xlo,
+                                                    const float *__restrict__ xsum, const int *__restrict__ pair_tok,
+                                                    int bf16sim, __bf16 *Hhi, __bf16 *Hlo, __bf16 *Shi, __bf16 *Slo,
+                                                    float *hpr, float *hps, float *__restrict__ Y,
+                                                    float *__restrict__ Ysh) {
+  __shared__ __attribute__((aligned(16))) pf_smem sm;
+  __shared__ int s_tile;
+  unsigned xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  const int q = xcc & (PF_NQ - 1);
+  if (threadIdx.x == 0) s_tile = __hip_atomic_fetch_add(Q.next + q, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const int t = s_tile;
+  if (t >= Q.count[q]) return;
+  const unsigned d = (unsigned)Q.tiles[(size_t)q * Q.cap + t];
+  const int item = (int)((d & ~PF_DN_TILE) >> 8), nt = (int)(d & 255);
+  const pf_item it = items[item];
+  if (!(d & PF_DN_TILE)) {
+    if (it.seg == L.E)
+      gate_up_dispatch<true>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Shi, Slo, hps, sm);
+    else
+      gate_up_dispatch<false>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Hhi, Hlo, hpr, sm);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's h stores are in L2
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(Q.gu_done + item, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    if (threadIdx.x == 0) {
+      const int need = it.seg == L.E ? L.SI / PF_GU_N : L.I / PF_GU_N;
+      int spins = 0;
+      while (__hip_atomic_load(Q.gu_done + item, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
+        if (++spins > PF_SPIN_MAX) {
+          __hip_atomic_store(Q.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    __syncthreads();
+    if (it.seg == L.E)
+      down_dispatch<true>(L, it, nt, Shi, Slo, hps, Ysh, sm);
+    else
+      down_dispatch<false>(L, it, nt, Hhi, Hlo, hpr, Y, sm);
+  }
+}
+
+// XCC id of each block, to check that a grid's blocks cover all PF_NQ XCDs before the fused kernel
+// is used.
+__global__ void __launch_bounds__(64) k_pf_xcc_probe(int *__restrict__ out) {
+  unsigned xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  if (threadIdx.x == 0) out[blockIdx.x] = (int)xcc;
 }
 
 // ---------------------------------------------------------------------------------- combine
@@ -771,6 +904,7 @@ struct pf_ws {
   float *ps;        // [T][4][64] partial router scores
   float *hpr, *hps; // Σh partials per (row, gate_up n-tile): routed [TK][I/128], shared [T][SI/128]
   int *tiles_gu, *tiles_dn;  // routed GEMM tiles (item << 8 | n-tile) in launch order
+  int *qtiles, *qcount, *qnext, *gu_done, *err;  // fused kernel: work queues, counters, wait error
 };
 
 size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -783,6 +917,16 @@ int pf_grid(const dsh_layer_t *L, int T, int ntS, int ntR) {
   const int n = pf_shared_items(T) * ntS + pf_max_routed_items(L, T) * ntR;
   return (n + 7) & ~7;
 }
+
+// Tiles one fused-kernel queue can hold: every gate_up and down tile of the largest work list.
+size_t pf_queue_cap(const dsh_layer_t *L, int T) {
+  const size_t r = pf_max_routed_items(L, T), sh = pf_shared_items(T);
+  return r * (L->I / PF_GU_N) + sh * (L->SI / PF_GU_N) + (r + sh) * (L->H / PF_DN_N);
+}
+
+int g_pf_xcd_min = 0;  // fewest blocks any XCD received out of a probe grid of PF_PROBE blocks
+int g_pf_auto = -1;   // -1 unchecked, 1 the grid's blocks cover all PF_NQ XCDs, 0 not
+int g_pf_fused = -1;  // path in use
 
 // Carves the workspace; returns its size (ws may be NULL to size it).
 size_t pf_carve(const dsh_layer_t *L, int T, void *base, pf_ws *w) {
@@ -815,6 +959,11 @@ size_t pf_carve(const dsh_layer_t *L, int T, void *base, pf_ws *w) {
   TAKE(hps, float, (size_t)T * (SI / PF_GU_N));
   TAKE(tiles_gu, int, (size_t)pf_max_routed_items(L, T) * (I / PF_GU_N));
   TAKE(tiles_dn, int, (size_t)pf_max_routed_items(L, T) * (H / PF_DN_N));
+  TAKE(qtiles, int, (size_t)PF_NQ * pf_queue_cap(L, T));
+  TAKE(qcount, int, PF_NQ);
+  TAKE(qnext, int, PF_NQ);
+  TAKE(gu_done, int, pf_max_routed_items(L, T) + pf_shared_items(T));
+  TAKE(err, int, 1);
 #undef TAKE
   return off;
 }
@@ -831,6 +980,53 @@ int dsh_pf_supported(const dsh_layer_t *L) {
 }
 
 size_t dsh_pf_workspace_bytes(const dsh_layer_t *L, int T) { return pf_carve(L, T, NULL, NULL); }
+
+// Checks, once, that a grid's blocks are dealt evenly over all PF_NQ XCDs (each XCD's work queue is
+// served only by its own blocks); otherwise the two-kernel path is used.
+// Synchronous: call outside stream capture. force: 1 fused, 0 two kernels, -1 decide by the check,
+// -2 only make sure the check has run (keeps a path chosen earlier).
+hipError_t dsh_pf_init(int force) {
+  if (g_pf_auto < 0) {
+    int *d = NULL;
+    hipError_t e = hipMalloc(&d, sizeof(int) * PF_PROBE);
+    if (e != hipSuccess) return e;
+    k_pf_xcc_probe<<<PF_PROBE, 64>>>(d);
+    int *h = (int *)malloc(sizeof(int) * PF_PROBE);
+    e = hipGetLastError();
+    if (e == hipSuccess && h) e = hipMemcpy(h, d, sizeof(int) * PF_PROBE, hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    int per[PF_NQ] = {0}, bad = 0;
+    if (e == hipSuccess && h)
+      for (int i = 0; i < PF_PROBE; i++) {
+        if (h[i] >= 0 && h[i] < PF_NQ)
+          per[h[i]]++;
+        else
+          bad = 1;
+      }
+    free(h);
+    if (e != hipSuccess) return e;
+    g_pf_xcd_min = PF_PROBE;
+    for (int q = 0; q < PF_NQ; q++) g_pf_xcd_min = per[q] < g_pf_xcd_min ? per[q] : g_pf_xcd_min;
+    // the fused launch gives each XCD its share of a grid sized for the longest queue: blocks
+    // must be dealt evenly over all PF_NQ XCDs
+    g_pf_auto = g_pf_fused = !bad && g_pf_xcd_min * PF_NQ >= PF_PROBE - PF_NQ ? 1 : 0;
+  }
+  if (force >= 0)
+    g_pf_fused = force ? 1 : 0;
+  else if (force == -1 || g_pf_fused < 0)
+    g_pf_fused = g_pf_auto;
+  return hipSuccess;
+}
+
+int dsh_pf_fused(void) { return g_pf_fused == 1; }
+
+int dsh_pf_wait_error(const void *ws, const dsh_layer_t *L, int T) {
+  pf_ws w;
+  pf_carve(L, T, (void *)ws, &w);
+  int v = 0;
+  if (hipMemcpy(&v, w.err, sizeof v, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+  return v;
+}
 
 hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int route_mode, int nthreads, int residual,
                               int bf16sim, float *out, void *ws, int *idx_out, float *w_out, hipStream_t s) {
@@ -854,13 +1050,25 @@ hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int r
     k_pf_select<DSH_ROUTE_DECODE><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, w.Xhi, w.Xlo, w.xsum, w.idx,
                                                                 w.w);
   }
+  const int n_items_max = pf_max_routed_items(L, T) + pf_shared_items(T);
+  const bool fused = g_pf_fused == 1 && n_items_max < (1 << 22);
+  pf_queues Q{w.qtiles, w.qcount, w.qnext, w.gu_done, w.err, (int)pf_queue_cap(L, T), L->I / PF_GU_N, L->SI / PF_GU_N,
+              H / PF_DN_N, H / PF_KS, L->I / PF_KS, L->SI / PF_KS, fused ? 1 : 0};
   k_pf_plan<<<1, 1024, 0, s>>>(w.idx, T, K, E, L->I / PF_GU_N, H / PF_DN_N, w.seg_off, w.items, w.counts,
-                               w.tiles_gu, w.tiles_dn, w.pair_tok, w.pos_of);
-  k_pf_gate_up<<<pf_grid(L, T, L->SI / PF_GU_N, L->I / PF_GU_N), 256, 0, s>>>(
-      *L, w.items, w.counts, w.Xhi, w.Xlo, w.xsum, w.pair_tok, bf16sim, w.Hhi, w.Hlo, w.Shi, w.Slo, w.hpr, w.hps,
-      w.tiles_gu);
-  k_pf_down<<<pf_grid(L, T, H / PF_DN_N, H / PF_DN_N), 256, 0, s>>>(*L, w.items, w.counts, w.Hhi, w.Hlo, w.Shi,
-                                                                     w.Slo, w.hpr, w.hps, w.Y, w.Ysh, w.tiles_dn);
+                               w.tiles_gu, w.tiles_dn, w.pair_tok, w.pos_of, Q);
+  if (fused) {
+    // blocks per XCD >= tiles of the longest queue (at most ceil(items / PF_NQ) items)
+    const int per_item = max(L->I / PF_GU_N, L->SI / PF_GU_N) + H / PF_DN_N;
+    const int blocks = PF_NQ * ((n_items_max + PF_NQ - 1) / PF_NQ) * per_item;
+    k_pf_moe<<<blocks, 256, 0, s>>>(*L, w.items, Q, w.Xhi, w.Xlo, w.xsum, w.pair_tok, bf16sim, w.Hhi,
+                                         w.Hlo, w.Shi, w.Slo, w.hpr, w.hps, w.Y, w.Ysh);
+  } else {
+    k_pf_gate_up<<<pf_grid(L, T, L->SI / PF_GU_N, L->I / PF_GU_N), 256, 0, s>>>(
+        *L, w.items, w.counts, w.Xhi, w.Xlo, w.xsum, w.pair_tok, bf16sim, w.Hhi, w.Hlo, w.Shi, w.Slo, w.hpr, w.hps,
+        w.tiles_gu);
+    k_pf_down<<<pf_grid(L, T, H / PF_DN_N, H / PF_DN_N), 256, 0, s>>>(*L, w.items, w.counts, w.Hhi, w.Hlo, w.Shi,
+                                                                       w.Slo, w.hpr, w.hps, w.Y, w.Ysh, w.tiles_dn);
+  }
   k_pf_combine<<<T, 256, 0, s>>>(X, w.idx, w.w, w.pos_of, w.Y, w.Ysh, H, K, residual, bf16sim, out);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess && idx_out)

@@ -28,7 +28,7 @@ struct ds_hip_layer {
   hipGraphExec_t pf_exec;
   struct pf_key {
     const void *out, *x, *ws, *idx, *w;
-    int T, mode, residual, bf16sim, threads;
+    int T, mode, residual, bf16sim, threads, fused;
   } pf_key;
 };
 
@@ -313,6 +313,7 @@ int ds_hip_layer_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
   if (!dsh_pf_supported(&L->d))
     return dsr_failf("ds_hip_layer_prefill: shape H=%d I=%d SI=%d not supported (needs H %% 256 == 0, I and SI %% 128 == 0)",
                      L->H, L->I, L->SI);
+  DSR_TRY(dsh_pf_init(-2), "prefill init");
   void *ws = dsr_scratch(DSR_SLOT_PF, dsh_pf_workspace_bytes(&L->d, T));
   if (!ws) return -1;
   struct pf_key key;
@@ -327,6 +328,7 @@ int ds_hip_layer_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
   key.residual = residual;
   key.bf16sim = ds_bf16_simulate_python;
   key.threads = dsr_threads();
+  key.fused = dsh_pf_fused();
   if (!L->pf_exec || memcmp(&key, &L->pf_key, sizeof key) != 0) {
     /* the seven kernels (and the idx/w copies) captured once, then one graph launch per call */
     if (L->pf_exec) {
@@ -352,6 +354,24 @@ int ds_hip_layer_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
   }
   DSR_TRY(hipGraphLaunch(L->pf_exec, dsr_stream), "prefill graph launch");
   return 0;
+}
+
+/* Prefill GEMM path: 1 the fused persistent kernel, 0 the two-kernel path, -1 automatic (fused when
+ * a grid's blocks cover every XCD). Returns the path now in use (or -1 on error). */
+int ds_hip_prefill_path(int mode) {
+  if (dsr_init()) return -1;
+  if (dsh_pf_init(mode < 0 ? -1 : mode) != hipSuccess) return dsr_failf("ds_hip_prefill_path: init failed");
+  return dsh_pf_fused();
+}
+
+/* After a prefill call of T tokens on layer L: 1 if the fused kernel's bounded wait expired (the
+ * output is then not valid), 0 if not. Synchronises the library stream. */
+int ds_hip_prefill_wait_error(ds_hip_layer_t *L, int T) {
+  if (!L || T <= 0) return dsr_failf("ds_hip_prefill_wait_error: invalid arguments");
+  DSR_TRY(hipStreamSynchronize(dsr_stream), "sync");
+  void *ws = dsr_scratch(DSR_SLOT_PF, dsh_pf_workspace_bytes(&L->d, T));
+  if (!ws) return -1;
+  return dsh_pf_wait_error(ws, &L->d, T);
 }
 
 /* Average device time of n back-to-back prefill calls (HIP events on the library stream). */

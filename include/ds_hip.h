@@ -88,6 +88,15 @@ int ds_hip_layer_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
 /* Average device time (ms) of n back-to-back ds_hip_layer_prefill calls (no residual). */
 int ds_hip_time_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, int T, int route_mode, int n, float *ms);
 
+/* Prefill GEMM path (no counterpart in the reference): 1 = one persistent kernel with a work queue
+ * per XCD, 0 = separate gate_up and down kernels, -1 = automatic (persistent when a grid's blocks
+ * cover every XCD). Returns the path in use, -1 on error. */
+int ds_hip_prefill_path(int mode);
+
+/* After a prefill call of T tokens on L: 1 if the persistent kernel's bounded wait for a gate_up
+ * tile expired (that call's output is not valid), 0 if not, -1 on error. Synchronises. */
+int ds_hip_prefill_wait_error(ds_hip_layer_t *L, int T);
+
 /* ---------------- decode stack: n MoE layers + argmax LM head ---------------- */
 typedef struct ds_hip_stack ds_hip_stack_t;
 

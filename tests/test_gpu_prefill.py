@@ -19,6 +19,18 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-3
 
 
+@pytest.fixture(params=[1, 0], ids=["fused", "two_kernels"])
+def path(request, dev):
+    """Runs a test on both prefill GEMM paths (the persistent kernel only where the device supports
+    it), then restores the automatic choice."""
+    L = dev.load()
+    if request.param == 1 and L.ds_hip_prefill_path(-1) != 1:
+        pytest.skip("persistent prefill kernel not available on this device")
+    assert L.ds_hip_prefill_path(request.param) == request.param
+    yield request.param
+    L.ds_hip_prefill_path(-1)
+
+
 def gpu_prefill(dev, h, X, mode, residual=0, K=6):
     L = dev.load()
     T = X.shape[0]
@@ -28,6 +40,7 @@ def gpu_prefill(dev, h, X, mode, residual=0, K=6):
     wd = dev.DeviceBuffer(4 * T * K)
     dev.check(L.ds_hip_layer_prefill(h, od.ptr, xd.ptr, T, mode, residual, idd.ptr, wd.ptr), "prefill")
     dev.check(L.ds_hip_sync(), "sync")
+    assert L.ds_hip_prefill_wait_error(h, T) == 0
     return (od.to_array(np.float32).reshape(X.shape), idd.to_array(np.int32).reshape(T, K),
             wd.to_array(np.float32).reshape(T, K))
 
@@ -59,7 +72,7 @@ def check_routing(B, lay, X, idx, w, mode):
 
 @pytest.mark.parametrize("T", [1, 5, 64, 130])
 @pytest.mark.parametrize("mode", [0, 1])
-def test_prefill_small_layer(dev, B, mode, T):
+def test_prefill_small_layer(dev, B, mode, T, path):
     L = dev.load()
     lay = B.make_moe_layer(61, hidden=256, inter=128, n_experts=16)
     h = upload_layer(dev, lay)
@@ -96,7 +109,7 @@ def test_prefill_one_token_equals_decode(dev, B, mode):
         L.ds_hip_layer_destroy(h)
 
 
-def test_prefill_residual(dev, B):
+def test_prefill_residual(dev, B, path):
     L = dev.load()
     lay = B.make_moe_layer(63, hidden=256, inter=128, n_experts=16)
     h = upload_layer(dev, lay)
@@ -124,7 +137,7 @@ def test_prefill_rejects_unsupported_shape(dev, B):
         L.ds_hip_layer_destroy(h)
 
 
-def test_prefill_config3(dev, B):
+def test_prefill_config3(dev, B, path):
     """Config 3: 662 tokens through one config-2 layer (f32 router, renormalised top-6). Routing is
     checked for every token, the block output against the f64 oracle on 24 sampled tokens."""
     L = dev.load()
