@@ -39,7 +39,7 @@ __device__ __forceinline__ void load_f16x(const float *p, float *o) {
 // route_load issues the ROUTE_BATCH partial loads of each wave (rows wave, wave+4, ...; at most
 // 4 * ROUTE_BATCH partials, checked by dsh_dec_supported), route_reduce sums them in that order
 // and stores the wave sums, and
-// route_select (wave 0) adds the four wave sums in wave order and selects the experts
+// route_select (every wave, for itself) adds the four wave sums in wave order and selects the experts
 // (same semantics as k_core.hip's top-k helpers). Results in s_idx/s_w (LDS), visible after the
 // next barrier.
 #define ROUTE_BATCH 40
@@ -126,7 +126,7 @@ __global__ void __launch_bounds__(64) k_dec_scores_bf16(const uint16_t *__restri
 template <int CPL>
 __device__ __forceinline__ void gate_up_body(const dsh_layer_t &L, const float *x, const float *partials, int np,
                                              int mode, int bf16sim, const dsh_layer_work_t &wk, int blk, int *s_idx,
-                                             float *s_w, float (*s_red)[64], float *s_x) {
+                                             float *s_w, float (*s_red)[64], route_scratch *s_scr, float *s_x) {
   constexpr int XV = (64 * CPL + 255) / 256;  // 16-byte pieces of x per thread
   const int H = L.H, I = L.I, K = L.K, SI = L.SI;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane & 15, grp = lane >> 4;
@@ -159,8 +159,10 @@ __device__ __forceinline__ void gate_up_body(const dsh_layer_t &L, const float *
   }
   route_reduce(np, L.E, pv, s_red);
   __syncthreads();  // s_red, s_x
-  if (wave == 0) route_select(L.E, K, mode, s_idx, s_w, s_red);
-  __syncthreads();  // s_idx, s_w
+  // every wave selects the experts itself (identical results), so no second barrier is needed
+  route_select(L.E, K, mode, s_idx + 64 * wave, s_w + 64 * wave, s_red, s_scr + wave);
+  s_idx += 64 * wave;
+  s_w += 64 * wave;
 
   const int ru = blk * 12 + wave * 3 + max(grp - 1, 0);
   const int r = ru < KI ? ru : 0;
@@ -221,7 +223,7 @@ __device__ __forceinline__ void gate_up_body(const dsh_layer_t &L, const float *
     }
     if (dst) *dst = val;
   }
-  if (blk == 0 && threadIdx.x < K) {  // block 0 publishes the routing (read by the host API)
+  if (blk == 0 && threadIdx.x < K) {  // block 0 (wave 0) publishes the routing (read by the host API)
     wk.idx[threadIdx.x] = s_idx[threadIdx.x];
     wk.w[threadIdx.x] = s_w[threadIdx.x];
   }
@@ -231,12 +233,13 @@ template <int CPL>
 __global__ void __launch_bounds__(256) k_dec_gate_up(dsh_layer_t L, const float *x_in, const int *__restrict__ step,
                                                      int stride, const float *partials, int np, int mode, int bf16sim,
                                                      dsh_layer_work_t wk) {
-  __shared__ int s_idx[64];
-  __shared__ float s_w[64];
+  __shared__ int s_idx[4 * 64];
+  __shared__ float s_w[4 * 64];
   __shared__ float s_red[4][64];
+  __shared__ route_scratch s_scr[4];
   __shared__ __attribute__((aligned(16))) float s_x[256 * CPL];
   gate_up_body<CPL>(L, at_step(x_in, step, stride), partials, np, mode, bf16sim, wk, blockIdx.x, s_idx, s_w, s_red,
-                    s_x);
+                    s_scr, s_x);
 }
 
 // ============================================================================ down + combine
