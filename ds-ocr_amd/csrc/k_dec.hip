@@ -114,97 +114,147 @@ __global__ void __launch_bounds__(64) k_dec_scores_bf16(const uint16_t *__restri
 
 // ============================================================================ gate_up + SwiGLU
 // A unit is one row pair (gate row, up row) handled by 16 lanes; lane sub reads the 16-byte chunks
-// sub + 16m (m < CPL) of both rows (H == 256*CPL). Block b, wave w: lanes 0-15 take shared-expert
-// unit 4b+w (rows u and SI+u), lanes 16-63 take routed units 12b+3w+0..2 of the K*I routed ones
-// (slot k = u/I, intermediate i = u%I). Every lane issues the same loads in the same order: x,
-// the routing partials and the shared rows first (lanes 16-63 repeat lanes 0-15's shared addresses,
-// which the wave's load coalesces), the routed rows after the routing (lanes 0-15 repeat lanes
-// 16-31's). With no load or store under a branch, every wait covers exactly the loads it needs.
-// x is staged once per block in LDS; all stores happen at the end. The empty asm statements keep
-// the compiler from reordering the three load groups (x and partials are not __restrict__ so that
-// they cannot be moved across them).
+// sub + 16m (m < CPL) of both rows (H == 256*CPL). Block b: wave 0 takes the shared expert's units
+// 4b + g (lane group g = lane / 16; rows u and SI + u), waves 1-3 the routed units 12b + 4(w-1) + g
+// of the K*I routed ones (slot k = u/I, intermediate i = u%I). The shared wave loads its rows at
+// once and never routes; the routed waves select the experts (each for itself) and then load.
+//
+// The dots run on the integer dot unit: x is split once per block into four signed 8-bit limbs,
+// X = rint(x * 2^(29-e)) = L3*2^24 + L2*2^16 + L1*2^8 + L0 with 2^e > max|x| (|X| <= 2^29, so L3
+// fits), and a row's dot is sum_j q_j X_j (q = u - 128, the stored signed code) in int32 per limb,
+// scaled back by 2^(e-29). X is exact for every x_j within 2^6 of max|x| (a 24-bit mantissa fits in
+// 30 bits); smaller ones are rounded by at most 2^(e-30), far below the f32 rounding of a dot. The
+// products and sums are exact; the only rounding is the final f32 combination of the limb sums. The +128 of
+// the unsigned codes moves into the offset term: scale*Σu*x + off*Σx = scale*Σq*x + (off +
+// 128*scale)*Σx (ds_quantize.c:163-166), with Σx summed once per block.
+// Every lane of a wave issues the same loads in the same order (x, the routing partials, then its
+// rows); all stores happen at the end. The empty asm statements keep the compiler from reordering
+// the load groups (x and partials are not __restrict__ so that they cannot be moved across them).
 template <int CPL>
 __device__ __forceinline__ void gate_up_body(const dsh_layer_t &L, const float *x, const float *partials, int np,
                                              int mode, int bf16sim, const dsh_layer_work_t &wk, int blk, int *s_idx,
-                                             float *s_w, float (*s_red)[64], route_scratch *s_scr, float *s_x) {
+                                             float *s_w, float (*s_red)[64], route_scratch *s_scr, float *s_stat,
+                                             unsigned *s_lq) {
   constexpr int XV = (64 * CPL + 255) / 256;  // 16-byte pieces of x per thread
+  constexpr int NP = 64 * CPL;                // pieces (4 elements) of x, = words per limb array
+  constexpr int NL = 4;                       // limbs
   const int H = L.H, I = L.I, K = L.K, SI = L.SI;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane & 15, grp = lane >> 4;
   const int KI = K * I;
+  const bool shared_wave = wave == 0;
 
   f32x4 xr[XV];
 #pragma unroll
-  for (int j = 0; j < XV; j++) xr[j] = ((const f32x4 *)x)[min((int)threadIdx.x + 256 * j, 64 * CPL - 1)];
+  for (int j = 0; j < XV; j++) xr[j] = ((const f32x4 *)x)[min((int)threadIdx.x + 256 * j, NP - 1)];
   asm volatile("" ::: "memory");  // keeps the issue order: x, partials, shared rows
   float pv[ROUTE_BATCH];
   route_load(partials, np, pv);
   asm volatile("" ::: "memory");
-  const int su = blk * 4 + wave;
+  const int su = blk * 4 + grp;
   const int suc = su < SI ? su : 0;
-  u32x4 sg[CPL], sup[CPL];
-  {
+  u32x4 wg[CPL], wu[CPL];
+  if (shared_wave) {
     const int8_t *grow = L.sgu_q + (size_t)suc * H;
     const int8_t *urow = L.sgu_q + (size_t)(SI + suc) * H;
 #pragma unroll
     for (int m = 0; m < CPL; m++) {
-      sg[m] = dsh_load_nt(grow + 16 * (sub + 16 * m));
-      sup[m] = dsh_load_nt(urow + 16 * (sub + 16 * m));
+      wg[m] = dsh_load_nt(grow + 16 * (sub + 16 * m));
+      wu[m] = dsh_load_nt(urow + 16 * (sub + 16 * m));
     }
   }
   asm volatile("" ::: "memory");
+  {  // max|x| and Σx of the pieces this thread owns (clamped duplicates skipped), per wave
+    float mx = 0.0f, sx = 0.0f;
 #pragma unroll
-  for (int j = 0; j < XV; j++) {
-    const int t = min((int)threadIdx.x + 256 * j, 64 * CPL - 1);  // duplicate stores of the same value
-    ((f32x4 *)s_x)[t] = xr[j];
+    for (int j = 0; j < XV; j++) {
+      const bool own = (int)threadIdx.x + 256 * j < NP;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        mx = own ? fmaxf(mx, fabsf(xr[j][c])) : mx;
+        sx += own ? xr[j][c] : 0.0f;
+      }
+    }
+    mx = dsh_wave_max(mx);
+    sx = dsh_wave_sum(sx);
+    if (lane == 0) {
+      s_stat[wave] = mx;
+      s_stat[4 + wave] = sx;
+    }
   }
   route_reduce(np, L.E, pv, s_red);
-  __syncthreads();  // s_red, s_x
-  // every wave selects the experts itself (identical results), so no second barrier is needed
-  route_select(L.E, K, mode, s_idx + 64 * wave, s_w + 64 * wave, s_red, s_scr + wave);
-  s_idx += 64 * wave;
-  s_w += 64 * wave;
+  __syncthreads();  // s_red, s_stat
+  const float xmax = fmaxf(fmaxf(s_stat[0], s_stat[1]), fmaxf(s_stat[2], s_stat[3]));
+  const float xsum = ((s_stat[4] + s_stat[5]) + s_stat[6]) + s_stat[7];
+  const int ex = __builtin_amdgcn_frexp_expf(xmax);  // xmax < 2^ex
 
-  const int ru = blk * 12 + wave * 3 + max(grp - 1, 0);
-  const int r = ru < KI ? ru : 0;
-  const int k = r / I, i = r - k * I;
-  const int e = s_idx[k];
-  const size_t base = (size_t)max(e, 0) * 2 * I;
-  u32x4 rg[CPL], rup[CPL];
-  {
+  int ru = 0, r = 0, e = 0;
+  float2 sog, sou;
+  if (!shared_wave) {
+    route_select(L.E, K, mode, s_idx + 64 * wave, s_w + 64 * wave, s_red, s_scr + wave);
+    s_idx += 64 * wave;
+    s_w += 64 * wave;
+    ru = blk * 12 + (wave - 1) * 4 + grp;
+    r = ru < KI ? ru : 0;
+    const int k = r / I, i = r - k * I;
+    e = s_idx[k];
+    const size_t base = (size_t)max(e, 0) * 2 * I;
     const int8_t *grow = L.gu_q + (base + i) * H;
     const int8_t *urow = L.gu_q + (base + I + i) * H;
 #pragma unroll
     for (int m = 0; m < CPL; m++) {
-      rg[m] = dsh_load_nt(grow + 16 * (sub + 16 * m));
-      rup[m] = dsh_load_nt(urow + 16 * (sub + 16 * m));
+      wg[m] = dsh_load_nt(grow + 16 * (sub + 16 * m));
+      wu[m] = dsh_load_nt(urow + 16 * (sub + 16 * m));
     }
+    sog = so_pair(L.gu_so, base + i);
+    sou = so_pair(L.gu_so, base + I + i);
+  } else {
+    sog = so_pair(L.sgu_so, suc);
+    sou = so_pair(L.sgu_so, SI + suc);
   }
-  const bool is_shared = grp == 0;
-  const float2 sog = is_shared ? so_pair(L.sgu_so, suc) : so_pair(L.gu_so, base + i);
-  const float2 sou = is_shared ? so_pair(L.sgu_so, SI + suc) : so_pair(L.gu_so, base + I + i);
-  float xpart = 0.0f, dg = 0.0f, du = 0.0f;
+  // x → limbs, piece p (elements 4p..4p+3) into word p of each limb array
+#pragma unroll
+  for (int j = 0; j < XV; j++) {
+    const int p = min((int)threadIdx.x + 256 * j, NP - 1);  // duplicates store identical words
+    unsigned wl[NL] = {};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      int X = (int)__builtin_rintf(__builtin_ldexpf(xr[j][c], 29 - ex));
+#pragma unroll
+      for (int l = 0; l < NL; l++) {
+        const int d = l < NL - 1 ? __builtin_amdgcn_sbfe(X, 0, 8) : X;  // balanced digit; the top one is the rest
+        wl[l] |= ((unsigned)d & 255u) << (8 * c);
+        X = (X - d) >> 8;
+      }
+    }
+#pragma unroll
+    for (int l = 0; l < NL; l++) s_lq[l * NP + p] = wl[l];
+  }
+  __syncthreads();  // limbs
+  int ag[NL] = {}, au[NL] = {};  // |sum| <= 16*CPL * 128 * 128 < 2^21
 #pragma unroll
   for (int m = 0; m < CPL; m++) {
-    float xv[16];
-    load_f16x(s_x + 16 * (sub + 16 * m), xv);
-    float s = 0.0f;
+    const int c = sub + 16 * m;  // 16-element chunk = 4 words
 #pragma unroll
-    for (int j = 0; j < 16; j++) s += xv[j];
-    xpart += s;
-    u32x4 wg, wu;
+    for (int l = 0; l < NL; l++) {
+      const u32x4 lw = *(const u32x4 *)(s_lq + l * NP + 4 * c);
 #pragma unroll
-    for (int d = 0; d < 4; d++) {
-      wg[d] = is_shared ? sg[m][d] : rg[m][d];
-      wu[d] = is_shared ? sup[m][d] : rup[m][d];
+      for (int d = 0; d < 4; d++) {
+        ag[l] = __builtin_amdgcn_sdot4((int)wg[m][d], (int)lw[d], ag[l], false);
+        au[l] = __builtin_amdgcn_sdot4((int)wu[m][d], (int)lw[d], au[l], false);
+      }
     }
-    dg = dsh_dot16_u8(wg, xv, dg);
-    du = dsh_dot16_u8(wu, xv, du);
   }
-  const float xsum = dsh_row16_sum(xpart);
-  dg = dsh_row16_sum(dg);
-  du = dsh_row16_sum(du);
-  float g = __builtin_fmaf(sog.x, dg, sog.y * xsum);
-  float up = __builtin_fmaf(sou.x, du, sou.y * xsum);
+  float dg = (float)ag[NL - 1], du = (float)au[NL - 1];
+#pragma unroll
+  for (int l = NL - 2; l >= 0; l--) {
+    dg = __builtin_fmaf(dg, 256.0f, (float)ag[l]);
+    du = __builtin_fmaf(du, 256.0f, (float)au[l]);
+  }
+  dg = __builtin_ldexpf(dsh_row16_sum(dg), ex - 29);
+  du = __builtin_ldexpf(dsh_row16_sum(du), ex - 29);
+  const float og = __builtin_fmaf(128.0f, sog.x, sog.y), ou = __builtin_fmaf(128.0f, sou.x, sou.y);
+  float g = __builtin_fmaf(sog.x, dg, og * xsum);
+  float up = __builtin_fmaf(sou.x, du, ou * xsum);
   if (bf16sim) {
     g = dsh_bf16_round_half_up(g);
     up = dsh_bf16_round_half_up(up);
@@ -215,7 +265,7 @@ __device__ __forceinline__ void gate_up_body(const dsh_layer_t &L, const float *
   if (sub == 0) {
     float *dst = nullptr;
     float val = hv;
-    if (is_shared) {
+    if (shared_wave) {
       if (su < SI) dst = wk.h + KI + su;
     } else if (ru < KI) {
       dst = wk.h + r;
@@ -223,9 +273,9 @@ __device__ __forceinline__ void gate_up_body(const dsh_layer_t &L, const float *
     }
     if (dst) *dst = val;
   }
-  if (blk == 0 && threadIdx.x < K) {  // block 0 (wave 0) publishes the routing (read by the host API)
-    wk.idx[threadIdx.x] = s_idx[threadIdx.x];
-    wk.w[threadIdx.x] = s_w[threadIdx.x];
+  if (blk == 0 && wave == 1 && lane < K) {  // block 0 publishes the routing (read by the down kernel)
+    wk.idx[lane] = s_idx[lane];
+    wk.w[lane] = s_w[lane];
   }
 }
 
@@ -237,9 +287,10 @@ __global__ void __launch_bounds__(256) k_dec_gate_up(dsh_layer_t L, const float 
   __shared__ float s_w[4 * 64];
   __shared__ float s_red[4][64];
   __shared__ route_scratch s_scr[4];
-  __shared__ __attribute__((aligned(16))) float s_x[256 * CPL];
+  __shared__ float s_stat[8];
+  __shared__ __attribute__((aligned(16))) unsigned s_lq[4 * 64 * CPL];
   gate_up_body<CPL>(L, at_step(x_in, step, stride), partials, np, mode, bf16sim, wk, blockIdx.x, s_idx, s_w, s_red,
-                    s_scr, s_x);
+                    s_scr, s_stat, s_lq);
 }
 
 // ============================================================================ down + combine
@@ -301,6 +352,14 @@ __global__ void __launch_bounds__(512) k_dec_down(dsh_layer_t L, const float *__
   float hv[16];
   load_f16x(wk.h + hbase + 16 * ch, hv);
   const float2 so = so_pair(seg < K ? L.dn_so : L.sdn_so, so_base + r0 + myrow);
+  // what the combine needs, issued with the loads above so that it costs no round trip after the
+  // barrier: the top-k weights, the shared expert's scale/offset and the residual of row r0 + lane % R
+  float cw[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) cw[k] = wk.w[min(k, K - 1)];
+  const int crow = r0 + (lane & (R - 1));
+  const float2 sso = so_pair(L.sdn_so, crow);
+  const float xres = x[crow];
 
   float hp = 0.0f;
   if (lane_on) {
@@ -325,23 +384,27 @@ __global__ void __launch_bounds__(512) k_dec_down(dsh_layer_t L, const float *__
   if (seg == 0) {
     float outv = 0.0f;
     if (lane < R) {
-      const int r = r0 + lane;
-      for (int k = 0; k < K; k++) {
-        float v = s_val[k][lane];
-        if (bf16sim) v = dsh_bf16_round_half_up(v);
-        outv = __builtin_fmaf(wk.w[k], v, outv);
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        if (k < K) {
+          float v = s_val[k][lane];
+          if (bf16sim) v = dsh_bf16_round_half_up(v);
+          outv = __builtin_fmaf(cw[k], v, outv);
+        }
       }
       float sdot = 0.0f, shs = 0.0f;
-      for (int k = K; k < 8; k++) {
-        sdot += s_val[k][lane];
-        shs += s_hs[k];
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        if (k >= K) {
+          sdot += s_val[k][lane];
+          shs += s_hs[k];
+        }
       }
-      float2 sso = so_pair(L.sdn_so, r);
       float sh = __builtin_fmaf(sso.x, sdot, sso.y * shs);
       if (bf16sim) sh = dsh_bf16_round_half_up(sh);
       outv = outv + sh;
-      float xo = residual ? x[r] + outv : outv;
-      x_out[r] = xo;
+      float xo = residual ? xres + outv : outv;
+      x_out[crow] = xo;
       s_x[lane] = xo;
     }
     if (WrT_next) {

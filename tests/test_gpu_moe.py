@@ -14,6 +14,12 @@ import golden_cases as G  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
+# bf16 simulation rounds gate/up, h and every expert output to bf16 (round half up on the bits). An
+# unrounded value that differs by ~1e-6 relative -- as any summation order other than the reference's
+# sequential f32 chain does, and that chain itself is ~1e-6 from the exact value -- crosses a rounding
+# boundary now and then, so a layer output agrees with the reference to a few bf16 ulps of the output
+# scale instead of to 1e-3 (measured over 40 seeds: at most 5.5e-3, about 1.4 ulps; 2^-6 = 4 ulps).
+TOL_BF16SIM = 2.0 ** -6
 
 
 def bits(a):
@@ -76,9 +82,10 @@ def test_small_layer_vs_oracle(dev, B, mode, sim):
                 assert np.abs(w - rw).max() < 1e-5
             err = rel_err(out, ro)
             print(f"small layer mode={mode} sim={sim} seed={s}: {err:.2e}")
-            assert err < TOL
+            tol = TOL_BF16SIM if sim else TOL
+            assert err < tol
             outr, _, _ = layer_forward(dev, h, x, mode, residual=1)
-            assert rel_err(outr, x + ro) < TOL
+            assert rel_err(outr, x + ro) < tol
     finally:
         dev.set_bf16sim(0)
         L.ds_hip_layer_destroy(h)
