@@ -99,6 +99,14 @@ SIGNATURES = {
     "ds_hip_stack_kernel_count": (C.c_int, [vp]),
     "ds_hip_stack_kernel_name": (C.c_char_p, [vp, C.c_int]),
     "ds_hip_profile_stack": (C.c_int, [vp, C.c_int, f32p]),
+    "ds_hip_safetensors_info": (C.c_int, [C.POINTER(C.c_char_p), C.c_int, C.c_char_p, C.POINTER(C.c_int),
+                                          C.POINTER(C.c_int64), C.c_int]),
+    "ds_hip_load_moe_layers": (C.c_int, [C.POINTER(C.c_char_p), C.c_int, C.c_int, C.c_int, C.c_int,
+                                         C.POINTER(vp)]),
+    "ds_hip_load_lm_head": (C.c_int, [C.POINTER(C.c_char_p), C.c_int, C.POINTER(vp), C.POINTER(C.c_int),
+                                      C.POINTER(C.c_int)]),
+    "ds_hip_arena_save": (C.c_int, [C.c_char_p, C.POINTER(vp), C.c_int, vp, C.c_int]),
+    "ds_hip_arena_load": (C.c_int, [C.c_char_p, C.POINTER(vp), C.c_int, C.POINTER(vp), C.POINTER(C.c_int)]),
 }
 
 # Data symbols (mode globals).

@@ -8,6 +8,7 @@
  * without any host round trip. The reference allocates every block separately
  * (ds_quantize.c:57-59) and gathers experts through ds_dec_layer_t.experts_int4[64].
  */
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -19,6 +20,7 @@ struct ds_hip_layer {
   int H, I, E, K, SI;
   void *arena;
   size_t bytes;
+  size_t wbytes; /* the weight regions 0-9: the arena's prefix that a saved arena holds */
   dsh_layer_t d;          /* device pointers into the arena */
   dsh_layer_work_t wk;    /* work buffers (in the arena) */
   float *partials;        /* [H/8][64] router partial scores */
@@ -79,6 +81,7 @@ ds_hip_layer_t *ds_hip_layer_create(int hidden, int inter, int n_experts, int to
   hipMemsetAsync(L->arena, 0, n, dsr_stream);
   char *b = (char *)L->arena;
   L->bytes = n;
+  L->wbytes = off[10];
   L->H = hidden;
   L->I = inter;
   L->E = n_experts;
@@ -391,6 +394,252 @@ int ds_hip_time_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, i
   hipEventDestroy(a);
   hipEventDestroy(b);
   return rc;
+}
+
+/* ================================================================ persisted arena
+ * File (little-endian): a 256-byte header
+ *   [0,8) magic "DSI8ARNA"  [8,12) version (1)  [12,16) n_layers  [16,36) hidden, inter, n_experts,
+ *   top_k, shared_inter  [36,40) vocab (0: no LM head)  [40,48) layer_bytes  [48,56) lm_bytes
+ *   [56,64) checksum of everything after the header  [64,256) zero
+ * then per layer a 64-byte record (u32 has f32 router, u32 has bf16 router, zero) and layer_bytes
+ * bytes: the arena's weight regions exactly as they sit in device memory (routed gate_up codes,
+ * routed down codes, shared gate_up, shared down, the four (scale, offset) pair arrays, f32 router,
+ * bf16 router; each region 256-byte aligned), then lm_bytes of the bf16 LM head [vocab][hidden].
+ * The transposed f32 router is rebuilt on load. The checksum folds 8-byte words four at a time. */
+#define ARENA_MAGIC "DSI8ARNA"
+#define ARENA_VERSION 1u
+#define ARENA_CHUNK ((size_t)64 << 20)
+
+typedef struct {
+  char magic[8];
+  uint32_t version, n_layers, hidden, inter, n_experts, top_k, shared_inter, vocab;
+  uint64_t layer_bytes, lm_bytes, checksum;
+  uint8_t zero[192];
+} arena_header_t;
+typedef struct {
+  uint32_t have_f32, have_bf16;
+  uint8_t zero[56];
+} arena_record_t;
+
+_Static_assert(sizeof(arena_header_t) == 256, "arena header layout");
+_Static_assert(sizeof(arena_record_t) == 64, "arena layer record layout");
+
+typedef struct {
+  uint64_t h[4];
+  uint8_t tail[8];
+  int ntail;
+} arena_sum_t;
+
+static void sum_init(arena_sum_t *c) {
+  memset(c, 0, sizeof *c);
+  c->h[0] = 0x9E3779B97F4A7C15ull;
+  c->h[1] = 0xC2B2AE3D27D4EB4Full;
+  c->h[2] = 0x165667B19E3779F9ull;
+  c->h[3] = 0x27D4EB2F165667C5ull;
+}
+static inline uint64_t sum_mix(uint64_t h, uint64_t w) {
+  h ^= w;
+  h *= 0x100000001B3ull;
+  return (h << 29) | (h >> 35);
+}
+static void sum_add(arena_sum_t *c, const void *p, size_t n) {
+  const uint8_t *b = (const uint8_t *)p;
+  while (n && c->ntail) {  // finish a partial word
+    c->tail[c->ntail++] = *b++;
+    n--;
+    if (c->ntail == 8) {
+      uint64_t w;
+      memcpy(&w, c->tail, 8);
+      c->h[0] = sum_mix(c->h[0], w);
+      c->ntail = 0;
+    }
+  }
+  size_t nw = n / 32;
+  for (size_t i = 0; i < nw; i++, b += 32) {
+    uint64_t w[4];
+    memcpy(w, b, 32);
+    for (int k = 0; k < 4; k++) c->h[k] = sum_mix(c->h[k], w[k]);
+  }
+  n -= nw * 32;
+  while (n >= 8) {
+    uint64_t w;
+    memcpy(&w, b, 8);
+    c->h[0] = sum_mix(c->h[0], w);
+    b += 8;
+    n -= 8;
+  }
+  while (n--) c->tail[c->ntail++] = *b++;
+}
+static uint64_t sum_final(arena_sum_t *c) {
+  if (c->ntail) {
+    memset(c->tail + c->ntail, 0, 8 - c->ntail);
+    uint64_t w;
+    memcpy(&w, c->tail, 8);
+    c->h[0] = sum_mix(c->h[0], w ^ (uint64_t)c->ntail);
+  }
+  return c->h[0] ^ (c->h[1] * 3) ^ (c->h[2] * 5) ^ (c->h[3] * 7);
+}
+
+/* Writes n bytes at device address src to f through the host buffer buf (ARENA_CHUNK bytes). */
+static int arena_write_dev(FILE *f, const void *src, size_t n, void *buf, arena_sum_t *c) {
+  for (size_t o = 0; o < n; o += ARENA_CHUNK) {
+    size_t k = n - o < ARENA_CHUNK ? n - o : ARENA_CHUNK;
+    if (dsr_d2h(buf, (const char *)src + o, k)) return -1;
+    sum_add(c, buf, k);
+    if (fwrite(buf, 1, k, f) != k) return dsr_failf("ds_hip_arena_save: write failed");
+  }
+  return 0;
+}
+static int arena_read_dev(FILE *f, void *dst, size_t n, void *buf, arena_sum_t *c) {
+  for (size_t o = 0; o < n; o += ARENA_CHUNK) {
+    size_t k = n - o < ARENA_CHUNK ? n - o : ARENA_CHUNK;
+    if (fread(buf, 1, k, f) != k) return dsr_failf("ds_hip_arena_load: file is truncated");
+    sum_add(c, buf, k);
+    DSR_TRY(hipMemcpyAsync((char *)dst + o, buf, k, hipMemcpyHostToDevice, dsr_stream), "arena upload");
+    DSR_TRY(hipStreamSynchronize(dsr_stream), "arena upload");
+  }
+  return 0;
+}
+
+int ds_hip_arena_save(const char *path, ds_hip_layer_t *const *layers, int n_layers, const uint16_t *lm_head_dev,
+                      int vocab) {
+  if (!path || !layers || n_layers <= 0 || (lm_head_dev && vocab <= 0))
+    return dsr_failf("ds_hip_arena_save: invalid arguments");
+  const ds_hip_layer_t *L0 = layers[0];
+  if (!L0) return dsr_failf("ds_hip_arena_save: NULL layer");
+  for (int i = 1; i < n_layers; i++) {
+    const ds_hip_layer_t *L = layers[i];
+    if (!L || L->H != L0->H || L->I != L0->I || L->E != L0->E || L->K != L0->K || L->SI != L0->SI)
+      return dsr_failf("ds_hip_arena_save: layer %d has another shape than layer 0", i);
+  }
+  if (dsr_init()) return -1;
+  arena_header_t hd;
+  memset(&hd, 0, sizeof hd);
+  memcpy(hd.magic, ARENA_MAGIC, 8);
+  hd.version = ARENA_VERSION;
+  hd.n_layers = (uint32_t)n_layers;
+  hd.hidden = (uint32_t)L0->H;
+  hd.inter = (uint32_t)L0->I;
+  hd.n_experts = (uint32_t)L0->E;
+  hd.top_k = (uint32_t)L0->K;
+  hd.shared_inter = (uint32_t)L0->SI;
+  hd.vocab = lm_head_dev ? (uint32_t)vocab : 0u;
+  hd.layer_bytes = L0->wbytes;
+  hd.lm_bytes = lm_head_dev ? (uint64_t)vocab * (uint64_t)L0->H * 2u : 0u;
+  FILE *f = fopen(path, "wb");
+  if (!f) return dsr_failf("ds_hip_arena_save: cannot open %s", path);
+  void *buf = NULL;
+  int rc = 0;
+  if (hipHostMalloc(&buf, ARENA_CHUNK, hipHostMallocDefault) != hipSuccess) {
+    buf = NULL;
+    rc = dsr_failf("ds_hip_arena_save: pinned staging allocation failed");
+  }
+  arena_sum_t c;
+  sum_init(&c);
+  if (!rc && fwrite(&hd, sizeof hd, 1, f) != 1) rc = dsr_failf("ds_hip_arena_save: write failed");
+  if (!rc) rc = hipStreamSynchronize(dsr_stream) == hipSuccess ? 0 : dsr_failf("ds_hip_arena_save: stream error");
+  for (int i = 0; i < n_layers && !rc; i++) {
+    arena_record_t r;
+    memset(&r, 0, sizeof r);
+    r.have_f32 = (uint32_t)layers[i]->have_f32;
+    r.have_bf16 = (uint32_t)layers[i]->have_bf16;
+    sum_add(&c, &r, sizeof r);
+    if (fwrite(&r, sizeof r, 1, f) != 1) rc = dsr_failf("ds_hip_arena_save: write failed");
+    if (!rc) rc = arena_write_dev(f, layers[i]->arena, layers[i]->wbytes, buf, &c);
+  }
+  if (!rc && lm_head_dev) rc = arena_write_dev(f, lm_head_dev, hd.lm_bytes, buf, &c);
+  if (!rc) {
+    hd.checksum = sum_final(&c);
+    if (fseek(f, 0, SEEK_SET) || fwrite(&hd, sizeof hd, 1, f) != 1) rc = dsr_failf("ds_hip_arena_save: write failed");
+  }
+  if (fclose(f) && !rc) rc = dsr_failf("ds_hip_arena_save: close failed");
+  if (buf) hipHostFree(buf);
+  return rc;
+}
+
+int ds_hip_arena_load(const char *path, ds_hip_layer_t **layers, int max_layers, uint16_t **lm_head_dev, int *vocab) {
+  if (!path || !layers || max_layers <= 0) return dsr_failf("ds_hip_arena_load: invalid arguments");
+  if (lm_head_dev) *lm_head_dev = NULL;
+  if (vocab) *vocab = 0;
+  FILE *f = fopen(path, "rb");
+  if (!f) return dsr_failf("ds_hip_arena_load: cannot open %s", path);
+  arena_header_t hd;
+  int rc = 0, made = 0;
+  void *buf = NULL;
+  uint16_t *lm = NULL;
+  if (fread(&hd, sizeof hd, 1, f) != 1 || memcmp(hd.magic, ARENA_MAGIC, 8)) {
+    rc = dsr_failf("ds_hip_arena_load: %s is not a packed INT8 arena", path);
+  } else if (hd.version != ARENA_VERSION) {
+    rc = dsr_failf("ds_hip_arena_load: format version %u, expected %u", hd.version, ARENA_VERSION);
+  } else if (hd.n_layers == 0 || (int)hd.n_layers > max_layers) {
+    rc = dsr_failf("ds_hip_arena_load: %u layers in the file, room for %d", hd.n_layers, max_layers);
+  } else if (hd.lm_bytes != (uint64_t)hd.vocab * hd.hidden * 2u) {
+    rc = dsr_failf("ds_hip_arena_load: inconsistent LM head size");
+  }
+  if (!rc && fseek(f, 0, SEEK_END) == 0) {
+    const uint64_t want = sizeof hd + (uint64_t)hd.n_layers * (sizeof(arena_record_t) + hd.layer_bytes) + hd.lm_bytes;
+    const long got = ftell(f);
+    if (got < 0 || (uint64_t)got != want)
+      rc = dsr_failf("ds_hip_arena_load: file size %ld, the header describes %llu", got, (unsigned long long)want);
+    else if (fseek(f, (long)sizeof hd, SEEK_SET))
+      rc = dsr_failf("ds_hip_arena_load: seek failed");
+  }
+  if (!rc && hipHostMalloc(&buf, ARENA_CHUNK, hipHostMallocDefault) != hipSuccess) {
+    buf = NULL;
+    rc = dsr_failf("ds_hip_arena_load: pinned staging allocation failed");
+  }
+  arena_sum_t c;
+  sum_init(&c);
+  for (uint32_t i = 0; i < hd.n_layers && !rc; i++) {
+    ds_hip_layer_t *L = ds_hip_layer_create((int)hd.hidden, (int)hd.inter, (int)hd.n_experts, (int)hd.top_k,
+                                            (int)hd.shared_inter);
+    if (!L) {
+      rc = -1;
+      break;
+    }
+    layers[made++] = L;
+    if (L->wbytes != hd.layer_bytes) {
+      rc = dsr_failf("ds_hip_arena_load: layer section of %llu bytes, this build lays out %zu",
+                     (unsigned long long)hd.layer_bytes, L->wbytes);
+      break;
+    }
+    arena_record_t r;
+    if (fread(&r, sizeof r, 1, f) != 1) {
+      rc = dsr_failf("ds_hip_arena_load: file is truncated");
+      break;
+    }
+    sum_add(&c, &r, sizeof r);
+    rc = arena_read_dev(f, L->arena, L->wbytes, buf, &c);
+    if (rc) break;
+    L->have_f32 = r.have_f32 != 0;
+    L->have_bf16 = r.have_bf16 != 0;
+    if (L->have_f32) {
+      hipError_t e = dsh_launch_transpose_f32(L->d.router_f32, (float *)L->d.router_f32_t, L->E, L->H, dsr_stream);
+      if (e != hipSuccess) rc = dsr_fail("router transpose", e);
+    }
+  }
+  if (!rc && hd.lm_bytes) {
+    if (hipMalloc((void **)&lm, hd.lm_bytes) != hipSuccess) {
+      lm = NULL;
+      rc = dsr_failf("ds_hip_arena_load: LM head allocation failed");
+    } else {
+      rc = arena_read_dev(f, lm, hd.lm_bytes, buf, &c);
+    }
+  }
+  if (!rc && sum_final(&c) != hd.checksum) rc = dsr_failf("ds_hip_arena_load: checksum mismatch (corrupt file)");
+  if (!rc && hipStreamSynchronize(dsr_stream) != hipSuccess) rc = dsr_failf("ds_hip_arena_load: stream error");
+  fclose(f);
+  if (buf) hipHostFree(buf);
+  if (rc) {
+    for (int i = 0; i < made; i++) ds_hip_layer_destroy(layers[i]);
+    for (int i = 0; i < made; i++) layers[i] = NULL;
+    if (lm) hipFree(lm);
+    return -1;
+  }
+  if (lm_head_dev) *lm_head_dev = lm;
+  else if (lm) hipFree(lm);
+  if (vocab) *vocab = (int)hd.vocab;
+  return (int)hd.n_layers;
 }
 
 /* ================================================================ decode stack */

@@ -97,6 +97,40 @@ int ds_hip_prefill_path(int mode);
  * tile expired (that call's output is not valid), 0 if not, -1 on error. Synchronises. */
 int ds_hip_prefill_wait_error(ds_hip_layer_t *L, int T);
 
+/* ---------------- weights: checkpoints and the persisted INT8 arena ---------------- */
+/* Tensor dtypes reported by ds_hip_safetensors_info. */
+enum { DS_HIP_ST_BF16 = 0, DS_HIP_ST_F32 = 1, DS_HIP_ST_F16 = 2, DS_HIP_ST_OTHER = 3 };
+/* Looks a tensor up in a set of safetensors shards (the reference reads them through
+ * ds_safetensors.h:50-75 / multi_safetensors_find); writes its dtype and up to max_dims extents and
+ * returns its rank, or -1. Host only (no GPU needed). */
+int ds_hip_safetensors_info(const char *const *files, int n_files, const char *name, int *dtype, int64_t *shape,
+                            int max_dims);
+/* Builds n_layers device MoE layers from DeepSeek-OCR safetensors shards, layers first_layer ..
+ * first_layer + n_layers - 1, with the reference's tensor names (ds_ocr.c:653-680):
+ * model.layers.{l}.mlp.gate.weight (router, BF16 or F32), ...mlp.experts.{e}.{gate,up,down}_proj.weight
+ * and ...mlp.shared_experts.{gate,up,down}_proj.weight (BF16). Shapes come from the tensors; top_k
+ * from the model config. gate and up rows are fused as the reference does (ds_ocr.c:696-768) and
+ * quantized on the device, bit-identical to ds_quantize_moe_int4 (ds_ocr.c:781-841). A BF16 router
+ * also gives the f32 router (its values widened); an F32 router gives no bf16 router. Returns
+ * n_layers (layers[0..n) filled) or -1 (nothing left allocated). Synchronous. */
+int ds_hip_load_moe_layers(const char *const *files, int n_files, int first_layer, int n_layers, int top_k,
+                           ds_hip_layer_t **layers);
+/* Uploads lm_head.weight (BF16 [vocab, hidden]; ds_ocr.c:686) to a new device buffer (free with
+ * ds_hip_free). Returns 0 or -1. */
+int ds_hip_load_lm_head(const char *const *files, int n_files, uint16_t **lm_head_dev, int *vocab, int *hidden);
+/* Persisted packed INT8 arena. No counterpart in the reference, which re-quantizes every expert at
+ * each load (ds_quantize_moe_int4, ds_ocr.c:781-841); for integrations that keep the packed weights
+ * instead of the BF16 checkpoint. Saves the layers (same shape) -- INT8 codes, (scale, offset)
+ * pairs, routers -- and optionally the bf16 LM head (lm_head_dev NULL: none) to path, versioned and
+ * checksummed. Returns 0 or -1. */
+int ds_hip_arena_save(const char *path, ds_hip_layer_t *const *layers, int n_layers, const uint16_t *lm_head_dev,
+                      int vocab);
+/* Reads a file written by ds_hip_arena_save into new layers (layers[0..n), n <= max_layers) and, if
+ * it holds an LM head, a new device buffer (*lm_head_dev, free with ds_hip_free; *vocab). Checks the
+ * format version, shapes, size and checksum. Returns the number of layers or -1 (nothing left
+ * allocated). */
+int ds_hip_arena_load(const char *path, ds_hip_layer_t **layers, int max_layers, uint16_t **lm_head_dev, int *vocab);
+
 /* ---------------- decode stack: n MoE layers + argmax LM head ---------------- */
 typedef struct ds_hip_stack ds_hip_stack_t;
 
