@@ -21,6 +21,7 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 H, I, E, K, SI, VOCAB, LAYERS = 1280, 896, 64, 6, 1792, 129280, 11
+DENSE_I = 6848  # layer 0's dense FFN (intermediate_size of DeepSeek-OCR's decoder)
 PEAK_HBM_GBS = 8000.0
 # HBM bytes per launch of the LM-head kernel, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of
 # this benchmark, scaled by the counters' reading for a 256 MiB device copy (FETCH_SIZE x 2.0,
@@ -58,6 +59,23 @@ def make_layer(dev, seed, gu, dn, rf, rb):
     dev.check(L.ds_hip_layer_set_router_dev(h, rf.ptr, rb.ptr), "router")
     dev.check(L.ds_hip_sync(), "sync")
     return h
+
+
+def make_dense(dev):
+    """DeepSeek-OCR's layer-0 dense FFN (gate/up 6848x1280, down 1280x6848, bf16) with seeded
+    N(0, 0.02) weights, rounded to bf16 to nearest even."""
+    L = dev.load()
+    rng = np.random.default_rng(606)
+
+    def bf16(n):
+        u = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.02)).view(np.uint32)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+    g, u, d = bf16(DENSE_I * H), bf16(DENSE_I * H), bf16(H * DENSE_I)
+    D = L.ds_hip_dense_create(H, DENSE_I, g.ctypes.data, u.ctypes.data, d.ctypes.data)
+    if not D:
+        raise RuntimeError(L.ds_hip_last_error().decode())
+    return D
 
 
 def host_layers(dev, handles, rf_host, rb_host):
@@ -134,6 +152,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-tokens", type=int, default=662, help="config-3 prefill measurement (0: skip)")
     ap.add_argument("--prefill-reps", type=int, default=20)
+    ap.add_argument("--dense-layer", action="store_true",
+                    help="prepend DeepSeek-OCR's layer-0 dense SwiGLU FFN (1280x6848 bf16) to every step")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (HBM counter calibration)")
     args = ap.parse_args()
@@ -170,6 +190,9 @@ def main():
     S = L.ds_hip_stack_create(arr, LAYERS, lm.ptr, VOCAB, route)
     if not S:
         raise RuntimeError(L.ds_hip_last_error().decode())
+    dense = make_dense(dev) if args.dense_layer else None
+    if dense:
+        dev.check(L.ds_hip_stack_set_dense(S, dense), "set dense")
     dev.check(L.ds_hip_stack_bind(S, xs.ptr, H, toks.ptr), "bind")
     bytes_per_step = L.ds_hip_stack_bytes_per_step(S)
 
@@ -229,12 +252,14 @@ def main():
 
     xs_host = xs.to_array(np.float32).reshape(n_inputs, H)[args.warmup:].copy()
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and not dense:  # the reference CPU leg runs the MoE layers and the head only
         try:
             cpu = cpu_baseline(dev, handles, rfs, rbs, lm, xs_host, gpu_tokens[args.warmup:], route, args.cpu_seconds)
         except Exception as exc:  # report, never hide
             cpu = {"error": repr(exc)}
     L.ds_hip_stack_destroy(S)
+    if dense:
+        L.ds_hip_dense_destroy(dense)
     for h in handles:
         L.ds_hip_layer_destroy(h)
 
@@ -251,7 +276,8 @@ def main():
         "vs_baseline": None,
         "dtype": "int8 weights (u8 codes + f32 scale/offset), f32 accumulate; bf16 LM head",
         "data": "synthetic: seeded N(0,0.02) weights generated on device, seeded N(0,1) f32 hidden states",
-        "config": {"workload": "config 5: 11 DeepSeek3B-MoE INT8 layers (H1280, 64x[1792x1280 + 1280x896] "
+        "config": {"workload": ("layer-0 dense SwiGLU FFN 1280x6848 bf16 + " if dense else "") +
+                               "config 5: 11 DeepSeek3B-MoE INT8 layers (H1280, 64x[1792x1280 + 1280x896] "
                                "routed top-6 + 2 shared, f32 router renormalised) + argmax LM head 129280x1280 "
                                "bf16, batch 1, 226-step decode",
                    "route": args.route, "global_batch": 1, "parallelism": "single GPU"},

@@ -99,6 +99,11 @@ SIGNATURES = {
     "ds_hip_stack_kernel_count": (C.c_int, [vp]),
     "ds_hip_stack_kernel_name": (C.c_char_p, [vp, C.c_int]),
     "ds_hip_profile_stack": (C.c_int, [vp, C.c_int, f32p]),
+    "ds_hip_dense_create": (vp, [C.c_int, C.c_int, vp, vp, vp]),
+    "ds_hip_dense_destroy": (None, [vp]),
+    "ds_hip_dense_forward": (C.c_int, [vp, vp, vp, C.c_int]),
+    "ds_hip_stack_set_dense": (C.c_int, [vp, vp]),
+    "ds_hip_load_dense": (C.c_int, [C.POINTER(C.c_char_p), C.c_int, C.c_int, C.POINTER(vp)]),
     "ds_hip_safetensors_info": (C.c_int, [C.POINTER(C.c_char_p), C.c_int, C.c_char_p, C.POINTER(C.c_int),
                                           C.POINTER(C.c_int64), C.c_int]),
     "ds_hip_load_moe_layers": (C.c_int, [C.POINTER(C.c_char_p), C.c_int, C.c_int, C.c_int, C.c_int,

@@ -93,6 +93,15 @@ hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int
 /* ---- latency-oriented decode kernels (k_dec.hip) ---- */
 int dsh_dec_supported(int H, int I, int E, int K, int SI);
 int dsh_dec_partials(int H); /* partial score rows written per layer in CFG mode */
+/* ---- dense SwiGLU FFN (k_dense.hip) ---- */
+int dsh_dense_supported(int H, int I);
+hipError_t dsh_launch_dense_gate_up(const uint16_t *Wg, const uint16_t *Wu, const float *x_in, const int *step,
+                                    int stride, int H, int I, float *h, hipStream_t s);
+/* x_out[H] = (residual ? x : 0) + Wd·h; with WrT_next ([H][E_next] f32), the next MoE layer's router
+ * partial scores over 8-row blocks (H / 8 rows of 64, the format k_dec_down writes). */
+hipError_t dsh_launch_dense_down(const uint16_t *Wd, const float *h, const float *x_in, const int *step, int stride,
+                                 int H, int I, int residual, float *x_out, const float *WrT_next, int E_next,
+                                 float *partials_next, hipStream_t s);
 hipError_t dsh_launch_transpose_f32(const float *src, float *dst, int rows, int cols, hipStream_t s);
 hipError_t dsh_launch_dec_partial_scores(const float *WrT, const float *x_in, const int *step, int stride, int H, int E,
                                          float *partials, hipStream_t s);

@@ -642,11 +642,75 @@ int ds_hip_arena_load(const char *path, ds_hip_layer_t **layers, int max_layers,
   return (int)hd.n_layers;
 }
 
+/* ================================================================ dense FFN (layer 0) */
+struct ds_hip_dense {
+  int H, I;
+  void *arena; /* gate [I][H] | up [I][H] | down [H][I] bf16 | h [I] f32 */
+  const uint16_t *wg, *wu, *wd;
+  float *h;
+};
+
+ds_hip_dense_t *ds_hip_dense_create(int hidden, int inter, const uint16_t *gate, const uint16_t *up,
+                                    const uint16_t *down) {
+  if (dsr_init()) return NULL;
+  if (!gate || !up || !down || !dsh_dense_supported(hidden, inter)) {
+    dsr_failf("ds_hip_dense_create: invalid arguments or shape H=%d I=%d (need H %% 128 == 0, H <= 2048, I %% 8 == 0, "
+              "I <= 16384)", hidden, inter);
+    return NULL;
+  }
+  ds_hip_dense_t *D = (ds_hip_dense_t *)calloc(1, sizeof *D);
+  if (!D) return NULL;
+  const size_t w = (size_t)hidden * inter * 2, wa = al(w);
+  hipError_t e = hipMalloc(&D->arena, 3 * wa + al((size_t)inter * 4));
+  if (e != hipSuccess) {
+    dsr_fail("dense FFN allocation", e);
+    free(D);
+    return NULL;
+  }
+  char *b = (char *)D->arena;
+  D->H = hidden;
+  D->I = inter;
+  D->wg = (const uint16_t *)b;
+  D->wu = (const uint16_t *)(b + wa);
+  D->wd = (const uint16_t *)(b + 2 * wa);
+  D->h = (float *)(b + 3 * wa);
+  if (dsr_h2d((void *)D->wg, gate, w) || dsr_h2d((void *)D->wu, up, w) || dsr_h2d((void *)D->wd, down, w) ||
+      hipStreamSynchronize(dsr_stream) != hipSuccess) {
+    hipFree(D->arena);
+    free(D);
+    return NULL;
+  }
+  return D;
+}
+
+void ds_hip_dense_destroy(ds_hip_dense_t *D) {
+  if (!D) return;
+  hipStreamSynchronize(dsr_stream);
+  hipFree(D->arena);
+  free(D);
+}
+
+static hipError_t dense_enqueue(const ds_hip_dense_t *D, float *out, const float *x, const int *step, int stride,
+                                int residual, const ds_hip_layer_t *next, float *partials_next) {
+  hipError_t e = dsh_launch_dense_gate_up(D->wg, D->wu, x, step, stride, D->H, D->I, D->h, dsr_stream);
+  if (e == hipSuccess)
+    e = dsh_launch_dense_down(D->wd, D->h, x, step, stride, D->H, D->I, residual, out,
+                              next ? next->d.router_f32_t : NULL, next ? next->E : 0, partials_next, dsr_stream);
+  return e;
+}
+
+int ds_hip_dense_forward(ds_hip_dense_t *D, float *out_dev, const float *x_dev, int residual) {
+  if (!D || !out_dev || !x_dev) return dsr_failf("ds_hip_dense_forward: invalid arguments");
+  DSR_TRY(dense_enqueue(D, out_dev, x_dev, NULL, 0, residual, NULL, NULL), "dense FFN");
+  return 0;
+}
+
 /* ================================================================ decode stack */
 
 struct ds_hip_stack {
   ds_hip_layer_t **layers;
   int n_layers;
+  const ds_hip_dense_t *dense; /* optional dense FFN layer before the MoE layers */
   const uint16_t *lm;
   int vocab, H;
   int route_mode, bf16sim;
@@ -723,6 +787,14 @@ void ds_hip_stack_destroy(ds_hip_stack_t *S) {
   free(S);
 }
 
+int ds_hip_stack_set_dense(ds_hip_stack_t *S, ds_hip_dense_t *D) {
+  if (!S) return dsr_failf("ds_hip_stack_set_dense: NULL stack");
+  if (S->bound) return dsr_failf("ds_hip_stack_set_dense: call before ds_hip_stack_bind");
+  if (D && D->H != S->H) return dsr_failf("ds_hip_stack_set_dense: hidden %d, the stack has %d", D->H, S->H);
+  S->dense = D;
+  return 0;
+}
+
 size_t ds_hip_stack_bytes_per_step(const ds_hip_stack_t *S) {
   if (!S) return 0;
   size_t per_layer = 0;
@@ -731,7 +803,8 @@ size_t ds_hip_stack_bytes_per_step(const ds_hip_stack_t *S) {
   per_layer += K * (2 * I * H + 2 * I * 8) + K * (H * I + H * 8); /* routed experts */
   per_layer += 2 * SI * H + 2 * SI * 8 + H * SI + H * 8;          /* shared expert */
   per_layer += E * H * (S->route_mode == DS_HIP_ROUTE_CFG ? 4 : 2); /* router */
-  return per_layer * (size_t)S->n_layers + (size_t)S->vocab * S->H * 2;
+  size_t dense = S->dense ? (size_t)3 * S->dense->H * S->dense->I * 2 : 0;
+  return per_layer * (size_t)S->n_layers + dense + (size_t)S->vocab * S->H * 2;
 }
 
 /* Kernels launched per decode step (for profiling). */
@@ -739,7 +812,9 @@ size_t ds_hip_stack_bytes_per_step(const ds_hip_stack_t *S) {
  * DECODE routing: scores, gate_up and down per layer. Then the LM head (2 kernels). */
 static int stack_kernel_count(const ds_hip_stack_t *S) {
   int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
-  return (cfg ? 1 : S->n_layers) + 2 * S->n_layers + 2;
+  /* with a dense layer first, its down kernel writes the first MoE layer's CFG partials */
+  int scores = cfg ? (S->dense ? 0 : 1) : S->n_layers;
+  return (S->dense ? 2 : 0) + scores + 2 * S->n_layers + 2;
 }
 
 /* One decode step; ev (optional) receives an event before the first kernel and after each one.
@@ -751,14 +826,26 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
   const int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
   const dsh_layer_work_t *wk = &S->layers[0]->wk;
   if (ev) e = hipEventRecord(ev[n++], dsr_stream);
+  const int dense = S->dense != NULL;
+  if (dense) {  /* layer 0: x = x + FFN(x); in CFG mode also the first MoE layer's router partials */
+    e = dsh_launch_dense_gate_up(S->dense->wg, S->dense->wu, S->xs, S->step, S->stride, S->dense->H, S->dense->I,
+                                 S->dense->h, dsr_stream);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+    if (e == hipSuccess)
+      e = dsh_launch_dense_down(S->dense->wd, S->dense->h, S->xs, S->step, S->stride, S->dense->H, S->dense->I, 1,
+                                S->xbuf, cfg ? S->layers[0]->d.router_f32_t : NULL, cfg ? S->layers[0]->E : 0,
+                                cfg ? S->partials[0] : NULL, dsr_stream);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+  }
   for (int l = 0; l < S->n_layers && e == hipSuccess; l++) {
     const ds_hip_layer_t *L = S->layers[l];
-    const float *xin = l == 0 ? S->xs : S->xbuf;
-    const int *st = l == 0 ? S->step : NULL;
-    int stride = l == 0 ? S->stride : 0;
+    const int first = l == 0 && !dense; /* reads the step's input directly */
+    const float *xin = first ? S->xs : S->xbuf;
+    const int *st = first ? S->step : NULL;
+    int stride = first ? S->stride : 0;
     float *pin = S->partials[l & 1], *pout = S->partials[(l + 1) & 1];
     int np = L->np;
-    if (!cfg || l == 0) {
+    if (!cfg || first) {
       e = scores_enqueue(L, xin, st, stride, S->route_mode, pin, &np);
       if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
       if (e != hipSuccess) break;
@@ -892,6 +979,12 @@ const char *ds_hip_stack_kernel_name(const ds_hip_stack_t *S, int i) {
   if (i == nk - 2) return "lm_head.argmax";
   if (i == nk - 1) return "lm_head.final";
   const int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
+  if (S->dense) {
+    if (i == 0) return "dense.gate_up";
+    if (i == 1) return "dense.down";
+    i -= 2;
+    if (cfg) i += 1; /* no separate scores kernel */
+  }
   if (cfg && i == 0) return "scores";
   const int per = cfg ? 2 : 3; /* kernels per layer */
   const int j = (cfg ? i - 1 : i) % per;

@@ -433,6 +433,30 @@ int ds_hip_load_moe_layers(const char *const *files, int n_files, int first_laye
   return n_layers;
 }
 
+int ds_hip_load_dense(const char *const *files, int n_files, int layer, ds_hip_dense_t **dense) {
+  if (!dense || layer < 0) return dsr_failf("ds_hip_load_dense: invalid arguments");
+  *dense = NULL;
+  st_set_t *S = st_open(files, n_files);
+  if (!S) return -1;
+  char name[ST_NAME];
+  snprintf(name, sizeof name, "model.layers.%d.mlp.gate_proj.weight", layer);
+  const st_tensor_t *g = st_bf16_2d(S, name, -1, -1);
+  const st_tensor_t *u = NULL, *d = NULL;
+  if (g) {
+    snprintf(name, sizeof name, "model.layers.%d.mlp.up_proj.weight", layer);
+    u = st_bf16_2d(S, name, g->shape[0], g->shape[1]);
+  }
+  if (u) {
+    snprintf(name, sizeof name, "model.layers.%d.mlp.down_proj.weight", layer);
+    d = st_bf16_2d(S, name, g->shape[1], g->shape[0]);
+  }
+  if (d)
+    *dense = ds_hip_dense_create((int)g->shape[1], (int)g->shape[0], (const uint16_t *)g->data,
+                                 (const uint16_t *)u->data, (const uint16_t *)d->data);
+  st_close(S);
+  return *dense ? 0 : -1;
+}
+
 int ds_hip_load_lm_head(const char *const *files, int n_files, uint16_t **lm_head_dev, int *vocab, int *hidden) {
   if (!lm_head_dev) return dsr_failf("ds_hip_load_lm_head: invalid arguments");
   *lm_head_dev = NULL;

@@ -97,6 +97,18 @@ int ds_hip_prefill_path(int mode);
  * tile expired (that call's output is not valid), 0 if not, -1 on error. Synchronises. */
 int ds_hip_prefill_wait_error(ds_hip_layer_t *L, int T);
 
+/* ---------------- dense FFN layer (layer 0 of the decoder) ---------------- */
+/* The decoder's dense SwiGLU FFN (ds_moe_decoder.c:75-105, dense_ffn_forward): gate [inter, hidden],
+ * up [inter, hidden], down [hidden, inter] BF16 host arrays, uploaded once. Needs hidden % 128 == 0
+ * (<= 2048) and inter % 8 == 0 (<= 16384). f32 dots of the exact bf16 values in a lane-parallel order
+ * (the reference's AVX-512 chains differ by f32 rounding), fast-exp SwiGLU as ds_swiglu_direct. */
+typedef struct ds_hip_dense ds_hip_dense_t;
+ds_hip_dense_t *ds_hip_dense_create(int hidden, int inter, const uint16_t *gate, const uint16_t *up,
+                                    const uint16_t *down);
+void ds_hip_dense_destroy(ds_hip_dense_t *D);
+/* out_dev[hidden] = (residual ? x : 0) + FFN(x_dev); out_dev may equal x_dev. Asynchronous. */
+int ds_hip_dense_forward(ds_hip_dense_t *D, float *out_dev, const float *x_dev, int residual);
+
 /* ---------------- weights: checkpoints and the persisted INT8 arena ---------------- */
 /* Tensor dtypes reported by ds_hip_safetensors_info. */
 enum { DS_HIP_ST_BF16 = 0, DS_HIP_ST_F32 = 1, DS_HIP_ST_F16 = 2, DS_HIP_ST_OTHER = 3 };
@@ -115,6 +127,9 @@ int ds_hip_safetensors_info(const char *const *files, int n_files, const char *n
  * n_layers (layers[0..n) filled) or -1 (nothing left allocated). Synchronous. */
 int ds_hip_load_moe_layers(const char *const *files, int n_files, int first_layer, int n_layers, int top_k,
                            ds_hip_layer_t **layers);
+/* The dense FFN of layer `layer` (model.layers.{l}.mlp.{gate,up,down}_proj.weight, BF16;
+ * ds_ocr.c:653-657) as a device handle. Returns 0 or -1. */
+int ds_hip_load_dense(const char *const *files, int n_files, int layer, ds_hip_dense_t **dense);
 /* Uploads lm_head.weight (BF16 [vocab, hidden]; ds_ocr.c:686) to a new device buffer (free with
  * ds_hip_free). Returns 0 or -1. */
 int ds_hip_load_lm_head(const char *const *files, int n_files, uint16_t **lm_head_dev, int *vocab, int *hidden);
@@ -137,6 +152,11 @@ typedef struct ds_hip_stack ds_hip_stack_t;
 /* lm_head_dev: bf16 [vocab, hidden] on the device (borrowed). Layers are borrowed. */
 ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers, const uint16_t *lm_head_dev,
                                     int vocab, int route_mode);
+/* Puts a dense FFN layer before the MoE layers (the decoder's layer 0): a step then runs
+ * x = x + FFN(x) on the step's input first, and in CFG routing its down kernel also writes the first
+ * MoE layer's router partials (no separate scores kernel). Call before ds_hip_stack_bind; the dense
+ * handle must outlive the stack. D = NULL removes it. */
+int ds_hip_stack_set_dense(ds_hip_stack_t *S, ds_hip_dense_t *D);
 void ds_hip_stack_destroy(ds_hip_stack_t *S);
 /* Step s reads its input hidden state from xs_dev + s*stride (stride 0: always xs_dev) and writes
  * its token to tokens_dev[s]; s is a device counter advanced by every step. Captures the graph. */
