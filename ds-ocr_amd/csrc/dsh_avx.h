@@ -54,6 +54,23 @@ __device__ __forceinline__ void load_bf16x8(const uint16_t *w, float *o) {
   }
 }
 
+// The 2-accumulator reduction: a0 + a1, then _mm512_reduce_add_ps's tree, from the 32 chains held
+// as 8 per lane (lane L of the 4-lane group owns chains 8L..8L+7). Lane 0 returns the sum.
+__device__ __forceinline__ float avx_tree32(const float *a) {
+  // A[i] = a0[i] + a1[i]: lane 0 gets A[0..7] (+lane 2), lane 1 gets A[8..15] (+lane 3).
+  float A[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) A[j] = a[j] + __shfl_down(a[j], 2, 4);
+  // T3[i] = A[8+i] + A[i] (lane 1 holds A[8..15]).
+  float T3[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) T3[j] = __shfl_down(A[j], 1, 4) + A[j];
+  float T6[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) T6[j] = T3[4 + j] + T3[j];
+  return (T6[0] + T6[2]) + (T6[1] + T6[3]);
+}
+
 // With add set (matvec path), "addend" is the bias term added after the tree and before the scalar
 // tail (ds_kernels_avx.c:84-87: "+ (bias ? bias[o] : 0.0f)"); the argmax path adds nothing.
 
@@ -83,18 +100,7 @@ __device__ float avx_row(const uint16_t *__restrict__ w, const float *x, int in_
       }
       k += 16;
     }
-    // A[i] = a0[i] + a1[i]: lane 0 gets A[0..7] (+lane 2), lane 1 gets A[8..15] (+lane 3).
-    float A[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) A[j] = a[j] + __shfl_down(a[j], 2, 4);
-    // T3[i] = A[8+i] + A[i] (lane 1 holds A[8..15]).
-    float T3[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) T3[j] = __shfl_down(A[j], 1, 4) + A[j];
-    float T6[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) T6[j] = T3[4 + j] + T3[j];
-    res = (T6[0] + T6[2]) + (T6[1] + T6[3]);
+    res = avx_tree32(a);
     if (add) res = res + addend;
     if (L == 0) {
       if (fused_tail)
@@ -126,3 +132,26 @@ __device__ float avx_row(const uint16_t *__restrict__ w, const float *x, int in_
   return res;
 }
 
+
+// avx_row's 4-row / 2-row group path for in_dim == 32*N32 (no 16-column step and no tail), with the
+// lane's 16-byte pieces (columns 32i + 8L .. 32i + 8L + 7) already in registers: wv[i]. x: 16-byte
+// aligned. Same chains, order and tree as avx_row.
+template <int N32>
+__device__ __forceinline__ float avx_row_regs32(const u32x4 *wv, const float *x, int L, bool add, float addend) {
+  float a[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) a[j] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N32; i++) {
+    const f32x4 x0 = ((const f32x4 *)x)[8 * i + 2 * L], x1 = ((const f32x4 *)x)[8 * i + 2 * L + 1];
+    const float xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      a[2 * d] = __builtin_fmaf(dsh_bf16lo(wv[i][d]), xv[2 * d], a[2 * d]);
+      a[2 * d + 1] = __builtin_fmaf(dsh_bf16hi(wv[i][d]), xv[2 * d + 1], a[2 * d + 1]);
+    }
+  }
+  float res = avx_tree32(a);
+  if (add) res = res + addend;
+  return res;
+}

@@ -96,19 +96,40 @@ __global__ void __launch_bounds__(256) k_transpose_f32(const float *__restrict__
     if (c0 + i < cols && r0 + tx < rows) dst[(size_t)(c0 + i) * rows + r0 + tx] = t[tx][i];
 }
 
-// DECODE mode: full scores in the reference's AVX-512 order, written as the single partial.
+// DECODE mode: full scores in the reference's AVX-512 order, written as the single partial. 16 rows
+// per 64-lane block, 4 lanes per row (H == 32*N32): each lane loads its 16-byte pieces of the row
+// (N32 of them) straight into registers, all in flight with x's pieces, which are staged in LDS. Rows
+// on the reference's single-row path (an odd thread chunk) read theirs in avx_row's loop.
+template <int N32>
 __global__ void __launch_bounds__(64) k_dec_scores_bf16(const uint16_t *__restrict__ Wr, const float *__restrict__ x_in,
-                                                        const int *__restrict__ step, int stride, int H, int E,
-                                                        int chunk, float *__restrict__ partials) {
-  extern __shared__ float xs[];
+                                                        const int *__restrict__ step, int stride, int E, int chunk,
+                                                        float *__restrict__ partials) {
+  constexpr int H = 32 * N32, NX = H / 4, XP = (NX + 63) / 64;
+  __shared__ __attribute__((aligned(16))) float xs[H];
   const float *x = at_step(x_in, step, stride);
-  for (int i = threadIdx.x; i < H; i += 64) xs[i] = x[i];
+  const int L = threadIdx.x & 3, e = blockIdx.x * 16 + (threadIdx.x >> 2);
+  const int ec = min(e, E - 1);
+  f32x4 xr[XP];
+#pragma unroll
+  for (int j = 0; j < XP; j++) xr[j] = ((const f32x4 *)x)[min((int)threadIdx.x + 64 * j, NX - 1)];
+  asm volatile("" ::: "memory");  // x first: its LDS stores wait for x only
+  const u32x4 *row = (const u32x4 *)(Wr + (size_t)ec * H);
+  u32x4 wv[N32];
+#pragma unroll
+  for (int i = 0; i < N32; i++) wv[i] = row[4 * i + L];
+#pragma unroll
+  for (int j = 0; j < XP; j++) {
+    const int i = threadIdx.x + 64 * j;
+    if (i < NX) ((f32x4 *)xs)[i] = xr[j];
+  }
   __syncthreads();
-  const int L = threadIdx.x & 3;
-  const int e = blockIdx.x * 16 + (threadIdx.x >> 2);
   if (e >= E) return;
-  int path = row_path(e, E, chunk, false);
-  float v = avx_row<true>(Wr + (size_t)e * H, xs, H, L, path == DSH_ROW_SINGLE, true, 0.0f, path != DSH_ROW_GROUP4);
+  const int path = row_path(e, E, chunk, false);
+  float v;
+  if (path == DSH_ROW_SINGLE)
+    v = avx_row<true>(Wr + (size_t)e * H, xs, H, L, true, true, 0.0f, true);
+  else
+    v = avx_row_regs32<N32>(wv, xs, L, true, 0.0f);
   if (L == 0) partials[e] = v;
 }
 
@@ -567,8 +588,18 @@ hipError_t dsh_launch_dec_partial_scores(const float *WrT, const float *x_in, co
 
 hipError_t dsh_launch_dec_scores_bf16(const uint16_t *Wr, const float *x_in, const int *step, int stride, int H, int E,
                                       int nthreads, float *partials, hipStream_t s) {
-  k_dec_scores_bf16<<<(E + 15) / 16, 64, (size_t)H * 4, s>>>(Wr, x_in, step, stride, H, E,
-                                                              dsh_chunk_len(E, nthreads), partials);
+  const int blocks = (E + 15) / 16, chunk = dsh_chunk_len(E, nthreads);
+#define SC(N)                                                                                  \
+  case N:                                                                                      \
+    k_dec_scores_bf16<8 * N><<<blocks, 64, 0, s>>>(Wr, x_in, step, stride, E, chunk, partials); \
+    break;
+  if (H % 256) return hipErrorInvalidValue;
+  switch (H / 256) {
+    SC(1) SC(2) SC(3) SC(4) SC(5) SC(6) SC(7) SC(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef SC
   return hipGetLastError();
 }
 

@@ -91,6 +91,32 @@ def test_small_layer_vs_oracle(dev, B, mode, sim):
         L.ds_hip_layer_destroy(h)
 
 
+@pytest.mark.parametrize("threads", [6, 5, 3, 16])
+def test_decode_routing_over_thread_chunks(dev, B, threads):
+    """DECODE-mode router scores follow the reference's row chunking over its threads: with these
+    counts some rows take the 2-row and the single-row AVX-512 paths. Expert ids and weights must be
+    bit-identical to the oracle run with the same thread count."""
+    L = dev.load()
+    lay = B.make_moe_layer(71, hidden=512, inter=128, n_experts=18, top_k=6, n_shared=2)
+    h = upload_layer(dev, lay)
+    orl = lay.or_layer()
+    try:
+        L.ds_set_threads(threads)
+        for s in range(3):
+            x = B.normal_f32(lay.hidden, 7100 + s)
+            out, idx, w = layer_forward(dev, h, x, dev.ROUTE_DECODE)
+            ro = np.empty(lay.hidden, np.float32)
+            ri = np.empty(6, np.int32)
+            rw = np.empty(6, np.float32)
+            B.oracle().or_moe_layer_decode(ro, x, C.byref(orl), 0, 0, threads, ri, rw)
+            assert np.array_equal(idx, ri)
+            assert np.array_equal(bits(w), bits(rw))
+            assert rel_err(out, ro) < TOL
+    finally:
+        L.ds_set_threads(1)
+        L.ds_hip_layer_destroy(h)
+
+
 def test_layer_rejects_unsupported_shape(dev):
     L = dev.load()
     assert not L.ds_hip_layer_create(256, 100, 16, 6, 200)
