@@ -238,12 +238,19 @@ __global__ void __launch_bounds__(256) k_argmax_avx(const uint16_t *__restrict__
   }
 }
 
-// Reduces n candidate keys to one index (and value).
+// Reduces n candidate keys to one index (and value); 4 candidates per thread loaded together
+// (clamped addresses), one round trip per 1024 candidates.
 __global__ void __launch_bounds__(256) k_argmax_final(const unsigned long long *__restrict__ cand, int n,
                                                       int *__restrict__ out_idx, float *__restrict__ out_val) {
   __shared__ unsigned long long wbest[4];
   unsigned long long b = 0ull;
-  for (int i = threadIdx.x; i < n; i += 256) b = dsh_umax64(b, cand[i]);
+  for (int i0 = 0; i0 < n; i0 += 1024) {
+    unsigned long long c[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) c[j] = cand[min(i0 + (int)threadIdx.x + 256 * j, n - 1)];  // duplicates are harmless
+#pragma unroll
+    for (int j = 0; j < 4; j++) b = dsh_umax64(b, c[j]);
+  }
   b = dsh_wave_max_u64(b);
   if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = b;
   __syncthreads();

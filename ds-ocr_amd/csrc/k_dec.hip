@@ -539,18 +539,27 @@ __global__ void __launch_bounds__(256) k_dec_lm_argmax(const uint16_t *W, const 
 }
 
 // Final reduction of the candidates; writes tokens[*step] (or tokens[0]) and advances *step.
+// The step index and a batch of 4 candidates per thread are loaded together (clamped addresses, no
+// branches), so the kernel waits for one round trip per 1024 candidates.
 __global__ void __launch_bounds__(256) k_lm_argmax_final(const unsigned long long *__restrict__ cand, int n,
                                                          int *__restrict__ tokens, int *__restrict__ step) {
   __shared__ unsigned long long wbest[4];
+  const int s = step ? *step : 0;
   unsigned long long b = 0ull;
-  for (int i = threadIdx.x; i < n; i += 256) b = dsh_umax64(b, cand[i]);
+  for (int i0 = 0; i0 < n; i0 += 1024) {
+    unsigned long long c[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) c[j] = cand[min(i0 + (int)threadIdx.x + 256 * j, n - 1)];  // duplicates are harmless
+#pragma unroll
+    for (int j = 0; j < 4; j++) b = dsh_umax64(b, c[j]);
+  }
   b = dsh_wave_max_u64(b);
   if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = b;
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int i = 1; i < 4; i++) wbest[0] = dsh_umax64(wbest[0], wbest[i]);
-    int s = step ? *step : 0;
-    tokens[s] = dsh_key_index(wbest[0]);
+    unsigned long long best = wbest[0];
+    for (int i = 1; i < 4; i++) best = dsh_umax64(best, wbest[i]);
+    tokens[s] = dsh_key_index(best);
     if (step) *step = s + 1;
   }
 }
