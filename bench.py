@@ -154,6 +154,9 @@ def main():
     ap.add_argument("--prefill-reps", type=int, default=20)
     ap.add_argument("--dense-layer", action="store_true",
                     help="prepend DeepSeek-OCR's layer-0 dense SwiGLU FFN (1280x6848 bf16) to every step")
+    ap.add_argument("--repeat-penalty", type=float, default=1.0,
+                    help="> 1: the reference's repetition penalty after each argmax, over the run's tokens")
+    ap.add_argument("--no-repeat-ngram", type=int, default=0, help="> 0: the reference's n-gram ban")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (HBM counter calibration)")
     args = ap.parse_args()
@@ -190,6 +193,9 @@ def main():
     S = L.ds_hip_stack_create(arr, LAYERS, lm.ptr, VOCAB, route)
     if not S:
         raise RuntimeError(L.ds_hip_last_error().decode())
+    sampling = args.repeat_penalty > 1.0 or args.no_repeat_ngram > 0
+    if sampling:
+        dev.check(L.ds_hip_stack_set_sampling(S, args.repeat_penalty, args.no_repeat_ngram, n_inputs), "sampling")
     dense = make_dense(dev) if args.dense_layer else None
     if dense:
         dev.check(L.ds_hip_stack_set_dense(S, dense), "set dense")
@@ -252,7 +258,7 @@ def main():
 
     xs_host = xs.to_array(np.float32).reshape(n_inputs, H)[args.warmup:].copy()
     cpu = None
-    if not args.no_cpu and not dense:  # the reference CPU leg runs the MoE layers and the head only
+    if not args.no_cpu and not dense and not sampling:  # the reference CPU leg: MoE layers + argmax head
         try:
             cpu = cpu_baseline(dev, handles, rfs, rbs, lm, xs_host, gpu_tokens[args.warmup:], route, args.cpu_seconds)
         except Exception as exc:  # report, never hide
@@ -277,6 +283,8 @@ def main():
         "dtype": "int8 weights (u8 codes + f32 scale/offset), f32 accumulate; bf16 LM head",
         "data": "synthetic: seeded N(0,0.02) weights generated on device, seeded N(0,1) f32 hidden states",
         "config": {"workload": ("layer-0 dense SwiGLU FFN 1280x6848 bf16 + " if dense else "") +
+                               (f"repetition penalty {args.repeat_penalty} / no-repeat n-gram {args.no_repeat_ngram} "
+                                "after the argmax + " if sampling else "") +
                                "config 5: 11 DeepSeek3B-MoE INT8 layers (H1280, 64x[1792x1280 + 1280x896] "
                                "routed top-6 + 2 shared, f32 router renormalised) + argmax LM head 129280x1280 "
                                "bf16, batch 1, 226-step decode",

@@ -93,6 +93,14 @@ hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int
 /* ---- latency-oriented decode kernels (k_dec.hip) ---- */
 int dsh_dec_supported(int H, int I, int E, int K, int SI);
 int dsh_dec_partials(int H); /* partial score rows written per layer in CFG mode */
+/* ---- greedy token choice with repetition penalty and n-gram ban (k_sample.hip) ---- */
+int dsh_sample_supported(int H);
+/* After the argmax. Stack form (step != NULL): history tokens[0..min(*step - 1, hist_len)), token
+ * tokens[*step - 1]. Explicit form (step == NULL): history hist[0..hist_len), token tokens[0].
+ * vals: [hist_len + 1] floats, lg: [vocab] floats, flag: one int (device workspace). */
+hipError_t dsh_launch_sample(const uint16_t *W, const float *x, int H, int vocab, int nthreads, float rp, int ngram_n,
+                             const int *step, int *tokens, const int *hist, int hist_len, float *vals, float *lg,
+                             int *flag, hipStream_t s);
 /* ---- dense SwiGLU FFN (k_dense.hip) ---- */
 int dsh_dense_supported(int H, int I);
 hipError_t dsh_launch_dense_gate_up(const uint16_t *Wg, const uint16_t *Wu, const float *x_in, const int *step,

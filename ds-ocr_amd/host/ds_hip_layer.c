@@ -728,7 +728,33 @@ struct ds_hip_stack {
   hipGraph_t graph;
   hipGraphExec_t exec;
   int bound;
+  /* greedy sampling rules after the argmax (ds_hip_stack_set_sampling) */
+  float rp;
+  int ngram, hist_cap;
+  void *smp_work; /* [hist_cap + 1] dots, [vocab] logits, flag */
 };
+
+int ds_hip_lm_head_sample(const float *x_dev, const uint16_t *lm_head_dev, int hidden, int vocab, const int *history_dev,
+                          int history_len, float repeat_penalty, int no_repeat_ngram_size, int *token_dev) {
+  if (!x_dev || !lm_head_dev || !token_dev || hidden <= 0 || vocab <= 0 || history_len < 0 ||
+      (history_len > 0 && !history_dev) || no_repeat_ngram_size < 0 || !(repeat_penalty == repeat_penalty))
+    return dsr_failf("ds_hip_lm_head_sample: invalid arguments");
+  if (!dsh_sample_supported(hidden)) return dsr_failf("ds_hip_lm_head_sample: hidden %d not supported", hidden);
+  if (dsr_init()) return -1;
+  const int T = dsr_threads();
+  const int nb = dsh_argmax_avx_blocks(vocab);
+  unsigned long long *cand = (unsigned long long *)dsr_scratch(DSR_SLOT_C, sizeof(unsigned long long) * (size_t)nb);
+  float *vals = (float *)dsr_scratch(DSR_SLOT_A, (size_t)(history_len + 1) * 4);
+  float *lg = (float *)dsr_scratch(DSR_SLOT_B, (size_t)vocab * 4);
+  int *flag = (int *)dsr_scratch(DSR_SLOT_IDX, 16);
+  if (!cand || !vals || !lg || !flag) return -1;
+  DSR_TRY(dsh_launch_argmax_avx(lm_head_dev, x_dev, cand, NULL, hidden, vocab, T, token_dev, NULL, dsr_stream),
+          "LM-head argmax");
+  DSR_TRY(dsh_launch_sample(lm_head_dev, x_dev, hidden, vocab, T, repeat_penalty, no_repeat_ngram_size, NULL,
+                            token_dev, history_dev, history_len, vals, lg, flag, dsr_stream),
+          "sampling rules");
+  return 0;
+}
 
 ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers, const uint16_t *lm_head_dev,
                                     int vocab, int route_mode) {
@@ -783,8 +809,33 @@ void ds_hip_stack_destroy(ds_hip_stack_t *S) {
   if (S->exec) hipGraphExecDestroy(S->exec);
   if (S->graph) hipGraphDestroy(S->graph);
   hipFree(S->work);
+  if (S->smp_work) hipFree(S->smp_work);
   free(S->layers);
   free(S);
+}
+
+static int smp_active(const ds_hip_stack_t *S) { return S->rp > 1.0f || S->ngram > 0; }
+static float *smp_vals(const ds_hip_stack_t *S) { return (float *)S->smp_work; }
+static float *smp_logits(const ds_hip_stack_t *S) { return (float *)S->smp_work + al((size_t)(S->hist_cap + 1) * 4) / 4; }
+static int *smp_flag(const ds_hip_stack_t *S) { return (int *)(smp_logits(S) + al((size_t)S->vocab * 4) / 4); }
+
+int ds_hip_stack_set_sampling(ds_hip_stack_t *S, float repeat_penalty, int no_repeat_ngram_size, int history_cap) {
+  if (!S) return dsr_failf("ds_hip_stack_set_sampling: NULL stack");
+  if (S->bound) return dsr_failf("ds_hip_stack_set_sampling: call before ds_hip_stack_bind");
+  if (no_repeat_ngram_size < 0 || history_cap < 0 || !(repeat_penalty == repeat_penalty))
+    return dsr_failf("ds_hip_stack_set_sampling: invalid arguments");
+  if (!dsh_sample_supported(S->H)) return dsr_failf("ds_hip_stack_set_sampling: hidden %d not supported", S->H);
+  if (S->smp_work) {
+    hipFree(S->smp_work);
+    S->smp_work = NULL;
+  }
+  S->rp = repeat_penalty;
+  S->ngram = no_repeat_ngram_size;
+  S->hist_cap = history_cap;
+  if (!smp_active(S)) return 0;
+  size_t bytes = al((size_t)(history_cap + 1) * 4) + al((size_t)S->vocab * 4) + 256;
+  DSR_TRY(hipMalloc(&S->smp_work, bytes), "sampling workspace");
+  return 0;
 }
 
 int ds_hip_stack_set_dense(ds_hip_stack_t *S, ds_hip_dense_t *D) {
@@ -814,7 +865,7 @@ static int stack_kernel_count(const ds_hip_stack_t *S) {
   int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
   /* with a dense layer first, its down kernel writes the first MoE layer's CFG partials */
   int scores = cfg ? (S->dense ? 0 : 1) : S->n_layers;
-  return (S->dense ? 2 : 0) + scores + 2 * S->n_layers + 2;
+  return (S->dense ? 2 : 0) + scores + 2 * S->n_layers + 2 + (smp_active(S) ? 1 : 0);
 }
 
 /* One decode step; ev (optional) receives an event before the first kernel and after each one.
@@ -869,6 +920,13 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
   if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
   if (e == hipSuccess) e = dsh_launch_lm_argmax_final(S->cand, S->ncand, S->tokens, S->step, dsr_stream);
   if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+  if (e == hipSuccess && smp_active(S)) {
+    /* the repetition penalty and the n-gram ban over this stack's earlier tokens; one event after
+     * all of the sampler's kernels */
+    e = dsh_launch_sample(S->lm, S->xbuf, S->H, S->vocab, dsr_threads(), S->rp, S->ngram, S->step, S->tokens, NULL,
+                          S->hist_cap, smp_vals(S), smp_logits(S), smp_flag(S), dsr_stream);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+  }
   return e;
 }
 
@@ -976,6 +1034,10 @@ int ds_hip_stack_kernel_count(const ds_hip_stack_t *S) { return S ? stack_kernel
 const char *ds_hip_stack_kernel_name(const ds_hip_stack_t *S, int i) {
   if (!S || i < 0 || i >= stack_kernel_count(S)) return NULL;
   int nk = stack_kernel_count(S);
+  if (smp_active(S)) {
+    if (i == nk - 1) return "sample";
+    nk--;
+  }
   if (i == nk - 2) return "lm_head.argmax";
   if (i == nk - 1) return "lm_head.final";
   const int cfg = S->route_mode == DS_HIP_ROUTE_CFG;

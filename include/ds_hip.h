@@ -149,6 +149,18 @@ int ds_hip_arena_load(const char *path, ds_hip_layer_t **layers, int max_layers,
 /* ---------------- decode stack: n MoE layers + argmax LM head ---------------- */
 typedef struct ds_hip_stack ds_hip_stack_t;
 
+/* Greedy sampling rules of ds_decoder_forward at temperature 0 (ds_moe_decoder.c:1036-1095 and the
+ * full-logits path :1105-1237) applied after each step's argmax, on the device: the repetition
+ * penalty (> 1 enables it) over the stack's earlier tokens (the first history_cap of them, as the
+ * reference's capped token_history) and the n-gram ban (no_repeat_ngram_size > 0). Call before
+ * ds_hip_stack_bind; (1.0, 0, 0) turns them off. The full-logits path computes the logits in
+ * ds_bf16_matvec_pub's order. */
+int ds_hip_stack_set_sampling(ds_hip_stack_t *S, float repeat_penalty, int no_repeat_ngram_size, int history_cap);
+/* The same rules for one hidden state, device pointers: token_dev[0] receives the chosen token
+ * (argmax, penalty over history_dev[0..history_len), n-gram ban). Asynchronous. */
+int ds_hip_lm_head_sample(const float *x_dev, const uint16_t *lm_head_dev, int hidden, int vocab, const int *history_dev,
+                          int history_len, float repeat_penalty, int no_repeat_ngram_size, int *token_dev);
+
 /* lm_head_dev: bf16 [vocab, hidden] on the device (borrowed). Layers are borrowed. */
 ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers, const uint16_t *lm_head_dev,
                                     int vocab, int route_mode);

@@ -65,6 +65,8 @@ def _load_oracle():
         "or_argmax_logits_avx512": (None, [f32p, f32p, u16p, C.c_int, C.c_int, C.c_int]),
         "or_argmax_bf16": (C.c_int, [f32p, u16p, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float)]),
         "or_bf16_dot_row": (C.c_float, [f32p, u16p, C.c_int, C.c_int]),
+        "or_lm_sample_greedy": (C.c_int, [f32p, u16p, C.c_int, C.c_int, i32p_opt, C.c_int, C.c_float, C.c_int,
+                                           C.c_int, C.c_void_p]),
         "or_linear_f32": (None, [f32p, f32p, f32p, C.c_int, C.c_int]),
         "or_moe_top_k": (None, [i32p, f32p, f32p, C.c_int, C.c_int]),
         "or_softmax_topk_decode": (None, [i32p, f32p, f32p, C.c_int, C.c_int]),

@@ -384,6 +384,79 @@ float or_bf16_dot_row(const float *x, const uint16_t *W, int in_dim, int row) {
   return s;
 }
 
+/* The reference's penalty (ds_moe_decoder.c:1048, :1058, :1191-1195): divide positive logits,
+ * multiply the others. */
+static float or_penalize(float v, float rp) { return v > 0 ? v / rp : v * rp; }
+
+/* 1 if the last (n-1)-token prefix of hist occurs at position i with hist[i + n - 1] == tok. */
+static int or_ngram_bans(const int *hist, int hist_len, int p, int i, int tok) {
+  for (int j = 0; j < p; j++)
+    if (hist[i + j] != hist[hist_len - p + j]) return 0;
+  return hist[i + p] == tok;
+}
+
+/* ds_moe_decoder.c:1036-1095 (fast path) and :1105-1237 (full path, temperature 0). The full
+ * path's logits come from ds_bf16_matvec_pub (the reference's branch without an F32 copy of the
+ * head; with one it calls a BLAS sgemm, whose summation order is the BLAS library's). */
+int or_lm_sample_greedy(const float *x, const uint16_t *W, int in_dim, int vocab, const int *hist, int hist_len,
+                        float rp, int ngram_n, int nthreads, int *used_full) {
+  int best = or_argmax_bf16(x, W, in_dim, vocab, nthreads, NULL);
+  float best_val = or_bf16_dot_row(x, W, in_dim, best);
+  if (rp > 1.0f && hist && hist_len > 0) {
+    for (int i = 0; i < hist_len; i++)
+      if (hist[i] == best) {
+        best_val = or_penalize(best_val, rp);
+        break;
+      }
+    for (int i = 0; i < hist_len; i++) {
+      int tid = hist[i];
+      if (tid >= 0 && tid < vocab && tid != best) {
+        float v = or_penalize(or_bf16_dot_row(x, W, in_dim, tid), rp);
+        if (v > best_val) {
+          best_val = v;
+          best = tid;
+        }
+      }
+    }
+  }
+  int full = 0;
+  if (ngram_n > 0 && hist_len >= ngram_n - 1) {
+    int p = ngram_n - 1;
+    for (int i = 0; i <= hist_len - p - 1 && !full; i++) full = or_ngram_bans(hist, hist_len, p, i, best);
+  }
+  if (used_full) *used_full = full;
+  if (!full) return best;
+  float *lg = (float *)malloc((size_t)vocab * sizeof(float));
+  if (!lg) return -1;
+  or_bf16_matvec_avx512(lg, x, W, in_dim, vocab, nthreads);
+  if (rp > 1.0f && hist && hist_len > 0) {
+    for (int i = 0; i < hist_len; i++) {
+      int tid = hist[i];
+      if (tid >= 0 && tid < vocab) lg[tid] = or_penalize(lg[tid], rp);
+    }
+  }
+  if (ngram_n > 0 && hist_len >= ngram_n - 1) {
+    int p = ngram_n - 1;
+    for (int i = 0; i <= hist_len - p - 1; i++) {
+      int m = 1;
+      for (int j = 0; j < p && m; j++) m = hist[i + j] == hist[hist_len - p + j];
+      if (m) {
+        int banned = hist[i + p];
+        if (banned >= 0 && banned < vocab) lg[banned] = -1e30f;
+      }
+    }
+  }
+  int tok = 0;
+  float b = lg[0];
+  for (int i = 1; i < vocab; i++)
+    if (lg[i] > b) {
+      b = lg[i];
+      tok = i;
+    }
+  free(lg);
+  return tok;
+}
+
 /* ---------------------------------------------------------------- router */
 
 /* ds_linear without USE_BLAS (ds_kernels.c:639-652), as GCC 11 -O3 (AVX-512) compiles its inner

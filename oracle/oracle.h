@@ -69,6 +69,13 @@ int or_argmax_bf16(const float *x, const uint16_t *W, int in_dim, int out_dim, i
                    float *best_val);
 /* ds_bf16_dot_row non-NEON branch (ds_kernels.c:1000-1008). */
 float or_bf16_dot_row(const float *x, const uint16_t *W, int in_dim, int row);
+/* Greedy token choice of ds_decoder_forward at temperature 0 (ds_moe_decoder.c:1036-1095): argmax,
+ * then the repetition penalty over the history (the argmax's own logit once, every other history
+ * token's logit from ds_bf16_dot_row), then the n-gram ban; a banned choice falls to the full-logits
+ * path (:1105-1237) with logits in ds_bf16_matvec_pub's order, the penalty per history occurrence,
+ * banned tokens at -1e30 and the first maximum. *used_full (optional) tells which path chose. */
+int or_lm_sample_greedy(const float *x, const uint16_t *W, int in_dim, int vocab, const int *hist, int hist_len,
+                        float repeat_penalty, int ngram_n, int nthreads, int *used_full);
 
 /* ---------------- router ---------------- */
 /* ds_linear without BLAS, seq=1 (ds_kernels.c:639-652): sequential fused chain per row. */
