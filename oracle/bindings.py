@@ -36,6 +36,15 @@ class OrBlock(C.Structure):
                 ("out_dim", C.c_int), ("in_dim", C.c_int)]
 
 
+class OrAttn(C.Structure):
+    """or_attn_t (oracle.h)."""
+    _fields_ = [("hidden", C.c_int), ("n_heads", C.c_int), ("head_dim", C.c_int), ("kv_stride", C.c_int),
+                ("eps", C.c_float), ("theta", C.c_float),
+                ("wq", C.c_void_p), ("wk", C.c_void_p), ("wv", C.c_void_p), ("wo", C.c_void_p),
+                ("input_norm", C.c_void_p), ("post_norm", C.c_void_p), ("q_norm", C.c_void_p),
+                ("k_norm", C.c_void_p)]
+
+
 class OrLayer(C.Structure):
     _fields_ = [("hidden", C.c_int), ("inter", C.c_int), ("n_experts", C.c_int), ("top_k", C.c_int),
                 ("shared_inter", C.c_int), ("router_f32", C.c_void_p), ("router_bf16", C.c_void_p),
@@ -65,6 +74,16 @@ def _load_oracle():
         "or_argmax_logits_avx512": (None, [f32p, f32p, u16p, C.c_int, C.c_int, C.c_int]),
         "or_argmax_bf16": (C.c_int, [f32p, u16p, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float)]),
         "or_bf16_dot_row": (C.c_float, [f32p, u16p, C.c_int, C.c_int]),
+        "or_rms_norm": (None, [f32p, f32p, f32p, C.c_int, C.c_float]),
+        "or_residual_rms_norm": (None, [f32p, f32p, f32p, f32p, f32p, C.c_int, C.c_float]),
+        "or_rope_row": (None, [f32p, f32p, C.c_int, C.c_int, C.c_float]),
+        "or_apply_rope": (None, [f32p, f32p, f32p, C.c_int, C.c_int]),
+        "or_rms_norm_per_head": (None, [f32p, f32p, C.c_int, C.c_int, C.c_float]),
+        "or_dot_f32": (C.c_float, [f32p, f32p, C.c_int]),
+        "or_attn_ranges": (C.c_int, [i32p, C.c_int, C.c_int, C.c_int]),
+        "or_attention_decode": (None, [f32p, f32p, f32p, f32p, C.c_int, C.c_int, C.c_float, C.c_int, i32p, C.c_int]),
+        "or_qkv": (None, [f32p, f32p, f32p, f32p, u16p, u16p, u16p, C.c_int, C.c_int, C.c_int, C.c_int]),
+        "or_decoder_attn": (None, [f32p, f32p, f32p, C.c_void_p, f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int]),
         "or_lm_sample_greedy": (C.c_int, [f32p, u16p, C.c_int, C.c_int, i32p_opt, C.c_int, C.c_float, C.c_int,
                                            C.c_int, C.c_void_p]),
         "or_linear_f32": (None, [f32p, f32p, f32p, C.c_int, C.c_int]),
@@ -127,6 +146,18 @@ def ref(variant="v4"):
         "ref_moe_layer": (None, [f32p, f32p, vp, C.c_int, i32p_opt, f32p_opt]),
         "ref_decode_steps": (C.c_double, [vp, C.c_int, u16p, C.c_int, f32p, C.c_int, C.c_int, i32p]),
         "ref_decode_hidden": (None, [f32p, vp, C.c_int, f32p, C.c_int]),
+        "ds_set_threads": (None, [C.c_int]),
+        "ds_rms_norm": (None, [f32p, f32p, f32p, C.c_int, C.c_int, C.c_float]),
+        "ds_residual_rms_norm": (None, [f32p, f32p, f32p, f32p, f32p, C.c_int, C.c_float]),
+        "ds_compute_rope_neox": (None, [f32p, f32p, i32p, C.c_int, C.c_int, C.c_float]),
+        "ds_apply_rope_neox": (None, [f32p, f32p, f32p, C.c_int, C.c_int, C.c_int]),
+        "ds_rms_norm_per_head": (None, [f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_float]),
+        "ds_linear_nobias_bf16_qkv": (None, [f32p, f32p, f32p, f32p, u16p, u16p, u16p, C.c_int, C.c_int, C.c_int]),
+        "ds_linear_nobias_bf16": (None, [f32p, f32p, u16p, C.c_int, C.c_int, C.c_int]),
+        "ds_causal_attention_aligned": (None, [f32p, f32p, f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                               C.c_float, C.c_int, C.c_int]),
+        "ds_rswa_attention_aligned": (None, [f32p, f32p, f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
+                                             C.c_int, C.c_int, C.c_int, C.c_int]),
         "ds_set_threads": (None, [C.c_int]),
         "ds_get_threads": (C.c_int, []),
         "ds_int4_dequantize_f32": (None, [f32p, vp]),

@@ -457,6 +457,204 @@ int or_lm_sample_greedy(const float *x, const uint16_t *W, int in_dim, int vocab
   return tok;
 }
 
+/* ---------------------------------------------------------------- decoder attention block */
+
+/* Sum of squares as the AVX-512 branches of ds_rms_norm / ds_rms_norm_per_head compute it
+ * (ds_kernels.c:1387-1440, :1473-1500): 16 lanes of fused squares over the leading multiple of 16,
+ * the reduce tree, then the tail added with fused squares (GCC contracts the scalar line). */
+static float or_sumsq16(const float *x, int n) {
+  float acc[16];
+  for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+  int i = 0;
+  for (; i + 16 <= n; i += 16)
+    for (int l = 0; l < 16; l++) acc[l] = fmaf(x[i + l], x[i + l], acc[l]);
+  float s = tree16(acc);
+  for (; i < n; i++) s = fmaf(x[i], x[i], s);
+  return s;
+}
+
+/* ds_rms_norm for one row, AVX-512 branch: out = (x*w)*r on the leading multiple of 16, then
+ * (x*r)*w on the tail, r = 1/sqrtf(sum/n + eps). */
+void or_rms_norm(float *out, const float *x, const float *w, int n, float eps) {
+  float r = 1.0f / sqrtf(or_sumsq16(x, n) / n + eps);
+  int j = 0;
+  for (; j + 16 <= n; j += 16)
+    for (int l = 0; l < 16; l++) out[j + l] = (x[j + l] * w[j + l]) * r;
+  for (; j < n; j++) out[j] = x[j] * r * w[j];
+}
+
+/* ds_residual_rms_norm, AVX-512 branch (ds_kernels.c:1544-1600): out = x + res (rounded), the
+ * squares of out summed as above, norm_out as or_rms_norm. */
+void or_residual_rms_norm(float *out, float *norm_out, const float *x, const float *res, const float *w, int n,
+                          float eps) {
+  for (int i = 0; i < n; i++) out[i] = x[i] + res[i];
+  or_rms_norm(norm_out, out, w, n, eps);
+}
+
+/* ds_compute_rope_neox for one position (ds_kernels.c:2407-2424): the host libm's powf, cosf, sinf. */
+void or_rope_row(float *cos_out, float *sin_out, int pos, int head_dim, float theta) {
+  int half = head_dim / 2;
+  for (int d = 0; d < half; d++) {
+    float freq = 1.0f / powf(theta, (float)(2 * d) / (float)head_dim);
+    float angle = (float)pos * freq;
+    cos_out[d] = cos_out[d + half] = cosf(angle);
+    sin_out[d] = sin_out[d + half] = sinf(angle);
+  }
+}
+
+/* ds_apply_rope_neox for one token (ds_kernels.c:2426-2455); GCC fuses the first product of each
+ * line into the subtraction / addition (fmaf(x1, c, -(x2*s)) and fmaf(x1, s, x2*c)). */
+void or_apply_rope(float *x, const float *c, const float *sn, int n_heads, int head_dim) {
+  int half = head_dim / 2;
+  for (int h = 0; h < n_heads; h++) {
+    float *v = x + h * head_dim;
+    for (int d = 0; d < half; d++) {
+      float x1 = v[d], x2 = v[d + half];
+      v[d] = fmaf(x1, c[d], -(x2 * sn[d]));
+      v[d + half] = fmaf(x1, sn[d + half], x2 * c[d + half]);
+    }
+  }
+}
+
+/* ds_rms_norm_per_head, AVX-512 branch (in place). */
+void or_rms_norm_per_head(float *x, const float *w, int n_heads, int head_dim, float eps) {
+  for (int h = 0; h < n_heads; h++) or_rms_norm(x + h * head_dim, x + h * head_dim, w, head_dim, eps);
+}
+
+/* ds_dot_f32_avx, AVX-512 branch (ds_kernels_avx.c:357-377): four 16-lane accumulators over
+ * 64-element blocks, added pairwise, 16-element steps, the reduce tree, fused tail. */
+float or_dot_f32(const float *a, const float *b, int n) {
+  float a0[16], a1[16], a2[16], a3[16], acc[16];
+  for (int l = 0; l < 16; l++) a0[l] = a1[l] = a2[l] = a3[l] = 0.0f;
+  int i = 0;
+  for (; i + 64 <= n; i += 64)
+    for (int l = 0; l < 16; l++) {
+      a0[l] = fmaf(a[i + l], b[i + l], a0[l]);
+      a1[l] = fmaf(a[i + 16 + l], b[i + 16 + l], a1[l]);
+      a2[l] = fmaf(a[i + 32 + l], b[i + 32 + l], a2[l]);
+      a3[l] = fmaf(a[i + 48 + l], b[i + 48 + l], a3[l]);
+    }
+  for (int l = 0; l < 16; l++) acc[l] = (a0[l] + a1[l]) + (a2[l] + a3[l]);
+  for (; i + 16 <= n; i += 16)
+    for (int l = 0; l < 16; l++) acc[l] = fmaf(a[i + l], b[i + l], acc[l]);
+  float s = tree16(acc);
+  for (; i < n; i++) s = fmaf(a[i], b[i], s);
+  return s;
+}
+
+/* One head of single-token MHA decode attention over the KV rows in [r0, r1) then [r2, r3)
+ * (ds_kernels.c:2124-2160 causal: one range; :2270-2330 R-SWA: reference then window): online
+ * softmax with ds_fast_expf; on a new maximum sum_e = fma(sum_e, corr, 1) and o = o*corr + v
+ * (ds_vec_scale_add), otherwise sum_e += wt and o += wt*v (ds_vec_axpy_inplace); then o *= 1/sum_e. */
+static void or_attn_head(float *o, const float *q, const float *kh, const float *vh, int head_dim, float scale,
+                         int kv_stride, const int *rng, int nrng) {
+  float max_s = -1e30f, sum_e = 0.0f;
+  for (int d = 0; d < head_dim; d++) o[d] = 0.0f;
+  for (int r = 0; r < nrng; r++)
+    for (int j = rng[2 * r]; j < rng[2 * r + 1]; j++) {
+      const float *kr = kh + (size_t)j * kv_stride, *vr = vh + (size_t)j * kv_stride;
+      float score = or_dot_f32(q, kr, head_dim) * scale;
+      if (score > max_s) {
+        float corr = or_fast_expf(max_s - score);
+        sum_e = fmaf(sum_e, corr, 1.0f);  /* GCC contracts the reference's sum_e * corr + 1.0f */
+        for (int d = 0; d < head_dim; d++) o[d] = fmaf(o[d], corr, vr[d]);
+        max_s = score;
+      } else {
+        float wt = or_fast_expf(score - max_s);
+        sum_e += wt;
+        for (int d = 0; d < head_dim; d++) o[d] = fmaf(vr[d], wt, o[d]);
+      }
+    }
+  if (sum_e > 0.0f) {
+    float inv = 1.0f / sum_e;
+    for (int d = 0; d < head_dim; d++) o[d] = o[d] * inv;
+  }
+}
+
+/* The KV ranges decoder_layer_forward attends to for the token at cache position pos
+ * (ds_moe_decoder.c:396-423): [0, pos+1), or with R-SWA (window > 0, pos >= prefill_len) the
+ * reference tokens [0, prefill_len) and the window [max(prefill_len, pos+1-window), pos+1) when
+ * they do not touch. Returns the number of ranges. */
+int or_attn_ranges(int *rng, int pos, int prefill_len, int window) {
+  int kv = pos + 1;
+  if (window > 0 && pos >= prefill_len) {
+    int ws = prefill_len > kv - window ? prefill_len : kv - window;
+    if (ws > prefill_len) {
+      rng[0] = 0;
+      rng[1] = prefill_len;
+      rng[2] = ws;
+      rng[3] = kv;
+      return 2;
+    }
+  }
+  rng[0] = 0;
+  rng[1] = kv;
+  return 1;
+}
+
+void or_attention_decode(float *out, const float *Q, const float *K, const float *V, int n_heads, int head_dim,
+                         float scale, int kv_stride, const int *rng, int nrng) {
+  for (int h = 0; h < n_heads; h++)
+    or_attn_head(out + h * head_dim, Q + h * head_dim, K + h * head_dim, V + h * head_dim, head_dim, scale,
+                 kv_stride, rng, nrng);
+}
+
+/* ds_linear_nobias_bf16_qkv (ds_kernels.c:844-915): rows of [q; k; v] chunked over the threads,
+ * each thread's part of each matrix one ds_bf16_matvec_fused range. */
+void or_qkv(float *q, float *k, float *v, const float *x, const uint16_t *Wq, const uint16_t *Wk, const uint16_t *Wv,
+            int in_dim, int q_dim, int kv_dim, int nthreads) {
+  if (nthreads <= 1) {
+    matvec_range_avx512(q, x, Wq, in_dim, 0, q_dim);
+    matvec_range_avx512(k, x, Wk, in_dim, 0, kv_dim);
+    matvec_range_avx512(v, x, Wv, in_dim, 0, kv_dim);
+    return;
+  }
+  int total = q_dim + 2 * kv_dim, chunk = (total + nthreads - 1) / nthreads;
+  int ends[3] = {q_dim, q_dim + kv_dim, total};
+  float *ys[3] = {q, k, v};
+  const uint16_t *Ws[3] = {Wq, Wk, Wv};
+  for (int t = 0; t < nthreads; t++) {
+    int start = t * chunk, end = start + chunk;
+    if (end > total) end = total;
+    if (start >= end) continue;
+    for (int m = 0; m < 3; m++) {
+      int base = m ? ends[m - 1] : 0;
+      int s = start > base ? start - base : 0;
+      int e = (end < ends[m] ? end : ends[m]) - base;
+      if (s < e) matvec_range_avx512(ys[m] + s, x, Ws[m], in_dim, s, e);
+    }
+  }
+}
+
+/* The attention half of decoder_layer_forward for one token (ds_moe_decoder.c:339-431, MHA):
+ * x_norm = RMSNorm(x); q, k, v; optional per-head q/k norms; RoPE at pos; k and v stored in the
+ * caches' row pos; attention over or_attn_ranges; h = x + Wo·attn; n = RMSNorm(h). h and n are
+ * what the MLP and its residual take. */
+void or_decoder_attn(float *h, float *n, const float *x, const or_attn_t *A, float *Kc, float *Vc, int pos,
+                     int prefill_len, int window, int nthreads) {
+  int H = A->hidden, qd = A->n_heads * A->head_dim;
+  float *xn = (float *)malloc((size_t)H * 4), *q = (float *)malloc((size_t)qd * 4);
+  float *k = (float *)malloc((size_t)qd * 4), *v = (float *)malloc((size_t)qd * 4);
+  float *att = (float *)malloc((size_t)qd * 4), *proj = (float *)malloc((size_t)H * 4);
+  float *c = (float *)malloc((size_t)A->head_dim * 4), *sn = (float *)malloc((size_t)A->head_dim * 4);
+  or_rms_norm(xn, x, A->input_norm, H, A->eps);
+  or_qkv(q, k, v, xn, A->wq, A->wk, A->wv, H, qd, qd, nthreads);
+  if (A->q_norm) or_rms_norm_per_head(q, A->q_norm, A->n_heads, A->head_dim, A->eps);
+  if (A->k_norm) or_rms_norm_per_head(k, A->k_norm, A->n_heads, A->head_dim, A->eps);
+  or_rope_row(c, sn, pos, A->head_dim, A->theta);
+  or_apply_rope(q, c, sn, A->n_heads, A->head_dim);
+  or_apply_rope(k, c, sn, A->n_heads, A->head_dim);
+  memcpy(Kc + (size_t)pos * A->kv_stride, k, (size_t)qd * 4);
+  memcpy(Vc + (size_t)pos * A->kv_stride, v, (size_t)qd * 4);
+  int rng[4];
+  int nr = or_attn_ranges(rng, pos, prefill_len, window);
+  or_attention_decode(att, q, Kc, Vc, A->n_heads, A->head_dim, 1.0f / sqrtf((float)A->head_dim), A->kv_stride,
+                      rng, nr);
+  or_bf16_matvec_avx512(proj, att, A->wo, qd, H, nthreads);
+  or_residual_rms_norm(h, n, x, proj, A->post_norm, H, A->eps);
+  free(xn), free(q), free(k), free(v), free(att), free(proj), free(c), free(sn);
+}
+
 /* ---------------------------------------------------------------- router */
 
 /* ds_linear without USE_BLAS (ds_kernels.c:639-652), as GCC 11 -O3 (AVX-512) compiles its inner

@@ -77,6 +77,29 @@ float or_bf16_dot_row(const float *x, const uint16_t *W, int in_dim, int row);
 int or_lm_sample_greedy(const float *x, const uint16_t *W, int in_dim, int vocab, const int *hist, int hist_len,
                         float repeat_penalty, int ngram_n, int nthreads, int *used_full);
 
+/* ---------------- decoder attention block (single-token decode, MHA) ---------------- */
+typedef struct {
+  int hidden, n_heads, head_dim, kv_stride; /* kv_stride: floats between cache rows (>= n_heads*head_dim) */
+  float eps, theta;
+  const uint16_t *wq, *wk, *wv, *wo;        /* bf16 [n_heads*head_dim][hidden] x3, [hidden][n_heads*head_dim] */
+  const float *input_norm, *post_norm;      /* [hidden] */
+  const float *q_norm, *k_norm;             /* [head_dim] or NULL */
+} or_attn_t;
+void or_rms_norm(float *out, const float *x, const float *w, int n, float eps);
+void or_residual_rms_norm(float *out, float *norm_out, const float *x, const float *res, const float *w, int n,
+                          float eps);
+void or_rope_row(float *cos_out, float *sin_out, int pos, int head_dim, float theta);
+void or_apply_rope(float *x, const float *c, const float *sn, int n_heads, int head_dim);
+void or_rms_norm_per_head(float *x, const float *w, int n_heads, int head_dim, float eps);
+float or_dot_f32(const float *a, const float *b, int n);
+int or_attn_ranges(int *rng, int pos, int prefill_len, int window);
+void or_attention_decode(float *out, const float *Q, const float *K, const float *V, int n_heads, int head_dim,
+                         float scale, int kv_stride, const int *rng, int nrng);
+void or_qkv(float *q, float *k, float *v, const float *x, const uint16_t *Wq, const uint16_t *Wk, const uint16_t *Wv,
+            int in_dim, int q_dim, int kv_dim, int nthreads);
+void or_decoder_attn(float *h, float *n, const float *x, const or_attn_t *A, float *Kc, float *Vc, int pos,
+                     int prefill_len, int window, int nthreads);
+
 /* ---------------- router ---------------- */
 /* ds_linear without BLAS, seq=1 (ds_kernels.c:639-652): sequential fused chain per row. */
 void or_linear_f32(float *y, const float *x, const float *W, int in_dim, int out_dim);
