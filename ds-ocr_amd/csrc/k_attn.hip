@@ -1,0 +1,391 @@
+// k_attn.hip — the attention half of one decoder layer for one token (decoder_layer_forward,
+// ds_moe_decoder.c:339-431; MHA, single-token decode) on the device, as four launches:
+//   k_attn_qkv   : x_norm = ds_rms_norm(x) in its AVX-512 order (recomputed by every block), then
+//                  the rows of [Wq; Wk; Wv] in ds_linear_nobias_bf16_qkv's AVX-512 order with its
+//                  split of the rows over the reference's threads (ds_kernels.c:844-915); v goes
+//                  straight into the V cache row pos;
+//   k_attn_core  : one block per head: the optional per-head q/k norms, RoPE from the position's
+//                  cos/sin row (ds_apply_rope_neox), the roped k into the K cache row pos, then the
+//                  online-softmax attention over the causal or R-SWA ranges (see below);
+//   k_attn_oproj : proj = Wo·att in ds_bf16_matvec_threaded's order;
+//   k_attn_post  : h = x + proj and n = ds_rms_norm(h) (ds_residual_rms_norm, AVX-512 order).
+// Everything except the attention's output accumulation is bit-exact with the reference. The
+// reference's attention is a sequential online softmax with ds_fast_expf (ds_kernels.c:2124-2160,
+// :2270-2330). Its branch at each position depends only on the running maximum, so this kernel
+// takes the same branches with the same exp arguments: a prefix-max scan gives each position's
+// running maximum P, its factor f = fast_exp(P - s) on a new maximum (the correction) or
+// fast_exp(s - P) (its weight), and a suffix product of the later corrections gives each V row's
+// final coefficient c; o = sum c*v and sum_e = sum c are then sums in any order. The result differs
+// from the reference's sequential recurrence by f32 rounding only.
+#include "dsh.h"
+#include "dsh_avx.h"
+#include "k_core.h"
+
+__device__ __forceinline__ int attn_pos(const int *pos_ptr, int pos_add) { return (pos_ptr ? *pos_ptr : 0) + pos_add; }
+
+// ds_rms_norm's sum of squares (AVX-512 branch): 16 lanes of fused squares over n/16 steps, then
+// the reduce tree. Called by all threads; x in LDS, n % 16 == 0. Returns r = 1/sqrtf(sum/n + eps)
+// to every thread (s_r: one LDS float).
+__device__ float attn_rms_scale(const float *x, int n, float eps, float *s_r) {
+  if (threadIdx.x < 16) {
+    float acc = 0.0f;
+    for (int i = 0; i < n; i += 16) acc = __builtin_fmaf(x[i + threadIdx.x], x[i + threadIdx.x], acc);
+    // tree16: T3[i] = A[8+i] + A[i]; T6[j] = T3[4+j] + T3[j]; (T6[0]+T6[2]) + (T6[1]+T6[3])
+    const float t3 = __shfl_down(acc, 8, 16) + acc;
+    const float t6 = __shfl_down(t3, 4, 16) + t3;
+    const float t02 = __shfl_down(t6, 2, 16) + t6;  // lane 0: T6[0]+T6[2]; lane 1: T6[1]+T6[3]
+    const float s = t02 + __shfl_down(t02, 1, 16);
+    if (threadIdx.x == 0) *s_r = 1.0f / __builtin_sqrtf(s / (float)n + eps);
+  }
+  __syncthreads();
+  return *s_r;
+}
+
+// Path of global row R of [q; k; v] under ds_linear_nobias_bf16_qkv's split: thread t takes rows
+// [t*chunk, min((t+1)*chunk, total)) and runs one ds_bf16_matvec_fused per matrix over its part.
+__device__ __forceinline__ int qkv_row_path(int R, int q_dim, int kv_dim, int nthreads) {
+  const int total = q_dim + 2 * kv_dim;
+  const int m = R < q_dim ? 0 : (R < q_dim + kv_dim ? 1 : 2);
+  const int base = m == 0 ? 0 : (m == 1 ? q_dim : q_dim + kv_dim);
+  const int mend = m == 0 ? q_dim : (m == 1 ? q_dim + kv_dim : total);
+  int s = base, e = mend;
+  if (nthreads > 1) {
+    const int chunk = (total + nthreads - 1) / nthreads;
+    const int t = R / chunk;
+    s = max(t * chunk, base);
+    e = min(min((t + 1) * chunk, total), mend);
+  }
+  const int len = e - s, off = R - s;
+  if (off < (len & ~3)) return DSH_ROW_GROUP4;
+  return off < (len & ~1) ? DSH_ROW_GROUP2 : DSH_ROW_SINGLE;
+}
+
+// One bf16 row of length 32*N32 against x (LDS) at lane L of its 4-lane group, in the path's order.
+template <int N32>
+__device__ __forceinline__ float attn_row(const uint16_t *w, const u32x4 *wv, const float *x, int L, int path) {
+  if (path == DSH_ROW_SINGLE) return avx_row<true>(w, x, 32 * N32, L, true, true, 0.0f, true);
+  return avx_row_regs32<N32>(wv, x, L, true, 0.0f);
+}
+
+// Every lane's 16-byte pieces of its row (columns 32i + 8L .. +7), issued together.
+template <int N32>
+__device__ __forceinline__ void attn_row_load(u32x4 *wv, const uint16_t *w, int L) {
+#pragma unroll
+  for (int i = 0; i < N32; i++) wv[i] = ((const u32x4 *)w)[4 * i + L];
+}
+
+// ---------------------------------------------------------------------------- QKV
+// 64 rows of [q; k; v] per 256-thread block (4 lanes per row). H == 32*N32.
+template <int N32>
+__global__ void __launch_bounds__(256) k_attn_qkv(dsh_attn_t A, const float *x_in, const int *step, int stride,
+                                                  const int *pos_ptr, int pos_add, int nthreads) {
+  constexpr int H = 32 * N32;
+  __shared__ __attribute__((aligned(16))) float s_x[H];
+  __shared__ float s_r;
+  const int qd = A.n_heads * A.head_dim, total = 3 * qd;
+  const int L = threadIdx.x & 3;
+  const int R = blockIdx.x * 64 + (threadIdx.x >> 2);
+  const int Rc = R < total ? R : total - 1;
+  const int m = Rc < qd ? 0 : (Rc < 2 * qd ? 1 : 2), r = Rc - m * qd;
+  const uint16_t *w = (m == 0 ? A.wq : (m == 1 ? A.wk : A.wv)) + (size_t)r * H;
+  const int path = qkv_row_path(Rc, qd, qd, nthreads);
+  u32x4 wv[N32];
+  if (path != DSH_ROW_SINGLE) attn_row_load<N32>(wv, w, L);
+  const float *x = step ? x_in + (size_t)(*step) * stride : x_in;
+  for (int i = threadIdx.x; i < H / 4; i += 256) ((f32x4 *)s_x)[i] = ((const f32x4 *)x)[i];
+  __syncthreads();
+  const float rs = attn_rms_scale(s_x, H, A.eps, &s_r);
+  float xn[(H + 255) / 256];
+#pragma unroll
+  for (int k = 0; k < (H + 255) / 256; k++) {
+    const int i = threadIdx.x + 256 * k;
+    if (i < H) xn[k] = (s_x[i] * A.in_norm[i]) * rs;
+  }
+  __syncthreads();  // every thread has read s_x
+#pragma unroll
+  for (int k = 0; k < (H + 255) / 256; k++) {
+    const int i = threadIdx.x + 256 * k;
+    if (i < H) s_x[i] = xn[k];
+  }
+  __syncthreads();
+  const float v = attn_row<N32>(w, wv, s_x, L, path);
+  if (L == 0 && R < total) {
+    if (m == 0)
+      A.q[r] = v;
+    else if (m == 1)
+      A.k[r] = v;
+    else
+      A.vc[(size_t)attn_pos(pos_ptr, pos_add) * A.kv_stride + r] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------- attention core
+#define ATTN_THREADS 256
+
+// Inclusive scan over the block's threads (ATTN_THREADS) with an associative op; s_w: 4 floats.
+template <typename Op>
+__device__ __forceinline__ float attn_block_scan(float v, Op op, float *s_w) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float u = __shfl_up(v, o);
+    if (lane >= o) v = op(u, v);
+  }
+  if (lane == 63) s_w[wave] = v;
+  __syncthreads();
+  for (int w = 0; w < wave; w++) v = op(s_w[w], v);
+  __syncthreads();
+  return v;
+}
+
+// ds_dot_f32 in its AVX-512 order for n % 64 == 0 (ds_kernels_avx.c:357-377): four 16-lane
+// accumulators over 64-element blocks, added pairwise, then the reduce tree. q in LDS, k global.
+__device__ __forceinline__ float attn_dot(const float *q, const float *k, int n) {
+  float a[4][16];
+#pragma unroll
+  for (int m = 0; m < 4; m++)
+#pragma unroll
+    for (int l = 0; l < 16; l++) a[m][l] = 0.0f;
+  for (int i = 0; i < n; i += 64) {
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const f32x4 kv = ((const f32x4 *)(k + i + 16 * m))[c];
+        const f32x4 qv = ((const f32x4 *)(q + i + 16 * m))[c];
+#pragma unroll
+        for (int e = 0; e < 4; e++) a[m][4 * c + e] = __builtin_fmaf(qv[e], kv[e], a[m][4 * c + e]);
+      }
+    }
+  }
+  float A16[16];
+#pragma unroll
+  for (int l = 0; l < 16; l++) A16[l] = (a[0][l] + a[1][l]) + (a[2][l] + a[3][l]);
+  float T3[8], T6[4];
+#pragma unroll
+  for (int i = 0; i < 8; i++) T3[i] = A16[8 + i] + A16[i];
+#pragma unroll
+  for (int j = 0; j < 4; j++) T6[j] = T3[4 + j] + T3[j];
+  return (T6[0] + T6[2]) + (T6[1] + T6[3]);
+}
+
+// One block per head; dynamic LDS: 2 * max_kv floats (scores / factors, coefficients).
+__global__ void __launch_bounds__(ATTN_THREADS) k_attn_core(dsh_attn_t A, const int *pos_ptr, int pos_add,
+                                                            int prefill_len, int window, int max_kv) {
+  extern __shared__ __attribute__((aligned(16))) float s_dyn[];
+  __shared__ __attribute__((aligned(16))) float s_q[DSH_ATTN_MAX_HD], s_k[DSH_ATTN_MAX_HD];
+  __shared__ float s_w[4], s_r;
+  __shared__ __attribute__((aligned(16))) float s_o[ATTN_THREADS];
+  float *s_s = s_dyn, *s_c = s_dyn + max_kv;
+  const int h = blockIdx.x, hd = A.head_dim, half = hd / 2, tid = threadIdx.x;
+  const int pos = attn_pos(pos_ptr, pos_add);
+  const float *cs = A.rope_cos + (size_t)pos * hd, *sn = A.rope_sin + (size_t)pos * hd;
+  // raw q and k of this head; the optional per-head norms (ds_rms_norm_per_head), then RoPE
+  if (tid < hd) {
+    s_q[tid] = A.q[h * hd + tid];
+    s_k[tid] = A.k[h * hd + tid];
+  }
+  __syncthreads();
+  for (int which = 0; which < 2; which++) {
+    const float *nw = which ? A.k_norm : A.q_norm;
+    float *v = which ? s_k : s_q;
+    if (nw) {
+      const float r = attn_rms_scale(v, hd, A.eps, &s_r);
+      float y = 0.0f;
+      if (tid < hd) y = (v[tid] * nw[tid]) * r;
+      __syncthreads();
+      if (tid < hd) v[tid] = y;
+      __syncthreads();
+    }
+  }
+  float rq = 0.0f, rk = 0.0f;
+  if (tid < hd) {
+    const int d = tid < half ? tid : tid - half;
+    const float q1 = s_q[d], q2 = s_q[d + half], k1 = s_k[d], k2 = s_k[d + half];
+    if (tid < half) {
+      rq = __builtin_fmaf(q1, cs[d], -(q2 * sn[d]));
+      rk = __builtin_fmaf(k1, cs[d], -(k2 * sn[d]));
+    } else {
+      rq = __builtin_fmaf(q1, sn[tid], q2 * cs[tid]);
+      rk = __builtin_fmaf(k1, sn[tid], k2 * cs[tid]);
+    }
+  }
+  __syncthreads();
+  if (tid < hd) {
+    s_q[tid] = rq;
+    s_k[tid] = rk;
+    A.kc[(size_t)pos * A.kv_stride + h * hd + tid] = rk;
+  }
+  __syncthreads();
+  // the attended positions: [0, pos+1), or R-SWA's reference tokens and window
+  const int kv = pos + 1;
+  int r0 = 0, r1 = kv, r2 = kv, r3 = kv;
+  if (window > 0 && pos >= prefill_len) {
+    const int ws = prefill_len > kv - window ? prefill_len : kv - window;
+    if (ws > prefill_len) {
+      r1 = prefill_len;
+      r2 = ws;
+    }
+  }
+  const int n = (r1 - r0) + (r3 - r2);
+  const float scale = 1.0f / __builtin_sqrtf((float)hd);
+  auto jpos = [&](int p) { return p < r1 ? p : r2 + (p - r1); };
+  // scores, bit-exact (the token's own k from LDS)
+  for (int p = tid; p < n; p += ATTN_THREADS) {
+    const int j = jpos(p);
+    const float *kr = j == pos ? s_k : A.kc + (size_t)j * A.kv_stride + h * hd;
+    s_s[p] = attn_dot(s_q, kr, hd) * scale;
+  }
+  __syncthreads();
+  // running maximum before each position: exclusive prefix max over contiguous segments
+  const int seg = (n + ATTN_THREADS - 1) / ATTN_THREADS;
+  const int p0 = min(tid * seg, n), p1 = min(p0 + seg, n);
+  float sm = -__builtin_huge_valf();
+  for (int p = p0; p < p1; p++) sm = fmaxf(sm, s_s[p]);
+  const float incl = attn_block_scan(sm, [](float a, float b) { return fmaxf(a, b); }, s_w);
+  s_o[tid] = incl;
+  __syncthreads();
+  // the reference starts from max_s = -1e30 (a NaN score is never a new maximum: fmaxf skips it)
+  float P = fmaxf(-1e30f, tid ? s_o[tid - 1] : -__builtin_huge_valf());
+  __syncthreads();
+  // factors: a = correction on a new maximum (else 1), g = 1 on a new maximum (else the weight);
+  // s_s[p] <- a, s_c[p] <- g
+  float prod = 1.0f;
+  for (int p = p0; p < p1; p++) {
+    const float s = s_s[p];
+    const bool nm = s > P;
+    const float f = dsh_fast_expf(nm ? P - s : s - P);
+    s_s[p] = nm ? f : 1.0f;
+    s_c[p] = nm ? 1.0f : f;
+    prod *= nm ? f : 1.0f;
+    P = nm ? s : P;
+  }
+  // product of the corrections after each segment: exclusive suffix product over the threads
+  __syncthreads();
+  s_o[tid] = prod;
+  __syncthreads();
+  float after = 1.0f;
+  for (int t = ATTN_THREADS - 1; t > tid; t--) after *= s_o[t];
+  for (int p = p1 - 1; p >= p0; p--) {
+    s_c[p] *= after;  // c = g * (product of the later corrections)
+    after *= s_s[p];
+  }
+  __syncthreads();
+  // o = sum c*v over the positions, split into ATTN_THREADS / hd parts; sum_e = sum c
+  const int parts = ATTN_THREADS / hd, part = tid / hd, d = tid - part * hd;
+  float acc = 0.0f, csum = 0.0f;
+  if (part < parts) {
+    const int pa = n * part / parts, pb = n * (part + 1) / parts;
+    for (int p = pa; p < pb; p++) {
+      const float c = s_c[p];
+      acc = __builtin_fmaf(c, A.vc[(size_t)jpos(p) * A.kv_stride + h * hd + d], acc);
+      csum += c;
+    }
+  }
+  __syncthreads();
+  s_o[tid] = acc;
+  if (d == 0) s_s[part] = csum;  // the scores area is free now
+  __syncthreads();
+  if (tid < hd) {
+    float o = 0.0f, se = 0.0f;
+    for (int k = 0; k < parts; k++) {
+      o += s_o[k * hd + tid];
+      se += s_s[k];
+    }
+    if (se > 0.0f) o = o * (1.0f / se);
+    A.att[h * hd + tid] = o;
+  }
+}
+
+// ---------------------------------------------------------------------------- O projection
+// 64 output rows per 256-thread block; att (q_dim == 32*N32) staged in LDS.
+template <int N32>
+__global__ void __launch_bounds__(256) k_attn_oproj(dsh_attn_t A, int chunk) {
+  constexpr int QD = 32 * N32;
+  __shared__ __attribute__((aligned(16))) float s_a[QD];
+  const int L = threadIdx.x & 3;
+  const int r = blockIdx.x * 64 + (threadIdx.x >> 2);
+  const int rc = r < A.H ? r : A.H - 1;
+  const uint16_t *w = A.wo + (size_t)rc * QD;
+  const int path = row_path(rc, A.H, chunk, false);
+  u32x4 wv[N32];
+  if (path != DSH_ROW_SINGLE) attn_row_load<N32>(wv, w, L);
+  for (int i = threadIdx.x; i < QD / 4; i += 256) ((f32x4 *)s_a)[i] = ((const f32x4 *)A.att)[i];
+  __syncthreads();
+  const float v = attn_row<N32>(w, wv, s_a, L, path);
+  if (L == 0 && r < A.H) A.proj[r] = v;
+}
+
+// ---------------------------------------------------------------------------- residual RMSNorm
+// One 256-thread block: h = x + proj (rounded), n = (h*w)*r (ds_residual_rms_norm, AVX-512).
+template <int N32>
+__global__ void __launch_bounds__(256) k_attn_post(dsh_attn_t A, const float *x_in, const int *step, int stride,
+                                                   float *h_out, float *n_out) {
+  constexpr int H = 32 * N32;
+  __shared__ __attribute__((aligned(16))) float s_h[H];
+  __shared__ float s_r;
+  const float *x = step ? x_in + (size_t)(*step) * stride : x_in;
+  for (int i = threadIdx.x; i < H; i += 256) {
+    const float v = x[i] + A.proj[i];
+    s_h[i] = v;
+    h_out[i] = v;
+  }
+  __syncthreads();
+  const float r = attn_rms_scale(s_h, H, A.eps, &s_r);
+  for (int i = threadIdx.x; i < H; i += 256) n_out[i] = (s_h[i] * A.post_norm[i]) * r;
+}
+
+extern "C" {
+
+int dsh_attn_supported(int H, int n_heads, int head_dim) {
+  const int qd = n_heads * head_dim;
+  return H % 256 == 0 && H / 256 >= 1 && H / 256 <= 8 && head_dim % 64 == 0 && head_dim <= DSH_ATTN_MAX_HD &&
+         head_dim <= ATTN_THREADS && qd % 256 == 0 && qd / 256 >= 1 && qd / 256 <= 8;
+}
+
+// scores/factors and coefficients; at least 8 floats (the per-part sums reuse the first ones)
+size_t dsh_attn_core_lds(int max_kv) { return (size_t)(2 * max_kv > 8 ? 2 * max_kv : 8) * sizeof(float); }
+
+hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *step, int stride, const int *pos_ptr,
+                           int pos_add, int prefill_len, int window, int max_kv, int nthreads, float *h_out,
+                           float *n_out, hipStream_t s) {
+  if (!dsh_attn_supported(A->H, A->n_heads, A->head_dim)) return hipErrorInvalidValue;
+  const int qd = A->n_heads * A->head_dim;
+#define QKV(N)                                                                                     \
+  case N:                                                                                          \
+    k_attn_qkv<8 * N><<<(3 * qd + 63) / 64, 256, 0, s>>>(*A, x_in, step, stride, pos_ptr, pos_add, \
+                                                          nthreads);                               \
+    break;
+  switch (A->H / 256) {
+    QKV(1) QKV(2) QKV(3) QKV(4) QKV(5) QKV(6) QKV(7) QKV(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef QKV
+  k_attn_core<<<A->n_heads, ATTN_THREADS, dsh_attn_core_lds(max_kv), s>>>(*A, pos_ptr, pos_add, prefill_len, window,
+                                                                         max_kv > 4 ? max_kv : 4);
+  const int chunk = dsh_chunk_len(A->H, nthreads);
+#define OP(N)                                                             \
+  case N:                                                                 \
+    k_attn_oproj<8 * N><<<(A->H + 63) / 64, 256, 0, s>>>(*A, chunk);      \
+    break;
+  switch (qd / 256) {
+    OP(1) OP(2) OP(3) OP(4) OP(5) OP(6) OP(7) OP(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef OP
+#define PO(N)                                                                        \
+  case N:                                                                            \
+    k_attn_post<8 * N><<<1, 256, 0, s>>>(*A, x_in, step, stride, h_out, n_out);      \
+    break;
+  switch (A->H / 256) {
+    PO(1) PO(2) PO(3) PO(4) PO(5) PO(6) PO(7) PO(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef PO
+  return hipGetLastError();
+}
+
+}  // extern "C"

@@ -93,6 +93,25 @@ hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int
 /* ---- latency-oriented decode kernels (k_dec.hip) ---- */
 int dsh_dec_supported(int H, int I, int E, int K, int SI);
 int dsh_dec_partials(int H); /* partial score rows written per layer in CFG mode */
+/* ---- attention half of a decoder layer, one token (k_attn.hip) ---- */
+#define DSH_ATTN_MAX_HD 256
+typedef struct {
+  const uint16_t *wq, *wk, *wv, *wo;         /* bf16 [qd][H] x3, [H][qd] (qd = n_heads*head_dim) */
+  const float *in_norm, *post_norm;          /* [H] */
+  const float *q_norm, *k_norm;              /* [head_dim] or NULL */
+  const float *rope_cos, *rope_sin;          /* [max_seq][head_dim] */
+  float *kc, *vc;                            /* [max_seq][kv_stride] */
+  float *q, *k, *att, *proj;                 /* scratch: [qd] x3, [H] */
+  int H, n_heads, head_dim, kv_stride, max_seq;
+  float eps;
+} dsh_attn_t;
+int dsh_attn_supported(int H, int n_heads, int head_dim);
+size_t dsh_attn_core_lds(int max_kv);
+/* h_out = x + Wo·attention(...), n_out = RMSNorm(h_out) for the token at cache position
+ * (pos_ptr ? *pos_ptr : 0) + pos_add; x = x_in + (*step)*stride when step != NULL. */
+hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *step, int stride, const int *pos_ptr,
+                           int pos_add, int prefill_len, int window, int max_kv, int nthreads, float *h_out,
+                           float *n_out, hipStream_t s);
 /* ---- greedy token choice with repetition penalty and n-gram ban (k_sample.hip) ---- */
 int dsh_sample_supported(int H);
 /* After the argmax. Stack form (step != NULL): history tokens[0..min(*step - 1, hist_len)), token

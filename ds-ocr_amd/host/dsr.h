@@ -50,4 +50,10 @@ const void *dsr_weight_device(const void *host, size_t bytes);
 /* Emulated reference CPU thread count (ds_set_threads). */
 int dsr_threads(void);
 
+/* Attention half of a decoder layer (ds_hip_attn.c): its launches for one token at cache position
+ * (pos_ptr ? *pos_ptr : 0) + pos_add, input x_in (+ (*step)*stride when step != NULL). */
+struct ds_hip_attn;
+hipError_t ds_hip_attn_enqueue(const struct ds_hip_attn *A, const float *x_in, const int *step, int stride,
+                               const int *pos_ptr, int pos_add, float *h_out, float *n_out);
+
 #endif

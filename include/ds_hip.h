@@ -146,6 +146,34 @@ int ds_hip_arena_save(const char *path, ds_hip_layer_t *const *layers, int n_lay
  * allocated). */
 int ds_hip_arena_load(const char *path, ds_hip_layer_t **layers, int max_layers, uint16_t **lm_head_dev, int *vocab);
 
+/* ---------------- attention half of a decoder layer, one token ---------------- */
+/* decoder_layer_forward up to the MLP (ds_moe_decoder.c:339-431; MHA): x_norm = ds_rms_norm(x),
+ * q/k/v = ds_linear_nobias_bf16_qkv, optional per-head q/k norms, RoPE (ds_compute_rope_neox /
+ * ds_apply_rope_neox), k and v into the F32 KV cache, causal or R-SWA attention
+ * (ds_causal_attention_aligned / ds_rswa_attention_aligned), O projection, then
+ * ds_residual_rms_norm: h = x + proj and n = RMSNorm(h) -- the MLP's input and residual. Every step
+ * but the attention's output sum is bit-exact with the reference; that sum differs by f32 rounding.
+ * No counterpart object in the reference (its layer keeps these in ds_ctx_t). */
+typedef struct ds_hip_attn ds_hip_attn_t;
+#define DS_HIP_ATTN_MAX_SEQ 7680 /* KV positions per layer (the softmax keeps 2 floats per position in LDS) */
+/* Weights: bf16 [n_heads*head_dim][hidden] for wq, wk, wv, bf16 [hidden][n_heads*head_dim] for wo;
+ * norms f32 [hidden] (q_norm, k_norm: [head_dim] or NULL). Host arrays, uploaded. */
+ds_hip_attn_t *ds_hip_attn_create(int hidden, int n_heads, int head_dim, int max_seq, float rms_eps, float rope_theta,
+                                  const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, const uint16_t *wo,
+                                  const float *input_norm, const float *post_attn_norm, const float *q_norm,
+                                  const float *k_norm);
+void ds_hip_attn_destroy(ds_hip_attn_t *A);
+/* R-SWA (Unlimited-OCR): tokens at positions >= prefill_len attend to [0, prefill_len) and the last
+ * sliding_window positions (ds_moe_decoder.c:396-423); sliding_window 0: causal. */
+int ds_hip_attn_set_window(ds_hip_attn_t *A, int prefill_len, int sliding_window);
+/* The device KV caches ([max_seq][kv_stride] f32 each; k rows roped). */
+int ds_hip_attn_kv(const ds_hip_attn_t *A, float **k_cache_dev, float **v_cache_dev, int *kv_stride);
+/* Uploads n_pos cached rows (e.g. from a prefill) from host arrays with row stride host_stride. */
+int ds_hip_attn_load_kv(ds_hip_attn_t *A, const float *k_host, const float *v_host, int n_pos, int host_stride);
+/* One token at cache position pos: writes its k, v into the caches, h_dev = x + O(attention),
+ * n_dev = RMSNorm(h) (device [hidden] each). Asynchronous. */
+int ds_hip_attn_forward(ds_hip_attn_t *A, float *h_dev, float *n_dev, const float *x_dev, int pos);
+
 /* ---------------- decode stack: n MoE layers + argmax LM head ---------------- */
 typedef struct ds_hip_stack ds_hip_stack_t;
 
