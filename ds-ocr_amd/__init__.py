@@ -104,6 +104,7 @@ SIGNATURES = {
     "ds_hip_attn_kv": (C.c_int, [vp, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p), C.POINTER(C.c_int)]),
     "ds_hip_attn_load_kv": (C.c_int, [vp, vp, vp, C.c_int, C.c_int]),
     "ds_hip_attn_forward": (C.c_int, [vp, vp, vp, vp, C.c_int]),
+    "ds_hip_stack_set_attention": (C.c_int, [vp, vp, C.c_int, vp, C.c_float, C.c_int, C.c_int]),
     "ds_hip_stack_set_sampling": (C.c_int, [vp, C.c_float, C.c_int, C.c_int]),
     "ds_hip_lm_head_sample": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, C.c_int, C.c_float, C.c_int, vp]),
     "ds_hip_stack_kernel_name": (C.c_char_p, [vp, C.c_int]),

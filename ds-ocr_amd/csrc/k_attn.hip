@@ -317,22 +317,60 @@ __global__ void __launch_bounds__(256) k_attn_oproj(dsh_attn_t A, int chunk) {
 }
 
 // ---------------------------------------------------------------------------- residual RMSNorm
-// One 256-thread block: h = x + proj (rounded), n = (h*w)*r (ds_residual_rms_norm, AVX-512).
-template <int N32>
+// R rows per 256-thread block (H / R blocks): every block forms h = x + proj (rounded) in LDS and
+// the RMSNorm scale (ds_residual_rms_norm, AVX-512 order), writes its rows of h and n = (h*w)*r
+// and, given the next MoE layer's transposed f32 router WrT ([H][E]), the partial router scores of
+// its rows (the format of k_dec_partial_scores: one row of 64 per block, its rows added in order).
+template <int N32, int R>
 __global__ void __launch_bounds__(256) k_attn_post(dsh_attn_t A, const float *x_in, const int *step, int stride,
-                                                   float *h_out, float *n_out) {
+                                                   float *h_out, float *n_out, const float *__restrict__ WrT, int E,
+                                                   float *__restrict__ partials) {
   constexpr int H = 32 * N32;
   __shared__ __attribute__((aligned(16))) float s_h[H];
-  __shared__ float s_r;
+  __shared__ float s_r, s_n[R];
   const float *x = step ? x_in + (size_t)(*step) * stride : x_in;
-  for (int i = threadIdx.x; i < H; i += 256) {
-    const float v = x[i] + A.proj[i];
-    s_h[i] = v;
-    h_out[i] = v;
+  const int r0 = blockIdx.x * R;
+  float wr[R];
+  if (WrT && (int)threadIdx.x < E) {
+#pragma unroll
+    for (int j = 0; j < R; j++) wr[j] = WrT[(size_t)(r0 + j) * E + threadIdx.x];
   }
+  for (int i = threadIdx.x; i < H; i += 256) s_h[i] = x[i] + A.proj[i];
   __syncthreads();
   const float r = attn_rms_scale(s_h, H, A.eps, &s_r);
-  for (int i = threadIdx.x; i < H; i += 256) n_out[i] = (s_h[i] * A.post_norm[i]) * r;
+  if (threadIdx.x < R) {
+    const int i = r0 + threadIdx.x;
+    const float nv = (s_h[i] * A.post_norm[i]) * r;
+    h_out[i] = s_h[i];
+    n_out[i] = nv;
+    s_n[threadIdx.x] = nv;
+  }
+  __syncthreads();
+  if (WrT && threadIdx.x < 64) {
+    float p = 0.0f;
+    if ((int)threadIdx.x < E) {
+#pragma unroll
+      for (int j = 0; j < R; j++) p = __builtin_fmaf(wr[j], s_n[j], p);
+    }
+    partials[(size_t)blockIdx.x * 64 + threadIdx.x] = (int)threadIdx.x < E ? p : 0.0f;
+  }
+}
+
+// ds_rms_norm of the last hidden state before the LM head (ds_moe_decoder.c:1000), AVX-512 order;
+// trunc: ds_bf16_truncate_array after it (:1016-1018, bf16 simulation of model version 3).
+template <int N32>
+__global__ void __launch_bounds__(256) k_final_norm(const float *__restrict__ x, const float *__restrict__ w,
+                                                    float eps, int trunc, float *__restrict__ out) {
+  constexpr int H = 32 * N32;
+  __shared__ __attribute__((aligned(16))) float s_x[H];
+  __shared__ float s_r;
+  for (int i = threadIdx.x; i < H; i += 256) s_x[i] = x[i];
+  __syncthreads();
+  const float r = attn_rms_scale(s_x, H, eps, &s_r);
+  for (int i = threadIdx.x; i < H; i += 256) {
+    const float v = (s_x[i] * w[i]) * r;
+    out[i] = trunc ? dsh_bf16_round_half_up(v) : v;
+  }
 }
 
 extern "C" {
@@ -348,7 +386,7 @@ size_t dsh_attn_core_lds(int max_kv) { return (size_t)(2 * max_kv > 8 ? 2 * max_
 
 hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *step, int stride, const int *pos_ptr,
                            int pos_add, int prefill_len, int window, int max_kv, int nthreads, float *h_out,
-                           float *n_out, hipStream_t s) {
+                           float *n_out, const float *WrT_next, int E_next, float *partials_next, hipStream_t s) {
   if (!dsh_attn_supported(A->H, A->n_heads, A->head_dim)) return hipErrorInvalidValue;
   const int qd = A->n_heads * A->head_dim;
 #define QKV(N)                                                                                     \
@@ -375,16 +413,42 @@ hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *st
       return hipErrorInvalidValue;
   }
 #undef OP
-#define PO(N)                                                                        \
-  case N:                                                                            \
-    k_attn_post<8 * N><<<1, 256, 0, s>>>(*A, x_in, step, stride, h_out, n_out);      \
+#define PO(N, RR)                                                                                           \
+  case N:                                                                                                   \
+    k_attn_post<8 * N, RR><<<A->H / RR, 256, 0, s>>>(*A, x_in, step, stride, h_out, n_out, WrT_next, E_next, \
+                                                     partials_next);                                        \
     break;
-  switch (A->H / 256) {
-    PO(1) PO(2) PO(3) PO(4) PO(5) PO(6) PO(7) PO(8)
+  if (WrT_next && (E_next <= 0 || E_next > 64)) return hipErrorInvalidValue;
+  if (A->H / dsh_dec_partials(A->H) == 8) {
+    switch (A->H / 256) {
+      PO(1, 8) PO(2, 8) PO(3, 8) PO(4, 8) PO(5, 8)
+      default:
+        return hipErrorInvalidValue;
+    }
+  } else {
+    switch (A->H / 256) {
+      PO(6, 16) PO(7, 16) PO(8, 16)
+      default:
+        return hipErrorInvalidValue;
+    }
+  }
+#undef PO
+  return hipGetLastError();
+}
+
+hipError_t dsh_launch_final_norm(const float *x, const float *w, int H, float eps, int trunc, float *out,
+                                 hipStream_t s) {
+#define FN(N)                                                            \
+  case N:                                                                \
+    k_final_norm<8 * N><<<1, 256, 0, s>>>(x, w, eps, trunc, out);        \
+    break;
+  if (H % 256) return hipErrorInvalidValue;
+  switch (H / 256) {
+    FN(1) FN(2) FN(3) FN(4) FN(5) FN(6) FN(7) FN(8)
     default:
       return hipErrorInvalidValue;
   }
-#undef PO
+#undef FN
   return hipGetLastError();
 }
 

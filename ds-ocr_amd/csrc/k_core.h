@@ -109,9 +109,14 @@ int dsh_attn_supported(int H, int n_heads, int head_dim);
 size_t dsh_attn_core_lds(int max_kv);
 /* h_out = x + Wo·attention(...), n_out = RMSNorm(h_out) for the token at cache position
  * (pos_ptr ? *pos_ptr : 0) + pos_add; x = x_in + (*step)*stride when step != NULL. */
+/* With WrT_next ([H][E_next] f32), the last kernel also writes the following MoE layer's router
+ * partials from n (dsh_dec_partials(H) rows of 64). */
 hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *step, int stride, const int *pos_ptr,
                            int pos_add, int prefill_len, int window, int max_kv, int nthreads, float *h_out,
-                           float *n_out, hipStream_t s);
+                           float *n_out, const float *WrT_next, int E_next, float *partials_next, hipStream_t s);
+/* out = ds_rms_norm(x) (AVX-512 order), then bf16 truncation when trunc. */
+hipError_t dsh_launch_final_norm(const float *x, const float *w, int H, float eps, int trunc, float *out,
+                                 hipStream_t s);
 /* ---- greedy token choice with repetition penalty and n-gram ban (k_sample.hip) ---- */
 int dsh_sample_supported(int H);
 /* After the argmax. Stack form (step != NULL): history tokens[0..min(*step - 1, hist_len)), token
@@ -127,8 +132,8 @@ hipError_t dsh_launch_dense_gate_up(const uint16_t *Wg, const uint16_t *Wu, cons
 /* x_out[H] = (residual ? x : 0) + Wd·h; with WrT_next ([H][E_next] f32), the next MoE layer's router
  * partial scores over 8-row blocks (H / 8 rows of 64, the format k_dec_down writes). */
 hipError_t dsh_launch_dense_down(const uint16_t *Wd, const float *h, const float *x_in, const int *step, int stride,
-                                 int H, int I, int residual, float *x_out, const float *WrT_next, int E_next,
-                                 float *partials_next, hipStream_t s);
+                                 int H, int I, int residual, const float *resid, float *x_out, const float *WrT_next,
+                                 int E_next, float *partials_next, hipStream_t s);
 hipError_t dsh_launch_transpose_f32(const float *src, float *dst, int rows, int cols, hipStream_t s);
 hipError_t dsh_launch_dec_partial_scores(const float *WrT, const float *x_in, const int *step, int stride, int H, int E,
                                          float *partials, hipStream_t s);
@@ -137,9 +142,10 @@ hipError_t dsh_launch_dec_scores_bf16(const uint16_t *Wr, const float *x_in, con
 hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const int *step, int stride,
                                   const float *partials, int np, int route_mode, int bf16sim,
                                   const dsh_layer_work_t *wk, hipStream_t s);
+/* x_out = (residual ? (resid ? resid : x) : 0) + MoE(x) rows. */
 hipError_t dsh_launch_dec_down(const dsh_layer_t *L, const float *x_in, const int *step, int stride, float *x_out,
-                               int residual, int bf16sim, const dsh_layer_work_t *wk, const float *WrT_next,
-                               int E_next, float *partials_next, hipStream_t s);
+                               int residual, const float *resid, int bf16sim, const dsh_layer_work_t *wk,
+                               const float *WrT_next, int E_next, float *partials_next, hipStream_t s);
 int dsh_dec_lm_blocks(int vocab);
 int dsh_dec_lm_supported(int in_dim);
 int dsh_dec_lm_eligible(const void *W, int in_dim, int vocab, int nthreads);

@@ -327,7 +327,8 @@ __global__ void __launch_bounds__(256) k_dec_gate_up(dsh_layer_t L, const float 
 template <int R>
 __global__ void __launch_bounds__(512) k_dec_down(dsh_layer_t L, const float *__restrict__ x_in,
                                                   const int *__restrict__ step, int stride, float *__restrict__ x_out,
-                                                  int residual, int bf16sim, dsh_layer_work_t wk,
+                                                  int residual, const float *__restrict__ resid, int bf16sim,
+                                                  dsh_layer_work_t wk,
                                                   const float *__restrict__ WrT_next, int E_next,
                                                   float *__restrict__ partials_next) {
   static_assert(R == 8 || R == 16, "row butterfly for 8 or 16 rows");
@@ -380,7 +381,7 @@ __global__ void __launch_bounds__(512) k_dec_down(dsh_layer_t L, const float *__
   for (int k = 0; k < 8; k++) cw[k] = wk.w[min(k, K - 1)];
   const int crow = r0 + (lane & (R - 1));
   const float2 sso = so_pair(L.sdn_so, crow);
-  const float xres = x[crow];
+  const float xres = resid ? resid[crow] : x[crow];  // the residual: the layer input unless given
 
   float hp = 0.0f;
   if (lane_on) {
@@ -634,14 +635,14 @@ hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const
 }
 
 hipError_t dsh_launch_dec_down(const dsh_layer_t *L, const float *x_in, const int *step, int stride, float *x_out,
-                               int residual, int bf16sim, const dsh_layer_work_t *wk, const float *WrT_next,
-                               int E_next, float *partials_next, hipStream_t s) {
+                               int residual, const float *resid, int bf16sim, const dsh_layer_work_t *wk,
+                               const float *WrT_next, int E_next, float *partials_next, hipStream_t s) {
   if (dec_rows(L->H) == 8)
-    k_dec_down<8><<<L->H / 8, 512, 0, s>>>(*L, x_in, step, stride, x_out, residual, bf16sim, *wk, WrT_next, E_next,
-                                           partials_next);
+    k_dec_down<8><<<L->H / 8, 512, 0, s>>>(*L, x_in, step, stride, x_out, residual, resid, bf16sim, *wk, WrT_next,
+                                           E_next, partials_next);
   else
-    k_dec_down<16><<<L->H / 16, 512, 0, s>>>(*L, x_in, step, stride, x_out, residual, bf16sim, *wk, WrT_next, E_next,
-                                             partials_next);
+    k_dec_down<16><<<L->H / 16, 512, 0, s>>>(*L, x_in, step, stride, x_out, residual, resid, bf16sim, *wk, WrT_next,
+                                             E_next, partials_next);
   return hipGetLastError();
 }
 

@@ -78,7 +78,8 @@ __global__ void __launch_bounds__(16 * UPB) k_dense_gate_up(const uint16_t *__re
 #define DENSE_NB 16
 __global__ void __launch_bounds__(512) k_dense_down(const uint16_t *__restrict__ Wd, const float *__restrict__ h,
                                                     const float *x_in, const int *__restrict__ step, int stride,
-                                                    int H, int I, int residual, float *__restrict__ x_out,
+                                                    int H, int I, int residual, const float *__restrict__ resid,
+                                                    float *__restrict__ x_out,
                                                     const float *__restrict__ WrT_next, int E_next,
                                                     float *__restrict__ partials_next) {
   extern __shared__ __attribute__((aligned(16))) float s_h[];  // I floats
@@ -102,7 +103,7 @@ __global__ void __launch_bounds__(512) k_dense_down(const uint16_t *__restrict__
 #pragma unroll
     for (int j = 0; j < DENSE_ROWS; j++) wr[j] = WrT_next[(size_t)(r0 + j) * E_next + lane];
   }
-  const float xres = residual && wave == 0 && lane < DENSE_ROWS ? x[r0 + lane] : 0.0f;
+  const float xres = residual && wave == 0 && lane < DENSE_ROWS ? (resid ? resid : x)[r0 + lane] : 0.0f;
   asm volatile("" ::: "memory");
   u32x4 w[DENSE_NB];
   auto load_segment = [&](int c0) {
@@ -178,10 +179,10 @@ hipError_t dsh_launch_dense_gate_up(const uint16_t *Wg, const uint16_t *Wu, cons
 }
 
 hipError_t dsh_launch_dense_down(const uint16_t *Wd, const float *h, const float *x_in, const int *step, int stride,
-                                 int H, int I, int residual, float *x_out, const float *WrT_next, int E_next,
-                                 float *partials_next, hipStream_t s) {
+                                 int H, int I, int residual, const float *resid, float *x_out, const float *WrT_next,
+                                 int E_next, float *partials_next, hipStream_t s) {
   if (!dsh_dense_supported(H, I) || (WrT_next && (E_next <= 0 || E_next > 64))) return hipErrorInvalidValue;
-  k_dense_down<<<H / DENSE_ROWS, 512, (size_t)I * 4, s>>>(Wd, h, x_in, step, stride, H, I, residual, x_out, WrT_next,
+  k_dense_down<<<H / DENSE_ROWS, 512, (size_t)I * 4, s>>>(Wd, h, x_in, step, stride, H, I, residual, resid, x_out, WrT_next,
                                                           E_next, partials_next);
   return hipGetLastError();
 }

@@ -284,7 +284,7 @@ static hipError_t layer_enqueue(const ds_hip_layer_t *L, const dsh_layer_work_t 
   if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
   int chain = next && route_mode == DS_HIP_ROUTE_CFG;
   if (e == hipSuccess)
-    e = dsh_launch_dec_down(&L->d, x_in, step, stride, x_out, residual, bf16sim, wk,
+    e = dsh_launch_dec_down(&L->d, x_in, step, stride, x_out, residual, NULL, bf16sim, wk,
                             chain ? next->d.router_f32_t : NULL, chain ? next->E : 0, chain ? partials : NULL,
                             dsr_stream);
   if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
@@ -694,7 +694,7 @@ static hipError_t dense_enqueue(const ds_hip_dense_t *D, float *out, const float
                                 int residual, const ds_hip_layer_t *next, float *partials_next) {
   hipError_t e = dsh_launch_dense_gate_up(D->wg, D->wu, x, step, stride, D->H, D->I, D->h, dsr_stream);
   if (e == hipSuccess)
-    e = dsh_launch_dense_down(D->wd, D->h, x, step, stride, D->H, D->I, residual, out,
+    e = dsh_launch_dense_down(D->wd, D->h, x, step, stride, D->H, D->I, residual, NULL, out,
                               next ? next->d.router_f32_t : NULL, next ? next->E : 0, partials_next, dsr_stream);
   return e;
 }
@@ -728,6 +728,12 @@ struct ds_hip_stack {
   hipGraph_t graph;
   hipGraphExec_t exec;
   int bound;
+  /* full decoder step (ds_hip_stack_set_attention): one attention block per decoder layer */
+  ds_hip_attn_t **attn;
+  int n_attn, pos0, trunc_final;
+  float final_eps;
+  void *att_work;          /* h [H], n [H], the LM head's input [H], final norm weights [H] */
+  float *hbuf, *nbuf, *fbuf, *final_norm;
   /* greedy sampling rules after the argmax (ds_hip_stack_set_sampling) */
   float rp;
   int ngram, hist_cap;
@@ -810,6 +816,8 @@ void ds_hip_stack_destroy(ds_hip_stack_t *S) {
   if (S->graph) hipGraphDestroy(S->graph);
   hipFree(S->work);
   if (S->smp_work) hipFree(S->smp_work);
+  if (S->att_work) hipFree(S->att_work);
+  free(S->attn);
   free(S->layers);
   free(S);
 }
@@ -838,10 +846,50 @@ int ds_hip_stack_set_sampling(ds_hip_stack_t *S, float repeat_penalty, int no_re
   return 0;
 }
 
+/* The LM head's input: the final RMSNorm's output in a full decoder step, else the last layer's. */
+static const float *lm_in(const ds_hip_stack_t *S) { return S->attn ? S->fbuf : S->xbuf; }
+
+int ds_hip_stack_set_attention(ds_hip_stack_t *S, ds_hip_attn_t *const *attn, int n_attn, const float *final_norm,
+                               float final_eps, int pos0, int trunc_final) {
+  if (!S) return dsr_failf("ds_hip_stack_set_attention: NULL stack");
+  if (S->bound) return dsr_failf("ds_hip_stack_set_attention: call before ds_hip_stack_bind");
+  if (!attn && n_attn == 0) { /* back to MoE layers only */
+    free(S->attn);
+    S->attn = NULL;
+    S->n_attn = 0;
+    return 0;
+  }
+  const int want = (S->dense ? 1 : 0) + S->n_layers;
+  if (!attn || n_attn != want || !final_norm || pos0 < 0)
+    return dsr_failf("ds_hip_stack_set_attention: need %d attention blocks (dense layer, then each MoE layer), the "
+                     "final norm and pos0 >= 0", want);
+  for (int i = 0; i < n_attn; i++)
+    if (!attn[i] || ds_hip_attn_hidden(attn[i]) != S->H)
+      return dsr_failf("ds_hip_stack_set_attention: block %d missing or hidden size differs", i);
+  if (!S->att_work) DSR_TRY(hipMalloc(&S->att_work, (size_t)4 * al((size_t)S->H * 4)), "decoder step buffers");
+  char *b = (char *)S->att_work;
+  const size_t r = al((size_t)S->H * 4);
+  S->hbuf = (float *)b;
+  S->nbuf = (float *)(b + r);
+  S->fbuf = (float *)(b + 2 * r);
+  S->final_norm = (float *)(b + 3 * r);
+  if (dsr_h2d(S->final_norm, final_norm, (size_t)S->H * 4)) return -1;
+  free(S->attn);
+  S->attn = (ds_hip_attn_t **)malloc(sizeof(ds_hip_attn_t *) * (size_t)n_attn);
+  if (!S->attn) return dsr_failf("ds_hip_stack_set_attention: out of memory");
+  memcpy(S->attn, attn, sizeof(ds_hip_attn_t *) * (size_t)n_attn);
+  S->n_attn = n_attn;
+  S->pos0 = pos0;
+  S->final_eps = final_eps;
+  S->trunc_final = trunc_final ? 1 : 0;
+  return 0;
+}
+
 int ds_hip_stack_set_dense(ds_hip_stack_t *S, ds_hip_dense_t *D) {
   if (!S) return dsr_failf("ds_hip_stack_set_dense: NULL stack");
   if (S->bound) return dsr_failf("ds_hip_stack_set_dense: call before ds_hip_stack_bind");
   if (D && D->H != S->H) return dsr_failf("ds_hip_stack_set_dense: hidden %d, the stack has %d", D->H, S->H);
+  if (S->attn) return dsr_failf("ds_hip_stack_set_dense: call before ds_hip_stack_set_attention");
   S->dense = D;
   return 0;
 }
@@ -855,66 +903,161 @@ size_t ds_hip_stack_bytes_per_step(const ds_hip_stack_t *S) {
   per_layer += 2 * SI * H + 2 * SI * 8 + H * SI + H * 8;          /* shared expert */
   per_layer += E * H * (S->route_mode == DS_HIP_ROUTE_CFG ? 4 : 2); /* router */
   size_t dense = S->dense ? (size_t)3 * S->dense->H * S->dense->I * 2 : 0;
+  for (int i = 0; i < S->n_attn; i++) dense += ds_hip_attn_weight_bytes(S->attn[i]); /* KV reads not counted */
   return per_layer * (size_t)S->n_layers + dense + (size_t)S->vocab * S->H * 2;
 }
 
 /* Kernels launched per decode step (for profiling). */
 /* Kernels per step: CFG routing: the first layer's partial scores, then gate_up and down per layer;
  * DECODE routing: scores, gate_up and down per layer. Then the LM head (2 kernels). */
-static int stack_kernel_count(const ds_hip_stack_t *S) {
-  int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
-  /* with a dense layer first, its down kernel writes the first MoE layer's CFG partials */
-  int scores = cfg ? (S->dense ? 0 : 1) : S->n_layers;
-  return (S->dense ? 2 : 0) + scores + 2 * S->n_layers + 2 + (smp_active(S) ? 1 : 0);
+/* The launch groups of one step, in the order step_enqueue records an event after each; names may
+ * be NULL. Returns the count. */
+static int stack_names(const ds_hip_stack_t *S, const char **names) {
+  const int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
+  int n = 0;
+#define NM(str)                   \
+  do {                            \
+    if (names) names[n] = (str);  \
+    n++;                          \
+  } while (0)
+  if (S->attn) {
+    if (S->dense) {
+      NM("attention");
+      NM("dense.gate_up");
+      NM("dense.down");
+    }
+    for (int l = 0; l < S->n_layers; l++) {
+      NM("attention");
+      if (!cfg) NM("scores");
+      NM("gate_up");
+      NM("down");
+    }
+    NM("final_norm");
+  } else {
+    if (S->dense) {
+      NM("dense.gate_up");
+      NM("dense.down");
+    }
+    for (int l = 0; l < S->n_layers; l++) {
+      /* with a dense layer first, its down kernel writes the first MoE layer's CFG partials */
+      if (!cfg || (l == 0 && !S->dense)) NM("scores");
+      NM("gate_up");
+      NM("down");
+    }
+  }
+  NM("lm_head.argmax");
+  NM("lm_head.final");
+  if (smp_active(S)) NM("sample");
+#undef NM
+  return n;
 }
+
+static int stack_kernel_count(const ds_hip_stack_t *S) { return stack_names(S, NULL); }
 
 /* One decode step; ev (optional) receives an event before the first kernel and after each one.
  * Layer l reads router partials from partials[l & 1]; in CFG mode its down kernel writes layer
  * l+1's into partials[(l + 1) & 1]. */
+/* A full decoder step's layers (ds_moe_decoder.c:339-474 per layer): the attention half, then the
+ * MLP on n with h as its residual. In CFG routing the attention's last kernel writes the MoE
+ * layer's router partials from n; in DECODE routing the scores kernel reads n. */
+static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *nev) {
+  hipError_t e = hipSuccess;
+  const int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
+  const dsh_layer_work_t *wk = &S->layers[0]->wk;
+  const float *xin = S->xs;
+  const int *st = S->step;
+  int stride = S->stride, a = 0;
+  if (S->dense) {
+    e = ds_hip_attn_enqueue(S->attn[a++], xin, st, stride, S->step, S->pos0, S->hbuf, S->nbuf, NULL, 0, NULL);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+    if (e == hipSuccess)
+      e = dsh_launch_dense_gate_up(S->dense->wg, S->dense->wu, S->nbuf, NULL, 0, S->dense->H, S->dense->I,
+                                   S->dense->h, dsr_stream);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+    if (e == hipSuccess)
+      e = dsh_launch_dense_down(S->dense->wd, S->dense->h, S->nbuf, NULL, 0, S->dense->H, S->dense->I, 1, S->hbuf,
+                                S->xbuf, NULL, 0, NULL, dsr_stream);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+    xin = S->xbuf;
+    st = NULL;
+    stride = 0;
+  }
+  for (int l = 0; l < S->n_layers && e == hipSuccess; l++) {
+    const ds_hip_layer_t *L = S->layers[l];
+    float *pin = S->partials[l & 1];
+    int np = L->np;
+    e = ds_hip_attn_enqueue(S->attn[a++], xin, st, stride, S->step, S->pos0, S->hbuf, S->nbuf,
+                            cfg ? L->d.router_f32_t : NULL, cfg ? L->E : 0, cfg ? pin : NULL);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+    if (e == hipSuccess && !cfg) {
+      e = scores_enqueue(L, S->nbuf, NULL, 0, S->route_mode, pin, &np);
+      if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+    }
+    if (e == hipSuccess)
+      e = dsh_launch_dec_gate_up(&L->d, S->nbuf, NULL, 0, pin, np, S->route_mode, S->bf16sim, wk, dsr_stream);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+    if (e == hipSuccess)
+      e = dsh_launch_dec_down(&L->d, S->nbuf, NULL, 0, S->xbuf, 1, S->hbuf, S->bf16sim, wk, NULL, 0, NULL, dsr_stream);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+    xin = S->xbuf;
+    st = NULL;
+    stride = 0;
+  }
+  if (e == hipSuccess)
+    e = dsh_launch_final_norm(S->xbuf, S->final_norm, S->H, S->final_eps, S->trunc_final && S->bf16sim, S->fbuf,
+                              dsr_stream);
+  if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+  return e;
+}
+
 static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
   hipError_t e = hipSuccess;
   int n = 0;
   const int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
   const dsh_layer_work_t *wk = &S->layers[0]->wk;
   if (ev) e = hipEventRecord(ev[n++], dsr_stream);
-  const int dense = S->dense != NULL;
-  if (dense) {  /* layer 0: x = x + FFN(x); in CFG mode also the first MoE layer's router partials */
-    e = dsh_launch_dense_gate_up(S->dense->wg, S->dense->wu, S->xs, S->step, S->stride, S->dense->H, S->dense->I,
-                                 S->dense->h, dsr_stream);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
-    if (e == hipSuccess)
-      e = dsh_launch_dense_down(S->dense->wd, S->dense->h, S->xs, S->step, S->stride, S->dense->H, S->dense->I, 1,
-                                S->xbuf, cfg ? S->layers[0]->d.router_f32_t : NULL, cfg ? S->layers[0]->E : 0,
-                                cfg ? S->partials[0] : NULL, dsr_stream);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
-  }
-  for (int l = 0; l < S->n_layers && e == hipSuccess; l++) {
-    const ds_hip_layer_t *L = S->layers[l];
-    const int first = l == 0 && !dense; /* reads the step's input directly */
-    const float *xin = first ? S->xs : S->xbuf;
-    const int *st = first ? S->step : NULL;
-    int stride = first ? S->stride : 0;
-    float *pin = S->partials[l & 1], *pout = S->partials[(l + 1) & 1];
-    int np = L->np;
-    if (!cfg || first) {
-      e = scores_enqueue(L, xin, st, stride, S->route_mode, pin, &np);
+  if (S->attn) {
+    e = layers_full_enqueue(S, ev, &n);
+  } else {
+    const int dense = S->dense != NULL;
+    if (dense) {  /* layer 0: x = x + FFN(x); in CFG mode also the first MoE layer's router partials */
+      e = dsh_launch_dense_gate_up(S->dense->wg, S->dense->wu, S->xs, S->step, S->stride, S->dense->H, S->dense->I,
+                                   S->dense->h, dsr_stream);
       if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
-      if (e != hipSuccess) break;
+      if (e == hipSuccess)
+        e = dsh_launch_dense_down(S->dense->wd, S->dense->h, S->xs, S->step, S->stride, S->dense->H, S->dense->I, 1, NULL,
+                                  S->xbuf, cfg ? S->layers[0]->d.router_f32_t : NULL, cfg ? S->layers[0]->E : 0,
+                                  cfg ? S->partials[0] : NULL, dsr_stream);
+      if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
     }
-    const ds_hip_layer_t *next = cfg && l + 1 < S->n_layers ? S->layers[l + 1] : NULL;
-    e = dsh_launch_dec_gate_up(&L->d, xin, st, stride, pin, np, S->route_mode, S->bf16sim, wk, dsr_stream);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
-    if (e == hipSuccess)
-      e = dsh_launch_dec_down(&L->d, xin, st, stride, S->xbuf, 1, S->bf16sim, wk, next ? next->d.router_f32_t : NULL,
-                              next ? next->E : 0, next ? pout : NULL, dsr_stream);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+    for (int l = 0; l < S->n_layers && e == hipSuccess; l++) {
+      const ds_hip_layer_t *L = S->layers[l];
+      const int first = l == 0 && !dense; /* reads the step's input directly */
+      const float *xin = first ? S->xs : S->xbuf;
+      const int *st = first ? S->step : NULL;
+      int stride = first ? S->stride : 0;
+      float *pin = S->partials[l & 1], *pout = S->partials[(l + 1) & 1];
+      int np = L->np;
+      if (!cfg || first) {
+        e = scores_enqueue(L, xin, st, stride, S->route_mode, pin, &np);
+        if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+        if (e != hipSuccess) break;
+      }
+      const ds_hip_layer_t *next = cfg && l + 1 < S->n_layers ? S->layers[l + 1] : NULL;
+      e = dsh_launch_dec_gate_up(&L->d, xin, st, stride, pin, np, S->route_mode, S->bf16sim, wk, dsr_stream);
+      if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+      if (e == hipSuccess)
+        e = dsh_launch_dec_down(&L->d, xin, st, stride, S->xbuf, 1, NULL, S->bf16sim, wk, next ? next->d.router_f32_t : NULL,
+                                next ? next->E : 0, next ? pout : NULL, dsr_stream);
+      if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+    }
   }
   if (e != hipSuccess) return e;
   if (S->lm_fast) {
-    e = dsh_launch_dec_lm_argmax(S->lm, S->xbuf, S->H, S->vocab, S->cand, dsr_stream);
+    e = dsh_launch_dec_lm_argmax(S->lm, lm_in(S), S->H, S->vocab, S->cand, dsr_stream);
   } else {
     int T = dsr_threads();
-    e = dsh_launch_argmax_avx_partial(S->lm, S->xbuf, S->cand, NULL, S->H, S->vocab,
+    e = dsh_launch_argmax_avx_partial(S->lm, lm_in(S), S->cand, NULL, S->H, S->vocab,
                                       T > 1 ? (S->vocab + T - 1) / T : S->vocab, dsr_stream);
   }
   if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
@@ -923,7 +1066,7 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
   if (e == hipSuccess && smp_active(S)) {
     /* the repetition penalty and the n-gram ban over this stack's earlier tokens; one event after
      * all of the sampler's kernels */
-    e = dsh_launch_sample(S->lm, S->xbuf, S->H, S->vocab, dsr_threads(), S->rp, S->ngram, S->step, S->tokens, NULL,
+    e = dsh_launch_sample(S->lm, lm_in(S), S->H, S->vocab, dsr_threads(), S->rp, S->ngram, S->step, S->tokens, NULL,
                           S->hist_cap, smp_vals(S), smp_logits(S), smp_flag(S), dsr_stream);
     if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
   }
@@ -1012,10 +1155,10 @@ int ds_hip_time_lm_head(ds_hip_stack_t *S, int n, float *ms) {
   hipError_t e = hipEventRecord(a, dsr_stream);
   for (int i = 0; i < n && e == hipSuccess; i++) {
     if (S->lm_fast) {
-      e = dsh_launch_dec_lm_argmax(S->lm, S->xbuf, S->H, S->vocab, S->cand, dsr_stream);
+      e = dsh_launch_dec_lm_argmax(S->lm, lm_in(S), S->H, S->vocab, S->cand, dsr_stream);
     } else {
       int T = dsr_threads();
-      e = dsh_launch_argmax_avx_partial(S->lm, S->xbuf, S->cand, NULL, S->H, S->vocab,
+      e = dsh_launch_argmax_avx_partial(S->lm, lm_in(S), S->cand, NULL, S->H, S->vocab,
                                         T > 1 ? (S->vocab + T - 1) / T : S->vocab, dsr_stream);
     }
   }
@@ -1033,25 +1176,12 @@ int ds_hip_stack_kernel_count(const ds_hip_stack_t *S) { return S ? stack_kernel
 
 const char *ds_hip_stack_kernel_name(const ds_hip_stack_t *S, int i) {
   if (!S || i < 0 || i >= stack_kernel_count(S)) return NULL;
-  int nk = stack_kernel_count(S);
-  if (smp_active(S)) {
-    if (i == nk - 1) return "sample";
-    nk--;
-  }
-  if (i == nk - 2) return "lm_head.argmax";
-  if (i == nk - 1) return "lm_head.final";
-  const int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
-  if (S->dense) {
-    if (i == 0) return "dense.gate_up";
-    if (i == 1) return "dense.down";
-    i -= 2;
-    if (cfg) i += 1; /* no separate scores kernel */
-  }
-  if (cfg && i == 0) return "scores";
-  const int per = cfg ? 2 : 3; /* kernels per layer */
-  const int j = (cfg ? i - 1 : i) % per;
-  if (!cfg && j == 0) return "scores";
-  return j == per - 2 ? "gate_up" : "down";
+  const char **names = (const char **)malloc(sizeof(const char *) * (size_t)stack_kernel_count(S));
+  if (!names) return NULL;
+  stack_names(S, names);
+  const char *r = names[i];
+  free(names);
+  return r;
 }
 
 int ds_hip_profile_stack(ds_hip_stack_t *S, int n_steps, float *ms_out) {

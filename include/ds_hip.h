@@ -189,6 +189,15 @@ int ds_hip_stack_set_sampling(ds_hip_stack_t *S, float repeat_penalty, int no_re
 int ds_hip_lm_head_sample(const float *x_dev, const uint16_t *lm_head_dev, int hidden, int vocab, const int *history_dev,
                           int history_len, float repeat_penalty, int no_repeat_ngram_size, int *token_dev);
 
+/* Makes each step a whole decoder step (ds_decoder_forward for one token, ds_moe_decoder.c:339-474
+ * and :1000): attn[i] is decoder layer i's attention half (the dense layer's first when one is set,
+ * then one per MoE layer; call after ds_hip_stack_set_dense), each followed by its MLP on the
+ * post-attention RMSNorm with the attention's output as the residual; then ds_rms_norm with
+ * final_norm ([hidden] host array, final_eps) -- bf16-truncated when trunc_final and the bf16
+ * simulation are on (model version 3) -- feeds the LM head. Step s is cache position pos0 + s.
+ * Before ds_hip_stack_bind; (NULL, 0, ...) returns to MoE layers only. Blocks are borrowed. */
+int ds_hip_stack_set_attention(ds_hip_stack_t *S, ds_hip_attn_t *const *attn, int n_attn, const float *final_norm,
+                               float final_eps, int pos0, int trunc_final);
 /* lm_head_dev: bf16 [vocab, hidden] on the device (borrowed). Layers are borrowed. */
 ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers, const uint16_t *lm_head_dev,
                                     int vocab, int route_mode);
