@@ -78,6 +78,33 @@ def make_dense(dev):
     return D
 
 
+def make_attention(dev, n, kv, max_seq):
+    """n decoder attention blocks (DeepSeek-OCR: 10 heads x 128, seeded N(0, 0.02) bf16 projections,
+    unit norms) with kv seeded cached positions each."""
+    L = dev.load()
+    rng = np.random.default_rng(909)
+    qd = 10 * 128
+
+    def bf16(m):
+        u = (rng.standard_normal(m, dtype=np.float32) * np.float32(0.02)).view(np.uint32)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+    ones = np.ones(H, np.float32)
+    out = []
+    for _ in range(n):
+        w = [bf16(qd * H) for _ in range(4)]
+        A = L.ds_hip_attn_create(H, 10, 128, max_seq, 1e-6, 10000.0, *[a.ctypes.data for a in w], ones.ctypes.data,
+                                 ones.ctypes.data, None, None)
+        if not A:
+            raise RuntimeError(L.ds_hip_last_error().decode())
+        if kv:
+            k = (rng.standard_normal(kv * qd, dtype=np.float32) * np.float32(0.3))
+            v = rng.standard_normal(kv * qd, dtype=np.float32)
+            dev.check(L.ds_hip_attn_load_kv(A, k.ctypes.data, v.ctypes.data, kv, qd), "kv")
+        out.append(A)
+    return out
+
+
 def host_layers(dev, handles, rf_host, rb_host):
     """Copies the device layers' INT8 blocks to the host (for the reference CPU baseline)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -154,6 +181,9 @@ def main():
     ap.add_argument("--prefill-reps", type=int, default=20)
     ap.add_argument("--dense-layer", action="store_true",
                     help="prepend DeepSeek-OCR's layer-0 dense SwiGLU FFN (1280x6848 bf16) to every step")
+    ap.add_argument("--decoder-step", type=int, default=-1, metavar="KV",
+                    help=">= 0: whole decoder steps (attention 10x128 + MLP per layer, the dense layer 0, final "
+                         "norm) after KV cached positions")
     ap.add_argument("--repeat-penalty", type=float, default=1.0,
                     help="> 1: the reference's repetition penalty after each argmax, over the run's tokens")
     ap.add_argument("--no-repeat-ngram", type=int, default=0, help="> 0: the reference's n-gram ban")
@@ -196,9 +226,17 @@ def main():
     sampling = args.repeat_penalty > 1.0 or args.no_repeat_ngram > 0
     if sampling:
         dev.check(L.ds_hip_stack_set_sampling(S, args.repeat_penalty, args.no_repeat_ngram, n_inputs), "sampling")
-    dense = make_dense(dev) if args.dense_layer else None
+    full = args.decoder_step >= 0
+    dense = make_dense(dev) if (args.dense_layer or full) else None
     if dense:
         dev.check(L.ds_hip_stack_set_dense(S, dense), "set dense")
+    attns = []
+    if full:
+        attns = make_attention(dev, LAYERS + 1, args.decoder_step, args.decoder_step + n_inputs + 1)
+        fnorm = np.ones(H, np.float32)
+        arr_a = (C.c_void_p * len(attns))(*attns)
+        dev.check(L.ds_hip_stack_set_attention(S, arr_a, len(attns), fnorm.ctypes.data, 1e-6, args.decoder_step, 0),
+                  "set attention")
     dev.check(L.ds_hip_stack_bind(S, xs.ptr, H, toks.ptr), "bind")
     bytes_per_step = L.ds_hip_stack_bytes_per_step(S)
 
@@ -258,7 +296,7 @@ def main():
 
     xs_host = xs.to_array(np.float32).reshape(n_inputs, H)[args.warmup:].copy()
     cpu = None
-    if not args.no_cpu and not dense and not sampling:  # the reference CPU leg: MoE layers + argmax head
+    if not args.no_cpu and not dense and not sampling and not full:  # the reference CPU leg: MoE layers + argmax head
         try:
             cpu = cpu_baseline(dev, handles, rfs, rbs, lm, xs_host, gpu_tokens[args.warmup:], route, args.cpu_seconds)
         except Exception as exc:  # report, never hide
@@ -266,6 +304,8 @@ def main():
     L.ds_hip_stack_destroy(S)
     if dense:
         L.ds_hip_dense_destroy(dense)
+    for A in attns:
+        L.ds_hip_attn_destroy(A)
     for h in handles:
         L.ds_hip_layer_destroy(h)
 
@@ -282,7 +322,9 @@ def main():
         "vs_baseline": None,
         "dtype": "int8 weights (u8 codes + f32 scale/offset), f32 accumulate; bf16 LM head",
         "data": "synthetic: seeded N(0,0.02) weights generated on device, seeded N(0,1) f32 hidden states",
-        "config": {"workload": ("layer-0 dense SwiGLU FFN 1280x6848 bf16 + " if dense else "") +
+        "config": {"workload": (f"whole decoder steps after {args.decoder_step} cached positions: attention "
+                                 "(10 heads x 128, f32 KV cache) per layer + " if full else "") +
+                               ("layer-0 dense SwiGLU FFN 1280x6848 bf16 + " if dense else "") +
                                (f"repetition penalty {args.repeat_penalty} / no-repeat n-gram {args.no_repeat_ngram} "
                                 "after the argmax + " if sampling else "") +
                                "config 5: 11 DeepSeek3B-MoE INT8 layers (H1280, 64x[1792x1280 + 1280x896] "

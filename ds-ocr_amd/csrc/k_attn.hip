@@ -1,18 +1,20 @@
 // k_attn.hip — the attention half of one decoder layer for one token (decoder_layer_forward,
-// ds_moe_decoder.c:339-431; MHA, single-token decode) on the device, as four launches:
-//   k_attn_qkv   : x_norm = ds_rms_norm(x) in its AVX-512 order (recomputed by every block), then
-//                  the rows of [Wq; Wk; Wv] in ds_linear_nobias_bf16_qkv's AVX-512 order with its
-//                  split of the rows over the reference's threads (ds_kernels.c:844-915); v goes
-//                  straight into the V cache row pos;
-//   k_attn_core  : one block per head: the optional per-head q/k norms, RoPE from the position's
-//                  cos/sin row (ds_apply_rope_neox), the roped k into the K cache row pos, then the
-//                  online-softmax attention over the causal or R-SWA ranges (see below);
-//   k_attn_oproj : proj = Wo·att in ds_bf16_matvec_threaded's order;
-//   k_attn_post  : h = x + proj and n = ds_rms_norm(h) (ds_residual_rms_norm, AVX-512 order).
-// Everything except the attention's output accumulation is bit-exact with the reference. The
-// reference's attention is a sequential online softmax with ds_fast_expf (ds_kernels.c:2124-2160,
-// :2270-2330). Its branch at each position depends only on the running maximum, so this kernel
-// takes the same branches with the same exp arguments: a prefix-max scan gives each position's
+// ds_moe_decoder.c:339-431; MHA, single-token decode) on the device:
+//   k_attn_qkv     : x_norm = ds_rms_norm(x) in its AVX-512 order (recomputed by every block), then
+//                    the rows of [Wq; Wk; Wv] in ds_linear_nobias_bf16_qkv's AVX-512 order with its
+//                    split of the rows over the reference's threads (ds_kernels.c:844-915); v goes
+//                    straight into the V cache row pos;
+//   k_attn_scores  : per head x chunk of positions, the optional per-head q/k norms and RoPE
+//                    (ds_apply_rope_neox, recomputed by every block), the roped k into the K cache row
+//                    pos, and the scores;
+//   k_attn_coef, k_attn_av, k_attn_combine : the online-softmax attention over the causal or R-SWA
+//                    positions (below), spread over heads x position chunks;
+//   k_attn_oproj   : proj = Wo·att in ds_bf16_matvec_threaded's order;
+//   k_attn_post    : h = x + proj and n = ds_rms_norm(h) (ds_residual_rms_norm, AVX-512 order).
+// Everything except the attention's output sum is bit-exact with the reference. The reference's
+// attention is a sequential online softmax with ds_fast_expf (ds_kernels.c:2124-2160,
+// :2270-2330). Its branch at each position depends only on the running maximum, so these kernels
+// take the same branches with the same exp arguments: a prefix-max scan gives each position's
 // running maximum P, its factor f = fast_exp(P - s) on a new maximum (the correction) or
 // fast_exp(s - P) (its weight), and a suffix product of the later corrections gives each V row's
 // final coefficient c; o = sum c*v and sum_e = sum c are then sums in any order. The result differs
@@ -146,6 +148,7 @@ __device__ __forceinline__ float attn_dot(const float *q, const float *k, int n)
   for (int m = 0; m < 4; m++)
 #pragma unroll
     for (int l = 0; l < 16; l++) a[m][l] = 0.0f;
+#pragma unroll
   for (int i = 0; i < n; i += 64) {
 #pragma unroll
     for (int m = 0; m < 4; m++) {
@@ -169,73 +172,101 @@ __device__ __forceinline__ float attn_dot(const float *q, const float *k, int n)
   return (T6[0] + T6[2]) + (T6[1] + T6[3]);
 }
 
-// One block per head; dynamic LDS: 2 * max_kv floats (scores / factors, coefficients).
-__global__ void __launch_bounds__(ATTN_THREADS) k_attn_core(dsh_attn_t A, const int *pos_ptr, int pos_add,
-                                                            int prefill_len, int window, int max_kv) {
-  extern __shared__ __attribute__((aligned(16))) float s_dyn[];
-  __shared__ __attribute__((aligned(16))) float s_q[DSH_ATTN_MAX_HD], s_k[DSH_ATTN_MAX_HD];
-  __shared__ float s_w[4], s_r;
-  __shared__ __attribute__((aligned(16))) float s_o[ATTN_THREADS];
-  float *s_s = s_dyn, *s_c = s_dyn + max_kv;
-  const int h = blockIdx.x, hd = A.head_dim, half = hd / 2, tid = threadIdx.x;
-  const int pos = attn_pos(pos_ptr, pos_add);
+// The attended positions of the token at cache position pos: p < r1 is position p, then r2 + (p - r1)
+// ([0, pos+1), or R-SWA's reference tokens [0, prefill_len) and window [ws, pos+1)).
+struct attn_span {
+  int r1, r2, n;
+  __device__ __forceinline__ int j(int p) const { return p < r1 ? p : r2 + (p - r1); }
+};
+__device__ __forceinline__ attn_span attn_positions(int pos, int prefill_len, int window) {
+  const int kv = pos + 1;
+  attn_span sp{kv, kv, kv};
+  if (window > 0 && pos >= prefill_len) {
+    const int ws = prefill_len > kv - window ? prefill_len : kv - window;
+    if (ws > prefill_len) sp = attn_span{prefill_len, ws, prefill_len + (kv - ws)};
+  }
+  return sp;
+}
+
+// The optional per-head norms (ds_rms_norm_per_head) and RoPE of one head's q and k (in LDS, hd
+// threads of the block active). Called by every thread of the block.
+__device__ void attn_rope_head(const dsh_attn_t &A, int h, int pos, float *s_q, float *s_k, float *s_r) {
+  const int hd = A.head_dim, half = hd / 2, tid = threadIdx.x;
   const float *cs = A.rope_cos + (size_t)pos * hd, *sn = A.rope_sin + (size_t)pos * hd;
-  // raw q and k of this head; the optional per-head norms (ds_rms_norm_per_head), then RoPE
-  if (tid < hd) {
-    s_q[tid] = A.q[h * hd + tid];
-    s_k[tid] = A.k[h * hd + tid];
+  for (int d = tid; d < hd; d += blockDim.x) {
+    s_q[d] = A.q[h * hd + d];
+    s_k[d] = A.k[h * hd + d];
   }
   __syncthreads();
   for (int which = 0; which < 2; which++) {
     const float *nw = which ? A.k_norm : A.q_norm;
     float *v = which ? s_k : s_q;
     if (nw) {
-      const float r = attn_rms_scale(v, hd, A.eps, &s_r);
-      float y = 0.0f;
-      if (tid < hd) y = (v[tid] * nw[tid]) * r;
+      const float r = attn_rms_scale(v, hd, A.eps, s_r);
+      float y[DSH_ATTN_MAX_HD / 64];
+      for (int d = tid, i = 0; d < hd; d += blockDim.x, i++) y[i] = (v[d] * nw[d]) * r;
       __syncthreads();
-      if (tid < hd) v[tid] = y;
+      for (int d = tid, i = 0; d < hd; d += blockDim.x, i++) v[d] = y[i];
       __syncthreads();
     }
   }
-  float rq = 0.0f, rk = 0.0f;
-  if (tid < hd) {
-    const int d = tid < half ? tid : tid - half;
+  float rq[DSH_ATTN_MAX_HD / 64], rk[DSH_ATTN_MAX_HD / 64];
+  for (int t = tid, i = 0; t < hd; t += blockDim.x, i++) {
+    const int d = t < half ? t : t - half;
     const float q1 = s_q[d], q2 = s_q[d + half], k1 = s_k[d], k2 = s_k[d + half];
-    if (tid < half) {
-      rq = __builtin_fmaf(q1, cs[d], -(q2 * sn[d]));
-      rk = __builtin_fmaf(k1, cs[d], -(k2 * sn[d]));
+    if (t < half) {
+      rq[i] = __builtin_fmaf(q1, cs[d], -(q2 * sn[d]));
+      rk[i] = __builtin_fmaf(k1, cs[d], -(k2 * sn[d]));
     } else {
-      rq = __builtin_fmaf(q1, sn[tid], q2 * cs[tid]);
-      rk = __builtin_fmaf(k1, sn[tid], k2 * cs[tid]);
+      rq[i] = __builtin_fmaf(q1, sn[t], q2 * cs[t]);
+      rk[i] = __builtin_fmaf(k1, sn[t], k2 * cs[t]);
     }
   }
   __syncthreads();
-  if (tid < hd) {
-    s_q[tid] = rq;
-    s_k[tid] = rk;
-    A.kc[(size_t)pos * A.kv_stride + h * hd + tid] = rk;
+  for (int t = tid, i = 0; t < hd; t += blockDim.x, i++) {
+    s_q[t] = rq[i];
+    s_k[t] = rk[i];
   }
   __syncthreads();
-  // the attended positions: [0, pos+1), or R-SWA's reference tokens and window
-  const int kv = pos + 1;
-  int r0 = 0, r1 = kv, r2 = kv, r3 = kv;
-  if (window > 0 && pos >= prefill_len) {
-    const int ws = prefill_len > kv - window ? prefill_len : kv - window;
-    if (ws > prefill_len) {
-      r1 = prefill_len;
-      r2 = ws;
-    }
+}
+
+// Scores, bit-exact: 64 attended positions per 64-thread block (grid: heads x chunks of the cache),
+// one thread per position; sc[h][p] = ds_dot_f32(q, k_j) * (1/sqrtf(head_dim)). Every block ropes
+// the head's q (and k) itself; the block holding the token's own position writes its roped k into
+// the K cache row pos and uses it from LDS.
+template <int HD>
+__global__ void __launch_bounds__(64) k_attn_scores(dsh_attn_t A, const int *pos_ptr, int pos_add, int prefill_len,
+                                                    int window) {
+  __shared__ __attribute__((aligned(16))) float s_q[HD], s_k[HD];
+  __shared__ float s_r;
+  const int h = blockIdx.x, p = blockIdx.y * 64 + threadIdx.x;
+  const int pos = attn_pos(pos_ptr, pos_add);
+  const attn_span sp = attn_positions(pos, prefill_len, window);
+  if ((int)blockIdx.y * 64 >= sp.n) return;  // whole block
+  attn_rope_head(A, h, pos, s_q, s_k, &s_r);
+  const bool own = ((int)blockIdx.y + 1) * 64 >= sp.n;  // this block holds position n-1 == pos
+  if (own)
+    for (int d = threadIdx.x; d < HD; d += 64) A.kc[(size_t)pos * A.kv_stride + h * HD + d] = s_k[d];
+  if (p < sp.n) {
+    const int j = sp.j(p);
+    const float scale = 1.0f / __builtin_sqrtf((float)HD);
+    A.sc[(size_t)h * A.max_seq + p] =
+        attn_dot(s_q, j == pos ? s_k : A.kc + (size_t)j * A.kv_stride + h * HD, HD) * scale;
   }
-  const int n = (r1 - r0) + (r3 - r2);
-  const float scale = 1.0f / __builtin_sqrtf((float)hd);
-  auto jpos = [&](int p) { return p < r1 ? p : r2 + (p - r1); };
-  // scores, bit-exact (the token's own k from LDS)
-  for (int p = tid; p < n; p += ATTN_THREADS) {
-    const int j = jpos(p);
-    const float *kr = j == pos ? s_k : A.kc + (size_t)j * A.kv_stride + h * hd;
-    s_s[p] = attn_dot(s_q, kr, hd) * scale;
-  }
+}
+
+// Per head: the reference's sequence of branches (see the top of this file) as coefficients:
+// sc[h][p] <- c_p, se[h] <- sum_e. Dynamic LDS: 2 * max_seq floats.
+__global__ void __launch_bounds__(ATTN_THREADS) k_attn_coef(dsh_attn_t A, const int *pos_ptr, int pos_add,
+                                                            int prefill_len, int window) {
+  extern __shared__ __attribute__((aligned(16))) float s_dyn[];
+  __shared__ float s_w[4];
+  __shared__ __attribute__((aligned(16))) float s_o[ATTN_THREADS];
+  float *s_s = s_dyn, *s_c = s_dyn + A.max_seq;
+  const int h = blockIdx.x, tid = threadIdx.x;
+  const int n = attn_positions(attn_pos(pos_ptr, pos_add), prefill_len, window).n;
+  float *sc = A.sc + (size_t)h * A.max_seq;
+  for (int p = tid; p < n; p += ATTN_THREADS) s_s[p] = sc[p];
   __syncthreads();
   // running maximum before each position: exclusive prefix max over contiguous segments
   const int seg = (n + ATTN_THREADS - 1) / ATTN_THREADS;
@@ -260,57 +291,84 @@ __global__ void __launch_bounds__(ATTN_THREADS) k_attn_core(dsh_attn_t A, const 
     prod *= nm ? f : 1.0f;
     P = nm ? s : P;
   }
-  // product of the corrections after each segment: exclusive suffix product over the threads
-  __syncthreads();
+  // product of the corrections after each segment: a scan over the threads in reverse order
+  // (thread t holds segment ATTN_THREADS-1-t's product; the exclusive suffix of segment tid is the
+  // inclusive value of thread ATTN_THREADS-2-tid)
   s_o[tid] = prod;
   __syncthreads();
-  float after = 1.0f;
-  for (int t = ATTN_THREADS - 1; t > tid; t--) after *= s_o[t];
+  const float rprod = s_o[ATTN_THREADS - 1 - tid];
+  __syncthreads();
+  const float rincl = attn_block_scan(rprod, [](float a, float b) { return a * b; }, s_w);
+  s_o[tid] = rincl;
+  __syncthreads();
+  float after = tid < ATTN_THREADS - 1 ? s_o[ATTN_THREADS - 2 - tid] : 1.0f;
+  float csum = 0.0f;
   for (int p = p1 - 1; p >= p0; p--) {
-    s_c[p] *= after;  // c = g * (product of the later corrections)
+    const float c = s_c[p] * after;  // c = g * (product of the later corrections)
+    sc[p] = c;
+    csum += c;
     after *= s_s[p];
   }
+  const float tot = attn_block_scan(csum, [](float a, float b) { return a + b; }, s_w);
+  if (tid == ATTN_THREADS - 1) A.se[h] = tot;
+}
+
+// V: 32 attended positions per block of head_dim threads (grid: heads x chunks), every v load of a
+// thread in flight together; part[h][chunk][d] = sum over the chunk of c_p * v_p[d].
+#define ATTN_VCH 32
+__global__ void __launch_bounds__(DSH_ATTN_MAX_HD) k_attn_av(dsh_attn_t A, const int *pos_ptr, int pos_add,
+                                                             int prefill_len, int window) {
+  __shared__ float s_c[ATTN_VCH];
+  const int h = blockIdx.x, hd = A.head_dim, d = threadIdx.x, p0 = blockIdx.y * ATTN_VCH;
+  const attn_span sp = attn_positions(attn_pos(pos_ptr, pos_add), prefill_len, window);
+  if (p0 >= sp.n) return;  // whole block
+  const int cnt = min(ATTN_VCH, sp.n - p0);
+  if (d < ATTN_VCH) s_c[d] = d < cnt ? A.sc[(size_t)h * A.max_seq + p0 + d] : 0.0f;
+  float v[ATTN_VCH];
+#pragma unroll
+  for (int q = 0; q < ATTN_VCH; q++) v[q] = A.vc[(size_t)sp.j(p0 + min(q, cnt - 1)) * A.kv_stride + h * hd + d];
   __syncthreads();
-  // o = sum c*v over the positions, split into ATTN_THREADS / hd parts; sum_e = sum c
-  const int parts = ATTN_THREADS / hd, part = tid / hd, d = tid - part * hd;
-  float acc = 0.0f, csum = 0.0f;
-  if (part < parts) {
-    const int pa = n * part / parts, pb = n * (part + 1) / parts;
-    for (int p = pa; p < pb; p++) {
-      const float c = s_c[p];
-      acc = __builtin_fmaf(c, A.vc[(size_t)jpos(p) * A.kv_stride + h * hd + d], acc);
-      csum += c;
-    }
+  float acc = 0.0f;
+#pragma unroll
+  for (int q = 0; q < ATTN_VCH; q++) acc = __builtin_fmaf(s_c[q], v[q], acc);  // s_c is 0 past cnt
+  A.part[((size_t)h * (A.max_seq / ATTN_VCH + 1) + blockIdx.y) * hd + d] = acc;
+}
+
+// Per head: the chunk sums in chunk order, times 1/sum_e (ds_vec_scale_inplace; sum_e > 0).
+__global__ void __launch_bounds__(DSH_ATTN_MAX_HD) k_attn_combine(dsh_attn_t A, const int *pos_ptr, int pos_add,
+                                                                  int prefill_len, int window) {
+  const int h = blockIdx.x, hd = A.head_dim, d = threadIdx.x;
+  const int n = attn_positions(attn_pos(pos_ptr, pos_add), prefill_len, window).n;
+  const int nch = (n + ATTN_VCH - 1) / ATTN_VCH;
+  const float *pt = A.part + (size_t)h * (A.max_seq / ATTN_VCH + 1) * hd + d;
+  float o = 0.0f;
+  for (int c0 = 0; c0 < nch; c0 += 16) {  // 16 loads in flight, then the adds in chunk order
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 16; q++) v[q] = pt[(size_t)min(c0 + q, nch - 1) * hd];
+#pragma unroll
+    for (int q = 0; q < 16; q++)
+      if (c0 + q < nch) o += v[q];
   }
-  __syncthreads();
-  s_o[tid] = acc;
-  if (d == 0) s_s[part] = csum;  // the scores area is free now
-  __syncthreads();
-  if (tid < hd) {
-    float o = 0.0f, se = 0.0f;
-    for (int k = 0; k < parts; k++) {
-      o += s_o[k * hd + tid];
-      se += s_s[k];
-    }
-    if (se > 0.0f) o = o * (1.0f / se);
-    A.att[h * hd + tid] = o;
-  }
+  const float se = A.se[h];
+  if (se > 0.0f) o = o * (1.0f / se);
+  A.att[h * hd + d] = o;
 }
 
 // ---------------------------------------------------------------------------- O projection
-// 64 output rows per 256-thread block; att (q_dim == 32*N32) staged in LDS.
+// 16 output rows per 64-thread block; att (q_dim == 32*N32) staged in LDS.
 template <int N32>
-__global__ void __launch_bounds__(256) k_attn_oproj(dsh_attn_t A, int chunk) {
+__global__ void __launch_bounds__(64) k_attn_oproj(dsh_attn_t A, int chunk) {
   constexpr int QD = 32 * N32;
   __shared__ __attribute__((aligned(16))) float s_a[QD];
   const int L = threadIdx.x & 3;
-  const int r = blockIdx.x * 64 + (threadIdx.x >> 2);
+  const int r = blockIdx.x * 16 + (threadIdx.x >> 2);
   const int rc = r < A.H ? r : A.H - 1;
   const uint16_t *w = A.wo + (size_t)rc * QD;
   const int path = row_path(rc, A.H, chunk, false);
   u32x4 wv[N32];
   if (path != DSH_ROW_SINGLE) attn_row_load<N32>(wv, w, L);
-  for (int i = threadIdx.x; i < QD / 4; i += 256) ((f32x4 *)s_a)[i] = ((const f32x4 *)A.att)[i];
+  for (int i = threadIdx.x; i < QD / 4; i += 64) ((f32x4 *)s_a)[i] = ((const f32x4 *)A.att)[i];
   __syncthreads();
   const float v = attn_row<N32>(w, wv, s_a, L, path);
   if (L == 0 && r < A.H) A.proj[r] = v;
@@ -382,16 +440,16 @@ int dsh_attn_supported(int H, int n_heads, int head_dim) {
 }
 
 // scores/factors and coefficients; at least 8 floats (the per-part sums reuse the first ones)
-size_t dsh_attn_core_lds(int max_kv) { return (size_t)(2 * max_kv > 8 ? 2 * max_kv : 8) * sizeof(float); }
+size_t dsh_attn_core_lds(int max_kv) { return (size_t)2 * max_kv * sizeof(float); }
 
 hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *step, int stride, const int *pos_ptr,
-                           int pos_add, int prefill_len, int window, int max_kv, int nthreads, float *h_out,
+                           int pos_add, int prefill_len, int window, int nthreads, float *h_out,
                            float *n_out, const float *WrT_next, int E_next, float *partials_next, hipStream_t s) {
   if (!dsh_attn_supported(A->H, A->n_heads, A->head_dim)) return hipErrorInvalidValue;
   const int qd = A->n_heads * A->head_dim;
 #define QKV(N)                                                                                     \
   case N:                                                                                          \
-    k_attn_qkv<8 * N><<<(3 * qd + 63) / 64, 256, 0, s>>>(*A, x_in, step, stride, pos_ptr, pos_add, \
+    k_attn_qkv<8 * N><<<(3 * qd + 63) / 64, 256, 0, s>>>(*A, x_in, step, stride, pos_ptr, pos_add,  \
                                                           nthreads);                               \
     break;
   switch (A->H / 256) {
@@ -400,12 +458,31 @@ hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *st
       return hipErrorInvalidValue;
   }
 #undef QKV
-  k_attn_core<<<A->n_heads, ATTN_THREADS, dsh_attn_core_lds(max_kv), s>>>(*A, pos_ptr, pos_add, prefill_len, window,
-                                                                         max_kv > 4 ? max_kv : 4);
+  const dim3 gs(A->n_heads, (A->max_seq + 63) / 64), gv(A->n_heads, (A->max_seq + ATTN_VCH - 1) / ATTN_VCH);
+  switch (A->head_dim) {
+    case 64:
+      k_attn_scores<64><<<gs, 64, 0, s>>>(*A, pos_ptr, pos_add, prefill_len, window);
+      break;
+    case 128:
+      k_attn_scores<128><<<gs, 64, 0, s>>>(*A, pos_ptr, pos_add, prefill_len, window);
+      break;
+    case 192:
+      k_attn_scores<192><<<gs, 64, 0, s>>>(*A, pos_ptr, pos_add, prefill_len, window);
+      break;
+    case 256:
+      k_attn_scores<256><<<gs, 64, 0, s>>>(*A, pos_ptr, pos_add, prefill_len, window);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  k_attn_coef<<<A->n_heads, ATTN_THREADS, dsh_attn_core_lds(A->max_seq), s>>>(*A, pos_ptr, pos_add, prefill_len,
+                                                                             window);
+  k_attn_av<<<gv, A->head_dim, 0, s>>>(*A, pos_ptr, pos_add, prefill_len, window);
+  k_attn_combine<<<A->n_heads, A->head_dim, 0, s>>>(*A, pos_ptr, pos_add, prefill_len, window);
   const int chunk = dsh_chunk_len(A->H, nthreads);
 #define OP(N)                                                             \
   case N:                                                                 \
-    k_attn_oproj<8 * N><<<(A->H + 63) / 64, 256, 0, s>>>(*A, chunk);      \
+    k_attn_oproj<8 * N><<<(A->H + 15) / 16, 64, 0, s>>>(*A, chunk);       \
     break;
   switch (qd / 256) {
     OP(1) OP(2) OP(3) OP(4) OP(5) OP(6) OP(7) OP(8)

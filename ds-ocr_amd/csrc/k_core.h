@@ -102,6 +102,7 @@ typedef struct {
   const float *rope_cos, *rope_sin;          /* [max_seq][head_dim] */
   float *kc, *vc;                            /* [max_seq][kv_stride] */
   float *q, *k, *att, *proj;                 /* scratch: [qd] x3, [H] */
+  float *sc, *part, *se;                     /* [n_heads][max_seq], [n_heads][max_seq/32+1][head_dim], [n_heads] */
   int H, n_heads, head_dim, kv_stride, max_seq;
   float eps;
 } dsh_attn_t;
@@ -112,7 +113,7 @@ size_t dsh_attn_core_lds(int max_kv);
 /* With WrT_next ([H][E_next] f32), the last kernel also writes the following MoE layer's router
  * partials from n (dsh_dec_partials(H) rows of 64). */
 hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *step, int stride, const int *pos_ptr,
-                           int pos_add, int prefill_len, int window, int max_kv, int nthreads, float *h_out,
+                           int pos_add, int prefill_len, int window, int nthreads, float *h_out,
                            float *n_out, const float *WrT_next, int E_next, float *partials_next, hipStream_t s);
 /* out = ds_rms_norm(x) (AVX-512 order), then bf16 truncation when trunc. */
 hipError_t dsh_launch_final_norm(const float *x, const float *w, int H, float eps, int trunc, float *out,

@@ -47,7 +47,7 @@ ds_hip_attn_t *ds_hip_attn_create(int hidden, int n_heads, int head_dim, int max
   if (!A) return NULL;
   const size_t H = hidden, qd = (size_t)n_heads * head_dim, hd = head_dim;
   const size_t kv_stride = (qd + 15) & ~(size_t)15; /* rows 64-byte aligned, as the reference's cache */
-  size_t off[16], n = 0;
+  size_t off[17], n = 0;
   int k = 0;
 #define REGION(b) (off[k++] = n, n += al256(b))
   REGION(qd * H * 2);                       /* 0 wq */
@@ -63,6 +63,9 @@ ds_hip_attn_t *ds_hip_attn_create(int hidden, int n_heads, int head_dim, int max
   REGION((size_t)max_seq * kv_stride * 4);  /* 10 K cache */
   REGION((size_t)max_seq * kv_stride * 4);  /* 11 V cache */
   REGION(qd * 4 * 3 + H * 4);               /* 12 scratch: q, k, att, proj */
+  REGION((size_t)n_heads * max_seq * 4);    /* 13 scores, then coefficients */
+  REGION((size_t)n_heads * (max_seq / 32 + 1) * hd * 4); /* 14 per-chunk V sums */
+  REGION((size_t)n_heads * 4);              /* 15 softmax sums */
 #undef REGION
   hipError_t e = hipMalloc(&A->arena, n);
   if (e != hipSuccess) {
@@ -108,6 +111,9 @@ ds_hip_attn_t *ds_hip_attn_create(int hidden, int n_heads, int head_dim, int max
   d->k = d->q + qd;
   d->att = d->k + qd;
   d->proj = d->att + qd;
+  d->sc = (float *)(b + off[13]);
+  d->part = (float *)(b + off[14]);
+  d->se = (float *)(b + off[15]);
   d->H = hidden;
   d->n_heads = n_heads;
   d->head_dim = head_dim;
@@ -157,8 +163,8 @@ int ds_hip_attn_load_kv(ds_hip_attn_t *A, const float *k_host, const float *v_ho
 hipError_t ds_hip_attn_enqueue(const ds_hip_attn_t *A, const float *x_in, const int *step, int stride,
                                const int *pos_ptr, int pos_add, float *h_out, float *n_out, const float *WrT_next,
                                int E_next, float *partials_next) {
-  return dsh_launch_attn(&A->d, x_in, step, stride, pos_ptr, pos_add, A->prefill_len, A->window, A->d.max_seq,
-                         dsr_threads(), h_out, n_out, WrT_next, E_next, partials_next, dsr_stream);
+  return dsh_launch_attn(&A->d, x_in, step, stride, pos_ptr, pos_add, A->prefill_len, A->window, dsr_threads(),
+                         h_out, n_out, WrT_next, E_next, partials_next, dsr_stream);
 }
 
 int ds_hip_attn_hidden(const ds_hip_attn_t *A) { return A ? A->d.H : 0; }
