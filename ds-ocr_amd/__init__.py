@@ -66,6 +66,7 @@ SIGNATURES = {
     "ds_hip_free": (None, [vp]),
     "ds_hip_memcpy_h2d": (C.c_int, [vp, vp, C.c_size_t]),
     "ds_hip_memcpy_d2h": (C.c_int, [vp, vp, C.c_size_t]),
+    "ds_hip_time_stream_read": (C.c_int, [vp, C.c_size_t, C.c_int, C.POINTER(C.c_float)]),
     "ds_hip_memcpy_d2d": (C.c_int, [vp, vp, C.c_size_t]),
     "ds_hip_sync": (C.c_int, []),
     "ds_hip_fill_normal_bf16": (C.c_int, [vp, C.c_size_t, C.c_uint64, C.c_float]),

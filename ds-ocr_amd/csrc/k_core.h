@@ -20,6 +20,9 @@ hipError_t dsh_launch_quantize_bf16_so(const uint16_t *W, int8_t *q, float *so, 
 hipError_t dsh_launch_quant_rms(const int8_t *q, const float *scale, const float *offset, const uint16_t *W,
                                 int out_dim, int in_dim, double *work, hipStream_t s);
 hipError_t dsh_launch_gemm_bf16w(const float *X, const uint16_t *W, float *Y, int M, int K, int N, hipStream_t s);
+/* Reads bytes (a multiple of 16) of src once; sink: [1024] words, written only on an impossible
+ * value. The roofline reference for the HBM-bound kernels. */
+hipError_t dsh_launch_stream_read(const void *src, size_t bytes, unsigned *sink, hipStream_t s);
 hipError_t dsh_launch_fill_normal_bf16(uint16_t *dst, size_t n, uint64_t seed, float std_, hipStream_t s);
 hipError_t dsh_launch_fill_normal_f32(float *dst, size_t n, uint64_t seed, float mean, float std_, hipStream_t s);
 hipError_t dsh_launch_dequantize(const int8_t *q, const float *scale, const float *offset, float *out, int out_dim,

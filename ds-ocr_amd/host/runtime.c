@@ -386,6 +386,28 @@ int ds_hip_memcpy_d2d(void *dst, const void *src, size_t n) {
   return 0;
 }
 
+int ds_hip_time_stream_read(const void *src_dev, size_t bytes, int n, float *ms) {
+  if (dsr_init()) return -1;
+  if (!src_dev || bytes < 16 || n <= 0 || !ms) return dsr_failf("ds_hip_time_stream_read: invalid arguments");
+  unsigned *sink = (unsigned *)dsr_scratch(DSR_SLOT_IDX, 1024 * sizeof(unsigned));
+  if (!sink) return -1;
+  hipEvent_t a, b;
+  DSR_TRY(hipEventCreate(&a), "event");
+  DSR_TRY(hipEventCreate(&b), "event");
+  hipError_t e = dsh_launch_stream_read(src_dev, bytes & ~(size_t)15, sink, dsr_stream); /* warm-up */
+  if (e == hipSuccess) e = hipEventRecord(a, dsr_stream);
+  for (int i = 0; i < n && e == hipSuccess; i++) e = dsh_launch_stream_read(src_dev, bytes & ~(size_t)15, sink, dsr_stream);
+  if (e == hipSuccess) e = hipEventRecord(b, dsr_stream);
+  if (e == hipSuccess) e = hipEventSynchronize(b);
+  float t = 0;
+  if (e == hipSuccess) e = hipEventElapsedTime(&t, a, b);
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  if (e != hipSuccess) return dsr_fail("stream read timing", e);
+  *ms = t / n;
+  return 0;
+}
+
 int ds_hip_sync(void) {
   if (dsr_init()) return -1;
   DSR_TRY(hipStreamSynchronize(dsr_stream), "synchronize");

@@ -33,6 +33,9 @@ void ds_hip_free(void *p_dev);
 int ds_hip_memcpy_h2d(void *dst_dev, const void *src, size_t bytes);
 int ds_hip_memcpy_d2h(void *dst, const void *src_dev, size_t bytes);
 int ds_hip_memcpy_d2d(void *dst_dev, const void *src_dev, size_t bytes);
+/* Average time of n back-to-back launches of a plain streaming read of bytes of src_dev (the
+ * achievable-bandwidth reference for the HBM-bound kernels; no counterpart in the reference). */
+int ds_hip_time_stream_read(const void *src_dev, size_t bytes, int n, float *ms);
 int ds_hip_sync(void);
 /* Seeded synthetic data generated on the device (counter-based SplitMix64 + Box–Muller). */
 int ds_hip_fill_normal_bf16(uint16_t *dst_dev, size_t n, uint64_t seed, float std_);
