@@ -184,6 +184,9 @@ def main():
     ap.add_argument("--decoder-step", type=int, default=-1, metavar="KV",
                     help=">= 0: whole decoder steps (attention 10x128 + MLP per layer, the dense layer 0, final "
                          "norm) after KV cached positions")
+    ap.add_argument("--decoder-kv", type=int, default=1000,
+                    help="also time whole decoder steps (attention + MLP per layer, final norm, head) after this "
+                         "many cached positions, as the line's 'decoder_step' entry (-1: skip)")
     ap.add_argument("--repeat-penalty", type=float, default=1.0,
                     help="> 1: the reference's repetition penalty after each argmax, over the run's tokens")
     ap.add_argument("--no-repeat-ngram", type=int, default=0, help="> 0: the reference's n-gram ban")
@@ -299,6 +302,40 @@ def main():
         xp.close()
         op.close()
 
+    # whole decoder steps: 12 layers with their attention halves after kv cached
+    # positions, timed like the main line over 40 steps after 5 warm-up steps
+    decoder = None
+    if args.decoder_kv >= 0 and not full:
+        kv, n_dec = args.decoder_kv, 45
+        dense2 = make_dense(dev)
+        attns2 = make_attention(dev, LAYERS + 1, kv, kv + n_dec + 1)
+        arr2 = (C.c_void_p * LAYERS)(*handles)
+        S2 = L.ds_hip_stack_create(arr2, LAYERS, lm.ptr, VOCAB, route)
+        if not S2:
+            raise RuntimeError(L.ds_hip_last_error().decode())
+        dev.check(L.ds_hip_stack_set_dense(S2, dense2), "set dense")
+        fnorm = np.ones(H, np.float32)
+        arr_a2 = (C.c_void_p * len(attns2))(*attns2)
+        dev.check(L.ds_hip_stack_set_attention(S2, arr_a2, len(attns2), fnorm.ctypes.data, 1e-6, kv, 0), "attention")
+        toks2 = dev.DeviceBuffer(n_dec * 4)
+        dev.check(L.ds_hip_stack_bind(S2, xs.ptr, H, toks2.ptr), "bind")
+        dev.check(L.ds_hip_stack_run(S2, 5), "warmup")
+        dev.check(L.ds_hip_sync(), "sync")
+        ms2 = C.c_float(0)
+        dev.check(L.ds_hip_time_stack(S2, n_dec - 5, C.byref(ms2)), "timed decoder steps")
+        step_ms = ms2.value / (n_dec - 5)
+        decoder = {"config": f"12 decoder layers (dense layer 0 + the 11 MoE layers above), each with its attention "
+                             f"half (10 heads x 128, f32 KV cache), final RMSNorm, argmax head; tokens at cache "
+                             f"positions {kv + 5}..{kv + n_dec - 1} after {kv} seeded cached positions",
+                   "steps": n_dec - 5, "ms_per_step": round(step_ms, 5), "tok_per_s": round(1e3 / step_ms, 2),
+                   "bytes_per_step_weights": int(L.ds_hip_stack_bytes_per_step(S2)),
+                   "note": "bytes exclude the KV reads (about 10 KB per cached position and layer)"}
+        L.ds_hip_stack_destroy(S2)
+        for A in attns2:
+            L.ds_hip_attn_destroy(A)
+        L.ds_hip_dense_destroy(dense2)
+        toks2.close()
+
     xs_host = xs.to_array(np.float32).reshape(n_inputs, H)[args.warmup:].copy()
     cpu = None
     if not args.no_cpu and not dense and not sampling and not full:  # the reference CPU leg: MoE layers + argmax head
@@ -349,6 +386,7 @@ def main():
                                          "way: the achievable HBM read rate on this box"},
         "kernels": kernel_ms,
         "prefill": prefill,
+        "decoder_step": decoder,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
