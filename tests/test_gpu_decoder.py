@@ -104,3 +104,83 @@ def test_decoder_step_vs_oracle(dev, B, mode, rswa):
         for h_ in hs:
             L.ds_hip_layer_destroy(h_)
         L.ds_hip_dense_destroy(D)
+
+
+def test_decoder_step_deepseek_size(dev, B):
+    """DeepSeek-OCR's decoder at full size: layer 0 dense (1280 x 6848), layers 1-11 config-2 MoE
+    (64 experts + 2 shared, INT8), 12 attention halves (10 heads x 128) after 64 cached positions,
+    R-SWA (reference 64 tokens, window 8), final RMSNorm, the 129280 x 1280 head; 3 steps in DECODE
+    routing against the oracle composed in the reference's order."""
+    from test_gpu_moe import export_layer, make_device_layer
+    L = dev.load()
+    O = B.oracle()
+    Hf, I0f, vocab, pos0, steps = 1280, 6848, 129280, 64, 3
+    qd = 10 * 128
+    made = [make_device_layer(dev, 130 + l) for l in range(11)]
+    hs = [m[0] for m in made]
+    g, u, d = (B.normal_bf16(I0f * Hf, 950 + i, 0.02) for i in range(3))
+    D = L.ds_hip_dense_create(Hf, I0f, g.ctypes.data, u.ctypes.data, d.ctypes.data)
+    assert D, L.ds_hip_last_error()
+    ws = [attn_weights(Hf, 10, 128, 1000 + 10 * i) for i in range(12)]
+    attns = [make(dev, w, Hf, 10, 128, 128) for w in ws]
+    oas = [or_attn(w, Hf, 10, 128, qd) for w in ws]
+    caches = []
+    for i, A in enumerate(attns):
+        kp, vp = rnd(pos0 * qd, 1200 + i, 0.3), rnd(pos0 * qd, 1300 + i)
+        dev.check(L.ds_hip_attn_load_kv(A, kp.ctypes.data, vp.ctypes.data, pos0, qd), "load kv")
+        dev.check(L.ds_hip_attn_set_window(A, pos0, 8), "window")
+        Kc, Vc = np.zeros(128 * qd, np.float32), np.zeros(128 * qd, np.float32)
+        Kc[:pos0 * qd], Vc[:pos0 * qd] = kp, vp
+        caches.append((Kc, Vc))
+    fnorm = rnd(Hf, 1400, 0.1) + 1
+    lm = dev.DeviceBuffer(vocab * Hf * 2)
+    dev.check(L.ds_hip_fill_normal_bf16(lm.ptr, vocab * Hf, 4343, 0.02), "fill")
+    xs = np.stack([rnd(Hf, 1500 + s) for s in range(steps)])
+    S = None
+    try:
+        arr = (C.c_void_p * 11)(*hs)
+        S = L.ds_hip_stack_create(arr, 11, lm.ptr, vocab, 0)
+        assert S, L.ds_hip_last_error()
+        dev.check(L.ds_hip_stack_set_dense(S, D), "dense")
+        at = (C.c_void_p * 12)(*attns)
+        dev.check(L.ds_hip_stack_set_attention(S, at, 12, fnorm.ctypes.data, 1e-6, pos0, 0), "attention")
+        xd = dev.DeviceBuffer.from_array(xs)
+        td = dev.DeviceBuffer(4 * steps)
+        dev.check(L.ds_hip_stack_bind(S, xd.ptr, Hf, td.ptr), "bind")
+        hidden = []
+        for _ in range(steps):
+            dev.check(L.ds_hip_stack_run(S, 1), "run")
+            hx = np.empty(Hf, np.float32)
+            dev.check(L.ds_hip_stack_hidden(S, hx), "hidden")
+            hidden.append(hx)
+        toks = td.to_array(np.int32)
+        lm_w = lm.to_array(np.uint16)
+        lays = [export_layer(dev, B, *m) for m in made]
+        orls = [lay.or_layer() for lay in lays]
+        gu = np.concatenate([g, u])
+        for s in range(steps):
+            pos = pos0 + s
+            x = xs[s].copy()
+            h, n = np.empty(Hf, np.float32), np.empty(Hf, np.float32)
+            out = np.empty(Hf, np.float32)
+            O.or_decoder_attn(h, n, x, C.byref(oas[0]), caches[0][0], caches[0][1], pos, pos0, 8, 1)
+            O.or_expert_bf16(out, n, gu, d, Hf, I0f, 0, 1)
+            x = h + out
+            for i in range(11):
+                O.or_decoder_attn(h, n, x, C.byref(oas[i + 1]), caches[i + 1][0], caches[i + 1][1], pos, pos0, 8, 1)
+                O.or_moe_layer_decode(out, n, C.byref(orls[i]), 0, 0, 1, None, None)
+                x = h + out
+            err = rel_err(hidden[s], x)
+            f = np.empty(Hf, np.float32)
+            O.or_rms_norm(f, hidden[s], fnorm, Hf, 1e-6)
+            print(f"DeepSeek-size decoder step {s}: hidden err {err:.2e}, token {toks[s]}")
+            assert err < TOL
+            assert toks[s] == O.or_argmax_bf16(f, lm_w, Hf, vocab, 1, None)
+    finally:
+        if S:
+            L.ds_hip_stack_destroy(S)
+        for A in attns:
+            L.ds_hip_attn_destroy(A)
+        for h_ in hs:
+            L.ds_hip_layer_destroy(h_)
+        L.ds_hip_dense_destroy(D)
