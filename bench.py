@@ -190,6 +190,9 @@ def main():
     ap.add_argument("--repeat-penalty", type=float, default=1.0,
                     help="> 1: the reference's repetition penalty after each argmax, over the run's tokens")
     ap.add_argument("--no-repeat-ngram", type=int, default=0, help="> 0: the reference's n-gram ban")
+    ap.add_argument("--layer-kernels", type=int, choices=[1, 2], default=1,
+                    help="MoE layer kernels in CFG routing: 1 (down split over intermediate units, per-XCD "
+                         "output copies) or 2 (gate_up, then down with the combine in top-k order)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (HBM counter calibration)")
     args = ap.parse_args()
@@ -240,8 +243,10 @@ def main():
         arr_a = (C.c_void_p * len(attns))(*attns)
         dev.check(L.ds_hip_stack_set_attention(S, arr_a, len(attns), fnorm.ctypes.data, 1e-6, args.decoder_step, 0),
                   "set attention")
+    dev.check(L.ds_hip_stack_set_layer_kernels(S, 1 if args.layer_kernels == 1 else 0), "layer kernels")
     dev.check(L.ds_hip_stack_bind(S, xs.ptr, H, toks.ptr), "bind")
     bytes_per_step = L.ds_hip_stack_bytes_per_step(S)
+    layer_kernels = L.ds_hip_stack_layer_kernels(S)
 
     # warmup, then exactly --steps timed steps (graph launches) between synchronisations
     dev.check(L.ds_hip_stack_run(S, args.warmup), "warmup")
@@ -372,7 +377,8 @@ def main():
                                "config 5: 11 DeepSeek3B-MoE INT8 layers (H1280, 64x[1792x1280 + 1280x896] "
                                "routed top-6 + 2 shared, f32 router renormalised) + argmax LM head 129280x1280 "
                                "bf16, batch 1, 226-step decode",
-                   "route": args.route, "global_batch": 1, "parallelism": "single GPU"},
+                   "route": args.route, "moe_layer_kernels": layer_kernels, "global_batch": 1,
+                   "parallelism": "single GPU"},
         "hbm": {"bytes_per_step": int(bytes_per_step), "achieved_gbs": round(step_gbs, 1),
                 "frac_of_peak": round(step_gbs / PEAK_HBM_GBS, 4), "peak_gbs": PEAK_HBM_GBS,
                 "wall_s_timed_region": round(wall, 4)},

@@ -158,6 +158,31 @@ hipError_t dsh_launch_dec_lm_argmax_depth(const uint16_t *W, const float *x, int
 hipError_t dsh_launch_dec_lm_argmax(const uint16_t *W, const float *x, int in_dim, int vocab,
                                     unsigned long long *cand, hipStream_t s);
 
+/* ---- one kernel per MoE layer, down split over intermediate units (k_layer.hip) ---- */
+typedef struct {
+  const int8_t *dnT, *sdnT; /* down tiles of the routed experts [E][I/32], of the shared expert [SI/32] */
+  const float *M, *sM;      /* next router x down products, tiles as the down tiles; NULL: last layer */
+  const float *z, *sz;      /* next router x down offsets: [E][64], [64] */
+  const float *WrT_next;    /* [H][E_next]; NULL: last layer */
+  int E_next;
+} dsh_split_t;
+int dsh_layer_split_supported(const dsh_layer_t *L);
+int dsh_layer_split_blocks(const dsh_layer_t *L);
+int dsh_layer_split_copies(void);
+size_t dsh_layer_split_tile_bytes(const dsh_layer_t *L); /* routed + shared down tiles */
+size_t dsh_layer_split_m_floats(const dsh_layer_t *L);   /* routed + shared M tiles */
+/* Fills the tiles (and, with WrT_next, M and z) of layer L from its arena. */
+hipError_t dsh_launch_layer_build(const dsh_layer_t *L, const float *WrT_next, int E_next, int8_t *dnT, int8_t *sdnT,
+                                  float *M, float *sM, float *z, float *sz, hipStream_t s);
+/* x_out ([copies][H]) += x + MoE(x); lg_out ([copies][64]) += the next layer's router scores (when F->M).
+ * Input: ncopies == 1: x = x_in + (*step)*stride (step may be NULL), router partials [np <= 160][64];
+ * ncopies == copies: x = Σ copies of x_in, router scores as [copies][64]. Clears zero_p[0..zero_n). */
+hipError_t dsh_launch_dec_layer(const dsh_layer_t *L, const dsh_split_t *F, const float *x_in, const int *step,
+                                int stride, int ncopies, const float *partials, int np, float *x_out, float *lg_out,
+                                float *zero_p, int zero_n, hipStream_t s);
+/* out = Σ copies of X ([copies][H]); clears X and zero_p[0..zero_n). */
+hipError_t dsh_launch_dec_copy_sum(float *X, int H, float *out, float *zero_p, int zero_n, hipStream_t s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -738,6 +738,13 @@ struct ds_hip_stack {
   float rp;
   int ngram, hist_cap;
   void *smp_work; /* [hist_cap + 1] dots, [vocab] logits, flag */
+  /* one kernel per MoE layer (k_layer.hip): per-layer down tiles and next-router products, and the
+   * layer outputs kept as per-XCD copies; built by ds_hip_stack_bind */
+  int split_want, split;
+  void *split_arena;
+  dsh_split_t *sp;   /* [n_layers] */
+  float *xc;         /* layer l's output (l = 1..n_layers): region l-1 of [copies][H] + [copies][64] */
+  size_t xc_region;  /* floats per region */
 };
 
 int ds_hip_lm_head_sample(const float *x_dev, const uint16_t *lm_head_dev, int hidden, int vocab, const int *history_dev,
@@ -806,6 +813,7 @@ ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers,
   S->cand = (unsigned long long *)((char *)S->work + off_c);
   S->partials[0] = (float *)((char *)S->work + off_p);
   S->partials[1] = (float *)((char *)S->work + off_p + np_bytes);
+  S->split_want = 1;
   return S;
 }
 
@@ -817,6 +825,8 @@ void ds_hip_stack_destroy(ds_hip_stack_t *S) {
   hipFree(S->work);
   if (S->smp_work) hipFree(S->smp_work);
   if (S->att_work) hipFree(S->att_work);
+  if (S->split_arena) hipFree(S->split_arena);
+  free(S->sp);
   free(S->attn);
   free(S->layers);
   free(S);
@@ -933,6 +943,15 @@ static int stack_names(const ds_hip_stack_t *S, const char **names) {
       NM("down");
     }
     NM("final_norm");
+  } else if (S->split) {
+    if (S->dense) {
+      NM("dense.gate_up");
+      NM("dense.down");
+    } else {
+      NM("scores");
+    }
+    for (int l = 0; l < S->n_layers; l++) NM("layer");
+    NM("copy_sum");
   } else {
     if (S->dense) {
       NM("dense.gate_up");
@@ -1010,6 +1029,117 @@ static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *ne
   return e;
 }
 
+/* The MoE layers as one kernel each (CFG routing): layer l reads its input (the step's input or the
+ * dense layer's output for l = 0, else the copies region l - 1 with its router scores) and adds
+ * into region l; it also clears region l - 2, read by layer l - 2 (every region is zero at the
+ * end of a step). The copy sum then writes the plain output for the LM head. */
+static float *xc_region(const ds_hip_stack_t *S, int l) { return S->xc + (size_t)l * S->xc_region; }
+
+static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *nev) {
+  hipError_t e = hipSuccess;
+  const int dense = S->dense != NULL, NL = S->n_layers, H = S->H, C = dsh_layer_split_copies();
+  const int zn = (int)S->xc_region;
+  int np0 = S->layers[0]->np;
+  if (!dense) {
+    e = scores_enqueue(S->layers[0], S->xs, S->step, S->stride, S->route_mode, S->partials[0], &np0);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+  }
+  for (int l = 0; l < NL && e == hipSuccess; l++) {
+    const ds_hip_layer_t *L = S->layers[l];
+    float *out = xc_region(S, l);
+    float *zp = l >= 2 ? xc_region(S, l - 2) : NULL;
+    if (l == 0)
+      e = dsh_launch_dec_layer(&L->d, &S->sp[l], dense ? S->xbuf : S->xs, dense ? NULL : S->step,
+                               dense ? 0 : S->stride, 1, S->partials[0], np0, out, out + (size_t)C * H, zp,
+                               zp ? zn : 0, dsr_stream);
+    else {
+      float *in = xc_region(S, l - 1);
+      e = dsh_launch_dec_layer(&L->d, &S->sp[l], in, NULL, 0, C, in + (size_t)C * H, C, out, out + (size_t)C * H, zp,
+                               zp ? zn : 0, dsr_stream);
+    }
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+  }
+  if (e == hipSuccess)
+    e = dsh_launch_dec_copy_sum(xc_region(S, NL - 1), H, S->xbuf, NL >= 2 ? xc_region(S, NL - 2) : NULL,
+                                NL >= 2 ? zn : 0, dsr_stream);
+  if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+  return e;
+}
+
+/* Whether the one-kernel layers apply: CFG routing, no bf16 simulation, no attention, supported
+ * shapes. */
+static int split_eligible(const ds_hip_stack_t *S) {
+  if (!S->split_want || S->route_mode != DS_HIP_ROUTE_CFG || S->bf16sim || S->attn) return 0;
+  for (int l = 0; l < S->n_layers; l++)
+    if (!dsh_layer_split_supported(&S->layers[l]->d) || !S->layers[l]->have_f32) return 0;
+  return 1;
+}
+
+/* Allocates and fills the per-layer tiles and products and the copies regions. */
+static int split_build(ds_hip_stack_t *S) {
+  if (S->split_arena) {
+    hipFree(S->split_arena);
+    S->split_arena = NULL;
+  }
+  free(S->sp);
+  S->sp = NULL;
+  const int NL = S->n_layers, C = dsh_layer_split_copies();
+  size_t bytes = 0;
+  for (int l = 0; l < NL; l++) {
+    const dsh_layer_t *d = &S->layers[l]->d;
+    bytes += al(dsh_layer_split_tile_bytes(d));
+    if (l + 1 < NL) bytes += al(dsh_layer_split_m_floats(d) * 4) + al((size_t)(d->E + 1) * 64 * 4);
+  }
+  S->xc_region = (size_t)C * S->H + (size_t)C * 64;
+  bytes += al((size_t)NL * S->xc_region * 4);
+  S->sp = (dsh_split_t *)calloc((size_t)NL, sizeof(dsh_split_t));
+  if (!S->sp) return dsr_failf("split layer tables: out of memory");
+  hipError_t e = hipMalloc(&S->split_arena, bytes);
+  if (e != hipSuccess) {
+    S->split_arena = NULL;
+    return dsr_fail("one-kernel layer arena allocation", e);
+  }
+  char *b = (char *)S->split_arena;
+  for (int l = 0; l < NL && e == hipSuccess; l++) {
+    const dsh_layer_t *d = &S->layers[l]->d;
+    dsh_split_t *F = &S->sp[l];
+    int8_t *tiles = (int8_t *)b;
+    const size_t routed = (size_t)d->E * d->I * d->H;
+    b += al(dsh_layer_split_tile_bytes(d));
+    float *M = NULL, *z = NULL;
+    const dsh_layer_t *nx = l + 1 < NL ? &S->layers[l + 1]->d : NULL;
+    if (nx) {
+      M = (float *)b;
+      b += al(dsh_layer_split_m_floats(d) * 4);
+      z = (float *)b;
+      b += al((size_t)(d->E + 1) * 64 * 4);
+    }
+    F->dnT = tiles;
+    F->sdnT = tiles + routed;
+    F->M = M;
+    F->sM = M ? M + (size_t)d->E * d->I * 64 : NULL;
+    F->z = z;
+    F->sz = z ? z + (size_t)d->E * 64 : NULL;
+    F->WrT_next = nx ? nx->router_f32_t : NULL;
+    F->E_next = nx ? nx->E : 0;
+    e = dsh_launch_layer_build(d, F->WrT_next, F->E_next, tiles, tiles + routed, M, (float *)F->sM, z, (float *)F->sz,
+                               dsr_stream);
+  }
+  S->xc = (float *)b;
+  if (e == hipSuccess) e = hipMemsetAsync(S->xc, 0, (size_t)NL * S->xc_region * 4, dsr_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(dsr_stream);
+  if (e != hipSuccess) return dsr_fail("one-kernel layer tables", e);
+  return 0;
+}
+
+int ds_hip_stack_set_layer_kernels(ds_hip_stack_t *S, int one_kernel) {
+  if (!S || S->bound) return dsr_failf("ds_hip_stack_set_layer_kernels: NULL stack or already bound");
+  S->split_want = one_kernel != 0;
+  return 0;
+}
+
+int ds_hip_stack_layer_kernels(const ds_hip_stack_t *S) { return S && S->split ? 1 : 2; }
+
 static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
   hipError_t e = hipSuccess;
   int n = 0;
@@ -1030,6 +1160,9 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
                                   cfg ? S->partials[0] : NULL, dsr_stream);
       if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
     }
+    if (S->split && e == hipSuccess) {
+      e = split_layers_enqueue(S, ev, &n);
+    } else
     for (int l = 0; l < S->n_layers && e == hipSuccess; l++) {
       const ds_hip_layer_t *L = S->layers[l];
       const int first = l == 0 && !dense; /* reads the step's input directly */
@@ -1087,6 +1220,8 @@ int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int *t
   S->stride = stride;
   S->tokens = tokens_dev;
   DSR_TRY(hipStreamSynchronize(dsr_stream), "bind");
+  S->split = split_eligible(S);
+  if (S->split && split_build(S)) return -1;
   DSR_TRY(hipStreamBeginCapture(dsr_stream, hipStreamCaptureModeThreadLocal), "graph capture begin");
   hipError_t e = step_enqueue(S, NULL);
   hipGraph_t g = NULL;
@@ -1106,6 +1241,8 @@ int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int *t
 int ds_hip_stack_reset(ds_hip_stack_t *S) {
   if (!S) return -1;
   DSR_TRY(hipMemsetAsync(S->work, 0, S->work_bytes, dsr_stream), "reset stack");
+  if (S->split && S->xc)
+    DSR_TRY(hipMemsetAsync(S->xc, 0, (size_t)S->n_layers * S->xc_region * 4, dsr_stream), "reset stack");
   return 0;
 }
 
