@@ -92,6 +92,9 @@ hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int r
 /* Final reduction of per-block argmax candidates: writes tokens[*step] (tokens[0] when step is
  * NULL) and advances *step. */
 hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int *tokens, int *step, hipStream_t s);
+/* The same, also clearing zero_p[0..zero_n) (16-byte aligned, zero_n % 4 == 0). */
+hipError_t dsh_launch_lm_argmax_final_clear(const unsigned long long *cand, int n, int *tokens, int *step,
+                                            float *zero_p, int zero_n, hipStream_t s);
 
 /* ---- latency-oriented decode kernels (k_dec.hip) ---- */
 int dsh_dec_supported(int H, int I, int E, int K, int SI);
@@ -157,6 +160,10 @@ hipError_t dsh_launch_dec_lm_argmax_depth(const uint16_t *W, const float *x, int
                                           unsigned long long *cand, int depth, hipStream_t s);
 hipError_t dsh_launch_dec_lm_argmax(const uint16_t *W, const float *x, int in_dim, int vocab,
                                     unsigned long long *cand, hipStream_t s);
+/* The same head on x = Σ of ncopies (8) copies [ncopies][in_dim] (in_dim <= 2048); x_out (optional)
+ * receives that sum. */
+hipError_t dsh_launch_dec_lm_argmax_copies(const uint16_t *W, const float *xc, int ncopies, int in_dim, int vocab,
+                                           unsigned long long *cand, float *x_out, hipStream_t s);
 
 /* ---- one kernel per MoE layer, down split over intermediate units (k_layer.hip) ---- */
 typedef struct {

@@ -454,12 +454,18 @@ __global__ void __launch_bounds__(512) k_dec_down(dsh_layer_t L, const float *__
 // and accumulates its 32 chains in registers; x is uniform across the wave (scalar loads). A ring of
 // D lines of loads is kept in flight. Requires in_dim % 64 == 0. Each block writes its
 // (max, lowest index) key.
-template <int D>
+// XC > 0: x is XC copies [XC][in_dim] whose sum (in copy order) is the input; each block forms it
+// in LDS after issuing its first line of loads (block 0 also stores it to x_out when given).
+// (Finishing the argmax in the last block to arrive, with an acquire-release counter, was measured
+// ~20 us slower than the separate final kernel: every block's release writes back its XCD's L2.)
+template <int D, int XC>
 __global__ void __launch_bounds__(256) k_dec_lm_argmax(const uint16_t *W, const float *__restrict__ x,
-                                                       int in_dim, int vocab, unsigned long long *__restrict__ cand) {
+                                                       int in_dim, int vocab, unsigned long long *__restrict__ cand,
+                                                       float *__restrict__ x_out) {
   constexpr int PITCH = 144;
   __shared__ __attribute__((aligned(16))) uint8_t tile[4][64 * PITCH];
   __shared__ unsigned long long wbest[4];
+  __shared__ __attribute__((aligned(16))) float s_xs[XC ? 2048 : 4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r0 = (blockIdx.x * 4 + wave) * 64;
   const size_t row_bytes = (size_t)in_dim * 2;
@@ -485,6 +491,29 @@ __global__ void __launch_bounds__(256) k_dec_lm_argmax(const uint16_t *W, const 
     for (int j = 0; j < 8; j++) ring[s][j] = dsh_load_nt(src[j] + 128 * s);
     asm volatile("" ::: "memory");
   }
+  if constexpr (XC > 0) {  // the input: sum of the copies, two 4-float pieces per thread at most
+    const int npc = in_dim >> 2;
+    const int p0 = threadIdx.x, p1 = min((int)threadIdx.x + 256, npc - 1);
+    f32x4 a[XC], b[XC];
+#pragma unroll
+    for (int c = 0; c < XC; c++) {
+      a[c] = ((const f32x4 *)(x + (size_t)c * in_dim))[min(p0, npc - 1)];
+      b[c] = ((const f32x4 *)(x + (size_t)c * in_dim))[p1];
+    }
+    f32x4 sa = a[0], sb = b[0];
+#pragma unroll
+    for (int c = 1; c < XC; c++) {
+      sa += a[c];
+      sb += b[c];
+    }
+    if (p0 < npc) *(f32x4 *)(s_xs + 4 * p0) = sa;
+    if ((int)threadIdx.x + 256 < npc) *(f32x4 *)(s_xs + 4 * p1) = sb;
+    if (x_out && blockIdx.x == 0) {
+      if (p0 < npc) *(f32x4 *)(x_out + 4 * p0) = sa;
+      if ((int)threadIdx.x + 256 < npc) *(f32x4 *)(x_out + 4 * p1) = sb;
+    }
+    __syncthreads();
+  }
   for (int t0 = 0; t0 < NT; t0 += D) {
 #pragma unroll
     for (int s = 0; s < D; s++) {
@@ -502,7 +531,7 @@ __global__ void __launch_bounds__(256) k_dec_lm_argmax(const uint16_t *W, const 
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       const uint8_t *mine = wtile + lane * PITCH;
-      const float *xt = x + 64 * t;
+      const float *xt = (XC > 0 ? s_xs : x) + 64 * t;
 #pragma unroll
       for (int p = 0; p < 8; p++) {
         u32x4 v = *(const u32x4 *)(mine + 16 * p);
@@ -541,9 +570,12 @@ __global__ void __launch_bounds__(256) k_dec_lm_argmax(const uint16_t *W, const 
 
 // Final reduction of the candidates; writes tokens[*step] (or tokens[0]) and advances *step.
 // The step index and a batch of 4 candidates per thread are loaded together (clamped addresses, no
-// branches), so the kernel waits for one round trip per 1024 candidates.
+// branches), so the kernel waits for one round trip per 1024 candidates. Also clears
+// zero_p[0..zero_n) (16-byte aligned, zero_n % 4 == 0).
 __global__ void __launch_bounds__(256) k_lm_argmax_final(const unsigned long long *__restrict__ cand, int n,
-                                                         int *__restrict__ tokens, int *__restrict__ step) {
+                                                         int *__restrict__ tokens, int *__restrict__ step,
+                                                         float *__restrict__ zero_p, int zero_n) {
+  for (int i = 4 * threadIdx.x; i < zero_n; i += 1024) *(f32x4 *)(zero_p + i) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   __shared__ unsigned long long wbest[4];
   const int s = step ? *step : 0;
   unsigned long long b = 0ull;
@@ -661,7 +693,14 @@ int dsh_dec_lm_eligible(const void *W, int in_dim, int vocab, int nthreads) {
 }
 
 hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int *tokens, int *step, hipStream_t s) {
-  k_lm_argmax_final<<<1, 256, 0, s>>>(cand, n, tokens, step);
+  k_lm_argmax_final<<<1, 256, 0, s>>>(cand, n, tokens, step, nullptr, 0);
+  return hipGetLastError();
+}
+
+hipError_t dsh_launch_lm_argmax_final_clear(const unsigned long long *cand, int n, int *tokens, int *step,
+                                            float *zero_p, int zero_n, hipStream_t s) {
+  if (((uintptr_t)zero_p & 15) || zero_n % 4) return hipErrorInvalidValue;
+  k_lm_argmax_final<<<1, 256, 0, s>>>(cand, n, tokens, step, zero_p, zero_n);
   return hipGetLastError();
 }
 
@@ -673,17 +712,25 @@ hipError_t dsh_launch_dec_lm_argmax_depth(const uint16_t *W, const float *x, int
   const int nb = dsh_dec_lm_blocks(vocab);
   switch (depth) {
     case 1:
-      k_dec_lm_argmax<1><<<nb, 256, 0, s>>>(W, x, in_dim, vocab, cand);
+      k_dec_lm_argmax<1, 0><<<nb, 256, 0, s>>>(W, x, in_dim, vocab, cand, nullptr);
       break;
     case 2:
-      k_dec_lm_argmax<2><<<nb, 256, 0, s>>>(W, x, in_dim, vocab, cand);
+      k_dec_lm_argmax<2, 0><<<nb, 256, 0, s>>>(W, x, in_dim, vocab, cand, nullptr);
       break;
     case 4:
-      k_dec_lm_argmax<4><<<nb, 256, 0, s>>>(W, x, in_dim, vocab, cand);
+      k_dec_lm_argmax<4, 0><<<nb, 256, 0, s>>>(W, x, in_dim, vocab, cand, nullptr);
       break;
     default:
       return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t dsh_launch_dec_lm_argmax_copies(const uint16_t *W, const float *xc, int ncopies, int in_dim, int vocab,
+                                           unsigned long long *cand, float *x_out, hipStream_t s) {
+  if (!dsh_dec_lm_supported(in_dim) || in_dim > 2048 || ((uintptr_t)W & 15) || vocab <= 0 || ncopies != 8)
+    return hipErrorInvalidValue;
+  k_dec_lm_argmax<1, 8><<<dsh_dec_lm_blocks(vocab), 256, 0, s>>>(W, xc, in_dim, vocab, cand, x_out);
   return hipGetLastError();
 }
 

@@ -951,7 +951,7 @@ static int stack_names(const ds_hip_stack_t *S, const char **names) {
       NM("scores");
     }
     for (int l = 0; l < S->n_layers; l++) NM("layer");
-    NM("copy_sum");
+    if (!S->lm_fast) NM("copy_sum");
   } else {
     if (S->dense) {
       NM("dense.gate_up");
@@ -1059,11 +1059,26 @@ static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *n
     }
     if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
   }
-  if (e == hipSuccess)
-    e = dsh_launch_dec_copy_sum(xc_region(S, NL - 1), H, S->xbuf, NL >= 2 ? xc_region(S, NL - 2) : NULL,
-                                NL >= 2 ? zn : 0, dsr_stream);
-  if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+  if (!S->lm_fast) { /* the plain output for the general LM-head path (the fast head sums the copies) */
+    if (e == hipSuccess)
+      e = dsh_launch_dec_copy_sum(xc_region(S, NL - 1), H, S->xbuf, NL >= 2 ? xc_region(S, NL - 2) : NULL,
+                                  NL >= 2 ? zn : 0, dsr_stream);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+  }
   return e;
+}
+
+/* The fast LM head on the last layer's copies (its block 0 writes the plain output, the hidden
+ * state); the final kernel after it then clears the last two copies regions. */
+static hipError_t split_lm_enqueue(ds_hip_stack_t *S) {
+  return dsh_launch_dec_lm_argmax_copies(S->lm, xc_region(S, S->n_layers - 1), dsh_layer_split_copies(), S->H,
+                                         S->vocab, S->cand, S->xbuf, dsr_stream);
+}
+
+static hipError_t split_final_enqueue(ds_hip_stack_t *S) {
+  const int NL = S->n_layers;
+  return dsh_launch_lm_argmax_final_clear(S->cand, S->ncand, S->tokens, S->step, xc_region(S, NL >= 2 ? NL - 2 : 0),
+                                          (int)S->xc_region * (NL >= 2 ? 2 : 1), dsr_stream);
 }
 
 /* Whether the one-kernel layers apply: CFG routing, no bf16 simulation, no attention, supported
@@ -1186,7 +1201,10 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
     }
   }
   if (e != hipSuccess) return e;
-  if (S->lm_fast) {
+  const int lm_copies = S->split && S->lm_fast;
+  if (lm_copies) {
+    e = split_lm_enqueue(S);
+  } else if (S->lm_fast) {
     e = dsh_launch_dec_lm_argmax(S->lm, lm_in(S), S->H, S->vocab, S->cand, dsr_stream);
   } else {
     int T = dsr_threads();
@@ -1194,7 +1212,8 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
                                       T > 1 ? (S->vocab + T - 1) / T : S->vocab, dsr_stream);
   }
   if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
-  if (e == hipSuccess) e = dsh_launch_lm_argmax_final(S->cand, S->ncand, S->tokens, S->step, dsr_stream);
+  if (e == hipSuccess)
+    e = lm_copies ? split_final_enqueue(S) : dsh_launch_lm_argmax_final(S->cand, S->ncand, S->tokens, S->step, dsr_stream);
   if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
   if (e == hipSuccess && smp_active(S)) {
     /* the repetition penalty and the n-gram ban over this stack's earlier tokens; one event after
@@ -1291,7 +1310,10 @@ int ds_hip_time_lm_head(ds_hip_stack_t *S, int n, float *ms) {
   int rc = 0;
   hipError_t e = hipEventRecord(a, dsr_stream);
   for (int i = 0; i < n && e == hipSuccess; i++) {
-    if (S->lm_fast) {
+    if (S->split && S->lm_fast) {  /* the step's head kernel without its final block's work */
+      e = dsh_launch_dec_lm_argmax_copies(S->lm, xc_region(S, S->n_layers - 1), dsh_layer_split_copies(), S->H,
+                                          S->vocab, S->cand, NULL, dsr_stream);
+    } else if (S->lm_fast) {
       e = dsh_launch_dec_lm_argmax(S->lm, lm_in(S), S->H, S->vocab, S->cand, dsr_stream);
     } else {
       int T = dsr_threads();
