@@ -146,6 +146,9 @@ hipError_t dsh_launch_dec_partial_scores(const float *WrT, const float *x_in, co
                                          float *partials, hipStream_t s);
 hipError_t dsh_launch_dec_scores_bf16(const uint16_t *Wr, const float *x_in, const int *step, int stride, int H, int E,
                                       int nthreads, float *partials, hipStream_t s);
+/* ncopies == 8: x = Σ of the 8 copies [8][H] at x_in (in copy order; step must be NULL). */
+hipError_t dsh_launch_dec_scores_bf16_copies(const uint16_t *Wr, const float *x_in, const int *step, int stride,
+                                             int ncopies, int H, int E, int nthreads, float *partials, hipStream_t s);
 hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const int *step, int stride,
                                   const float *partials, int np, int route_mode, int bf16sim,
                                   const dsh_layer_work_t *wk, hipStream_t s);
@@ -183,10 +186,12 @@ hipError_t dsh_launch_layer_build(const dsh_layer_t *L, const float *WrT_next, i
                                   float *M, float *sM, float *z, float *sz, hipStream_t s);
 /* x_out ([copies][H]) += x + MoE(x); lg_out ([copies][64]) += the next layer's router scores (when F->M).
  * Input: ncopies == 1: x = x_in + (*step)*stride (step may be NULL), router partials [np <= 160][64];
- * ncopies == copies: x = Σ copies of x_in, router scores as [copies][64]. Clears zero_p[0..zero_n). */
+ * ncopies == copies: x = Σ copies of x_in, router partials [np <= 8][64] (CFG: the score copies).
+ * route_mode: DSH_ROUTE_CFG or DSH_ROUTE_DECODE (then np == 1: the exact scores; empty slots add
+ * nothing). Clears zero_p[0..zero_n). */
 hipError_t dsh_launch_dec_layer(const dsh_layer_t *L, const dsh_split_t *F, const float *x_in, const int *step,
-                                int stride, int ncopies, const float *partials, int np, float *x_out, float *lg_out,
-                                float *zero_p, int zero_n, hipStream_t s);
+                                int stride, int ncopies, const float *partials, int np, int route_mode, float *x_out,
+                                float *lg_out, float *zero_p, int zero_n, hipStream_t s);
 /* out = Σ copies of X ([copies][H]); clears X and zero_p[0..zero_n). */
 hipError_t dsh_launch_dec_copy_sum(float *X, int H, float *out, float *zero_p, int zero_n, hipStream_t s);
 

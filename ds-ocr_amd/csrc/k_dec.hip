@@ -103,7 +103,7 @@ __global__ void __launch_bounds__(256) k_transpose_f32(const float *__restrict__
 template <int N32>
 __global__ void __launch_bounds__(64) k_dec_scores_bf16(const uint16_t *__restrict__ Wr, const float *__restrict__ x_in,
                                                         const int *__restrict__ step, int stride, int E, int chunk,
-                                                        float *__restrict__ partials) {
+                                                        float *__restrict__ partials, int ncopies) {
   constexpr int H = 32 * N32, NX = H / 4, XP = (NX + 63) / 64;
   __shared__ __attribute__((aligned(16))) float xs[H];
   const float *x = at_step(x_in, step, stride);
@@ -112,6 +112,17 @@ __global__ void __launch_bounds__(64) k_dec_scores_bf16(const uint16_t *__restri
   f32x4 xr[XP];
 #pragma unroll
   for (int j = 0; j < XP; j++) xr[j] = ((const f32x4 *)x)[min((int)threadIdx.x + 64 * j, NX - 1)];
+  if (ncopies > 1) {  // x = Σ of 8 copies [8][H], added in copy order (as the one-kernel layer does)
+    f32x4 xc[XP][7];
+#pragma unroll
+    for (int j = 0; j < XP; j++)
+#pragma unroll
+      for (int c = 0; c < 7; c++) xc[j][c] = ((const f32x4 *)(x + (size_t)(c + 1) * H))[min((int)threadIdx.x + 64 * j, NX - 1)];
+#pragma unroll
+    for (int j = 0; j < XP; j++)
+#pragma unroll
+      for (int c = 0; c < 7; c++) xr[j] += xc[j][c];
+  }
   asm volatile("" ::: "memory");  // x first: its LDS stores wait for x only
   const u32x4 *row = (const u32x4 *)(Wr + (size_t)ec * H);
   u32x4 wv[N32];
@@ -628,12 +639,13 @@ hipError_t dsh_launch_dec_partial_scores(const float *WrT, const float *x_in, co
   return hipGetLastError();
 }
 
-hipError_t dsh_launch_dec_scores_bf16(const uint16_t *Wr, const float *x_in, const int *step, int stride, int H, int E,
-                                      int nthreads, float *partials, hipStream_t s) {
+hipError_t dsh_launch_dec_scores_bf16_copies(const uint16_t *Wr, const float *x_in, const int *step, int stride,
+                                             int ncopies, int H, int E, int nthreads, float *partials, hipStream_t s) {
   const int blocks = (E + 15) / 16, chunk = dsh_chunk_len(E, nthreads);
-#define SC(N)                                                                                  \
-  case N:                                                                                      \
-    k_dec_scores_bf16<8 * N><<<blocks, 64, 0, s>>>(Wr, x_in, step, stride, E, chunk, partials); \
+  if (ncopies != 1 && (ncopies != 8 || step)) return hipErrorInvalidValue;
+#define SC(N)                                                                                             \
+  case N:                                                                                                 \
+    k_dec_scores_bf16<8 * N><<<blocks, 64, 0, s>>>(Wr, x_in, step, stride, E, chunk, partials, ncopies); \
     break;
   if (H % 256) return hipErrorInvalidValue;
   switch (H / 256) {
@@ -643,6 +655,11 @@ hipError_t dsh_launch_dec_scores_bf16(const uint16_t *Wr, const float *x_in, con
   }
 #undef SC
   return hipGetLastError();
+}
+
+hipError_t dsh_launch_dec_scores_bf16(const uint16_t *Wr, const float *x_in, const int *step, int stride, int H, int E,
+                                      int nthreads, float *partials, hipStream_t s) {
+  return dsh_launch_dec_scores_bf16_copies(Wr, x_in, step, stride, 1, H, E, nthreads, partials, s);
 }
 
 static int dec_gate_up_blocks(const dsh_layer_t *L) {

@@ -74,8 +74,8 @@ __device__ __forceinline__ void dl_issue(dl_regs<CPL> &R, const int8_t *gu, cons
 template <int CPL, int NREP, int RB>
 __global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F, const float *x_in,
                                                    const int *__restrict__ step, int stride,
-                                                   const float *partials, int np, float *x_out, float *lg_out,
-                                                   float *zero_p, int zero_n) {
+                                                   const float *partials, int np, int mode, float *x_out,
+                                                   float *lg_out, float *zero_p, int zero_n) {
   constexpr int H = 256 * CPL, NP = 64 * CPL, XV = (NP + 511) / 512, NL = 4;
   __shared__ int s_idx[8 * 64];
   __shared__ float s_w[8 * 64];
@@ -163,9 +163,13 @@ __global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F,
 
   float wexp = 1.0f;  // this block's expert weight (1 for the shared expert)
   if (!shared_blk) {
-    route_select(L.E, L.K, DSH_ROUTE_CFG, s_idx + 64 * wave, s_w + 64 * wave, s_red, s_scr + wave);
-    const int e = s_idx[64 * wave + slot];
+    route_select(L.E, L.K, mode, s_idx + 64 * wave, s_w + 64 * wave, s_red, s_scr + wave);
+    int e = s_idx[64 * wave + slot];
     wexp = s_w[64 * wave + slot];
+    if (e < 0) {  // DECODE routing left this slot empty: expert 0's rows, added with weight 0
+      e = 0;
+      wexp = 0.0f;
+    }
     const size_t g0 = (size_t)e * 2 * I + (size_t)sl * DL_UB;
     const size_t tile = (size_t)e * NSL + sl;
     dl_issue<CPL>(R, L.gu_q, L.gu_so, g0, g0 + I, F.dnT + tile * DL_UB * H, L.dn_so + (size_t)e * H * 2,
@@ -385,19 +389,20 @@ hipError_t dsh_launch_layer_build(const dsh_layer_t *L, const float *WrT_next, i
 }
 
 hipError_t dsh_launch_dec_layer(const dsh_layer_t *L, const dsh_split_t *F, const float *x_in, const int *step,
-                                int stride, int ncopies, const float *partials, int np, float *x_out, float *lg_out,
-                                float *zero_p, int zero_n, hipStream_t s) {
+                                int stride, int ncopies, const float *partials, int np, int route_mode, float *x_out,
+                                float *lg_out, float *zero_p, int zero_n, hipStream_t s) {
   const int nb = dsh_layer_split_blocks(L);
   if (ncopies != 1 && ncopies != DL_REP) return hipErrorInvalidValue;
-  if (ncopies == 1 ? np > 160 : np > 8) return hipErrorInvalidValue;
+  if (np < 1 || (ncopies == 1 ? np > 160 : np > 8)) return hipErrorInvalidValue;
+  if (route_mode != DSH_ROUTE_CFG && (route_mode != DSH_ROUTE_DECODE || np != 1 || F->M)) return hipErrorInvalidValue;
 #define DLK(N)                                                                                                   \
   case N:                                                                                                        \
     if (ncopies == 1)                                                                                            \
-      k_dec_layer<N, 1, 40><<<nb, 512, 0, s>>>(*L, *F, x_in, step, stride, partials, np, x_out, lg_out, zero_p,  \
-                                               zero_n);                                                          \
+      k_dec_layer<N, 1, 40><<<nb, 512, 0, s>>>(*L, *F, x_in, step, stride, partials, np, route_mode, x_out,    \
+                                               lg_out, zero_p, zero_n);                                                          \
     else                                                                                                         \
-      k_dec_layer<N, DL_REP, 2><<<nb, 512, 0, s>>>(*L, *F, x_in, step, stride, partials, np, x_out, lg_out,      \
-                                                   zero_p, zero_n);                                              \
+      k_dec_layer<N, DL_REP, 2><<<nb, 512, 0, s>>>(*L, *F, x_in, step, stride, partials, np, route_mode, x_out, \
+                                                   lg_out, zero_p, zero_n);                                              \
     break;
   switch (L->H / 256) {
     DLK(1) DLK(2) DLK(3) DLK(4) DLK(5) DLK(6) DLK(7) DLK(8)

@@ -947,10 +947,11 @@ static int stack_names(const ds_hip_stack_t *S, const char **names) {
     if (S->dense) {
       NM("dense.gate_up");
       NM("dense.down");
-    } else {
-      NM("scores");
     }
-    for (int l = 0; l < S->n_layers; l++) NM("layer");
+    for (int l = 0; l < S->n_layers; l++) {
+      if (!cfg || (l == 0 && !S->dense)) NM("scores");
+      NM("layer");
+    }
     if (!S->lm_fast) NM("copy_sum");
   } else {
     if (S->dense) {
@@ -1038,24 +1039,36 @@ static float *xc_region(const ds_hip_stack_t *S, int l) { return S->xc + (size_t
 static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *nev) {
   hipError_t e = hipSuccess;
   const int dense = S->dense != NULL, NL = S->n_layers, H = S->H, C = dsh_layer_split_copies();
+  const int cfg = S->route_mode == DS_HIP_ROUTE_CFG, mode = cfg ? DSH_ROUTE_CFG : DSH_ROUTE_DECODE;
   const int zn = (int)S->xc_region;
   int np0 = S->layers[0]->np;
-  if (!dense) {
-    e = scores_enqueue(S->layers[0], S->xs, S->step, S->stride, S->route_mode, S->partials[0], &np0);
+  if (!dense || !cfg) {
+    e = scores_enqueue(S->layers[0], dense ? S->xbuf : S->xs, dense ? NULL : S->step, dense ? 0 : S->stride,
+                       S->route_mode, S->partials[0], &np0);
     if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
   }
   for (int l = 0; l < NL && e == hipSuccess; l++) {
     const ds_hip_layer_t *L = S->layers[l];
     float *out = xc_region(S, l);
     float *zp = l >= 2 ? xc_region(S, l - 2) : NULL;
-    if (l == 0)
+    if (l == 0) {
       e = dsh_launch_dec_layer(&L->d, &S->sp[l], dense ? S->xbuf : S->xs, dense ? NULL : S->step,
-                               dense ? 0 : S->stride, 1, S->partials[0], np0, out, out + (size_t)C * H, zp,
+                               dense ? 0 : S->stride, 1, S->partials[0], np0, mode, out, out + (size_t)C * H, zp,
                                zp ? zn : 0, dsr_stream);
-    else {
+    } else {
       float *in = xc_region(S, l - 1);
-      e = dsh_launch_dec_layer(&L->d, &S->sp[l], in, NULL, 0, C, in + (size_t)C * H, C, out, out + (size_t)C * H, zp,
-                               zp ? zn : 0, dsr_stream);
+      const float *pin = in + (size_t)C * H;  /* CFG: the score copies the previous layer accumulated */
+      int np = C;
+      if (!cfg) { /* DECODE: the exact scores of the summed input */
+        e = dsh_launch_dec_scores_bf16_copies(L->d.router_bf16, in, NULL, 0, C, H, L->E, dsr_threads(),
+                                              S->partials[l & 1], dsr_stream);
+        if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+        pin = S->partials[l & 1];
+        np = 1;
+      }
+      if (e == hipSuccess)
+        e = dsh_launch_dec_layer(&L->d, &S->sp[l], in, NULL, 0, C, pin, np, mode, out, out + (size_t)C * H, zp,
+                                 zp ? zn : 0, dsr_stream);
     }
     if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
   }
@@ -1081,12 +1094,12 @@ static hipError_t split_final_enqueue(ds_hip_stack_t *S) {
                                           (int)S->xc_region * (NL >= 2 ? 2 : 1), dsr_stream);
 }
 
-/* Whether the one-kernel layers apply: CFG routing, no bf16 simulation, no attention, supported
- * shapes. */
+/* Whether the one-kernel layers apply: no bf16 simulation, no attention, supported shapes (in
+ * DECODE routing each layer keeps its exact scores kernel before it). */
 static int split_eligible(const ds_hip_stack_t *S) {
-  if (!S->split_want || S->route_mode != DS_HIP_ROUTE_CFG || S->bf16sim || S->attn) return 0;
+  if (!S->split_want || S->bf16sim || S->attn) return 0;
   for (int l = 0; l < S->n_layers; l++)
-    if (!dsh_layer_split_supported(&S->layers[l]->d) || !S->layers[l]->have_f32) return 0;
+    if (!dsh_layer_split_supported(&S->layers[l]->d)) return 0;
   return 1;
 }
 
@@ -1103,7 +1116,8 @@ static int split_build(ds_hip_stack_t *S) {
   for (int l = 0; l < NL; l++) {
     const dsh_layer_t *d = &S->layers[l]->d;
     bytes += al(dsh_layer_split_tile_bytes(d));
-    if (l + 1 < NL) bytes += al(dsh_layer_split_m_floats(d) * 4) + al((size_t)(d->E + 1) * 64 * 4);
+    if (l + 1 < NL && S->route_mode == DS_HIP_ROUTE_CFG)
+      bytes += al(dsh_layer_split_m_floats(d) * 4) + al((size_t)(d->E + 1) * 64 * 4);
   }
   S->xc_region = (size_t)C * S->H + (size_t)C * 64;
   bytes += al((size_t)NL * S->xc_region * 4);
@@ -1122,7 +1136,8 @@ static int split_build(ds_hip_stack_t *S) {
     const size_t routed = (size_t)d->E * d->I * d->H;
     b += al(dsh_layer_split_tile_bytes(d));
     float *M = NULL, *z = NULL;
-    const dsh_layer_t *nx = l + 1 < NL ? &S->layers[l + 1]->d : NULL;
+    /* the next router's products: CFG routing only (DECODE scores come from the exact kernel) */
+    const dsh_layer_t *nx = l + 1 < NL && S->route_mode == DS_HIP_ROUTE_CFG ? &S->layers[l + 1]->d : NULL;
     if (nx) {
       M = (float *)b;
       b += al(dsh_layer_split_m_floats(d) * 4);

@@ -209,13 +209,14 @@ ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers,
  * MoE layer's router partials (no separate scores kernel). Call before ds_hip_stack_bind; the dense
  * handle must outlive the stack. D = NULL removes it. */
 int ds_hip_stack_set_dense(ds_hip_stack_t *S, ds_hip_dense_t *D);
-/* MoE layer kernels of the stack's steps in CFG routing (the default, one_kernel = 1): one kernel
- * per layer, the down product split over the intermediate units with the layer output added up
- * in per-XCD copies (device tables built by ds_hip_stack_bind: the down weights in unit tiles and
- * the next router's products with them, about 91 MB per layer at DeepSeek's shape); the low bits
- * of the output then depend on the order of the device's atomic adds. one_kernel = 0: two kernels
- * per layer (gate_up, then down with the combine in top-k order; deterministic). DECODE routing,
- * the bf16 simulation and attention stacks always use two. Call before ds_hip_stack_bind. */
+/* MoE layer kernels of the stack's steps (the default, one_kernel = 1): one kernel per layer, the
+ * down product split over the intermediate units with the layer output added up in per-XCD copies
+ * (device tables built by ds_hip_stack_bind: the down weights in unit tiles, ~76 MB per layer at
+ * DeepSeek's shape, and in CFG routing the next router's products with them, ~15 MB); DECODE
+ * routing keeps its exact scores kernel before each layer. The low bits of the output then depend
+ * on the order of the device's atomic adds. one_kernel = 0: two kernels per layer (gate_up, then
+ * down with the combine in top-k order; deterministic). The bf16 simulation and attention stacks
+ * always use two. Call before ds_hip_stack_bind. */
 int ds_hip_stack_set_layer_kernels(ds_hip_stack_t *S, int one_kernel);
 /* Kernels per MoE layer of the bound stack (1 or 2). */
 int ds_hip_stack_layer_kernels(const ds_hip_stack_t *S);

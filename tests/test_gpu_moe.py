@@ -214,7 +214,7 @@ def run_stack(dev, layers, lm, vocab, xs, mode, graph=True, kernels=None):
             dev.check(L.ds_hip_stack_set_layer_kernels(S, 1 if kernels == 1 else 0), "layer kernels")
         dev.check(L.ds_hip_stack_bind(S, xd.ptr, xs.shape[1], td.ptr), "bind")
         if kernels is not None:
-            assert L.ds_hip_stack_layer_kernels(S) == (1 if kernels == 1 and mode == 1 else 2)
+            assert L.ds_hip_stack_layer_kernels(S) == (1 if kernels == 1 else 2)
         hidden = []
         for _ in range(n):
             dev.check(L.ds_hip_stack_run(S, 1) if graph else L.ds_hip_stack_run_eager(S, 1), "run")
@@ -271,13 +271,15 @@ def test_small_stack_vs_oracle(dev, B, mode):
             L.ds_hip_layer_destroy(h)
 
 
+@pytest.mark.parametrize("mode", [0, 1])
 @pytest.mark.parametrize("n_layers", [1, 2, 4])
-def test_one_kernel_layers_vs_oracle(dev, B, n_layers):
-    """CFG stacks with one kernel per MoE layer (down split over intermediate units, the output added
-    up in per-XCD copies, the next router's scores accumulated from precomputed products): every
-    step's hidden state against the oracle and against the two-kernel layers; more steps than
-    layers, so the copies must be cleared between steps; graph and eager runs agree to f32
-    rounding (the atomic adds make the low bits order-dependent)."""
+def test_one_kernel_layers_vs_oracle(dev, B, n_layers, mode):
+    """Stacks with one kernel per MoE layer (down split over intermediate units, the output added up
+    in per-XCD copies; CFG: the next router's scores accumulated from precomputed products, DECODE:
+    the exact bf16 scores kernel on the summed copies before each layer): every step's hidden state
+    against the oracle and against the two-kernel layers; more steps than layers, so the copies
+    must be cleared between steps; graph and eager runs agree to f32 rounding (the atomic adds make
+    the low bits order-dependent)."""
     L = dev.load()
     lays = [B.make_moe_layer(140 + i, hidden=256, inter=128, n_experts=16) for i in range(n_layers)]
     hs = [upload_layer(dev, lay) for lay in lays]
@@ -286,13 +288,13 @@ def test_one_kernel_layers_vs_oracle(dev, B, n_layers):
     lm = dev.DeviceBuffer.from_array(lm_w)
     xs = np.stack([B.normal_f32(256, 1400 + s) for s in range(6)])
     try:
-        toks1, hid1 = run_stack(dev, hs, lm, vocab, xs, 1, kernels=1)
-        toks1e, hid1e = run_stack(dev, hs, lm, vocab, xs, 1, graph=False, kernels=1)
-        toks2, hid2 = run_stack(dev, hs, lm, vocab, xs, 1, kernels=2)
-        rt, rh = oracle_decode(B, lays, lm_w, vocab, xs, 1)
+        toks1, hid1 = run_stack(dev, hs, lm, vocab, xs, mode, kernels=1)
+        toks1e, hid1e = run_stack(dev, hs, lm, vocab, xs, mode, graph=False, kernels=1)
+        toks2, hid2 = run_stack(dev, hs, lm, vocab, xs, mode, kernels=2)
+        rt, rh = oracle_decode(B, lays, lm_w, vocab, xs, mode)
         for s in range(len(xs)):
             err, err2, erre = rel_err(hid1[s], rh[s]), rel_err(hid1[s], hid2[s]), rel_err(hid1e[s], hid1[s])
-            print(f"one-kernel layers x{n_layers} step {s}: vs oracle {err:.2e}, vs two-kernel {err2:.2e}, "
+            print(f"one-kernel layers x{n_layers} mode {mode} step {s}: vs oracle {err:.2e}, vs two-kernel {err2:.2e}, "
                   f"eager vs graph {erre:.2e}; token {toks1[s]} vs {rt[s]}")
             assert err < TOL and err2 < 1e-4 and erre < 1e-4
             assert toks1[s] == B.oracle().or_argmax_bf16(hid1[s], lm_w, 256, vocab, 1, None)
