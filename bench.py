@@ -323,6 +323,7 @@ def main():
         arr_a2 = (C.c_void_p * len(attns2))(*attns2)
         dev.check(L.ds_hip_stack_set_attention(S2, arr_a2, len(attns2), fnorm.ctypes.data, 1e-6, kv, 0), "attention")
         toks2 = dev.DeviceBuffer(n_dec * 4)
+        dev.check(L.ds_hip_stack_set_layer_kernels(S2, 1 if args.layer_kernels == 1 else 0), "layer kernels")
         dev.check(L.ds_hip_stack_bind(S2, xs.ptr, H, toks2.ptr), "bind")
         dev.check(L.ds_hip_stack_run(S2, 5), "warmup")
         dev.check(L.ds_hip_sync(), "sync")

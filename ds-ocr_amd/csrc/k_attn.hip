@@ -78,9 +78,17 @@ __device__ __forceinline__ void attn_row_load(u32x4 *wv, const uint16_t *w, int 
 
 // ---------------------------------------------------------------------------- QKV
 // 64 rows of [q; k; v] per 256-thread block (4 lanes per row). H == 32*N32.
+// x[i] (f32x4 pieces) summed over ncopies copies [ncopies][H] in copy order (1: the plain vector).
+__device__ __forceinline__ f32x4 attn_x4(const float *x, int H, int ncopies, int i) {
+  f32x4 v = ((const f32x4 *)x)[i];
+  for (int c = 1; c < ncopies; c++) v += ((const f32x4 *)(x + (size_t)c * H))[i];
+  return v;
+}
+
 template <int N32>
 __global__ void __launch_bounds__(256) k_attn_qkv(dsh_attn_t A, const float *x_in, const int *step, int stride,
-                                                  const int *pos_ptr, int pos_add, int nthreads) {
+                                                  int ncopies, float *x_plain, const int *pos_ptr, int pos_add,
+                                                  int nthreads) {
   constexpr int H = 32 * N32;
   __shared__ __attribute__((aligned(16))) float s_x[H];
   __shared__ float s_r;
@@ -94,7 +102,11 @@ __global__ void __launch_bounds__(256) k_attn_qkv(dsh_attn_t A, const float *x_i
   u32x4 wv[N32];
   if (path != DSH_ROW_SINGLE) attn_row_load<N32>(wv, w, L);
   const float *x = step ? x_in + (size_t)(*step) * stride : x_in;
-  for (int i = threadIdx.x; i < H / 4; i += 256) ((f32x4 *)s_x)[i] = ((const f32x4 *)x)[i];
+  for (int i = threadIdx.x; i < H / 4; i += 256) {
+    const f32x4 v = attn_x4(x, H, ncopies, i);
+    ((f32x4 *)s_x)[i] = v;
+    if (x_plain && blockIdx.x == 0) ((f32x4 *)x_plain)[i] = v;  // for the residual kernel
+  }
   __syncthreads();
   const float rs = attn_rms_scale(s_x, H, A.eps, &s_r);
   float xn[(H + 255) / 256];
@@ -381,8 +393,8 @@ __global__ void __launch_bounds__(64) k_attn_oproj(dsh_attn_t A, int chunk) {
 // its rows (the format of k_dec_partial_scores: one row of 64 per block, its rows added in order).
 template <int N32, int R>
 __global__ void __launch_bounds__(256) k_attn_post(dsh_attn_t A, const float *x_in, const int *step, int stride,
-                                                   float *h_out, float *n_out, const float *__restrict__ WrT, int E,
-                                                   float *__restrict__ partials) {
+                                                   int ncopies, float *h_out, float *n_out,
+                                                   const float *__restrict__ WrT, int E, float *__restrict__ partials) {
   constexpr int H = 32 * N32;
   __shared__ __attribute__((aligned(16))) float s_h[H];
   __shared__ float s_r, s_n[R];
@@ -393,7 +405,10 @@ __global__ void __launch_bounds__(256) k_attn_post(dsh_attn_t A, const float *x_
 #pragma unroll
     for (int j = 0; j < R; j++) wr[j] = WrT[(size_t)(r0 + j) * E + threadIdx.x];
   }
-  for (int i = threadIdx.x; i < H; i += 256) s_h[i] = x[i] + A.proj[i];
+  for (int i = threadIdx.x; i < H / 4; i += 256) {
+    const f32x4 xv = attn_x4(x, H, ncopies, i), pv = ((const f32x4 *)A.proj)[i];
+    ((f32x4 *)s_h)[i] = xv + pv;
+  }
   __syncthreads();
   const float r = attn_rms_scale(s_h, H, A.eps, &s_r);
   if (threadIdx.x < R) {
@@ -417,12 +432,17 @@ __global__ void __launch_bounds__(256) k_attn_post(dsh_attn_t A, const float *x_
 // ds_rms_norm of the last hidden state before the LM head (ds_moe_decoder.c:1000), AVX-512 order;
 // trunc: ds_bf16_truncate_array after it (:1016-1018, bf16 simulation of model version 3).
 template <int N32>
-__global__ void __launch_bounds__(256) k_final_norm(const float *__restrict__ x, const float *__restrict__ w,
-                                                    float eps, int trunc, float *__restrict__ out) {
+__global__ void __launch_bounds__(256) k_final_norm(const float *__restrict__ x, int ncopies,
+                                                    const float *__restrict__ w, float eps, int trunc,
+                                                    float *__restrict__ out, float *__restrict__ x_out) {
   constexpr int H = 32 * N32;
   __shared__ __attribute__((aligned(16))) float s_x[H];
   __shared__ float s_r;
-  for (int i = threadIdx.x; i < H; i += 256) s_x[i] = x[i];
+  for (int i = threadIdx.x; i < H / 4; i += 256) {
+    const f32x4 v = attn_x4(x, H, ncopies, i);
+    ((f32x4 *)s_x)[i] = v;
+    if (x_out) ((f32x4 *)x_out)[i] = v;
+  }
   __syncthreads();
   const float r = attn_rms_scale(s_x, H, eps, &s_r);
   for (int i = threadIdx.x; i < H; i += 256) {
@@ -442,15 +462,19 @@ int dsh_attn_supported(int H, int n_heads, int head_dim) {
 // scores/factors and coefficients; at least 8 floats (the per-part sums reuse the first ones)
 size_t dsh_attn_core_lds(int max_kv) { return (size_t)2 * max_kv * sizeof(float); }
 
-hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *step, int stride, const int *pos_ptr,
-                           int pos_add, int prefill_len, int window, int nthreads, float *h_out,
-                           float *n_out, const float *WrT_next, int E_next, float *partials_next, hipStream_t s) {
+hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *step, int stride, int ncopies,
+                           float *x_plain, const int *pos_ptr, int pos_add, int prefill_len, int window, int nthreads,
+                           float *h_out, float *n_out, const float *WrT_next, int E_next, float *partials_next,
+                           hipStream_t s) {
   if (!dsh_attn_supported(A->H, A->n_heads, A->head_dim)) return hipErrorInvalidValue;
+  if (ncopies < 1 || ncopies > 8 || (ncopies > 1 && (step || !x_plain))) return hipErrorInvalidValue;
+  const float *x_post = ncopies > 1 ? x_plain : x_in;  // the residual kernel reads one plain vector
   const int qd = A->n_heads * A->head_dim;
 #define QKV(N)                                                                                     \
   case N:                                                                                          \
-    k_attn_qkv<8 * N><<<(3 * qd + 63) / 64, 256, 0, s>>>(*A, x_in, step, stride, pos_ptr, pos_add,  \
-                                                          nthreads);                               \
+    k_attn_qkv<8 * N><<<(3 * qd + 63) / 64, 256, 0, s>>>(*A, x_in, step, stride, ncopies,            \
+                                                          ncopies > 1 ? x_plain : nullptr, pos_ptr, \
+                                                          pos_add, nthreads);                      \
     break;
   switch (A->H / 256) {
     QKV(1) QKV(2) QKV(3) QKV(4) QKV(5) QKV(6) QKV(7) QKV(8)
@@ -492,8 +516,8 @@ hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *st
 #undef OP
 #define PO(N, RR)                                                                                           \
   case N:                                                                                                   \
-    k_attn_post<8 * N, RR><<<A->H / RR, 256, 0, s>>>(*A, x_in, step, stride, h_out, n_out, WrT_next, E_next, \
-                                                     partials_next);                                        \
+    k_attn_post<8 * N, RR><<<A->H / RR, 256, 0, s>>>(*A, x_post, ncopies > 1 ? nullptr : step, stride, 1,     \
+                                                     h_out, n_out, WrT_next, E_next, partials_next);        \
     break;
   if (WrT_next && (E_next <= 0 || E_next > 64)) return hipErrorInvalidValue;
   if (A->H / dsh_dec_partials(A->H) == 8) {
@@ -513,13 +537,13 @@ hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *st
   return hipGetLastError();
 }
 
-hipError_t dsh_launch_final_norm(const float *x, const float *w, int H, float eps, int trunc, float *out,
-                                 hipStream_t s) {
-#define FN(N)                                                            \
-  case N:                                                                \
-    k_final_norm<8 * N><<<1, 256, 0, s>>>(x, w, eps, trunc, out);        \
+hipError_t dsh_launch_final_norm(const float *x, int ncopies, const float *w, int H, float eps, int trunc, float *out,
+                                 float *x_out, hipStream_t s) {
+#define FN(N)                                                                         \
+  case N:                                                                             \
+    k_final_norm<8 * N><<<1, 256, 0, s>>>(x, ncopies, w, eps, trunc, out, x_out);     \
     break;
-  if (H % 256) return hipErrorInvalidValue;
+  if (H % 256 || ncopies < 1 || ncopies > 8) return hipErrorInvalidValue;
   switch (H / 256) {
     FN(1) FN(2) FN(3) FN(4) FN(5) FN(6) FN(7) FN(8)
     default:

@@ -115,15 +115,19 @@ typedef struct {
 int dsh_attn_supported(int H, int n_heads, int head_dim);
 size_t dsh_attn_core_lds(int max_kv);
 /* h_out = x + Wo·attention(...), n_out = RMSNorm(h_out) for the token at cache position
- * (pos_ptr ? *pos_ptr : 0) + pos_add; x = x_in + (*step)*stride when step != NULL. */
+ * (pos_ptr ? *pos_ptr : 0) + pos_add; x = x_in + (*step)*stride when step != NULL; ncopies > 1:
+ * x = Σ of the copies [ncopies][H] at x_in in copy order (step NULL), also written to x_plain ([H]) for the
+ * residual kernel. */
 /* With WrT_next ([H][E_next] f32), the last kernel also writes the following MoE layer's router
  * partials from n (dsh_dec_partials(H) rows of 64). */
-hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *step, int stride, const int *pos_ptr,
-                           int pos_add, int prefill_len, int window, int nthreads, float *h_out,
-                           float *n_out, const float *WrT_next, int E_next, float *partials_next, hipStream_t s);
-/* out = ds_rms_norm(x) (AVX-512 order), then bf16 truncation when trunc. */
-hipError_t dsh_launch_final_norm(const float *x, const float *w, int H, float eps, int trunc, float *out,
-                                 hipStream_t s);
+hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *step, int stride, int ncopies,
+                           float *x_plain, const int *pos_ptr, int pos_add, int prefill_len, int window, int nthreads,
+                           float *h_out, float *n_out, const float *WrT_next, int E_next, float *partials_next,
+                           hipStream_t s);
+/* out = ds_rms_norm(x) (AVX-512 order), then bf16 truncation when trunc; x = Σ of ncopies copies
+ * [ncopies][H] (1: plain), also written to x_out when given. */
+hipError_t dsh_launch_final_norm(const float *x, int ncopies, const float *w, int H, float eps, int trunc, float *out,
+                                 float *x_out, hipStream_t s);
 /* ---- greedy token choice with repetition penalty and n-gram ban (k_sample.hip) ---- */
 int dsh_sample_supported(int H);
 /* After the argmax. Stack form (step != NULL): history tokens[0..min(*step - 1, hist_len)), token
@@ -184,14 +188,15 @@ size_t dsh_layer_split_m_floats(const dsh_layer_t *L);   /* routed + shared M ti
 /* Fills the tiles (and, with WrT_next, M and z) of layer L from its arena. */
 hipError_t dsh_launch_layer_build(const dsh_layer_t *L, const float *WrT_next, int E_next, int8_t *dnT, int8_t *sdnT,
                                   float *M, float *sM, float *z, float *sz, hipStream_t s);
-/* x_out ([copies][H]) += x + MoE(x); lg_out ([copies][64]) += the next layer's router scores (when F->M).
+/* x_out ([copies][H]) += (resid ? resid : x) + MoE(x); lg_out ([copies][64]) += the next layer's router scores (when F->M).
  * Input: ncopies == 1: x = x_in + (*step)*stride (step may be NULL), router partials [np <= 160][64];
  * ncopies == copies: x = Σ copies of x_in, router partials [np <= 8][64] (CFG: the score copies).
  * route_mode: DSH_ROUTE_CFG or DSH_ROUTE_DECODE (then np == 1: the exact scores; empty slots add
  * nothing). Clears zero_p[0..zero_n). */
 hipError_t dsh_launch_dec_layer(const dsh_layer_t *L, const dsh_split_t *F, const float *x_in, const int *step,
-                                int stride, int ncopies, const float *partials, int np, int route_mode, float *x_out,
-                                float *lg_out, float *zero_p, int zero_n, hipStream_t s);
+                                int stride, int ncopies, const float *partials, int np, int route_mode,
+                                const float *resid, float *x_out, float *lg_out, float *zero_p, int zero_n,
+                                hipStream_t s);
 /* out = Σ copies of X ([copies][H]); clears X and zero_p[0..zero_n). */
 hipError_t dsh_launch_dec_copy_sum(float *X, int H, float *out, float *zero_p, int zero_n, hipStream_t s);
 

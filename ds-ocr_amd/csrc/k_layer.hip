@@ -74,8 +74,9 @@ __device__ __forceinline__ void dl_issue(dl_regs<CPL> &R, const int8_t *gu, cons
 template <int CPL, int NREP, int RB>
 __global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F, const float *x_in,
                                                    const int *__restrict__ step, int stride,
-                                                   const float *partials, int np, int mode, float *x_out,
-                                                   float *lg_out, float *zero_p, int zero_n) {
+                                                   const float *partials, int np, int mode,
+                                                   const float *__restrict__ resid, float *x_out, float *lg_out,
+                                                   float *zero_p, int zero_n) {
   constexpr int H = 256 * CPL, NP = 64 * CPL, XV = (NP + 511) / 512, NL = 4;
   __shared__ int s_idx[8 * 64];
   __shared__ float s_w[8 * 64];
@@ -106,6 +107,11 @@ __global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F,
   if (!shared_blk && wave < 4) {
 #pragma unroll
     for (int j = 0; j < RB; j++) pv[j] = partials[(size_t)min(wave + 4 * j, np - 1) * 64 + lane];
+  }
+  float rv[CPL];  // block 0: the residual rows it adds (when it is not the input)
+  if (blk == 0 && resid && !half) {
+#pragma unroll
+    for (int k = 0; k < CPL; k++) rv[k] = resid[th + 256 * k];
   }
   const bool base_blk = F.WrT_next && blk < H / 8;  // adds Wr'·x over rows 8*blk .. 8*blk + 7
   float wr[8];
@@ -266,7 +272,7 @@ __global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F,
       const int r = th + 256 * k;
       const float d = dk[k] + s_dn[r];
       float c = wexp * __builtin_fmaf(R.dso[k].x, d, R.dso[k].y * hs);
-      if (blk == 0) c += s_x[r];  // the residual, added once
+      if (blk == 0) c += resid ? rv[k] : s_x[r];  // the residual, added once
       __hip_atomic_fetch_add(xo + r, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
@@ -389,8 +395,9 @@ hipError_t dsh_launch_layer_build(const dsh_layer_t *L, const float *WrT_next, i
 }
 
 hipError_t dsh_launch_dec_layer(const dsh_layer_t *L, const dsh_split_t *F, const float *x_in, const int *step,
-                                int stride, int ncopies, const float *partials, int np, int route_mode, float *x_out,
-                                float *lg_out, float *zero_p, int zero_n, hipStream_t s) {
+                                int stride, int ncopies, const float *partials, int np, int route_mode,
+                                const float *resid, float *x_out, float *lg_out, float *zero_p, int zero_n,
+                                hipStream_t s) {
   const int nb = dsh_layer_split_blocks(L);
   if (ncopies != 1 && ncopies != DL_REP) return hipErrorInvalidValue;
   if (np < 1 || (ncopies == 1 ? np > 160 : np > 8)) return hipErrorInvalidValue;
@@ -398,11 +405,11 @@ hipError_t dsh_launch_dec_layer(const dsh_layer_t *L, const dsh_split_t *F, cons
 #define DLK(N)                                                                                                   \
   case N:                                                                                                        \
     if (ncopies == 1)                                                                                            \
-      k_dec_layer<N, 1, 40><<<nb, 512, 0, s>>>(*L, *F, x_in, step, stride, partials, np, route_mode, x_out,    \
-                                               lg_out, zero_p, zero_n);                                                          \
+      k_dec_layer<N, 1, 40><<<nb, 512, 0, s>>>(*L, *F, x_in, step, stride, partials, np, route_mode, resid,    \
+                                               x_out, lg_out, zero_p, zero_n);                                                          \
     else                                                                                                         \
-      k_dec_layer<N, DL_REP, 2><<<nb, 512, 0, s>>>(*L, *F, x_in, step, stride, partials, np, route_mode, x_out, \
-                                                   lg_out, zero_p, zero_n);                                              \
+      k_dec_layer<N, DL_REP, 2><<<nb, 512, 0, s>>>(*L, *F, x_in, step, stride, partials, np, route_mode, resid, \
+                                                   x_out, lg_out, zero_p, zero_n);                                              \
     break;
   switch (L->H / 256) {
     DLK(1) DLK(2) DLK(3) DLK(4) DLK(5) DLK(6) DLK(7) DLK(8)

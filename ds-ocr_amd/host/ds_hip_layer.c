@@ -939,8 +939,12 @@ static int stack_names(const ds_hip_stack_t *S, const char **names) {
     for (int l = 0; l < S->n_layers; l++) {
       NM("attention");
       if (!cfg) NM("scores");
-      NM("gate_up");
-      NM("down");
+      if (S->split) {
+        NM("layer");
+      } else {
+        NM("gate_up");
+        NM("down");
+      }
     }
     NM("final_norm");
   } else if (S->split) {
@@ -980,15 +984,18 @@ static int stack_kernel_count(const ds_hip_stack_t *S) { return stack_names(S, N
 /* A full decoder step's layers (ds_moe_decoder.c:339-474 per layer): the attention half, then the
  * MLP on n with h as its residual. In CFG routing the attention's last kernel writes the MoE
  * layer's router partials from n; in DECODE routing the scores kernel reads n. */
+static float *xc_region(const ds_hip_stack_t *S, int l);
+
 static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *nev) {
   hipError_t e = hipSuccess;
-  const int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
+  const int cfg = S->route_mode == DS_HIP_ROUTE_CFG, C = dsh_layer_split_copies();
   const dsh_layer_work_t *wk = &S->layers[0]->wk;
   const float *xin = S->xs;
   const int *st = S->step;
-  int stride = S->stride, a = 0;
+  int stride = S->stride, a = 0, nc = 1; /* nc: copies of xin (one-kernel layers: the per-XCD copies) */
   if (S->dense) {
-    e = ds_hip_attn_enqueue(S->attn[a++], xin, st, stride, S->step, S->pos0, S->hbuf, S->nbuf, NULL, 0, NULL);
+    e = ds_hip_attn_enqueue(S->attn[a++], xin, st, stride, 1, NULL, S->step, S->pos0, S->hbuf, S->nbuf, NULL, 0,
+                            NULL);
     if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
     if (e == hipSuccess)
       e = dsh_launch_dense_gate_up(S->dense->wg, S->dense->wu, S->nbuf, NULL, 0, S->dense->H, S->dense->I,
@@ -1006,26 +1013,42 @@ static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *ne
     const ds_hip_layer_t *L = S->layers[l];
     float *pin = S->partials[l & 1];
     int np = L->np;
-    e = ds_hip_attn_enqueue(S->attn[a++], xin, st, stride, S->step, S->pos0, S->hbuf, S->nbuf,
+    /* with the copies, the attention's first kernel also writes their sum to xbuf for its residual */
+    e = ds_hip_attn_enqueue(S->attn[a++], xin, st, stride, nc, nc > 1 ? S->xbuf : NULL, S->step, S->pos0, S->hbuf,
+                            S->nbuf,
                             cfg ? L->d.router_f32_t : NULL, cfg ? L->E : 0, cfg ? pin : NULL);
     if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
     if (e == hipSuccess && !cfg) {
       e = scores_enqueue(L, S->nbuf, NULL, 0, S->route_mode, pin, &np);
       if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
     }
-    if (e == hipSuccess)
-      e = dsh_launch_dec_gate_up(&L->d, S->nbuf, NULL, 0, pin, np, S->route_mode, S->bf16sim, wk, dsr_stream);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
-    if (e == hipSuccess)
-      e = dsh_launch_dec_down(&L->d, S->nbuf, NULL, 0, S->xbuf, 1, S->hbuf, S->bf16sim, wk, NULL, 0, NULL, dsr_stream);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
-    xin = S->xbuf;
+    if (S->split) { /* one kernel: MoE(n) + h into the copies region l, clearing region l - 2 */
+      float *out = xc_region(S, l), *zp = l >= 2 ? xc_region(S, l - 2) : NULL;
+      if (e == hipSuccess)
+        e = dsh_launch_dec_layer(&L->d, &S->sp[l], S->nbuf, NULL, 0, 1, pin, np,
+                                 cfg ? DSH_ROUTE_CFG : DSH_ROUTE_DECODE, S->hbuf, out, out + (size_t)C * S->H, zp,
+                                 zp ? (int)S->xc_region : 0, dsr_stream);
+      if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+      xin = out;
+      nc = C;
+    } else {
+      if (e == hipSuccess)
+        e = dsh_launch_dec_gate_up(&L->d, S->nbuf, NULL, 0, pin, np, S->route_mode, S->bf16sim, wk, dsr_stream);
+      if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+      if (e == hipSuccess)
+        e = dsh_launch_dec_down(&L->d, S->nbuf, NULL, 0, S->xbuf, 1, S->hbuf, S->bf16sim, wk, NULL, 0, NULL,
+                                dsr_stream);
+      if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+      xin = S->xbuf;
+      nc = 1;
+    }
     st = NULL;
     stride = 0;
   }
+  /* the final norm; with the copies it also writes their sum (the hidden state) to xbuf */
   if (e == hipSuccess)
-    e = dsh_launch_final_norm(S->xbuf, S->final_norm, S->H, S->final_eps, S->trunc_final && S->bf16sim, S->fbuf,
-                              dsr_stream);
+    e = dsh_launch_final_norm(xin, nc, S->final_norm, S->H, S->final_eps, S->trunc_final && S->bf16sim, S->fbuf,
+                              nc > 1 ? S->xbuf : NULL, dsr_stream);
   if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
   return e;
 }
@@ -1053,7 +1076,7 @@ static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *n
     float *zp = l >= 2 ? xc_region(S, l - 2) : NULL;
     if (l == 0) {
       e = dsh_launch_dec_layer(&L->d, &S->sp[l], dense ? S->xbuf : S->xs, dense ? NULL : S->step,
-                               dense ? 0 : S->stride, 1, S->partials[0], np0, mode, out, out + (size_t)C * H, zp,
+                               dense ? 0 : S->stride, 1, S->partials[0], np0, mode, NULL, out, out + (size_t)C * H, zp,
                                zp ? zn : 0, dsr_stream);
     } else {
       float *in = xc_region(S, l - 1);
@@ -1067,7 +1090,7 @@ static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *n
         np = 1;
       }
       if (e == hipSuccess)
-        e = dsh_launch_dec_layer(&L->d, &S->sp[l], in, NULL, 0, C, pin, np, mode, out, out + (size_t)C * H, zp,
+        e = dsh_launch_dec_layer(&L->d, &S->sp[l], in, NULL, 0, C, pin, np, mode, NULL, out, out + (size_t)C * H, zp,
                                  zp ? zn : 0, dsr_stream);
     }
     if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
@@ -1097,7 +1120,7 @@ static hipError_t split_final_enqueue(ds_hip_stack_t *S) {
 /* Whether the one-kernel layers apply: no bf16 simulation, no attention, supported shapes (in
  * DECODE routing each layer keeps its exact scores kernel before it). */
 static int split_eligible(const ds_hip_stack_t *S) {
-  if (!S->split_want || S->bf16sim || S->attn) return 0;
+  if (!S->split_want || S->bf16sim) return 0;
   for (int l = 0; l < S->n_layers; l++)
     if (!dsh_layer_split_supported(&S->layers[l]->d)) return 0;
   return 1;
@@ -1116,7 +1139,7 @@ static int split_build(ds_hip_stack_t *S) {
   for (int l = 0; l < NL; l++) {
     const dsh_layer_t *d = &S->layers[l]->d;
     bytes += al(dsh_layer_split_tile_bytes(d));
-    if (l + 1 < NL && S->route_mode == DS_HIP_ROUTE_CFG)
+    if (l + 1 < NL && S->route_mode == DS_HIP_ROUTE_CFG && !S->attn)
       bytes += al(dsh_layer_split_m_floats(d) * 4) + al((size_t)(d->E + 1) * 64 * 4);
   }
   S->xc_region = (size_t)C * S->H + (size_t)C * 64;
@@ -1137,7 +1160,7 @@ static int split_build(ds_hip_stack_t *S) {
     b += al(dsh_layer_split_tile_bytes(d));
     float *M = NULL, *z = NULL;
     /* the next router's products: CFG routing only (DECODE scores come from the exact kernel) */
-    const dsh_layer_t *nx = l + 1 < NL && S->route_mode == DS_HIP_ROUTE_CFG ? &S->layers[l + 1]->d : NULL;
+    const dsh_layer_t *nx = l + 1 < NL && S->route_mode == DS_HIP_ROUTE_CFG && !S->attn ? &S->layers[l + 1]->d : NULL;
     if (nx) {
       M = (float *)b;
       b += al(dsh_layer_split_m_floats(d) * 4);
@@ -1216,7 +1239,8 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
     }
   }
   if (e != hipSuccess) return e;
-  const int lm_copies = S->split && S->lm_fast;
+  const int lm_copies = S->split && S->lm_fast && !S->attn;
+  const int clear_in_final = S->split && (S->lm_fast || S->attn); /* else copy_sum cleared them */
   if (lm_copies) {
     e = split_lm_enqueue(S);
   } else if (S->lm_fast) {
@@ -1228,7 +1252,8 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
   }
   if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
   if (e == hipSuccess)
-    e = lm_copies ? split_final_enqueue(S) : dsh_launch_lm_argmax_final(S->cand, S->ncand, S->tokens, S->step, dsr_stream);
+    e = clear_in_final ? split_final_enqueue(S)
+                       : dsh_launch_lm_argmax_final(S->cand, S->ncand, S->tokens, S->step, dsr_stream);
   if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
   if (e == hipSuccess && smp_active(S)) {
     /* the repetition penalty and the n-gram ban over this stack's earlier tokens; one event after
@@ -1325,7 +1350,7 @@ int ds_hip_time_lm_head(ds_hip_stack_t *S, int n, float *ms) {
   int rc = 0;
   hipError_t e = hipEventRecord(a, dsr_stream);
   for (int i = 0; i < n && e == hipSuccess; i++) {
-    if (S->split && S->lm_fast) {  /* the step's head kernel without its final block's work */
+    if (S->split && S->lm_fast && !S->attn) {  /* the head kernel of the step (on the layer copies) */
       e = dsh_launch_dec_lm_argmax_copies(S->lm, xc_region(S, S->n_layers - 1), dsh_layer_split_copies(), S->H,
                                           S->vocab, S->cand, NULL, dsr_stream);
     } else if (S->lm_fast) {

@@ -54,8 +54,8 @@ int dsr_threads(void);
  * (pos_ptr ? *pos_ptr : 0) + pos_add, input x_in (+ (*step)*stride when step != NULL). */
 struct ds_hip_attn;
 hipError_t ds_hip_attn_enqueue(const struct ds_hip_attn *A, const float *x_in, const int *step, int stride,
-                               const int *pos_ptr, int pos_add, float *h_out, float *n_out, const float *WrT_next,
-                               int E_next, float *partials_next);
+                               int ncopies, float *x_plain, const int *pos_ptr, int pos_add, float *h_out, float *n_out,
+                               const float *WrT_next, int E_next, float *partials_next);
 int ds_hip_attn_hidden(const struct ds_hip_attn *A);
 size_t ds_hip_attn_weight_bytes(const struct ds_hip_attn *A); /* projections and norms read per token */
 
