@@ -78,11 +78,34 @@ __device__ __forceinline__ void attn_row_load(u32x4 *wv, const uint16_t *w, int 
 
 // ---------------------------------------------------------------------------- QKV
 // 64 rows of [q; k; v] per 256-thread block (4 lanes per row). H == 32*N32.
-// x[i] (f32x4 pieces) summed over ncopies copies [ncopies][H] in copy order (1: the plain vector).
-__device__ __forceinline__ f32x4 attn_x4(const float *x, int H, int ncopies, int i) {
-  f32x4 v = ((const f32x4 *)x)[i];
-  for (int c = 1; c < ncopies; c++) v += ((const f32x4 *)(x + (size_t)c * H))[i];
-  return v;
+// Pieces i0 and i1 (f32x4; i1 < 0: none) of x into LDS dst, x summed over ncopies (1 or 8) copies
+// [ncopies][H] in copy order; every load is issued before the first add. Also to x_out when given.
+__device__ __forceinline__ void attn_x_pieces(const float *x, int H, int ncopies, int i0, int i1, float *dst,
+                                              float *x_out) {
+  const f32x4 *x4 = (const f32x4 *)x;
+  const int H4 = H / 4, j0 = i0 < 0 ? 0 : i0, j1 = i1 < 0 ? j0 : i1;
+  f32x4 a = x4[j0], b = x4[j1];
+  if (ncopies == 8) {
+    f32x4 ca[7], cb[7];
+#pragma unroll
+    for (int c = 0; c < 7; c++) {
+      ca[c] = x4[(size_t)(c + 1) * H4 + j0];
+      cb[c] = x4[(size_t)(c + 1) * H4 + j1];
+    }
+#pragma unroll
+    for (int c = 0; c < 7; c++) {
+      a += ca[c];
+      b += cb[c];
+    }
+  }
+  if (i0 >= 0) {
+    ((f32x4 *)dst)[i0] = a;
+    if (x_out) ((f32x4 *)x_out)[i0] = a;
+  }
+  if (i1 >= 0) {
+    ((f32x4 *)dst)[i1] = b;
+    if (x_out) ((f32x4 *)x_out)[i1] = b;
+  }
 }
 
 template <int N32>
@@ -102,11 +125,9 @@ __global__ void __launch_bounds__(256) k_attn_qkv(dsh_attn_t A, const float *x_i
   u32x4 wv[N32];
   if (path != DSH_ROW_SINGLE) attn_row_load<N32>(wv, w, L);
   const float *x = step ? x_in + (size_t)(*step) * stride : x_in;
-  for (int i = threadIdx.x; i < H / 4; i += 256) {
-    const f32x4 v = attn_x4(x, H, ncopies, i);
-    ((f32x4 *)s_x)[i] = v;
-    if (x_plain && blockIdx.x == 0) ((f32x4 *)x_plain)[i] = v;  // for the residual kernel
-  }
+  // H/4 <= 512 pieces: at most two per thread (block 0 also writes x for the residual kernel)
+  attn_x_pieces(x, H, ncopies, (int)threadIdx.x < H / 4 ? (int)threadIdx.x : -1,
+                (int)threadIdx.x + 256 < H / 4 ? (int)threadIdx.x + 256 : -1, s_x, blockIdx.x == 0 ? x_plain : nullptr);
   __syncthreads();
   const float rs = attn_rms_scale(s_x, H, A.eps, &s_r);
   float xn[(H + 255) / 256];
@@ -393,7 +414,7 @@ __global__ void __launch_bounds__(64) k_attn_oproj(dsh_attn_t A, int chunk) {
 // its rows (the format of k_dec_partial_scores: one row of 64 per block, its rows added in order).
 template <int N32, int R>
 __global__ void __launch_bounds__(256) k_attn_post(dsh_attn_t A, const float *x_in, const int *step, int stride,
-                                                   int ncopies, float *h_out, float *n_out,
+                                                   float *h_out, float *n_out,
                                                    const float *__restrict__ WrT, int E, float *__restrict__ partials) {
   constexpr int H = 32 * N32;
   __shared__ __attribute__((aligned(16))) float s_h[H];
@@ -406,7 +427,7 @@ __global__ void __launch_bounds__(256) k_attn_post(dsh_attn_t A, const float *x_
     for (int j = 0; j < R; j++) wr[j] = WrT[(size_t)(r0 + j) * E + threadIdx.x];
   }
   for (int i = threadIdx.x; i < H / 4; i += 256) {
-    const f32x4 xv = attn_x4(x, H, ncopies, i), pv = ((const f32x4 *)A.proj)[i];
+    const f32x4 xv = ((const f32x4 *)x)[i], pv = ((const f32x4 *)A.proj)[i];
     ((f32x4 *)s_h)[i] = xv + pv;
   }
   __syncthreads();
@@ -438,11 +459,8 @@ __global__ void __launch_bounds__(256) k_final_norm(const float *__restrict__ x,
   constexpr int H = 32 * N32;
   __shared__ __attribute__((aligned(16))) float s_x[H];
   __shared__ float s_r;
-  for (int i = threadIdx.x; i < H / 4; i += 256) {
-    const f32x4 v = attn_x4(x, H, ncopies, i);
-    ((f32x4 *)s_x)[i] = v;
-    if (x_out) ((f32x4 *)x_out)[i] = v;
-  }
+  attn_x_pieces(x, H, ncopies, (int)threadIdx.x < H / 4 ? (int)threadIdx.x : -1,
+                (int)threadIdx.x + 256 < H / 4 ? (int)threadIdx.x + 256 : -1, s_x, x_out);
   __syncthreads();
   const float r = attn_rms_scale(s_x, H, eps, &s_r);
   for (int i = threadIdx.x; i < H; i += 256) {
@@ -467,7 +485,7 @@ hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *st
                            float *h_out, float *n_out, const float *WrT_next, int E_next, float *partials_next,
                            hipStream_t s) {
   if (!dsh_attn_supported(A->H, A->n_heads, A->head_dim)) return hipErrorInvalidValue;
-  if (ncopies < 1 || ncopies > 8 || (ncopies > 1 && (step || !x_plain))) return hipErrorInvalidValue;
+  if ((ncopies != 1 && ncopies != 8) || (ncopies > 1 && (step || !x_plain))) return hipErrorInvalidValue;
   const float *x_post = ncopies > 1 ? x_plain : x_in;  // the residual kernel reads one plain vector
   const int qd = A->n_heads * A->head_dim;
 #define QKV(N)                                                                                     \
@@ -516,7 +534,7 @@ hipError_t dsh_launch_attn(const dsh_attn_t *A, const float *x_in, const int *st
 #undef OP
 #define PO(N, RR)                                                                                           \
   case N:                                                                                                   \
-    k_attn_post<8 * N, RR><<<A->H / RR, 256, 0, s>>>(*A, x_post, ncopies > 1 ? nullptr : step, stride, 1,     \
+    k_attn_post<8 * N, RR><<<A->H / RR, 256, 0, s>>>(*A, x_post, ncopies > 1 ? nullptr : step, stride,        \
                                                      h_out, n_out, WrT_next, E_next, partials_next);        \
     break;
   if (WrT_next && (E_next <= 0 || E_next > 64)) return hipErrorInvalidValue;
@@ -543,7 +561,7 @@ hipError_t dsh_launch_final_norm(const float *x, int ncopies, const float *w, in
   case N:                                                                             \
     k_final_norm<8 * N><<<1, 256, 0, s>>>(x, ncopies, w, eps, trunc, out, x_out);     \
     break;
-  if (H % 256 || ncopies < 1 || ncopies > 8) return hipErrorInvalidValue;
+  if (H % 256 || (ncopies != 1 && ncopies != 8)) return hipErrorInvalidValue;
   switch (H / 256) {
     FN(1) FN(2) FN(3) FN(4) FN(5) FN(6) FN(7) FN(8)
     default:
