@@ -311,7 +311,7 @@ __global__ void __launch_bounds__(256) k_dec_copy_sum(float *X, int H, float *ou
 // (bytes): piece q = 2k + j/16 of thread t's rows sits at (q*256 + t)*16.
 __global__ void __launch_bounds__(256) k_layer_build_tiles(const int8_t *__restrict__ dn, int H, int I, int n_mat,
                                                            int8_t *__restrict__ tiles) {
-  const int CPL = H / 256, NSL = I / DL_UB;
+  const int CPL = H / 256;
   const size_t per_mat = (size_t)H * I / 16;  // 16-byte pieces
   const size_t n = per_mat * n_mat;
   for (size_t g = (size_t)blockIdx.x * 256 + threadIdx.x; g < n; g += (size_t)gridDim.x * 256) {
@@ -323,7 +323,6 @@ __global__ void __launch_bounds__(256) k_layer_build_tiles(const int8_t *__restr
     const int s = (int)(rest / (2 * CPL));
     const int k = q >> 1, half = q & 1;
     const int r = t + 256 * k, i = DL_UB * s + 16 * half;
-    (void)NSL;
     const u32x4 v = *(const u32x4 *)(dn + (mat * H + r) * (size_t)I + i);
     *(u32x4 *)(tiles + g * 16) = v;
   }

@@ -216,7 +216,8 @@ int ds_hip_stack_set_dense(ds_hip_stack_t *S, ds_hip_dense_t *D);
  * routing keeps its exact scores kernel before each layer. The low bits of the output then depend
  * on the order of the device's atomic adds. one_kernel = 0: two kernels per layer (gate_up, then
  * down with the combine in top-k order; deterministic). The bf16 simulation always uses two.
- * Call before ds_hip_stack_bind. */
+ * Call before ds_hip_stack_bind; the tables copy the layers' weights at bind time, so bind again
+ * after changing a layer's experts or router. */
 int ds_hip_stack_set_layer_kernels(ds_hip_stack_t *S, int one_kernel);
 /* Kernels per MoE layer of the bound stack (1 or 2). */
 int ds_hip_stack_layer_kernels(const ds_hip_stack_t *S);
