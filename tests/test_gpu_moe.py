@@ -199,9 +199,10 @@ def test_config2_layer_vs_oracle(dev, B):
         L.ds_hip_layer_destroy(h)
 
 
-def run_stack(dev, layers, lm, vocab, xs, mode, graph=True, kernels=None):
+def run_stack(dev, layers, lm, vocab, xs, mode, graph=True, kernels=None, expect=None):
     """Runs xs through a stack step by step; kernels = 1 or 2 picks the MoE layer kernels (default:
-    the library's choice)."""
+    the library's choice); expect: the kernels per layer the bound stack must report (default: the
+    ones picked)."""
     L = dev.load()
     arr = (C.c_void_p * len(layers))(*layers)
     S = L.ds_hip_stack_create(arr, len(layers), lm.ptr, vocab, mode)
@@ -214,7 +215,7 @@ def run_stack(dev, layers, lm, vocab, xs, mode, graph=True, kernels=None):
             dev.check(L.ds_hip_stack_set_layer_kernels(S, 1 if kernels == 1 else 0), "layer kernels")
         dev.check(L.ds_hip_stack_bind(S, xd.ptr, xs.shape[1], td.ptr), "bind")
         if kernels is not None:
-            assert L.ds_hip_stack_layer_kernels(S) == (1 if kernels == 1 else 2)
+            assert L.ds_hip_stack_layer_kernels(S) == (expect or (1 if kernels == 1 else 2))
         hidden = []
         for _ in range(n):
             dev.check(L.ds_hip_stack_run(S, 1) if graph else L.ds_hip_stack_run_eager(S, 1), "run")
@@ -299,6 +300,34 @@ def test_one_kernel_layers_vs_oracle(dev, B, n_layers, mode):
             assert err < TOL and err2 < 1e-4 and erre < 1e-4
             assert toks1[s] == B.oracle().or_argmax_bf16(hid1[s], lm_w, 256, vocab, 1, None)
             assert toks1e[s] == B.oracle().or_argmax_bf16(hid1e[s], lm_w, 256, vocab, 1, None)
+    finally:
+        for h in hs:
+            L.ds_hip_layer_destroy(h)
+
+
+@pytest.mark.parametrize("shape", [(512, 256, 32, 4, 4), (768, 384, 8, 6, 2), (2048, 64, 16, 6, 2)])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_one_kernel_layer_shapes(dev, B, shape, mode):
+    """Other hidden sizes (other kernel instantiations), expert counts and top-k for the one-kernel
+    layers, against the oracle; a shape whose blocks cannot cover the next router's rows (H/8 rows
+    of 8 per block) falls back to the two-kernel layers."""
+    H, I, E, K, NS = shape
+    L = dev.load()
+    lays = [B.make_moe_layer(160 + i, hidden=H, inter=I, n_experts=E, top_k=K, n_shared=NS) for i in range(2)]
+    hs = [upload_layer(dev, lay) for lay in lays]
+    vocab = 1000
+    lm_w = B.normal_bf16(vocab * H, 161, 0.02)
+    lm = dev.DeviceBuffer.from_array(lm_w)
+    xs = np.stack([B.normal_f32(H, 1600 + s) for s in range(3)])
+    one = (NS * I + K * I) // 32 >= H // 8
+    try:
+        toks, hid = run_stack(dev, hs, lm, vocab, xs, mode, kernels=1, expect=1 if one else 2)
+        rt, rh = oracle_decode(B, lays, lm_w, vocab, xs, mode)
+        for s in range(len(xs)):
+            err = rel_err(hid[s], rh[s])
+            print(f"shape {shape} mode {mode} ({'one' if one else 'two'} kernels) step {s}: err {err:.2e}")
+            assert err < TOL
+            assert toks[s] == B.oracle().or_argmax_bf16(hid[s], lm_w, H, vocab, 1, None)
     finally:
         for h in hs:
             L.ds_hip_layer_destroy(h)
