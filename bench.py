@@ -282,6 +282,20 @@ def main():
     dev.check(L.ds_hip_time_stream_read(lm.ptr, lm_bytes, 50, C.byref(rd_t)), "stream read timing")
     read_gbs = lm_bytes / (rd_t.value * 1e-3) / 1e9
     step_gbs = bytes_per_step / (ms_per_step * 1e-3) / 1e9
+    # one MoE layer kernel alone (layer 5 of 11, 50 launches back to back; one-kernel layers only):
+    # its algorithmic bytes are the step's minus the head's, per layer
+    layer_roof = None
+    if layer_kernels == 1 and not full:
+        lt = C.c_float(0)
+        dev.check(L.ds_hip_time_stack_layer(S, min(5, LAYERS - 1), 50, C.byref(lt)), "layer timing")
+        layer_bytes = (bytes_per_step - lm_bytes - (3 * H * DENSE_I * 2 if dense else 0)) // LAYERS
+        layer_gbs = layer_bytes / (lt.value * 1e-3) / 1e9
+        layer_roof = {"kernel": "k_dec_layer (one MoE layer; 11 launches per step)", "bound": "hbm",
+                      "achieved": round(layer_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                      "frac": round(layer_gbs / PEAK_HBM_GBS, 4), "bytes_per_launch": layer_bytes,
+                      "avg_ms": round(lt.value, 5),
+                      "avg_ms_note": "layer 5, 50 back-to-back launches between HIP events on the library "
+                                     "stream; latency-bound (routing, then 22 MB of routed rows, per launch)"}
 
     # prefill (config 3): 662 seeded tokens through one config-2 layer (the first decode layer)
     prefill = None
@@ -391,6 +405,7 @@ def main():
                      "stream_read_gbs": round(read_gbs, 1), "frac_of_stream_read": round(lm_gbs / read_gbs, 4),
                      "stream_read_note": "a plain nontemporal streaming read of the same bytes, timed the same "
                                          "way: the achievable HBM read rate on this box"},
+        "roofline_moe_layer": layer_roof,
         "kernels": kernel_ms,
         "prefill": prefill,
         "decoder_step": decoder,

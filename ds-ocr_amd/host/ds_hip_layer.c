@@ -1340,6 +1340,38 @@ int ds_hip_time_stack(ds_hip_stack_t *S, int n_steps, float *ms) {
   return rc;
 }
 
+/* One-kernel MoE layer `layer` of a bound stack alone, n launches back to back between two events,
+ * on the inputs the last step left (the same bytes as in a step); the output regions are cleared
+ * afterwards, so the next step starts as after a reset of the copies. */
+int ds_hip_time_stack_layer(ds_hip_stack_t *S, int layer, int n, float *ms) {
+  if (!S || !S->bound || !S->split || S->attn || layer < 0 || layer >= S->n_layers || n <= 0 || !ms)
+    return dsr_failf("ds_hip_time_stack_layer: needs a bound stack with one-kernel layers and no attention");
+  const ds_hip_layer_t *L = S->layers[layer];
+  const int C = dsh_layer_split_copies(), H = S->H, cfg = S->route_mode == DS_HIP_ROUTE_CFG;
+  const int mode = cfg ? DSH_ROUTE_CFG : DSH_ROUTE_DECODE, dense = S->dense != NULL;
+  float *out = xc_region(S, layer);
+  const float *in = layer ? xc_region(S, layer - 1) : (dense ? S->xbuf : S->xs);
+  const float *pin = layer && cfg ? in + (size_t)C * H : S->partials[layer & 1];
+  const int np = layer ? (cfg ? C : 1) : (cfg ? L->np : 1);
+  hipEvent_t a, b;
+  DSR_TRY(hipEventCreate(&a), "event");
+  DSR_TRY(hipEventCreate(&b), "event");
+  hipError_t e = hipEventRecord(a, dsr_stream);
+  for (int i = 0; i < n && e == hipSuccess; i++)
+    e = dsh_launch_dec_layer(&L->d, &S->sp[layer], in, layer || dense ? NULL : S->step, layer || dense ? 0 : S->stride,
+                             layer ? C : 1, pin, np, mode, NULL, out, out + (size_t)C * H, NULL, 0, dsr_stream);
+  if (e == hipSuccess) e = hipEventRecord(b, dsr_stream);
+  if (e == hipSuccess) e = hipEventSynchronize(b);
+  if (e == hipSuccess) e = hipEventElapsedTime(ms, a, b);
+  if (e == hipSuccess) e = hipMemsetAsync(S->xc, 0, (size_t)S->n_layers * S->xc_region * 4, dsr_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(dsr_stream);
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  if (e != hipSuccess) return dsr_fail("ds_hip_time_stack_layer", e);
+  *ms /= (float)n;
+  return 0;
+}
+
 /* LM-head argmax kernel alone on the stack's current hidden state: n launches back to back
  * between two events (kernel time plus the launch gaps). */
 int ds_hip_time_lm_head(ds_hip_stack_t *S, int n, float *ms) {

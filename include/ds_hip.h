@@ -240,6 +240,9 @@ int ds_hip_time_stack(ds_hip_stack_t *S, int n_steps, float *ms);
 /* Average time of the LM-head argmax kernel over n back-to-back launches on the stack's current
  * hidden state (no token written; includes the launch gaps). */
 int ds_hip_time_lm_head(ds_hip_stack_t *S, int n, float *ms);
+/* One-kernel MoE layer `layer` of a bound stack (no attention) alone: n launches back to back between
+ * two events on the inputs the last step left; clears the layers' output copies afterwards. */
+int ds_hip_time_stack_layer(ds_hip_stack_t *S, int layer, int n, float *ms);
 /* Kernels one decode step launches, and the kind of kernel i ("scores", "gate_up", "down",
  * "lm_head.argmax", "lm_head.final"). */
 int ds_hip_stack_kernel_count(const ds_hip_stack_t *S);
