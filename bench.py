@@ -27,7 +27,8 @@ PEAK_HBM_GBS = 8000.0
 # this benchmark, scaled by the counters' reading for a 256 MiB device copy (FETCH_SIZE x 2.0,
 # WRITE_SIZE x 1.0); profiles/lm_head_argmax_config5_hbm.md holds the runs. Re-measure when the
 # kernel changes.
-LM_TRAFFIC_BYTES = 331074329
+LM_TRAFFIC_BYTES = 331384453
+LAYER_TRAFFIC_BYTES = 32057077  # k_dec_layer<5, 8, 2>, same runs
 
 
 def product():
@@ -292,7 +293,8 @@ def main():
         layer_gbs = layer_bytes / (lt.value * 1e-3) / 1e9
         layer_roof = {"kernel": "k_dec_layer (one MoE layer; 11 launches per step)", "bound": "hbm",
                       "achieved": round(layer_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                      "frac": round(layer_gbs / PEAK_HBM_GBS, 4), "bytes_per_launch": layer_bytes,
+                      "frac": round(layer_gbs / PEAK_HBM_GBS, 4), "traffic": LAYER_TRAFFIC_BYTES,
+                      "bytes_per_launch": layer_bytes,
                       "avg_ms": round(lt.value, 5),
                       "avg_ms_note": "layer 5, 50 back-to-back launches between HIP events on the library "
                                      "stream; latency-bound (routing, then 22 MB of routed rows, per launch)"}
