@@ -1,4 +1,5 @@
-// k_layer.hip — one kernel per MoE layer for the decode stack in CFG routing (f32 router).
+// k_layer.hip — one kernel per MoE layer for the decode stacks (CFG routing with the f32 router;
+// DECODE routing with the exact bf16 scores computed before each layer).
 //
 // The two-kernel layer (k_dec.hip) needs a grid-wide boundary between gate_up and down because
 // every down row reads all of h. Here the down product is split over the intermediate dimension
@@ -24,6 +25,9 @@
 #define DL_UB 32  // intermediate units per block
 #define DL_REP 8  // copies of each accumulated output
 
+// The XCD this wave runs on: s_getreg_b32 hwreg(HW_REG_XCC_ID, 0, 4) (register id 20, 4 bits at
+// offset 0). It only picks which copy the block adds into (every copy is summed), so any value is
+// correct; the id spreads the atomics of different XCDs over different addresses.
 __device__ __forceinline__ int dl_copy() { return __builtin_amdgcn_s_getreg((3 << 11) | 20) & (DL_REP - 1); }
 
 // Loads of one block's units (512 threads, 8 waves): gate and up rows of four units per wave (16
