@@ -130,19 +130,25 @@ def host_layers(dev, handles, rf_host, rb_host):
     return out
 
 
+def cpu_model():
+    for line in open("/proc/cpuinfo"):
+        if line.startswith("model name"):
+            return line.split(":", 1)[1].strip()
+    return "unknown"
+
+
 def cpu_baseline(dev, handles, rfs, rbs, lm, xs_host, gpu_tokens, route, budget_s):
     """The reference CPU path (ds-ocr's own C, oracle/_ref) on this host: moe_forward's INT8 branch
-    for 11 layers + ds_argmax_matvec_bf16, threads = min(cores, 16) as the reference clamps."""
+    for 11 layers + ds_argmax_matvec_bf16 per step. Rows: the reference's own thread count
+    (min(cores, 16): ds_kernels.c:123, :518-519 clamp it) and 1 thread; each row runs a bounded
+    sample of the same steps (about budget_s of CPU time)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import bindings as B
     flags = open("/proc/cpuinfo").read()
     variant = "v4" if (" avx512f " in flags and " avx512bw " in flags) else "v3"
     R = B.ref(variant)
-    kind = "reference"
     if R is None:
         return None
-    threads = min(16, os.cpu_count() or 1)
-    R.ds_set_threads(threads)
     rf_host = [rf.to_array(np.float32) for rf in rfs]
     rb_host = [rb.to_array(np.uint16) for rb in rbs]
     lays = host_layers(dev, handles, rf_host, rb_host)
@@ -151,22 +157,62 @@ def cpu_baseline(dev, handles, rfs, rbs, lm, xs_host, gpu_tokens, route, budget_
     arr = C.create_string_buffer(len(bufs) * R.ref_layer_sizeof())
     for i, b in enumerate(bufs):
         C.memmove(C.addressof(arr) + i * R.ref_layer_sizeof(), b, R.ref_layer_sizeof())
-    toks = np.zeros(len(xs_host), np.int32)
-    t1 = R.ref_decode_steps(C.addressof(arr), LAYERS, lm_w, VOCAB, xs_host, 1, route, toks)
-    n = int(max(1, min(len(xs_host), budget_s / max(t1, 1e-6))))
-    secs = R.ref_decode_steps(C.addressof(arr), LAYERS, lm_w, VOCAB, xs_host, n, route, toks)
-    agree = int(np.sum(toks[:n] == gpu_tokens[:n]))
-    model = "unknown"
-    for line in open("/proc/cpuinfo"):
-        if line.startswith("model name"):
-            model = line.split(":", 1)[1].strip()
-            break
-    return {"value": round(n / secs, 3), "unit": "tok/s", "cores": threads, "kind": kind,
-            "sample": f"{n} decode steps of the same 11-layer + LM-head workload (first {n} inputs), "
-                      f"reference ds-ocr C path built -O3 -march=x86-64-{variant}, {threads} threads "
-                      f"(reference clamp 16) on '{model}' ({os.cpu_count()} logical CPUs); "
-                      f"tokens equal to the GPU's on {agree}/{n} steps",
-            "ms_per_step": round(1000 * secs / n, 3)}
+    ncpu = os.cpu_count() or 1
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else ncpu
+    clamp = min(16, affinity)
+    rows = []
+    for threads in ([clamp, 1] if clamp > 1 else [1]):
+        R.ds_set_threads(threads)
+        toks = np.zeros(len(xs_host), np.int32)
+        t1 = R.ref_decode_steps(C.addressof(arr), LAYERS, lm_w, VOCAB, xs_host, 1, route, toks)
+        n = int(max(1, min(len(xs_host), budget_s / max(t1, 1e-6))))
+        secs = R.ref_decode_steps(C.addressof(arr), LAYERS, lm_w, VOCAB, xs_host, n, route, toks)
+        rows.append({"threads": threads, "value": round(n / secs, 3), "unit": "tok/s",
+                     "ms_per_step": round(1000 * secs / n, 3), "steps": n,
+                     "tokens_equal_to_gpu": int(np.sum(toks[:n] == gpu_tokens[:n]))})
+    main = rows[0]
+    return {"value": main["value"], "unit": "tok/s", "cores": main["threads"], "kind": "reference",
+            "sample": f"{main['steps']} decode steps of the same 11-layer + LM-head workload (the timed region's "
+                      f"first {main['steps']} inputs, same weights exported from the device), reference ds-ocr C "
+                      f"path built -O3 -march=x86-64-{variant}, {main['threads']} threads (the reference clamps "
+                      f"to 16) on '{cpu_model()}'; tokens equal to the GPU's on "
+                      f"{main['tokens_equal_to_gpu']}/{main['steps']} steps",
+            "ms_per_step": main["ms_per_step"], "rows": rows,
+            "host": {"cpu": cpu_model(), "logical_cpus": ncpu, "affinity_cpus": affinity},
+            "unclamped_row": ("not run: the reference's thread pool clamps to 16 threads (ds_kernels.c:123, "
+                              f":518-519) and this process may use {affinity} CPUs" if affinity > 16 else
+                              f"equal to the clamped row: this process may use {affinity} CPUs")}
+
+
+def pct(v, q):
+    return round(float(np.percentile(np.asarray(v, np.float64), q)), 5)
+
+
+def bench_plan(steps, warmup, each, span, profile):
+    """The main stack's step-running calls, as phases separated by resets: (call, steps) in order.
+    Returns the input rows / token slots the stack needs and the phases."""
+    phases = [[("run", warmup), ("time", steps)], [("each", each)], [("profile", profile)], [("span", span)]]
+    rows = max(1, max(sum(n for _, n in ph) for ph in phases))
+    return rows, phases
+
+
+def decoder_plan(n_warm, n_timed):
+    phases = [[("run", n_warm), ("time", n_timed)]]
+    return n_warm + n_timed, phases
+
+
+def check_plan(L, rows, stride, n_tokens, kv_room, phases):
+    """Checks every phase of a plan against the stack's capacity rule before anything runs."""
+    cap = L.ds_hip_stack_capacity_for(rows, stride, n_tokens, kv_room)
+    if cap < 0:
+        raise ValueError(f"invalid stack buffers: rows {rows}, stride {stride}, tokens {n_tokens}")
+    for ph in phases:
+        done = 0
+        for call, n in ph:
+            if not L.ds_hip_steps_fit(cap, done, n):
+                raise ValueError(f"plan {ph}: {call} of {n} steps after {done} passes the capacity {cap}")
+            done += n
+    return cap
 
 
 def main():
@@ -175,11 +221,15 @@ def main():
     ap.add_argument("--steps", type=int, default=226)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--route", choices=["cfg", "decode"], default="cfg")
+    ap.add_argument("--dist-steps", type=int, default=200,
+                    help="graph launches timed one by one for the median and p10/p90 (at least 100)")
+    ap.add_argument("--span-steps", type=int, default=100,
+                    help="eager steps whose MoE-layer span gives the layer kernel's average duration")
     ap.add_argument("--profile-steps", type=int, default=20)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-tokens", type=int, default=662, help="config-3 prefill measurement (0: skip)")
-    ap.add_argument("--prefill-reps", type=int, default=20)
+    ap.add_argument("--prefill-reps", type=int, default=100)
     ap.add_argument("--dense-layer", action="store_true",
                     help="prepend DeepSeek-OCR's layer-0 dense SwiGLU FFN (1280x6848 bf16) to every step")
     ap.add_argument("--decoder-step", type=int, default=-1, metavar="KV",
@@ -192,8 +242,8 @@ def main():
                     help="> 1: the reference's repetition penalty after each argmax, over the run's tokens")
     ap.add_argument("--no-repeat-ngram", type=int, default=0, help="> 0: the reference's n-gram ban")
     ap.add_argument("--layer-kernels", type=int, choices=[1, 2], default=1,
-                    help="MoE layer kernels in CFG routing: 1 (down split over intermediate units, per-XCD "
-                         "output copies) or 2 (gate_up, then down with the combine in top-k order)")
+                    help="MoE layer kernels: 1 (down split over intermediate units, per-XCD output copies) or 2 "
+                         "(gate_up, then down with the combine in top-k order)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (HBM counter calibration)")
     args = ap.parse_args()
@@ -201,10 +251,22 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (sharding the decode "
                                    "path over several GPUs is not implemented)"}))
         sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        sys.exit("--steps must be >= 1 and --warmup >= 0")
     dev = product()
     L = dev.load()
-    dev.check(L.ds_hip_init(), "init")
     route = dev.ROUTE_CFG if args.route == "cfg" else dev.ROUTE_DECODE
+    full = args.decoder_step >= 0
+    n_each = max(100, args.dist_steps)
+    n_span = max(10, args.span_steps)
+    rows, phases = bench_plan(args.steps, args.warmup, n_each, n_span, args.profile_steps)
+    kv_room = rows + 1 if full else -1
+    check_plan(L, rows, H, rows, kv_room, phases)
+    n_dec_warm, n_dec = 5, 40
+    dec_rows, dec_phases = decoder_plan(n_dec_warm, n_dec)
+    if args.decoder_kv >= 0 and not full:
+        check_plan(L, dec_rows, H, dec_rows, dec_rows + 1, dec_phases)
+    dev.check(L.ds_hip_init(), "init")
 
     gu = dev.DeviceBuffer(2 * SI * H * 2)
     dn = dev.DeviceBuffer(H * SI * 2)
@@ -222,32 +284,34 @@ def main():
         dev.check(L.ds_hip_sync(), "sync")
         src.close()
         dst.close()
-    n_inputs = args.warmup + args.steps
-    xs = dev.DeviceBuffer(n_inputs * H * 4)
-    dev.check(L.ds_hip_fill_normal_f32(xs.ptr, n_inputs * H, 777, 0.0, 1.0), "fill")
-    toks = dev.DeviceBuffer(n_inputs * 4)
+    xs = dev.DeviceBuffer(rows * H * 4)
+    dev.check(L.ds_hip_fill_normal_f32(xs.ptr, rows * H, 777, 0.0, 1.0), "fill")
+    toks = dev.DeviceBuffer(rows * 4)
     arr = (C.c_void_p * LAYERS)(*handles)
     S = L.ds_hip_stack_create(arr, LAYERS, lm.ptr, VOCAB, route)
     if not S:
         raise RuntimeError(L.ds_hip_last_error().decode())
     sampling = args.repeat_penalty > 1.0 or args.no_repeat_ngram > 0
     if sampling:
-        dev.check(L.ds_hip_stack_set_sampling(S, args.repeat_penalty, args.no_repeat_ngram, n_inputs), "sampling")
-    full = args.decoder_step >= 0
+        dev.check(L.ds_hip_stack_set_sampling(S, args.repeat_penalty, args.no_repeat_ngram, rows), "sampling")
     dense = make_dense(dev) if (args.dense_layer or full) else None
     if dense:
         dev.check(L.ds_hip_stack_set_dense(S, dense), "set dense")
     attns = []
     if full:
-        attns = make_attention(dev, LAYERS + 1, args.decoder_step, args.decoder_step + n_inputs + 1)
+        attns = make_attention(dev, LAYERS + 1, args.decoder_step, args.decoder_step + kv_room)
         fnorm = np.ones(H, np.float32)
         arr_a = (C.c_void_p * len(attns))(*attns)
         dev.check(L.ds_hip_stack_set_attention(S, arr_a, len(attns), fnorm.ctypes.data, 1e-6, args.decoder_step, 0),
                   "set attention")
     dev.check(L.ds_hip_stack_set_layer_kernels(S, 1 if args.layer_kernels == 1 else 0), "layer kernels")
-    dev.check(L.ds_hip_stack_bind(S, xs.ptr, H, toks.ptr), "bind")
+    dev.check(L.ds_hip_stack_bind(S, xs.ptr, H, rows, toks.ptr, rows), "bind")
+    if L.ds_hip_stack_capacity(S) < rows:
+        raise RuntimeError(f"stack capacity {L.ds_hip_stack_capacity(S)} < planned {rows}")
     bytes_per_step = L.ds_hip_stack_bytes_per_step(S)
     layer_kernels = L.ds_hip_stack_layer_kernels(S)
+    nk = L.ds_hip_stack_kernel_count(S)
+    names = [L.ds_hip_stack_kernel_name(S, i).decode() for i in range(nk)]
 
     # warmup, then exactly --steps timed steps (graph launches) between synchronisations
     dev.check(L.ds_hip_stack_run(S, args.warmup), "warmup")
@@ -257,47 +321,77 @@ def main():
     dev.check(L.ds_hip_time_stack(S, args.steps, C.byref(ms)), "timed steps")
     dev.check(L.ds_hip_sync(), "sync")
     wall = time.perf_counter() - t0
-    gpu_tokens = toks.to_array(np.int32)
+    gpu_tokens = toks.to_array(np.int32)[args.warmup:args.warmup + args.steps].copy()
     ms_per_step = ms.value / args.steps
+
+    # the step-time distribution: n_each graph launches with an event between consecutive ones
+    dev.check(L.ds_hip_stack_reset(S), "reset")
+    dev.check(L.ds_hip_stack_run(S, 0), "run")
+    each = np.zeros(n_each, np.float32)
+    dev.check(L.ds_hip_time_stack_each(S, n_each, each), "per-step timing")
+    rerun = toks.to_array(np.int32)
+    lo, hi = args.warmup, min(args.warmup + args.steps, n_each)
+    rerun_equal = int(np.sum(rerun[lo:hi] == gpu_tokens[:max(0, hi - lo)])) if hi > lo else 0
 
     # per-kernel durations (eager launches with HIP events around every kernel)
     dev.check(L.ds_hip_stack_reset(S), "reset")
-    nk = L.ds_hip_stack_kernel_count(S)
-    names = [L.ds_hip_stack_kernel_name(S, i).decode() for i in range(nk)]
     per = np.zeros(nk, np.float32)
-    dev.check(L.ds_hip_profile_stack(S, min(args.profile_steps, n_inputs), per), "profile")
+    dev.check(L.ds_hip_profile_stack(S, args.profile_steps, per), "profile")
     kinds = {}
     for k, v in zip(names, per):
         kinds.setdefault(k, []).append(float(v))
     kernel_ms = {k: {"avg_ms": round(float(np.mean(v)), 5), "launches_per_step": len(v),
                      "ms_per_step": round(float(np.sum(v)), 5)} for k, v in kinds.items()}
+
+    # the MoE layers' span inside real eager steps: events before the first and after the last layer
+    # kernel only, so the span / 11 is the layer kernel's average launch duration on real inputs, over
+    # 11 distinct layers' weights (308 MB per step, more than the 256 MB MALL)
+    moe = [i for i, n in enumerate(names)
+           if n in ("layer", "gate_up", "down") or (n == "scores" and route == dev.ROUTE_DECODE)]
+    dev.check(L.ds_hip_stack_reset(S), "reset")
+    span = np.zeros(n_span, np.float32)
+    dev.check(L.ds_hip_time_stack_span(S, n_span, moe[0], moe[-1] + 1, span), "layer span timing")
     lm_bytes = VOCAB * H * 2
+    dense_bytes = 3 * H * DENSE_I * 2 if dense else 0
+    attn_bytes = 0
+    layer_bytes = (bytes_per_step - lm_bytes - dense_bytes - attn_bytes) // LAYERS
+    layer_ms = float(np.median(span)) / LAYERS
+    layer_gbs = layer_bytes / (layer_ms * 1e-3) / 1e9
+    layer_kernel = ("k_dec_layer (one kernel per MoE layer: k_dec_layer<5, 1, 40> for the first, k_dec_layer<5, 8, 2> "
+                    "for the other 10)" if layer_kernels == 1 else "k_dec_gate_up<5> + k_dec_down<8> (two kernels per "
+                                                                   "MoE layer)")
+    if route == dev.ROUTE_DECODE:
+        layer_kernel += " with its k_dec_scores_bf16 kernel"
+    roofline = {"kernel": layer_kernel, "bound": "hbm", "achieved": round(layer_gbs, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(layer_gbs / PEAK_HBM_GBS, 4),
+                "traffic": LAYER_TRAFFIC_BYTES if (layer_kernels == 1 and route == dev.ROUTE_CFG and not full) else None,
+                "bytes_per_launch": int(layer_bytes), "launches_per_step": LAYERS,
+                "avg_ms": round(layer_ms, 5), "p10_ms": round(pct(span, 10) / LAYERS, 5),
+                "p90_ms": round(pct(span, 90) / LAYERS, 5),
+                "avg_ms_method": f"median over {n_span} eager steps of the span from the first to the last MoE-layer "
+                                 "kernel (HIP events on the library stream, none between the layers), divided by "
+                                 f"{LAYERS}: real inputs and 11 distinct layers' weights; includes the kernel "
+                                 "boundaries between the layers",
+                "why_this_kernel": "the MoE layers take the largest share of the step (11 launches), ahead of the "
+                                   "LM head (1 launch)"}
     # the LM-head kernel alone, 50 launches back to back on the last step's hidden state
     lm_t = C.c_float(0)
     dev.check(L.ds_hip_time_lm_head(S, 50, C.byref(lm_t)), "lm head timing")
     lm_ms = lm_t.value
     lm_gbs = lm_bytes / (lm_ms * 1e-3) / 1e9
-    # achievable HBM read rate on this box: a plain streaming read of the same 331 MB (the head itself),
-    # 50 back-to-back launches like the LM-head timing above
+    # achievable HBM read rate on this box: a plain streaming read of the same 331 MB
     rd_t = C.c_float(0)
     dev.check(L.ds_hip_time_stream_read(lm.ptr, lm_bytes, 50, C.byref(rd_t)), "stream read timing")
     read_gbs = lm_bytes / (rd_t.value * 1e-3) / 1e9
+    roofline_lm = {"kernel": "k_dec_lm_argmax<1, 8> (LM-head argmax, 1 launch per step)", "bound": "hbm",
+                   "achieved": round(lm_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                   "frac": round(lm_gbs / PEAK_HBM_GBS, 4), "traffic": LM_TRAFFIC_BYTES,
+                   "bytes_per_launch": lm_bytes, "avg_ms": round(lm_ms, 5),
+                   "avg_ms_method": "50 back-to-back launches between HIP events on the library stream",
+                   "stream_read_gbs": round(read_gbs, 1), "frac_of_stream_read": round(lm_gbs / read_gbs, 4),
+                   "stream_read_note": "a plain nontemporal streaming read of the same bytes, timed the same way: "
+                                       "the achievable HBM read rate on this box"}
     step_gbs = bytes_per_step / (ms_per_step * 1e-3) / 1e9
-    # one MoE layer kernel alone (layer 5 of 11, 50 launches back to back; one-kernel layers only):
-    # its algorithmic bytes are the step's minus the head's, per layer
-    layer_roof = None
-    if layer_kernels == 1 and not full:
-        lt = C.c_float(0)
-        dev.check(L.ds_hip_time_stack_layer(S, min(5, LAYERS - 1), 50, C.byref(lt)), "layer timing")
-        layer_bytes = (bytes_per_step - lm_bytes - (3 * H * DENSE_I * 2 if dense else 0)) // LAYERS
-        layer_gbs = layer_bytes / (lt.value * 1e-3) / 1e9
-        layer_roof = {"kernel": "k_dec_layer (one MoE layer; 11 launches per step)", "bound": "hbm",
-                      "achieved": round(layer_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                      "frac": round(layer_gbs / PEAK_HBM_GBS, 4), "traffic": LAYER_TRAFFIC_BYTES,
-                      "bytes_per_launch": layer_bytes,
-                      "avg_ms": round(lt.value, 5),
-                      "avg_ms_note": "layer 5, 50 back-to-back launches between HIP events on the library "
-                                     "stream; latency-bound (routing, then 22 MB of routed rows, per launch)"}
 
     # prefill (config 3): 662 seeded tokens through one config-2 layer (the first decode layer)
     prefill = None
@@ -310,8 +404,7 @@ def main():
         dev.check(L.ds_hip_time_prefill(handles[0], op.ptr, xp.ptr, T, route, args.prefill_reps, C.byref(pt)),
                   "prefill timing")
         us = pt.value * 1e3
-        # algorithmic work: K routed + shared experts per token (2 flops per weight element) and
-        # the router; the MFMAs run each product twice (hi and lo halves of the activations)
+        # algorithmic work: K routed + shared experts per token (2 flops per weight element) and the router
         flops = T * (K * 2 * (2 * I * H + H * I) + 2 * (2 * SI * H + H * SI) + 2 * E * H)
         wbytes = E * (2 * I * H + 2 * I * 8 + H * I + H * 8) + 2 * SI * H + 2 * SI * 8 + H * SI + H * 8
         prefill = {"config": "config 3: 662 tokens x 1280 through one config-2 layer", "tokens": T,
@@ -319,17 +412,19 @@ def main():
                    "algorithmic_tflops": round(flops / (us * 1e-6) / 1e12, 2),
                    "mfma_frac_of_bf16_peak": round(flops / (us * 1e-6) / 2.5e15, 4),
                    "weight_bytes": wbytes, "weight_gbs": round(wbytes / (us * 1e-6) / 1e9, 1),
+                   "hbm_frac": round(wbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                   "us_method": f"{args.prefill_reps} back-to-back calls (one graph launch each) between HIP events",
                    "note": "MFMA work is 2x the algorithmic flops (bf16 hi/lo activation split)"}
         xp.close()
         op.close()
 
-    # whole decoder steps: 12 layers with their attention halves after kv cached
-    # positions, timed like the main line over 40 steps after 5 warm-up steps
+    # whole decoder steps (12 layers with their attention halves after kv cached positions), with
+    # their own input rows and token slots
     decoder = None
     if args.decoder_kv >= 0 and not full:
-        kv, n_dec = args.decoder_kv, 45
+        kv = args.decoder_kv
         dense2 = make_dense(dev)
-        attns2 = make_attention(dev, LAYERS + 1, kv, kv + n_dec + 1)
+        attns2 = make_attention(dev, LAYERS + 1, kv, kv + dec_rows + 1)
         arr2 = (C.c_void_p * LAYERS)(*handles)
         S2 = L.ds_hip_stack_create(arr2, LAYERS, lm.ptr, VOCAB, route)
         if not S2:
@@ -338,18 +433,20 @@ def main():
         fnorm = np.ones(H, np.float32)
         arr_a2 = (C.c_void_p * len(attns2))(*attns2)
         dev.check(L.ds_hip_stack_set_attention(S2, arr_a2, len(attns2), fnorm.ctypes.data, 1e-6, kv, 0), "attention")
-        toks2 = dev.DeviceBuffer(n_dec * 4)
+        xs2 = dev.DeviceBuffer(dec_rows * H * 4)
+        dev.check(L.ds_hip_fill_normal_f32(xs2.ptr, dec_rows * H, 778, 0.0, 1.0), "fill")
+        toks2 = dev.DeviceBuffer(dec_rows * 4)
         dev.check(L.ds_hip_stack_set_layer_kernels(S2, 1 if args.layer_kernels == 1 else 0), "layer kernels")
-        dev.check(L.ds_hip_stack_bind(S2, xs.ptr, H, toks2.ptr), "bind")
-        dev.check(L.ds_hip_stack_run(S2, 5), "warmup")
+        dev.check(L.ds_hip_stack_bind(S2, xs2.ptr, H, dec_rows, toks2.ptr, dec_rows), "bind")
+        dev.check(L.ds_hip_stack_run(S2, n_dec_warm), "warmup")
         dev.check(L.ds_hip_sync(), "sync")
         ms2 = C.c_float(0)
-        dev.check(L.ds_hip_time_stack(S2, n_dec - 5, C.byref(ms2)), "timed decoder steps")
-        step_ms = ms2.value / (n_dec - 5)
+        dev.check(L.ds_hip_time_stack(S2, n_dec, C.byref(ms2)), "timed decoder steps")
+        step_ms = ms2.value / n_dec
         decoder = {"config": f"12 decoder layers (dense layer 0 + the 11 MoE layers above), each with its attention "
                              f"half (10 heads x 128, f32 KV cache), final RMSNorm, argmax head; tokens at cache "
-                             f"positions {kv + 5}..{kv + n_dec - 1} after {kv} seeded cached positions",
-                   "steps": n_dec - 5, "ms_per_step": round(step_ms, 5), "tok_per_s": round(1e3 / step_ms, 2),
+                             f"positions {kv + n_dec_warm}..{kv + dec_rows - 1} after {kv} seeded cached positions",
+                   "steps": n_dec, "ms_per_step": round(step_ms, 5), "tok_per_s": round(1e3 / step_ms, 2),
                    "bytes_per_step_weights": int(L.ds_hip_stack_bytes_per_step(S2)),
                    "note": "bytes exclude the KV reads (about 10 KB per cached position and layer)"}
         L.ds_hip_stack_destroy(S2)
@@ -357,14 +454,19 @@ def main():
             L.ds_hip_attn_destroy(A)
         L.ds_hip_dense_destroy(dense2)
         toks2.close()
+        xs2.close()
 
-    xs_host = xs.to_array(np.float32).reshape(n_inputs, H)[args.warmup:].copy()
+    xs_host = xs.to_array(np.float32).reshape(rows, H)[args.warmup:args.warmup + args.steps].copy()
     cpu = None
     if not args.no_cpu and not dense and not sampling and not full:  # the reference CPU leg: MoE layers + argmax head
         try:
-            cpu = cpu_baseline(dev, handles, rfs, rbs, lm, xs_host, gpu_tokens[args.warmup:], route, args.cpu_seconds)
+            cpu = cpu_baseline(dev, handles, rfs, rbs, lm, xs_host, gpu_tokens, route, args.cpu_seconds)
         except Exception as exc:  # report, never hide
             cpu = {"error": repr(exc)}
+    elif not args.no_cpu:
+        cpu = {"skipped": "the reference CPU leg covers the MoE layers + LM head only (config 5); this run adds "
+                          + ", ".join(x for x, on in (("the dense layer", dense), ("sampling rules", sampling),
+                                                      ("attention", full)) if on)}
     L.ds_hip_stack_destroy(S)
     if dense:
         L.ds_hip_dense_destroy(dense)
@@ -373,6 +475,15 @@ def main():
     for h in handles:
         L.ds_hip_layer_destroy(h)
 
+    workload = ((f"whole decoder steps after {args.decoder_step} cached positions: attention "
+                 "(10 heads x 128, f32 KV cache) per layer + " if full else "") +
+                ("layer-0 dense SwiGLU FFN 1280x6848 bf16 + " if dense else "") +
+                (f"repetition penalty {args.repeat_penalty} / no-repeat n-gram {args.no_repeat_ngram} "
+                 "after the argmax + " if sampling else "") +
+                "config 5: 11 DeepSeek3B-MoE INT8 layers (H1280, 64x[1792x1280 + 1280x896] routed top-6 + 2 shared, "
+                f"{'f32 router renormalised' if route == dev.ROUTE_CFG else 'bf16 router, fast-exp softmax over 64'}) "
+                f"+ argmax LM head 129280x1280 bf16, batch 1; {args.steps} timed decode steps after {args.warmup} "
+                "warm-up steps, each on a fresh seeded input")
     line = {
         "metric": "INT8 MoE decode tok/s (batch 1) + achieved HBM GB/s as % of peak",
         "value": round(args.steps / (ms.value * 1e-3), 2),
@@ -381,33 +492,25 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
+        "ms_per_step_dist": {"median": pct(each, 50), "p10": pct(each, 10), "p90": pct(each, 90), "n": n_each,
+                             "method": "graph launches one after another with an event between consecutive "
+                                       "launches (launch-to-launch time), after a reset"},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8 weights (u8 codes + f32 scale/offset), f32 accumulate; bf16 LM head",
         "data": "synthetic: seeded N(0,0.02) weights generated on device, seeded N(0,1) f32 hidden states",
-        "config": {"workload": (f"whole decoder steps after {args.decoder_step} cached positions: attention "
-                                 "(10 heads x 128, f32 KV cache) per layer + " if full else "") +
-                               ("layer-0 dense SwiGLU FFN 1280x6848 bf16 + " if dense else "") +
-                               (f"repetition penalty {args.repeat_penalty} / no-repeat n-gram {args.no_repeat_ngram} "
-                                "after the argmax + " if sampling else "") +
-                               "config 5: 11 DeepSeek3B-MoE INT8 layers (H1280, 64x[1792x1280 + 1280x896] "
-                               "routed top-6 + 2 shared, f32 router renormalised) + argmax LM head 129280x1280 "
-                               "bf16, batch 1, 226-step decode",
-                   "route": args.route, "moe_layer_kernels": layer_kernels, "global_batch": 1,
-                   "parallelism": "single GPU"},
+        "config": {"workload": workload, "route": args.route, "moe_layer_kernels": layer_kernels,
+                   "global_batch": 1, "parallelism": "single GPU"},
         "hbm": {"bytes_per_step": int(bytes_per_step), "achieved_gbs": round(step_gbs, 1),
                 "frac_of_peak": round(step_gbs / PEAK_HBM_GBS, 4), "peak_gbs": PEAK_HBM_GBS,
+                "frac_of_peak_median": round(bytes_per_step / (pct(each, 50) * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                 "wall_s_timed_region": round(wall, 4)},
-        "roofline": {"kernel": "k_dec_lm_argmax (LM-head argmax, the largest kernel)", "bound": "hbm",
-                     "achieved": round(lm_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(lm_gbs / PEAK_HBM_GBS, 4), "traffic": LM_TRAFFIC_BYTES,
-                     "bytes_per_launch": lm_bytes, "avg_ms": round(lm_ms, 5),
-                     "avg_ms_note": "50 back-to-back launches between HIP events on the library stream",
-                     "stream_read_gbs": round(read_gbs, 1), "frac_of_stream_read": round(lm_gbs / read_gbs, 4),
-                     "stream_read_note": "a plain nontemporal streaming read of the same bytes, timed the same "
-                                         "way: the achievable HBM read rate on this box"},
-        "roofline_moe_layer": layer_roof,
+        "roofline": roofline,
+        "roofline_lm_head": roofline_lm,
+        "determinism": {"rerun_tokens_equal": rerun_equal, "of": max(0, hi - lo),
+                        "note": "tokens of the timed steps against a second graph run of the same inputs; the "
+                                f"{'one-kernel' if layer_kernels == 1 else 'two-kernel'} layers produced both"},
         "kernels": kernel_ms,
         "prefill": prefill,
         "decoder_step": decoder,

@@ -89,7 +89,14 @@ SIGNATURES = {
     "ds_hip_prefill_wait_error": (C.c_int, [vp, C.c_int]),
     "ds_hip_stack_create": (vp, [vp, C.c_int, vp, C.c_int, C.c_int]),
     "ds_hip_stack_destroy": (None, [vp]),
-    "ds_hip_stack_bind": (C.c_int, [vp, vp, C.c_int, vp]),
+    "ds_hip_stack_bind": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, C.c_int]),
+    "ds_hip_stack_set_embedding": (C.c_int, [vp, vp, C.c_int]),
+    "ds_hip_stack_capacity": (C.c_int, [vp]),
+    "ds_hip_stack_steps_left": (C.c_int, [vp]),
+    "ds_hip_stack_capacity_for": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int]),
+    "ds_hip_steps_fit": (C.c_int, [C.c_int, C.c_int, C.c_int]),
+    "ds_hip_time_stack_each": (C.c_int, [vp, C.c_int, f32p]),
+    "ds_hip_time_stack_span": (C.c_int, [vp, C.c_int, C.c_int, C.c_int, f32p]),
     "ds_hip_stack_reset": (C.c_int, [vp]),
     "ds_hip_stack_run": (C.c_int, [vp, C.c_int]),
     "ds_hip_stack_run_eager": (C.c_int, [vp, C.c_int]),
@@ -116,7 +123,6 @@ SIGNATURES = {
     "ds_hip_stack_set_dense": (C.c_int, [vp, vp]),
     "ds_hip_stack_set_layer_kernels": (C.c_int, [vp, C.c_int]),
     "ds_hip_stack_layer_kernels": (C.c_int, [vp]),
-    "ds_hip_time_stack_layer": (C.c_int, [vp, C.c_int, C.c_int, C.POINTER(C.c_float)]),
     "ds_hip_load_dense": (C.c_int, [C.POINTER(C.c_char_p), C.c_int, C.c_int, C.POINTER(vp)]),
     "ds_hip_safetensors_info": (C.c_int, [C.POINTER(C.c_char_p), C.c_int, C.c_char_p, C.POINTER(C.c_int),
                                           C.POINTER(C.c_int64), C.c_int]),

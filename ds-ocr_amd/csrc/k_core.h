@@ -90,11 +90,15 @@ hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int r
                               int bf16sim, float *out, void *ws, int *idx_out, float *w_out, hipStream_t s);
 
 /* Final reduction of per-block argmax candidates: writes tokens[*step] (tokens[0] when step is
- * NULL) and advances *step. */
-hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int *tokens, int *step, hipStream_t s);
-/* The same, also clearing zero_p[0..zero_n) (16-byte aligned, zero_n % 4 == 0). */
-hipError_t dsh_launch_lm_argmax_final_clear(const unsigned long long *cand, int n, int *tokens, int *step,
-                                            float *zero_p, int zero_n, hipStream_t s);
+ * NULL) and advances *step. Also clears zero_p[0..zero_n) (16-byte aligned, zero_n % 4 == 0; 0 for
+ * none) and, when emb_out != NULL, writes the chosen token's bf16 embedding row emb[token][0..H)
+ * widened to f32 into emb_out (the next step's input; H % 8 == 0). */
+hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int *tokens, int *step, float *zero_p,
+                                      int zero_n, const uint16_t *emb, int emb_vocab, int H, float *emb_out,
+                                      hipStream_t s);
+/* emb[tokens[*step - 1]][0..H) widened to f32 into out (a token outside [0, emb_vocab): unchanged). */
+hipError_t dsh_launch_embed_next(const int *tokens, const int *step, const uint16_t *emb, int emb_vocab, int H,
+                                 float *out, hipStream_t s);
 
 /* ---- latency-oriented decode kernels (k_dec.hip) ---- */
 int dsh_dec_supported(int H, int I, int E, int K, int SI);

@@ -583,9 +583,39 @@ __global__ void __launch_bounds__(256) k_dec_lm_argmax(const uint16_t *W, const 
 // The step index and a batch of 4 candidates per thread are loaded together (clamped addresses, no
 // branches), so the kernel waits for one round trip per 1024 candidates. Also clears
 // zero_p[0..zero_n) (16-byte aligned, zero_n % 4 == 0).
+// The next decode step's input (ds_ocr.c:2271-2278): the BF16 embedding row of token tok widened
+// by << 16; a token outside [0, emb_vocab) leaves the row as it was, as the reference's guard does.
+// Called by all threads of the block with the same tok; H % 8 == 0.
+__device__ __forceinline__ void embed_row(const uint16_t *__restrict__ emb, int emb_vocab, int H, int tok,
+                                          float *__restrict__ out) {
+  if (tok < 0 || tok >= emb_vocab) return;
+  const uint16_t *r = emb + (size_t)tok * H;
+  for (int i = 8 * (int)threadIdx.x; i < H; i += 8 * (int)blockDim.x) {
+    const uint4 u = *(const uint4 *)(r + i);
+    const unsigned w[4] = {u.x, u.y, u.z, u.w};
+    f32x4 lo, hi;
+    lo[0] = __uint_as_float(w[0] << 16), lo[1] = __uint_as_float(w[0] & 0xFFFF0000u);
+    lo[2] = __uint_as_float(w[1] << 16), lo[3] = __uint_as_float(w[1] & 0xFFFF0000u);
+    hi[0] = __uint_as_float(w[2] << 16), hi[1] = __uint_as_float(w[2] & 0xFFFF0000u);
+    hi[2] = __uint_as_float(w[3] << 16), hi[3] = __uint_as_float(w[3] & 0xFFFF0000u);
+    *(f32x4 *)(out + i) = lo;
+    *(f32x4 *)(out + i + 4) = hi;
+  }
+}
+
+// tokens[*step - 1]'s embedding into out (after the sampling rules changed the step's token).
+__global__ void __launch_bounds__(256) k_embed_next(const int *__restrict__ tokens, const int *__restrict__ step,
+                                                    const uint16_t *__restrict__ emb, int emb_vocab, int H,
+                                                    float *__restrict__ out) {
+  const int s = *step - 1;
+  if (s >= 0) embed_row(emb, emb_vocab, H, tokens[s], out);
+}
+
 __global__ void __launch_bounds__(256) k_lm_argmax_final(const unsigned long long *__restrict__ cand, int n,
                                                          int *__restrict__ tokens, int *__restrict__ step,
-                                                         float *__restrict__ zero_p, int zero_n) {
+                                                         float *__restrict__ zero_p, int zero_n,
+                                                         const uint16_t *__restrict__ emb, int emb_vocab, int H,
+                                                         float *__restrict__ emb_out) {
   for (int i = 4 * threadIdx.x; i < zero_n; i += 1024) *(f32x4 *)(zero_p + i) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   __shared__ unsigned long long wbest[4];
   const int s = step ? *step : 0;
@@ -600,11 +630,18 @@ __global__ void __launch_bounds__(256) k_lm_argmax_final(const unsigned long lon
   b = dsh_wave_max_u64(b);
   if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = b;
   __syncthreads();
+  __shared__ int s_tok;
   if (threadIdx.x == 0) {
     unsigned long long best = wbest[0];
     for (int i = 1; i < 4; i++) best = dsh_umax64(best, wbest[i]);
-    tokens[s] = dsh_key_index(best);
+    const int tok = dsh_key_index(best);
+    tokens[s] = tok;
+    s_tok = tok;
     if (step) *step = s + 1;
+  }
+  if (emb_out) {
+    __syncthreads();
+    embed_row(emb, emb_vocab, H, s_tok, emb_out);
   }
 }
 
@@ -709,15 +746,22 @@ int dsh_dec_lm_eligible(const void *W, int in_dim, int vocab, int nthreads) {
   return 1;
 }
 
-hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int *tokens, int *step, hipStream_t s) {
-  k_lm_argmax_final<<<1, 256, 0, s>>>(cand, n, tokens, step, nullptr, 0);
+hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int *tokens, int *step, float *zero_p,
+                                      int zero_n, const uint16_t *emb, int emb_vocab, int H, float *emb_out,
+                                      hipStream_t s) {
+  if (((uintptr_t)zero_p & 15) || zero_n % 4 || zero_n < 0 || n <= 0) return hipErrorInvalidValue;
+  if (emb_out && (!emb || emb_vocab <= 0 || H <= 0 || H % 8 || ((uintptr_t)emb & 15) || ((uintptr_t)emb_out & 15)))
+    return hipErrorInvalidValue;
+  k_lm_argmax_final<<<1, 256, 0, s>>>(cand, n, tokens, step, zero_p, zero_n, emb, emb_vocab, H, emb_out);
   return hipGetLastError();
 }
 
-hipError_t dsh_launch_lm_argmax_final_clear(const unsigned long long *cand, int n, int *tokens, int *step,
-                                            float *zero_p, int zero_n, hipStream_t s) {
-  if (((uintptr_t)zero_p & 15) || zero_n % 4) return hipErrorInvalidValue;
-  k_lm_argmax_final<<<1, 256, 0, s>>>(cand, n, tokens, step, zero_p, zero_n);
+hipError_t dsh_launch_embed_next(const int *tokens, const int *step, const uint16_t *emb, int emb_vocab, int H,
+                                 float *out, hipStream_t s) {
+  if (!tokens || !step || !emb || !out || emb_vocab <= 0 || H <= 0 || H % 8 || ((uintptr_t)emb & 15) ||
+      ((uintptr_t)out & 15))
+    return hipErrorInvalidValue;
+  k_embed_next<<<1, 256, 0, s>>>(tokens, step, emb, emb_vocab, H, out);
   return hipGetLastError();
 }
 

@@ -169,6 +169,8 @@ hipError_t ds_hip_attn_enqueue(const ds_hip_attn_t *A, const float *x_in, const 
 
 int ds_hip_attn_hidden(const ds_hip_attn_t *A) { return A ? A->d.H : 0; }
 
+int ds_hip_attn_max_seq(const ds_hip_attn_t *A) { return A ? A->d.max_seq : 0; }
+
 size_t ds_hip_attn_weight_bytes(const ds_hip_attn_t *A) {
   return A ? (size_t)4 * A->d.H * A->d.n_heads * A->d.head_dim * 2 + (size_t)2 * A->d.H * 4 : 0;
 }

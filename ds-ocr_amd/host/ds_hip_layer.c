@@ -255,6 +255,15 @@ static int check_router(const ds_hip_layer_t *L, int route_mode) {
   return 0;
 }
 
+/* Event marks between a step's launch groups: ev == NULL records nothing; otherwise mark i records
+ * ev[i] when that entry is non-NULL (so a caller can bracket any range of kernels) and always
+ * advances the count. */
+static hipError_t mark(hipEvent_t *ev, int *n) {
+  if (!ev) return hipSuccess;
+  hipEvent_t x = ev[(*n)++];
+  return x ? hipEventRecord(x, dsr_stream) : hipSuccess;
+}
+
 /* Router partial scores of layer L for input x (CFG: f32 partials; DECODE: exact full scores as
  * one partial). Returns the number of partial rows through *np. */
 static hipError_t scores_enqueue(const ds_hip_layer_t *L, const float *x_in, const int *step, int stride,
@@ -277,17 +286,17 @@ static hipError_t layer_enqueue(const ds_hip_layer_t *L, const dsh_layer_work_t 
   hipError_t e = hipSuccess;
   if (!have_scores) {
     e = scores_enqueue(L, x_in, step, stride, route_mode, partials, &np);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+    if (e == hipSuccess) e = mark(ev, nev);
   }
   if (e == hipSuccess)
     e = dsh_launch_dec_gate_up(&L->d, x_in, step, stride, partials, np, route_mode, bf16sim, wk, dsr_stream);
-  if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+  if (e == hipSuccess) e = mark(ev, nev);
   int chain = next && route_mode == DS_HIP_ROUTE_CFG;
   if (e == hipSuccess)
     e = dsh_launch_dec_down(&L->d, x_in, step, stride, x_out, residual, NULL, bf16sim, wk,
                             chain ? next->d.router_f32_t : NULL, chain ? next->E : 0, chain ? partials : NULL,
                             dsr_stream);
-  if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+  if (e == hipSuccess) e = mark(ev, nev);
   return e;
 }
 
@@ -725,6 +734,17 @@ struct ds_hip_stack {
   const float *xs;
   int stride;
   int *tokens;
+  /* what the step's first kernels read: xs + (*step)*stride, or the embedding feed's row */
+  const float *in;
+  const int *in_step;
+  int in_stride;
+  /* steps launched since the bind or the last reset, and how many the bound buffers allow */
+  int done, cap;
+  /* autoregressive input (ds_hip_stack_set_embedding): step s >= 1 reads the widened embedding of
+   * token s - 1, which the step before wrote into ebuf */
+  const uint16_t *emb;
+  int emb_vocab;
+  float *ebuf;
   hipGraph_t graph;
   hipGraphExec_t exec;
   int bound;
@@ -798,7 +818,7 @@ ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers,
   S->ncand = S->lm_fast ? dsh_dec_lm_blocks(vocab) : dsh_argmax_avx_blocks(vocab);
   const size_t np_bytes = al((size_t)layers[0]->np * 64 * 4);
   size_t off_x = 256, off_c = off_x + al((size_t)H * 4), off_p = off_c + al((size_t)S->ncand * 8);
-  size_t bytes = off_p + 2 * np_bytes;
+  size_t off_e = off_p + 2 * np_bytes, bytes = off_e + al((size_t)H * 4);
   hipError_t e = hipMalloc(&S->work, bytes);
   if (e != hipSuccess) {
     dsr_fail("stack allocation", e);
@@ -813,6 +833,7 @@ ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers,
   S->cand = (unsigned long long *)((char *)S->work + off_c);
   S->partials[0] = (float *)((char *)S->work + off_p);
   S->partials[1] = (float *)((char *)S->work + off_p + np_bytes);
+  S->ebuf = (float *)((char *)S->work + off_e);
   S->split_want = 1;
   return S;
 }
@@ -990,21 +1011,21 @@ static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *ne
   hipError_t e = hipSuccess;
   const int cfg = S->route_mode == DS_HIP_ROUTE_CFG, C = dsh_layer_split_copies();
   const dsh_layer_work_t *wk = &S->layers[0]->wk;
-  const float *xin = S->xs;
-  const int *st = S->step;
-  int stride = S->stride, a = 0, nc = 1; /* nc: copies of xin (one-kernel layers: the per-XCD copies) */
+  const float *xin = S->in;
+  const int *st = S->in_step;
+  int stride = S->in_stride, a = 0, nc = 1; /* nc: copies of xin (one-kernel layers: the per-XCD copies) */
   if (S->dense) {
     e = ds_hip_attn_enqueue(S->attn[a++], xin, st, stride, 1, NULL, S->step, S->pos0, S->hbuf, S->nbuf, NULL, 0,
                             NULL);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+    if (e == hipSuccess) e = mark(ev, nev);
     if (e == hipSuccess)
       e = dsh_launch_dense_gate_up(S->dense->wg, S->dense->wu, S->nbuf, NULL, 0, S->dense->H, S->dense->I,
                                    S->dense->h, dsr_stream);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+    if (e == hipSuccess) e = mark(ev, nev);
     if (e == hipSuccess)
       e = dsh_launch_dense_down(S->dense->wd, S->dense->h, S->nbuf, NULL, 0, S->dense->H, S->dense->I, 1, S->hbuf,
                                 S->xbuf, NULL, 0, NULL, dsr_stream);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+    if (e == hipSuccess) e = mark(ev, nev);
     xin = S->xbuf;
     st = NULL;
     stride = 0;
@@ -1017,10 +1038,10 @@ static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *ne
     e = ds_hip_attn_enqueue(S->attn[a++], xin, st, stride, nc, nc > 1 ? S->xbuf : NULL, S->step, S->pos0, S->hbuf,
                             S->nbuf,
                             cfg ? L->d.router_f32_t : NULL, cfg ? L->E : 0, cfg ? pin : NULL);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+    if (e == hipSuccess) e = mark(ev, nev);
     if (e == hipSuccess && !cfg) {
       e = scores_enqueue(L, S->nbuf, NULL, 0, S->route_mode, pin, &np);
-      if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+      if (e == hipSuccess) e = mark(ev, nev);
     }
     if (S->split) { /* one kernel: MoE(n) + h into the copies region l, clearing region l - 2 */
       float *out = xc_region(S, l), *zp = l >= 2 ? xc_region(S, l - 2) : NULL;
@@ -1028,17 +1049,17 @@ static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *ne
         e = dsh_launch_dec_layer(&L->d, &S->sp[l], S->nbuf, NULL, 0, 1, pin, np,
                                  cfg ? DSH_ROUTE_CFG : DSH_ROUTE_DECODE, S->hbuf, out, out + (size_t)C * S->H, zp,
                                  zp ? (int)S->xc_region : 0, dsr_stream);
-      if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+      if (e == hipSuccess) e = mark(ev, nev);
       xin = out;
       nc = C;
     } else {
       if (e == hipSuccess)
         e = dsh_launch_dec_gate_up(&L->d, S->nbuf, NULL, 0, pin, np, S->route_mode, S->bf16sim, wk, dsr_stream);
-      if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+      if (e == hipSuccess) e = mark(ev, nev);
       if (e == hipSuccess)
         e = dsh_launch_dec_down(&L->d, S->nbuf, NULL, 0, S->xbuf, 1, S->hbuf, S->bf16sim, wk, NULL, 0, NULL,
                                 dsr_stream);
-      if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+      if (e == hipSuccess) e = mark(ev, nev);
       xin = S->xbuf;
       nc = 1;
     }
@@ -1049,7 +1070,7 @@ static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *ne
   if (e == hipSuccess)
     e = dsh_launch_final_norm(xin, nc, S->final_norm, S->H, S->final_eps, S->trunc_final && S->bf16sim, S->fbuf,
                               nc > 1 ? S->xbuf : NULL, dsr_stream);
-  if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+  if (e == hipSuccess) e = mark(ev, nev);
   return e;
 }
 
@@ -1066,17 +1087,17 @@ static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *n
   const int zn = (int)S->xc_region;
   int np0 = S->layers[0]->np;
   if (!dense || !cfg) {
-    e = scores_enqueue(S->layers[0], dense ? S->xbuf : S->xs, dense ? NULL : S->step, dense ? 0 : S->stride,
+    e = scores_enqueue(S->layers[0], dense ? S->xbuf : S->in, dense ? NULL : S->in_step, dense ? 0 : S->in_stride,
                        S->route_mode, S->partials[0], &np0);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+    if (e == hipSuccess) e = mark(ev, nev);
   }
   for (int l = 0; l < NL && e == hipSuccess; l++) {
     const ds_hip_layer_t *L = S->layers[l];
     float *out = xc_region(S, l);
     float *zp = l >= 2 ? xc_region(S, l - 2) : NULL;
     if (l == 0) {
-      e = dsh_launch_dec_layer(&L->d, &S->sp[l], dense ? S->xbuf : S->xs, dense ? NULL : S->step,
-                               dense ? 0 : S->stride, 1, S->partials[0], np0, mode, NULL, out, out + (size_t)C * H, zp,
+      e = dsh_launch_dec_layer(&L->d, &S->sp[l], dense ? S->xbuf : S->in, dense ? NULL : S->in_step,
+                               dense ? 0 : S->in_stride, 1, S->partials[0], np0, mode, NULL, out, out + (size_t)C * H, zp,
                                zp ? zn : 0, dsr_stream);
     } else {
       float *in = xc_region(S, l - 1);
@@ -1085,7 +1106,7 @@ static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *n
       if (!cfg) { /* DECODE: the exact scores of the summed input */
         e = dsh_launch_dec_scores_bf16_copies(L->d.router_bf16, in, NULL, 0, C, H, L->E, dsr_threads(),
                                               S->partials[l & 1], dsr_stream);
-        if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+        if (e == hipSuccess) e = mark(ev, nev);
         pin = S->partials[l & 1];
         np = 1;
       }
@@ -1093,13 +1114,13 @@ static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *n
         e = dsh_launch_dec_layer(&L->d, &S->sp[l], in, NULL, 0, C, pin, np, mode, NULL, out, out + (size_t)C * H, zp,
                                  zp ? zn : 0, dsr_stream);
     }
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+    if (e == hipSuccess) e = mark(ev, nev);
   }
   if (!S->lm_fast) { /* the plain output for the general LM-head path (the fast head sums the copies) */
     if (e == hipSuccess)
       e = dsh_launch_dec_copy_sum(xc_region(S, NL - 1), H, S->xbuf, NL >= 2 ? xc_region(S, NL - 2) : NULL,
                                   NL >= 2 ? zn : 0, dsr_stream);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[(*nev)++], dsr_stream);
+    if (e == hipSuccess) e = mark(ev, nev);
   }
   return e;
 }
@@ -1111,10 +1132,15 @@ static hipError_t split_lm_enqueue(ds_hip_stack_t *S) {
                                          S->vocab, S->cand, S->xbuf, dsr_stream);
 }
 
-static hipError_t split_final_enqueue(ds_hip_stack_t *S) {
-  const int NL = S->n_layers;
-  return dsh_launch_lm_argmax_final_clear(S->cand, S->ncand, S->tokens, S->step, xc_region(S, NL >= 2 ? NL - 2 : 0),
-                                          (int)S->xc_region * (NL >= 2 ? 2 : 1), dsr_stream);
+/* The step's final kernel: the token into tokens[step], the step counter advanced, the last copies
+ * regions cleared (one-kernel layers) and, with the embedding feed and no sampling rules after it,
+ * the next step's input row. */
+static hipError_t final_enqueue(ds_hip_stack_t *S, int clear) {
+  const int NL = S->n_layers, embed = S->emb && !smp_active(S);
+  float *zp = clear ? xc_region(S, NL >= 2 ? NL - 2 : 0) : NULL;
+  const int zn = clear ? (int)S->xc_region * (NL >= 2 ? 2 : 1) : 0;
+  return dsh_launch_lm_argmax_final(S->cand, S->ncand, S->tokens, S->step, zp, zn, embed ? S->emb : NULL,
+                                    S->emb_vocab, S->H, embed ? S->ebuf : NULL, dsr_stream);
 }
 
 /* Whether the one-kernel layers apply: no bf16 simulation, no attention, supported shapes (in
@@ -1198,20 +1224,20 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
   int n = 0;
   const int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
   const dsh_layer_work_t *wk = &S->layers[0]->wk;
-  if (ev) e = hipEventRecord(ev[n++], dsr_stream);
+  e = mark(ev, &n);
   if (S->attn) {
     e = layers_full_enqueue(S, ev, &n);
   } else {
     const int dense = S->dense != NULL;
     if (dense) {  /* layer 0: x = x + FFN(x); in CFG mode also the first MoE layer's router partials */
-      e = dsh_launch_dense_gate_up(S->dense->wg, S->dense->wu, S->xs, S->step, S->stride, S->dense->H, S->dense->I,
+      e = dsh_launch_dense_gate_up(S->dense->wg, S->dense->wu, S->in, S->in_step, S->in_stride, S->dense->H, S->dense->I,
                                    S->dense->h, dsr_stream);
-      if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+      if (e == hipSuccess) e = mark(ev, &n);
       if (e == hipSuccess)
-        e = dsh_launch_dense_down(S->dense->wd, S->dense->h, S->xs, S->step, S->stride, S->dense->H, S->dense->I, 1, NULL,
+        e = dsh_launch_dense_down(S->dense->wd, S->dense->h, S->in, S->in_step, S->in_stride, S->dense->H, S->dense->I, 1, NULL,
                                   S->xbuf, cfg ? S->layers[0]->d.router_f32_t : NULL, cfg ? S->layers[0]->E : 0,
                                   cfg ? S->partials[0] : NULL, dsr_stream);
-      if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+      if (e == hipSuccess) e = mark(ev, &n);
     }
     if (S->split && e == hipSuccess) {
       e = split_layers_enqueue(S, ev, &n);
@@ -1219,23 +1245,23 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
     for (int l = 0; l < S->n_layers && e == hipSuccess; l++) {
       const ds_hip_layer_t *L = S->layers[l];
       const int first = l == 0 && !dense; /* reads the step's input directly */
-      const float *xin = first ? S->xs : S->xbuf;
-      const int *st = first ? S->step : NULL;
-      int stride = first ? S->stride : 0;
+      const float *xin = first ? S->in : S->xbuf;
+      const int *st = first ? S->in_step : NULL;
+      int stride = first ? S->in_stride : 0;
       float *pin = S->partials[l & 1], *pout = S->partials[(l + 1) & 1];
       int np = L->np;
       if (!cfg || first) {
         e = scores_enqueue(L, xin, st, stride, S->route_mode, pin, &np);
-        if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+        if (e == hipSuccess) e = mark(ev, &n);
         if (e != hipSuccess) break;
       }
       const ds_hip_layer_t *next = cfg && l + 1 < S->n_layers ? S->layers[l + 1] : NULL;
       e = dsh_launch_dec_gate_up(&L->d, xin, st, stride, pin, np, S->route_mode, S->bf16sim, wk, dsr_stream);
-      if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+      if (e == hipSuccess) e = mark(ev, &n);
       if (e == hipSuccess)
         e = dsh_launch_dec_down(&L->d, xin, st, stride, S->xbuf, 1, NULL, S->bf16sim, wk, next ? next->d.router_f32_t : NULL,
                                 next ? next->E : 0, next ? pout : NULL, dsr_stream);
-      if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+      if (e == hipSuccess) e = mark(ev, &n);
     }
   }
   if (e != hipSuccess) return e;
@@ -1250,23 +1276,66 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
     e = dsh_launch_argmax_avx_partial(S->lm, lm_in(S), S->cand, NULL, S->H, S->vocab,
                                       T > 1 ? (S->vocab + T - 1) / T : S->vocab, dsr_stream);
   }
-  if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
-  if (e == hipSuccess)
-    e = clear_in_final ? split_final_enqueue(S)
-                       : dsh_launch_lm_argmax_final(S->cand, S->ncand, S->tokens, S->step, dsr_stream);
-  if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+  if (e == hipSuccess) e = mark(ev, &n);
+  if (e == hipSuccess) e = final_enqueue(S, clear_in_final);
+  if (e == hipSuccess) e = mark(ev, &n);
   if (e == hipSuccess && smp_active(S)) {
-    /* the repetition penalty and the n-gram ban over this stack's earlier tokens; one event after
-     * all of the sampler's kernels */
+    /* the repetition penalty and the n-gram ban over this stack's earlier tokens, then (embedding
+     * feed) the final token's row; one event after all of these kernels */
     e = dsh_launch_sample(S->lm, lm_in(S), S->H, S->vocab, dsr_threads(), S->rp, S->ngram, S->step, S->tokens, NULL,
                           S->hist_cap, smp_vals(S), smp_logits(S), smp_flag(S), dsr_stream);
-    if (e == hipSuccess && ev) e = hipEventRecord(ev[n++], dsr_stream);
+    if (e == hipSuccess && S->emb)
+      e = dsh_launch_embed_next(S->tokens, S->step, S->emb, S->emb_vocab, S->H, S->ebuf, dsr_stream);
+    if (e == hipSuccess) e = mark(ev, &n);
   }
   return e;
 }
 
-int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int *tokens_dev) {
-  if (!S || !xs_dev || !tokens_dev || stride < 0) return dsr_failf("ds_hip_stack_bind: invalid arguments");
+int ds_hip_stack_capacity_for(int n_rows, int stride, int n_tokens, int kv_room) {
+  if (n_rows < 1 || n_tokens < 1 || stride < 0) return -1;
+  int cap = n_tokens;
+  if (stride > 0 && n_rows < cap) cap = n_rows;
+  if (kv_room >= 0 && kv_room < cap) cap = kv_room;
+  return cap;
+}
+
+int ds_hip_steps_fit(int capacity, int steps_done, int n) {
+  return capacity >= 0 && steps_done >= 0 && n >= 0 && steps_done <= capacity && n <= capacity - steps_done;
+}
+
+/* KV positions left for the stack's steps: min over its attention blocks of max_seq - pos0 (-1:
+ * no attention). */
+static int stack_kv_room(const ds_hip_stack_t *S) {
+  if (!S->attn) return -1;
+  int room = -1;
+  for (int i = 0; i < S->n_attn; i++) {
+    int r = ds_hip_attn_max_seq(S->attn[i]) - S->pos0;
+    if (r < 0) r = 0;
+    if (room < 0 || r < room) room = r;
+  }
+  return room;
+}
+
+int ds_hip_stack_set_embedding(ds_hip_stack_t *S, const uint16_t *tok_embeddings_dev, int vocab) {
+  if (!S) return dsr_failf("ds_hip_stack_set_embedding: NULL stack");
+  if (S->bound) return dsr_failf("ds_hip_stack_set_embedding: call before ds_hip_stack_bind");
+  if (!tok_embeddings_dev) {
+    S->emb = NULL;
+    S->emb_vocab = 0;
+    return 0;
+  }
+  if (vocab <= 0 || S->H % 8 || ((uintptr_t)tok_embeddings_dev & 15))
+    return dsr_failf("ds_hip_stack_set_embedding: need vocab > 0, hidden %% 8 == 0 and a 16-byte aligned table");
+  S->emb = tok_embeddings_dev;
+  S->emb_vocab = vocab;
+  return 0;
+}
+
+int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int n_rows, int *tokens_dev,
+                      int n_tokens) {
+  if (!S || !xs_dev || !tokens_dev || stride < 0 || n_rows < 1 || n_tokens < 1)
+    return dsr_failf("ds_hip_stack_bind: invalid arguments (need xs_dev, tokens_dev, stride >= 0, n_rows >= 1, "
+                     "n_tokens >= 1)");
   if (S->exec) {
     hipGraphExecDestroy(S->exec);
     S->exec = NULL;
@@ -1275,9 +1344,15 @@ int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int *t
     hipGraphDestroy(S->graph);
     S->graph = NULL;
   }
+  S->bound = 0;
   S->xs = xs_dev;
   S->stride = stride;
   S->tokens = tokens_dev;
+  /* with the embedding feed only row 0 of xs is read (at reset, into ebuf) */
+  S->in = S->emb ? S->ebuf : xs_dev;
+  S->in_step = S->emb ? NULL : S->step;
+  S->in_stride = S->emb ? 0 : stride;
+  S->cap = ds_hip_stack_capacity_for(n_rows, S->emb ? 0 : stride, n_tokens, stack_kv_room(S));
   DSR_TRY(hipStreamSynchronize(dsr_stream), "bind");
   S->split = split_eligible(S);
   if (S->split && split_build(S)) return -1;
@@ -1296,25 +1371,47 @@ int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int *t
   return ds_hip_stack_reset(S);
 }
 
-/* Zeroes the step counter (and the work buffers with it). */
+int ds_hip_stack_capacity(const ds_hip_stack_t *S) { return S && S->bound ? S->cap : 0; }
+
+int ds_hip_stack_steps_left(const ds_hip_stack_t *S) { return S && S->bound ? S->cap - S->done : 0; }
+
+/* Zeroes the step counter (and the work buffers with it); with the embedding feed, row 0 of the
+ * bound input becomes the first step's input. */
 int ds_hip_stack_reset(ds_hip_stack_t *S) {
-  if (!S) return -1;
+  if (!S || !S->bound) return dsr_failf("ds_hip_stack_reset: stack not bound");
   DSR_TRY(hipMemsetAsync(S->work, 0, S->work_bytes, dsr_stream), "reset stack");
   if (S->split && S->xc)
     DSR_TRY(hipMemsetAsync(S->xc, 0, (size_t)S->n_layers * S->xc_region * 4, dsr_stream), "reset stack");
+  if (S->emb)
+    DSR_TRY(hipMemcpyAsync(S->ebuf, S->xs, (size_t)S->H * 4, hipMemcpyDeviceToDevice, dsr_stream), "reset stack");
+  S->done = 0;
+  return 0;
+}
+
+/* Refuses, before anything is launched, n more steps than the bound buffers hold. */
+static int steps_check(const ds_hip_stack_t *S, int n, const char *who) {
+  if (!S || !S->bound) return dsr_failf("%s: stack not bound", who);
+  if (!ds_hip_steps_fit(S->cap, S->done, n))
+    return dsr_failf("%s: %d more steps after %d would pass the stack's capacity of %d (rows of the bound input, "
+                     "length of the token array, KV positions); reset or bind larger buffers",
+                     who, n, S->done, S->cap);
   return 0;
 }
 
 int ds_hip_stack_run(ds_hip_stack_t *S, int n_steps) {
-  if (!S || !S->bound) return dsr_failf("ds_hip_stack_run: stack not bound");
-  for (int i = 0; i < n_steps; i++) DSR_TRY(hipGraphLaunch(S->exec, dsr_stream), "graph launch");
+  if (steps_check(S, n_steps, "ds_hip_stack_run")) return -1;
+  for (int i = 0; i < n_steps; i++) {
+    DSR_TRY(hipGraphLaunch(S->exec, dsr_stream), "graph launch");
+    S->done++;
+  }
   return 0;
 }
 
 int ds_hip_stack_run_eager(ds_hip_stack_t *S, int n_steps) {
-  if (!S || !S->bound) return dsr_failf("ds_hip_stack_run_eager: stack not bound");
+  if (steps_check(S, n_steps, "ds_hip_stack_run_eager")) return -1;
   for (int i = 0; i < n_steps; i++) {
     hipError_t e = step_enqueue(S, NULL);
+    S->done++;
     if (e != hipSuccess) return dsr_fail("decode step", e);
   }
   return 0;
@@ -1326,7 +1423,8 @@ int ds_hip_stack_hidden(ds_hip_stack_t *S, float *x_host) {
 }
 
 int ds_hip_time_stack(ds_hip_stack_t *S, int n_steps, float *ms) {
-  if (!S || !S->bound || !ms) return dsr_failf("ds_hip_time_stack: invalid arguments");
+  if (!ms) return dsr_failf("ds_hip_time_stack: invalid arguments");
+  if (steps_check(S, n_steps, "ds_hip_time_stack")) return -1;
   hipEvent_t a, b;
   DSR_TRY(hipEventCreate(&a), "event");
   DSR_TRY(hipEventCreate(&b), "event");
@@ -1340,35 +1438,68 @@ int ds_hip_time_stack(ds_hip_stack_t *S, int n_steps, float *ms) {
   return rc;
 }
 
-/* One-kernel MoE layer `layer` of a bound stack alone, n launches back to back between two events,
- * on the inputs the last step left (the same bytes as in a step); the output regions are cleared
- * afterwards, so the next step starts as after a reset of the copies. */
-int ds_hip_time_stack_layer(ds_hip_stack_t *S, int layer, int n, float *ms) {
-  if (!S || !S->bound || !S->split || S->attn || layer < 0 || layer >= S->n_layers || n <= 0 || !ms)
-    return dsr_failf("ds_hip_time_stack_layer: needs a bound stack with one-kernel layers and no attention");
-  const ds_hip_layer_t *L = S->layers[layer];
-  const int C = dsh_layer_split_copies(), H = S->H, cfg = S->route_mode == DS_HIP_ROUTE_CFG;
-  const int mode = cfg ? DSH_ROUTE_CFG : DSH_ROUTE_DECODE, dense = S->dense != NULL;
-  float *out = xc_region(S, layer);
-  const float *in = layer ? xc_region(S, layer - 1) : (dense ? S->xbuf : S->xs);
-  const float *pin = layer && cfg ? in + (size_t)C * H : S->partials[layer & 1];
-  const int np = layer ? (cfg ? C : 1) : (cfg ? L->np : 1);
-  hipEvent_t a, b;
-  DSR_TRY(hipEventCreate(&a), "event");
-  DSR_TRY(hipEventCreate(&b), "event");
-  hipError_t e = hipEventRecord(a, dsr_stream);
-  for (int i = 0; i < n && e == hipSuccess; i++)
-    e = dsh_launch_dec_layer(&L->d, &S->sp[layer], in, layer || dense ? NULL : S->step, layer || dense ? 0 : S->stride,
-                             layer ? C : 1, pin, np, mode, NULL, out, out + (size_t)C * H, NULL, 0, dsr_stream);
-  if (e == hipSuccess) e = hipEventRecord(b, dsr_stream);
-  if (e == hipSuccess) e = hipEventSynchronize(b);
-  if (e == hipSuccess) e = hipEventElapsedTime(ms, a, b);
-  if (e == hipSuccess) e = hipMemsetAsync(S->xc, 0, (size_t)S->n_layers * S->xc_region * 4, dsr_stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(dsr_stream);
-  hipEventDestroy(a);
-  hipEventDestroy(b);
-  if (e != hipSuccess) return dsr_fail("ds_hip_time_stack_layer", e);
-  *ms /= (float)n;
+/* Creates n events (all or none). */
+static int events_create(hipEvent_t *ev, int n) {
+  for (int i = 0; i < n; i++)
+    if (hipEventCreate(&ev[i]) != hipSuccess) {
+      while (i--) hipEventDestroy(ev[i]);
+      return dsr_failf("event creation failed");
+    }
+  return 0;
+}
+
+static void events_destroy(hipEvent_t *ev, int n) {
+  for (int i = 0; i < n; i++)
+    if (ev[i]) hipEventDestroy(ev[i]);
+}
+
+int ds_hip_time_stack_each(ds_hip_stack_t *S, int n_steps, float *ms_each) {
+  if (!ms_each || n_steps <= 0) return dsr_failf("ds_hip_time_stack_each: invalid arguments");
+  if (steps_check(S, n_steps, "ds_hip_time_stack_each")) return -1;
+  hipEvent_t *ev = (hipEvent_t *)calloc((size_t)n_steps + 1, sizeof(hipEvent_t));
+  if (!ev || events_create(ev, n_steps + 1)) {
+    free(ev);
+    return dsr_failf("ds_hip_time_stack_each: events");
+  }
+  hipError_t e = hipEventRecord(ev[0], dsr_stream);
+  for (int i = 0; i < n_steps && e == hipSuccess; i++) {
+    e = hipGraphLaunch(S->exec, dsr_stream);
+    S->done++;
+    if (e == hipSuccess) e = hipEventRecord(ev[i + 1], dsr_stream);
+  }
+  if (e == hipSuccess) e = hipEventSynchronize(ev[n_steps]);
+  for (int i = 0; i < n_steps && e == hipSuccess; i++) e = hipEventElapsedTime(&ms_each[i], ev[i], ev[i + 1]);
+  events_destroy(ev, n_steps + 1);
+  free(ev);
+  if (e != hipSuccess) return dsr_fail("ds_hip_time_stack_each", e);
+  return 0;
+}
+
+int ds_hip_time_stack_span(ds_hip_stack_t *S, int n_steps, int k0, int k1, float *ms_each) {
+  if (!ms_each || n_steps <= 0) return dsr_failf("ds_hip_time_stack_span: invalid arguments");
+  if (steps_check(S, n_steps, "ds_hip_time_stack_span")) return -1;
+  const int nk = stack_kernel_count(S);
+  if (k0 < 0 || k1 <= k0 || k1 > nk) return dsr_failf("ds_hip_time_stack_span: kernel range [%d, %d) of %d", k0, k1, nk);
+  hipEvent_t *marks = (hipEvent_t *)calloc((size_t)nk + 1, sizeof(hipEvent_t));
+  hipEvent_t *ev = (hipEvent_t *)calloc(2 * (size_t)n_steps, sizeof(hipEvent_t));
+  if (!marks || !ev || events_create(ev, 2 * n_steps)) {
+    free(marks);
+    free(ev);
+    return dsr_failf("ds_hip_time_stack_span: events");
+  }
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < n_steps && e == hipSuccess; i++) {
+    marks[k0] = ev[2 * i];
+    marks[k1] = ev[2 * i + 1];
+    e = step_enqueue(S, marks);
+    S->done++;
+  }
+  if (e == hipSuccess) e = hipEventSynchronize(ev[2 * n_steps - 1]);
+  for (int i = 0; i < n_steps && e == hipSuccess; i++) e = hipEventElapsedTime(&ms_each[i], ev[2 * i], ev[2 * i + 1]);
+  events_destroy(ev, 2 * n_steps);
+  free(ev);
+  free(marks);
+  if (e != hipSuccess) return dsr_fail("ds_hip_time_stack_span", e);
   return 0;
 }
 
@@ -1416,7 +1547,8 @@ const char *ds_hip_stack_kernel_name(const ds_hip_stack_t *S, int i) {
 }
 
 int ds_hip_profile_stack(ds_hip_stack_t *S, int n_steps, float *ms_out) {
-  if (!S || !S->bound || !ms_out || n_steps <= 0) return dsr_failf("ds_hip_profile_stack: invalid arguments");
+  if (!ms_out || n_steps <= 0) return dsr_failf("ds_hip_profile_stack: invalid arguments");
+  if (steps_check(S, n_steps, "ds_hip_profile_stack")) return -1;
   int nk = stack_kernel_count(S);
   hipEvent_t *ev = (hipEvent_t *)calloc((size_t)(nk + 1), sizeof(hipEvent_t));
   double *acc = (double *)calloc((size_t)nk, sizeof(double));
@@ -1424,7 +1556,9 @@ int ds_hip_profile_stack(ds_hip_stack_t *S, int n_steps, float *ms_out) {
   for (int i = 0; i <= nk; i++)
     if (hipEventCreate(&ev[i]) != hipSuccess) rc = -1;
   for (int s = 0; s < n_steps && rc == 0; s++) {
-    if (step_enqueue(S, ev) != hipSuccess || hipEventSynchronize(ev[nk]) != hipSuccess) {
+    hipError_t e = step_enqueue(S, ev);
+    S->done++;
+    if (e != hipSuccess || hipEventSynchronize(ev[nk]) != hipSuccess) {
       rc = -1;
       break;
     }

@@ -57,6 +57,7 @@ hipError_t ds_hip_attn_enqueue(const struct ds_hip_attn *A, const float *x_in, c
                                int ncopies, float *x_plain, const int *pos_ptr, int pos_add, float *h_out, float *n_out,
                                const float *WrT_next, int E_next, float *partials_next);
 int ds_hip_attn_hidden(const struct ds_hip_attn *A);
+int ds_hip_attn_max_seq(const struct ds_hip_attn *A); /* KV positions the caches hold */
 size_t ds_hip_attn_weight_bytes(const struct ds_hip_attn *A); /* projections and norms read per token */
 
 #endif

@@ -222,9 +222,35 @@ int ds_hip_stack_set_layer_kernels(ds_hip_stack_t *S, int one_kernel);
 /* Kernels per MoE layer of the bound stack (1 or 2). */
 int ds_hip_stack_layer_kernels(const ds_hip_stack_t *S);
 void ds_hip_stack_destroy(ds_hip_stack_t *S);
-/* Step s reads its input hidden state from xs_dev + s*stride (stride 0: always xs_dev) and writes
- * its token to tokens_dev[s]; s is a device counter advanced by every step. Captures the graph. */
-int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int *tokens_dev);
+/* Autoregressive input (ds_ocr.c:2271-2278, the decode loop's "embedding for next token"): with a
+ * table set, step s >= 1 reads the BF16 embedding row of the token step s - 1 chose (after the
+ * sampling rules, when set), widened to f32 by << 16, and step 0 reads row 0 of the bound input
+ * (the caller's first input, e.g. the embedding of the prefill's token). A token outside
+ * [0, vocab) leaves the input as it was, as the reference's guard does. The row is written on the
+ * device by the step that chose the token, so n steps run with no host round trip.
+ * tok_embeddings_dev: bf16 [vocab][hidden] on the device, 16-byte aligned, borrowed; hidden % 8 == 0.
+ * Call before ds_hip_stack_bind; NULL turns the feed off. */
+int ds_hip_stack_set_embedding(ds_hip_stack_t *S, const uint16_t *tok_embeddings_dev, int vocab);
+/* Binds the steps' input and output and captures the graph. Step s (counted from the bind or the
+ * last reset) reads its input hidden state from xs_dev + s*stride (stride 0: always xs_dev; the
+ * embedding feed reads only row 0, at reset) and writes its token to tokens_dev[s]. n_rows is the
+ * number of rows xs_dev holds and n_tokens the length of tokens_dev: the stack then runs at most
+ * ds_hip_stack_capacity(S) steps between resets -- the smaller of n_tokens, n_rows (when rows are
+ * read per step) and, for whole decoder steps, the KV positions left (max_seq - pos0) -- and every
+ * call that launches steps refuses, before launching anything, to go past it. */
+int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int n_rows, int *tokens_dev,
+                      int n_tokens);
+/* Steps a bound stack may run between resets, and how many of them are left. */
+int ds_hip_stack_capacity(const ds_hip_stack_t *S);
+int ds_hip_stack_steps_left(const ds_hip_stack_t *S);
+/* The capacity rule on its own (host arithmetic, no device): n_rows rows of input read per step
+ * when stride > 0, n_tokens token slots, kv_room KV positions left (-1: no attention). Returns the
+ * capacity, or -1 for invalid arguments. */
+int ds_hip_stack_capacity_for(int n_rows, int stride, int n_tokens, int kv_room);
+/* 1 if n more steps fit after steps_done of a capacity, else 0 (host arithmetic). */
+int ds_hip_steps_fit(int capacity, int steps_done, int n);
+/* Zeroes the step counter and the step's work buffers (with the embedding feed, row 0 of the bound
+ * input becomes the next step's input). */
 int ds_hip_stack_reset(ds_hip_stack_t *S);
 /* Launches n_steps decode steps (one graph launch each), asynchronously. */
 int ds_hip_stack_run(ds_hip_stack_t *S, int n_steps);
@@ -235,14 +261,19 @@ int ds_hip_stack_hidden(ds_hip_stack_t *S, float *x_host);
 size_t ds_hip_stack_bytes_per_step(const ds_hip_stack_t *S);
 
 /* ---------------- timing (HIP events on the library stream) ---------------- */
+/* Every timing call that runs steps counts them against the stack's capacity, like ds_hip_stack_run. */
 /* Wall time of n_steps graph launches. */
 int ds_hip_time_stack(ds_hip_stack_t *S, int n_steps, float *ms);
+/* n_steps graph launches with an event between consecutive launches: ms_each[i] is step i's
+ * launch-to-launch time (for medians and percentiles). */
+int ds_hip_time_stack_each(ds_hip_stack_t *S, int n_steps, float *ms_each);
+/* n_steps eager steps, each with one event before kernel group k0 and one after group k1 - 1
+ * (groups as ds_hip_stack_kernel_name numbers them): ms_each[i] is that span in step i, on the
+ * step's real inputs. E.g. the MoE layers of a step, for their average launch duration. */
+int ds_hip_time_stack_span(ds_hip_stack_t *S, int n_steps, int k0, int k1, float *ms_each);
 /* Average time of the LM-head argmax kernel over n back-to-back launches on the stack's current
  * hidden state (no token written; includes the launch gaps). */
 int ds_hip_time_lm_head(ds_hip_stack_t *S, int n, float *ms);
-/* One-kernel MoE layer `layer` of a bound stack (no attention) alone: n launches back to back between
- * two events on the inputs the last step left; clears the layers' output copies afterwards. */
-int ds_hip_time_stack_layer(ds_hip_stack_t *S, int layer, int n, float *ms);
 /* Kernels one decode step launches, and the kind of kernel i ("scores", "gate_up", "down",
  * "lm_head.argmax", "lm_head.final"). */
 int ds_hip_stack_kernel_count(const ds_hip_stack_t *S);

@@ -63,7 +63,7 @@ def test_decoder_step_vs_oracle(dev, B, mode, rswa):
         assert names[0] == "attention" and names[-3] == "final_norm" and names.count("attention") == 3
         xd = dev.DeviceBuffer.from_array(xs)
         td = dev.DeviceBuffer(4 * steps)
-        dev.check(L.ds_hip_stack_bind(S, xd.ptr, H, td.ptr), "bind")
+        dev.check(L.ds_hip_stack_bind(S, xd.ptr, H, len(xs), td.ptr, steps), "bind")
         worst = 0.0
         for s in range(steps):
             pos = pos0 + s
@@ -146,7 +146,7 @@ def test_decoder_step_deepseek_size(dev, B):
         dev.check(L.ds_hip_stack_set_attention(S, at, 12, fnorm.ctypes.data, 1e-6, pos0, 0), "attention")
         xd = dev.DeviceBuffer.from_array(xs)
         td = dev.DeviceBuffer(4 * steps)
-        dev.check(L.ds_hip_stack_bind(S, xd.ptr, Hf, td.ptr), "bind")
+        dev.check(L.ds_hip_stack_bind(S, xd.ptr, Hf, len(xs), td.ptr, steps), "bind")
         hidden = []
         for _ in range(steps):
             dev.check(L.ds_hip_stack_run(S, 1), "run")

@@ -101,7 +101,7 @@ def test_stack_with_dense_layer_vs_oracle(dev, B, mode):
             assert ("scores" in names) == (mode == 0)  # CFG: the dense down writes the partials
             xd = dev.DeviceBuffer.from_array(xs)
             td = dev.DeviceBuffer(4 * len(xs))
-            dev.check(L.ds_hip_stack_bind(S, xd.ptr, H, td.ptr), "bind")
+            dev.check(L.ds_hip_stack_bind(S, xd.ptr, H, len(xs), td.ptr, len(xs)), "bind")
             assert L.ds_hip_stack_set_dense(S, D) == -1  # only before binding
             for s in range(len(xs)):
                 dev.check(L.ds_hip_stack_run(S, 1), "run")

@@ -213,7 +213,7 @@ def run_stack(dev, layers, lm, vocab, xs, mode, graph=True, kernels=None, expect
         td = dev.DeviceBuffer(4 * n)
         if kernels is not None:
             dev.check(L.ds_hip_stack_set_layer_kernels(S, 1 if kernels == 1 else 0), "layer kernels")
-        dev.check(L.ds_hip_stack_bind(S, xd.ptr, xs.shape[1], td.ptr), "bind")
+        dev.check(L.ds_hip_stack_bind(S, xd.ptr, xs.shape[1], n, td.ptr, n), "bind")
         if kernels is not None:
             assert L.ds_hip_stack_layer_kernels(S) == (expect or (1 if kernels == 1 else 2))
         hidden = []

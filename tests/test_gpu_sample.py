@@ -94,7 +94,7 @@ def test_stack_sampling_vs_oracle(dev, B, cap):
         assert names[-1] == "sample"
         xd = dev.DeviceBuffer.from_array(x)
         td = dev.DeviceBuffer(4 * n_steps)
-        dev.check(L.ds_hip_stack_bind(S, xd.ptr, 0, td.ptr), "bind")
+        dev.check(L.ds_hip_stack_bind(S, xd.ptr, 0, 1, td.ptr, n_steps), "bind")
         assert L.ds_hip_stack_set_sampling(S, 1.0, 0, 0) == -1  # only before binding
         hidden = []
         for _ in range(n_steps):

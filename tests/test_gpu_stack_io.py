@@ -1,0 +1,161 @@
+"""The decode stack's input and output on the GPU: the capacity the bound buffers give (calls that
+would run past it are refused before anything is launched), and the autoregressive embedding feed
+(ds_ocr.c:2271-2278: each step's input is the widened bf16 embedding of the previous step's token,
+written on the device), against the oracle composed the same way."""
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+from test_gpu_moe import oracle_decode, rel_err, upload_layer  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def small_stack(dev, B, seed, n_layers=2, H=256, vocab=3000):
+    lays = [B.make_moe_layer(seed + i, hidden=H, inter=128, n_experts=16) for i in range(n_layers)]
+    hs = [upload_layer(dev, lay) for lay in lays]
+    lm_w = B.normal_bf16(vocab * H, seed + 50, 0.02)
+    return lays, hs, lm_w
+
+
+def widen(row_bf16):
+    return (row_bf16.astype(np.uint32) << 16).view(np.float32)
+
+
+@pytest.mark.parametrize("kernels", [1, 2])
+def test_capacity_refuses_overrun_before_launch(dev, B, kernels):
+    L = dev.load()
+    H, vocab = 256, 3000
+    lays, hs, lm_w = small_stack(dev, B, 500)
+    lm = dev.DeviceBuffer.from_array(lm_w)
+    xs = np.stack([B.normal_f32(H, 5000 + s) for s in range(3)])
+    xd = dev.DeviceBuffer.from_array(xs)
+    td = dev.DeviceBuffer(4 * 4)
+    td.write(np.full(4, -7, np.int32))
+    arr = (C.c_void_p * len(hs))(*hs)
+    S = L.ds_hip_stack_create(arr, len(hs), lm.ptr, vocab, dev.ROUTE_CFG)
+    assert S, L.ds_hip_last_error()
+    try:
+        dev.check(L.ds_hip_stack_set_layer_kernels(S, 1 if kernels == 1 else 0), "kernels")
+        assert L.ds_hip_stack_bind(S, xd.ptr, H, 0, td.ptr, 4) == -1  # no rows
+        dev.check(L.ds_hip_stack_bind(S, xd.ptr, H, 3, td.ptr, 4), "bind")
+        assert L.ds_hip_stack_capacity(S) == 3 and L.ds_hip_stack_steps_left(S) == 3
+        dev.check(L.ds_hip_stack_run(S, 2), "run")
+        assert L.ds_hip_stack_run(S, 2) == -1  # 2 + 2 > 3 rows of input
+        assert b"capacity" in L.ds_hip_last_error()
+        ms = C.c_float(0)
+        assert L.ds_hip_time_stack(S, 2, C.byref(ms)) == -1
+        assert L.ds_hip_stack_run_eager(S, 2) == -1
+        assert L.ds_hip_profile_stack(S, 2, np.zeros(64, np.float32)) == -1
+        assert L.ds_hip_time_stack_each(S, 2, np.zeros(2, np.float32)) == -1
+        assert L.ds_hip_stack_steps_left(S) == 1
+        dev.check(L.ds_hip_sync(), "sync")
+        t = td.to_array(np.int32)
+        assert (t[:2] >= 0).all() and t[2] == -7 and t[3] == -7  # the refused calls launched nothing
+        dev.check(L.ds_hip_stack_run(S, 1), "run")
+        assert L.ds_hip_stack_run(S, 1) == -1
+        dev.check(L.ds_hip_stack_reset(S), "reset")
+        dev.check(L.ds_hip_stack_run(S, 3), "run after reset")
+        dev.check(L.ds_hip_sync(), "sync")
+        assert td.to_array(np.int32)[3] == -7
+        # stride 0: the token slots are the limit
+        dev.check(L.ds_hip_stack_bind(S, xd.ptr, 0, 1, td.ptr, 4), "bind")
+        assert L.ds_hip_stack_capacity(S) == 4
+        dev.check(L.ds_hip_stack_run(S, 4), "run")
+        assert L.ds_hip_stack_run(S, 1) == -1
+        dev.check(L.ds_hip_sync(), "sync")
+    finally:
+        L.ds_hip_stack_destroy(S)
+        for h in hs:
+            L.ds_hip_layer_destroy(h)
+
+
+@pytest.mark.parametrize("mode,kernels", [(1, 1), (1, 2), (0, 1)])
+def test_embedding_feed_autoregressive(dev, B, mode, kernels):
+    """Six fed-back steps: step 0 reads the bound row, every later step the embedding of the token the
+    step before chose; tokens and hidden states against the oracle fed the GPU's own tokens (so a
+    near tie cannot make the two runs diverge), and the tokens must equal the oracle's argmax of
+    the GPU's hidden state bit for bit. Graph and eager runs agree on the tokens."""
+    L = dev.load()
+    H, vocab, n = 256, 3000, 6
+    lays, hs, lm_w = small_stack(dev, B, 520)
+    emb = B.normal_bf16(vocab * H, 530, 0.5).reshape(vocab, H)
+    lm = dev.DeviceBuffer.from_array(lm_w)
+    ed = dev.DeviceBuffer.from_array(emb)
+    x0 = B.normal_f32(H, 5300)
+    xd = dev.DeviceBuffer.from_array(x0)
+    td = dev.DeviceBuffer(4 * n)
+    arr = (C.c_void_p * len(hs))(*hs)
+    S = L.ds_hip_stack_create(arr, len(hs), lm.ptr, vocab, mode)
+    assert S, L.ds_hip_last_error()
+    try:
+        dev.check(L.ds_hip_stack_set_layer_kernels(S, 1 if kernels == 1 else 0), "kernels")
+        dev.check(L.ds_hip_stack_set_embedding(S, ed.ptr, vocab), "embedding")
+        dev.check(L.ds_hip_stack_bind(S, xd.ptr, H, 1, td.ptr, n), "bind")
+        assert L.ds_hip_stack_capacity(S) == n  # one input row serves: later inputs come from the table
+        hid = []
+        for _ in range(n):
+            dev.check(L.ds_hip_stack_run(S, 1), "run")
+            hx = np.empty(H, np.float32)
+            dev.check(L.ds_hip_stack_hidden(S, hx), "hidden")
+            hid.append(hx)
+        toks = td.to_array(np.int32)
+        x = x0.copy()
+        for s in range(n):
+            _, rh = oracle_decode(B, lays, lm_w, vocab, x[None, :], mode)
+            err = rel_err(hid[s], rh[0])
+            want = B.oracle().or_argmax_bf16(hid[s], lm_w, H, vocab, 1, None)
+            print(f"embedding feed mode {mode} kernels {kernels} step {s}: token {toks[s]} (oracle on GPU state "
+                  f"{want}), hidden err {err:.2e}")
+            assert err < TOL and toks[s] == want
+            x = widen(emb[toks[s]])
+        dev.check(L.ds_hip_stack_reset(S), "reset")
+        dev.check(L.ds_hip_stack_run_eager(S, n), "eager")
+        assert np.array_equal(td.to_array(np.int32), toks)
+    finally:
+        L.ds_hip_stack_destroy(S)
+        for h in hs:
+            L.ds_hip_layer_destroy(h)
+
+
+def test_embedding_feed_with_sampling(dev, B):
+    """With the repetition penalty and n-gram ban after the argmax, the fed-back row is the embedding
+    of the token the rules chose (written after them)."""
+    L = dev.load()
+    H, vocab, n = 256, 3000, 8
+    lays, hs, lm_w = small_stack(dev, B, 540)
+    emb = B.normal_bf16(vocab * H, 550, 0.5).reshape(vocab, H)
+    lm = dev.DeviceBuffer.from_array(lm_w)
+    ed = dev.DeviceBuffer.from_array(emb)
+    x0 = B.normal_f32(H, 5500)
+    xd = dev.DeviceBuffer.from_array(x0)
+    td = dev.DeviceBuffer(4 * n)
+    arr = (C.c_void_p * len(hs))(*hs)
+    S = L.ds_hip_stack_create(arr, len(hs), lm.ptr, vocab, dev.ROUTE_CFG)
+    assert S, L.ds_hip_last_error()
+    try:
+        dev.check(L.ds_hip_stack_set_sampling(S, 1.3, 2, n), "sampling")
+        dev.check(L.ds_hip_stack_set_embedding(S, ed.ptr, vocab), "embedding")
+        dev.check(L.ds_hip_stack_bind(S, xd.ptr, 0, 1, td.ptr, n), "bind")
+        hid = []
+        for _ in range(n):
+            dev.check(L.ds_hip_stack_run(S, 1), "run")
+            hx = np.empty(H, np.float32)
+            dev.check(L.ds_hip_stack_hidden(S, hx), "hidden")
+            hid.append(hx)
+        toks = td.to_array(np.int32)
+        x = x0.copy()
+        for s in range(n):
+            _, rh = oracle_decode(B, lays, lm_w, vocab, x[None, :], dev.ROUTE_CFG)
+            assert rel_err(hid[s], rh[0]) < TOL
+            x = widen(emb[toks[s]])  # the next input is the embedding of the token the rules chose
+    finally:
+        L.ds_hip_stack_destroy(S)
+        for h in hs:
+            L.ds_hip_layer_destroy(h)
