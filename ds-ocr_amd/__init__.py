@@ -92,6 +92,7 @@ SIGNATURES = {
     "ds_hip_stack_bind": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, C.c_int]),
     "ds_hip_stack_set_embedding": (C.c_int, [vp, vp, C.c_int]),
     "ds_hip_stack_capacity": (C.c_int, [vp]),
+    "ds_hip_argmax_bf16_noalloc": (C.c_int, [vp, vp, vp, C.c_int, C.c_int]),
     "ds_hip_stack_steps_left": (C.c_int, [vp]),
     "ds_hip_stack_capacity_for": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int]),
     "ds_hip_steps_fit": (C.c_int, [C.c_int, C.c_int, C.c_int]),

@@ -38,6 +38,12 @@ hipError_t dsh_launch_split_swiglu(float *h, const float *gu, int inter, int bf1
 hipError_t dsh_launch_bf16_matvec_avx(const uint16_t *W, const float *x, const float *bias, float *y, int in_dim,
                                       int out_dim, int nthreads, hipStream_t s);
 int dsh_argmax_avx_blocks(int out_dim);
+/* Candidate keys in the file-scope device array of k_core.hip: DSH_STATIC_CAND entries (out_dim up
+ * to 64 * DSH_STATIC_CAND rows). _init looks its address up for the current device (once per
+ * device; 0 or -1); dsh_static_scratch returns the current device's address (NULL before _init). */
+#define DSH_STATIC_CAND 4096
+int dsh_static_scratch_init(void);
+unsigned long long *dsh_static_scratch(void);
 hipError_t dsh_launch_argmax_avx(const uint16_t *W, const float *x, unsigned long long *cand, float *logits,
                                  int in_dim, int out_dim, int nthreads, int *out_idx, float *out_val, hipStream_t s);
 hipError_t dsh_launch_argmax_avx_partial(const uint16_t *W, const float *x, unsigned long long *cand, float *logits,

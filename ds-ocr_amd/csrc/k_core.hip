@@ -835,3 +835,36 @@ hipError_t dsh_launch_topk(const float *scores, int n, int k, int mode, int *idx
 }
 
 }  // extern "C"
+
+// ============================================================================ static scratch
+// The candidate keys of the allocation-free argmax entry point live in this file-scope device
+// array (one (value, index) key per 64-row block of the matrix), so that entry point needs no
+// hipMalloc. Each GPU holds its own copy for the life of the process. In host code `scratch` is
+// only a stand-in for the symbol: its device address, per device, comes from hipGetSymbolAddress
+// at set-up (dsh_static_scratch_init, with that device current) and only that address is passed to
+// kernels. Every block of the argmax writes its key before the final kernel reads them, so nothing
+// has to start at zero; calls that overlap on one device share the array and race.
+static __device__ __align__(256) unsigned long long scratch[DSH_STATIC_CAND];
+
+#define DSH_MAX_DEVICES 64
+static unsigned long long *g_scratch_dev[DSH_MAX_DEVICES];
+
+extern "C" {
+
+int dsh_static_scratch_init(void) {
+  int d = -1;
+  if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= DSH_MAX_DEVICES) return -1;
+  if (g_scratch_dev[d]) return 0;
+  void *p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return -1;
+  g_scratch_dev[d] = (unsigned long long *)p;
+  return 0;
+}
+
+unsigned long long *dsh_static_scratch(void) {
+  int d = -1;
+  if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= DSH_MAX_DEVICES) return nullptr;
+  return g_scratch_dev[d];
+}
+
+}  // extern "C"

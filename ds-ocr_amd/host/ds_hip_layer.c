@@ -1609,6 +1609,20 @@ int ds_hip_argmax_bf16(int *idx_dev, const float *x_dev, const uint16_t *W_dev, 
   return 0;
 }
 
+int ds_hip_argmax_bf16_noalloc(int *idx_dev, const float *x_dev, const uint16_t *W_dev, int in_dim, int out_dim) {
+  if (!dsr_ready()) return dsr_failf("ds_hip_argmax_bf16_noalloc: call ds_hip_init first");
+  if (!idx_dev || !x_dev || !W_dev || in_dim <= 0 || out_dim <= 0)
+    return dsr_failf("ds_hip_argmax_bf16_noalloc: invalid arguments");
+  if (dsh_argmax_avx_blocks(out_dim) > DSH_STATIC_CAND)
+    return dsr_failf("ds_hip_argmax_bf16_noalloc: out_dim %d exceeds the maximum of %d rows", out_dim,
+                     64 * DSH_STATIC_CAND);
+  unsigned long long *cand = dsh_static_scratch();
+  if (!cand) return dsr_failf("ds_hip_argmax_bf16_noalloc: no static scratch on this device");
+  DSR_TRY(dsh_launch_argmax_avx(W_dev, x_dev, cand, NULL, in_dim, out_dim, dsr_threads(), idx_dev, NULL, dsr_stream),
+          "argmax");
+  return 0;
+}
+
 int ds_hip_fill_normal_bf16(uint16_t *dst_dev, size_t n, uint64_t seed, float std_) {
   if (dsr_init()) return -1;
   DSR_TRY(dsh_launch_fill_normal_bf16(dst_dev, n, seed, std_, dsr_stream), "fill normal");

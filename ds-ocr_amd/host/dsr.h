@@ -13,6 +13,8 @@ extern hipStream_t dsr_stream;
 
 /* Initialises device 0 and the library stream once. Returns 0, or -1 (message printed). */
 int dsr_init(void);
+/* 1 once dsr_init has succeeded (no side effects). */
+int dsr_ready(void);
 /* Records and prints a failure; returns -1. */
 int dsr_fail(const char *what, hipError_t e);
 int dsr_failf(const char *fmt, ...);

@@ -50,9 +50,16 @@ int dsr_init(void) {
     g_init = -1;
     return dsr_fail("HIP init", e);
   }
+  /* the device address of the allocation-free entry points' scratch array (device 0 is current) */
+  if (dsh_static_scratch_init()) {
+    g_init = -1;
+    return dsr_failf("HIP init: the device address of the static scratch array is not available");
+  }
   g_init = 1;
   return 0;
 }
+
+int dsr_ready(void) { return g_init == 1; }
 
 int ds_hip_init(void) { return dsr_init(); }
 

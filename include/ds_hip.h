@@ -49,6 +49,13 @@ int ds_hip_int8_matvec(float *y_dev, const float *x_dev, const int8_t *q_dev, co
 /* Argmax of W x (bf16 W [out_dim, in_dim]) in the reference's order for ds_get_threads() threads;
  * writes the index to *idx_dev. */
 int ds_hip_argmax_bf16(int *idx_dev, const float *x_dev, const uint16_t *W_dev, int in_dim, int out_dim);
+/* ds_hip_argmax_bf16 without any allocation: no counterpart in the reference; for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The per-block candidate keys live in a static device array of the library
+ * (262144 rows at most: out_dim beyond that is refused with an error); ds_hip_init must have been
+ * called. Same result as ds_hip_argmax_bf16. Every call on a device shares that device's array, so
+ * calls that overlap on one device (several host threads or streams) race. */
+int ds_hip_argmax_bf16_noalloc(int *idx_dev, const float *x_dev, const uint16_t *W_dev, int in_dim, int out_dim);
 
 /* ---------------- device-resident MoE layer ---------------- */
 enum { DS_HIP_ROUTE_DECODE = 0, DS_HIP_ROUTE_CFG = 1 };
