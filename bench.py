@@ -137,22 +137,23 @@ def cpu_model():
     return "unknown"
 
 
-def cpu_baseline(dev, handles, rfs, rbs, lm, xs_host, gpu_tokens, route, budget_s):
+def ref_variant():
+    flags = open("/proc/cpuinfo").read()
+    return "v4" if (" avx512f " in flags and " avx512bw " in flags) else "v3"
+
+
+def cpu_baseline(lays, lm_w, xs_host, gpu_tokens, route, budget_s, dropin=None):
     """The reference CPU path (ds-ocr's own C, oracle/_ref) on this host: moe_forward's INT8 branch
     for 11 layers + ds_argmax_matvec_bf16 per step. Rows: the reference's own thread count
-    (min(cores, 16): ds_kernels.c:123, :518-519 clamp it) and 1 thread; each row runs a bounded
-    sample of the same steps (about budget_s of CPU time)."""
+    (min(cores, 16): ds_kernels.c:123, :518-519 clamp it) and 1 thread in the bench's routing, and
+    the reference thread count in DECODE routing (moe_forward's own router) beside the drop-in leg;
+    each row runs a bounded sample of the same steps (about budget_s of CPU time)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import bindings as B
-    flags = open("/proc/cpuinfo").read()
-    variant = "v4" if (" avx512f " in flags and " avx512bw " in flags) else "v3"
+    variant = ref_variant()
     R = B.ref(variant)
     if R is None:
         return None
-    rf_host = [rf.to_array(np.float32) for rf in rfs]
-    rb_host = [rb.to_array(np.uint16) for rb in rbs]
-    lays = host_layers(dev, handles, rf_host, rb_host)
-    lm_w = lm.to_array(np.uint16)
     bufs = [lay.ref_layer(variant) for lay in lays]
     arr = C.create_string_buffer(len(bufs) * R.ref_layer_sizeof())
     for i, b in enumerate(bufs):
@@ -161,15 +162,23 @@ def cpu_baseline(dev, handles, rfs, rbs, lm, xs_host, gpu_tokens, route, budget_
     affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else ncpu
     clamp = min(16, affinity)
     rows = []
-    for threads in ([clamp, 1] if clamp > 1 else [1]):
+    plan = [(clamp, route)] + ([(1, route)] if clamp > 1 else [])
+    if dropin is not None:
+        plan.append((clamp, 0))
+    for threads, rt in plan:
         R.ds_set_threads(threads)
         toks = np.zeros(len(xs_host), np.int32)
-        t1 = R.ref_decode_steps(C.addressof(arr), LAYERS, lm_w, VOCAB, xs_host, 1, route, toks)
+        t1 = R.ref_decode_steps(C.addressof(arr), LAYERS, lm_w, VOCAB, xs_host, 1, rt, toks)
         n = int(max(1, min(len(xs_host), budget_s / max(t1, 1e-6))))
-        secs = R.ref_decode_steps(C.addressof(arr), LAYERS, lm_w, VOCAB, xs_host, n, route, toks)
-        rows.append({"threads": threads, "value": round(n / secs, 3), "unit": "tok/s",
-                     "ms_per_step": round(1000 * secs / n, 3), "steps": n,
-                     "tokens_equal_to_gpu": int(np.sum(toks[:n] == gpu_tokens[:n]))})
+        secs = R.ref_decode_steps(C.addressof(arr), LAYERS, lm_w, VOCAB, xs_host, n, rt, toks)
+        row = {"threads": threads, "route": "cfg" if rt == 1 else "decode", "value": round(n / secs, 3),
+               "unit": "tok/s", "ms_per_step": round(1000 * secs / n, 3), "steps": n}
+        if rt == route:
+            row["tokens_equal_to_gpu"] = int(np.sum(toks[:n] == gpu_tokens[:n]))
+        if dropin is not None and rt == 0:
+            m = min(n, len(dropin["tokens"]))
+            dropin["tokens_equal_to_reference_decode_route"] = f"{int(np.sum(toks[:m] == dropin['tokens'][:m]))}/{m}"
+        rows.append(row)
     main = rows[0]
     return {"value": main["value"], "unit": "tok/s", "cores": main["threads"], "kind": "reference",
             "sample": f"{main['steps']} decode steps of the same 11-layer + LM-head workload (the timed region's "
@@ -182,6 +191,55 @@ def cpu_baseline(dev, handles, rfs, rbs, lm, xs_host, gpu_tokens, route, budget_
             "unclamped_row": ("not run: the reference's thread pool clamps to 16 threads (ds_kernels.c:123, "
                               f":518-519) and this process may use {affinity} CPUs" if affinity > 16 else
                               f"equal to the clamped row: this process may use {affinity} CPUs")}
+
+
+class DropinLayer(C.Structure):
+    """dropin_layer_t of ds-ocr_amd/examples/moe_forward_dropin.c."""
+    _fields_ = [("hidden", C.c_int), ("inter", C.c_int), ("n_experts", C.c_int), ("top_k", C.c_int),
+                ("shared_inter", C.c_int), ("router_bf16", C.c_void_p), ("gate_up", C.c_void_p),
+                ("down", C.c_void_p), ("shared_gate_up", C.c_void_p), ("shared_down", C.c_void_p)]
+
+
+def dropin_leg(dev, lays, lm_w, xs_host, n_steps):
+    """The per-function drop-in path: the reference's decode step (moe_forward's calls for 11 layers,
+    then ds_argmax_matvec_bf16) through the C API with host pointers, as an unchanged reference
+    caller runs it (ds-ocr_amd/examples/moe_forward_dropin.c); weights registered once first."""
+    ex = C.CDLL(os.path.join(ROOT, "ds-ocr_amd", "examples", "libdropin_example.so"))
+    ex.dropin_register.restype = C.c_int
+    ex.dropin_register.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int]
+    ex.dropin_decode_steps.restype = C.c_double
+    ex.dropin_decode_steps.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p]
+    keep = []
+    arr = (DropinLayer * len(lays))()
+    for l, lay in enumerate(lays):
+        gu = (dev.Int4Block * lay.n_experts)(*[dev.block_from_arrays(b.q, b.scale, b.offset) for b in lay.gu])
+        dn = (dev.Int4Block * lay.n_experts)(*[dev.block_from_arrays(b.q, b.scale, b.offset) for b in lay.dn])
+        sgu = dev.block_from_arrays(lay.sgu.q, lay.sgu.scale, lay.sgu.offset)
+        sdn = dev.block_from_arrays(lay.sdn.q, lay.sdn.scale, lay.sdn.offset)
+        keep += [gu, dn, sgu, sdn]
+        arr[l] = DropinLayer(lay.hidden, lay.inter, lay.n_experts, lay.top_k, lay.shared_inter,
+                             lay.router_bf16.ctypes.data, C.addressof(gu), C.addressof(dn), C.addressof(sgu),
+                             C.addressof(sdn))
+    t0 = time.perf_counter()
+    if ex.dropin_register(C.addressof(arr), len(lays), lm_w.ctypes.data, VOCAB):
+        raise RuntimeError("drop-in registration: " + dev.load().ds_hip_last_error().decode())
+    reg_s = time.perf_counter() - t0
+    n = min(n_steps, len(xs_host))
+    toks = np.zeros(len(xs_host), np.int32)
+    ex.dropin_decode_steps(C.addressof(arr), len(lays), lm_w.ctypes.data, VOCAB, xs_host.ctypes.data, 1,
+                           toks.ctypes.data)  # warm-up step
+    secs = ex.dropin_decode_steps(C.addressof(arr), len(lays), lm_w.ctypes.data, VOCAB, xs_host.ctypes.data, n,
+                                  toks.ctypes.data)
+    if secs <= 0:
+        raise RuntimeError("drop-in leg failed")
+    return {"value": round(n / secs, 3), "unit": "tok/s", "ms_per_step": round(1000 * secs / n, 3), "steps": n,
+            "route": "decode (moe_forward's bf16 router, host softmax/top-k as the reference caller does it)",
+            "register_s": round(reg_s, 2), "tokens": toks[:n],
+            "calls_per_step": LAYERS * (1 + K + 1 + 1 + 2) + 1,
+            "method": "host wall clock around n steps of ds-ocr_amd/examples/moe_forward_dropin.c: per layer "
+                      "ds_moe_router_bf16, 6 x ds_expert_forward_fused_int4, ds_expert_combine, the shared "
+                      "expert, 2 x ds_vec_add; then ds_argmax_matvec_bf16; every call synchronous with host "
+                      "activations (the drop-in boundary)"}
 
 
 def pct(v, q):
@@ -228,6 +286,8 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-dropin", action="store_true", help="skip the per-function drop-in leg")
+    ap.add_argument("--dropin-steps", type=int, default=20)
     ap.add_argument("--prefill-tokens", type=int, default=662, help="config-3 prefill measurement (0: skip)")
     ap.add_argument("--prefill-reps", type=int, default=100)
     ap.add_argument("--dense-layer", action="store_true",
@@ -458,9 +518,24 @@ def main():
 
     xs_host = xs.to_array(np.float32).reshape(rows, H)[args.warmup:args.warmup + args.steps].copy()
     cpu = None
+    dropin = None
     if not args.no_cpu and not dense and not sampling and not full:  # the reference CPU leg: MoE layers + argmax head
         try:
-            cpu = cpu_baseline(dev, handles, rfs, rbs, lm, xs_host, gpu_tokens, route, args.cpu_seconds)
+            lays = host_layers(dev, handles, [rf.to_array(np.float32) for rf in rfs],
+                               [rb.to_array(np.uint16) for rb in rbs])
+            lm_w = lm.to_array(np.uint16)
+            if not args.no_dropin:
+                try:
+                    dropin = dropin_leg(dev, lays, lm_w, xs_host, args.dropin_steps)
+                except Exception as exc:  # report, never hide
+                    dropin = {"error": repr(exc)}
+            cpu = cpu_baseline(lays, lm_w, xs_host, gpu_tokens, route, args.cpu_seconds,
+                               dropin if dropin and "tokens" in dropin else None)
+            if dropin and "tokens" in dropin:
+                dropin.pop("tokens")
+                ref_dec = [r for r in cpu["rows"] if r["route"] == "decode"] if cpu else []
+                if ref_dec:
+                    dropin["vs_cpu_baseline_decode_route"] = round(dropin["value"] / ref_dec[0]["value"], 3)
         except Exception as exc:  # report, never hide
             cpu = {"error": repr(exc)}
     elif not args.no_cpu:
@@ -515,6 +590,7 @@ def main():
         "prefill": prefill,
         "decoder_step": decoder,
         "cpu_baseline": cpu,
+        "dropin_per_function": dropin,
     }
     print(json.dumps(line))
 

@@ -172,11 +172,15 @@ void ds_expert_forward_fused(float *out, const float *x, const uint16_t *gate_up
 /* ds_kernels.c:981-1011 (non-NEON branch). */
 float ds_bf16_dot_row(const float *x, const uint16_t *W_bf16, int in_dim, int tok_id) {
   if (!x || !W_bf16 || in_dim <= 0 || tok_id < 0) return 0.0f;
-  /* Only the selected row is uploaded; the key is the row's own address. */
-  const uint16_t *row = W_bf16 + (size_t)tok_id * in_dim;
-  const uint16_t *Wd = (const uint16_t *)dsr_weight_device(row, (size_t)in_dim * 2);
+  if (dsr_init()) return 0.0f;
+  /* The reference's callers pass the LM head after the argmax has registered it
+   * (ds_moe_decoder.c:1041-1043): read the row from that device copy; otherwise stage this one row. */
+  const size_t row_bytes = (size_t)in_dim * 2;
+  const uint16_t *head = (const uint16_t *)dsr_weight_lookup(W_bf16, row_bytes * ((size_t)tok_id + 1));
+  const uint16_t *Wd = head ? head + (size_t)tok_id * in_dim : (const uint16_t *)dsr_scratch(DSR_SLOT_D, row_bytes);
   float *xd = (float *)dsr_scratch(DSR_SLOT_X, F4(in_dim)), *od = (float *)dsr_scratch(DSR_SLOT_Y, F4(1));
   if (!Wd || !xd || !od || dsr_h2d(xd, x, F4(in_dim))) return 0.0f;
+  if (!head && dsr_h2d((void *)Wd, W_bf16 + (size_t)tok_id * in_dim, row_bytes)) return 0.0f;
   hipError_t e = dsh_launch_bf16_dot_row(Wd, xd, in_dim, 0, od, dsr_stream);
   if (e != hipSuccess) {
     dsr_fail("ds_bf16_dot_row", e);
@@ -194,10 +198,22 @@ int ds_argmax_matvec_bf16(const float *x, const uint16_t *W_bf16, int in_dim, in
 
 /* ds_kernels.c:1020-1099. The argmax itself, and the exclusion fallbacks of both the single-thread
  * branch (rescan in 8192-row chunks, a chunk whose best is excluded is skipped) and the threaded
- * branch (best non-excluded per-thread winner; the excluded best if none) run on the device. */
+ * branch (best non-excluded per-thread winner; the excluded best if none) run on the device.
+ * The reference's CPU path always returns an index its caller may use as a row
+ * (ds_moe_decoder.c:1041-1043 reads that row at once); on a device error (reported on stderr and in
+ * ds_hip_last_error) or invalid arguments this returns 0, never an index outside [0, out_dim). */
+static int argmax_excluding(const float *x, const uint16_t *W_bf16, int in_dim, int out_dim, const int *exclude_ids,
+                            int n_exclude);
+
 int ds_argmax_matvec_bf16_excluding(const float *x, const uint16_t *W_bf16, int in_dim, int out_dim,
                                     const int *exclude_ids, int n_exclude) {
-  if (!x || !W_bf16 || in_dim <= 0 || out_dim <= 0) return -1;
+  int idx = argmax_excluding(x, W_bf16, in_dim, out_dim, exclude_ids, n_exclude);
+  return idx >= 0 && idx < out_dim ? idx : 0;
+}
+
+static int argmax_excluding(const float *x, const uint16_t *W_bf16, int in_dim, int out_dim, const int *exclude_ids,
+                            int n_exclude) {
+  if (!x || !W_bf16 || in_dim <= 0 || out_dim <= 0) return dsr_failf("ds_argmax_matvec_bf16: invalid arguments");
   if (n_exclude < 0 || (n_exclude > 0 && !exclude_ids)) n_exclude = 0;
   const uint16_t *Wd = (const uint16_t *)dsr_weight_device(W_bf16, (size_t)out_dim * in_dim * 2);
   float *xd = (float *)dsr_scratch(DSR_SLOT_X, F4(in_dim));

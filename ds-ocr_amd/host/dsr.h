@@ -32,7 +32,8 @@ int dsr_h2d(void *dst, const void *src, size_t n);
 int dsr_d2h(void *dst, const void *src, size_t n); /* synchronises the stream */
 
 /* Device copy of an INT8 block, uploaded on first use (keyed by the qweight host pointer plus a
- * sampled fingerprint of the host arrays, so a reused host address is detected). */
+ * sampled fingerprint of the host arrays, so a new block at a reused address is detected; in-place
+ * edits need ds_hip_weights_changed). */
 typedef struct {
   int8_t *q;
   float *scale;
@@ -48,6 +49,8 @@ void dsr_block_forget(const void *qweight);
 
 /* Device copy of a host weight array (bf16 / f32), uploaded on first use, same keying. */
 const void *dsr_weight_device(const void *host, size_t bytes);
+/* The device copy of a registered weight array of at least `bytes`, or NULL (no upload). */
+const void *dsr_weight_lookup(const void *host, size_t bytes);
 
 /* Emulated reference CPU thread count (ds_set_threads). */
 int dsr_threads(void);

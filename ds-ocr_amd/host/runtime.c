@@ -109,65 +109,21 @@ static uint64_t fnv(uint64_t h, const void *p, size_t n) {
   return h;
 }
 
-/* Content hash of every byte: four lanes of the xxHash64 round (acc = rotl(acc + w*P2, 31) * P1)
- * over 32-byte stripes, the tail through FNV-1a. Any change of a cached host array is seen, also
- * when a new array reuses a freed one's address; arrays of 32 MiB and more are hashed in parallel
- * slices. */
-#define XXP1 11400714785092567791ull
-#define XXP2 14029467366897019727ull
-static uint64_t rotl64(uint64_t v, int r) { return (v << r) | (v >> (64 - r)); }
-
-static uint64_t hash_slice(const unsigned char *b, size_t n, uint64_t seed) {
-  uint64_t v[4] = {seed + XXP1 + XXP2, seed + XXP2, seed, seed - XXP1};
-  size_t i = 0;
-  for (; i + 32 <= n; i += 32) {
-    for (int l = 0; l < 4; l++) {
-      uint64_t w;
-      memcpy(&w, b + i + 8 * l, 8);
-      v[l] = rotl64(v[l] + w * XXP2, 31) * XXP1;
-    }
-  }
-  uint64_t h = rotl64(v[0], 1) + rotl64(v[1], 7) + rotl64(v[2], 12) + rotl64(v[3], 18);
-  return fnv(h ^ (uint64_t)n, b + i, n - i);
-}
-
-typedef struct {
-  const unsigned char *b;
-  size_t n;
-  uint64_t h;
-} slice_t;
-
-static void *hash_worker(void *arg) {
-  slice_t *s = (slice_t *)arg;
-  s->h = hash_slice(s->b, s->n, 0x9E3779B97F4A7C15ull);
-  return NULL;
-}
+/* Weights are registered once: a host array is keyed by its address and size, like the reference's
+ * read-only mmap'd weights and INT8 blocks that are never rewritten (ds_ocr.c:611-622; the Metal
+ * backend registers expert blocks the same way, ds_metal.m:244-258). To notice a new array placed at
+ * a freed one's address, each key also keeps a sampled fingerprint: 16 windows of 256 bytes spread
+ * evenly over the array (the whole array when it is at most 4 KiB), about 4 KiB read per call
+ * whatever the size. A caller that edits registered weights in place calls ds_hip_weights_changed. */
+#define FP_WINDOWS 16
+#define FP_WINDOW 256
 
 static uint64_t fingerprint(const void *p, size_t n) {
   const unsigned char *b = (const unsigned char *)p;
   uint64_t h = fnv(1469598103934665603ull, &n, sizeof n);
-  enum { MAXS = 8 };
-  long ncpu = sysconf(_SC_NPROCESSORS_ONLN);
-  int ns = n >= ((size_t)32 << 20) ? (int)(ncpu < MAXS ? (ncpu < 1 ? 1 : ncpu) : MAXS) : 1;
-  slice_t sl[MAXS];
-  pthread_t th[MAXS];
-  int started[MAXS] = {0};
-  size_t per = ((n / (size_t)ns) + 31) & ~(size_t)31;
-  for (int i = 0; i < ns; i++) {
-    size_t s0 = per * (size_t)i < n ? per * (size_t)i : n;
-    size_t s1 = i == ns - 1 ? n : (per * (size_t)(i + 1) < n ? per * (size_t)(i + 1) : n);
-    sl[i].b = b + s0;
-    sl[i].n = s1 - s0;
-    if (i > 0 && pthread_create(&th[i], NULL, hash_worker, &sl[i]) == 0) started[i] = 1;
-  }
-  hash_worker(&sl[0]);
-  for (int i = 1; i < ns; i++) {
-    if (started[i])
-      pthread_join(th[i], NULL);
-    else
-      hash_worker(&sl[i]);
-  }
-  for (int i = 0; i < ns; i++) h = fnv(h, &sl[i].h, sizeof sl[i].h);
+  if (n <= (size_t)FP_WINDOWS * FP_WINDOW) return fnv(h, b, n);
+  const size_t step = (n - FP_WINDOW) / (FP_WINDOWS - 1);
+  for (int i = 0; i < FP_WINDOWS; i++) h = fnv(h, b + (size_t)i * step, FP_WINDOW);
   return h;
 }
 
@@ -300,6 +256,37 @@ void dsr_block_forget(const void *qweight) {
   if (!qweight) return;
   entry_t *e = find(qweight, 1);
   if (e) drop(e);
+}
+
+int ds_hip_register_block(const ds_int4_block_t *block) {
+  if (!block || !block->qweight || !block->scale || !block->offset || block->out_dim <= 0 || block->in_dim <= 0)
+    return dsr_failf("ds_hip_register_block: invalid block");
+  dsr_dblock_t db;
+  return dsr_block_device(block, &db);
+}
+
+int ds_hip_register_weights(const void *host, size_t bytes) {
+  if (!host || !bytes) return dsr_failf("ds_hip_register_weights: invalid arguments");
+  return dsr_weight_device(host, bytes) ? 0 : -1;
+}
+
+int ds_hip_weights_changed(const void *host_ptr) {
+  if (!host_ptr) return dsr_failf("ds_hip_weights_changed: NULL pointer");
+  if (g_init != 1) return 0; /* nothing registered yet */
+  int dropped = 0;
+  for (int is_block = 0; is_block < 2; is_block++) {
+    entry_t *e = find(host_ptr, is_block);
+    if (e) {
+      drop(e);
+      dropped++;
+    }
+  }
+  return dropped;
+}
+
+const void *dsr_weight_lookup(const void *host, size_t bytes) {
+  entry_t *e = find(host, 0);
+  return e && e->bytes >= bytes ? e->dev : NULL;
 }
 
 const void *dsr_weight_device(const void *host, size_t bytes) {

@@ -41,6 +41,18 @@ int ds_hip_sync(void);
 int ds_hip_fill_normal_bf16(uint16_t *dst_dev, size_t n, uint64_t seed, float std_);
 int ds_hip_fill_normal_f32(float *dst_dev, size_t n, uint64_t seed, float mean, float std_);
 
+/* The per-function API (ds_quantize.h, ds_kernels.h) keeps one device copy per host weight array and
+ * INT8 block, registered on first use and keyed by its address (plus a sampled fingerprint that
+ * catches a new array at a freed one's address). Weights edited in place after they were used must
+ * be announced: host_ptr is the array (or a block's qweight); its device copy is dropped and
+ * uploaded again at the next use. Returns the number of copies dropped (0 if none), -1 on error.
+ * No counterpart in the reference, whose weights are read-only mmaps (ds_ocr.c:611-622). */
+int ds_hip_weights_changed(const void *host_ptr);
+/* Registers (uploads) a block or a weight array now rather than at its first use, e.g. at load time
+ * so the first tokens do not pay for the uploads. 0 or -1. */
+int ds_hip_register_block(const ds_int4_block_t *block);
+int ds_hip_register_weights(const void *host, size_t bytes);
+
 /* ---------------- device-pointer kernels ---------------- */
 int ds_hip_quantize_bf16(int8_t *q_dev, float *scale_dev, float *offset_dev, const uint16_t *W_dev, int out_dim,
                          int in_dim);

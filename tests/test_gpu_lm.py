@@ -95,8 +95,9 @@ def test_lm_argmax_config5_head(dev, B):
 
 
 def test_weights_changed_in_place_are_seen(dev, B):
-    """The host API keeps device copies of host weights; editing one row of the same array (same
-    address, same size) between calls must still change the answer."""
+    """The host API registers host weights once (keyed by address); an in-place edit of one row is
+    announced with ds_hip_weights_changed and must then change the answer; a new array at another
+    address is uploaded on its own."""
     L = dev.load()
     in_dim, vocab = 128, 4096
     W, x = planted(B, in_dim, vocab, 77, "random")
@@ -104,4 +105,22 @@ def test_weights_changed_in_place_are_seen(dev, B):
     assert first == B.oracle().or_argmax_bf16(x, W, in_dim, vocab, 1, None)
     target = vocab - 5 if first != vocab - 5 else 7
     W[target] = B.f32_to_bf16_rne(np.sign(x) * 0.5)
+    assert L.ds_hip_weights_changed(W.ctypes.data) == 1
     assert L.ds_argmax_matvec_bf16(x, W, in_dim, vocab) == target
+    assert L.ds_hip_weights_changed(W.ctypes.data) == 1
+    assert L.ds_hip_weights_changed(W.ctypes.data) == 0  # nothing registered any more
+    W2 = W.copy()
+    W2[target] = W2[first]
+    assert L.ds_argmax_matvec_bf16(x, W2, in_dim, vocab) == min(first, target)
+    # ds_bf16_dot_row reads the row from the registered head: equal to the oracle's sequential chain
+    v = L.ds_bf16_dot_row(x, W2, in_dim, target)
+    assert np.float32(v).view(np.uint32) == np.float32(B.oracle().or_bf16_dot_row(x, W2, in_dim, target)).view(np.uint32)
+
+
+def test_argmax_never_returns_an_index_outside_the_rows(dev, B):
+    """Invalid arguments (or a device error) give 0, a row the reference's caller may read
+    (ds_moe_decoder.c:1041-1043), never -1."""
+    L = dev.load()
+    W, x = planted(B, 128, 256, 78, "random")
+    assert L.ds_argmax_matvec_bf16(x, W, 0, 256) == 0
+    assert L.ds_argmax_matvec_bf16(x, W, 128, 0) == 0
