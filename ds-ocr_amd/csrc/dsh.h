@@ -26,6 +26,12 @@ __device__ __forceinline__ float dsh_fast_expf(float x) {
   return __uint_as_float(i);
 }
 
+// expf rounded correctly (exp in double precision, then one rounding to float). The reference's
+// ds_moe_top_k calls the host's expf (ds_kernels.c:233), glibc 2.35's on the benchmark hosts; over
+// every float in [-104, 0] (the softmax's arguments, x - max) that agrees with the correctly rounded
+// value except on 97,052 of 1,120,927,745 arguments (8.7e-5), where glibc is 1 ulp off.
+__device__ __forceinline__ float dsh_expf_cr(float x) { return (float)exp((double)x); }
+
 // ds_swiglu_direct element (ds_kernels.c:1771): (g / (1 + fe(-g))) * u. Division is IEEE
 // correctly rounded (hipcc default), matching the x86 divss.
 __device__ __forceinline__ float dsh_swiglu(float g, float u) { return (g / (1.0f + dsh_fast_expf(-g))) * u; }
@@ -113,6 +119,47 @@ __device__ __forceinline__ float dsh_dot16_u8(u32x4 w, const float *x, float acc
 
 __device__ __forceinline__ u32x4 dsh_load_nt(const void *p) {
   return __builtin_nontemporal_load((const u32x4 *)p);
+}
+
+// The reference's INT8 row loop in its own order (int8_matvec_generic, ds_quantize.c:163-166, which
+// GCC keeps scalar and contracts): dot = fma(u_j, x_j, dot) for j = 0, 1, ... with the exact code
+// u = q + 128, and with XS also xs += x_j in the same loop. One lane runs one row, so the result
+// is bit-identical to the reference's. row: 16-byte aligned, n % 16 == 0; x in LDS (the lanes of a
+// wave read the same x_j at once: a broadcast). Loads run PF 16-byte chunks ahead in registers.
+template <bool XS>
+__device__ __forceinline__ float dsh_row_chain(const int8_t *row, const float *x, int n, float &xs) {
+  constexpr int PF = 16;
+  const int C = n >> 4;
+  u32x4 buf[PF];
+#pragma unroll
+  for (int j = 0; j < PF; j++) buf[j] = j < C ? dsh_load_nt(row + 16 * j) : u32x4{0u, 0u, 0u, 0u};
+  float dot = 0.0f;
+  for (int g = 0; g < C; g += PF) {
+    u32x4 cur[PF];
+#pragma unroll
+    for (int j = 0; j < PF; j++) cur[j] = buf[j];
+#pragma unroll
+    for (int j = 0; j < PF; j++)
+      if (g + PF + j < C) buf[j] = dsh_load_nt(row + 16 * (g + PF + j));
+#pragma unroll
+    for (int j = 0; j < PF; j++) {
+      if (g + j < C) {
+        const float *xc = x + 16 * (g + j);
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+          float u[4];
+          dsh_u8x4_to_f32(cur[j][d], u[0], u[1], u[2], u[3]);
+          const f32x4 xv = *(const f32x4 *)(xc + 4 * d);
+#pragma unroll
+          for (int c = 0; c < 4; c++) {
+            dot = __builtin_fmaf(u[c], xv[c], dot);
+            if (XS) xs += xv[c];
+          }
+        }
+      }
+    }
+  }
+  return dot;
 }
 
 __device__ __forceinline__ f32x4 dsh_load_f4(const float *p) { return *(const f32x4 *)p; }

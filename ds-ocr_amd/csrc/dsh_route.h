@@ -22,7 +22,8 @@ struct route_scratch {
 // equal values give two lanes the same count, which that read-back detects, and then every lane
 // recounts with the index tie-break (values above its own, plus equal values at lower indices).
 // CFG (ds_moe_top_k): top-K on the raw scores, then softmax over the K chosen in selection order
-// (expf, max first, sequential sum); slots past the selectable count get expert 0 and weight 0.
+// (correctly rounded expf, max first, sequential sum); slots past the selectable count get expert 0
+// and weight 0.
 // DECODE (ds_moe_decoder.c:145-183): fast-exp softmax over all experts (max, sequential sum in
 // expert order, 1/sum), top-K on the probabilities, weights = those probabilities; empty slots get
 // expert -1 and weight -1e30.
@@ -89,7 +90,7 @@ __device__ __forceinline__ void route_select(int E, int K, int mode, int *s_idx,
   if (mode == DSH_ROUTE_CFG) {
     // the first selected is the largest; lanes past ns hold +0, which leaves the sum as is
     const float mx = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(my_val)));
-    const float ev = mine ? expf(my_val - mx) : 0.0f;
+    const float ev = mine ? dsh_expf_cr(my_val - mx) : 0.0f;
     float sum = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j));

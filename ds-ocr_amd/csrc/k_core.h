@@ -27,6 +27,9 @@ hipError_t dsh_launch_fill_normal_bf16(uint16_t *dst, size_t n, uint64_t seed, f
 hipError_t dsh_launch_fill_normal_f32(float *dst, size_t n, uint64_t seed, float mean, float std_, hipStream_t s);
 hipError_t dsh_launch_dequantize(const int8_t *q, const float *scale, const float *offset, float *out, int out_dim,
                                  int in_dim, hipStream_t s);
+/* The reference's own per-row order (bit-identical to int8_matvec_generic); in_dim <= 16384. */
+hipError_t dsh_launch_int8_matvec_exact(const int8_t *q, const float *scale, const float *offset, const float *x,
+                                        float *y, int in_dim, int row_start, int nrows, hipStream_t s);
 hipError_t dsh_launch_int8_matvec(const int8_t *q, const float *scale, const float *offset, const float *x, float *y,
                                   int in_dim, int row_start, int nrows, hipStream_t s);
 hipError_t dsh_launch_swiglu(float *out, const float *g, const float *u, size_t n, hipStream_t s);
@@ -79,6 +82,7 @@ typedef struct {
   int *idx;      /* [K] selected experts */
   float *w;      /* [K] routing weights */
   float *h;      /* [K*I + SI] SwiGLU outputs (routed slots, then shared) */
+  float *eo;     /* [K+1][H] expert outputs: routed slots, then shared (bf16 simulation) */
 } dsh_layer_work_t;
 
 /* ---- prefill MoE block (k_prefill.hip) ---- */
@@ -163,6 +167,9 @@ hipError_t dsh_launch_dec_scores_bf16(const uint16_t *Wr, const float *x_in, con
 /* ncopies == 8: x = Σ of the 8 copies [8][H] at x_in (in copy order; step must be NULL). */
 hipError_t dsh_launch_dec_scores_bf16_copies(const uint16_t *Wr, const float *x_in, const int *step, int stride,
                                              int ncopies, int H, int E, int nthreads, float *partials, hipStream_t s);
+/* CFG router scores of x in ds_linear's exact order (no BLAS), written as one partial (np = 1). */
+hipError_t dsh_launch_dec_scores_f32_exact(const float *WrT, const float *x_in, const int *step, int stride, int H,
+                                          int E, float *partials, hipStream_t s);
 hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const int *step, int stride,
                                   const float *partials, int np, int route_mode, int bf16sim,
                                   const dsh_layer_work_t *wk, hipStream_t s);

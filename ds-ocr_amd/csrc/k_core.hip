@@ -148,6 +148,37 @@ __global__ void __launch_bounds__(256) k_int8_matvec_any(const int8_t *__restric
   if (lane == 0) y[rr] = __builtin_fmaf(scale[r], dot, offset[r] * xs);
 }
 
+// The reference's per-row order exactly (int8_matvec_generic, ds_quantize.c:154-170): one lane per
+// row runs the row's two sequential chains, dot = fma(u_j, x_j, dot) and xs += x_j, then
+// y = fma(scale, dot, offset * xs) (GCC's contraction of the epilogue), so y is bit-identical to the
+// reference's. x is staged in LDS (dynamic, in_dim floats). ALIGNED: in_dim % 16 == 0 and q 16-byte
+// aligned (dsh_row_chain); otherwise one byte at a time.
+template <bool ALIGNED>
+__global__ void __launch_bounds__(256) k_int8_matvec_chain(const int8_t *__restrict__ q,
+                                                           const float *__restrict__ scale,
+                                                           const float *__restrict__ offset,
+                                                           const float *__restrict__ x, float *__restrict__ y,
+                                                           int in_dim, int row_start, int nrows) {
+  extern __shared__ __attribute__((aligned(16))) float s_x[];
+  for (int i = threadIdx.x; i < in_dim; i += 256) s_x[i] = x[i];
+  __syncthreads();
+  const int rr = blockIdx.x * 256 + threadIdx.x;
+  if (rr >= nrows) return;
+  const int r = row_start + rr;
+  const int8_t *qr = q + (size_t)r * in_dim;
+  float dot, xs = 0.0f;
+  if (ALIGNED) {
+    dot = dsh_row_chain<true>(qr, s_x, in_dim, xs);
+  } else {
+    dot = 0.0f;
+    for (int c = 0; c < in_dim; c++) {
+      dot = __builtin_fmaf((float)((int)qr[c] + 128), s_x[c], dot);
+      xs += s_x[c];
+    }
+  }
+  y[rr] = __builtin_fmaf(scale[r], dot, offset[r] * xs);
+}
+
 // ============================================================================ elementwise
 // ds_swiglu_direct (ds_kernels.c:1739-1789), fast-exp branch, for seq rows of inter.
 __global__ void k_swiglu(float *__restrict__ out, const float *__restrict__ g, const float *__restrict__ u, size_t n) {
@@ -325,7 +356,7 @@ __device__ void topk_cfg_wave(const float *scores, int n, int k, int *idx, float
     float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_ss), j));
     if (v > mx) mx = v;
   }
-  float ev = lane < ns ? expf(my_ss - mx) : 0.0f;
+  float ev = lane < ns ? dsh_expf_cr(my_ss - mx) : 0.0f;
   float sum = 0.0f;
   for (int j = 0; j < ns; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j));
   float inv = 1.0f / sum;
@@ -698,6 +729,19 @@ hipError_t dsh_launch_dequantize(const int8_t *q, const float *scale, const floa
   int blocks = (int)((n + 255) / 256);
   if (blocks > 8192) blocks = 8192;
   k_dequantize<<<blocks, 256, 0, s>>>(q, scale, offset, out, out_dim, in_dim);
+  return LAUNCH_CHECK();
+}
+
+hipError_t dsh_launch_int8_matvec_exact(const int8_t *q, const float *scale, const float *offset, const float *x,
+                                        float *y, int in_dim, int row_start, int nrows, hipStream_t s) {
+  if (nrows <= 0) return hipSuccess;
+  const size_t lds = (size_t)in_dim * sizeof(float);
+  if (in_dim <= 0 || lds > 64 * 1024) return hipErrorInvalidValue;
+  const bool aligned = in_dim % 16 == 0 && ((uintptr_t)q & 15) == 0;
+  if (aligned)
+    k_int8_matvec_chain<true><<<(nrows + 255) / 256, 256, lds, s>>>(q, scale, offset, x, y, in_dim, row_start, nrows);
+  else
+    k_int8_matvec_chain<false><<<(nrows + 255) / 256, 256, lds, s>>>(q, scale, offset, x, y, in_dim, row_start, nrows);
   return LAUNCH_CHECK();
 }
 

@@ -83,6 +83,44 @@ __global__ void __launch_bounds__(64) k_dec_partial_scores(const float *__restri
   partials[(size_t)blockIdx.x * 64 + lane] = lane < E ? p : 0.0f;
 }
 
+// CFG mode, exact: the full f32 router scores in ds_linear's order (no BLAS, seq 1, ds_kernels.c:639-652,
+// as GCC compiles it: rounded products added in index order, the tail past the last multiple of 8
+// fused), written as the single partial. One wave, lane = expert, reading the transposed router
+// row k (E floats, one coalesced load) PF rows ahead; x staged in LDS. Used where routing must
+// match the reference bit for bit (the bf16 simulation); about one 2*H-long dependent chain.
+__global__ void __launch_bounds__(64) k_dec_scores_f32_exact(const float *__restrict__ WrT, const float *__restrict__ x_in,
+                                                             const int *__restrict__ step, int stride, int H, int E,
+                                                             float *__restrict__ partials) {
+  constexpr int PF = 32;
+  __shared__ __attribute__((aligned(16))) float s_x[2048];
+  const float *x = at_step(x_in, step, stride);
+  const int lane = threadIdx.x, ec = min(lane, E - 1);
+  for (int i = lane; i < H; i += 64) s_x[i] = x[i];
+  __syncthreads();
+  float ring[PF];
+#pragma unroll
+  for (int j = 0; j < PF; j++) ring[j] = WrT[(size_t)min(j, H - 1) * E + ec];
+  const int m = H >= 16 ? (H & ~15) + ((H - (H & ~15)) >= 8 ? 8 : 0) : (H >= 8 ? 8 : 0);
+  float sc = 0.0f;
+  for (int k0 = 0; k0 < H; k0 += PF) {
+    float w[PF];
+#pragma unroll
+    for (int j = 0; j < PF; j++) {
+      w[j] = ring[j];
+      ring[j] = WrT[(size_t)min(k0 + PF + j, H - 1) * E + ec];
+    }
+#pragma unroll
+    for (int j = 0; j < PF; j++) {
+      const int k = k0 + j;
+      if (k < m)
+        sc = __fadd_rn(sc, __fmul_rn(s_x[k], w[j]));
+      else if (k < H)
+        sc = __builtin_fmaf(s_x[k], w[j], sc);
+    }
+  }
+  partials[lane] = lane < E ? sc : 0.0f;
+}
+
 // dst[c][r] = src[r][c] for a rows x cols f32 matrix (32x32 tiles through LDS).
 __global__ void __launch_bounds__(256) k_transpose_f32(const float *__restrict__ src, float *__restrict__ dst, int rows,
                                                        int cols) {
@@ -455,6 +493,175 @@ __global__ void __launch_bounds__(512) k_dec_down(dsh_layer_t L, const float *__
   }
 }
 
+// ============================================================================ bf16 simulation
+// With ds_bf16_simulate_python the reference rounds gate, up, the SwiGLU output and every expert's
+// output to bf16 (ds_quantize.c:311-320). A value summed in any order other than the reference's
+// lands on the other side of a rounding boundary now and then, so these kernels compute every
+// rounded value in the reference's own order (dsh_row_chain: one lane per row, the row's
+// sequential fused chain, ds_quantize.c:163-166; Σx and Σh as sequential sums): for the same routing
+// the layer output is bit-identical to the reference's. One lane per row makes them latency-bound
+// (one 1280-long chain per projection); the unrounded mode keeps the fast kernels above.
+//
+// k_sim_gate_up: block b owns units 128b .. 128b+127 (the routed units k*I + i, then the shared
+// expert's); threads 0-127 run the units' gate rows, 128-255 their up rows, and lane 0 of a fifth
+// wave sums x. Waves 0-3 route as k_dec_gate_up does (each for itself). h = bf16(SwiGLU(bf16(g),
+// bf16(u))); block 0 publishes the routing.
+__global__ void __launch_bounds__(320) k_sim_gate_up(dsh_layer_t L, const float *x_in, const int *__restrict__ step,
+                                                     int stride, const float *partials, int np, int mode,
+                                                     dsh_layer_work_t wk) {
+  __shared__ __attribute__((aligned(16))) float s_x[2048];
+  __shared__ int s_idx[4 * 64];
+  __shared__ float s_w[4 * 64];
+  __shared__ float s_red[4][64];
+  __shared__ route_scratch s_scr[4];
+  __shared__ float s_up[128];
+  __shared__ float s_xsum;
+  const float *x = at_step(x_in, step, stride);
+  const int H = L.H, I = L.I, K = L.K, SI = L.SI, KI = K * I;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  for (int i = t; i < H; i += 320) s_x[i] = x[i];
+  if (wave < 4) {
+    float pv[ROUTE_BATCH];
+    route_load(partials, np, pv);
+    route_reduce(np, L.E, pv, s_red);
+  }
+  __syncthreads();  // s_x, s_red
+  const int u = blockIdx.x * 128 + (t & 127), part = (t >> 7) & 1;
+  const bool active = wave < 4 && u < KI + SI;
+  float dot = 0.0f;
+  float2 so = make_float2(0.0f, 0.0f);
+  int e = 0;
+  if (wave == 4) {
+    if (lane == 0) {  // Σx, added in element order as the reference's loop does
+      float xs = 0.0f;
+      for (int i = 0; i < H; i += 4) {
+        const f32x4 v = *(const f32x4 *)(s_x + i);
+        xs += v[0];
+        xs += v[1];
+        xs += v[2];
+        xs += v[3];
+      }
+      s_xsum = xs;
+    }
+  } else {
+    route_select(L.E, K, mode, s_idx + 64 * wave, s_w + 64 * wave, s_red, s_scr + wave);
+    if (active) {
+      const int8_t *row;
+      if (u < KI) {
+        const int k = u / I, i = u - k * I;
+        e = s_idx[64 * wave + k];
+        const size_t r = (size_t)max(e, 0) * 2 * I + (size_t)part * I + i;
+        row = L.gu_q + r * H;
+        so = so_pair(L.gu_so, r);
+      } else {
+        const size_t r = (size_t)part * SI + (u - KI);
+        row = L.sgu_q + r * H;
+        so = so_pair(L.sgu_so, r);
+      }
+      float unused = 0.0f;
+      dot = dsh_row_chain<false>(row, s_x, H, unused);
+    }
+  }
+  __syncthreads();  // s_xsum
+  float y = 0.0f;
+  if (active) {
+    y = dsh_bf16_round_half_up(__builtin_fmaf(so.x, dot, so.y * s_xsum));
+    if (part) s_up[t & 127] = y;
+  }
+  __syncthreads();  // s_up
+  if (active && !part) {
+    const float hv = dsh_bf16_round_half_up(dsh_swiglu(y, s_up[t]));
+    wk.h[u] = (u < KI && e < 0) ? 0.0f : hv;
+  }
+  if (blockIdx.x == 0 && wave == 0 && lane < K) {
+    wk.idx[lane] = s_idx[lane];
+    wk.w[lane] = s_w[lane];
+  }
+}
+
+// k_sim_down: block (64-row tile, segment seg): lane r of wave 0 runs output row 64*tile + r of routed
+// slot seg (seg < K: expert idx[seg] on its I SwiGLU outputs) or of the shared expert (seg == K, on
+// its SI outputs); lane 0 of wave 1 sums h. e = bf16(fma(scale, dot, offset * Σh)) into eo[seg][row]
+// (0 for a DECODE slot left empty).
+__global__ void __launch_bounds__(128) k_sim_down(dsh_layer_t L, dsh_layer_work_t wk) {
+  __shared__ __attribute__((aligned(16))) float s_h[7 * 1024];
+  __shared__ float s_hsum;
+  const int H = L.H, I = L.I, K = L.K, SI = L.SI;
+  const int seg = blockIdx.y, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int n = seg < K ? I : SI;
+  const float *h = wk.h + (seg < K ? seg * I : K * I);
+  for (int i = t; i < n; i += 128) s_h[i] = h[i];
+  const int e = seg < K ? wk.idx[seg] : 0;
+  __syncthreads();  // s_h
+  const int r = blockIdx.x * 64 + lane;
+  float dot = 0.0f;
+  float2 so = make_float2(0.0f, 0.0f);
+  if (wave == 0) {
+    const int8_t *row;
+    if (seg < K) {
+      const size_t rr = (size_t)max(e, 0) * H + r;
+      row = L.dn_q + rr * I;
+      so = so_pair(L.dn_so, rr);
+    } else {
+      row = L.sdn_q + (size_t)r * SI;
+      so = so_pair(L.sdn_so, r);
+    }
+    float unused = 0.0f;
+    dot = dsh_row_chain<false>(row, s_h, n, unused);
+  } else if (lane == 0) {
+    float hs = 0.0f;
+    for (int i = 0; i < n; i += 4) {
+      const f32x4 v = *(const f32x4 *)(s_h + i);
+      hs += v[0];
+      hs += v[1];
+      hs += v[2];
+      hs += v[3];
+    }
+    s_hsum = hs;
+  }
+  __syncthreads();  // s_hsum
+  if (wave == 0)
+    wk.eo[(size_t)seg * H + r] =
+        (seg < K && e < 0) ? 0.0f : dsh_bf16_round_half_up(__builtin_fmaf(so.x, dot, so.y * s_hsum));
+}
+
+// k_sim_combine: R rows per 64-lane block, as k_dec_down's combine: out = Σ_k fma(w_k, e_k, out) in
+// top-k order (ds_expert_combine, ds_kernels.c:359-371), + the shared output, + the residual; then
+// (WrT_next) this block's partial router scores for the next layer.
+template <int R>
+__global__ void __launch_bounds__(64) k_sim_combine(dsh_layer_t L, const float *__restrict__ x_in,
+                                                    const int *__restrict__ step, int stride, float *x_out,
+                                                    int residual, const float *__restrict__ resid,
+                                                    dsh_layer_work_t wk, const float *__restrict__ WrT_next,
+                                                    int E_next, float *__restrict__ partials_next) {
+  __shared__ float s_x[R];
+  const float *x = at_step(x_in, step, stride);
+  const int H = L.H, K = L.K, lane = threadIdx.x, r0 = blockIdx.x * R;
+  float wr[R];
+  if (WrT_next && lane < E_next) {
+#pragma unroll
+    for (int j = 0; j < R; j++) wr[j] = WrT_next[(size_t)(r0 + j) * E_next + lane];
+  }
+  if (lane < R) {
+    const int r = r0 + lane;
+    float out = 0.0f;
+    for (int k = 0; k < K; k++) out = __builtin_fmaf(wk.w[k], wk.eo[(size_t)k * H + r], out);
+    out = out + wk.eo[(size_t)K * H + r];
+    const float xo = residual ? (resid ? resid[r] : x[r]) + out : out;
+    x_out[r] = xo;
+    s_x[lane] = xo;
+  }
+  if (WrT_next) {
+    __syncthreads();
+    float p = 0.0f;
+    if (lane < E_next) {
+#pragma unroll
+      for (int j = 0; j < R; j++) p = __builtin_fmaf(wr[j], s_x[j], p);
+    }
+    partials_next[(size_t)blockIdx.x * 64 + lane] = lane < E_next ? p : 0.0f;
+  }
+}
+
 // ============================================================================ LM-head argmax
 // One row per lane, bit-exact 2-accumulator AVX-512 order (ds_kernels_avx.c:162-245, 4-row group
 // path; the stack only takes this kernel when every row of the reference's thread chunks is on that
@@ -703,9 +910,22 @@ static int dec_gate_up_blocks(const dsh_layer_t *L) {
   return max((L->SI + 3) / 4, (L->K * L->I + 11) / 12);
 }
 
+hipError_t dsh_launch_dec_scores_f32_exact(const float *WrT, const float *x_in, const int *step, int stride, int H,
+                                          int E, float *partials, hipStream_t s) {
+  if (H <= 0 || H > 2048 || E <= 0 || E > 64) return hipErrorInvalidValue;
+  k_dec_scores_f32_exact<<<1, 64, 0, s>>>(WrT, x_in, step, stride, H, E, partials);
+  return hipGetLastError();
+}
+
 hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const int *step, int stride,
                                   const float *partials, int np, int route_mode, int bf16sim,
                                   const dsh_layer_work_t *wk, hipStream_t s) {
+  if (bf16sim) {  // every rounded value in the reference's order
+    if (L->H > 2048 || L->H % 16) return hipErrorInvalidValue;
+    k_sim_gate_up<<<(L->K * L->I + L->SI + 127) / 128, 320, 0, s>>>(*L, x_in, step, stride, partials, np, route_mode,
+                                                                    *wk);
+    return hipGetLastError();
+  }
   const int blocks = dec_gate_up_blocks(L);
 #define GU(N)                                                                                                  \
   case N:                                                                                                      \
@@ -723,6 +943,17 @@ hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const
 hipError_t dsh_launch_dec_down(const dsh_layer_t *L, const float *x_in, const int *step, int stride, float *x_out,
                                int residual, const float *resid, int bf16sim, const dsh_layer_work_t *wk,
                                const float *WrT_next, int E_next, float *partials_next, hipStream_t s) {
+  if (bf16sim) {  // every rounded value in the reference's order, then the combine
+    if (L->H % 64 || L->I % 16 || L->SI % 16 || L->SI > 7 * 1024 || !wk->eo) return hipErrorInvalidValue;
+    k_sim_down<<<dim3(L->H / 64, L->K + 1), 128, 0, s>>>(*L, *wk);
+    if (dec_rows(L->H) == 8)
+      k_sim_combine<8><<<L->H / 8, 64, 0, s>>>(*L, x_in, step, stride, x_out, residual, resid, *wk, WrT_next, E_next,
+                                                partials_next);
+    else
+      k_sim_combine<16><<<L->H / 16, 64, 0, s>>>(*L, x_in, step, stride, x_out, residual, resid, *wk, WrT_next,
+                                                  E_next, partials_next);
+    return hipGetLastError();
+  }
   if (dec_rows(L->H) == 8)
     k_dec_down<8><<<L->H / 8, 512, 0, s>>>(*L, x_in, step, stride, x_out, residual, resid, bf16sim, *wk, WrT_next,
                                            E_next, partials_next);

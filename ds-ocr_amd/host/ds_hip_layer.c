@@ -53,7 +53,7 @@ ds_hip_layer_t *ds_hip_layer_create(int hidden, int inter, int n_experts, int to
   ds_hip_layer_t *L = (ds_hip_layer_t *)calloc(1, sizeof *L);
   if (!L) return NULL;
   size_t H = hidden, I = inter, E = n_experts, K = top_k, SI = shared_inter;
-  size_t off[16], n = 0, k = 0;
+  size_t off[17], n = 0, k = 0;
 #define REGION(bytes) (off[k++] = n, n += al(bytes))
   REGION(E * 2 * I * H);          /* 0 gu_q */
   REGION(E * H * I);              /* 1 dn_q */
@@ -71,6 +71,7 @@ ds_hip_layer_t *ds_hip_layer_create(int hidden, int inter, int n_experts, int to
   REGION((K * I + SI) * 4);       /* 13 h */
   REGION((H / 8) * 64 * 4);       /* 14 router partial scores */
   REGION(E * H * 4);              /* 15 router f32, transposed [H][E] */
+  REGION((K + 1) * H * 4);        /* 16 expert outputs (bf16 simulation) */
 #undef REGION
   hipError_t e = hipMalloc(&L->arena, n);
   if (e != hipSuccess) {
@@ -107,6 +108,7 @@ ds_hip_layer_t *ds_hip_layer_create(int hidden, int inter, int n_experts, int to
   L->wk.idx = (int *)(b + off[11]);
   L->wk.w = (float *)(b + off[12]);
   L->wk.h = (float *)(b + off[13]);
+  L->wk.eo = (float *)(b + off[16]);
   L->partials = (float *)(b + off[14]);
   L->np = dsh_dec_partials(hidden);
   return L;
@@ -264,10 +266,15 @@ static hipError_t mark(hipEvent_t *ev, int *n) {
   return x ? hipEventRecord(x, dsr_stream) : hipSuccess;
 }
 
-/* Router partial scores of layer L for input x (CFG: f32 partials; DECODE: exact full scores as
- * one partial). Returns the number of partial rows through *np. */
+/* Router partial scores of layer L for input x (CFG: f32 partials, or with the bf16 simulation the
+ * exact full scores as one partial; DECODE: exact full scores as one partial). Returns the number of
+ * partial rows through *np. */
 static hipError_t scores_enqueue(const ds_hip_layer_t *L, const float *x_in, const int *step, int stride,
-                                 int route_mode, float *partials, int *np) {
+                                 int route_mode, int bf16sim, float *partials, int *np) {
+  if (route_mode == DS_HIP_ROUTE_CFG && bf16sim) { /* exact: ds_linear's own order */
+    *np = 1;
+    return dsh_launch_dec_scores_f32_exact(L->d.router_f32_t, x_in, step, stride, L->H, L->E, partials, dsr_stream);
+  }
   if (route_mode == DS_HIP_ROUTE_CFG) {
     *np = L->np;
     return dsh_launch_dec_partial_scores(L->d.router_f32_t, x_in, step, stride, L->H, L->E, partials, dsr_stream);
@@ -285,13 +292,13 @@ static hipError_t layer_enqueue(const ds_hip_layer_t *L, const dsh_layer_work_t 
                                 hipEvent_t *ev, int *nev) {
   hipError_t e = hipSuccess;
   if (!have_scores) {
-    e = scores_enqueue(L, x_in, step, stride, route_mode, partials, &np);
+    e = scores_enqueue(L, x_in, step, stride, route_mode, bf16sim, partials, &np);
     if (e == hipSuccess) e = mark(ev, nev);
   }
   if (e == hipSuccess)
     e = dsh_launch_dec_gate_up(&L->d, x_in, step, stride, partials, np, route_mode, bf16sim, wk, dsr_stream);
   if (e == hipSuccess) e = mark(ev, nev);
-  int chain = next && route_mode == DS_HIP_ROUTE_CFG;
+  int chain = next && route_mode == DS_HIP_ROUTE_CFG && !bf16sim;
   if (e == hipSuccess)
     e = dsh_launch_dec_down(&L->d, x_in, step, stride, x_out, residual, NULL, bf16sim, wk,
                             chain ? next->d.router_f32_t : NULL, chain ? next->E : 0, chain ? partials : NULL,
@@ -959,7 +966,7 @@ static int stack_names(const ds_hip_stack_t *S, const char **names) {
     }
     for (int l = 0; l < S->n_layers; l++) {
       NM("attention");
-      if (!cfg) NM("scores");
+      if (!cfg || S->bf16sim) NM("scores");
       if (S->split) {
         NM("layer");
       } else {
@@ -984,8 +991,9 @@ static int stack_names(const ds_hip_stack_t *S, const char **names) {
       NM("dense.down");
     }
     for (int l = 0; l < S->n_layers; l++) {
-      /* with a dense layer first, its down kernel writes the first MoE layer's CFG partials */
-      if (!cfg || (l == 0 && !S->dense)) NM("scores");
+      /* with a dense layer first, its down kernel writes the first MoE layer's CFG partials; the bf16
+       * simulation computes every layer's scores exactly */
+      if (!cfg || S->bf16sim || (l == 0 && !S->dense)) NM("scores");
       NM("gate_up");
       NM("down");
     }
@@ -1010,6 +1018,8 @@ static float *xc_region(const ds_hip_stack_t *S, int l);
 static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *nev) {
   hipError_t e = hipSuccess;
   const int cfg = S->route_mode == DS_HIP_ROUTE_CFG, C = dsh_layer_split_copies();
+  /* CFG scores as partials from the kernel before (the bf16 simulation computes them exactly instead) */
+  const int cfgp = cfg && !S->bf16sim;
   const dsh_layer_work_t *wk = &S->layers[0]->wk;
   const float *xin = S->in;
   const int *st = S->in_step;
@@ -1037,10 +1047,10 @@ static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *ne
     /* with the copies, the attention's first kernel also writes their sum to xbuf for its residual */
     e = ds_hip_attn_enqueue(S->attn[a++], xin, st, stride, nc, nc > 1 ? S->xbuf : NULL, S->step, S->pos0, S->hbuf,
                             S->nbuf,
-                            cfg ? L->d.router_f32_t : NULL, cfg ? L->E : 0, cfg ? pin : NULL);
+                            cfgp ? L->d.router_f32_t : NULL, cfgp ? L->E : 0, cfgp ? pin : NULL);
     if (e == hipSuccess) e = mark(ev, nev);
-    if (e == hipSuccess && !cfg) {
-      e = scores_enqueue(L, S->nbuf, NULL, 0, S->route_mode, pin, &np);
+    if (e == hipSuccess && !cfgp) {
+      e = scores_enqueue(L, S->nbuf, NULL, 0, S->route_mode, S->bf16sim, pin, &np);
       if (e == hipSuccess) e = mark(ev, nev);
     }
     if (S->split) { /* one kernel: MoE(n) + h into the copies region l, clearing region l - 2 */
@@ -1088,7 +1098,7 @@ static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *n
   int np0 = S->layers[0]->np;
   if (!dense || !cfg) {
     e = scores_enqueue(S->layers[0], dense ? S->xbuf : S->in, dense ? NULL : S->in_step, dense ? 0 : S->in_stride,
-                       S->route_mode, S->partials[0], &np0);
+                       S->route_mode, S->bf16sim, S->partials[0], &np0);
     if (e == hipSuccess) e = mark(ev, nev);
   }
   for (int l = 0; l < NL && e == hipSuccess; l++) {
@@ -1223,6 +1233,7 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
   hipError_t e = hipSuccess;
   int n = 0;
   const int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
+  const int cfgp = cfg && !S->bf16sim; /* CFG scores as partials from the kernel before */
   const dsh_layer_work_t *wk = &S->layers[0]->wk;
   e = mark(ev, &n);
   if (S->attn) {
@@ -1235,8 +1246,8 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
       if (e == hipSuccess) e = mark(ev, &n);
       if (e == hipSuccess)
         e = dsh_launch_dense_down(S->dense->wd, S->dense->h, S->in, S->in_step, S->in_stride, S->dense->H, S->dense->I, 1, NULL,
-                                  S->xbuf, cfg ? S->layers[0]->d.router_f32_t : NULL, cfg ? S->layers[0]->E : 0,
-                                  cfg ? S->partials[0] : NULL, dsr_stream);
+                                  S->xbuf, cfgp ? S->layers[0]->d.router_f32_t : NULL, cfgp ? S->layers[0]->E : 0,
+                                  cfgp ? S->partials[0] : NULL, dsr_stream);
       if (e == hipSuccess) e = mark(ev, &n);
     }
     if (S->split && e == hipSuccess) {
@@ -1250,12 +1261,12 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
       int stride = first ? S->in_stride : 0;
       float *pin = S->partials[l & 1], *pout = S->partials[(l + 1) & 1];
       int np = L->np;
-      if (!cfg || first) {
-        e = scores_enqueue(L, xin, st, stride, S->route_mode, pin, &np);
+      if (!cfgp || first) {
+        e = scores_enqueue(L, xin, st, stride, S->route_mode, S->bf16sim, pin, &np);
         if (e == hipSuccess) e = mark(ev, &n);
         if (e != hipSuccess) break;
       }
-      const ds_hip_layer_t *next = cfg && l + 1 < S->n_layers ? S->layers[l + 1] : NULL;
+      const ds_hip_layer_t *next = cfgp && l + 1 < S->n_layers ? S->layers[l + 1] : NULL;
       e = dsh_launch_dec_gate_up(&L->d, xin, st, stride, pin, np, S->route_mode, S->bf16sim, wk, dsr_stream);
       if (e == hipSuccess) e = mark(ev, &n);
       if (e == hipSuccess)

@@ -112,14 +112,21 @@ float ds_int4_quant_error_rms(const ds_int4_block_t *block, const uint16_t *W_bf
   return h[1] > 0 ? sqrtf((float)(h[0] / h[1])) : 0.0f;
 }
 
+/* The matvec of the per-function API: the reference's own per-row order (bit-identical results);
+ * rows longer than the exact kernel stages in LDS use the lane-parallel kernel (f32 rounding). */
+static hipError_t int8_mv(const dsr_dblock_t *db, const float *xd, float *yd, int in_dim, int row_start, int nrows) {
+  if ((size_t)in_dim * 4 <= 64 * 1024)
+    return dsh_launch_int8_matvec_exact(db->q, db->scale, db->offset, xd, yd, in_dim, row_start, nrows, dsr_stream);
+  return dsh_launch_int8_matvec(db->q, db->scale, db->offset, xd, yd, in_dim, row_start, nrows, dsr_stream);
+}
+
 static int matvec_dev(float *y, const float *x, const ds_int4_block_t *block, int row_start, int nrows) {
   dsr_dblock_t db;
   if (dsr_block_device(block, &db)) return -1;
   float *xd = (float *)dsr_scratch(DSR_SLOT_X, (size_t)block->in_dim * 4);
   float *yd = (float *)dsr_scratch(DSR_SLOT_Y, (size_t)nrows * 4);
   if (!xd || !yd || dsr_h2d(xd, x, (size_t)block->in_dim * 4)) return -1;
-  hipError_t e =
-      dsh_launch_int8_matvec(db.q, db.scale, db.offset, xd, yd, block->in_dim, row_start, nrows, dsr_stream);
+  hipError_t e = int8_mv(&db, xd, yd, block->in_dim, row_start, nrows);
   if (e != hipSuccess) return dsr_fail("int8 matvec kernel", e);
   return dsr_d2h(y, yd, (size_t)nrows * 4);
 }
@@ -141,7 +148,8 @@ void ds_int4_matvec_rows(float *y, const float *x, const ds_int4_block_t *block,
   matvec_dev(y, x, block, row_start, nrows);
 }
 
-/* ds_quantize.c:301-321: gate_up matvec -> split -> [bf16] -> SwiGLU -> [bf16] -> down -> [bf16]. */
+/* ds_quantize.c:301-321: gate_up matvec -> split -> [bf16] -> SwiGLU -> [bf16] -> down -> [bf16];
+ * every step in the reference's order, so the output is bit-identical in both modes. */
 void ds_expert_forward_fused_int4(float *out, const float *x, const ds_int4_block_t *gate_up_int4,
                                   const ds_int4_block_t *down_int4, int hidden, int intermediate, float *gate_up_buf,
                                   float *gate_buf, float *up_buf, float *hidden_buf) {
@@ -164,9 +172,9 @@ void ds_expert_forward_fused_int4(float *out, const float *x, const ds_int4_bloc
   float *hd = (float *)dsr_scratch(DSR_SLOT_B, (size_t)intermediate * 4);
   float *od = (float *)dsr_scratch(DSR_SLOT_Y, (size_t)hidden * 4);
   if (!xd || !gu || !hd || !od || dsr_h2d(xd, x, (size_t)hidden * 4)) return;
-  hipError_t e = dsh_launch_int8_matvec(g.q, g.scale, g.offset, xd, gu, hidden, 0, 2 * intermediate, dsr_stream);
+  hipError_t e = int8_mv(&g, xd, gu, hidden, 0, 2 * intermediate);
   if (e == hipSuccess) e = dsh_launch_split_swiglu(hd, gu, intermediate, bf16sim, dsr_stream);
-  if (e == hipSuccess) e = dsh_launch_int8_matvec(d.q, d.scale, d.offset, hd, od, intermediate, 0, hidden, dsr_stream);
+  if (e == hipSuccess) e = int8_mv(&d, hd, od, intermediate, 0, hidden);
   if (e == hipSuccess && bf16sim) e = dsh_launch_bf16_trunc(od, (size_t)hidden, dsr_stream);
   if (e != hipSuccess) {
     dsr_fail("expert kernels", e);

@@ -86,14 +86,13 @@ def test_int8_matvec_dequant_rms(dev, B, name):
         L.ds_int4_matvec(y, x, C.byref(blk))
         yo = np.empty(meta["out"], np.float32)
         O.or_int8_matvec_rows(yo, x, ref.q, ref.scale, ref.offset, meta["in"], 0, meta["out"])
-        err = rel_err(y, yo)
-        print(f"{name}: matvec max|a-b|/max|b| = {err:.2e}")
-        assert err < 1e-5
-        assert rel_err(y, GOLD[f"{name}.y"]) < 1e-5
+        # one lane per row in the reference's own sequential order: bit-identical
+        assert same_bits(y, yo), rel_err(y, yo)
+        assert same_bits(y, GOLD[f"{name}.y"])
         rs, rn = meta["rows"]
         yr = np.empty(rn, np.float32)
         L.ds_int4_matvec_rows(yr, x, C.byref(blk), rs, rn)
-        assert np.abs(yr - y[rs:rs + rn]).max() < 1e-5  # test_int4.c:109-127 bar
+        assert same_bits(yr, y[rs:rs + rn])  # test_int4.c:109-127 asks for 1e-5
         d = np.empty((meta["out"], meta["in"]), np.float32)
         L.ds_int4_dequantize_f32(d, C.byref(blk))
         do = np.empty_like(d)
@@ -156,9 +155,36 @@ def test_expert_int8(dev, B, sim):
     eo = np.empty(lay.hidden, np.float32)
     O.or_expert_int8(eo, x, C.byref(g.or_block()), C.byref(d.or_block()), lay.hidden, lay.inter, sim)
     assert same_bits(eo, ref)
-    err = rel_err(out, ref)
-    print(f"expert int8 sim={sim}: {err:.2e}")
-    assert err < TOL
+    print(f"expert int8 sim={sim}: {rel_err(out, ref):.2e}")
+    assert same_bits(out, ref)
+
+
+@pytest.mark.parametrize("sim", [0, 1])
+def test_expert_int8_full_shape(dev, B, sim):
+    """ds_expert_forward_fused_int4 through the C-ABI at DeepSeek's shapes: routed (gate_up
+    1792x1280, down 1280x896) and shared (3584x1280, 1280x1792), bf16 simulation off and on,
+    bit-identical to the oracle's restatement of the reference (pinned to the reference build)."""
+    L = dev.load()
+    O = B.oracle()
+    for I, seed in ((896, 610), (1792, 620)):
+        gu = B.or_quantize_bf16(B.normal_bf16(2 * I * 1280, seed, 0.02).reshape(2 * I, 1280))
+        dn = B.or_quantize_bf16(B.normal_bf16(1280 * I, seed + 1, 0.02).reshape(1280, I))
+        gb = dev.block_from_arrays(gu.q, gu.scale, gu.offset)
+        db = dev.block_from_arrays(dn.q, dn.scale, dn.offset)
+        for xs in range(3):
+            x = B.normal_f32(1280, seed + 10 + xs)
+            dev.set_bf16sim(sim)
+            try:
+                out = np.empty(1280, np.float32)
+                L.ds_expert_forward_fused_int4(out, x, C.byref(gb), C.byref(db), 1280, I, None, None, None, None)
+            finally:
+                dev.set_bf16sim(0)
+            eo = np.empty(1280, np.float32)
+            O.or_expert_int8(eo, x, C.byref(gu.or_block()), C.byref(dn.or_block()), 1280, I, sim)
+            print(f"expert int8 I={I} sim={sim} x{xs}: {rel_err(out, eo):.2e}")
+            assert same_bits(out, eo)
+        L.ds_hip_weights_changed(gu.q.ctypes.data)
+        L.ds_hip_weights_changed(dn.q.ctypes.data)
 
 
 def test_elementwise_bit_exact(dev, B):
