@@ -242,6 +242,79 @@ def dropin_leg(dev, lays, lm_w, xs_host, n_steps):
                       "activations (the drop-in boundary)"}
 
 
+def fast_expf_np(x):
+    """ds_fast_expf (ds_kernels.h:296-302) vectorised: Schraudolph's bit trick with GCC's fused
+    12102203*x + 1064866805, saturating below -88 and above 88."""
+    x = np.asarray(x, np.float32)
+    v = (np.float64(12102203.0) * x.astype(np.float64) + 1064866805.0).astype(np.float32)  # one rounding: fused
+    out = v.astype(np.int64).astype(np.uint32).view(np.float32)
+    out = np.where(x < -88.0, np.float32(0.0), out)
+    return np.where(x > 88.0, np.float32(1e38), out).astype(np.float32)
+
+
+def prefill_cpu_baseline(lay, X, reps, budget_s):
+    """The reference's prefill MoE block (ds_moe_decoder.c:629-809) on the host: router sgemm, the
+    fast-exp softmax and top-k per token, the shared expert and every routed expert's gathered
+    tokens as sgemm calls (gate, up, down), scatter-add of the weighted outputs, residual. The
+    sgemms are OpenBLAS's (numpy's bundled OpenBLAS, the library the reference links for cblas_sgemm).
+    Weights are f32 copies made once (the reference's cached f32 views, ds_kernels.c:751-759); they
+    are the INT8 codes dequantized, the same values the GPU multiplies."""
+    H_, I_, E_, K_ = lay.hidden, lay.inter, lay.n_experts, lay.top_k
+
+    def deq(b):
+        return (b.scale[:, None] * (b.q.astype(np.float32) + np.float32(128.0)) + b.offset[:, None]).astype(np.float32)
+
+    gw = [deq(b) for b in lay.gu]
+    dw = [deq(b) for b in lay.dn]
+    sg, sd = deq(lay.sgu), deq(lay.sdn)
+    SI_ = lay.shared_inter
+    wr = (lay.router_bf16.astype(np.uint32) << 16).view(np.float32).reshape(E_, H_)
+
+    def silu_mul(g, u):
+        return (g / (np.float32(1.0) + fast_expf_np(-g))) * u
+
+    def one_call():
+        T_ = X.shape[0]
+        sc = X @ wr.T
+        p = fast_expf_np(sc - sc.max(axis=1, keepdims=True))
+        p = p * (np.float32(1.0) / p.sum(axis=1, dtype=np.float32, keepdims=True))
+        idx = np.argsort(-p, axis=1, kind="stable")[:, :K_]
+        wts = np.take_along_axis(p, idx, axis=1)
+        shared = silu_mul(X @ sg[:SI_].T, X @ sg[SI_:].T) @ sd.T
+        routed = np.zeros((T_, H_), np.float32)
+        for e in range(E_):
+            tok, slot = np.nonzero(idx == e)
+            if tok.size == 0:
+                continue
+            xe = X[tok]
+            out = silu_mul(xe @ gw[e][:I_].T, xe @ gw[e][I_:].T) @ dw[e].T
+            routed[tok] += wts[tok, slot][:, None] * out
+        return X + (routed + shared), idx
+
+    out, idx = one_call()  # warm-up
+    t1 = time.perf_counter()
+    one_call()
+    t_one = time.perf_counter() - t1
+    n = int(max(1, min(reps, budget_s / max(t_one, 1e-6))))
+    times = []
+    for _ in range(n):
+        t0 = time.perf_counter()
+        one_call()
+        times.append(time.perf_counter() - t0)
+    try:
+        from threadpoolctl import threadpool_info
+        blas_threads = [i.get("num_threads") for i in threadpool_info() if i.get("user_api") == "blas"]
+    except Exception:  # report, never hide
+        blas_threads = []
+    return {"median_ms": round(1e3 * float(np.median(times)), 3), "p10_ms": round(1e3 * float(np.percentile(times, 10)), 3),
+            "p90_ms": round(1e3 * float(np.percentile(times, 90)), 3), "calls": n,
+            "threads": blas_threads[0] if blas_threads else None,
+            "kind": "port: the reference's prefill block in numpy with OpenBLAS 0.3 sgemm (numpy's bundled OpenBLAS)",
+            "routing": "bf16 router widened, fast-exp softmax over 64, top-6 (the reference prefill's own routing)",
+            "note": "weights pre-converted to f32 once (the reference's cached f32 views); a call without the "
+                    "cache also converts every expert's weights"}, out, idx
+
+
 def pct(v, q):
     return round(float(np.percentile(np.asarray(v, np.float64), q)), 5)
 
@@ -455,6 +528,7 @@ def main():
 
     # prefill (config 3): 662 seeded tokens through one config-2 layer (the first decode layer)
     prefill = None
+    pf_host = None
     if args.prefill_tokens > 0:
         T = args.prefill_tokens
         xp = dev.DeviceBuffer(T * H * 4)
@@ -467,6 +541,13 @@ def main():
         # algorithmic work: K routed + shared experts per token (2 flops per weight element) and the router
         flops = T * (K * 2 * (2 * I * H + H * I) + 2 * (2 * SI * H + H * SI) + 2 * E * H)
         wbytes = E * (2 * I * H + 2 * I * 8 + H * I + H * 8) + 2 * SI * H + 2 * SI * 8 + H * SI + H * 8
+        if not args.no_cpu:  # the GPU's output in the reference prefill's own routing, for the CPU leg
+            idx_d = dev.DeviceBuffer(T * K * 4)
+            dev.check(L.ds_hip_layer_prefill(handles[0], op.ptr, xp.ptr, T, dev.ROUTE_DECODE, 1, idx_d.ptr, None),
+                      "prefill")
+            pf_host = (xp.to_array(np.float32).reshape(T, H), op.to_array(np.float32).reshape(T, H),
+                       idx_d.to_array(np.int32).reshape(T, K))
+            idx_d.close()
         prefill = {"config": "config 3: 662 tokens x 1280 through one config-2 layer", "tokens": T,
                    "us": round(us, 2), "tok_per_s": round(T / (us * 1e-6), 1),
                    "algorithmic_tflops": round(flops / (us * 1e-6) / 1e12, 2),
@@ -536,6 +617,18 @@ def main():
                 ref_dec = [r for r in cpu["rows"] if r["route"] == "decode"] if cpu else []
                 if ref_dec:
                     dropin["vs_cpu_baseline_decode_route"] = round(dropin["value"] / ref_dec[0]["value"], 3)
+            if prefill is not None and pf_host is not None:
+                try:
+                    pcpu, pout, pidx = prefill_cpu_baseline(lays[0], pf_host[0], 20, args.cpu_seconds)
+                    d = np.abs(pout.astype(np.float64) - pf_host[1]).max() / np.abs(pf_host[1]).max()
+                    pcpu["gpu_vs_cpu"] = {"max_abs_err_over_max": float(f"{d:.3e}"),
+                                          "routing_equal_tokens": f"{int(np.sum(np.all(pidx == pf_host[2], axis=1)))}/"
+                                                                  f"{pf_host[2].shape[0]}",
+                                          "note": "GPU prefill (DECODE routing, residual) against this OpenBLAS run"}
+                    pcpu["speedup_gpu"] = round(pcpu["median_ms"] * 1e3 / prefill["us"], 1)
+                    prefill["cpu_baseline"] = pcpu
+                except Exception as exc:  # report, never hide
+                    prefill["cpu_baseline"] = {"error": repr(exc)}
         except Exception as exc:  # report, never hide
             cpu = {"error": repr(exc)}
     elif not args.no_cpu:

@@ -78,6 +78,32 @@ def test_lm_argmax_vs_oracle(dev, B, in_dim, vocab, T, kind):
     assert got_dev == want, (path, got_dev, want)
 
 
+def test_config4_226_steps(dev, B):
+    """Config 4: the 129280 x 1280 bf16 head, 226 sequential steps, each on a fresh seeded
+    f32[1280] ~ N(0, 1) input, 16 reference threads: every index equal to the oracle's (the oracle's
+    226 argmaxes run on host threads; ctypes releases the GIL)."""
+    from concurrent.futures import ThreadPoolExecutor
+    L = dev.load()
+    V, H, N = 129280, 1280, 226
+    W = B.normal_bf16(V * H, 4242, 0.02)
+    xs = np.stack([B.normal_f32(H, 40000 + s) for s in range(N)])
+    Wd = dev.DeviceBuffer.from_array(W)
+    xd = dev.DeviceBuffer.from_array(xs)
+    idx = dev.DeviceBuffer(4 * N)
+    try:
+        L.ds_set_threads(16)
+        for s in range(N):
+            dev.check(L.ds_hip_argmax_bf16(idx.ptr + 4 * s, xd.ptr + 4 * H * s, Wd.ptr, H, V), "argmax")
+        dev.check(L.ds_hip_sync(), "sync")
+    finally:
+        L.ds_set_threads(1)
+    got = idx.to_array(np.int32)
+    with ThreadPoolExecutor(8) as ex:
+        want = np.array(list(ex.map(lambda s: B.oracle().or_argmax_bf16(xs[s], W, H, V, 16, None), range(N))))
+    print(f"config 4: {int(np.sum(got == want))}/{N} indices equal")
+    assert np.array_equal(got, want)
+
+
 def test_lm_argmax_config5_head(dev, B):
     """The full 129280 x 1280 head of config 5, 16 reference threads (chunks of 8080 rows)."""
     L = dev.load()

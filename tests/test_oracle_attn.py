@@ -14,11 +14,20 @@ import pytest
 sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "oracle"))
 import bindings as B  # noqa: E402
 
-R = B.ref("v4") if os.path.exists(B.ref_path("v4")) else None
-pytestmark = pytest.mark.skipif(R is None, reason="oracle/_ref not built (reference sources absent)")
 flags = open("/proc/cpuinfo").read()
-if " avx512f " not in flags:
-    pytestmark = pytest.mark.skip(reason="the pinned reference build needs AVX-512")
+pytestmark = [pytest.mark.skipif(not os.path.exists(B.ref_path("v4")),
+                                 reason="oracle/_ref not built (reference sources absent)"),
+              pytest.mark.skipif(" avx512f " not in flags, reason="the pinned reference build needs AVX-512")]
+
+
+class _LazyRef:
+    """The reference build, loaded at the first use by a test of this file (not at collection)."""
+
+    def __getattr__(self, name):
+        return getattr(B.ref("v4"), name)
+
+
+R = _LazyRef()
 
 
 def bits(a):
