@@ -1,35 +1,41 @@
 // k_prefill.hip — prefill MoE block (T tokens) for the device-resident layer: routing, an
-// expert-sorted grouped GEMM on bf16 MFMA with INT8 weights dequantized in registers, SwiGLU, the
-// down projection and a deterministic combine (ds_moe_decoder.c:629-809 is the reference block; it
-// runs sgemm on bf16 weights, this build runs the same layer's INT8 blocks).
+// expert-sorted grouped GEMM on the int8 MFMA with the INT8 weights as stored, SwiGLU, the down
+// projection and a deterministic combine (ds_moe_decoder.c:629-809 is the reference block; it runs
+// sgemm on bf16 weights, this build runs the same layer's INT8 blocks).
 //
-// Numerics. The stored codes q = u - 128 (-128..127) are exact in bf16. Each f32 activation a is
-// split into hi = bf16(a) and lo = bf16(a - hi), so a = hi + lo to about 2^-17 relative, and
-// Σ q·a = Σ q·hi + Σ q·lo is accumulated by the MFMA in f32 (products exact). The epilogue folds the
-// row's scale and offset: y = scale·Σu·a + offset·Σa = scale·Σq·a + (offset + 128·scale)·Σa.
+// Numerics. The stored codes q = u - 128 (-128..127) are the MFMA's B operand as they are. Each
+// activation row (x per token for gate_up, h per pair or token for down) is two signed 8-bit limbs
+// of X = rint(a·2^(15-e)) = 256·X1 + X0 with 2^e > max|a|·(1 + 2^-7) (|X0|, |X1| <= 128; a to 2^-15
+// of the row's maximum), so Σ q·a = 2^(e-15)·(256·Σ q·X1 + Σ q·X0) with exact int32 sums. x takes
+// one exponent per token. h is written by the gate_up tiles, each 128-unit n-tile of a row at its
+// own exponent (the tile's max |h|); the down GEMM aligns every n-tile to the row's largest exponent
+// (a right shift, ties to even) as it stages the limbs, so tiles below the row's exponent are
+// rounded twice. The epilogues fold the row's scale and offset: y = scale·Σu·a + offset·Σa =
+// scale·Σq·a + (offset + 128·scale)·Σa, with Σa of the f32 values.
 //
 // Kernels (one launch each, all sizes fixed by T, so a graph can hold them):
 //   k_pf_scores  router scores in the decode path's order, as four partial sums per token
-//   k_pf_select  per token: X → Xhi, Xlo (bf16), Σx; expert selection → idx, w
+//   k_pf_select  per token: x → the two int8 limbs and their scale, Σx; expert selection → idx, w
 //   k_pf_plan    expert-sorted (token, slot) pairs (stable: tokens in increasing order per expert),
 //                per-expert offsets and the GEMM work items (expert, up-to-PF_MT-row chunk)
-//   k_pf_gate_up grouped GEMM + SwiGLU → H (bf16 hi/lo) for routed pairs and for the shared expert
+//   k_pf_gate_up grouped GEMM + SwiGLU → h as limbs, its per-(row, n-tile) sums and maxima, for
+//                routed pairs and for the shared expert
 //   k_pf_down    grouped GEMM → Y (f32) per routed pair and per token for the shared expert
+//   k_pf_moe     both GEMMs in one launch (per-XCD work queues), in place of the two above
 //   k_pf_combine out[t] = (residual ? x : 0) + (Σ_k w_k·Y_k in ascending expert order + Y_shared)
 #include "dsh_avx.h"
 #include "dsh_route.h"
 #include "k_core.h"
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 #define PF_MT 64    // rows of A per work item: one or two MFMA sub-tiles of 32 rows
 #define PF_GU_N 128 // gate_up: intermediate units per block (128 gate + 128 up weight rows)
 #define PF_DN_N 256 // down: output rows per block
+#define PF_NT_MAX 16  // down: 128-column stages per A row (I, SI <= 2048)
 #define PF_TB 8     // tokens per DECODE-mode scores block
 #define PF_PLAN_LDS 8192  // (token, slot) entries the plan kernel caches in LDS
 #define PF_NQ 8           // work queues of the fused GEMM kernel: one per XCD
@@ -48,6 +54,12 @@ struct pf_queues {
   int enable;
 };
 
+// h as int8 limbs (low 0, high 1), each 128-column n-tile of a row at its own exponent: routed
+// [TK][I], shared [T][SI].
+struct pf_hq {
+  int8_t *r0, *r1, *s0, *s1;
+};
+
 struct pf_item {
   int seg;   // expert 0..E-1, or E for the shared expert
   int m0;    // first row of the chunk within the segment
@@ -56,24 +68,6 @@ struct pf_item {
 };
 
 // ---------------------------------------------------------------------------------- helpers
-__device__ __forceinline__ unsigned pk_bf16(float x, float y) {
-  return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{x, y}, bf16x2));
-}
-
-// 8 stored codes q (signed bytes, q = u - 128) → 8 exact bf16 values (one sign-extending byte
-// conversion per code and one pack per pair)
-__device__ __forceinline__ bf16x8 codes_to_bf16(u32x2 v) {
-  const int a = (int)v[0], b = (int)v[1];
-  u32x4 r;
-  r[0] = pk_bf16((float)((a << 24) >> 24), (float)((a << 16) >> 24));
-  r[1] = pk_bf16((float)((a << 8) >> 24), (float)(a >> 24));
-  r[2] = pk_bf16((float)((b << 24) >> 24), (float)((b << 16) >> 24));
-  r[3] = pk_bf16((float)((b << 8) >> 24), (float)(b >> 24));
-  return __builtin_bit_cast(bf16x8, r);
-}
-
-__device__ __forceinline__ bf16x8 ld_bf16x8(const __bf16 *p) { return *(const bf16x8 *)p; }
-
 // D[m][n] of a 32x32 MFMA tile held by lane l, register j: n = l % 32, m = 8*(j/4) + 4*(l/32) + j%4
 __device__ __forceinline__ int mfma_row(int lane, int j) { return 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3); }
 
@@ -186,15 +180,17 @@ __global__ void __launch_bounds__(256) k_pf_scores_bf16(const uint16_t *__restri
   }
 }
 
-// One wave per token: the bf16 hi/lo split of x and Σx, then the expert selection from the four
-// partial score rows (route_select: CFG top-k on raw scores + softmax over the k; DECODE fast-exp
-// softmax over all experts + top-k).
-#define PF_SEL_U 8  // x float4 loads per lane in flight
+// One wave per token: x's two int8 limbs (X0 low, X1 high) and their scale 2^(e-15), Σx, then the
+// expert selection from the four partial score rows (route_select: CFG top-k on raw scores +
+// softmax over the k; DECODE fast-exp softmax over all experts + top-k). H <= 256·PF_SEL_U: the
+// wave holds the whole row in registers.
+#define PF_SEL_U 8  // x float4 loads per lane
 template <int MODE>
 __global__ void __launch_bounds__(256) k_pf_select(const float *__restrict__ X, int T, int H, int E, int K,
-                                                   const float *__restrict__ ps, __bf16 *__restrict__ Xhi,
-                                                   __bf16 *__restrict__ Xlo, float *__restrict__ xsum,
-                                                   int *__restrict__ idx, float *__restrict__ w) {
+                                                   const float *__restrict__ ps, int8_t *__restrict__ X0,
+                                                   int8_t *__restrict__ X1, float *__restrict__ xsc,
+                                                   float *__restrict__ xsum, int *__restrict__ idx,
+                                                   float *__restrict__ w) {
   __shared__ float s_red[4][4][64];
   __shared__ int s_idx[4][64];
   __shared__ float s_w[4][64];
@@ -205,29 +201,41 @@ __global__ void __launch_bounds__(256) k_pf_select(const float *__restrict__ X, 
 #pragma unroll
   for (int r = 0; r < 4; r++) s_red[wave][r][lane] = ps[((size_t)t * 4 + r) * 64 + lane];
   const f32x4 *src = (const f32x4 *)(X + (size_t)t * H);
-  float s = 0.0f;
-  for (int c0 = 0; c0 < H / 4; c0 += 64 * PF_SEL_U) {
-    f32x4 xv[PF_SEL_U];
+  const int nc = H / 4;
+  f32x4 xv[PF_SEL_U];
 #pragma unroll
-    for (int u = 0; u < PF_SEL_U; u++) xv[u] = src[min(c0 + 64 * u + lane, H / 4 - 1)];
+  for (int u = 0; u < PF_SEL_U; u++) xv[u] = src[min(64 * u + lane, nc - 1)];
+  float s = 0.0f, mx = 0.0f;
 #pragma unroll
-    for (int u = 0; u < PF_SEL_U; u++) {
-      const int c = c0 + 64 * u + lane;
-      if (c >= H / 4) continue;
-      const f32x4 v = xv[u];
-      bf16x4 hi, lo;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        hi[i] = (__bf16)v[i];
-        lo[i] = (__bf16)(v[i] - (float)hi[i]);
-      }
-      *(bf16x4 *)(Xhi + (size_t)t * H + 4 * c) = hi;
-      *(bf16x4 *)(Xlo + (size_t)t * H + 4 * c) = lo;
-      s += (v[0] + v[1]) + (v[2] + v[3]);
-    }
+  for (int u = 0; u < PF_SEL_U; u++) {
+    if (64 * u + lane >= nc) continue;
+    const f32x4 v = xv[u];
+    s += (v[0] + v[1]) + (v[2] + v[3]);
+    mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v[0]), fabsf(v[1]))), fmaxf(fabsf(v[2]), fabsf(v[3])));
   }
   s = dsh_wave_sum(s);
-  if (lane == 0) xsum[t] = s;
+  mx = dsh_wave_max(mx);
+  const int ex = __builtin_amdgcn_frexp_expf(mx * 1.0078125f);  // 2^ex > max|x|·(1 + 2^-7)
+#pragma unroll
+  for (int u = 0; u < PF_SEL_U; u++) {
+    const int c = 64 * u + lane;
+    if (c >= nc) continue;
+    unsigned w0 = 0u, w1 = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int q = (int)__builtin_rintf(__builtin_ldexpf(xv[u][i], 15 - ex));  // |q| < 2^15 / (1 + 2^-7)
+      const int lo = __builtin_amdgcn_sbfe(q, 0, 8);                            // balanced low digit
+      const int hi = (q - lo) >> 8;                                              // |hi| <= 127
+      w0 |= ((unsigned)lo & 255u) << (8 * i);
+      w1 |= ((unsigned)hi & 255u) << (8 * i);
+    }
+    *(unsigned *)(X0 + (size_t)t * H + 4 * c) = w0;
+    *(unsigned *)(X1 + (size_t)t * H + 4 * c) = w1;
+  }
+  if (lane == 0) {
+    xsum[t] = s;
+    xsc[t] = __builtin_ldexpf(1.0f, ex - 15);
+  }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -443,111 +451,163 @@ __device__ __forceinline__ bool pf_tile(const int *counts, const int *tiles, int
 struct pf_smem {
   union {
     struct {
-      __bf16 A[2][2][PF_MT][64];      // [half-stage parity][hi, lo][row][column, swizzled]
+      int8_t A[2][2][PF_MT][PF_KS];   // [stage parity][low, high limb][row][column, swizzled]
       unsigned char B[4][64][PF_KS];  // per wave: its 64 weight rows x the stage's codes, swizzled
-    } t;
+    } q;                              // main loop
     float red[4][64][33];  // gate_up epilogue: h values per wave for the row sums
   } u;
   float hsum[4][2][32];  // Σh of the block's A rows (per wave, per 32-row sub-tile)
+  float hmx[4][2][32];   // gate_up: max |h| of the block's A rows (per wave, per 32-row sub-tile)
   float xs[PF_MT];       // gate_up: Σx of the block's A rows (their tokens)
+  float xsc[PF_MT];      // the A rows' limb scale 2^(e-15)
+  short ek[PF_MT][PF_NT_MAX];  // down: exponent of each A row's n-tiles
+  int erow[PF_MT];             // down: the A rows' common exponent (max over their n-tiles)
 };
+
+// Limb exponent of a set of values with max |v| = mx: 2^e > mx·(1 + 2^-7), so rint(v·2^(15-e)) + 128
+// stays within 16 bits and both limbs within 8.
+__device__ __forceinline__ int pf_limb_exp(float mx) { return __builtin_amdgcn_frexp_expf(mx * 1.0078125f); }
+
+// Four values to limbs: fma(v, f, 1.5·2^23 + 128) rounds v·f to the nearest integer (ties to even)
+// and leaves t = rint(v·f) + 128 in the low 16 bits of the result's bits (|t| < 2^22); two byte
+// permutes gather the four low bytes (xor 0x80: (t & 255) - 128) and the four high bytes (t >> 8).
+__device__ __forceinline__ void pf_limbs4(f32x4 v, float f, unsigned &lo, unsigned &hi) {
+  const float magic = 12583040.0f;  // 1.5·2^23 + 128
+  unsigned w[4];
+#pragma unroll
+  for (int b = 0; b < 4; b++) w[b] = __float_as_uint(__builtin_fmaf(v[b], f, magic));
+  const unsigned p01 = __builtin_amdgcn_perm(w[1], w[0], 0x05040100u);  // t0 b0, t0 b1, t1 b0, t1 b1
+  const unsigned p23 = __builtin_amdgcn_perm(w[3], w[2], 0x05040100u);
+  lo = __builtin_amdgcn_perm(p23, p01, 0x06040200u) ^ 0x80808080u;
+  hi = __builtin_amdgcn_perm(p23, p01, 0x07050301u);
+}
+
+// 16 values of one row (low limbs lo, high limbs hi) shifted right by d (1..31), rounded to nearest
+// with ties to even (with d = 1 every odd X is a tie; rounding those one way would bias the sums):
+// X = 256·hi + lo, X' = (X + 2^(d-1) - 1 + ((X >> d) & 1)) >> d, stored back as limbs of X' + 128
+// (as pf_limbs4).
+__device__ __forceinline__ void pf_align16(u32x4 &lo, u32x4 &hi, int d) {
+  const int r = (1 << (d - 1)) - 1;
+#pragma unroll
+  for (int w = 0; w < 4; w++) {
+    unsigned t[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      const int x = __builtin_amdgcn_sbfe((int)hi[w], 8 * b, 8) * 256 + __builtin_amdgcn_sbfe((int)lo[w], 8 * b, 8);
+      t[b] = (unsigned)(((x + r + ((x >> d) & 1)) >> d) + 128);
+    }
+    const unsigned p01 = __builtin_amdgcn_perm(t[1], t[0], 0x05040100u);
+    const unsigned p23 = __builtin_amdgcn_perm(t[3], t[2], 0x05040100u);
+    lo[w] = __builtin_amdgcn_perm(p23, p01, 0x06040200u) ^ 0x80808080u;
+    hi[w] = __builtin_amdgcn_perm(p23, p01, 0x07050301u);
+  }
+}
 
 // 16-byte chunk c of LDS row r sits at chunk c ^ pf_swz(r): 16 consecutive rows map one chunk to 16
 // distinct bank groups, and two consecutive rows fill 256 contiguous bytes
 __device__ __forceinline__ int pf_swz(int r) { return (r ^ (r >> 3)) & 7; }
 
-template <int NSUB>
-__device__ __forceinline__ void pf_mainloop(const __bf16 *Ahi, const __bf16 *Alo, const size_t *arow, int K,
-                                            const int8_t *brow0, const int8_t *brow1, f32x16 (&acc)[NSUB][2],
-                                            pf_smem &sm) {
+// The int8 main loop (both projections): weights are the B operand as stored codes, the activations
+// two int8 limbs (low, high). Per 128-column stage each wave streams its 64 weight rows' 128-byte
+// lines (8 lanes per row, PF_D stages ahead in registers) into its own LDS tile; the block's A rows
+// for the stage (8 adjacent lanes per row's 128 columns, one stage ahead in registers) go to a
+// double-buffered LDS tile, one barrier per stage. LDS rows are 128 bytes with 16-byte chunks
+// XOR-swizzled by pf_swz(row). Per 32-column slice s, lane half h takes bytes 32s + 16h .. +15 of
+// its A row and of its weight row (v_mfma_i32_32x32x32_i8; A and B take the same columns in the same
+// byte order, so the product is the dot product over the slice). acc[ms][q][l]: A sub-tile ms, weight
+// tile q, limb l, exact int32 sums.
+// A is two int8 limb arrays, A0 low and A1 high (gate_up: x at one exponent per row; down: h at
+// one exponent per row and 128-column stage). ALIGN (down): before a stage's A values go to LDS,
+// each is brought to its row's common exponent (pf_align16 with d = erow - ek of the row's stage;
+// sm.ek, sm.erow; trow: the table rows of this thread's two A rows).
+template <int NSUB, bool ALIGN>
+__device__ __forceinline__ void pf_mainloop_i8(const int8_t *A0, const int8_t *A1, const size_t *arow,
+                                               const int *trow, int K, const int8_t *brow0, const int8_t *brow1,
+                                               i32x16 (&acc)[NSUB][2][2], pf_smem &sm) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, l32 = lane & 31;
   const int ar = threadIdx.x >> 3, ac = threadIdx.x & 7;  // A copy: rows ar and ar + 32, chunk ac
-  const int nk = K / PF_KS, nkp = (nk + PF_D - 1) / PF_D * PF_D, nh = 2 * nk;
+  const int nk = K / PF_KS, nkp = (nk + PF_D - 1) / PF_D * PF_D;
 #pragma unroll
   for (int ms = 0; ms < NSUB; ms++)
 #pragma unroll
     for (int q = 0; q < 2; q++)
 #pragma unroll
-      for (int j = 0; j < 16; j++) acc[ms][q][j] = 0.0f;
-  // The weight addresses take a zero offset from an asm that depends on the A rows, so the
-  // prologue's weight loads are issued after the row indices are known, in the loop's order.
+      for (int l = 0; l < 2; l++)
+#pragma unroll
+        for (int j = 0; j < 16; j++) acc[ms][q][l][j] = 0;
   int zero = 0;
   asm volatile("" : "+v"(zero) : "v"((int)arow[0]), "v"((int)arow[1]));
   const size_t K8 = (size_t)8 * K;
   const int brow = lane >> 3, bch = lane & 7;
   const int8_t *p0 = brow0 + zero + (size_t)brow * K + 16 * bch;
   const int8_t *p1 = brow1 + zero + (size_t)brow * K + 16 * bch;
-  const int aw0 = 8 * (ac ^ pf_swz(ar)), aw1 = 8 * (ac ^ pf_swz(ar + 32));
+  const int aw0 = 16 * (ac ^ pf_swz(ar)), aw1 = 16 * (ac ^ pf_swz(ar + 32));
   u32x4 bR[PF_D][8];
-  bf16x8 aR[2][4];  // [half-stage parity][hi row ar, hi row ar+32, lo row ar, lo row ar+32]
+  u32x4 aR[4];  // X0 rows ar, ar+32, X1 rows ar, ar+32
   auto load_b = [&](u32x4(&dst)[8], int k) {
 #pragma unroll
     for (int i = 0; i < 8; i++) dst[i] = *(const u32x4 *)((i < 4 ? p0 : p1) + (i & 3) * K8 + (size_t)k * PF_KS);
   };
-  auto load_a = [&](bf16x8(&dst)[4], int hs) {
-    const size_t o = (size_t)hs * 64 + 8 * ac;
-    dst[0] = ld_bf16x8(Ahi + arow[0] + o);
-    dst[1] = ld_bf16x8(Ahi + arow[1] + o);
-    dst[2] = ld_bf16x8(Alo + arow[0] + o);
-    dst[3] = ld_bf16x8(Alo + arow[1] + o);
+  auto load_a = [&](u32x4(&dst)[4], int k) {
+    const size_t o = (size_t)k * PF_KS + 16 * ac;
+    dst[0] = *(const u32x4 *)(A0 + arow[0] + o);
+    dst[1] = *(const u32x4 *)(A0 + arow[1] + o);
+    dst[2] = *(const u32x4 *)(A1 + arow[0] + o);
+    dst[3] = *(const u32x4 *)(A1 + arow[1] + o);
+  };
+  auto store_a = [&](int a, int k) {
+    if (ALIGN) {
+      const int kc = min(k, nk - 1);
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        const int d = min(sm.erow[trow[c]] - (int)sm.ek[trow[c]][kc], 31);
+        if (d > 0) pf_align16(aR[c], aR[2 + c], d);
+      }
+    }
+    *(u32x4 *)&sm.u.q.A[a][0][ar][aw0] = aR[0];
+    *(u32x4 *)&sm.u.q.A[a][0][ar + 32][aw1] = aR[1];
+    *(u32x4 *)&sm.u.q.A[a][1][ar][aw0] = aR[2];
+    *(u32x4 *)&sm.u.q.A[a][1][ar + 32][aw1] = aR[3];
   };
 #pragma unroll
   for (int s = 0; s < PF_D; s++) {
     load_b(bR[s], min(s, nk - 1));
     asm volatile("" ::: "memory");
   }
-  load_a(aR[0], 0);
-  asm volatile("" ::: "memory");
-  load_a(aR[1], min(1, nh - 1));
+  load_a(aR, 0);
   asm volatile("" ::: "memory");
 
   auto group = [&](int kb0) {
 #pragma unroll
     for (int s = 0; s < PF_D; s++) {
       const int k = kb0 + s;
-      // the stage's weight lines → the wave's tile (the wave's reads of the previous stage are
-      // done: a wave's LDS operations complete in order)
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         const int r = 8 * i + brow;
-        *(u32x4 *)&sm.u.t.B[wave][r][16 * (bch ^ pf_swz(r))] = bR[s][i];
+        *(u32x4 *)&sm.u.q.B[wave][r][16 * (bch ^ pf_swz(r))] = bR[s][i];
       }
       load_b(bR[s], min(k + PF_D, nk - 1));
       asm volatile("" ::: "memory");
+      const int a = k & 1;
+      store_a(a, k);
+      load_a(aR, min(k + 1, nk - 1));
+      asm volatile("" ::: "memory");
+      __syncthreads();
+      if (k < nk) {
 #pragma unroll
-      for (int a = 0; a < 2; a++) {
-        *(bf16x8 *)&sm.u.t.A[a][0][ar][aw0] = aR[a][0];
-        *(bf16x8 *)&sm.u.t.A[a][0][ar + 32][aw1] = aR[a][1];
-        *(bf16x8 *)&sm.u.t.A[a][1][ar][aw0] = aR[a][2];
-        *(bf16x8 *)&sm.u.t.A[a][1][ar + 32][aw1] = aR[a][3];
-        load_a(aR[a], min(2 * k + a + 2, nh - 1));
-        asm volatile("" ::: "memory");
-        __syncthreads();
-        if (k < nk) {
+        for (int sl = 0; sl < 4; sl++) {
+          const int cb = 2 * sl + half;  // 16-byte chunk of this lane half
+          const i32x4 b0 = *(const i32x4 *)&sm.u.q.B[wave][l32][16 * (cb ^ pf_swz(l32))];
+          const i32x4 b1 = *(const i32x4 *)&sm.u.q.B[wave][32 + l32][16 * (cb ^ pf_swz(32 + l32))];
 #pragma unroll
-          for (int s2 = 0; s2 < 2; s2++) {
-            const int cb = 2 * (2 * a + s2) + half;  // weight chunk of this lane half
-            const u32x4 b0 = *(const u32x4 *)&sm.u.t.B[wave][l32][16 * (cb ^ pf_swz(l32))];
-            const u32x4 b1 = *(const u32x4 *)&sm.u.t.B[wave][32 + l32][16 * (cb ^ pf_swz(32 + l32))];
-            bf16x8 c0[2], c1[2];
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-              c0[u] = codes_to_bf16(u32x2{b0[2 * u], b0[2 * u + 1]});
-              c1[u] = codes_to_bf16(u32x2{b1[2 * u], b1[2 * u + 1]});
-            }
-#pragma unroll
-            for (int ms = 0; ms < NSUB; ms++)
-#pragma unroll
-              for (int u = 0; u < 2; u++) {
-                const int m = 32 * ms + l32;
-                const int ch = 4 * s2 + 2 * half + u;  // A chunk (8 columns) within the half-stage
-                const bf16x8 ah = *(const bf16x8 *)&sm.u.t.A[a][0][m][8 * (ch ^ pf_swz(m))];
-                const bf16x8 al = *(const bf16x8 *)&sm.u.t.A[a][1][m][8 * (ch ^ pf_swz(m))];
-                acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, c0[u], acc[ms][0], 0, 0, 0);
-                acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, c1[u], acc[ms][1], 0, 0, 0);
-                acc[ms][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, c0[u], acc[ms][0], 0, 0, 0);
-                acc[ms][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, c1[u], acc[ms][1], 0, 0, 0);
-              }
+          for (int ms = 0; ms < NSUB; ms++) {
+            const int m = 32 * ms + l32;
+            const i32x4 x0 = *(const i32x4 *)&sm.u.q.A[a][0][m][16 * (cb ^ pf_swz(m))];
+            const i32x4 x1 = *(const i32x4 *)&sm.u.q.A[a][1][m][16 * (cb ^ pf_swz(m))];
+            acc[ms][0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x0, b0, acc[ms][0][0], 0, 0, 0);
+            acc[ms][1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x0, b1, acc[ms][1][0], 0, 0, 0);
+            acc[ms][0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x1, b0, acc[ms][0][1], 0, 0, 0);
+            acc[ms][1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x1, b1, acc[ms][1][1], 0, 0, 0);
           }
         }
       }
@@ -561,10 +621,10 @@ __device__ __forceinline__ void pf_mainloop(const __bf16 *Ahi, const __bf16 *Alo
 // owns units i0 + 32w .. +31, tile 0 = their gate rows, tile 1 = their up rows, so the SwiGLU pairs
 // sit in the same lane and register.
 template <bool SHARED, int NSUB>
-__device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item &it, int nt, const __bf16 *Xhi,
-                                             const __bf16 *Xlo, const float *xsum, const int *pair_tok,
-                                             int bf16sim, __bf16 *Hhi, __bf16 *Hlo, float *hpart,
-                                             pf_smem &sm) {
+__device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item &it, int nt, const int8_t *X0,
+                                             const int8_t *X1, const float *xsc, const float *xsum,
+                                             const int *pair_tok, int bf16sim, int8_t *Hq0, int8_t *Hq1,
+                                             float *hpart, float *hmaxp, pf_smem &sm) {
   const int H = L.H;
   const int Iseg = SHARED ? L.SI : L.I, ntK = Iseg / PF_GU_N;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l32 = lane & 31;
@@ -580,24 +640,26 @@ __device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item
     tok[c] = SHARED ? it.m0 + rr : pair_tok[it.pos0 + it.m0 + rr];
     arow[c] = (size_t)tok[c] * H;
   }
-  // the rows' Σx for the epilogue, staged in LDS (visible after the main loop's first barrier)
+  // the rows' Σx and limb scales for the epilogue, staged in LDS (visible after the main loop's
+  // first barrier)
   if ((threadIdx.x & 7) == 0) {
-    const float x0 = xsum[tok[0]], x1 = xsum[tok[1]];
+    const float x0 = xsum[tok[0]], x1 = xsum[tok[1]], c0 = xsc[tok[0]], c1 = xsc[tok[1]];
     sm.xs[threadIdx.x >> 3] = x0;
     sm.xs[(threadIdx.x >> 3) + 32] = x1;
+    sm.xsc[threadIdx.x >> 3] = c0;
+    sm.xsc[(threadIdx.x >> 3) + 32] = c1;
   }
-  f32x16 acc[NSUB][2];
-  pf_mainloop<NSUB>(Xhi, Xlo, arow, H, wq + (size_t)u0 * H, wq + (size_t)(Iseg + u0) * H, acc, sm);
+  i32x16 acc[NSUB][2][2];
+  pf_mainloop_i8<NSUB, false>(X0, X1, arow, nullptr, H, wq + (size_t)u0 * H, wq + (size_t)(Iseg + u0) * H, acc, sm);
   // signed codes: offset + 128·scale multiplies Σa
   float2 sog = ((const float2 *)wso)[unit], sou = ((const float2 *)wso)[Iseg + unit];
   sog.y = __builtin_fmaf(128.0f, sog.x, sog.y);
   sou.y = __builtin_fmaf(128.0f, sou.x, sou.y);
   const size_t rbase = SHARED ? (size_t)it.m0 : (size_t)(it.pos0 + it.m0);
-  // The tile's h values (as the down GEMM sees them, hi + lo) also go to LDS for the row sums
-  // Σh over the block's 128 units, which the down epilogue needs for the offset term.
-  // The tile's h values go to LDS (per wave: 64 rows x its 32 units), from where each lane stores
-  // 16-byte runs of 8 units (hi and lo) and sums a row for Σh (over the block's 128 units, for the
-  // down epilogue's offset term; summed as the down GEMM sees the values, hi + lo).
+  // The tile's h values go to LDS (per wave: 64 rows x its 32 units); each lane sums a row (Σh over
+  // the block's 128 units, for the down epilogue's offset term) and takes its max |h|; the rows'
+  // maxima over the block's 128 units give each row's limb exponent for this n-tile, from which the
+  // lanes store 8-unit runs of both limbs.
   float(*red)[64][33] = sm.u.red;
   __syncthreads();  // every wave is done with the main loop's tiles
 #pragma unroll
@@ -607,9 +669,12 @@ __device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item
       const int m = ms * 32 + mfma_row(lane, j);
       float hv = 0.0f;
       if (m < it.mcnt) {
-        const float xs = sm.xs[m];
-        float g = __builtin_fmaf(sog.x, acc[ms][0][j], sog.y * xs);
-        float up = __builtin_fmaf(sou.x, acc[ms][1][j], sou.y * xs);
+        const float xs = sm.xs[m], sc = sm.xsc[m];
+        // Σ q·x = 2^(e-15)·(256·Σ q·X1 + Σ q·X0)
+        const float dg = sc * __builtin_fmaf(256.0f, (float)acc[ms][0][1][j], (float)acc[ms][0][0][j]);
+        const float du = sc * __builtin_fmaf(256.0f, (float)acc[ms][1][1][j], (float)acc[ms][1][0][j]);
+        float g = __builtin_fmaf(sog.x, dg, sog.y * xs);
+        float up = __builtin_fmaf(sou.x, du, sou.y * xs);
         if (bf16sim) {
           g = dsh_bf16_round_half_up(g);
           up = dsh_bf16_round_half_up(up);
@@ -622,78 +687,88 @@ __device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  {  // stores: lane → rows (lane / 4) + 16k, units 8·(lane % 4) .. +7 of the wave's 32
+  float part = 0.0f, pmax = 0.0f;  // lane = row: its sum (in unit order) and max |h| over the wave's 32 units
+  if (lane < 32 * NSUB) {
+#pragma unroll 8
+    for (int u = 0; u < 32; u++) {
+      const float hv = red[wave][lane][u];
+      part += hv;
+      pmax = fmaxf(pmax, fabsf(hv));
+    }
+  }
+  sm.hsum[wave][lane >> 5][lane & 31] = part;
+  sm.hmx[wave][lane >> 5][lane & 31] = pmax;
+  __syncthreads();
+  {  // stores: lane → rows (lane / 4) + 16k, units 8·(lane % 4) .. +7 of the wave's 32, as limbs
     const int g8 = 8 * (lane & 3);
 #pragma unroll
     for (int k = 0; k < 2 * NSUB; k++) {
       const int m = (lane >> 2) + 16 * k;
       if (m >= it.mcnt) continue;
-      bf16x8 hi8, lo8;
+      const int a = m >> 5, b = m & 31;
+      const float mx = fmaxf(fmaxf(sm.hmx[0][a][b], sm.hmx[1][a][b]), fmaxf(sm.hmx[2][a][b], sm.hmx[3][a][b]));
+      const float f = __builtin_ldexpf(1.0f, 15 - pf_limb_exp(mx));
+      f32x4 v0, v1;
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float hv = red[wave][m][g8 + i];
-        hi8[i] = (__bf16)hv;
-        lo8[i] = (__bf16)(hv - (float)hi8[i]);
+      for (int i = 0; i < 4; i++) {
+        v0[i] = red[wave][m][g8 + i];
+        v1[i] = red[wave][m][g8 + 4 + i];
       }
+      unsigned l0, h0, l1, h1;
+      pf_limbs4(v0, f, l0, h0);
+      pf_limbs4(v1, f, l1, h1);
       const size_t o = (rbase + m) * Iseg + u0 + g8;
-      *(bf16x8 *)(Hhi + o) = hi8;
-      *(bf16x8 *)(Hlo + o) = lo8;
+      *(u32x2 *)(Hq0 + o) = u32x2{l0, l1};
+      *(u32x2 *)(Hq1 + o) = u32x2{h0, h1};
     }
   }
-  float part = 0.0f;  // lane = row: its sum over the wave's 32 units, in unit order
-  if (lane < 32 * NSUB) {
-#pragma unroll 8
-    for (int u = 0; u < 32; u++) {
-      const float hv = red[wave][lane][u];
-      const __bf16 hi = (__bf16)hv;
-      part += (float)hi + (float)(__bf16)(hv - (float)hi);
-    }
-  }
-  sm.hsum[wave][lane >> 5][lane & 31] = part;
-  __syncthreads();
   if (threadIdx.x < it.mcnt) {
-    const int m = threadIdx.x;
-    const float tot = ((sm.hsum[0][m >> 5][m & 31] + sm.hsum[1][m >> 5][m & 31]) + sm.hsum[2][m >> 5][m & 31]) +
-                      sm.hsum[3][m >> 5][m & 31];
+    const int m = threadIdx.x, a = m >> 5, b = m & 31;
+    const float tot = ((sm.hsum[0][a][b] + sm.hsum[1][a][b]) + sm.hsum[2][a][b]) + sm.hsum[3][a][b];
+    const float mx = fmaxf(fmaxf(sm.hmx[0][a][b], sm.hmx[1][a][b]), fmaxf(sm.hmx[2][a][b], sm.hmx[3][a][b]));
     hpart[(rbase + m) * ntK + nt] = tot;
+    hmaxp[(rbase + m) * ntK + nt] = mx;
   }
 }
 
 template <bool SHARED>
-__device__ __forceinline__ void gate_up_dispatch(const dsh_layer_t &L, const pf_item &it, int nt, const __bf16 *Xhi,
-                                                 const __bf16 *Xlo, const float *xsum, const int *pair_tok,
-                                                 int bf16sim, __bf16 *Hhi, __bf16 *Hlo, float *hpart,
-                                                 pf_smem &sm) {
+__device__ __forceinline__ void gate_up_dispatch(const dsh_layer_t &L, const pf_item &it, int nt, const int8_t *X0,
+                                                 const int8_t *X1, const float *xsc, const float *xsum,
+                                                 const int *pair_tok, int bf16sim, int8_t *Hq0, int8_t *Hq1,
+                                                 float *hpart, float *hmaxp, pf_smem &sm) {
   if (it.mcnt <= 32)
-    gate_up_tile<SHARED, 1>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Hhi, Hlo, hpart, sm);
+    gate_up_tile<SHARED, 1>(L, it, nt, X0, X1, xsc, xsum, pair_tok, bf16sim, Hq0, Hq1, hpart, hmaxp, sm);
   else
-    gate_up_tile<SHARED, 2>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Hhi, Hlo, hpart, sm);
+    gate_up_tile<SHARED, 2>(L, it, nt, X0, X1, xsc, xsum, pair_tok, bf16sim, Hq0, Hq1, hpart, hmaxp, sm);
 }
 
 __global__ void __launch_bounds__(256, PF_OCC) k_pf_gate_up(dsh_layer_t L, const pf_item *__restrict__ items,
-                                                       const int *__restrict__ counts, const __bf16 *Xhi,
-                                                       const __bf16 *Xlo, const float *__restrict__ xsum,
+                                                       const int *__restrict__ counts, const int8_t *X0,
+                                                       const int8_t *X1, const float *__restrict__ xsc,
+                                                       const float *__restrict__ xsum,
                                                        const int *__restrict__ pair_tok, int bf16sim,
-                                                       __bf16 *__restrict__ Hhi, __bf16 *__restrict__ Hlo,
-                                                       __bf16 *__restrict__ Shi, __bf16 *__restrict__ Slo,
-                                                       float *__restrict__ hpr, float *__restrict__ hps,
+                                                       pf_hq hq, float *__restrict__ hpr, float *__restrict__ hps,
+                                                       float *__restrict__ hmr, float *__restrict__ hms,
                                                        const int *__restrict__ tiles) {
   __shared__ __attribute__((aligned(16))) pf_smem sm;
   int item, nt;
   if (!pf_tile(counts, tiles, L.SI / PF_GU_N, L.I / PF_GU_N, item, nt)) return;
   const pf_item it = items[item];
   if (it.seg == L.E)
-    gate_up_dispatch<true>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Shi, Slo, hps, sm);
+    gate_up_dispatch<true>(L, it, nt, X0, X1, xsc, xsum, pair_tok, bf16sim, hq.s0, hq.s1, hps, hms, sm);
   else
-    gate_up_dispatch<false>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Hhi, Hlo, hpr, sm);
+    gate_up_dispatch<false>(L, it, nt, X0, X1, xsc, xsum, pair_tok, bf16sim, hq.r0, hq.r1, hpr, hmr, sm);
 }
 
 // down: block = (work item, n-tile): the item's A rows (h of its pairs, or of tokens for the shared
-// expert) x 256 output rows; wave w owns rows n0 + 64w .. +63 as two 32-row tiles. Σh of each A row
-// is the sum, in n-tile order, of the per-n-tile row sums the gate_up epilogue wrote.
+// expert, as limbs) x 256 output rows; wave w owns rows n0 + 64w .. +63 as two 32-row tiles. Each A
+// row's exponent is the largest of its n-tiles' (from the max |h| per (row, n-tile) the gate_up
+// epilogues wrote; read at L2); the main loop aligns every stage to it. Σh of each A row is the sum,
+// in n-tile order, of the per-n-tile row sums the gate_up epilogue wrote.
 template <bool SHARED, int NSUB>
-__device__ __forceinline__ void down_tile(const dsh_layer_t &L, const pf_item &it, int nt, const __bf16 *Hhi,
-                                          const __bf16 *Hlo, const float *hpart, float *Y, pf_smem &sm) {
+__device__ __forceinline__ void down_tile(const dsh_layer_t &L, const pf_item &it, int nt, const int8_t *Hq0,
+                                          const int8_t *Hq1, const float *hpart, const float *hmaxp, float *Y,
+                                          pf_smem &sm) {
   const int H = L.H;
   const int Kd = SHARED ? L.SI : L.I, ntK = Kd / PF_GU_N;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, l32 = lane & 31;
@@ -701,19 +776,29 @@ __device__ __forceinline__ void down_tile(const dsh_layer_t &L, const pf_item &i
   const float *wso = SHARED ? L.sdn_so : L.dn_so + (size_t)it.seg * H * 2;
   const int nw = nt * PF_DN_N + wave * 64, n0 = nw + l32;
   const size_t rbase = SHARED ? (size_t)it.m0 : (size_t)(it.pos0 + it.m0);
+  if (threadIdx.x < PF_MT) sm.erow[threadIdx.x] = -1024;
+  __syncthreads();
+  for (int i = threadIdx.x; i < it.mcnt * ntK; i += 256) {
+    const int r = i / ntK;
+    const int e = pf_limb_exp(__hip_atomic_load(hmaxp + rbase * ntK + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    sm.ek[r][i - r * ntK] = (short)e;
+    atomicMax(&sm.erow[r], e);
+  }
+  __syncthreads();
+  if (threadIdx.x < it.mcnt) sm.xsc[threadIdx.x] = __builtin_ldexpf(1.0f, sm.erow[threadIdx.x] - 15);
   size_t arow[2];
+  int trow[2];
 #pragma unroll
   for (int c = 0; c < 2; c++) {
     const int r = (threadIdx.x >> 3) + 32 * c;
-    arow[c] = (rbase + (r < it.mcnt ? r : 0)) * Kd;
+    trow[c] = r < it.mcnt ? r : 0;
+    arow[c] = (rbase + trow[c]) * Kd;
   }
-  f32x16 acc[NSUB][2];
-  pf_mainloop<NSUB>(Hhi, Hlo, arow, Kd, wq + (size_t)nw * Kd, wq + (size_t)(nw + 32) * Kd, acc, sm);
+  i32x16 acc[NSUB][2][2];
+  pf_mainloop_i8<NSUB, true>(Hq0, Hq1, arow, trow, Kd, wq + (size_t)nw * Kd, wq + (size_t)(nw + 32) * Kd, acc, sm);
   {  // lane = row of the block: Σh from the gate_up partials (each wave for itself)
     float hs = 0.0f;
     if (lane < it.mcnt) {
-      // agent-scope atomic loads read the partials at L2 (in the fused kernel other CUs of this
-      // XCD wrote them, and lines of this CU's L1 may mix them with older data)
       const float *hp = hpart + (rbase + lane) * ntK;
       for (int k = 0; k < ntK; k++) hs += __hip_atomic_load(hp + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -733,24 +818,27 @@ __device__ __forceinline__ void down_tile(const dsh_layer_t &L, const pf_item &i
         const int m = ms * 32 + mfma_row(lane, j);
         if (m >= it.mcnt) continue;
         const float hs = sm.hsum[wave][ms][mfma_row(lane, j)];
-        Y[(rbase + m) * H + n0 + 32 * q] = __builtin_fmaf(so.x, acc[ms][q][j], so.y * hs);
+        // Σ q·h = 2^(erow-15)·(256·Σ q·H1 + Σ q·H0)
+        const float dot = sm.xsc[m] * __builtin_fmaf(256.0f, (float)acc[ms][q][1][j], (float)acc[ms][q][0][j]);
+        Y[(rbase + m) * H + n0 + 32 * q] = __builtin_fmaf(so.x, dot, so.y * hs);
       }
   }
 }
 
 template <bool SHARED>
-__device__ __forceinline__ void down_dispatch(const dsh_layer_t &L, const pf_item &it, int nt, const __bf16 *Hhi,
-                                              const __bf16 *Hlo, const float *hpart, float *Y, pf_smem &sm) {
+__device__ __forceinline__ void down_dispatch(const dsh_layer_t &L, const pf_item &it, int nt, const int8_t *Hq0,
+                                              const int8_t *Hq1, const float *hpart, const float *hmaxp, float *Y,
+                                              pf_smem &sm) {
   if (it.mcnt <= 32)
-    down_tile<SHARED, 1>(L, it, nt, Hhi, Hlo, hpart, Y, sm);
+    down_tile<SHARED, 1>(L, it, nt, Hq0, Hq1, hpart, hmaxp, Y, sm);
   else
-    down_tile<SHARED, 2>(L, it, nt, Hhi, Hlo, hpart, Y, sm);
+    down_tile<SHARED, 2>(L, it, nt, Hq0, Hq1, hpart, hmaxp, Y, sm);
 }
 
 __global__ void __launch_bounds__(256, PF_OCC) k_pf_down(dsh_layer_t L, const pf_item *__restrict__ items,
-                                                    const int *__restrict__ counts, const __bf16 *Hhi,
-                                                    const __bf16 *Hlo, const __bf16 *Shi, const __bf16 *Slo,
+                                                    const int *__restrict__ counts, pf_hq hq,
                                                     const float *__restrict__ hpr, const float *__restrict__ hps,
+                                                    const float *__restrict__ hmr, const float *__restrict__ hms,
                                                     float *__restrict__ Y, float *__restrict__ Ysh,
                                                     const int *__restrict__ tiles) {
   __shared__ __attribute__((aligned(16))) pf_smem sm;
@@ -758,9 +846,9 @@ __global__ void __launch_bounds__(256, PF_OCC) k_pf_down(dsh_layer_t L, const pf
   if (!pf_tile(counts, tiles, L.H / PF_DN_N, L.H / PF_DN_N, item, nt)) return;
   const pf_item it = items[item];
   if (it.seg == L.E)
-    down_dispatch<true>(L, it, nt, Shi, Slo, hps, Ysh, sm);
+    down_dispatch<true>(L, it, nt, hq.s0, hq.s1, hps, hms, Ysh, sm);
   else
-    down_dispatch<false>(L, it, nt, Hhi, Hlo, hpr, Y, sm);
+    down_dispatch<false>(L, it, nt, hq.r0, hq.r1, hpr, hmr, Y, sm);
 }
 
 // Fused grouped GEMM: one launch runs every gate_up and down tile, one tile per block. A block
@@ -772,16 +860,18 @@ __global__ void __launch_bounds__(256, PF_OCC) k_pf_down(dsh_layer_t L, const pf
 // down block's bounded wait always ends. As gate_up tiles finish, down tiles start in their place
 // (no tail between the two projections). Coherence is XCD-local: a gate_up block drains its stores
 // to the XCD's L2 (vmcnt(0) in every thread, then a barrier) before one thread bumps the item's
-// counter with an L2 atomic; the down block reads the counter at L2, and the h rows it then loads
-// were written by this XCD (each 128-byte line by one block) and never read here before. Claim
-// counters and item counters are zeroed by the plan kernel.
+// counter with an L2 atomic; the down block reads the counter at L2, and the h limbs it then loads
+// were written by this XCD (each 128-byte line by one block) and never read here before (the
+// per-row partials, which share lines across items, are read with L2 atomics). Claim counters and
+// item counters are zeroed by the plan kernel.
 #define PF_SPIN_MAX (1 << 22)
 #define PF_PROBE 4096  // blocks of the XCD placement check
 __global__ void __launch_bounds__(256, PF_OCC) k_pf_moe(dsh_layer_t L, const pf_item *__restrict__ items,
-                                                    pf_queues Q, const __bf16 *Xhi, const __bf16 *Xlo,
-                                                    const float *__restrict__ xsum, const int *__restrict__ pair_tok,
-                                                    int bf16sim, __bf16 *Hhi, __bf16 *Hlo, __bf16 *Shi, __bf16 *Slo,
-                                                    float *hpr, float *hps, float *__restrict__ Y,
+                                                    pf_queues Q, const int8_t *X0, const int8_t *X1,
+                                                    const float *__restrict__ xsc, const float *__restrict__ xsum,
+                                                    const int *__restrict__ pair_tok,
+                                                    int bf16sim, pf_hq hq, float *hpr, float *hps, float *hmr,
+                                                    float *hms, float *__restrict__ Y,
                                                     float *__restrict__ Ysh) {
   __shared__ __attribute__((aligned(16))) pf_smem sm;
   __shared__ int s_tile;
@@ -797,10 +887,10 @@ __global__ void __launch_bounds__(256, PF_OCC) k_pf_moe(dsh_layer_t L, const pf_
   const pf_item it = items[item];
   if (!(d & PF_DN_TILE)) {
     if (it.seg == L.E)
-      gate_up_dispatch<true>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Shi, Slo, hps, sm);
+      gate_up_dispatch<true>(L, it, nt, X0, X1, xsc, xsum, pair_tok, bf16sim, hq.s0, hq.s1, hps, hms, sm);
     else
-      gate_up_dispatch<false>(L, it, nt, Xhi, Xlo, xsum, pair_tok, bf16sim, Hhi, Hlo, hpr, sm);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's h stores are in L2
+      gate_up_dispatch<false>(L, it, nt, X0, X1, xsc, xsum, pair_tok, bf16sim, hq.r0, hq.r1, hpr, hmr, sm);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's limb and partial stores are in L2
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_fetch_add(Q.gu_done + item, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
@@ -817,9 +907,9 @@ __global__ void __launch_bounds__(256, PF_OCC) k_pf_moe(dsh_layer_t L, const pf_
     }
     __syncthreads();
     if (it.seg == L.E)
-      down_dispatch<true>(L, it, nt, Shi, Slo, hps, Ysh, sm);
+      down_dispatch<true>(L, it, nt, hq.s0, hq.s1, hps, hms, Ysh, sm);
     else
-      down_dispatch<false>(L, it, nt, Hhi, Hlo, hpr, Y, sm);
+      down_dispatch<false>(L, it, nt, hq.r0, hq.r1, hpr, hmr, Y, sm);
   }
 }
 
@@ -893,17 +983,19 @@ __global__ void __launch_bounds__(256) k_pf_combine(const float *__restrict__ X,
 // ---------------------------------------------------------------------------------- launchers
 namespace {
 struct pf_ws {
-  __bf16 *Xhi, *Xlo;
+  int8_t *X0, *X1;  // x as two int8 limbs [T][H]
+  float *xsc;       // their scale per token
   float *xsum;
   int *idx;
   float *w;
   int *seg_off, *counts;
   pf_item *items;
   int *pair_tok, *pos_of;
-  __bf16 *Hhi, *Hlo, *Shi, *Slo;
+  pf_hq hq;         // SwiGLU outputs h as int8 limbs: routed [TK][I], shared [T][SI]
   float *Y, *Ysh;
   float *ps;        // [T][4][64] partial router scores
   float *hpr, *hps; // Σh partials per (row, gate_up n-tile): routed [TK][I/128], shared [T][SI/128]
+  float *hmr, *hms; // max |h| per (row, gate_up n-tile), same layout
   int *tiles_gu, *tiles_dn;  // routed GEMM tiles (item << 8 | n-tile) in launch order
   int *qtiles, *qcount, *qnext, *gu_done, *err;  // fused kernel: work queues, counters, wait error
 };
@@ -939,8 +1031,9 @@ size_t pf_carve(const dsh_layer_t *L, int T, void *base, pf_ws *w) {
     if (w) w->field = (type *)(b + off);                  \
     off += al256(sizeof(type) * (size_t)(count));         \
   } while (0)
-  TAKE(Xhi, __bf16, T * H);
-  TAKE(Xlo, __bf16, T * H);
+  TAKE(X0, int8_t, T * H);
+  TAKE(X1, int8_t, T * H);
+  TAKE(xsc, float, T);
   TAKE(xsum, float, T);
   TAKE(idx, int, TK);
   TAKE(w, float, TK);
@@ -949,15 +1042,17 @@ size_t pf_carve(const dsh_layer_t *L, int T, void *base, pf_ws *w) {
   TAKE(items, pf_item, pf_max_routed_items(L, T) + pf_shared_items(T));
   TAKE(pair_tok, int, TK);
   TAKE(pos_of, int, TK);
-  TAKE(Hhi, __bf16, TK * I);
-  TAKE(Hlo, __bf16, TK * I);
-  TAKE(Shi, __bf16, T * SI);
-  TAKE(Slo, __bf16, T * SI);
+  TAKE(hq.r0, int8_t, TK * I);
+  TAKE(hq.r1, int8_t, TK * I);
+  TAKE(hq.s0, int8_t, T * SI);
+  TAKE(hq.s1, int8_t, T * SI);
   TAKE(Y, float, TK * H);
   TAKE(Ysh, float, T * H);
   TAKE(ps, float, (size_t)T * 4 * 64);
   TAKE(hpr, float, TK * (I / PF_GU_N));
   TAKE(hps, float, (size_t)T * (SI / PF_GU_N));
+  TAKE(hmr, float, TK * (I / PF_GU_N));
+  TAKE(hms, float, (size_t)T * (SI / PF_GU_N));
   TAKE(tiles_gu, int, (size_t)pf_max_routed_items(L, T) * (I / PF_GU_N));
   TAKE(tiles_dn, int, (size_t)pf_max_routed_items(L, T) * (H / PF_DN_N));
   TAKE(qtiles, int, (size_t)PF_NQ * pf_queue_cap(L, T));
@@ -977,6 +1072,8 @@ int dsh_pf_supported(const dsh_layer_t *L) {
   if (L->H % PF_KS || L->I % PF_KS || L->SI % PF_KS) return 0;
   if (L->E > 64 || L->K > 64 || L->K > L->E) return 0;
   if ((size_t)PF_TB * L->H * sizeof(float) > 96 * 1024) return 0;  // DECODE scores: x rows in LDS
+  if (L->H > 256 * PF_SEL_U) return 0;                              // k_pf_select holds a row per wave
+  if (L->I > PF_KS * PF_NT_MAX || L->SI > PF_KS * PF_NT_MAX) return 0;  // down: exponent table per row
   return 1;
 }
 
@@ -1044,11 +1141,12 @@ hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int r
       k_pf_scores_cfg<16><<<g, 256, 0, s>>>(L->router_f32_t, X, T, H, E, w.ps);
     else
       k_pf_scores_cfg<8><<<g, 256, 0, s>>>(L->router_f32_t, X, T, H, E, w.ps);
-    k_pf_select<DSH_ROUTE_CFG><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, w.Xhi, w.Xlo, w.xsum, w.idx, w.w);
+    k_pf_select<DSH_ROUTE_CFG><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, w.X0, w.X1, w.xsc, w.xsum, w.idx,
+                                                            w.w);
   } else {
     k_pf_scores_bf16<<<(T + PF_TB - 1) / PF_TB, 256, (size_t)PF_TB * H * sizeof(float), s>>>(
         L->router_bf16, X, T, H, E, nthreads, w.ps);
-    k_pf_select<DSH_ROUTE_DECODE><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, w.Xhi, w.Xlo, w.xsum, w.idx,
+    k_pf_select<DSH_ROUTE_DECODE><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, w.X0, w.X1, w.xsc, w.xsum, w.idx,
                                                                 w.w);
   }
   const int n_items_max = pf_max_routed_items(L, T) + pf_shared_items(T);
@@ -1061,14 +1159,14 @@ hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int r
     // blocks per XCD >= tiles of the longest queue (at most ceil(items / PF_NQ) items)
     const int per_item = max(L->I / PF_GU_N, L->SI / PF_GU_N) + H / PF_DN_N;
     const int blocks = PF_NQ * ((n_items_max + PF_NQ - 1) / PF_NQ) * per_item;
-    k_pf_moe<<<blocks, 256, 0, s>>>(*L, w.items, Q, w.Xhi, w.Xlo, w.xsum, w.pair_tok, bf16sim, w.Hhi,
-                                         w.Hlo, w.Shi, w.Slo, w.hpr, w.hps, w.Y, w.Ysh);
+    k_pf_moe<<<blocks, 256, 0, s>>>(*L, w.items, Q, w.X0, w.X1, w.xsc, w.xsum, w.pair_tok, bf16sim, w.hq, w.hpr,
+                                    w.hps, w.hmr, w.hms, w.Y, w.Ysh);
   } else {
     k_pf_gate_up<<<pf_grid(L, T, L->SI / PF_GU_N, L->I / PF_GU_N), 256, 0, s>>>(
-        *L, w.items, w.counts, w.Xhi, w.Xlo, w.xsum, w.pair_tok, bf16sim, w.Hhi, w.Hlo, w.Shi, w.Slo, w.hpr, w.hps,
+        *L, w.items, w.counts, w.X0, w.X1, w.xsc, w.xsum, w.pair_tok, bf16sim, w.hq, w.hpr, w.hps, w.hmr, w.hms,
         w.tiles_gu);
-    k_pf_down<<<pf_grid(L, T, H / PF_DN_N, H / PF_DN_N), 256, 0, s>>>(*L, w.items, w.counts, w.Hhi, w.Hlo, w.Shi,
-                                                                       w.Slo, w.hpr, w.hps, w.Y, w.Ysh, w.tiles_dn);
+    k_pf_down<<<pf_grid(L, T, H / PF_DN_N, H / PF_DN_N), 256, 0, s>>>(*L, w.items, w.counts, w.hq, w.hpr, w.hps,
+                                                                       w.hmr, w.hms, w.Y, w.Ysh, w.tiles_dn);
   }
   k_pf_combine<<<T, 256, 0, s>>>(X, w.idx, w.w, w.pos_of, w.Y, w.Ysh, H, K, residual, bf16sim, out);
   hipError_t e = hipGetLastError();
