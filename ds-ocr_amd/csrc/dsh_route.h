@@ -4,31 +4,21 @@
 #include "dsh.h"
 #include "k_core.h"
 
-// LDS scratch of one selecting wave.
-struct route_scratch {
-  alignas(16) float key[64];  // each expert's order value (-inf: not selectable)
-  int sel[64];                // expert at each rank
-  float val[64];              // its score (CFG) or probability (DECODE)
-};
-
 // One wave, lane = expert; s_red (LDS, visible to the wave) holds four partial score rows, added
 // in row order. Writes s_idx[0..K) and s_w[0..K) (visible to this wave after it returns).
 //
 // Order: larger value first, lower index on equal values, NaN and values <= -1e30 never selected,
 // ±0 equal (the reference's strict '>' scans, ds_kernels.c:193-243, ds_moe_decoder.c:160-183).
-// Each selectable lane counts the values above its own (64 broadcast reads of the wave's values in
-// LDS, one f32 compare each): with no equal values that count is its selection round, the same as
-// K successive arg-max rounds. Lanes whose count is below K write their slot and read it back; two
-// equal values give two lanes the same count, which that read-back detects, and then every lane
-// recounts with the index tie-break (values above its own, plus equal values at lower indices).
+// Selection runs in registers: round r takes the wave maximum of the keys still in play, the
+// lowest lane holding a key equal to it (ballot; -0 and +0 compare equal) becomes rank r, and its
+// key drops out; the same order as K successive arg-max scans.
 // CFG (ds_moe_top_k): top-K on the raw scores, then softmax over the K chosen in selection order
 // (correctly rounded expf, max first, sequential sum); slots past the selectable count get expert 0
 // and weight 0.
 // DECODE (ds_moe_decoder.c:145-183): fast-exp softmax over all experts (max, sequential sum in
 // expert order, 1/sum), top-K on the probabilities, weights = those probabilities; empty slots get
 // expert -1 and weight -1e30.
-__device__ __forceinline__ void route_select(int E, int K, int mode, int *s_idx, float *s_w, float (*s_red)[64],
-                                             route_scratch *scr) {
+__device__ __forceinline__ void route_select(int E, int K, int mode, int *s_idx, float *s_w, float (*s_red)[64]) {
   const int lane = threadIdx.x & 63;
   const float s = ((s_red[0][lane] + s_red[1][lane]) + s_red[2][lane]) + s_red[3][lane];
   float v = s;
@@ -44,46 +34,22 @@ __device__ __forceinline__ void route_select(int E, int K, int mode, int *s_idx,
     v = p * inv;
   }
   const bool selectable = lane < E && v > -1e30f;  // false for NaN
-  const float vk = selectable ? v : -__builtin_huge_valf();
-  scr->key[lane] = vk;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  int rank = 0;
-#pragma unroll
-  for (int j = 0; j < 64; j++) rank += scr->key[j] > vk ? 1 : 0;
+  float key = selectable ? v : -__builtin_huge_valf();
   const int nsel = __popcll(__ballot(selectable));
   const int ns = nsel < K ? nsel : K;  // experts selected
-  bool put = selectable && rank < K;
-  if (put) {
-    scr->sel[rank] = lane;
-    scr->val[rank] = v;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const bool mine = lane < ns;
-  int my_sel = scr->sel[lane];
-  float my_val = scr->val[lane];
-  if (__ballot(put && scr->sel[rank] != lane)) {  // equal values among the first K: index tie-break
-    rank = 0;
-    for (int j = 0; j < 64; j++) {
-      const float kj = scr->key[j];
-      rank += (kj > vk || (kj == vk && j < lane)) ? 1 : 0;
+  int my_sel = 0;           // lane r < ns: the expert of rank r
+  float my_val = -1e30f;    // and its value
+  for (int r = 0; r < ns; r++) {  // r < nsel: a selectable key (> -inf) is still in play
+    const float m = dsh_wave_max(key);
+    const unsigned long long eq = __ballot(key == m);
+    const int win = __builtin_ctzll(eq);
+    const float wv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), win));
+    if (lane == r) {
+      my_sel = win;
+      my_val = wv;
     }
-    put = selectable && rank < K;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the reads above are done
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (put) {
-      scr->sel[rank] = lane;
-      scr->val[rank] = v;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    my_sel = scr->sel[lane];
-    my_val = scr->val[lane];
+    if (lane == win) key = -__builtin_huge_valf();
   }
   my_sel = mine ? my_sel : 0;
   my_val = mine ? my_val : -1e30f;

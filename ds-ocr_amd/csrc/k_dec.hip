@@ -203,7 +203,7 @@ __global__ void __launch_bounds__(64) k_dec_scores_bf16(const uint16_t *__restri
 template <int CPL>
 __device__ __forceinline__ void gate_up_body(const dsh_layer_t &L, const float *x, const float *partials, int np,
                                              int mode, int bf16sim, const dsh_layer_work_t &wk, int blk, int *s_idx,
-                                             float *s_w, float (*s_red)[64], route_scratch *s_scr, float *s_stat,
+                                             float *s_w, float (*s_red)[64], float *s_stat,
                                              unsigned *s_lq) {
   constexpr int XV = (64 * CPL + 255) / 256;  // 16-byte pieces of x per thread
   constexpr int NP = 64 * CPL;                // pieces (4 elements) of x, = words per limb array
@@ -260,7 +260,7 @@ __device__ __forceinline__ void gate_up_body(const dsh_layer_t &L, const float *
   int ru = 0, r = 0, e = 0;
   float2 sog, sou;
   if (!shared_wave) {
-    route_select(L.E, K, mode, s_idx + 64 * wave, s_w + 64 * wave, s_red, s_scr + wave);
+    route_select(L.E, K, mode, s_idx + 64 * wave, s_w + 64 * wave, s_red);
     s_idx += 64 * wave;
     s_w += 64 * wave;
     ru = blk * 12 + (wave - 1) * 4 + grp;
@@ -356,11 +356,10 @@ __global__ void __launch_bounds__(256) k_dec_gate_up(dsh_layer_t L, const float 
   __shared__ int s_idx[4 * 64];
   __shared__ float s_w[4 * 64];
   __shared__ float s_red[4][64];
-  __shared__ route_scratch s_scr[4];
   __shared__ float s_stat[8];
   __shared__ __attribute__((aligned(16))) unsigned s_lq[4 * 64 * CPL];
   gate_up_body<CPL>(L, at_step(x_in, step, stride), partials, np, mode, bf16sim, wk, blockIdx.x, s_idx, s_w, s_red,
-                    s_scr, s_stat, s_lq);
+                    s_stat, s_lq);
 }
 
 // ============================================================================ down + combine
@@ -513,7 +512,6 @@ __global__ void __launch_bounds__(320) k_sim_gate_up(dsh_layer_t L, const float 
   __shared__ int s_idx[4 * 64];
   __shared__ float s_w[4 * 64];
   __shared__ float s_red[4][64];
-  __shared__ route_scratch s_scr[4];
   __shared__ float s_up[128];
   __shared__ float s_xsum;
   const float *x = at_step(x_in, step, stride);
@@ -544,7 +542,7 @@ __global__ void __launch_bounds__(320) k_sim_gate_up(dsh_layer_t L, const float 
       s_xsum = xs;
     }
   } else {
-    route_select(L.E, K, mode, s_idx + 64 * wave, s_w + 64 * wave, s_red, s_scr + wave);
+    route_select(L.E, K, mode, s_idx + 64 * wave, s_w + 64 * wave, s_red);
     if (active) {
       const int8_t *row;
       if (u < KI) {

@@ -71,47 +71,55 @@ __device__ __forceinline__ void dl_issue(dl_regs<CPL> &R, const int8_t *gu, cons
   }
 }
 
-// x_out copies [DL_REP][H] and lg_out copies [DL_REP][64] must be zero when the kernel starts
-// (the kernel of the layer after next, or the final sum, clears them: zero_p/zero_n).
-// NREP: copies of the input (1: a plain vector at x_in + step*stride); RB: router partial rows
-// loaded per wave by waves 0-3 (np <= 4 * RB).
-template <int CPL, int NREP, int RB>
-__global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F, const float *x_in,
-                                                   const int *__restrict__ step, int stride,
-                                                   const float *partials, int np, int mode,
-                                                   const float *__restrict__ resid, float *x_out, float *lg_out,
-                                                   float *zero_p, int zero_n) {
-  constexpr int H = 256 * CPL, NP = 64 * CPL, XV = (NP + 511) / 512, NL = 4;
-  __shared__ int s_idx[8 * 64];
-  __shared__ float s_w[8 * 64];
-  __shared__ float s_red[4][64];
-  __shared__ route_scratch s_scr[8];
-  __shared__ float s_stat[16];
-  __shared__ __attribute__((aligned(16))) unsigned s_lq[NL * NP];
-  __shared__ __attribute__((aligned(16))) float s_x[H];
-  __shared__ __attribute__((aligned(16))) float s_h[DL_UB];
-  __shared__ float s_dn[H];
-  __shared__ float s_lg[8][64];
+// LDS of one layer block.
+template <int CPL>
+struct dl_smem {
+  static constexpr int H = 256 * CPL, NP = 64 * CPL, NL = 4;
+  int s_idx[64];
+  float s_w[64];
+  float s_red[4][64];
+  float s_stat[16];
+  __attribute__((aligned(16))) unsigned s_lq[NL * NP];
+  __attribute__((aligned(16))) float s_x[H];
+  __attribute__((aligned(16))) float s_h[DL_UB];
+  float s_dn[H];
+  float s_lg[8][64];
+};
+
+// The block's work; SH: a shared-expert block (a compile-time split, so each kind of block runs
+// straight-line code and every wait for a load counts only that kind's own loads).
+template <int CPL, int NREP, int RB, bool SH>
+__device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t &F, const float *x_in,
+                                        const int *__restrict__ step, int stride, const float *partials, int np,
+                                        int mode, const float *__restrict__ resid, float *x_out, float *lg_out,
+                                        float *zero_p, int zero_n, dl_smem<CPL> &S) {
+  // x pieces (4 values each): routed blocks leave wave 0 free to select the expert while waves 1-7
+  // load and sum the input, so piece p belongs to thread XO + p % XT of round p / XT
+  constexpr int XO = SH ? 0 : 64, XT = 512 - XO;
+  constexpr int H = 256 * CPL, NP = 64 * CPL, XV = (NP + XT - 1) / XT, NL = 4;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, sub = lane & 15, grp = lane >> 4;
   const int th = t & 255, half = t >> 8;
   const int I = L.I, SI = L.SI, NS = SI / DL_UB, NSL = I / DL_UB, blk = blockIdx.x;
-  const bool shared_blk = blk < NS;
+  constexpr bool shared_blk = SH;
   const int rb = blk - NS, slot = shared_blk ? 0 : rb / NSL, sl = shared_blk ? blk : rb - slot * NSL;
   const float *x = step ? x_in + (size_t)(*step) * stride : x_in;
 
   for (int i = blk * 512 + t; i < zero_n; i += gridDim.x * 512) zero_p[i] = 0.0f;
 
-  f32x4 xr[XV][NREP];
-#pragma unroll
-  for (int j = 0; j < XV; j++)
-#pragma unroll
-    for (int c = 0; c < NREP; c++) xr[j][c] = ((const f32x4 *)(x + (size_t)c * H))[min(t + 512 * j, NP - 1)];
-  asm volatile("" ::: "memory");
+  // Loads in the order they are needed (a wave's loads complete in issue order): the router
+  // partials, then the input copies, the residual rows and the next router's rows.
   float pv[RB];
   if (!shared_blk && wave < 4) {
 #pragma unroll
     for (int j = 0; j < RB; j++) pv[j] = partials[(size_t)min(wave + 4 * j, np - 1) * 64 + lane];
   }
+  asm volatile("" ::: "memory");
+  f32x4 xr[XV][NREP];
+#pragma unroll
+  for (int j = 0; j < XV; j++)
+#pragma unroll
+    for (int c = 0; c < NREP; c++) xr[j][c] = ((const f32x4 *)(x + (size_t)c * H))[min(max(t - XO, 0) + XT * j, NP - 1)];
+  asm volatile("" ::: "memory");
   float rv[CPL];  // block 0: the residual rows it adds (when it is not the input)
   if (blk == 0 && resid && !half) {
 #pragma unroll
@@ -124,11 +132,30 @@ __global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F,
     for (int j = 0; j < 8; j++) wr[j] = F.WrT_next[(size_t)(blk * 8 + j) * F.E_next + lane];
   }
   asm volatile("" ::: "memory");
+  if (!shared_blk && wave < 4) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < RB; j++)
+      if (wave + 4 * j < np) acc += pv[j];
+    S.s_red[wave][lane] = lane < L.E ? acc : 0.0f;
+  }
+  __syncthreads();  // s_red
+
+  // Shared-expert blocks stream their weights at once. Routed blocks select their expert, then
+  // issue its weights only after the block's last barrier before the dot products: a wave's loads
+  // are accepted only as fast as the memory system drains them, so a barrier behind them would hold
+  // every wave until the block's whole stream has gone out; without one, each wave starts its gate
+  // and up products when its own rows arrive, while the down tile is still streaming.
   dl_regs<CPL> R;
-  if (shared_blk)
+  float wexp = 1.0f;  // this block's expert weight (1 for the shared expert)
+  int e = 0;
+  if constexpr (shared_blk) {
     dl_issue<CPL>(R, L.sgu_q, L.sgu_so, (size_t)sl * DL_UB, (size_t)SI + sl * DL_UB,
                   F.sdnT + (size_t)sl * DL_UB * H, L.sdn_so, F.sM ? F.sM + (size_t)sl * 2048 : nullptr, F.sz);
-  asm volatile("" ::: "memory");
+    asm volatile("" ::: "memory");
+  } else if (wave == 0) {  // the selection, read by every wave after the next barrier
+    route_select(L.E, L.K, mode, S.s_idx, S.s_w, S.s_red);
+  }
 
   // x: the copies summed in copy order; max|x| and Σx per wave
   f32x4 xs[XV];
@@ -139,9 +166,9 @@ __global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F,
       xs[j] = xr[j][0];
 #pragma unroll
       for (int c = 1; c < NREP; c++) xs[j] += xr[j][c];
-      const int p = t + 512 * j;
-      const bool own = p < NP;
-      if (own) *(f32x4 *)(s_x + 4 * p) = xs[j];
+      const int p = t - XO + XT * j;
+      const bool own = t >= XO && p < NP;
+      if (own) *(f32x4 *)(S.s_x + 4 * p) = xs[j];
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         mx = own ? fmaxf(mx, fabsf(xs[j][c])) : mx;
@@ -151,44 +178,31 @@ __global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F,
     mx = dsh_wave_max(mx);
     sx = dsh_wave_sum(sx);
     if (lane == 0) {
-      s_stat[wave] = mx;
-      s_stat[8 + wave] = sx;
+      S.s_stat[wave] = mx;
+      S.s_stat[8 + wave] = sx;
     }
   }
-  if (!shared_blk && wave < 4) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < RB; j++)
-      if (wave + 4 * j < np) acc += pv[j];
-    s_red[wave][lane] = lane < L.E ? acc : 0.0f;
-  }
-  __syncthreads();  // s_red, s_stat, s_x
-  float xmax = s_stat[0], xsum = s_stat[8];
+  __syncthreads();  // s_stat, s_x
+  float xmax = S.s_stat[0], xsum = S.s_stat[8];
 #pragma unroll
   for (int w = 1; w < 8; w++) {
-    xmax = fmaxf(xmax, s_stat[w]);
-    xsum += s_stat[8 + w];
+    xmax = fmaxf(xmax, S.s_stat[w]);
+    xsum += S.s_stat[8 + w];
   }
   const int ex = __builtin_amdgcn_frexp_expf(xmax);  // xmax < 2^ex
-
-  float wexp = 1.0f;  // this block's expert weight (1 for the shared expert)
-  if (!shared_blk) {
-    route_select(L.E, L.K, mode, s_idx + 64 * wave, s_w + 64 * wave, s_red, s_scr + wave);
-    int e = s_idx[64 * wave + slot];
-    wexp = s_w[64 * wave + slot];
+  if constexpr (!shared_blk) {
+    e = S.s_idx[slot];
+    wexp = S.s_w[slot];
     if (e < 0) {  // DECODE routing left this slot empty: expert 0's rows, added with weight 0
       e = 0;
       wexp = 0.0f;
     }
-    const size_t g0 = (size_t)e * 2 * I + (size_t)sl * DL_UB;
-    const size_t tile = (size_t)e * NSL + sl;
-    dl_issue<CPL>(R, L.gu_q, L.gu_so, g0, g0 + I, F.dnT + tile * DL_UB * H, L.dn_so + (size_t)e * H * 2,
-                  F.M ? F.M + tile * 2048 : nullptr, F.z ? F.z + (size_t)e * 64 : nullptr);
   }
+
   // x → limbs, piece p (elements 4p..4p+3) into word p of each limb array
 #pragma unroll
   for (int j = 0; j < XV; j++) {
-    const int p = t + 512 * j;
+    const int p = t - XO + XT * j;
     unsigned wl[NL] = {};
 #pragma unroll
     for (int c = 0; c < 4; c++) {
@@ -200,12 +214,19 @@ __global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F,
         X = (X - d) >> 8;
       }
     }
-    if (p < NP) {
+    if (t >= XO && p < NP) {
 #pragma unroll
-      for (int l = 0; l < NL; l++) s_lq[l * NP + p] = wl[l];
+      for (int l = 0; l < NL; l++) S.s_lq[l * NP + p] = wl[l];
     }
   }
   __syncthreads();  // limbs
+  if constexpr (!shared_blk) {
+    const size_t g0 = (size_t)e * 2 * I + (size_t)sl * DL_UB;
+    const size_t tile = (size_t)e * NSL + sl;
+    dl_issue<CPL>(R, L.gu_q, L.gu_so, g0, g0 + I, F.dnT + tile * DL_UB * H, L.dn_so + (size_t)e * H * 2,
+                  F.M ? F.M + tile * 2048 : nullptr, F.z ? F.z + (size_t)e * 64 : nullptr);
+    asm volatile("" ::: "memory");
+  }
   {
     int ag[NL] = {}, au[NL] = {};
 #pragma unroll
@@ -213,7 +234,7 @@ __global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F,
       const int c = sub + 16 * m;
 #pragma unroll
       for (int l = 0; l < NL; l++) {
-        const u32x4 lw = *(const u32x4 *)(s_lq + l * NP + 4 * c);
+        const u32x4 lw = *(const u32x4 *)(S.s_lq + l * NP + 4 * c);
 #pragma unroll
         for (int d = 0; d < 4; d++) {
           ag[l] = __builtin_amdgcn_sdot4((int)R.wg[m][d], (int)lw[d], ag[l], false);
@@ -232,13 +253,13 @@ __global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F,
     const float og = __builtin_fmaf(128.0f, R.sog.x, R.sog.y), ou = __builtin_fmaf(128.0f, R.sou.x, R.sou.y);
     const float g = __builtin_fmaf(R.sog.x, dg, og * xsum);
     const float up = __builtin_fmaf(R.sou.x, du, ou * xsum);
-    if (sub == 0) s_h[4 * wave + grp] = dsh_swiglu(g, up);
+    if (sub == 0) S.s_h[4 * wave + grp] = dsh_swiglu(g, up);
   }
   __syncthreads();  // s_h
   float hv[16];
 #pragma unroll
   for (int j = 0; j < 16; j += 4) {
-    const f32x4 v = *(const f32x4 *)(s_h + 16 * half + j);
+    const f32x4 v = *(const f32x4 *)(S.s_h + 16 * half + j);
     hv[j] = v[0];
     hv[j + 1] = v[1];
     hv[j + 2] = v[2];
@@ -249,20 +270,20 @@ __global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F,
   for (int k = 0; k < CPL; k++) dk[k] = dsh_dot16_u8(R.wd[k], hv, 0.0f);
   if (half) {
 #pragma unroll
-    for (int k = 0; k < CPL; k++) s_dn[th + 256 * k] = dk[k];
+    for (int k = 0; k < CPL; k++) S.s_dn[th + 256 * k] = dk[k];
   }
   if (F.M) {  // the next layer's router scores: this wave's four units
-    const f32x4 h4 = *(const f32x4 *)(s_h + 4 * wave);
+    const f32x4 h4 = *(const f32x4 *)(S.s_h + 4 * wave);
     float pm = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; j++) pm = __builtin_fmaf(R.mv[j], h4[j], pm);
-    s_lg[wave][lane] = pm;
+    S.s_lg[wave][lane] = pm;
   }
   __syncthreads();  // s_dn, s_lg
   float hs = 0.0f;  // Σh over the block's units
 #pragma unroll
   for (int j = 0; j < DL_UB; j += 4) {
-    const f32x4 v = *(const f32x4 *)(s_h + j);
+    const f32x4 v = *(const f32x4 *)(S.s_h + j);
     hs += v[0];
     hs += v[1];
     hs += v[2];
@@ -274,23 +295,42 @@ __global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F,
 #pragma unroll
     for (int k = 0; k < CPL; k++) {
       const int r = th + 256 * k;
-      const float d = dk[k] + s_dn[r];
+      const float d = dk[k] + S.s_dn[r];
       float c = wexp * __builtin_fmaf(R.dso[k].x, d, R.dso[k].y * hs);
-      if (blk == 0) c += resid ? rv[k] : s_x[r];  // the residual, added once
+      if (blk == 0) c += resid ? rv[k] : S.s_x[r];  // the residual, added once
       __hip_atomic_fetch_add(xo + r, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   if (F.M && wave == 0 && lane < F.E_next) {
-    float v = s_lg[0][lane];
+    float v = S.s_lg[0][lane];
 #pragma unroll
-    for (int w = 1; w < 8; w++) v += s_lg[w][lane];
+    for (int w = 1; w < 8; w++) v += S.s_lg[w][lane];
     v = wexp * __builtin_fmaf(R.zv, hs, v);
     if (base_blk) {
 #pragma unroll
-      for (int j = 0; j < 8; j++) v = __builtin_fmaf(wr[j], s_x[blk * 8 + j], v);
+      for (int j = 0; j < 8; j++) v = __builtin_fmaf(wr[j], S.s_x[blk * 8 + j], v);
     }
     __hip_atomic_fetch_add(lg_out + (size_t)cp * 64 + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+}
+
+// x_out copies [DL_REP][H] and lg_out copies [DL_REP][64] must be zero when the kernel starts
+// (the kernel of the layer after next, or the final sum, clears them: zero_p/zero_n).
+// NREP: copies of the input (1: a plain vector at x_in + step*stride); RB: router partial rows
+// loaded per wave by waves 0-3 (np <= 4 * RB). Blocks 0 .. SI/DL_UB - 1 run the shared expert.
+template <int CPL, int NREP, int RB>
+__global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F, const float *x_in,
+                                                   const int *__restrict__ step, int stride,
+                                                   const float *partials, int np, int mode,
+                                                   const float *__restrict__ resid, float *x_out, float *lg_out,
+                                                   float *zero_p, int zero_n) {
+  __shared__ dl_smem<CPL> S;
+  if ((int)blockIdx.x < L.SI / DL_UB)
+    dl_body<CPL, NREP, RB, true>(L, F, x_in, step, stride, partials, np, mode, resid, x_out, lg_out, zero_p, zero_n,
+                                 S);
+  else
+    dl_body<CPL, NREP, RB, false>(L, F, x_in, step, stride, partials, np, mode, resid, x_out, lg_out, zero_p,
+                                  zero_n, S);
 }
 
 // out[i] = Σ_c X[c][i] in copy order, then X is cleared; zero_p[0..zero_n) is cleared too.

@@ -194,7 +194,6 @@ __global__ void __launch_bounds__(256) k_pf_select(const float *__restrict__ X, 
   __shared__ float s_red[4][4][64];
   __shared__ int s_idx[4][64];
   __shared__ float s_w[4][64];
-  __shared__ route_scratch s_scr[4];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;  // no block-wide barriers below
@@ -239,7 +238,7 @@ __global__ void __launch_bounds__(256) k_pf_select(const float *__restrict__ X, 
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  route_select(E, K, MODE, s_idx[wave], s_w[wave], s_red[wave], s_scr + wave);
+  route_select(E, K, MODE, s_idx[wave], s_w[wave], s_red[wave]);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
