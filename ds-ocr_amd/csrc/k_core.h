@@ -73,6 +73,7 @@ typedef struct {
   const float *router_f32;     /* [E][H] */
   const float *router_f32_t;   /* [H][E]: the same f32 router transposed (partial scores read rows) */
   const uint16_t *router_bf16; /* [E][H] */
+  const float *router_norm;    /* [E]: ||router_f32 row||_2, rounded up (bounds on score rounding) */
   int H, I, E, K, SI;
 } dsh_layer_t;
 
@@ -160,6 +161,8 @@ hipError_t dsh_launch_dense_down(const uint16_t *Wd, const float *h, const float
                                  int H, int I, int residual, const float *resid, float *x_out, const float *WrT_next,
                                  int E_next, float *partials_next, hipStream_t s);
 hipError_t dsh_launch_transpose_f32(const float *src, float *dst, int rows, int cols, hipStream_t s);
+/* out[r] = ||A[r][0..cols)||_2 in f64, rounded up to f32. */
+hipError_t dsh_launch_row_norms(const float *A, int rows, int cols, float *out, hipStream_t s);
 hipError_t dsh_launch_dec_partial_scores(const float *WrT, const float *x_in, const int *step, int stride, int H, int E,
                                          float *partials, hipStream_t s);
 hipError_t dsh_launch_dec_scores_bf16(const uint16_t *Wr, const float *x_in, const int *step, int stride, int H, int E,

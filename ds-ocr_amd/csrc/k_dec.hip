@@ -121,6 +121,23 @@ __global__ void __launch_bounds__(64) k_dec_scores_f32_exact(const float *__rest
   partials[lane] = lane < E ? sc : 0.0f;
 }
 
+// out[r] = the Euclidean norm of row r, summed in f64 and rounded up to f32 (one block per row).
+__global__ void __launch_bounds__(256) k_row_norms(const float *__restrict__ A, int cols, float *__restrict__ out) {
+  __shared__ double s[4];
+  const float *a = A + (size_t)blockIdx.x * cols;
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < cols; i += 256) acc += (double)a[i] * (double)a[i];
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+  if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const double n = sqrt(((s[0] + s[1]) + s[2]) + s[3]);
+    float f = (float)n;
+    if ((double)f < n) f = __uint_as_float(__float_as_uint(f) + 1u);  // next float up (n >= 0, finite)
+    out[blockIdx.x] = f;
+  }
+}
+
 // dst[c][r] = src[r][c] for a rows x cols f32 matrix (32x32 tiles through LDS).
 __global__ void __launch_bounds__(256) k_transpose_f32(const float *__restrict__ src, float *__restrict__ dst, int rows,
                                                        int cols) {
@@ -866,6 +883,12 @@ int dsh_dec_supported(int H, int I, int E, int K, int SI) {
 }
 
 int dsh_dec_partials(int H) { return H / dec_rows(H); }
+
+hipError_t dsh_launch_row_norms(const float *A, int rows, int cols, float *out, hipStream_t s) {
+  if (rows <= 0 || cols <= 0) return hipErrorInvalidValue;
+  k_row_norms<<<rows, 256, 0, s>>>(A, cols, out);
+  return hipGetLastError();
+}
 
 hipError_t dsh_launch_transpose_f32(const float *src, float *dst, int rows, int cols, hipStream_t s) {
   k_transpose_f32<<<dim3((cols + 31) / 32, (rows + 31) / 32), 256, 0, s>>>(src, dst, rows, cols);

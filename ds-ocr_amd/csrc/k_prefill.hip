@@ -184,13 +184,24 @@ __global__ void __launch_bounds__(256) k_pf_scores_bf16(const uint16_t *__restri
 // expert selection from the four partial score rows (route_select: CFG top-k on raw scores +
 // softmax over the k; DECODE fast-exp softmax over all experts + top-k). H <= 256·PF_SEL_U: the
 // wave holds the whole row in registers.
+//
+// CFG: the partial-sum scores differ from ds_linear's sequential ones (ds_kernels.c:639-652) only
+// by rounding. Any order of the H products is within γ_{H+1}·Σ|w_i x_i| <= γ_{H+1}·||w_e||·||x|| of
+// the exact dot product (γ_n = n·u / (1 - n·u), u = 2^-24), so the two differ by at most
+// ε_e = 2·γ_{H+1}·||w_e||·||x||. The selection stands as it is when the intervals [s_e - ε_e,
+// s_e + ε_e] of the selected experts, taken in rank order, and of the best unselected one are
+// disjoint: then ds_moe_top_k on the sequential scores (ds_kernels.c:193-243) picks the same
+// experts in the same order. Otherwise the experts whose interval reaches the lowest selected
+// lower bound (the only ones that can be among the top K) are written as the token's candidate
+// mask, and k_pf_exact recomputes their scores in ds_linear's order and selects again.
 #define PF_SEL_U 8  // x float4 loads per lane
 template <int MODE>
 __global__ void __launch_bounds__(256) k_pf_select(const float *__restrict__ X, int T, int H, int E, int K,
-                                                   const float *__restrict__ ps, int8_t *__restrict__ X0,
-                                                   int8_t *__restrict__ X1, float *__restrict__ xsc,
-                                                   float *__restrict__ xsum, int *__restrict__ idx,
-                                                   float *__restrict__ w) {
+                                                   const float *__restrict__ ps, const float *__restrict__ wnorm,
+                                                   int8_t *__restrict__ X0, int8_t *__restrict__ X1,
+                                                   float *__restrict__ xsc, float *__restrict__ xsum,
+                                                   int *__restrict__ idx, float *__restrict__ w,
+                                                   unsigned long long *__restrict__ cmask) {
   __shared__ float s_red[4][4][64];
   __shared__ int s_idx[4][64];
   __shared__ float s_w[4][64];
@@ -204,13 +215,15 @@ __global__ void __launch_bounds__(256) k_pf_select(const float *__restrict__ X, 
   f32x4 xv[PF_SEL_U];
 #pragma unroll
   for (int u = 0; u < PF_SEL_U; u++) xv[u] = src[min(64 * u + lane, nc - 1)];
-  float s = 0.0f, mx = 0.0f;
+  float s = 0.0f, mx = 0.0f, ss = 0.0f;
 #pragma unroll
   for (int u = 0; u < PF_SEL_U; u++) {
     if (64 * u + lane >= nc) continue;
     const f32x4 v = xv[u];
     s += (v[0] + v[1]) + (v[2] + v[3]);
     mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v[0]), fabsf(v[1]))), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    if constexpr (MODE == DSH_ROUTE_CFG)
+      ss = __builtin_fmaf(v[3], v[3], __builtin_fmaf(v[2], v[2], __builtin_fmaf(v[1], v[1], __builtin_fmaf(v[0], v[0], ss))));
   }
   s = dsh_wave_sum(s);
   mx = dsh_wave_max(mx);
@@ -242,9 +255,155 @@ __global__ void __launch_bounds__(256) k_pf_select(const float *__restrict__ X, 
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if constexpr (MODE == DSH_ROUTE_CFG) {
+    // ||x|| from the f32 sum of squares (relative error below γ_H / 2 + u; 1e-4 covers it), the
+    // rounding margin of every expert, and the check of the selection in rank order
+    const float xn = __builtin_sqrtf(dsh_wave_sum(ss)) * 1.0001f;
+    const float un = 5.9604645e-8f * (float)(H + 1);
+    const float gam = 2.0f * un / (1.0f - un) * 1.0001f;
+    const float sc = ((s_red[wave][0][lane] + s_red[wave][1][lane]) + s_red[wave][2][lane]) + s_red[wave][3][lane];
+    const bool selectable = lane < E && sc > -1e30f;
+    const float eps = lane < E ? __builtin_fmaf(gam * xn, wnorm[lane], 1e-30f) : 0.0f;
+    const int ns = min(__popcll(__ballot(selectable)), K);
+    const int er = lane < ns ? s_idx[wave][lane] : 0;
+    const float vr = __shfl(sc, er), epr = __shfl(eps, er);
+    const float lo = vr - epr, hi = vr + epr;
+    const float hi_next = __shfl_down(hi, 1);
+    bool in_sel = false;
+    for (int r = 0; r < ns; r++) in_sel |= s_idx[wave][r] == lane;
+    const float hi_out = dsh_wave_max(selectable && !in_sel ? sc + eps : -__builtin_huge_valf());
+    const float lo_last = __shfl(lo, max(ns - 1, 0));
+    const bool bad = (lane < ns - 1 && !(lo > hi_next)) || (lane == 0 && ns > 0 && !(lo_last > hi_out));
+    unsigned long long m = 0ull;
+    if (__ballot(bad)) {  // not certain: the experts that can be in the top K
+      float lmin = lane < ns ? lo : __builtin_huge_valf();
+      lmin = -dsh_wave_max(-lmin);
+      m = __ballot(selectable && sc + eps >= lmin);
+    }
+    if (lane == 0) cmask[t] = m;
+  }
   if (lane < K) {
     idx[(size_t)t * K + lane] = s_idx[wave][lane];
     w[(size_t)t * K + lane] = s_w[wave][lane];
+  }
+}
+
+// CFG tokens whose selection the rounding bound could not confirm (cmask != 0): one block per
+// token; the candidates' router rows (up to G <= PF_EX_G at a time, G set so LDS stays within
+// 64 KB; rows H + 4 floats apart, so the lanes' 16-byte reads hit distinct banks) and x go to LDS, lane c of wave 0 sums candidate c's score in
+// ds_linear's order (ds_kernels.c:639-652 as GCC compiles it: rounded products added in index
+// order, the tail past the last multiple of 8 fused), the other experts are set aside, and the
+// selection and its softmax (route_select) run again: idx and w of the token are replaced.
+#define PF_EX_G 8
+#define PF_EX_LD ((PF_EX_G + 1) * 2048 / 4 / 256)  // f32x4 loads per thread for x and a group, H <= 2048
+__global__ void __launch_bounds__(256) k_pf_exact(const float *__restrict__ X, const float *__restrict__ Wr, int H,
+                                                  int E, int K, int G, const unsigned long long *__restrict__ cmask,
+                                                  int *__restrict__ idx, float *__restrict__ w) {
+  extern __shared__ __attribute__((aligned(16))) float s_dyn[];  // x [H], rows [G][H + 4]
+  __shared__ float s_red[4][64];
+  __shared__ int s_idx[64];
+  __shared__ float s_w[64];
+  const int t = blockIdx.x;
+  const unsigned long long mask = cmask[t];
+  if (!mask) return;
+  float *s_x = s_dyn, *s_rows = s_dyn + H;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q4 = H / 4;
+  bool first = true;
+  const int m = H >= 16 ? (H & ~15) + ((H - (H & ~15)) >= 8 ? 8 : 0) : (H >= 8 ? 8 : 0);
+  float mine = -1e30f;  // wave 0, lane e: the recomputed score of expert e (candidates only)
+  unsigned long long rest = mask;
+  while (rest) {
+    // the next PF_EX_G candidates (uniform), their rows into LDS
+    int ce[PF_EX_G], nc = 0;
+    while (rest && nc < G) {
+      ce[nc++] = __builtin_ctzll(rest);
+      rest &= rest - 1;
+    }
+    // every load of the group (and of x, with the first group) in flight before any store
+    const int n0 = first ? q4 : 0, tot = n0 + nc * q4;
+    f32x4 buf[PF_EX_LD];
+#pragma unroll
+    for (int j = 0; j < PF_EX_LD; j++) {
+      const int i = min((int)threadIdx.x + 256 * j, tot - 1);
+      const int c = (i - n0) / q4, o = i - n0 - c * q4;
+      buf[j] = i < n0 ? ((const f32x4 *)(X + (size_t)t * H))[i] : ((const f32x4 *)(Wr + (size_t)ce[min(c, nc - 1)] * H))[o];
+    }
+    __syncthreads();  // the previous group's reads are done
+#pragma unroll
+    for (int j = 0; j < PF_EX_LD; j++) {
+      const int i = threadIdx.x + 256 * j;
+      if (i >= tot) break;
+      const int c = (i - n0) / q4, o = i - n0 - c * q4;
+      if (i < n0)
+        ((f32x4 *)s_x)[i] = buf[j];
+      else
+        *(f32x4 *)(s_rows + (size_t)c * (H + 4) + 4 * o) = buf[j];
+    }
+    first = false;
+    __syncthreads();
+    if (wave == 0) {
+      float a = 0.0f;
+      if (lane < nc) {
+        // the rounded-product part (m is a multiple of 8) in steps of 16 values (a + x·r with
+        // contraction off: the product rounded, then the add), EX_D steps of LDS reads in flight
+        // (a ring of registers; the barriers keep each refill where it is written)
+        constexpr int EX_D = 4;
+        const f32x4 *x4 = (const f32x4 *)s_x, *r4 = (const f32x4 *)(s_rows + lane * (H + 4));
+        const int m16 = m & ~15, nst = m16 / 16;
+        f32x4 xq[EX_D][4], rq[EX_D][4];
+#pragma unroll
+        for (int d = 0; d < EX_D; d++)
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const int st = min(d, max(nst - 1, 0));
+            xq[d][q] = x4[4 * st + q];
+            rq[d][q] = r4[4 * st + q];
+          }
+        asm volatile("" ::: "memory");
+        for (int s0 = 0; s0 < nst; s0 += EX_D) {
+#pragma unroll
+          for (int d = 0; d < EX_D; d++) {
+            if (s0 + d < nst) {  // the step's 16 products first, then the dependent adds
+              float pr[16];
+#pragma unroll
+              for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) pr[4 * q + i] = xq[d][q][i] * rq[d][q][i];
+#pragma unroll
+              for (int j = 0; j < 16; j++) a = a + pr[j];
+            }
+            const int st = min(s0 + d + EX_D, max(nst - 1, 0));
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              xq[d][q] = x4[4 * st + q];
+              rq[d][q] = r4[4 * st + q];
+            }
+            asm volatile("" ::: "memory");
+          }
+        }
+        const float *rr = s_rows + lane * (H + 4);
+        for (int k = m16; k < m; k++) a = a + s_x[k] * rr[k];
+        for (int k = m; k < H; k++) a = __builtin_fmaf(s_x[k], rr[k], a);
+      }
+      for (int c = 0; c < nc; c++) {
+        const float v = __shfl(a, c);
+        if (lane == ce[c]) mine = v;
+      }
+    }
+  }
+  if (wave == 0) {
+    s_red[0][lane] = lane < E ? mine : -1e30f;
+    s_red[1][lane] = 0.0f;
+    s_red[2][lane] = 0.0f;
+    s_red[3][lane] = 0.0f;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    route_select(E, K, DSH_ROUTE_CFG, s_idx, s_w, s_red);
+    if (lane < K) {
+      idx[(size_t)t * K + lane] = s_idx[lane];
+      w[(size_t)t * K + lane] = s_w[lane];
+    }
   }
 }
 
@@ -995,6 +1154,7 @@ struct pf_ws {
   float *ps;        // [T][4][64] partial router scores
   float *hpr, *hps; // Σh partials per (row, gate_up n-tile): routed [TK][I/128], shared [T][SI/128]
   float *hmr, *hms; // max |h| per (row, gate_up n-tile), same layout
+  unsigned long long *cmask;  // CFG: per token, the experts whose scores are recomputed (0: none)
   int *tiles_gu, *tiles_dn;  // routed GEMM tiles (item << 8 | n-tile) in launch order
   int *qtiles, *qcount, *qnext, *gu_done, *err;  // fused kernel: work queues, counters, wait error
 };
@@ -1052,6 +1212,7 @@ size_t pf_carve(const dsh_layer_t *L, int T, void *base, pf_ws *w) {
   TAKE(hps, float, (size_t)T * (SI / PF_GU_N));
   TAKE(hmr, float, TK * (I / PF_GU_N));
   TAKE(hms, float, (size_t)T * (SI / PF_GU_N));
+  TAKE(cmask, unsigned long long, T);
   TAKE(tiles_gu, int, (size_t)pf_max_routed_items(L, T) * (I / PF_GU_N));
   TAKE(tiles_dn, int, (size_t)pf_max_routed_items(L, T) * (H / PF_DN_N));
   TAKE(qtiles, int, (size_t)PF_NQ * pf_queue_cap(L, T));
@@ -1140,13 +1301,16 @@ hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int r
       k_pf_scores_cfg<16><<<g, 256, 0, s>>>(L->router_f32_t, X, T, H, E, w.ps);
     else
       k_pf_scores_cfg<8><<<g, 256, 0, s>>>(L->router_f32_t, X, T, H, E, w.ps);
-    k_pf_select<DSH_ROUTE_CFG><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, w.X0, w.X1, w.xsc, w.xsum, w.idx,
-                                                            w.w);
+    k_pf_select<DSH_ROUTE_CFG><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, L->router_norm, w.X0, w.X1, w.xsc,
+                                                            w.xsum, w.idx, w.w, w.cmask);
+    const int G = min(PF_EX_G, (16384 - H) / (H + 4));  // H <= 2048: G >= 6
+    k_pf_exact<<<T, 256, sizeof(float) * ((size_t)H + (size_t)G * (H + 4)), s>>>(X, L->router_f32, H, E, K, G,
+                                                                                 w.cmask, w.idx, w.w);
   } else {
     k_pf_scores_bf16<<<(T + PF_TB - 1) / PF_TB, 256, (size_t)PF_TB * H * sizeof(float), s>>>(
         L->router_bf16, X, T, H, E, nthreads, w.ps);
-    k_pf_select<DSH_ROUTE_DECODE><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, w.X0, w.X1, w.xsc, w.xsum, w.idx,
-                                                                w.w);
+    k_pf_select<DSH_ROUTE_DECODE><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, nullptr, w.X0, w.X1, w.xsc,
+                                                                w.xsum, w.idx, w.w, nullptr);
   }
   const int n_items_max = pf_max_routed_items(L, T) + pf_shared_items(T);
   const bool fused = g_pf_fused == 1 && n_items_max < (1 << 22);

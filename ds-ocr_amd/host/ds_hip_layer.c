@@ -53,7 +53,7 @@ ds_hip_layer_t *ds_hip_layer_create(int hidden, int inter, int n_experts, int to
   ds_hip_layer_t *L = (ds_hip_layer_t *)calloc(1, sizeof *L);
   if (!L) return NULL;
   size_t H = hidden, I = inter, E = n_experts, K = top_k, SI = shared_inter;
-  size_t off[17], n = 0, k = 0;
+  size_t off[18], n = 0, k = 0;
 #define REGION(bytes) (off[k++] = n, n += al(bytes))
   REGION(E * 2 * I * H);          /* 0 gu_q */
   REGION(E * H * I);              /* 1 dn_q */
@@ -72,6 +72,7 @@ ds_hip_layer_t *ds_hip_layer_create(int hidden, int inter, int n_experts, int to
   REGION((H / 8) * 64 * 4);       /* 14 router partial scores */
   REGION(E * H * 4);              /* 15 router f32, transposed [H][E] */
   REGION((K + 1) * H * 4);        /* 16 expert outputs (bf16 simulation) */
+  REGION(E * 4);                  /* 17 f32 router row norms */
 #undef REGION
   hipError_t e = hipMalloc(&L->arena, n);
   if (e != hipSuccess) {
@@ -99,6 +100,7 @@ ds_hip_layer_t *ds_hip_layer_create(int hidden, int inter, int n_experts, int to
   L->d.router_f32 = (const float *)(b + off[8]);
   L->d.router_bf16 = (const uint16_t *)(b + off[9]);
   L->d.router_f32_t = (const float *)(b + off[15]);
+  L->d.router_norm = (const float *)(b + off[17]);
   L->d.H = hidden;
   L->d.I = inter;
   L->d.E = n_experts;
@@ -131,6 +133,7 @@ int ds_hip_layer_set_router(ds_hip_layer_t *L, const float *router_f32, const ui
     if (dsr_h2d((void *)L->d.router_f32, router_f32, n * 4)) return -1;
     DSR_TRY(dsh_launch_transpose_f32(L->d.router_f32, (float *)L->d.router_f32_t, L->E, L->H, dsr_stream),
             "router transpose");
+    DSR_TRY(dsh_launch_row_norms(L->d.router_f32, L->E, L->H, (float *)L->d.router_norm, dsr_stream), "router norms");
     L->have_f32 = 1;
   }
   if (router_bf16) {
@@ -149,6 +152,7 @@ int ds_hip_layer_set_router_dev(ds_hip_layer_t *L, const float *router_f32_dev, 
             "router copy");
     DSR_TRY(dsh_launch_transpose_f32(L->d.router_f32, (float *)L->d.router_f32_t, L->E, L->H, dsr_stream),
             "router transpose");
+    DSR_TRY(dsh_launch_row_norms(L->d.router_f32, L->E, L->H, (float *)L->d.router_norm, dsr_stream), "router norms");
     L->have_f32 = 1;
   }
   if (router_bf16_dev) {
