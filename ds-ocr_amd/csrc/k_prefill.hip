@@ -26,6 +26,7 @@
 #include "dsh_avx.h"
 #include "dsh_route.h"
 #include "k_core.h"
+#include <type_traits>
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
@@ -66,10 +67,6 @@ struct pf_item {
   int mcnt;  // rows in the chunk (1..PF_MT)
   int pos0;  // first routed pair position of the segment (routed only)
 };
-
-// ---------------------------------------------------------------------------------- helpers
-// D[m][n] of a 32x32 MFMA tile held by lane l, register j: n = l % 32, m = 8*(j/4) + 4*(l/32) + j%4
-__device__ __forceinline__ int mfma_row(int lane, int j) { return 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3); }
 
 // ---------------------------------------------------------------------------------- routing
 // Router scores in the decode path's order, kept as four partial sums per token and expert:
@@ -581,27 +578,11 @@ __device__ __forceinline__ bool pf_tile(const int *counts, const int *tiles, int
   return true;
 }
 
-// One block computes C[NSUB·32 A rows][4 waves x 2 tiles x 32 weight rows] = A · B^T over K columns:
-// A = activations split to bf16 (hi, lo), B = INT8 weight rows (codes → bf16 in registers).
-// K runs in stages of PF_KS = 128 columns, one 128-byte line of each weight row:
-// - weights: each wave streams its own 64 rows; per stage 8 loads in which 8 adjacent lanes read one
-//   row's full line (full lines keep HBM at its streaming rate), held in a PF_D-stage register ring
-//   and written to the wave's own LDS tile when the stage begins;
-// - A: the block's rows are copied in 64-column half-stages (8 adjacent lanes read one row's 128
-//   bytes of hi or lo; two half-stages ahead in registers) into a double-buffered LDS tile;
-// - both LDS tiles have 128-byte rows whose 16-byte chunks are XOR-swizzled by pf_swz(row), so the
-//   full-row writes and the MFMA reads (16 lanes, 16 rows, one chunk) are free of bank conflicts;
-// - per 32-column block, lane half h takes columns 16h..16h+15 as two MFMA k-slices of 8 (the same
-//   permutation of k for A and B leaves the product unchanged): one 16-byte LDS read gives a lane its
-//   16 codes of a weight row, one 16-byte read its 8 values of an A row.
-// One barrier per half-stage. The load order is the same in every stage and the first group of
-// PF_D stages is peeled, so the wait counts the compiler derives keep the rings full. Stages past
-// the last (K rounded up to PF_D stages) load a valid line and skip the math. A rows past the item's
-// count repeat a valid row; their results are never stored.
+// One block computes C[MB·16 A rows][4 waves x 64 weight rows] = A · B^T over K columns on the
+// int8 MFMA (v_mfma_i32_16x16x64_i8): A = activations as two int8 limbs, B = the weights' stored
+// codes. K runs in stages of PF_KS = 128 columns (one 128-byte line of each weight row), two
+// 64-column MFMA slices each; pf_mainloop_i8 below gives the details.
 #define PF_KS 128
-#ifndef PF_D
-#define PF_D 1   // weight-line stages in flight per wave
-#endif
 #ifndef PF_OCC
 #define PF_OCC 2  // GEMM blocks per CU the register budget is sized for
 #endif
@@ -609,16 +590,16 @@ __device__ __forceinline__ bool pf_tile(const int *counts, const int *tiles, int
 struct pf_smem {
   union {
     struct {
-      int8_t A[2][2][PF_MT][PF_KS];   // [stage parity][low, high limb][row][column, swizzled]
-      unsigned char B[4][64][PF_KS];  // per wave: its 64 weight rows x the stage's codes, swizzled
-    } q;                              // main loop
+      int8_t A[2][2][PF_MT][PF_KS];  // [stage parity][low, high limb][row][column, swizzled]
+    } q;                             // main loop
     float red[4][64][33];  // gate_up epilogue: h values per wave for the row sums
   } u;
-  float hsum[4][2][32];  // Σh of the block's A rows (per wave, per 32-row sub-tile)
-  float hmx[4][2][32];   // gate_up: max |h| of the block's A rows (per wave, per 32-row sub-tile)
+  float hsum[4][2][32];  // Σh of the block's A rows (per wave, per 32-row half)
+  float hmx[4][2][32];   // gate_up: max |h| of the block's A rows (per wave, per 32-row half)
   float xs[PF_MT];       // gate_up: Σx of the block's A rows (their tokens)
   float xsc[PF_MT];      // the A rows' limb scale 2^(e-15)
   short ek[PF_MT][PF_NT_MAX];  // down: exponent of each A row's n-tiles
+  float hp[PF_MT][PF_NT_MAX];  // down: Σh of each A row's n-tiles (the gate_up partials)
   int erow[PF_MT];             // down: the A rows' common exponent (max over their n-tiles)
 };
 
@@ -661,64 +642,87 @@ __device__ __forceinline__ void pf_align16(u32x4 &lo, u32x4 &hi, int d) {
   }
 }
 
+// SwiGLU of the prefill GEMM: (g / (1 + fast_exp(-g))) * u (ds_kernels.c:1771) with the quotient
+// from the hardware reciprocal and one Newton step (within an ulp of the correctly rounded
+// quotient; the prefill is compared with its reference under a tolerance, the decode path keeps
+// dsh_swiglu's exact division).
+__device__ __forceinline__ float pf_swiglu(float g, float u) {
+  // dsh_fast_expf(-g) without branches: the same bits for every input (0 below -88, 1e38 above
+  // 88, 0 for NaN; the argument clamped so the integer conversion stays in range)
+  const float x = -g, xc = __builtin_fminf(__builtin_fmaxf(x, -88.0f), 88.0f);
+  float ex = __uint_as_float((uint32_t)(int32_t)__builtin_fmaf(12102203.0f, xc, 1064866805.0f));
+  ex = x < -88.0f ? 0.0f : ex;
+  ex = x > 88.0f ? 1e38f : ex;
+  ex = x != x ? 0.0f : ex;
+  const float d = 1.0f + ex;
+  const float r = __builtin_amdgcn_rcpf(d);
+  float q = g * r;
+  q = __builtin_fmaf(__builtin_fmaf(-d, q, g), r, q);
+  return q * u;
+}
+
 // 16-byte chunk c of LDS row r sits at chunk c ^ pf_swz(r): 16 consecutive rows map one chunk to 16
 // distinct bank groups, and two consecutive rows fill 256 contiguous bytes
 __device__ __forceinline__ int pf_swz(int r) { return (r ^ (r >> 3)) & 7; }
 
-// The int8 main loop (both projections): weights are the B operand as stored codes, the activations
-// two int8 limbs (low, high). Per 128-column stage each wave streams its 64 weight rows' 128-byte
-// lines (8 lanes per row, PF_D stages ahead in registers) into its own LDS tile; the block's A rows
-// for the stage (8 adjacent lanes per row's 128 columns, one stage ahead in registers) go to a
-// double-buffered LDS tile, one barrier per stage. LDS rows are 128 bytes with 16-byte chunks
-// XOR-swizzled by pf_swz(row). Per 32-column slice s, lane half h takes bytes 32s + 16h .. +15 of
-// its A row and of its weight row (v_mfma_i32_32x32x32_i8; A and B take the same columns in the same
-// byte order, so the product is the dot product over the slice). acc[ms][q][l]: A sub-tile ms, weight
-// tile q, limb l, exact int32 sums.
+// The int8 main loop (both projections). Per 128-column stage:
+// - weights go from HBM straight into the MFMA's B operand registers: for n-block j (16 weight
+//   rows: j = 0, 1 from brow0, 2, 3 from brow1) and slice s, lane l loads bytes 64s + 16(l/16) .. +15
+//   of the stage in row 16j + l%16 (each load instruction reads 16 rows x 64 contiguous bytes); a
+//   slice's registers are reloaded with the next stage's slice as soon as its MFMAs are issued;
+// - A: the block's rows are copied (8 adjacent lanes per row's 128 bytes, one stage ahead in
+//   registers) into a double-buffered LDS tile with 128-byte rows whose 16-byte chunks are
+//   XOR-swizzled by pf_swz(row); lane l reads chunk 4s + l/16 of row 16mb + l%16, the same columns
+//   as its weight bytes, so each MFMA adds the exact products over the slice (A and B share the
+//   order of k inside the instruction, which leaves the sum unchanged);
+// - one barrier per stage.
+// acc[mb][j][l]: A rows 16mb .. +15, n-block j, limb l (low, high), exact int32 sums; lane l,
+// register i holds A row 16mb + 4(l/16) + i, weight row 16j + l%16. A rows past the item's count
+// repeat a valid row; their results are never stored.
 // A is two int8 limb arrays, A0 low and A1 high (gate_up: x at one exponent per row; down: h at
 // one exponent per row and 128-column stage). ALIGN (down): before a stage's A values go to LDS,
 // each is brought to its row's common exponent (pf_align16 with d = erow - ek of the row's stage;
 // sm.ek, sm.erow; trow: the table rows of this thread's two A rows).
-template <int NSUB, bool ALIGN>
+// pre() runs once the first stage's loads are issued (down: building the alignment table), so its
+// waits leave them in flight.
+template <int MB, bool ALIGN, typename Pre>
 __device__ __forceinline__ void pf_mainloop_i8(const int8_t *A0, const int8_t *A1, const size_t *arow,
                                                const int *trow, int K, const int8_t *brow0, const int8_t *brow1,
-                                               i32x16 (&acc)[NSUB][2][2], pf_smem &sm) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, l32 = lane & 31;
+                                               i32x4 (&acc)[MB][4][2], pf_smem &sm, Pre &&pre) {
+  const int lane = threadIdx.x & 63, r16 = lane & 15, kg = lane >> 4;
   const int ar = threadIdx.x >> 3, ac = threadIdx.x & 7;  // A copy: rows ar and ar + 32, chunk ac
-  const int nk = K / PF_KS, nkp = (nk + PF_D - 1) / PF_D * PF_D;
+  const int nk = K / PF_KS;
 #pragma unroll
-  for (int ms = 0; ms < NSUB; ms++)
+  for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-    for (int q = 0; q < 2; q++)
+    for (int j = 0; j < 4; j++)
 #pragma unroll
-      for (int l = 0; l < 2; l++)
-#pragma unroll
-        for (int j = 0; j < 16; j++) acc[ms][q][l][j] = 0;
+      for (int l = 0; l < 2; l++) acc[mb][j][l] = i32x4{0, 0, 0, 0};
   int zero = 0;
   asm volatile("" : "+v"(zero) : "v"((int)arow[0]), "v"((int)arow[1]));
-  const size_t K8 = (size_t)8 * K;
-  const int brow = lane >> 3, bch = lane & 7;
-  const int8_t *p0 = brow0 + zero + (size_t)brow * K + 16 * bch;
-  const int8_t *p1 = brow1 + zero + (size_t)brow * K + 16 * bch;
+  const size_t K16 = (size_t)16 * K;
+  const int8_t *p0 = brow0 + zero + (size_t)r16 * K + 16 * kg;
+  const int8_t *p1 = brow1 + zero + (size_t)r16 * K + 16 * kg;
   const int aw0 = 16 * (ac ^ pf_swz(ar)), aw1 = 16 * (ac ^ pf_swz(ar + 32));
-  u32x4 bR[PF_D][8];
-  u32x4 aR[4];  // X0 rows ar, ar+32, X1 rows ar, ar+32
-  auto load_b = [&](u32x4(&dst)[8], int k) {
+  i32x4 bR[2][4];  // [slice][n-block] of the stage
+  u32x4 aR[4];     // X0 rows ar, ar+32, X1 rows ar, ar+32
+  auto load_b = [&](int sl, int k) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) dst[i] = *(const u32x4 *)((i < 4 ? p0 : p1) + (i & 3) * K8 + (size_t)k * PF_KS);
+    for (int j = 0; j < 4; j++)
+      bR[sl][j] = *(const i32x4 *)((j < 2 ? p0 : p1) + (j & 1) * K16 + (size_t)k * PF_KS + 64 * sl);
   };
-  auto load_a = [&](u32x4(&dst)[4], int k) {
+  auto load_a = [&](int k) {
     const size_t o = (size_t)k * PF_KS + 16 * ac;
-    dst[0] = *(const u32x4 *)(A0 + arow[0] + o);
-    dst[1] = *(const u32x4 *)(A0 + arow[1] + o);
-    dst[2] = *(const u32x4 *)(A1 + arow[0] + o);
-    dst[3] = *(const u32x4 *)(A1 + arow[1] + o);
+    aR[0] = *(const u32x4 *)(A0 + arow[0] + o);
+    aR[1] = *(const u32x4 *)(A0 + arow[1] + o);
+    aR[2] = *(const u32x4 *)(A1 + arow[0] + o);
+    aR[3] = *(const u32x4 *)(A1 + arow[1] + o);
   };
   auto store_a = [&](int a, int k) {
     if (ALIGN) {
-      const int kc = min(k, nk - 1);
 #pragma unroll
       for (int c = 0; c < 2; c++) {
-        const int d = min(sm.erow[trow[c]] - (int)sm.ek[trow[c]][kc], 31);
+        const int d = min(sm.erow[trow[c]] - (int)sm.ek[trow[c]][k], 31);
         if (d > 0) pf_align16(aR[c], aR[2 + c], d);
       }
     }
@@ -727,66 +731,56 @@ __device__ __forceinline__ void pf_mainloop_i8(const int8_t *A0, const int8_t *A
     *(u32x4 *)&sm.u.q.A[a][1][ar][aw0] = aR[2];
     *(u32x4 *)&sm.u.q.A[a][1][ar + 32][aw1] = aR[3];
   };
-#pragma unroll
-  for (int s = 0; s < PF_D; s++) {
-    load_b(bR[s], min(s, nk - 1));
-    asm volatile("" ::: "memory");
-  }
-  load_a(aR, 0);
+  // the same issue order as in the loop (A, then slice 0, then slice 1), so the wait counts the
+  // compiler derives at the loop head leave the weight loads in flight
+  load_a(0);
   asm volatile("" ::: "memory");
-
-  auto group = [&](int kb0) {
+  load_b(0, 0);
+  asm volatile("" ::: "memory");
+  load_b(1, 0);
+  asm volatile("" ::: "memory");
+  pre();
+#pragma unroll 1
+  for (int k = 0; k < nk; k++) {
+    const int a = k & 1, kn = min(k + 1, nk - 1);
+    store_a(a, k);
+    load_a(kn);
+    asm volatile("" ::: "memory");
+    __syncthreads();
 #pragma unroll
-    for (int s = 0; s < PF_D; s++) {
-      const int k = kb0 + s;
+    for (int sl = 0; sl < 2; sl++) {
+      i32x4 x0[MB], x1[MB];
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const int r = 8 * i + brow;
-        *(u32x4 *)&sm.u.q.B[wave][r][16 * (bch ^ pf_swz(r))] = bR[s][i];
+      for (int mb = 0; mb < MB; mb++) {
+        const int m = 16 * mb + r16, c = 16 * ((4 * sl + kg) ^ pf_swz(m));
+        x0[mb] = *(const i32x4 *)&sm.u.q.A[a][0][m][c];
+        x1[mb] = *(const i32x4 *)&sm.u.q.A[a][1][m][c];
       }
-      load_b(bR[s], min(k + PF_D, nk - 1));
-      asm volatile("" ::: "memory");
-      const int a = k & 1;
-      store_a(a, k);
-      load_a(aR, min(k + 1, nk - 1));
-      asm volatile("" ::: "memory");
-      __syncthreads();
-      if (k < nk) {
 #pragma unroll
-        for (int sl = 0; sl < 4; sl++) {
-          const int cb = 2 * sl + half;  // 16-byte chunk of this lane half
-          const i32x4 b0 = *(const i32x4 *)&sm.u.q.B[wave][l32][16 * (cb ^ pf_swz(l32))];
-          const i32x4 b1 = *(const i32x4 *)&sm.u.q.B[wave][32 + l32][16 * (cb ^ pf_swz(32 + l32))];
+      for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-          for (int ms = 0; ms < NSUB; ms++) {
-            const int m = 32 * ms + l32;
-            const i32x4 x0 = *(const i32x4 *)&sm.u.q.A[a][0][m][16 * (cb ^ pf_swz(m))];
-            const i32x4 x1 = *(const i32x4 *)&sm.u.q.A[a][1][m][16 * (cb ^ pf_swz(m))];
-            acc[ms][0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x0, b0, acc[ms][0][0], 0, 0, 0);
-            acc[ms][1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x0, b1, acc[ms][1][0], 0, 0, 0);
-            acc[ms][0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x1, b0, acc[ms][0][1], 0, 0, 0);
-            acc[ms][1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x1, b1, acc[ms][1][1], 0, 0, 0);
-          }
+        for (int j = 0; j < 4; j++) {
+          acc[mb][j][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0[mb], bR[sl][j], acc[mb][j][0], 0, 0, 0);
+          acc[mb][j][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1[mb], bR[sl][j], acc[mb][j][1], 0, 0, 0);
         }
-      }
+      load_b(sl, kn);
+      asm volatile("" ::: "memory");
     }
-  };
-  group(0);
-  for (int kb0 = PF_D; kb0 < nkp; kb0 += PF_D) group(kb0);
+  }
 }
 
 // gate_up: block = (work item, n-tile): the item's A rows (tokens) x 128 intermediate units; wave w
-// owns units i0 + 32w .. +31, tile 0 = their gate rows, tile 1 = their up rows, so the SwiGLU pairs
-// sit in the same lane and register.
-template <bool SHARED, int NSUB>
+// owns units i0 + 32w .. +31: n-blocks 0, 1 = their gate rows, 2, 3 = their up rows, so each SwiGLU
+// pair sits in the same lane and register (n-blocks h and 2 + h).
+template <bool SHARED, int MB>
 __device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item &it, int nt, const int8_t *X0,
                                              const int8_t *X1, const float *xsc, const float *xsum,
                                              const int *pair_tok, int bf16sim, int8_t *Hq0, int8_t *Hq1,
                                              float *hpart, float *hmaxp, pf_smem &sm) {
   const int H = L.H;
   const int Iseg = SHARED ? L.SI : L.I, ntK = Iseg / PF_GU_N;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l32 = lane & 31;
-  const int u0 = nt * PF_GU_N + wave * 32, unit = u0 + l32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, kg = lane >> 4;
+  const int u0 = nt * PF_GU_N + wave * 32;
   const int8_t *wq = SHARED ? L.sgu_q : L.gu_q + (size_t)it.seg * 2 * L.I * H;
   const float *wso = SHARED ? L.sgu_so : L.gu_so + (size_t)it.seg * 2 * L.I * 2;
   size_t arow[2];
@@ -807,12 +801,24 @@ __device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item
     sm.xsc[threadIdx.x >> 3] = c0;
     sm.xsc[(threadIdx.x >> 3) + 32] = c1;
   }
-  i32x16 acc[NSUB][2][2];
-  pf_mainloop_i8<NSUB, false>(X0, X1, arow, nullptr, H, wq + (size_t)u0 * H, wq + (size_t)(Iseg + u0) * H, acc, sm);
+  // the lane's units' scales and offsets (units u0 + 16h + l%16), loaded before the main loop so
+  // the epilogue does not wait for them
+  float2 sog[2], sou[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int unit = u0 + 16 * h + r16;
+    sog[h] = ((const float2 *)wso)[unit];
+    sou[h] = ((const float2 *)wso)[Iseg + unit];
+  }
+  i32x4 acc[MB][4][2];
+  pf_mainloop_i8<MB, false>(X0, X1, arow, nullptr, H, wq + (size_t)u0 * H, wq + (size_t)(Iseg + u0) * H, acc, sm,
+                            [] {});
   // signed codes: offset + 128·scale multiplies Σa
-  float2 sog = ((const float2 *)wso)[unit], sou = ((const float2 *)wso)[Iseg + unit];
-  sog.y = __builtin_fmaf(128.0f, sog.x, sog.y);
-  sou.y = __builtin_fmaf(128.0f, sou.x, sou.y);
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    sog[h].y = __builtin_fmaf(128.0f, sog[h].x, sog[h].y);
+    sou[h].y = __builtin_fmaf(128.0f, sou[h].x, sou[h].y);
+  }
   const size_t rbase = SHARED ? (size_t)it.m0 : (size_t)(it.pos0 + it.m0);
   // The tile's h values go to LDS (per wave: 64 rows x its 32 units); each lane sums a row (Σh over
   // the block's 128 units, for the down epilogue's offset term) and takes its max |h|; the rows'
@@ -820,33 +826,40 @@ __device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item
   // lanes store 8-unit runs of both limbs.
   float(*red)[64][33] = sm.u.red;
   __syncthreads();  // every wave is done with the main loop's tiles
+  // rows past the item's count repeat row 0 (valid values, never stored); the bf16 simulation is
+  // one branch around the loop
+  auto h_out = [&](auto sim) {
 #pragma unroll
-  for (int ms = 0; ms < NSUB; ms++)
+    for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
-      const int m = ms * 32 + mfma_row(lane, j);
-      float hv = 0.0f;
-      if (m < it.mcnt) {
-        const float xs = sm.xs[m], sc = sm.xsc[m];
-        // Σ q·x = 2^(e-15)·(256·Σ q·X1 + Σ q·X0)
-        const float dg = sc * __builtin_fmaf(256.0f, (float)acc[ms][0][1][j], (float)acc[ms][0][0][j]);
-        const float du = sc * __builtin_fmaf(256.0f, (float)acc[ms][1][1][j], (float)acc[ms][1][0][j]);
-        float g = __builtin_fmaf(sog.x, dg, sog.y * xs);
-        float up = __builtin_fmaf(sou.x, du, sou.y * xs);
-        if (bf16sim) {
-          g = dsh_bf16_round_half_up(g);
-          up = dsh_bf16_round_half_up(up);
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int m = 16 * mb + 4 * kg + i;
+          const float xs = sm.xs[m], sc = sm.xsc[m];
+          // Σ q·x = 2^(e-15)·(256·Σ q·X1 + Σ q·X0)
+          const float dg = sc * __builtin_fmaf(256.0f, (float)acc[mb][h][1][i], (float)acc[mb][h][0][i]);
+          const float du = sc * __builtin_fmaf(256.0f, (float)acc[mb][2 + h][1][i], (float)acc[mb][2 + h][0][i]);
+          float g = __builtin_fmaf(sog[h].x, dg, sog[h].y * xs);
+          float up = __builtin_fmaf(sou[h].x, du, sou[h].y * xs);
+          if (decltype(sim)::value) {
+            g = dsh_bf16_round_half_up(g);
+            up = dsh_bf16_round_half_up(up);
+          }
+          float hv = pf_swiglu(g, up);
+          if (decltype(sim)::value) hv = dsh_bf16_round_half_up(hv);
+          red[wave][m][16 * h + r16] = hv;
         }
-        hv = dsh_swiglu(g, up);
-        if (bf16sim) hv = dsh_bf16_round_half_up(hv);
-      }
-      red[wave][m][l32] = hv;
-    }
+  };
+  if (bf16sim)
+    h_out(std::true_type{});
+  else
+    h_out(std::false_type{});
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   float part = 0.0f, pmax = 0.0f;  // lane = row: its sum (in unit order) and max |h| over the wave's 32 units
-  if (lane < 32 * NSUB) {
+  if (lane < 16 * MB) {
 #pragma unroll 8
     for (int u = 0; u < 32; u++) {
       const float hv = red[wave][lane][u];
@@ -860,7 +873,7 @@ __device__ __forceinline__ void gate_up_tile(const dsh_layer_t &L, const pf_item
   {  // stores: lane → rows (lane / 4) + 16k, units 8·(lane % 4) .. +7 of the wave's 32, as limbs
     const int g8 = 8 * (lane & 3);
 #pragma unroll
-    for (int k = 0; k < 2 * NSUB; k++) {
+    for (int k = 0; k < MB; k++) {
       const int m = (lane >> 2) + 16 * k;
       if (m >= it.mcnt) continue;
       const int a = m >> 5, b = m & 31;
@@ -895,9 +908,9 @@ __device__ __forceinline__ void gate_up_dispatch(const dsh_layer_t &L, const pf_
                                                  const int *pair_tok, int bf16sim, int8_t *Hq0, int8_t *Hq1,
                                                  float *hpart, float *hmaxp, pf_smem &sm) {
   if (it.mcnt <= 32)
-    gate_up_tile<SHARED, 1>(L, it, nt, X0, X1, xsc, xsum, pair_tok, bf16sim, Hq0, Hq1, hpart, hmaxp, sm);
-  else
     gate_up_tile<SHARED, 2>(L, it, nt, X0, X1, xsc, xsum, pair_tok, bf16sim, Hq0, Hq1, hpart, hmaxp, sm);
+  else
+    gate_up_tile<SHARED, 4>(L, it, nt, X0, X1, xsc, xsum, pair_tok, bf16sim, Hq0, Hq1, hpart, hmaxp, sm);
 }
 
 __global__ void __launch_bounds__(256, PF_OCC) k_pf_gate_up(dsh_layer_t L, const pf_item *__restrict__ items,
@@ -919,31 +932,62 @@ __global__ void __launch_bounds__(256, PF_OCC) k_pf_gate_up(dsh_layer_t L, const
 }
 
 // down: block = (work item, n-tile): the item's A rows (h of its pairs, or of tokens for the shared
-// expert, as limbs) x 256 output rows; wave w owns rows n0 + 64w .. +63 as two 32-row tiles. Each A
+// expert, as limbs) x 256 output rows; wave w owns rows n0 + 64w .. +63 as four 16-row n-blocks. Each A
 // row's exponent is the largest of its n-tiles' (from the max |h| per (row, n-tile) the gate_up
 // epilogues wrote; read at L2); the main loop aligns every stage to it. Σh of each A row is the sum,
 // in n-tile order, of the per-n-tile row sums the gate_up epilogue wrote.
-template <bool SHARED, int NSUB>
+template <bool SHARED, int MB>
 __device__ __forceinline__ void down_tile(const dsh_layer_t &L, const pf_item &it, int nt, const int8_t *Hq0,
                                           const int8_t *Hq1, const float *hpart, const float *hmaxp, float *Y,
                                           pf_smem &sm) {
   const int H = L.H;
   const int Kd = SHARED ? L.SI : L.I, ntK = Kd / PF_GU_N;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, l32 = lane & 31;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, kg = lane >> 4;
   const int8_t *wq = SHARED ? L.sdn_q : L.dn_q + (size_t)it.seg * H * L.I;
   const float *wso = SHARED ? L.sdn_so : L.dn_so + (size_t)it.seg * H * 2;
-  const int nw = nt * PF_DN_N + wave * 64, n0 = nw + l32;
+  const int nw = nt * PF_DN_N + wave * 64;
   const size_t rbase = SHARED ? (size_t)it.m0 : (size_t)(it.pos0 + it.m0);
-  if (threadIdx.x < PF_MT) sm.erow[threadIdx.x] = -1024;
-  __syncthreads();
-  for (int i = threadIdx.x; i < it.mcnt * ntK; i += 256) {
-    const int r = i / ntK;
-    const int e = pf_limb_exp(__hip_atomic_load(hmaxp + rbase * ntK + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    sm.ek[r][i - r * ntK] = (short)e;
-    atomicMax(&sm.erow[r], e);
+  // The gate_up partials of the A rows (max |h| and Σh per row and n-tile; at most PF_MT x
+  // PF_NT_MAX = 4 per thread), read at L2 and all issued at once, then the output rows' scales
+  // and offsets; all are in flight while the main loop issues its first stage.
+  const int ntot = it.mcnt * ntK;
+  float mxv[4], hpv[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const int i = threadIdx.x + 256 * c;
+    mxv[c] = 0.0f;
+    hpv[c] = 0.0f;
+    if (i < ntot) {
+      mxv[c] = __hip_atomic_load(hmaxp + rbase * ntK + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      hpv[c] = __hip_atomic_load(hpart + rbase * ntK + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
-  __syncthreads();
-  if (threadIdx.x < it.mcnt) sm.xsc[threadIdx.x] = __builtin_ldexpf(1.0f, sm.erow[threadIdx.x] - 15);
+  float2 so[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) so[j] = ((const float2 *)wso)[nw + 16 * j + r16];
+  if (threadIdx.x < PF_MT) sm.erow[threadIdx.x] = -1024;
+  // each A row's exponent (the largest of its n-tiles'), its limb scale and its Σh (n-tile order)
+  auto table = [&] {
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const int i = threadIdx.x + 256 * c;
+      if (i < ntot) {
+        const int r = i / ntK, k = i - r * ntK, e = pf_limb_exp(mxv[c]);
+        sm.ek[r][k] = (short)e;
+        sm.hp[r][k] = hpv[c];
+        atomicMax(&sm.erow[r], e);
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < it.mcnt) {
+      const int r = threadIdx.x;
+      sm.xsc[r] = __builtin_ldexpf(1.0f, sm.erow[r] - 15);
+      float hs = 0.0f;
+      for (int k = 0; k < ntK; k++) hs += sm.hp[r][k];
+      sm.hsum[0][r >> 5][r & 31] = hs;
+    }
+  };
   size_t arow[2];
   int trow[2];
 #pragma unroll
@@ -952,33 +996,23 @@ __device__ __forceinline__ void down_tile(const dsh_layer_t &L, const pf_item &i
     trow[c] = r < it.mcnt ? r : 0;
     arow[c] = (rbase + trow[c]) * Kd;
   }
-  i32x16 acc[NSUB][2][2];
-  pf_mainloop_i8<NSUB, true>(Hq0, Hq1, arow, trow, Kd, wq + (size_t)nw * Kd, wq + (size_t)(nw + 32) * Kd, acc, sm);
-  {  // lane = row of the block: Σh from the gate_up partials (each wave for itself)
-    float hs = 0.0f;
-    if (lane < it.mcnt) {
-      const float *hp = hpart + (rbase + lane) * ntK;
-      for (int k = 0; k < ntK; k++) hs += __hip_atomic_load(hp + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    sm.hsum[wave][half][l32] = hs;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  i32x4 acc[MB][4][2];
+  pf_mainloop_i8<MB, true>(Hq0, Hq1, arow, trow, Kd, wq + (size_t)nw * Kd, wq + (size_t)(nw + 32) * Kd, acc, sm,
+                           table);
 #pragma unroll
-  for (int q = 0; q < 2; q++) {
-    float2 so = ((const float2 *)wso)[n0 + 32 * q];
-    so.y = __builtin_fmaf(128.0f, so.x, so.y);  // signed codes: offset + 128·scale multiplies Σh
+  for (int j = 0; j < 4; j++) {
+    const int n = nw + 16 * j + r16;
+    so[j].y = __builtin_fmaf(128.0f, so[j].x, so[j].y);  // signed codes: offset + 128·scale multiplies Σh
 #pragma unroll
-    for (int ms = 0; ms < NSUB; ms++)
+    for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-      for (int j = 0; j < 16; j++) {
-        const int m = ms * 32 + mfma_row(lane, j);
+      for (int i = 0; i < 4; i++) {
+        const int m = 16 * mb + 4 * kg + i;
         if (m >= it.mcnt) continue;
-        const float hs = sm.hsum[wave][ms][mfma_row(lane, j)];
+        const float hs = sm.hsum[0][m >> 5][m & 31];
         // Σ q·h = 2^(erow-15)·(256·Σ q·H1 + Σ q·H0)
-        const float dot = sm.xsc[m] * __builtin_fmaf(256.0f, (float)acc[ms][q][1][j], (float)acc[ms][q][0][j]);
-        Y[(rbase + m) * H + n0 + 32 * q] = __builtin_fmaf(so.x, dot, so.y * hs);
+        const float dot = sm.xsc[m] * __builtin_fmaf(256.0f, (float)acc[mb][j][1][i], (float)acc[mb][j][0][i]);
+        Y[(rbase + m) * H + n] = __builtin_fmaf(so[j].x, dot, so[j].y * hs);
       }
   }
 }
@@ -988,9 +1022,9 @@ __device__ __forceinline__ void down_dispatch(const dsh_layer_t &L, const pf_ite
                                               const int8_t *Hq1, const float *hpart, const float *hmaxp, float *Y,
                                               pf_smem &sm) {
   if (it.mcnt <= 32)
-    down_tile<SHARED, 1>(L, it, nt, Hq0, Hq1, hpart, hmaxp, Y, sm);
-  else
     down_tile<SHARED, 2>(L, it, nt, Hq0, Hq1, hpart, hmaxp, Y, sm);
+  else
+    down_tile<SHARED, 4>(L, it, nt, Hq0, Hq1, hpart, hmaxp, Y, sm);
 }
 
 __global__ void __launch_bounds__(256, PF_OCC) k_pf_down(dsh_layer_t L, const pf_item *__restrict__ items,
