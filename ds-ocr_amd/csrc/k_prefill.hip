@@ -287,9 +287,11 @@ __global__ void __launch_bounds__(256) k_pf_select(const float *__restrict__ X, 
 
 // CFG tokens whose selection the rounding bound could not confirm (cmask != 0): one block per
 // token; the candidates' router rows (up to G <= PF_EX_G at a time, G set so LDS stays within
-// 64 KB; rows H + 4 floats apart, so the lanes' 16-byte reads hit distinct banks) and x go to LDS, lane c of wave 0 sums candidate c's score in
-// ds_linear's order (ds_kernels.c:639-652 as GCC compiles it: rounded products added in index
-// order, the tail past the last multiple of 8 fused), the other experts are set aside, and the
+// 64 KB; rows H + 4 floats apart, so the lanes' 16-byte reads hit distinct banks) and x go to LDS,
+// all threads replace the rows' values by the rounded products x_k·r_k, and lane c of wave 0 adds
+// candidate c's products in ds_linear's order (ds_kernels.c:639-652 as GCC compiles it: rounded
+// products added in index order, the tail past the last multiple of 8 fused; the chain lane issues
+// only the dependent adds), the other experts are set aside, and the
 // selection and its softmax (route_select) run again: idx and w of the token are replaced.
 #define PF_EX_G 8
 #define PF_EX_LD ((PF_EX_G + 1) * 2048 / 4 / 256)  // f32x4 loads per thread for x and a group, H <= 2048
@@ -338,48 +340,48 @@ __global__ void __launch_bounds__(256) k_pf_exact(const float *__restrict__ X, c
     }
     first = false;
     __syncthreads();
+    // the rounded products x_k·r_k of the first m columns (contraction off: one rounding each),
+    // by all threads, in place of the rows' values
+    {
+      const int m4 = m / 4;
+      for (int i = threadIdx.x; i < nc * m4; i += 256) {
+        const int c = i / m4, q = i - c * m4;
+        f32x4 *r = (f32x4 *)(s_rows + (size_t)c * (H + 4)) + q;
+        *r = ((const f32x4 *)s_x)[q] * *r;
+      }
+    }
+    __syncthreads();
     if (wave == 0) {
       float a = 0.0f;
       if (lane < nc) {
-        // the rounded-product part (m is a multiple of 8) in steps of 16 values (a + x·r with
-        // contraction off: the product rounded, then the add), EX_D steps of LDS reads in flight
-        // (a ring of registers; the barriers keep each refill where it is written)
+        // the dependent adds of the products in index order, 16 values per step, EX_D steps of
+        // LDS reads in flight (a ring of registers), then the fused tail
         constexpr int EX_D = 4;
-        const f32x4 *x4 = (const f32x4 *)s_x, *r4 = (const f32x4 *)(s_rows + lane * (H + 4));
+        const f32x4 *p4 = (const f32x4 *)(s_rows + lane * (H + 4));
         const int m16 = m & ~15, nst = m16 / 16;
-        f32x4 xq[EX_D][4], rq[EX_D][4];
+        f32x4 pq[EX_D][4];
 #pragma unroll
         for (int d = 0; d < EX_D; d++)
 #pragma unroll
-          for (int q = 0; q < 4; q++) {
-            const int st = min(d, max(nst - 1, 0));
-            xq[d][q] = x4[4 * st + q];
-            rq[d][q] = r4[4 * st + q];
-          }
+          for (int q = 0; q < 4; q++) pq[d][q] = p4[4 * min(d, max(nst - 1, 0)) + q];
         asm volatile("" ::: "memory");
         for (int s0 = 0; s0 < nst; s0 += EX_D) {
 #pragma unroll
           for (int d = 0; d < EX_D; d++) {
-            if (s0 + d < nst) {  // the step's 16 products first, then the dependent adds
-              float pr[16];
+            if (s0 + d < nst) {
 #pragma unroll
               for (int q = 0; q < 4; q++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) pr[4 * q + i] = xq[d][q][i] * rq[d][q][i];
-#pragma unroll
-              for (int j = 0; j < 16; j++) a = a + pr[j];
+                for (int i = 0; i < 4; i++) a = a + pq[d][q][i];
             }
             const int st = min(s0 + d + EX_D, max(nst - 1, 0));
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-              xq[d][q] = x4[4 * st + q];
-              rq[d][q] = r4[4 * st + q];
-            }
+            for (int q = 0; q < 4; q++) pq[d][q] = p4[4 * st + q];
             asm volatile("" ::: "memory");
           }
         }
         const float *rr = s_rows + lane * (H + 4);
-        for (int k = m16; k < m; k++) a = a + s_x[k] * rr[k];
+        for (int k = m16; k < m; k++) a = a + rr[k];
         for (int k = m; k < H; k++) a = __builtin_fmaf(s_x[k], rr[k], a);
       }
       for (int c = 0; c < nc; c++) {
