@@ -107,6 +107,15 @@ hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int r
 hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int *tokens, int *step, float *zero_p,
                                       int zero_n, const uint16_t *emb, int emb_vocab, int H, float *emb_out,
                                       hipStream_t s);
+/* The final reduction fused with the next step's router partials (CFG): *step already advanced
+ * (by the LM head's step_inc); writes tokens[*step - 1], clears zero_p like the kernel above, then
+ * the next step's input (emb_out != NULL: the token's embedding widened into emb_out, unchanged for
+ * a token outside the table; else row *step of x_in, skipped when *step >= rows) and its router
+ * partials[H / R][64] as dsh_launch_dec_partial_scores computes them. */
+hipError_t dsh_launch_lm_final_scores(const unsigned long long *cand, int n, int *tokens, const int *step,
+                                      float *zero_p, int zero_n, const uint16_t *emb, int emb_vocab, float *emb_out,
+                                      const float *x_in, int stride, int rows, const float *WrT, int H, int E,
+                                      float *partials, hipStream_t s);
 /* emb[tokens[*step - 1]][0..H) widened to f32 into out (a token outside [0, emb_vocab): unchanged). */
 hipError_t dsh_launch_embed_next(const int *tokens, const int *step, const uint16_t *emb, int emb_vocab, int H,
                                  float *out, hipStream_t s);
@@ -188,9 +197,9 @@ hipError_t dsh_launch_dec_lm_argmax_depth(const uint16_t *W, const float *x, int
 hipError_t dsh_launch_dec_lm_argmax(const uint16_t *W, const float *x, int in_dim, int vocab,
                                     unsigned long long *cand, hipStream_t s);
 /* The same head on x = Σ of ncopies (8) copies [ncopies][in_dim] (in_dim <= 2048); x_out (optional)
- * receives that sum. */
+ * receives that sum; step_inc (optional) is advanced by one. */
 hipError_t dsh_launch_dec_lm_argmax_copies(const uint16_t *W, const float *xc, int ncopies, int in_dim, int vocab,
-                                           unsigned long long *cand, float *x_out, hipStream_t s);
+                                           unsigned long long *cand, float *x_out, int *step_inc, hipStream_t s);
 
 /* ---- one kernel per MoE layer, down split over intermediate units (k_layer.hip) ---- */
 typedef struct {

@@ -694,7 +694,10 @@ __global__ void __launch_bounds__(64) k_sim_combine(dsh_layer_t L, const float *
 template <int D, int XC>
 __global__ void __launch_bounds__(256) k_dec_lm_argmax(const uint16_t *W, const float *__restrict__ x,
                                                        int in_dim, int vocab, unsigned long long *__restrict__ cand,
-                                                       float *__restrict__ x_out) {
+                                                       float *__restrict__ x_out, int *__restrict__ step_inc) {
+  // step_inc: the step counter, advanced here (no block of this kernel reads it) so that every
+  // block of the final kernel after it reads the same, already advanced value
+  if (step_inc && blockIdx.x == 0 && threadIdx.x == 0) *step_inc += 1;
   constexpr int PITCH = 144;
   __shared__ __attribute__((aligned(16))) uint8_t tile[4][64 * PITCH];
   __shared__ unsigned long long wbest[4];
@@ -867,6 +870,63 @@ __global__ void __launch_bounds__(256) k_lm_argmax_final(const unsigned long lon
   }
 }
 
+// The step's final kernel fused with the next step's router partials (CFG routing, one-kernel
+// layers). The LM head has advanced the step counter, so sn = *step is the next step and sn - 1
+// the token's slot, the same in every block. Each block: the argmax of the LM head's candidates
+// (redundantly, as k_lm_argmax_final: n is the head's block count), its share of the regions to
+// clear, and R rows r0 .. r0 + R - 1 of the next step's input with their router partials in
+// k_dec_partial_scores' order. The input is the token's embedding, widened and written to emb_out
+// (emb_out left as it is for a token outside the table, as embed_row), or row sn of x_in; with
+// sn >= rows there is no next step in the bound input and no partials are written.
+template <int R>
+__global__ void __launch_bounds__(64) k_lm_final_scores(const unsigned long long *__restrict__ cand, int n,
+                                                        int *__restrict__ tokens, const int *__restrict__ step,
+                                                        float *__restrict__ zero_p, int zero_n,
+                                                        const uint16_t *__restrict__ emb, int emb_vocab,
+                                                        float *__restrict__ emb_out, const float *__restrict__ x_in,
+                                                        int stride, int rows, const float *__restrict__ WrT, int E,
+                                                        float *__restrict__ partials) {
+  const int lane = threadIdx.x, sn = *step, r0 = blockIdx.x * R;
+  unsigned long long b = 0ull;
+  for (int i0 = 0; i0 < n; i0 += 512) {
+    unsigned long long c[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) c[j] = cand[min(i0 + lane + 64 * j, n - 1)];  // duplicates are harmless
+#pragma unroll
+    for (int j = 0; j < 8; j++) b = dsh_umax64(b, c[j]);
+  }
+  const int tok = dsh_key_index(dsh_wave_max_u64(b));
+  if (blockIdx.x == 0 && lane == 0) tokens[sn - 1] = tok;
+  for (int i = 4 * (blockIdx.x * 64 + lane); i < zero_n; i += 4 * 64 * (int)gridDim.x)
+    *(f32x4 *)(zero_p + i) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float xv[R];
+  if (emb_out) {
+    if (tok >= 0 && tok < emb_vocab) {
+      const uint16_t *er = emb + (size_t)tok * (size_t)(gridDim.x * R) + r0;
+#pragma unroll
+      for (int j = 0; j < R; j++) xv[j] = __uint_as_float((unsigned)er[j] << 16);
+      if (lane < R) emb_out[r0 + lane] = xv[lane];
+    } else {
+#pragma unroll
+      for (int j = 0; j < R; j++) xv[j] = emb_out[r0 + j];
+    }
+  } else {
+    if (sn >= rows) return;
+    const float *x = x_in + (size_t)sn * stride + r0;
+#pragma unroll
+    for (int j = 0; j < R; j++) xv[j] = x[j];
+  }
+  float p = 0.0f;
+  if (lane < E) {
+    float w[R];
+#pragma unroll
+    for (int j = 0; j < R; j++) w[j] = WrT[(size_t)(r0 + j) * E + lane];
+#pragma unroll
+    for (int j = 0; j < R; j++) p = __builtin_fmaf(w[j], xv[j], p);
+  }
+  partials[(size_t)blockIdx.x * 64 + lane] = lane < E ? p : 0.0f;
+}
+
 // ============================================================================ launchers
 // Rows per down block (and per router partial): keeps the partial count within 4 * ROUTE_BATCH.
 static inline int dec_rows(int H) { return H <= 32 * ROUTE_BATCH ? 8 : 16; }
@@ -998,6 +1058,22 @@ int dsh_dec_lm_eligible(const void *W, int in_dim, int vocab, int nthreads) {
   return 1;
 }
 
+hipError_t dsh_launch_lm_final_scores(const unsigned long long *cand, int n, int *tokens, const int *step,
+                                      float *zero_p, int zero_n, const uint16_t *emb, int emb_vocab, float *emb_out,
+                                      const float *x_in, int stride, int rows, const float *WrT, int H, int E,
+                                      float *partials, hipStream_t s) {
+  if (((uintptr_t)zero_p & 15) || zero_n % 4 || zero_n < 0 || n <= 0 || E <= 0 || E > 64 || H % dec_rows(H))
+    return hipErrorInvalidValue;
+  if (emb_out ? (!emb || emb_vocab <= 0) : (!x_in || rows <= 0 || stride < 0)) return hipErrorInvalidValue;
+  if (dec_rows(H) == 8)
+    k_lm_final_scores<8><<<H / 8, 64, 0, s>>>(cand, n, tokens, step, zero_p, zero_n, emb, emb_vocab, emb_out, x_in,
+                                             stride, rows, WrT, E, partials);
+  else
+    k_lm_final_scores<16><<<H / 16, 64, 0, s>>>(cand, n, tokens, step, zero_p, zero_n, emb, emb_vocab, emb_out, x_in,
+                                               stride, rows, WrT, E, partials);
+  return hipGetLastError();
+}
+
 hipError_t dsh_launch_lm_argmax_final(const unsigned long long *cand, int n, int *tokens, int *step, float *zero_p,
                                       int zero_n, const uint16_t *emb, int emb_vocab, int H, float *emb_out,
                                       hipStream_t s) {
@@ -1025,13 +1101,13 @@ hipError_t dsh_launch_dec_lm_argmax_depth(const uint16_t *W, const float *x, int
   const int nb = dsh_dec_lm_blocks(vocab);
   switch (depth) {
     case 1:
-      k_dec_lm_argmax<1, 0><<<nb, 256, 0, s>>>(W, x, in_dim, vocab, cand, nullptr);
+      k_dec_lm_argmax<1, 0><<<nb, 256, 0, s>>>(W, x, in_dim, vocab, cand, nullptr, nullptr);
       break;
     case 2:
-      k_dec_lm_argmax<2, 0><<<nb, 256, 0, s>>>(W, x, in_dim, vocab, cand, nullptr);
+      k_dec_lm_argmax<2, 0><<<nb, 256, 0, s>>>(W, x, in_dim, vocab, cand, nullptr, nullptr);
       break;
     case 4:
-      k_dec_lm_argmax<4, 0><<<nb, 256, 0, s>>>(W, x, in_dim, vocab, cand, nullptr);
+      k_dec_lm_argmax<4, 0><<<nb, 256, 0, s>>>(W, x, in_dim, vocab, cand, nullptr, nullptr);
       break;
     default:
       return hipErrorInvalidValue;
@@ -1040,10 +1116,10 @@ hipError_t dsh_launch_dec_lm_argmax_depth(const uint16_t *W, const float *x, int
 }
 
 hipError_t dsh_launch_dec_lm_argmax_copies(const uint16_t *W, const float *xc, int ncopies, int in_dim, int vocab,
-                                           unsigned long long *cand, float *x_out, hipStream_t s) {
+                                           unsigned long long *cand, float *x_out, int *step_inc, hipStream_t s) {
   if (!dsh_dec_lm_supported(in_dim) || in_dim > 2048 || ((uintptr_t)W & 15) || vocab <= 0 || ncopies != 8)
     return hipErrorInvalidValue;
-  k_dec_lm_argmax<1, 8><<<dsh_dec_lm_blocks(vocab), 256, 0, s>>>(W, xc, in_dim, vocab, cand, x_out);
+  k_dec_lm_argmax<1, 8><<<dsh_dec_lm_blocks(vocab), 256, 0, s>>>(W, xc, in_dim, vocab, cand, x_out, step_inc);
   return hipGetLastError();
 }
 

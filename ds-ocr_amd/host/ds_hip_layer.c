@@ -751,6 +751,11 @@ struct ds_hip_stack {
   int in_stride;
   /* steps launched since the bind or the last reset, and how many the bound buffers allow */
   int done, cap;
+  int rows; /* rows of the bound input */
+  /* the step's final kernel also computes the next step's first router partials (one-kernel layers,
+   * CFG routing, no dense layer, attention or sampling rules, the head on the layer copies): the
+   * partials always belong to the current step's input (reset and every run call compute them) */
+  int merged;
   /* autoregressive input (ds_hip_stack_set_embedding): step s >= 1 reads the widened embedding of
    * token s - 1, which the step before wrote into ebuf */
   const uint16_t *emb;
@@ -985,7 +990,7 @@ static int stack_names(const ds_hip_stack_t *S, const char **names) {
       NM("dense.down");
     }
     for (int l = 0; l < S->n_layers; l++) {
-      if (!cfg || (l == 0 && !S->dense)) NM("scores");
+      if (!cfg || (l == 0 && !S->dense && !S->merged)) NM("scores");
       NM("layer");
     }
     if (!S->lm_fast) NM("copy_sum");
@@ -1003,7 +1008,7 @@ static int stack_names(const ds_hip_stack_t *S, const char **names) {
     }
   }
   NM("lm_head.argmax");
-  NM("lm_head.final");
+  NM(S->merged ? "lm_head.final+scores" : "lm_head.final");
   if (smp_active(S)) NM("sample");
 #undef NM
   return n;
@@ -1100,7 +1105,7 @@ static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *n
   const int cfg = S->route_mode == DS_HIP_ROUTE_CFG, mode = cfg ? DSH_ROUTE_CFG : DSH_ROUTE_DECODE;
   const int zn = (int)S->xc_region;
   int np0 = S->layers[0]->np;
-  if (!dense || !cfg) {
+  if ((!dense || !cfg) && !S->merged) {
     e = scores_enqueue(S->layers[0], dense ? S->xbuf : S->in, dense ? NULL : S->in_step, dense ? 0 : S->in_stride,
                        S->route_mode, S->bf16sim, S->partials[0], &np0);
     if (e == hipSuccess) e = mark(ev, nev);
@@ -1143,7 +1148,7 @@ static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *n
  * state); the final kernel after it then clears the last two copies regions. */
 static hipError_t split_lm_enqueue(ds_hip_stack_t *S) {
   return dsh_launch_dec_lm_argmax_copies(S->lm, xc_region(S, S->n_layers - 1), dsh_layer_split_copies(), S->H,
-                                         S->vocab, S->cand, S->xbuf, dsr_stream);
+                                         S->vocab, S->cand, S->xbuf, S->merged ? S->step : NULL, dsr_stream);
 }
 
 /* The step's final kernel: the token into tokens[step], the step counter advanced, the last copies
@@ -1153,6 +1158,12 @@ static hipError_t final_enqueue(ds_hip_stack_t *S, int clear) {
   const int NL = S->n_layers, embed = S->emb && !smp_active(S);
   float *zp = clear ? xc_region(S, NL >= 2 ? NL - 2 : 0) : NULL;
   const int zn = clear ? (int)S->xc_region * (NL >= 2 ? 2 : 1) : 0;
+  if (S->merged) {
+    const ds_hip_layer_t *L0 = S->layers[0];
+    return dsh_launch_lm_final_scores(S->cand, S->ncand, S->tokens, S->step, zp, zn, embed ? S->emb : NULL,
+                                      S->emb_vocab, embed ? S->ebuf : NULL, S->xs, S->stride, S->rows,
+                                      L0->d.router_f32_t, S->H, L0->E, S->partials[0], dsr_stream);
+  }
   return dsh_launch_lm_argmax_final(S->cand, S->ncand, S->tokens, S->step, zp, zn, embed ? S->emb : NULL,
                                     S->emb_vocab, S->H, embed ? S->ebuf : NULL, dsr_stream);
 }
@@ -1164,6 +1175,23 @@ static int split_eligible(const ds_hip_stack_t *S) {
   for (int l = 0; l < S->n_layers; l++)
     if (!dsh_layer_split_supported(&S->layers[l]->d)) return 0;
   return 1;
+}
+
+/* Whether the final kernel also computes the next step's first router partials. */
+static int merged_eligible(const ds_hip_stack_t *S) {
+  return S->split && S->route_mode == DS_HIP_ROUTE_CFG && !S->bf16sim && !S->dense && !S->attn && S->lm_fast &&
+         !smp_active(S);
+}
+
+/* The current step's first router partials, where the step's final kernel computes the next ones
+ * (after a reset, and at every run call: the caller may have rewritten the bound input since). */
+static int scores_refresh(ds_hip_stack_t *S) {
+  if (!S->merged) return 0;
+  const ds_hip_layer_t *L0 = S->layers[0];
+  DSR_TRY(dsh_launch_dec_partial_scores(L0->d.router_f32_t, S->in, S->in_step, S->in_stride, S->H, L0->E,
+                                        S->partials[0], dsr_stream),
+          "router partials");
+  return 0;
 }
 
 /* Allocates and fills the per-layer tiles and products and the copies regions. */
@@ -1369,8 +1397,10 @@ int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int n_
   S->in_stride = S->emb ? 0 : stride;
   S->cap = ds_hip_stack_capacity_for(n_rows, S->emb ? 0 : stride, n_tokens, stack_kv_room(S));
   DSR_TRY(hipStreamSynchronize(dsr_stream), "bind");
+  S->rows = n_rows;
   S->split = split_eligible(S);
   if (S->split && split_build(S)) return -1;
+  S->merged = merged_eligible(S);
   DSR_TRY(hipStreamBeginCapture(dsr_stream, hipStreamCaptureModeThreadLocal), "graph capture begin");
   hipError_t e = step_enqueue(S, NULL);
   hipGraph_t g = NULL;
@@ -1400,7 +1430,7 @@ int ds_hip_stack_reset(ds_hip_stack_t *S) {
   if (S->emb)
     DSR_TRY(hipMemcpyAsync(S->ebuf, S->xs, (size_t)S->H * 4, hipMemcpyDeviceToDevice, dsr_stream), "reset stack");
   S->done = 0;
-  return 0;
+  return scores_refresh(S);
 }
 
 /* Refuses, before anything is launched, n more steps than the bound buffers hold. */
@@ -1413,8 +1443,7 @@ static int steps_check(const ds_hip_stack_t *S, int n, const char *who) {
   return 0;
 }
 
-int ds_hip_stack_run(ds_hip_stack_t *S, int n_steps) {
-  if (steps_check(S, n_steps, "ds_hip_stack_run")) return -1;
+static int graph_steps(ds_hip_stack_t *S, int n_steps) {
   for (int i = 0; i < n_steps; i++) {
     DSR_TRY(hipGraphLaunch(S->exec, dsr_stream), "graph launch");
     S->done++;
@@ -1422,8 +1451,13 @@ int ds_hip_stack_run(ds_hip_stack_t *S, int n_steps) {
   return 0;
 }
 
+int ds_hip_stack_run(ds_hip_stack_t *S, int n_steps) {
+  if (steps_check(S, n_steps, "ds_hip_stack_run") || scores_refresh(S)) return -1;
+  return graph_steps(S, n_steps);
+}
+
 int ds_hip_stack_run_eager(ds_hip_stack_t *S, int n_steps) {
-  if (steps_check(S, n_steps, "ds_hip_stack_run_eager")) return -1;
+  if (steps_check(S, n_steps, "ds_hip_stack_run_eager") || scores_refresh(S)) return -1;
   for (int i = 0; i < n_steps; i++) {
     hipError_t e = step_enqueue(S, NULL);
     S->done++;
@@ -1439,12 +1473,12 @@ int ds_hip_stack_hidden(ds_hip_stack_t *S, float *x_host) {
 
 int ds_hip_time_stack(ds_hip_stack_t *S, int n_steps, float *ms) {
   if (!ms) return dsr_failf("ds_hip_time_stack: invalid arguments");
-  if (steps_check(S, n_steps, "ds_hip_time_stack")) return -1;
+  if (steps_check(S, n_steps, "ds_hip_time_stack") || scores_refresh(S)) return -1;
   hipEvent_t a, b;
   DSR_TRY(hipEventCreate(&a), "event");
   DSR_TRY(hipEventCreate(&b), "event");
   int rc = 0;
-  if (hipEventRecord(a, dsr_stream) != hipSuccess || ds_hip_stack_run(S, n_steps) ||
+  if (hipEventRecord(a, dsr_stream) != hipSuccess || graph_steps(S, n_steps) ||
       hipEventRecord(b, dsr_stream) != hipSuccess || hipEventSynchronize(b) != hipSuccess ||
       hipEventElapsedTime(ms, a, b) != hipSuccess)
     rc = dsr_failf("ds_hip_time_stack: timing failed");
@@ -1470,7 +1504,7 @@ static void events_destroy(hipEvent_t *ev, int n) {
 
 int ds_hip_time_stack_each(ds_hip_stack_t *S, int n_steps, float *ms_each) {
   if (!ms_each || n_steps <= 0) return dsr_failf("ds_hip_time_stack_each: invalid arguments");
-  if (steps_check(S, n_steps, "ds_hip_time_stack_each")) return -1;
+  if (steps_check(S, n_steps, "ds_hip_time_stack_each") || scores_refresh(S)) return -1;
   hipEvent_t *ev = (hipEvent_t *)calloc((size_t)n_steps + 1, sizeof(hipEvent_t));
   if (!ev || events_create(ev, n_steps + 1)) {
     free(ev);
@@ -1492,7 +1526,7 @@ int ds_hip_time_stack_each(ds_hip_stack_t *S, int n_steps, float *ms_each) {
 
 int ds_hip_time_stack_span(ds_hip_stack_t *S, int n_steps, int k0, int k1, float *ms_each) {
   if (!ms_each || n_steps <= 0) return dsr_failf("ds_hip_time_stack_span: invalid arguments");
-  if (steps_check(S, n_steps, "ds_hip_time_stack_span")) return -1;
+  if (steps_check(S, n_steps, "ds_hip_time_stack_span") || scores_refresh(S)) return -1;
   const int nk = stack_kernel_count(S);
   if (k0 < 0 || k1 <= k0 || k1 > nk) return dsr_failf("ds_hip_time_stack_span: kernel range [%d, %d) of %d", k0, k1, nk);
   hipEvent_t *marks = (hipEvent_t *)calloc((size_t)nk + 1, sizeof(hipEvent_t));
@@ -1530,7 +1564,7 @@ int ds_hip_time_lm_head(ds_hip_stack_t *S, int n, float *ms) {
   for (int i = 0; i < n && e == hipSuccess; i++) {
     if (S->split && S->lm_fast && !S->attn) {  /* the head kernel of the step (on the layer copies) */
       e = dsh_launch_dec_lm_argmax_copies(S->lm, xc_region(S, S->n_layers - 1), dsh_layer_split_copies(), S->H,
-                                          S->vocab, S->cand, NULL, dsr_stream);
+                                          S->vocab, S->cand, NULL, NULL, dsr_stream);
     } else if (S->lm_fast) {
       e = dsh_launch_dec_lm_argmax(S->lm, lm_in(S), S->H, S->vocab, S->cand, dsr_stream);
     } else {
@@ -1563,7 +1597,7 @@ const char *ds_hip_stack_kernel_name(const ds_hip_stack_t *S, int i) {
 
 int ds_hip_profile_stack(ds_hip_stack_t *S, int n_steps, float *ms_out) {
   if (!ms_out || n_steps <= 0) return dsr_failf("ds_hip_profile_stack: invalid arguments");
-  if (steps_check(S, n_steps, "ds_hip_profile_stack")) return -1;
+  if (steps_check(S, n_steps, "ds_hip_profile_stack") || scores_refresh(S)) return -1;
   int nk = stack_kernel_count(S);
   hipEvent_t *ev = (hipEvent_t *)calloc((size_t)(nk + 1), sizeof(hipEvent_t));
   double *acc = (double *)calloc((size_t)nk, sizeof(double));

@@ -159,3 +159,55 @@ def test_embedding_feed_with_sampling(dev, B):
         L.ds_hip_stack_destroy(S)
         for h in hs:
             L.ds_hip_layer_destroy(h)
+
+
+def test_rewritten_input_rows_are_seen(dev, B):
+    """One-kernel layers in CFG routing: the step's final kernel also computes the next step's first
+    router partials, and every run call recomputes the current step's. Rows of the bound input the
+    caller rewrites between run calls must be what the later steps read: two steps, rows 2 and 3
+    rewritten, two more steps; those steps against a stack bound to the rewritten rows from the
+    start and against the oracle."""
+    L = dev.load()
+    H, vocab, n = 256, 3000, 4
+    lays, hs, lm_w = small_stack(dev, B, 560)
+    lm = dev.DeviceBuffer.from_array(lm_w)
+    xs = np.stack([B.normal_f32(H, 5600 + s) for s in range(n)])
+    xs_new = xs.copy()
+    xs_new[2:] = np.stack([B.normal_f32(H, 5700 + s) for s in range(2)])
+    arr = (C.c_void_p * len(hs))(*hs)
+
+    def run(x_bind, rewrite):
+        xd = dev.DeviceBuffer.from_array(x_bind)
+        td = dev.DeviceBuffer(4 * n)
+        S = L.ds_hip_stack_create(arr, len(hs), lm.ptr, vocab, dev.ROUTE_CFG)
+        assert S, L.ds_hip_last_error()
+        try:
+            dev.check(L.ds_hip_stack_set_layer_kernels(S, 1), "kernels")
+            dev.check(L.ds_hip_stack_bind(S, xd.ptr, H, n, td.ptr, n), "bind")
+            names = [L.ds_hip_stack_kernel_name(S, i).decode() for i in range(L.ds_hip_stack_kernel_count(S))]
+            assert names[-1] == "lm_head.final+scores" and "scores" not in names, names
+            hid = []
+            for s in range(n):
+                if s == 2 and rewrite:
+                    dev.check(L.ds_hip_sync(), "sync")
+                    xd.write(xs_new)
+                dev.check(L.ds_hip_stack_run(S, 1), "run")
+                hx = np.empty(H, np.float32)
+                dev.check(L.ds_hip_stack_hidden(S, hx), "hidden")
+                hid.append(hx)
+            return td.to_array(np.int32), np.stack(hid)
+        finally:
+            L.ds_hip_stack_destroy(S)
+
+    try:
+        toks, hid = run(xs, True)
+        toks_ref, hid_ref = run(xs_new, False)
+        _, rh = oracle_decode(B, lays, lm_w, vocab, xs_new, dev.ROUTE_CFG)
+        for s in range(n):
+            err, err_ref = rel_err(hid[s], rh[s]), rel_err(hid[s], hid_ref[s])
+            print(f"rewritten input, step {s}: vs oracle {err:.2e}, vs a stack bound to the new rows {err_ref:.2e}")
+            assert err < TOL and err_ref < 1e-5
+            assert toks[s] == B.oracle().or_argmax_bf16(hid[s], lm_w, H, vocab, 1, None)
+    finally:
+        for h in hs:
+            L.ds_hip_layer_destroy(h)
