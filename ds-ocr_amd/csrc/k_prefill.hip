@@ -447,11 +447,11 @@ __global__ void __launch_bounds__(1024) k_pf_plan(const int *__restrict__ idx, i
   }
   __syncthreads();
   if (wave == 0) {  // lane = expert
-    int c = 0;
-    for (int v = 0; v < 16; v++) {
-      run[v][lane] = c;
-      c += lane < E ? cnt[v][lane] : 0;
-    }
+    int cv[16], c = 0;  // the waves' counts, all read before the prefix
+#pragma unroll
+    for (int v = 0; v < 16; v++) cv[v] = lane < E ? cnt[v][lane] : 0;
+#pragma unroll
+    for (int v = 0; v < 16; v++) c += cv[v];
     int incl = c;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -459,7 +459,12 @@ __global__ void __launch_bounds__(1024) k_pf_plan(const int *__restrict__ idx, i
       if (lane >= d) incl += o;
     }
     const int off = incl - c;
-    for (int v = 0; v < 16; v++) run[v][lane] += off;
+    int r = off;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      run[v][lane] = r;
+      r += cv[v];
+    }
     if (lane < E) seg_off[lane] = off;
     const int total = __shfl(incl, 63);
     if (lane == 0) seg_off[E] = total;
@@ -473,12 +478,15 @@ __global__ void __launch_bounds__(1024) k_pf_plan(const int *__restrict__ idx, i
     const int nr = __shfl(ich, 63);
     ich -= nch;
     for (int j = 0; j < nch; j++) items[ich + j] = pf_item{lane, j * PF_MT, min(PF_MT, c - j * PF_MT), off};
-    // routed GEMM tiles, expert by expert: n-tile major, the expert's chunks adjacent, so the
-    // blocks that stream the same weight rows run side by side (item << 8 | n-tile)
-    for (int nt = 0; nt < nt_gu; nt++)
-      for (int j = 0; j < nch; j++) tiles_gu[ich * nt_gu + nt * nch + j] = ((ich + j) << 8) | nt;
-    for (int nt = 0; nt < nt_dn; nt++)
-      for (int j = 0; j < nch; j++) tiles_dn[ich * nt_dn + nt * nch + j] = ((ich + j) << 8) | nt;
+    // routed GEMM tiles of the two-launch path, expert by expert: n-tile major, the expert's chunks
+    // adjacent, so the blocks that stream the same weight rows run side by side (item << 8 |
+    // n-tile); the fused kernel takes its queues instead
+    if (!Q.enable) {
+      for (int nt = 0; nt < nt_gu; nt++)
+        for (int j = 0; j < nch; j++) tiles_gu[ich * nt_gu + nt * nch + j] = ((ich + j) << 8) | nt;
+      for (int nt = 0; nt < nt_dn; nt++)
+        for (int j = 0; j < nch; j++) tiles_dn[ich * nt_dn + nt * nch + j] = ((ich + j) << 8) | nt;
+    }
     const int ns = (T + PF_MT - 1) / PF_MT;
     for (int j = lane; j < ns; j += 64) items[nr + j] = pf_item{E, j * PF_MT, min(PF_MT, T - j * PF_MT), 0};
     if (lane == 0) {
@@ -530,7 +538,7 @@ __global__ void __launch_bounds__(1024) k_pf_plan(const int *__restrict__ idx, i
       for (int nt = 0; nt < Q.ndn; nt++) qt[dn0 + nt] = (int)(PF_DN_TILE | (u << 8) | nt);
     }
   }
-  __syncthreads();
+  // the pair positions (no barrier: they read only run and the cached entries, both complete)
   for (int base = lo; base < hi; base += 64) {
     const int i = base + lane;
     const int e = i < hi ? (cached ? cache[i] : idx[i]) : -1;
