@@ -1124,6 +1124,7 @@ __global__ void __launch_bounds__(64) k_pf_xcc_probe(int *__restrict__ out) {
 }
 
 // ---------------------------------------------------------------------------------- combine
+#define PF_CB 8  // routed slots whose rows a combine thread loads before adding them
 // One block per token: routed slots in ascending expert order (the reference's scatter-add order,
 // ds_moe_decoder.c:781-795; equal experts keep slot order), weights w_k, then the shared output
 // and the residual.
@@ -1154,31 +1155,56 @@ __global__ void __launch_bounds__(256) k_pf_combine(const float *__restrict__ X,
     if (lane == 0) s_n = n;
   }
   __syncthreads();
-  const int n = s_n;
-  for (int c = threadIdx.x; c < H / 4; c += 256) {
-    f32x4 routed = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j = 0; j < n; j++) {
-      f32x4 v = ((const f32x4 *)(Y + (size_t)s_pos[j] * H))[c];
-      const float wj = s_w[j];
+  // a thread's (up to) two 4-float columns (H <= 2048), every row's load of a group of PF_CB slots
+  // issued before the adds, which keep the slot order; clamped duplicates are loaded, not stored
+  const int n = s_n, nc = H / 4;
+  int cc[2];
+  f32x4 routed[2], sh[2], xr[2];
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        if (bf16sim) v[i] = dsh_bf16_round_half_up(v[i]);
-        routed[i] = __builtin_fmaf(wj, v[i], routed[i]);
-      }
+  for (int h = 0; h < 2; h++) {
+    cc[h] = min((int)threadIdx.x + 256 * h, nc - 1);
+    routed[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    sh[h] = ((const f32x4 *)(Ysh + (size_t)t * H))[cc[h]];
+    xr[h] = residual ? ((const f32x4 *)(X + (size_t)t * H))[cc[h]] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  for (int j0 = 0; j0 < n; j0 += PF_CB) {
+    f32x4 v[2][PF_CB];
+#pragma unroll
+    for (int j = 0; j < PF_CB; j++) {
+      const float *row = Y + (size_t)s_pos[min(j0 + j, n - 1)] * H;
+#pragma unroll
+      for (int h = 0; h < 2; h++) v[h][j] = ((const f32x4 *)row)[cc[h]];
     }
-    f32x4 sh = ((const f32x4 *)(Ysh + (size_t)t * H))[c];
+    // every load issued before the adds (their early exit would otherwise pull the loads in)
+    asm volatile("" : "+v"(v[0][0]), "+v"(v[0][1]), "+v"(v[0][2]), "+v"(v[0][3]), "+v"(v[0][4]), "+v"(v[0][5]),
+                 "+v"(v[0][6]), "+v"(v[0][7]), "+v"(v[1][0]), "+v"(v[1][1]), "+v"(v[1][2]), "+v"(v[1][3]),
+                 "+v"(v[1][4]), "+v"(v[1][5]), "+v"(v[1][6]), "+v"(v[1][7]));
+#pragma unroll
+    for (int j = 0; j < PF_CB; j++) {
+      if (j0 + j >= n) break;
+      const float wj = s_w[j0 + j];
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          float vv = v[h][j][i];
+          if (bf16sim) vv = dsh_bf16_round_half_up(vv);
+          routed[h][i] = __builtin_fmaf(wj, vv, routed[h][i]);
+        }
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    if ((int)threadIdx.x + 256 * h >= nc) break;
     f32x4 o;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      if (bf16sim) sh[i] = dsh_bf16_round_half_up(sh[i]);
-      o[i] = routed[i] + sh[i];
+      float s2 = sh[h][i];
+      if (bf16sim) s2 = dsh_bf16_round_half_up(s2);
+      o[i] = routed[h][i] + s2;
+      if (residual) o[i] = xr[h][i] + o[i];
     }
-    if (residual) {
-      const f32x4 x = ((const f32x4 *)(X + (size_t)t * H))[c];
-#pragma unroll
-      for (int i = 0; i < 4; i++) o[i] = x[i] + o[i];
-    }
-    ((f32x4 *)(out + (size_t)t * H))[c] = o;
+    ((f32x4 *)(out + (size_t)t * H))[cc[h]] = o;
   }
 }
 
