@@ -653,9 +653,12 @@ __device__ __forceinline__ void pf_align16(u32x4 &lo, u32x4 &hi, int d) {
 }
 
 // SwiGLU of the prefill GEMM: (g / (1 + fast_exp(-g))) * u (ds_kernels.c:1771) with the quotient
-// from the hardware reciprocal and one Newton step (within an ulp of the correctly rounded
-// quotient; the prefill is compared with its reference under a tolerance, the decode path keeps
-// dsh_swiglu's exact division).
+// from the hardware reciprocal refined by one Newton step. The reciprocal flushes a subnormal
+// result and g * r can fall below the normal range, so a denominator above 2^126 (g < -87) is
+// scaled, with g, by 2^-64, and |g| < 2^-96 is scaled by 2^64 and the quotient scaled back
+// (exact while the quotient is normal). Checked on the GPU over every 32-bit g: equal to the
+// correctly rounded division for every finite g whose quotient is a normal float; it can differ
+// only where |g| < 2.4e-38 (a gate value is an integer sum times two scales, never that small).
 __device__ __forceinline__ float pf_swiglu(float g, float u) {
   // dsh_fast_expf(-g) without branches: the same bits for every input (0 below -88, 1e38 above
   // 88, 0 for NaN; the argument clamped so the integer conversion stays in range)
@@ -664,11 +667,14 @@ __device__ __forceinline__ float pf_swiglu(float g, float u) {
   ex = x < -88.0f ? 0.0f : ex;
   ex = x > 88.0f ? 1e38f : ex;
   ex = x != x ? 0.0f : ex;
-  const float d = 1.0f + ex;
+  const float d0 = 1.0f + ex;
+  const bool big = d0 > 0x1p126f, tiny = __builtin_fabsf(g) < 0x1p-96f;
+  const float d = big ? d0 * 0x1p-64f : d0;
+  const float gs = g * (big ? 0x1p-64f : (tiny ? 0x1p64f : 1.0f));
   const float r = __builtin_amdgcn_rcpf(d);
-  float q = g * r;
-  q = __builtin_fmaf(__builtin_fmaf(-d, q, g), r, q);
-  return q * u;
+  float q = gs * r;
+  q = __builtin_fmaf(__builtin_fmaf(-d, q, gs), r, q);
+  return (tiny ? q * 0x1p-64f : q) * u;
 }
 
 // 16-byte chunk c of LDS row r sits at chunk c ^ pf_swz(r): 16 consecutive rows map one chunk to 16
