@@ -99,6 +99,10 @@ int dsh_pf_wait_error(const void *ws, const dsh_layer_t *L, int T);
 /* out[T][H] = (residual ? X : 0) + MoE(X); ws: dsh_pf_workspace_bytes(L, T) device bytes. */
 hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int route_mode, int nthreads, int residual,
                               int bf16sim, float *out, void *ws, int *idx_out, float *w_out, hipStream_t s);
+/* The prefill SwiGLU against the correctly rounded division over every 32-bit gate value: counts[0]
+ * = finite g with a zero or normal quotient whose results differ, counts[1] = those with a
+ * subnormal quotient (2 device words, cleared here). */
+hipError_t dsh_launch_pf_swiglu_check(unsigned long long *counts, hipStream_t s);
 
 /* Final reduction of per-block argmax candidates: writes tokens[*step] (tokens[0] when step is
  * NULL) and advances *step. Also clears zero_p[0..zero_n) (16-byte aligned, zero_n % 4 == 0; 0 for

@@ -656,9 +656,10 @@ __device__ __forceinline__ void pf_align16(u32x4 &lo, u32x4 &hi, int d) {
 // from the hardware reciprocal refined by one Newton step. The reciprocal flushes a subnormal
 // result and g * r can fall below the normal range, so a denominator above 2^126 (g < -87) is
 // scaled, with g, by 2^-64, and |g| < 2^-96 is scaled by 2^64 and the quotient scaled back
-// (exact while the quotient is normal). Checked on the GPU over every 32-bit g: equal to the
-// correctly rounded division for every finite g whose quotient is a normal float; it can differ
-// only where |g| < 2.4e-38 (a gate value is an integer sum times two scales, never that small).
+// (exact while the quotient is normal); the quotient takes g's sign (the Newton step turns -0 into
+// +0). k_pf_swiglu_check compares it with the correctly rounded division over every 32-bit g:
+// equal for every finite g whose quotient is zero or a normal float, so it can differ only where
+// |g| < 2.4e-38 (a gate value is an integer sum times two scales, never that small).
 __device__ __forceinline__ float pf_swiglu(float g, float u) {
   // dsh_fast_expf(-g) without branches: the same bits for every input (0 below -88, 1e38 above
   // 88, 0 for NaN; the argument clamped so the integer conversion stays in range)
@@ -674,7 +675,39 @@ __device__ __forceinline__ float pf_swiglu(float g, float u) {
   const float r = __builtin_amdgcn_rcpf(d);
   float q = gs * r;
   q = __builtin_fmaf(__builtin_fmaf(-d, q, gs), r, q);
-  return (tiny ? q * 0x1p-64f : q) * u;
+  return __builtin_copysignf(tiny ? q * 0x1p-64f : q, g) * u;
+}
+
+// pf_swiglu(g, 1) against dsh_swiglu(g, 1) for the 2^30 bit patterns g = base + i of one launch
+// (65536 blocks x 64 iterations x 256 threads; four launches cover every 32-bit g). counts[0] gets
+// the finite g whose correctly rounded quotient is zero or normal and whose results differ in any
+// bit, counts[1] the finite g with a subnormal quotient whose results differ. Two NaNs count as
+// equal: for 87.9895 < g <= 88 the fast exp's affine value is negative and its signed conversion
+// wraps to a NaN bit pattern, so both forms (and the reference) give NaN there.
+__global__ void __launch_bounds__(256) k_pf_swiglu_check(uint32_t base, unsigned long long *counts) {
+  unsigned long long n0 = 0, n1 = 0;
+  for (int it = 0; it < 64; it++) {
+    const uint32_t bits = base + ((uint32_t)(blockIdx.x * 64 + it) << 8) + threadIdx.x;
+    const float g = __uint_as_float(bits);
+    const float a = dsh_swiglu(g, 1.0f), b = pf_swiglu(g, 1.0f);
+    const bool differ = __builtin_isfinite(g) && !(a != a && b != b) && __float_as_uint(a) != __float_as_uint(b);
+    const bool sub = a != 0.0f && __builtin_fabsf(a) < 0x1p-126f;
+    n0 += __popcll(__ballot(differ && !sub));
+    n1 += __popcll(__ballot(differ && sub));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    if (n0) atomicAdd(&counts[0], n0);
+    if (n1) atomicAdd(&counts[1], n1);
+  }
+}
+
+hipError_t dsh_launch_pf_swiglu_check(unsigned long long *counts, hipStream_t s) {
+  hipError_t e = hipMemsetAsync(counts, 0, 2 * sizeof(unsigned long long), s);
+  for (uint32_t ch = 0; ch < 4 && e == hipSuccess; ch++) {
+    k_pf_swiglu_check<<<65536, 256, 0, s>>>(ch << 30, counts);
+    e = hipGetLastError();
+  }
+  return e;
 }
 
 // 16-byte chunk c of LDS row r sits at chunk c ^ pf_swz(r): 16 consecutive rows map one chunk to 16

@@ -387,6 +387,23 @@ int ds_hip_prefill_path(int mode) {
   return dsh_pf_fused();
 }
 
+/* The prefill SwiGLU against the correctly rounded division over all 2^32 gate values (u = 1):
+ * n_differ[0] = finite g with a zero or normal quotient whose results differ in any bit,
+ * n_differ[1] = finite g with a subnormal quotient whose results differ. Synchronous. */
+int ds_hip_check_prefill_swiglu(uint64_t *n_differ) {
+  if (dsr_init()) return -1;
+  if (!n_differ) return dsr_failf("ds_hip_check_prefill_swiglu: invalid arguments");
+  unsigned long long *c = (unsigned long long *)dsr_scratch(DSR_SLOT_IDX, 2 * sizeof(unsigned long long));
+  if (!c) return -1;
+  unsigned long long h[2];
+  DSR_TRY(dsh_launch_pf_swiglu_check(c, dsr_stream), "swiglu check");
+  DSR_TRY(hipMemcpyAsync(h, c, sizeof h, hipMemcpyDeviceToHost, dsr_stream), "copy");
+  DSR_TRY(hipStreamSynchronize(dsr_stream), "sync");
+  n_differ[0] = h[0];
+  n_differ[1] = h[1];
+  return 0;
+}
+
 /* After a prefill call of T tokens on layer L: 1 if the fused kernel's bounded wait expired (the
  * output is then not valid), 0 if not. Synchronises the library stream. */
 int ds_hip_prefill_wait_error(ds_hip_layer_t *L, int T) {

@@ -101,8 +101,9 @@ int ds_hip_layer_forward(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
 
 /* Prefill MoE block for T tokens (ds_moe_decoder.c:629-809, on this layer's INT8 blocks):
  * out_dev[T][hidden] = (residual ? x : 0) + MoE(x_dev[T][hidden]). Routing per token as
- * ds_hip_layer_forward (route_mode), experts as an expert-sorted grouped GEMM on bf16 MFMA, routed
- * outputs added in ascending expert order, then the shared expert. idx_dev/w_dev (optional,
+ * ds_hip_layer_forward (route_mode), experts as an expert-sorted grouped GEMM on the int8 MFMA
+ * (each f32 activation row as two 8-bit limbs, exact integer sums), routed outputs added in
+ * ascending expert order, then the shared expert. idx_dev/w_dev (optional,
  * [T][top_k]) receive the routing. Asynchronous; out_dev must not alias x_dev. */
 int ds_hip_layer_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, int T, int route_mode, int residual,
                          int *idx_dev, float *w_dev);
@@ -118,6 +119,13 @@ int ds_hip_prefill_path(int mode);
 /* After a prefill call of T tokens on L: 1 if the persistent kernel's bounded wait for a gate_up
  * tile expired (that call's output is not valid), 0 if not, -1 on error. Synchronises. */
 int ds_hip_prefill_wait_error(ds_hip_layer_t *L, int T);
+
+/* Self-check of the prefill SwiGLU (no counterpart in the reference): the GEMM epilogue's
+ * reciprocal-based (g / (1 + fast_exp(-g))) * u against the correctly rounded division of
+ * ds_swiglu_direct (ds_kernels.c:1771) over all 2^32 gate values, u = 1. n_differ[0]: finite g
+ * with a zero or normal quotient whose results differ in any bit (0 expected), n_differ[1]: finite
+ * g with a subnormal quotient (|g| < 2.4e-38) whose results differ. About a second; synchronous. */
+int ds_hip_check_prefill_swiglu(uint64_t *n_differ);
 
 /* ---------------- dense FFN layer (layer 0 of the decoder) ---------------- */
 /* The decoder's dense SwiGLU FFN (ds_moe_decoder.c:75-105, dense_ffn_forward): gate [inter, hidden],

@@ -238,3 +238,15 @@ def test_prefill_cfg_near_ties_recomputed(dev, B):
         assert ulp.max() <= 2, ulp.max()
     finally:
         L.ds_hip_layer_destroy(h)
+
+
+def test_prefill_swiglu_equals_division_on_every_gate_value(dev):
+    """The GEMM epilogue's SwiGLU quotient (hardware reciprocal, one Newton step, power-of-two
+    rescales at the ends of the range) against the correctly rounded division the decode kernels use
+    (ds_swiglu_direct, ds_kernels.c:1771), over all 2^32 gate values: every finite g whose quotient
+    is zero or normal gives the same bits; only quotients below 2^-126 may differ."""
+    L = dev.load()
+    n = (C.c_uint64 * 2)()
+    dev.check(L.ds_hip_check_prefill_swiglu(n), "swiglu check")
+    assert n[0] == 0, n[0]
+    assert n[1] <= 2 ** 25, n[1]  # only among the g with |g| < 2^-125 (2^24 bit patterns per sign)
