@@ -75,8 +75,7 @@ __device__ __forceinline__ void dl_issue(dl_regs<CPL> &R, const int8_t *gu, cons
 template <int CPL>
 struct dl_smem {
   static constexpr int H = 256 * CPL, NP = 64 * CPL, NL = 4;
-  int s_idx[64];
-  float s_w[64];
+  float s_w[1];  // routed blocks: the expert weight
   float s_red[4][64];
   float s_stat[16];
   __attribute__((aligned(16))) unsigned s_lq[NL * NP];
@@ -93,9 +92,8 @@ __device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t 
                                         const int *__restrict__ step, int stride, const float *partials, int np,
                                         int mode, const float *__restrict__ resid, float *x_out, float *lg_out,
                                         float *zero_p, int zero_n, dl_smem<CPL> &S) {
-  // x pieces (4 values each): routed blocks leave wave 0 free to select the expert while waves 1-7
-  // load and sum the input, so piece p belongs to thread XO + p % XT of round p / XT
-  constexpr int XO = SH ? 0 : 64, XT = 512 - XO;
+  // x pieces (4 values each): piece p belongs to thread XO + p % XT of round p / XT
+  constexpr int XO = 0, XT = 512 - XO;
   constexpr int H = 256 * CPL, NP = 64 * CPL, XV = (NP + XT - 1) / XT, NL = 4;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, sub = lane & 15, grp = lane >> 4;
   const int th = t & 255, half = t >> 8;
@@ -132,6 +130,24 @@ __device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t 
     for (int j = 0; j < 8; j++) wr[j] = F.WrT_next[(size_t)(blk * 8 + j) * F.E_next + lane];
   }
   asm volatile("" ::: "memory");
+
+  // A wave that issues its weight rows (15 loads per lane, 120 KB per block) cannot execute past
+  // them until the memory system has accepted them, which takes about as long as they take to
+  // arrive; whatever the wave does after the issue, and any barrier after it, waits that long. So
+  // each block finishes its preparation (x summed and converted to limbs, the selection) first and
+  // issues last, with no barrier between the issue and the dot products: each wave starts its gate
+  // and up products as its own rows arrive. Shared-expert blocks need no selection and issue right
+  // behind their input loads (which return first: a wave's loads complete in issue order). In a
+  // routed block every wave runs the selection's rounds up to the block's slot itself; wave 0 then
+  // finishes the rounds and the expert weight (the CFG softmax over all selected experts) while
+  // its rows stream, and passes it through LDS.
+  dl_regs<CPL> R;
+  float wexp = 1.0f;  // this block's expert weight (1 for the shared expert)
+  if constexpr (shared_blk) {
+    dl_issue<CPL>(R, L.sgu_q, L.sgu_so, (size_t)sl * DL_UB, (size_t)SI + sl * DL_UB,
+                  F.sdnT + (size_t)sl * DL_UB * H, L.sdn_so, F.sM ? F.sM + (size_t)sl * 2048 : nullptr, F.sz);
+    asm volatile("" ::: "memory");
+  }
   if (!shared_blk && wave < 4) {
     float acc = 0.0f;
 #pragma unroll
@@ -139,24 +155,6 @@ __device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t 
       if (wave + 4 * j < np) acc += pv[j];
     S.s_red[wave][lane] = lane < L.E ? acc : 0.0f;
   }
-  __syncthreads();  // s_red
-
-  // Shared-expert blocks stream their weights at once. Routed blocks select their expert, then
-  // issue its weights only after the block's last barrier before the dot products: a wave's loads
-  // are accepted only as fast as the memory system drains them, so a barrier behind them would hold
-  // every wave until the block's whole stream has gone out; without one, each wave starts its gate
-  // and up products when its own rows arrive, while the down tile is still streaming.
-  dl_regs<CPL> R;
-  float wexp = 1.0f;  // this block's expert weight (1 for the shared expert)
-  int e = 0;
-  if constexpr (shared_blk) {
-    dl_issue<CPL>(R, L.sgu_q, L.sgu_so, (size_t)sl * DL_UB, (size_t)SI + sl * DL_UB,
-                  F.sdnT + (size_t)sl * DL_UB * H, L.sdn_so, F.sM ? F.sM + (size_t)sl * 2048 : nullptr, F.sz);
-    asm volatile("" ::: "memory");
-  } else if (wave == 0) {  // the selection, read by every wave after the next barrier
-    route_select(L.E, L.K, mode, S.s_idx, S.s_w, S.s_red);
-  }
-
   // x: the copies summed in copy order; max|x| and Σx per wave
   f32x4 xs[XV];
   {
@@ -182,7 +180,7 @@ __device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t 
       S.s_stat[8 + wave] = sx;
     }
   }
-  __syncthreads();  // s_stat, s_x
+  __syncthreads();  // s_red, s_stat, s_x
   float xmax = S.s_stat[0], xsum = S.s_stat[8];
 #pragma unroll
   for (int w = 1; w < 8; w++) {
@@ -190,14 +188,6 @@ __device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t 
     xsum += S.s_stat[8 + w];
   }
   const int ex = __builtin_amdgcn_frexp_expf(xmax);  // xmax < 2^ex
-  if constexpr (!shared_blk) {
-    e = S.s_idx[slot];
-    wexp = S.s_w[slot];
-    if (e < 0) {  // DECODE routing left this slot empty: expert 0's rows, added with weight 0
-      e = 0;
-      wexp = 0.0f;
-    }
-  }
 
   // x → limbs, piece p (elements 4p..4p+3) into word p of each limb array
 #pragma unroll
@@ -221,11 +211,25 @@ __device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t 
   }
   __syncthreads();  // limbs
   if constexpr (!shared_blk) {
+    route_state st;
+    route_init(L.E, L.K, mode, S.s_red, st);
+    const int r1 = min(slot + 1, st.ns);
+    route_rounds(st, 0, r1);
+    // the slot's expert: rank `slot` (an empty slot streams expert 0's rows, added with weight 0)
+    const int e = slot < st.ns ? __builtin_amdgcn_readlane(st.sel, slot) : 0;
     const size_t g0 = (size_t)e * 2 * I + (size_t)sl * DL_UB;
     const size_t tile = (size_t)e * NSL + sl;
     dl_issue<CPL>(R, L.gu_q, L.gu_so, g0, g0 + I, F.dnT + tile * DL_UB * H, L.dn_so + (size_t)e * H * 2,
                   F.M ? F.M + tile * 2048 : nullptr, F.z ? F.z + (size_t)e * 64 : nullptr);
     asm volatile("" ::: "memory");
+    if (wave == 0) {
+      route_rounds(st, r1, st.ns);
+      int idx;
+      float w;
+      route_finish(mode, st, idx, w);
+      const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), slot));
+      if (lane == 0) S.s_w[0] = slot < st.ns ? ws : 0.0f;  // DECODE: an empty slot adds with weight 0
+    }
   }
   {
     int ag[NL] = {}, au[NL] = {};
@@ -255,7 +259,8 @@ __device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t 
     const float up = __builtin_fmaf(R.sou.x, du, ou * xsum);
     if (sub == 0) S.s_h[4 * wave + grp] = dsh_swiglu(g, up);
   }
-  __syncthreads();  // s_h
+  __syncthreads();  // s_h, s_w
+  if constexpr (!shared_blk) wexp = S.s_w[0];
   float hv[16];
 #pragma unroll
   for (int j = 0; j < 16; j += 4) {
