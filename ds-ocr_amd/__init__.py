@@ -128,6 +128,8 @@ SIGNATURES = {
     "ds_hip_stack_set_dense": (C.c_int, [vp, vp]),
     "ds_hip_stack_set_layer_kernels": (C.c_int, [vp, C.c_int]),
     "ds_hip_stack_layer_kernels": (C.c_int, [vp]),
+    "ds_hip_stack_set_lm_certified": (C.c_int, [vp, C.c_int]),
+    "ds_hip_stack_lm_certified": (C.c_int, [vp]),
     "ds_hip_load_dense": (C.c_int, [C.POINTER(C.c_char_p), C.c_int, C.c_int, C.POINTER(vp)]),
     "ds_hip_safetensors_info": (C.c_int, [C.POINTER(C.c_char_p), C.c_int, C.c_char_p, C.POINTER(C.c_int),
                                           C.POINTER(C.c_int64), C.c_int]),

@@ -1,0 +1,388 @@
+// k_lm.hip — the decode step's LM-head argmax in two passes, with the same result as the one-pass
+// kernel (k_dec_lm_argmax, the reference's 4-row-group AVX-512 order, ds_kernels_avx.c:162-245).
+//
+// The argmax needs every row's logit only to decide which row is largest. A per-row int8 copy of
+// the bf16 head (q = rint(w / s), s = max|w| / 127) gives an approximate logit A_r for half the
+// bytes, and a rigorous bound |L_r - A_r| <= B_r on the logit L_r the exact order computes:
+//   L_r - A_r = (L_r - Σ w x)                    rounding of the exact order: <= γ_64 ||w||_2 ||x||_2
+//             + Σ (w - s q) x                     quantization:  <= ||w - s q||_2 ||x||_2
+//             + s Σ q (x - x~)                    the input on a 2^(e-14) grid: <= s ||q||_1 2^(e-15)
+//             + (s Σ q x~ - A_r)                  one rounding of A_r: <= 2^-22 |A_r| (generous)
+// with |x| < 2^e. Per row, α_r = γ_64 ||w||_2 + ||w - s q||_2 and β_r = s ||q||_1 are computed
+// once (f64, rounded up to f32); per step B_r = α_r ||x||_2 + β_r 2^(e-15) + 2^-22 |A_r|.
+// Pass 1 (k_lm_q8_approx) streams the int8 rows, computes A_r from exact integer dot products of
+// the codes with the input's two 8-bit limbs, and writes U_r = A_r + B_r per row and the largest
+// A_r - B_r per block. Pass 2 (k_lm_q8_exact) takes LB = the largest A_r - B_r over all blocks:
+// the row holding the largest exact logit L* has U_r >= L* >= LB, and so does every row tied with
+// it, while a row with U_r < LB has L_r < L*. Pass 2 recomputes the rows with U_r >= LB in the
+// exact order and writes, per block of 256 rows, the same (max, lowest index) key as the one-pass
+// kernel (0 for a block without candidates), so the final reduction is unchanged. NaN or infinite
+// bounds make a row a candidate (the test is !(U_r < LB)), so such inputs fall back to the exact
+// computation of every row they touch.
+#include "dsh.h"
+#include "k_core.h"
+
+#define LM_Q8_ROWS 256  // rows per block in both passes (the one-pass kernel's block)
+
+namespace {
+
+template <int CTRL>
+__device__ __forceinline__ int lm_dppi(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+// exact integer sum over each aligned group of 16 lanes (every lane of the group gets it)
+__device__ __forceinline__ int lm_row16_sum_i(int v) {
+  v += lm_dppi<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += lm_dppi<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += lm_dppi<0x141>(v);  // row_half_mirror
+  v += lm_dppi<0x140>(v);  // row_mirror
+  return v;
+}
+
+__device__ __forceinline__ double lm_wave_max_d(double v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmax(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ double lm_wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// the next float above f (f finite)
+__device__ __forceinline__ float lm_next_up(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) == 0u) return __uint_as_float(1u);  // ±0: the smallest positive subnormal
+  return __uint_as_float((int32_t)u >= 0 ? u + 1u : u - 1u);
+}
+
+// the smallest float >= d (d finite or infinite, not NaN)
+__device__ __forceinline__ float lm_f32_up(double d) {
+  float f = (float)d;
+  if ((double)f < d) f = lm_next_up(f);
+  return f;
+}
+
+constexpr double LM_GAMMA64 = 64.0 * 0x1p-24 / (1.0 - 64.0 * 0x1p-24);
+
+}  // namespace
+
+// One wave per row: q (int8, [vocab][H]) and sab[3 r .. 3 r + 2] = (s, α_r, β_r). A row with a
+// non-finite weight gets α = β = +inf (always a candidate).
+__global__ void __launch_bounds__(256) k_lm_q8_build(const uint16_t *__restrict__ W, int H, int vocab,
+                                                     int8_t *__restrict__ q, float *__restrict__ sab) {
+  const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= vocab) return;  // wave-uniform
+  const uint16_t *w = W + (size_t)row * H;
+  float amax = 0.0f;
+  bool bad = false;
+  for (int j = lane; j < H; j += 64) {
+    const float v = __uint_as_float((uint32_t)w[j] << 16);
+    bad |= !__builtin_isfinite(v);
+    amax = fmaxf(amax, fabsf(v));
+  }
+  amax = dsh_wave_max(amax);
+  bad = __ballot(bad) != 0ull;
+  const float s = amax / 127.0f, inv = amax > 0.0f ? 1.0f / s : 0.0f;
+  double r2 = 0.0, w2 = 0.0, q1 = 0.0;
+  int8_t *qr = q + (size_t)row * H;
+  for (int j = lane; j < H; j += 64) {
+    const float v = __uint_as_float((uint32_t)w[j] << 16);
+    int qi = 0;
+    if (!bad && amax > 0.0f) qi = max(-127, min(127, (int)__builtin_rintf(v * inv)));
+    qr[j] = (int8_t)qi;
+    const double d = (double)v - (double)s * (double)qi;
+    r2 += d * d;
+    w2 += (double)v * (double)v;
+    q1 += (double)abs(qi);
+  }
+  r2 = lm_wave_sum_d(r2);
+  w2 = lm_wave_sum_d(w2);
+  q1 = lm_wave_sum_d(q1);
+  if (lane == 0) {
+    const double a = (LM_GAMMA64 * sqrt(w2) + sqrt(r2)) * (1.0 + 1e-12);
+    const double b = (double)s * q1 * (1.0 + 1e-12);
+    sab[3 * (size_t)row] = s;
+    sab[3 * (size_t)row + 1] = bad ? __builtin_inff() : lm_f32_up(a);
+    sab[3 * (size_t)row + 2] = bad ? __builtin_inff() : lm_f32_up(b);
+  }
+}
+
+// Pass 1. Block = 256 rows (wave w: rows 64w .. 64w + 63 of the block, four per round: lanes
+// 16g .. 16g + 15 take row 4k + g of round k, lane s of them the 16-byte pieces 16s + 256m of the
+// row, m < NM = H / 256, so each load instruction reads 4 rows x 256 contiguous bytes). The input
+// (XC > 0: the sum of XC copies in copy order, as the one-pass kernel forms it; block 0 writes it to
+// x_out) is put on the grid 2^(e-14) (|x| < 2^e) as two 8-bit limbs held by each lane for its own
+// columns; the row's dot products are exact int32 sums. D rounds of loads stay in flight.
+template <int NM, int XC>
+__global__ void __launch_bounds__(256) k_lm_q8_approx(const int8_t *__restrict__ q, const float *__restrict__ sab,
+                                                      const float *__restrict__ x, int vocab,
+                                                      float *__restrict__ x_out, double *__restrict__ U,
+                                                      double *__restrict__ LBb) {
+  constexpr int H = 256 * NM, D = 4, NR = 16;  // rounds of 4 rows per wave
+  __shared__ __attribute__((aligned(16))) float s_x[H];
+  __shared__ float s_sab[3 * LM_Q8_ROWS];
+  __shared__ float s_mx[4];
+  __shared__ double s_sq[4], s_lb[4];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, sub = lane & 15, grp = lane >> 4;
+  const int rb = blockIdx.x * LM_Q8_ROWS;
+  auto src = [&](int k) { return q + (size_t)min(rb + 64 * wave + 4 * k + grp, vocab - 1) * H + 16 * sub; };
+  u32x4 ring[D][NM];
+#pragma unroll
+  for (int k = 0; k < D; k++) {
+    const int8_t *p = src(k);
+#pragma unroll
+    for (int m = 0; m < NM; m++) ring[k][m] = dsh_load_nt(p + 256 * m);
+    asm volatile("" ::: "memory");
+  }
+  // the rows' constants and the input (issued after the first rounds of rows)
+  float cs[3];
+#pragma unroll
+  for (int c = 0; c < 3; c++) cs[c] = sab[3 * (size_t)min(rb + t, vocab - 1) + c];
+  constexpr int NPC = H / 4;  // 4-float pieces of x
+  f32x4 xa[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int p = min(t + 256 * h, NPC - 1);
+    if constexpr (XC > 0) {
+      f32x4 c4[XC];
+#pragma unroll
+      for (int c = 0; c < XC; c++) c4[c] = ((const f32x4 *)(x + (size_t)c * H))[p];
+      f32x4 s4 = c4[0];
+#pragma unroll
+      for (int c = 1; c < XC; c++) s4 += c4[c];
+      xa[h] = s4;
+    } else {
+      xa[h] = ((const f32x4 *)x)[p];
+    }
+  }
+  float mx = 0.0f;
+  double sq = 0.0;
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int p = t + 256 * h;
+    if (p < NPC) {
+      *(f32x4 *)(s_x + 4 * p) = xa[h];
+      if (XC > 0 && x_out && blockIdx.x == 0) *(f32x4 *)(x_out + 4 * p) = xa[h];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        mx = fmaxf(mx, fabsf(xa[h][c]));
+        sq += (double)xa[h][c] * (double)xa[h][c];
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 3; c++) s_sab[3 * t + c] = cs[c];
+  // a NaN input makes mx NaN-free but sq NaN, and the bounds below NaN: every row a candidate
+  mx = dsh_wave_max(mx);
+  sq = lm_wave_sum_d(sq);
+  if (lane == 0) {
+    s_mx[wave] = mx;
+    s_sq[wave] = sq;
+  }
+  __syncthreads();
+  const float xmax = fmaxf(fmaxf(s_mx[0], s_mx[1]), fmaxf(s_mx[2], s_mx[3]));
+  const double x2 = sqrt(((s_sq[0] + s_sq[1]) + (s_sq[2] + s_sq[3])) * (1.0 + 1e-12));
+  const int e = __builtin_amdgcn_frexp_expf(xmax);  // xmax < 2^e
+  const double grid = ldexp(1.0, e - 14), half_grid = ldexp(1.0, e - 15);
+  // this lane's columns 16 sub + 256 m + i as limbs: X = rint(x 2^(14-e)) (|X| <= 2^14) = 256 hi + lo
+  unsigned xlo[NM][4], xhi[NM][4];
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      unsigned lo = 0, hi = 0;
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const int X = (int)__builtin_rintf(__builtin_ldexpf(s_x[16 * sub + 256 * m + 4 * w + b], 14 - e));
+        const int l = __builtin_amdgcn_sbfe(X, 0, 8);
+        lo |= ((unsigned)l & 255u) << (8 * b);
+        hi |= ((unsigned)((X - l) >> 8) & 255u) << (8 * b);
+      }
+      xlo[m][w] = lo;
+      xhi[m][w] = hi;
+    }
+  double lbmax = -__builtin_inf();
+#pragma unroll
+  for (int k = 0; k < NR; k++) {
+    const int sl = k % D;
+    int dlo = 0, dhi = 0;
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        dlo = __builtin_amdgcn_sdot4((int)ring[sl][m][w], (int)xlo[m][w], dlo, false);
+        dhi = __builtin_amdgcn_sdot4((int)ring[sl][m][w], (int)xhi[m][w], dhi, false);
+      }
+    if (k + D < NR) {
+      const int8_t *p = src(k + D);
+#pragma unroll
+      for (int m = 0; m < NM; m++) ring[sl][m] = dsh_load_nt(p + 256 * m);
+      asm volatile("" ::: "memory");
+    }
+    dlo = lm_row16_sum_i(dlo);
+    dhi = lm_row16_sum_i(dhi);
+    const int rr = 64 * wave + 4 * k + grp, row = rb + rr;
+    if (sub == 0 && row < vocab) {
+      const double s = s_sab[3 * rr], a = s_sab[3 * rr + 1], b = s_sab[3 * rr + 2];
+      const double A = s * grid * (256.0 * (double)dhi + (double)dlo);
+      const double B = a * x2 + b * half_grid + 0x1p-22 * fabs(A);
+      U[row] = A + B;
+      lbmax = fmax(lbmax, A - B);
+    }
+  }
+  lbmax = lm_wave_max_d(lbmax);
+  if (lane == 0) s_lb[wave] = lbmax;
+  __syncthreads();
+  if (t == 0) LBb[blockIdx.x] = fmax(fmax(s_lb[0], s_lb[1]), fmax(s_lb[2], s_lb[3]));
+}
+
+// Pass 2. Block b = rows 256b .. 256b + 255, as the one-pass kernel's block. Candidates: rows with
+// !(U_r < LB). Each half-wave takes a candidate: lane c < 32 runs chain c (columns j = c mod 32 in
+// increasing order, fma(w_j, x_j, acc) from 0) and lane 0 of the half adds the chains as
+// _mm512_reduce_add_ps(a0 + a1) does (the one-pass kernel's tree). step_inc: advanced here, as the
+// one-pass kernel does, for the final kernel after it.
+__global__ void __launch_bounds__(256) k_lm_q8_exact(const uint16_t *__restrict__ W, const float *__restrict__ x,
+                                                     int H, int vocab, const double *__restrict__ U,
+                                                     const double *__restrict__ LBb, int nb,
+                                                     unsigned long long *__restrict__ cand, int *__restrict__ step_inc) {
+  if (step_inc && blockIdx.x == 0 && threadIdx.x == 0) *step_inc += 1;
+  __shared__ double s_lb[4];
+  __shared__ int s_n;
+  __shared__ int s_list[LM_Q8_ROWS];
+  __shared__ __attribute__((aligned(16))) float s_x[2048];
+  __shared__ float s_acc[8][32];
+  __shared__ unsigned long long s_best[8];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  double lb = -__builtin_inf();
+  for (int i = t; i < nb; i += 256) lb = fmax(lb, LBb[i]);
+  const int row = blockIdx.x * LM_Q8_ROWS + t;
+  const double u = row < vocab ? U[row] : 0.0;
+  lb = lm_wave_max_d(lb);
+  if (lane == 0) s_lb[wave] = lb;
+  if (t == 0) s_n = 0;
+  __syncthreads();
+  lb = fmax(fmax(s_lb[0], s_lb[1]), fmax(s_lb[2], s_lb[3]));
+  if (row < vocab && !(u < lb)) s_list[atomicAdd(&s_n, 1)] = row;
+  __syncthreads();
+  const int n = s_n;
+  if (n == 0) {
+    if (t == 0) cand[blockIdx.x] = 0ull;
+    return;
+  }
+  for (int i = t; i < H; i += 256) s_x[i] = x[i];
+  __syncthreads();
+  const int half = t >> 5, c = t & 31;
+  unsigned long long best = 0ull;
+  for (int k = half; k < n; k += 8) {
+    const int r = s_list[k];
+    const uint16_t *wr = W + (size_t)r * H;
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int j = c; j < H; j += 32) acc = __builtin_fmaf(__uint_as_float((uint32_t)wr[j] << 16), s_x[j], acc);
+    s_acc[half][c] = acc;
+    // the half's chains are read by its lane 0: LDS executes a wave's operations in order, the
+    // fences keep the compiler from reordering
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (c == 0) {
+      const float *a = s_acc[half];
+      float A[16], T3[8], T6[4];
+#pragma unroll
+      for (int i = 0; i < 16; i++) A[i] = a[i] + a[16 + i];
+#pragma unroll
+      for (int i = 0; i < 8; i++) T3[i] = A[8 + i] + A[i];
+#pragma unroll
+      for (int i = 0; i < 4; i++) T6[i] = T3[4 + i] + T3[i];
+      const float v = (T6[0] + T6[2]) + (T6[1] + T6[3]);
+      best = dsh_umax64(best, dsh_argmax_key(v, r));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  if (c == 0) s_best[half] = best;
+  __syncthreads();
+  if (t == 0) {
+    unsigned long long b = s_best[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++) b = dsh_umax64(b, s_best[i]);
+    cand[blockIdx.x] = b;
+  }
+}
+
+extern "C" {
+
+int dsh_lm_q8_supported(int H, int vocab) { return H > 0 && H % 256 == 0 && H <= 2048 && vocab > 0; }
+
+size_t dsh_lm_q8_bytes(int H, int vocab) {
+  const size_t al = 256;
+  auto up = [&](size_t n) { return (n + al - 1) / al * al; };
+  const size_t nb = (size_t)dsh_dec_lm_blocks(vocab);
+  return up((size_t)vocab * H) + up((size_t)vocab * 12) + up((size_t)vocab * 8) + up(nb * 8);
+}
+
+void dsh_lm_q8_carve(void *base, int H, int vocab, dsh_lm_q8_t *Q) {
+  const size_t al = 256;
+  auto up = [&](size_t n) { return (n + al - 1) / al * al; };
+  char *p = (char *)base;
+  Q->H = H;
+  Q->vocab = vocab;
+  Q->q = (int8_t *)p;
+  p += up((size_t)vocab * H);
+  Q->sab = (float *)p;
+  p += up((size_t)vocab * 12);
+  Q->U = (double *)p;
+  p += up((size_t)vocab * 8);
+  Q->LBb = (double *)p;
+}
+
+hipError_t dsh_launch_lm_q8_build(const uint16_t *W, const dsh_lm_q8_t *Q, hipStream_t s) {
+  if (!W || !Q || !dsh_lm_q8_supported(Q->H, Q->vocab)) return hipErrorInvalidValue;
+  k_lm_q8_build<<<(Q->vocab + 3) / 4, 256, 0, s>>>(W, Q->H, Q->vocab, Q->q, Q->sab);
+  return hipGetLastError();
+}
+
+// Pass 1. ncopies: 0 (x is the input) or 8 (x holds 8 copies whose sum is the input; block 0
+// writes the sum to x_out, which pass 2 then reads).
+hipError_t dsh_launch_lm_q8_approx(const dsh_lm_q8_t *Q, const float *x, int ncopies, float *x_out, hipStream_t s) {
+  if (!Q || !x || !dsh_lm_q8_supported(Q->H, Q->vocab) || (ncopies != 0 && ncopies != 8) || (ncopies && !x_out) ||
+      ((uintptr_t)x & 15) || (x_out && ((uintptr_t)x_out & 15)))
+    return hipErrorInvalidValue;
+  const int nb = dsh_dec_lm_blocks(Q->vocab);
+#define LM_Q8_CASE(nm)                                                                                          \
+  case nm:                                                                                                      \
+    if (ncopies)                                                                                                \
+      k_lm_q8_approx<nm, 8><<<nb, 256, 0, s>>>(Q->q, Q->sab, x, Q->vocab, x_out, Q->U, Q->LBb);                  \
+    else                                                                                                        \
+      k_lm_q8_approx<nm, 0><<<nb, 256, 0, s>>>(Q->q, Q->sab, x, Q->vocab, nullptr, Q->U, Q->LBb);                \
+    break;
+  switch (Q->H / 256) {
+    LM_Q8_CASE(1)
+    LM_Q8_CASE(2)
+    LM_Q8_CASE(3)
+    LM_Q8_CASE(4)
+    LM_Q8_CASE(5)
+    LM_Q8_CASE(6)
+    LM_Q8_CASE(7)
+    LM_Q8_CASE(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef LM_Q8_CASE
+  return hipGetLastError();
+}
+
+// Pass 2 on the input x (the plain input, or pass 1's x_out).
+hipError_t dsh_launch_lm_q8_exact(const uint16_t *W, const dsh_lm_q8_t *Q, const float *x,
+                                  unsigned long long *cand, int *step_inc, hipStream_t s) {
+  if (!W || !Q || !x || !cand || !dsh_lm_q8_supported(Q->H, Q->vocab)) return hipErrorInvalidValue;
+  const int nb = dsh_dec_lm_blocks(Q->vocab);
+  k_lm_q8_exact<<<nb, 256, 0, s>>>(W, x, Q->H, Q->vocab, Q->U, Q->LBb, nb, cand, step_inc);
+  return hipGetLastError();
+}
+
+}  // extern "C"

@@ -752,6 +752,10 @@ struct ds_hip_stack {
   int vocab, H;
   int route_mode, bf16sim;
   int lm_fast;
+  /* the argmax in two passes over an int8 copy of the head (same tokens; lm_fast heads only) */
+  void *lmq_mem;
+  dsh_lm_q8_t lmq;
+  int lm_cert;
   void *work;              /* step counter, x buffer, candidates, partials */
   size_t work_bytes;
   int *step;
@@ -822,6 +826,39 @@ int ds_hip_lm_head_sample(const float *x_dev, const uint16_t *lm_head_dev, int h
   return 0;
 }
 
+/* The int8 copy of the head and its bounds (k_lm.hip), built from the head's current contents.
+ * Without device memory for it the stack keeps the one-pass head (the same tokens). */
+static int lm_cert_build(ds_hip_stack_t *S) {
+  if (!S->lmq_mem) {
+    if (hipMalloc(&S->lmq_mem, dsh_lm_q8_bytes(S->H, S->vocab)) != hipSuccess) {
+      (void)hipGetLastError();
+      S->lmq_mem = NULL;
+      S->lm_cert = 0;
+      return 0;
+    }
+    dsh_lm_q8_carve(S->lmq_mem, S->H, S->vocab, &S->lmq);
+  }
+  DSR_TRY(dsh_launch_lm_q8_build(S->lm, &S->lmq, dsr_stream), "LM head int8 copy");
+  S->lm_cert = 1;
+  return 0;
+}
+
+int ds_hip_stack_set_lm_certified(ds_hip_stack_t *S, int on) {
+  if (!S) return dsr_failf("ds_hip_stack_set_lm_certified: NULL stack");
+  if (S->bound) return dsr_failf("ds_hip_stack_set_lm_certified: call before ds_hip_stack_bind");
+  if (!on) {
+    S->lm_cert = 0;
+    return 0;
+  }
+  if (!S->lm_fast || !dsh_lm_q8_supported(S->H, S->vocab))
+    return dsr_failf("ds_hip_stack_set_lm_certified: head %d x %d not supported", S->vocab, S->H);
+  if (lm_cert_build(S)) return -1;
+  if (!S->lm_cert) return dsr_failf("ds_hip_stack_set_lm_certified: no device memory for the int8 copy");
+  return 0;
+}
+
+int ds_hip_stack_lm_certified(const ds_hip_stack_t *S) { return S && S->lm_fast && S->lm_cert ? 1 : 0; }
+
 ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers, const uint16_t *lm_head_dev,
                                     int vocab, int route_mode) {
   if (dsr_init()) return NULL;
@@ -849,6 +886,7 @@ ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers,
   S->bf16sim = ds_bf16_simulate_python;
   S->lm_fast = dsh_dec_lm_eligible(lm_head_dev, H, vocab, dsr_threads());
   S->ncand = S->lm_fast ? dsh_dec_lm_blocks(vocab) : dsh_argmax_avx_blocks(vocab);
+  if (S->lm_fast && dsh_lm_q8_supported(H, vocab)) lm_cert_build(S);
   const size_t np_bytes = al((size_t)layers[0]->np * 64 * 4);
   size_t off_x = 256, off_c = off_x + al((size_t)H * 4), off_p = off_c + al((size_t)S->ncand * 8);
   size_t off_e = off_p + 2 * np_bytes, bytes = off_e + al((size_t)H * 4);
@@ -877,6 +915,7 @@ void ds_hip_stack_destroy(ds_hip_stack_t *S) {
   if (S->exec) hipGraphExecDestroy(S->exec);
   if (S->graph) hipGraphDestroy(S->graph);
   hipFree(S->work);
+  if (S->lmq_mem) hipFree(S->lmq_mem);
   if (S->smp_work) hipFree(S->smp_work);
   if (S->att_work) hipFree(S->att_work);
   if (S->split_arena) hipFree(S->split_arena);
@@ -968,7 +1007,10 @@ size_t ds_hip_stack_bytes_per_step(const ds_hip_stack_t *S) {
   per_layer += E * H * (S->route_mode == DS_HIP_ROUTE_CFG ? 4 : 2); /* router */
   size_t dense = S->dense ? (size_t)3 * S->dense->H * S->dense->I * 2 : 0;
   for (int i = 0; i < S->n_attn; i++) dense += ds_hip_attn_weight_bytes(S->attn[i]); /* KV reads not counted */
-  return per_layer * (size_t)S->n_layers + dense + (size_t)S->vocab * S->H * 2;
+  /* the head: the bf16 rows, or (two passes) the int8 codes, 12 bytes of constants and 8 bytes of
+   * bound written and read back per row (the few candidate rows pass 2 reads are not counted) */
+  const size_t head = S->lm_fast && S->lm_cert ? (size_t)S->vocab * ((size_t)S->H + 28) : (size_t)S->vocab * S->H * 2;
+  return per_layer * (size_t)S->n_layers + dense + head;
 }
 
 /* Kernels launched per decode step (for profiling). */
@@ -1024,7 +1066,12 @@ static int stack_names(const ds_hip_stack_t *S, const char **names) {
       NM("down");
     }
   }
-  NM("lm_head.argmax");
+  if (S->lm_fast && S->lm_cert) {
+    NM("lm_head.approx");
+    NM("lm_head.exact");
+  } else {
+    NM("lm_head.argmax");
+  }
   NM(S->merged ? "lm_head.final+scores" : "lm_head.final");
   if (smp_active(S)) NM("sample");
 #undef NM
@@ -1327,7 +1374,16 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
   if (e != hipSuccess) return e;
   const int lm_copies = S->split && S->lm_fast && !S->attn;
   const int clear_in_final = S->split && (S->lm_fast || S->attn); /* else copy_sum cleared them */
-  if (lm_copies) {
+  if (S->lm_fast && S->lm_cert) {
+    /* pass 1 on the layer copies (its block 0 writes the plain output, the hidden state, which pass
+     * 2 reads) or on the head's input; then pass 2 */
+    e = dsh_launch_lm_q8_approx(&S->lmq, lm_copies ? xc_region(S, S->n_layers - 1) : lm_in(S),
+                                lm_copies ? dsh_layer_split_copies() : 0, lm_copies ? S->xbuf : NULL, dsr_stream);
+    if (e == hipSuccess) e = mark(ev, &n);
+    if (e == hipSuccess)
+      e = dsh_launch_lm_q8_exact(S->lm, &S->lmq, lm_copies ? S->xbuf : lm_in(S), S->cand,
+                                 lm_copies && S->merged ? S->step : NULL, dsr_stream);
+  } else if (lm_copies) {
     e = split_lm_enqueue(S);
   } else if (S->lm_fast) {
     e = dsh_launch_dec_lm_argmax(S->lm, lm_in(S), S->H, S->vocab, S->cand, dsr_stream);
@@ -1579,7 +1635,12 @@ int ds_hip_time_lm_head(ds_hip_stack_t *S, int n, float *ms) {
   int rc = 0;
   hipError_t e = hipEventRecord(a, dsr_stream);
   for (int i = 0; i < n && e == hipSuccess; i++) {
-    if (S->split && S->lm_fast && !S->attn) {  /* the head kernel of the step (on the layer copies) */
+    if (S->lm_fast && S->lm_cert) {
+      /* both passes on the step's head input (the layer copies are cleared after a step; the last
+       * hidden state is the same vector, so the candidates are those of the last step) */
+      e = dsh_launch_lm_q8_approx(&S->lmq, lm_in(S), 0, NULL, dsr_stream);
+      if (e == hipSuccess) e = dsh_launch_lm_q8_exact(S->lm, &S->lmq, lm_in(S), S->cand, NULL, dsr_stream);
+    } else if (S->split && S->lm_fast && !S->attn) {  /* the head kernel of the step (on the layer copies) */
       e = dsh_launch_dec_lm_argmax_copies(S->lm, xc_region(S, S->n_layers - 1), dsh_layer_split_copies(), S->H,
                                           S->vocab, S->cand, NULL, NULL, dsr_stream);
     } else if (S->lm_fast) {
