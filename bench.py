@@ -29,7 +29,7 @@ PEAK_HBM_GBS = 8000.0
 # kernel changes.
 LM_TRAFFIC_BYTES = 331387295
 LAYER_TRAFFIC_BYTES = 32002791  # k_dec_layer<5, 8, 2>, same runs
-LM_CERT_TRAFFIC_BYTES = None  # the two-pass head (k_lm_q8_approx + k_lm_q8_exact): not measured yet
+LM_CERT_TRAFFIC_BYTES = None  # the bounded head (k_lm_q8_argmax): not measured yet
 
 
 def product():
@@ -375,9 +375,9 @@ def main():
     ap.add_argument("--repeat-penalty", type=float, default=1.0,
                     help="> 1: the reference's repetition penalty after each argmax, over the run's tokens")
     ap.add_argument("--no-repeat-ngram", type=int, default=0, help="> 0: the reference's n-gram ban")
-    ap.add_argument("--lm-head", choices=["two-pass", "one-pass"], default="two-pass",
-                    help="LM-head argmax: int8 copy with exact bounds then the candidate rows in bf16 (the same "
-                         "tokens), or the one-pass bf16 kernel")
+    ap.add_argument("--lm-head", choices=["bounded", "one-pass"], default="bounded",
+                    help="LM-head argmax: an int8 copy with exact bounds, then each block's candidate rows in bf16 "
+                         "(the same tokens), or the one-pass bf16 kernel")
     ap.add_argument("--layer-kernels", type=int, choices=[1, 2], default=1,
                     help="MoE layer kernels: 1 (down split over intermediate units, per-XCD output copies) or 2 "
                          "(gate_up, then down with the combine in top-k order)")
@@ -491,9 +491,9 @@ def main():
     dev.check(L.ds_hip_stack_reset(S), "reset")
     span = np.zeros(n_span, np.float32)
     dev.check(L.ds_hip_time_stack_span(S, n_span, moe[0], moe[-1] + 1, span), "layer span timing")
-    # the head's bytes per step: the bf16 rows, or (two passes) the int8 codes, 12 bytes of
-    # constants and 8 bytes of bound written and read back per row
-    lm_bytes = VOCAB * (H + 28) if cert else VOCAB * H * 2
+    # the head's bytes per step: the bf16 rows, or (bounded) the int8 codes and 12 bytes of
+    # constants per row (the few candidate rows read again in bf16 are not counted)
+    lm_bytes = VOCAB * (H + 12) if cert else VOCAB * H * 2
     dense_bytes = 3 * H * DENSE_I * 2 if dense else 0
     attn_bytes = 0
     layer_bytes = (bytes_per_step - lm_bytes - dense_bytes - attn_bytes) // LAYERS
@@ -515,7 +515,7 @@ def main():
                                  f"{LAYERS}: real inputs and 11 distinct layers' weights; includes the kernel "
                                  "boundaries between the layers",
                 "why_this_kernel": "the MoE layers take the largest share of the step (11 launches), ahead of the "
-                                   f"LM head ({2 if cert else 1} launch{'es' if cert else ''})"}
+                                   "LM head (1 launch)"}
     # the LM-head kernel alone, 50 launches back to back on the last step's hidden state
     lm_t = C.c_float(0)
     dev.check(L.ds_hip_time_lm_head(S, 50, C.byref(lm_t)), "lm head timing")
@@ -525,16 +525,16 @@ def main():
     rd_t = C.c_float(0)
     dev.check(L.ds_hip_time_stream_read(lm.ptr, lm_bytes, 50, C.byref(rd_t)), "stream read timing")
     read_gbs = lm_bytes / (rd_t.value * 1e-3) / 1e9
-    lm_kernel = ("k_lm_q8_approx<5, 0> + k_lm_q8_exact (LM-head argmax in two passes, 2 launches per step: the "
-                 "int8 copy of the head with a bound on every row's exact logit, then the candidate rows in the "
-                 "reference's bf16 order; the bench step runs k_lm_q8_approx<5, 8> on the layer copies)" if cert else
+    lm_kernel = ("k_lm_q8_argmax<5, 0> (LM-head argmax, 1 launch per step: the int8 copy of the head with a bound "
+                 "on every row's exact logit, then each block's candidate rows in the reference's bf16 order; the "
+                 "step runs k_lm_q8_argmax<5, 8> on the layer copies)" if cert else
                  "k_dec_lm_argmax<1, 8> (LM-head argmax, 1 launch per step)")
     roofline_lm = {"kernel": lm_kernel, "bound": "hbm",
                    "achieved": round(lm_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                    "frac": round(lm_gbs / PEAK_HBM_GBS, 4), "traffic": LM_CERT_TRAFFIC_BYTES if cert else LM_TRAFFIC_BYTES,
                    "bytes_per_launch": lm_bytes, "reference_bytes_per_launch": VOCAB * H * 2, "avg_ms": round(lm_ms, 5),
-                   "avg_ms_method": f"50 back-to-back {'pairs of launches' if cert else 'launches'} between HIP events "
-                                    "on the library stream, on the last step's hidden state",
+                   "avg_ms_method": "50 back-to-back launches between HIP events on the library stream, on the "
+                                    "last step's hidden state",
                    "stream_read_gbs": round(read_gbs, 1), "frac_of_stream_read": round(lm_gbs / read_gbs, 4),
                    "stream_read_note": "a plain nontemporal streaming read of the same bytes, timed the same way: "
                                        "the achievable HBM read rate on this box"}
@@ -665,7 +665,8 @@ def main():
                  "after the argmax + " if sampling else "") +
                 "config 5: 11 DeepSeek3B-MoE INT8 layers (H1280, 64x[1792x1280 + 1280x896] routed top-6 + 2 shared, "
                 f"{'f32 router renormalised' if route == dev.ROUTE_CFG else 'bf16 router, fast-exp softmax over 64'}) "
-                f"+ argmax LM head 129280x1280 bf16{' (two passes)' if cert else ''}, batch 1; {args.steps} timed "
+                f"+ argmax LM head 129280x1280 bf16{' (int8 copy with exact bounds)' if cert else ''}, batch 1; "
+                f"{args.steps} timed "
                 f"decode steps after {args.warmup} "
                 "warm-up steps, each on a fresh seeded input")
     line = {
@@ -683,7 +684,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8 weights (u8 codes + f32 scale/offset), f32 accumulate; bf16 LM head" +
-                 (" (argmax in two passes: an int8 copy with exact bounds, then the candidate rows in bf16; the "
+                 (" (argmax over an int8 copy with exact bounds, then each block's candidate rows in bf16; the "
                   "same tokens)" if cert else ""),
         "data": "synthetic: seeded N(0,0.02) weights generated on device, seeded N(0,1) f32 hidden states",
         "config": {"workload": workload, "route": args.route, "moe_layer_kernels": layer_kernels,

@@ -205,29 +205,26 @@ hipError_t dsh_launch_dec_lm_argmax(const uint16_t *W, const float *x, int in_di
 hipError_t dsh_launch_dec_lm_argmax_copies(const uint16_t *W, const float *xc, int ncopies, int in_dim, int vocab,
                                            unsigned long long *cand, float *x_out, int *step_inc, hipStream_t s);
 
-/* ---- the LM-head argmax in two passes over an int8 copy of the head (k_lm.hip) ---- */
+/* ---- the LM-head argmax over an int8 copy of the head with bounds (k_lm.hip) ---- */
 typedef struct {
-  int8_t *q;    /* [vocab][H] codes rint(w / s) */
-  float *sab;   /* [vocab][3]: s, α (bound per ||x||_2), β (bound per half grid step), both rounded up */
-  double *U;    /* [vocab] per step: upper bound of each row's logit */
-  double *LBb;  /* [blocks] per step: largest lower bound per block of 256 rows */
+  int8_t *q;   /* [vocab][H] codes rint(w / s) */
+  float *sab;  /* [vocab][3]: s, α (bound per ||x||_2), β (bound per half grid step), both rounded up */
   int H, vocab;
 } dsh_lm_q8_t;
 /* H % 256 == 0, H <= 2048. */
 int dsh_lm_q8_supported(int H, int vocab);
-/* Device bytes of the copy and its per-step buffers; dsh_lm_q8_carve lays them out from base
- * (256-byte aligned). */
+/* Device bytes of the copy; dsh_lm_q8_carve lays it out from base (256-byte aligned). */
 size_t dsh_lm_q8_bytes(int H, int vocab);
 void dsh_lm_q8_carve(void *base, int H, int vocab, dsh_lm_q8_t *Q);
 /* Builds the codes and the per-row constants from the bf16 head W [vocab][H]. */
 hipError_t dsh_launch_lm_q8_build(const uint16_t *W, const dsh_lm_q8_t *Q, hipStream_t s);
-/* Pass 1: ncopies 0: x is the input; 8: x holds 8 copies, whose sum block 0 writes to x_out
- * (required), the input of pass 2. */
-hipError_t dsh_launch_lm_q8_approx(const dsh_lm_q8_t *Q, const float *x, int ncopies, float *x_out, hipStream_t s);
-/* Pass 2 on the input x: cand[dsh_dec_lm_blocks(vocab)] receives the same per-block keys as the
- * one-pass kernel; step_inc (optional) is advanced by one. */
-hipError_t dsh_launch_lm_q8_exact(const uint16_t *W, const dsh_lm_q8_t *Q, const float *x,
-                                  unsigned long long *cand, int *step_inc, hipStream_t s);
+/* Blocks of the kernel (512 rows each). */
+int dsh_lm_q8_blocks(int vocab);
+/* cand[dsh_lm_q8_blocks(vocab)] receives each block's (max, lowest index) key. ncopies 0:
+ * x is the input; 8: x holds 8 copies, whose sum block 0 writes to x_out (optional). step_inc
+ * (optional) is advanced by one. */
+hipError_t dsh_launch_lm_q8(const uint16_t *W, const dsh_lm_q8_t *Q, const float *x, int ncopies, float *x_out,
+                            unsigned long long *cand, int *step_inc, hipStream_t s);
 
 /* ---- one kernel per MoE layer, down split over intermediate units (k_layer.hip) ---- */
 typedef struct {

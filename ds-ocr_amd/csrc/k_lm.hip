@@ -1,5 +1,6 @@
-// k_lm.hip — the decode step's LM-head argmax in two passes, with the same result as the one-pass
-// kernel (k_dec_lm_argmax, the reference's 4-row-group AVX-512 order, ds_kernels_avx.c:162-245).
+// k_lm.hip — the decode step's LM-head argmax over an int8 copy of the head, with the same result
+// as the one-pass kernel (k_dec_lm_argmax, the reference's 4-row-group AVX-512 order,
+// ds_kernels_avx.c:162-245).
 //
 // The argmax needs every row's logit only to decide which row is largest. A per-row int8 copy of
 // the bf16 head (q = rint(w / s), s = max|w| / 127) gives an approximate logit A_r for half the
@@ -10,19 +11,18 @@
 //             + (s Σ q x~ - A_r)                  one rounding of A_r: <= 2^-22 |A_r| (generous)
 // with |x| < 2^e. Per row, α_r = γ_64 ||w||_2 + ||w - s q||_2 and β_r = s ||q||_1 are computed
 // once (f64, rounded up to f32); per step B_r = α_r ||x||_2 + β_r 2^(e-15) + 2^-22 |A_r|.
-// Pass 1 (k_lm_q8_approx) streams the int8 rows, computes A_r from exact integer dot products of
-// the codes with the input's two 8-bit limbs, and writes U_r = A_r + B_r per row and the largest
-// A_r - B_r per block. Pass 2 (k_lm_q8_exact) takes LB = the largest A_r - B_r over all blocks:
-// the row holding the largest exact logit L* has U_r >= L* >= LB, and so does every row tied with
-// it, while a row with U_r < LB has L_r < L*. Pass 2 recomputes the rows with U_r >= LB in the
-// exact order and writes, per block of 256 rows, the same (max, lowest index) key as the one-pass
-// kernel (0 for a block without candidates), so the final reduction is unchanged. NaN or infinite
-// bounds make a row a candidate (the test is !(U_r < LB)), so such inputs fall back to the exact
-// computation of every row they touch.
+// k_lm_q8_argmax streams the int8 rows of its block of 512, computes A_r from exact integer dot
+// products of the codes with the input's two 8-bit limbs, and takes LB = the largest A_r - B_r
+// over the block. The row holding the block's largest exact logit has A_r + B_r >= its logit >= LB,
+// and so does every row tied with it, while a row with A_r + B_r < LB has a logit below another
+// row's of the block. So the block recomputes only its rows with A_r + B_r >= LB in the exact order
+// and writes the block's (max, lowest index) key, the one-pass kernel's key for its rows; the
+// final reduction is unchanged. NaN or infinite bounds make a row a candidate (the test is
+// !(A_r + B_r < LB)), so such inputs fall back to the exact computation of every row they touch.
 #include "dsh.h"
 #include "k_core.h"
 
-#define LM_Q8_ROWS 256  // rows per block in both passes (the one-pass kernel's block)
+#define LM_Q8_ROWS 512  // rows per block: 8 waves, one block per CU
 
 namespace {
 
@@ -110,25 +110,64 @@ __global__ void __launch_bounds__(256) k_lm_q8_build(const uint16_t *__restrict_
   }
 }
 
-// Pass 1. Block = 256 rows (wave w: rows 64w .. 64w + 63 of the block, four per round: lanes
-// 16g .. 16g + 15 take row 4k + g of round k, lane s of them the 16-byte pieces 16s + 256m of the
-// row, m < NM = H / 256, so each load instruction reads 4 rows x 256 contiguous bytes). The input
-// (XC > 0: the sum of XC copies in copy order, as the one-pass kernel forms it; block 0 writes it to
-// x_out) is put on the grid 2^(e-14) (|x| < 2^e) as two 8-bit limbs held by each lane for its own
-// columns; the row's dot products are exact int32 sums. D rounds of loads stay in flight.
+// Block = 512 rows, one block per CU (wave w: rows 64w .. 64w + 63 of the block, four per round:
+// lanes 16g .. 16g + 15
+// take row 4k + g of round k, lane s of them the 16-byte pieces 16s + 256m of the row, m < NM =
+// H / 256, so each load instruction reads 4 rows x 256 contiguous bytes). The input (XC > 0: the
+// sum of XC copies in copy order, as the one-pass kernel forms it; block 0 writes it to x_out) is
+// put on the grid 2^(e-14) (|x| < 2^e) as two 8-bit limbs (converted once per block in LDS, then
+// held by each lane for its own columns); the row's dot products are exact int32 sums, kept in LDS
+// per row. D rounds of loads stay in flight. After the stream each thread turns one row's sums into
+// its bound and the block takes its largest lower bound. Then each
+// half-wave recomputes a candidate row (staged in LDS by 16-byte loads, all in flight at once):
+// lane c < 32 runs chain c (columns j = c mod 32 in
+// increasing order, fma(w_j, x_j, acc) from 0) and lane 0 of the half adds the chains as
+// _mm512_reduce_add_ps(a0 + a1) does (the one-pass kernel's tree). step_inc: advanced by block 0,
+// as the one-pass kernel does, for the final kernel after it.
 template <int NM, int XC>
-__global__ void __launch_bounds__(256) k_lm_q8_approx(const int8_t *__restrict__ q, const float *__restrict__ sab,
-                                                      const float *__restrict__ x, int vocab,
-                                                      float *__restrict__ x_out, double *__restrict__ U,
-                                                      double *__restrict__ LBb) {
+// (W, q, sab and x are deliberately not __restrict__: the memory clobbers then keep their loads in
+// issue order)
+__global__ void __launch_bounds__(512) k_lm_q8_argmax(const uint16_t *W, const int8_t *q, const float *sab,
+                                                      const float *x,
+                                                      int vocab, float *__restrict__ x_out,
+                                                      unsigned long long *__restrict__ cand, int *__restrict__ step_inc) {
+  if (step_inc && blockIdx.x == 0 && threadIdx.x == 0) *step_inc += 1;
   constexpr int H = 256 * NM, D = 4, NR = 16;  // rounds of 4 rows per wave
   __shared__ __attribute__((aligned(16))) float s_x[H];
-  __shared__ float s_sab[3 * LM_Q8_ROWS];
-  __shared__ float s_mx[4];
-  __shared__ double s_sq[4], s_lb[4];
+  __shared__ __attribute__((aligned(16))) int8_t s_xq[2][H];  // the input's low and high limbs
+  __shared__ int2 s_d[LM_Q8_ROWS];                             // per row: Σ q·lo, Σ q·hi
+  __shared__ float s_mx[8];
+  __shared__ double s_sq[8], s_lb[8];
+  __shared__ int s_n;
+  __shared__ int s_list[LM_Q8_ROWS];
+  __shared__ float s_acc[16][32];
+  __shared__ __attribute__((aligned(16))) uint16_t s_row[16][H];  // a candidate row per half-wave
+  __shared__ unsigned long long s_best[16];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, sub = lane & 15, grp = lane >> 4;
   const int rb = blockIdx.x * LM_Q8_ROWS;
   auto src = [&](int k) { return q + (size_t)min(rb + 64 * wave + 4 * k + grp, vocab - 1) * H + 16 * sub; };
+  // the input first (it gates the limbs; a wave's loads complete in issue order), then this
+  // thread's row's constants, then the first D rounds of rows
+  constexpr int NPC = H / 4;  // 4-float pieces of x (<= 512: one per thread)
+  f32x4 xa;
+  {
+    const int p = min(t, NPC - 1);
+    if constexpr (XC > 0) {
+      f32x4 c4[XC];
+#pragma unroll
+      for (int c = 0; c < XC; c++) c4[c] = ((const f32x4 *)(x + (size_t)c * H))[p];
+      f32x4 s4 = c4[0];
+#pragma unroll
+      for (int c = 1; c < XC; c++) s4 += c4[c];
+      xa = s4;
+    } else {
+      xa = ((const f32x4 *)x)[p];
+    }
+  }
+  float cs[3];
+#pragma unroll
+  for (int c = 0; c < 3; c++) cs[c] = sab[3 * (size_t)min(rb + t, vocab - 1) + c];
+  asm volatile("" ::: "memory");
   u32x4 ring[D][NM];
 #pragma unroll
   for (int k = 0; k < D; k++) {
@@ -137,74 +176,57 @@ __global__ void __launch_bounds__(256) k_lm_q8_approx(const int8_t *__restrict__
     for (int m = 0; m < NM; m++) ring[k][m] = dsh_load_nt(p + 256 * m);
     asm volatile("" ::: "memory");
   }
-  // the rows' constants and the input (issued after the first rounds of rows)
-  float cs[3];
-#pragma unroll
-  for (int c = 0; c < 3; c++) cs[c] = sab[3 * (size_t)min(rb + t, vocab - 1) + c];
-  constexpr int NPC = H / 4;  // 4-float pieces of x
-  f32x4 xa[2];
-#pragma unroll
-  for (int h = 0; h < 2; h++) {
-    const int p = min(t + 256 * h, NPC - 1);
-    if constexpr (XC > 0) {
-      f32x4 c4[XC];
-#pragma unroll
-      for (int c = 0; c < XC; c++) c4[c] = ((const f32x4 *)(x + (size_t)c * H))[p];
-      f32x4 s4 = c4[0];
-#pragma unroll
-      for (int c = 1; c < XC; c++) s4 += c4[c];
-      xa[h] = s4;
-    } else {
-      xa[h] = ((const f32x4 *)x)[p];
-    }
-  }
   float mx = 0.0f;
   double sq = 0.0;
+  {
+    const bool own = t < NPC;
+    if (own) {
+      *(f32x4 *)(s_x + 4 * t) = xa;
+      if (XC > 0 && x_out && blockIdx.x == 0) *(f32x4 *)(x_out + 4 * t) = xa;
+    }
+    // the statistics take the piece through selects, so its loads are not moved into a branch
+    // (where the wait for them would also wait for the rows issued after them)
 #pragma unroll
-  for (int h = 0; h < 2; h++) {
-    const int p = t + 256 * h;
-    if (p < NPC) {
-      *(f32x4 *)(s_x + 4 * p) = xa[h];
-      if (XC > 0 && x_out && blockIdx.x == 0) *(f32x4 *)(x_out + 4 * p) = xa[h];
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        mx = fmaxf(mx, fabsf(xa[h][c]));
-        sq += (double)xa[h][c] * (double)xa[h][c];
-      }
+    for (int c = 0; c < 4; c++) {
+      const float v = own ? xa[c] : 0.0f;
+      mx = fmaxf(mx, fabsf(v));
+      sq += (double)v * (double)v;
     }
   }
-#pragma unroll
-  for (int c = 0; c < 3; c++) s_sab[3 * t + c] = cs[c];
-  // a NaN input makes mx NaN-free but sq NaN, and the bounds below NaN: every row a candidate
+  // a NaN input leaves mx NaN-free but makes sq, and so every bound, NaN: every row a candidate
   mx = dsh_wave_max(mx);
   sq = lm_wave_sum_d(sq);
   if (lane == 0) {
     s_mx[wave] = mx;
     s_sq[wave] = sq;
   }
+  if (t == 0) s_n = 0;
   __syncthreads();
-  const float xmax = fmaxf(fmaxf(s_mx[0], s_mx[1]), fmaxf(s_mx[2], s_mx[3]));
-  const double x2 = sqrt(((s_sq[0] + s_sq[1]) + (s_sq[2] + s_sq[3])) * (1.0 + 1e-12));
+  float xmax = s_mx[0];
+  double sq_all = s_sq[0];
+#pragma unroll
+  for (int w = 1; w < 8; w++) {
+    xmax = fmaxf(xmax, s_mx[w]);
+    sq_all += s_sq[w];
+  }
+  const double x2 = sqrt(sq_all * (1.0 + 1e-12));
   const int e = __builtin_amdgcn_frexp_expf(xmax);  // xmax < 2^e
   const double grid = ldexp(1.0, e - 14), half_grid = ldexp(1.0, e - 15);
-  // this lane's columns 16 sub + 256 m + i as limbs: X = rint(x 2^(14-e)) (|X| <= 2^14) = 256 hi + lo
-  unsigned xlo[NM][4], xhi[NM][4];
+  // the limbs: X = rint(x 2^(14-e)) (|X| <= 2^14) = 256 hi + lo, lo in [-128, 127], hi in [-64, 64]
+  for (int j = t; j < H; j += LM_Q8_ROWS) {
+    const int X = (int)__builtin_rintf(__builtin_ldexpf(s_x[j], 14 - e));
+    const int l = __builtin_amdgcn_sbfe(X, 0, 8);
+    s_xq[0][j] = (int8_t)l;
+    s_xq[1][j] = (int8_t)((X - l) >> 8);
+  }
+  __syncthreads();
+  // this lane's columns 16 sub + 256 m .. + 15
+  u32x4 xlo[NM], xhi[NM];
 #pragma unroll
-  for (int m = 0; m < NM; m++)
-#pragma unroll
-    for (int w = 0; w < 4; w++) {
-      unsigned lo = 0, hi = 0;
-#pragma unroll
-      for (int b = 0; b < 4; b++) {
-        const int X = (int)__builtin_rintf(__builtin_ldexpf(s_x[16 * sub + 256 * m + 4 * w + b], 14 - e));
-        const int l = __builtin_amdgcn_sbfe(X, 0, 8);
-        lo |= ((unsigned)l & 255u) << (8 * b);
-        hi |= ((unsigned)((X - l) >> 8) & 255u) << (8 * b);
-      }
-      xlo[m][w] = lo;
-      xhi[m][w] = hi;
-    }
-  double lbmax = -__builtin_inf();
+  for (int m = 0; m < NM; m++) {
+    xlo[m] = *(const u32x4 *)&s_xq[0][16 * sub + 256 * m];
+    xhi[m] = *(const u32x4 *)&s_xq[1][16 * sub + 256 * m];
+  }
 #pragma unroll
   for (int k = 0; k < NR; k++) {
     const int sl = k % D;
@@ -224,64 +246,40 @@ __global__ void __launch_bounds__(256) k_lm_q8_approx(const int8_t *__restrict__
     }
     dlo = lm_row16_sum_i(dlo);
     dhi = lm_row16_sum_i(dhi);
-    const int rr = 64 * wave + 4 * k + grp, row = rb + rr;
-    if (sub == 0 && row < vocab) {
-      const double s = s_sab[3 * rr], a = s_sab[3 * rr + 1], b = s_sab[3 * rr + 2];
-      const double A = s * grid * (256.0 * (double)dhi + (double)dlo);
-      const double B = a * x2 + b * half_grid + 0x1p-22 * fabs(A);
-      U[row] = A + B;
-      lbmax = fmax(lbmax, A - B);
-    }
+    if (sub == 0) s_d[64 * wave + 4 * k + grp] = int2{dlo, dhi};
   }
-  lbmax = lm_wave_max_d(lbmax);
+  __syncthreads();
+  // row rb + t: A = s 2^(e-14) (256 Σ q·hi + Σ q·lo), its bound B, the upper bound U = A + B
+  const int2 dd = s_d[t];
+  const double A = (double)cs[0] * grid * (256.0 * (double)dd.y + (double)dd.x);
+  const double B = (double)cs[1] * x2 + (double)cs[2] * half_grid + 0x1p-22 * fabs(A);
+  const double u = A + B;
+  const double lbmax = lm_wave_max_d(rb + t < vocab ? A - B : -__builtin_inf());
   if (lane == 0) s_lb[wave] = lbmax;
   __syncthreads();
-  if (t == 0) LBb[blockIdx.x] = fmax(fmax(s_lb[0], s_lb[1]), fmax(s_lb[2], s_lb[3]));
-}
-
-// Pass 2. Block b = rows 256b .. 256b + 255, as the one-pass kernel's block. Candidates: rows with
-// !(U_r < LB). Each half-wave takes a candidate: lane c < 32 runs chain c (columns j = c mod 32 in
-// increasing order, fma(w_j, x_j, acc) from 0) and lane 0 of the half adds the chains as
-// _mm512_reduce_add_ps(a0 + a1) does (the one-pass kernel's tree). step_inc: advanced here, as the
-// one-pass kernel does, for the final kernel after it.
-__global__ void __launch_bounds__(256) k_lm_q8_exact(const uint16_t *__restrict__ W, const float *__restrict__ x,
-                                                     int H, int vocab, const double *__restrict__ U,
-                                                     const double *__restrict__ LBb, int nb,
-                                                     unsigned long long *__restrict__ cand, int *__restrict__ step_inc) {
-  if (step_inc && blockIdx.x == 0 && threadIdx.x == 0) *step_inc += 1;
-  __shared__ double s_lb[4];
-  __shared__ int s_n;
-  __shared__ int s_list[LM_Q8_ROWS];
-  __shared__ __attribute__((aligned(16))) float s_x[2048];
-  __shared__ float s_acc[8][32];
-  __shared__ unsigned long long s_best[8];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  double lb = -__builtin_inf();
-  for (int i = t; i < nb; i += 256) lb = fmax(lb, LBb[i]);
-  const int row = blockIdx.x * LM_Q8_ROWS + t;
-  const double u = row < vocab ? U[row] : 0.0;
-  lb = lm_wave_max_d(lb);
-  if (lane == 0) s_lb[wave] = lb;
-  if (t == 0) s_n = 0;
-  __syncthreads();
-  lb = fmax(fmax(s_lb[0], s_lb[1]), fmax(s_lb[2], s_lb[3]));
-  if (row < vocab && !(u < lb)) s_list[atomicAdd(&s_n, 1)] = row;
+  double lb = s_lb[0];
+#pragma unroll
+  for (int w = 1; w < 8; w++) lb = fmax(lb, s_lb[w]);
+  if (rb + t < vocab && !(u < lb)) s_list[atomicAdd(&s_n, 1)] = rb + t;
   __syncthreads();
   const int n = s_n;
-  if (n == 0) {
-    if (t == 0) cand[blockIdx.x] = 0ull;
-    return;
-  }
-  for (int i = t; i < H; i += 256) s_x[i] = x[i];
-  __syncthreads();
   const int half = t >> 5, c = t & 31;
   unsigned long long best = 0ull;
-  for (int k = half; k < n; k += 8) {
+  for (int k = half; k < n; k += 16) {
     const int r = s_list[k];
-    const uint16_t *wr = W + (size_t)r * H;
+    // the row into LDS: NM 16-byte pieces per lane of the half, all in flight at once
+    const u32x4 *wr = (const u32x4 *)(W + (size_t)r * H);
+    u32x4 pc[NM];
+#pragma unroll
+    for (int i = 0; i < NM; i++) pc[i] = wr[c + 32 * i];
+#pragma unroll
+    for (int i = 0; i < NM; i++) *(u32x4 *)&s_row[half][8 * (c + 32 * i)] = pc[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     float acc = 0.0f;
 #pragma unroll 8
-    for (int j = c; j < H; j += 32) acc = __builtin_fmaf(__uint_as_float((uint32_t)wr[j] << 16), s_x[j], acc);
+    for (int j = c; j < H; j += 32) acc = __builtin_fmaf(__uint_as_float((uint32_t)s_row[half][j] << 16), s_x[j], acc);
     s_acc[half][c] = acc;
     // the half's chains are read by its lane 0: LDS executes a wave's operations in order, the
     // fences keep the compiler from reordering
@@ -309,7 +307,7 @@ __global__ void __launch_bounds__(256) k_lm_q8_exact(const uint16_t *__restrict_
   if (t == 0) {
     unsigned long long b = s_best[0];
 #pragma unroll
-    for (int i = 1; i < 8; i++) b = dsh_umax64(b, s_best[i]);
+    for (int i = 1; i < 16; i++) b = dsh_umax64(b, s_best[i]);
     cand[blockIdx.x] = b;
   }
 }
@@ -318,11 +316,12 @@ extern "C" {
 
 int dsh_lm_q8_supported(int H, int vocab) { return H > 0 && H % 256 == 0 && H <= 2048 && vocab > 0; }
 
+int dsh_lm_q8_blocks(int vocab) { return (vocab + LM_Q8_ROWS - 1) / LM_Q8_ROWS; }
+
 size_t dsh_lm_q8_bytes(int H, int vocab) {
   const size_t al = 256;
   auto up = [&](size_t n) { return (n + al - 1) / al * al; };
-  const size_t nb = (size_t)dsh_dec_lm_blocks(vocab);
-  return up((size_t)vocab * H) + up((size_t)vocab * 12) + up((size_t)vocab * 8) + up(nb * 8);
+  return up((size_t)vocab * H) + up((size_t)vocab * 12);
 }
 
 void dsh_lm_q8_carve(void *base, int H, int vocab, dsh_lm_q8_t *Q) {
@@ -334,10 +333,6 @@ void dsh_lm_q8_carve(void *base, int H, int vocab, dsh_lm_q8_t *Q) {
   Q->q = (int8_t *)p;
   p += up((size_t)vocab * H);
   Q->sab = (float *)p;
-  p += up((size_t)vocab * 12);
-  Q->U = (double *)p;
-  p += up((size_t)vocab * 8);
-  Q->LBb = (double *)p;
 }
 
 hipError_t dsh_launch_lm_q8_build(const uint16_t *W, const dsh_lm_q8_t *Q, hipStream_t s) {
@@ -346,19 +341,20 @@ hipError_t dsh_launch_lm_q8_build(const uint16_t *W, const dsh_lm_q8_t *Q, hipSt
   return hipGetLastError();
 }
 
-// Pass 1. ncopies: 0 (x is the input) or 8 (x holds 8 copies whose sum is the input; block 0
-// writes the sum to x_out, which pass 2 then reads).
-hipError_t dsh_launch_lm_q8_approx(const dsh_lm_q8_t *Q, const float *x, int ncopies, float *x_out, hipStream_t s) {
-  if (!Q || !x || !dsh_lm_q8_supported(Q->H, Q->vocab) || (ncopies != 0 && ncopies != 8) || (ncopies && !x_out) ||
+// ncopies: 0 (x is the input) or 8 (x holds 8 copies whose sum is the input; block 0 writes the sum
+// to x_out when given).
+hipError_t dsh_launch_lm_q8(const uint16_t *W, const dsh_lm_q8_t *Q, const float *x, int ncopies, float *x_out,
+                            unsigned long long *cand, int *step_inc, hipStream_t s) {
+  if (!W || !Q || !x || !cand || !dsh_lm_q8_supported(Q->H, Q->vocab) || (ncopies != 0 && ncopies != 8) ||
       ((uintptr_t)x & 15) || (x_out && ((uintptr_t)x_out & 15)))
     return hipErrorInvalidValue;
-  const int nb = dsh_dec_lm_blocks(Q->vocab);
-#define LM_Q8_CASE(nm)                                                                                          \
-  case nm:                                                                                                      \
-    if (ncopies)                                                                                                \
-      k_lm_q8_approx<nm, 8><<<nb, 256, 0, s>>>(Q->q, Q->sab, x, Q->vocab, x_out, Q->U, Q->LBb);                  \
-    else                                                                                                        \
-      k_lm_q8_approx<nm, 0><<<nb, 256, 0, s>>>(Q->q, Q->sab, x, Q->vocab, nullptr, Q->U, Q->LBb);                \
+  const int nb = dsh_lm_q8_blocks(Q->vocab);
+#define LM_Q8_CASE(nm)                                                                                           \
+  case nm:                                                                                                       \
+    if (ncopies)                                                                                                 \
+      k_lm_q8_argmax<nm, 8><<<nb, 512, 0, s>>>(W, Q->q, Q->sab, x, Q->vocab, x_out, cand, step_inc);             \
+    else                                                                                                         \
+      k_lm_q8_argmax<nm, 0><<<nb, 512, 0, s>>>(W, Q->q, Q->sab, x, Q->vocab, nullptr, cand, step_inc);           \
     break;
   switch (Q->H / 256) {
     LM_Q8_CASE(1)
@@ -373,15 +369,6 @@ hipError_t dsh_launch_lm_q8_approx(const dsh_lm_q8_t *Q, const float *x, int nco
       return hipErrorInvalidValue;
   }
 #undef LM_Q8_CASE
-  return hipGetLastError();
-}
-
-// Pass 2 on the input x (the plain input, or pass 1's x_out).
-hipError_t dsh_launch_lm_q8_exact(const uint16_t *W, const dsh_lm_q8_t *Q, const float *x,
-                                  unsigned long long *cand, int *step_inc, hipStream_t s) {
-  if (!W || !Q || !x || !cand || !dsh_lm_q8_supported(Q->H, Q->vocab)) return hipErrorInvalidValue;
-  const int nb = dsh_dec_lm_blocks(Q->vocab);
-  k_lm_q8_exact<<<nb, 256, 0, s>>>(W, x, Q->H, Q->vocab, Q->U, Q->LBb, nb, cand, step_inc);
   return hipGetLastError();
 }
 

@@ -752,7 +752,7 @@ struct ds_hip_stack {
   int vocab, H;
   int route_mode, bf16sim;
   int lm_fast;
-  /* the argmax in two passes over an int8 copy of the head (same tokens; lm_fast heads only) */
+  /* the argmax over an int8 copy of the head with exact bounds (same tokens; lm_fast heads only) */
   void *lmq_mem;
   dsh_lm_q8_t lmq;
   int lm_cert;
@@ -826,7 +826,7 @@ int ds_hip_lm_head_sample(const float *x_dev, const uint16_t *lm_head_dev, int h
   return 0;
 }
 
-/* The int8 copy of the head and its bounds (k_lm.hip), built from the head's current contents.
+/* The int8 copy of the head and its bound constants (k_lm.hip), built from the head's contents.
  * Without device memory for it the stack keeps the one-pass head (the same tokens). */
 static int lm_cert_build(ds_hip_stack_t *S) {
   if (!S->lmq_mem) {
@@ -1007,9 +1007,9 @@ size_t ds_hip_stack_bytes_per_step(const ds_hip_stack_t *S) {
   per_layer += E * H * (S->route_mode == DS_HIP_ROUTE_CFG ? 4 : 2); /* router */
   size_t dense = S->dense ? (size_t)3 * S->dense->H * S->dense->I * 2 : 0;
   for (int i = 0; i < S->n_attn; i++) dense += ds_hip_attn_weight_bytes(S->attn[i]); /* KV reads not counted */
-  /* the head: the bf16 rows, or (two passes) the int8 codes, 12 bytes of constants and 8 bytes of
-   * bound written and read back per row (the few candidate rows pass 2 reads are not counted) */
-  const size_t head = S->lm_fast && S->lm_cert ? (size_t)S->vocab * ((size_t)S->H + 28) : (size_t)S->vocab * S->H * 2;
+  /* the head: the bf16 rows, or (bounded) the int8 codes and 12 bytes of constants per row (the few
+   * candidate rows read again in bf16 are not counted) */
+  const size_t head = S->lm_fast && S->lm_cert ? (size_t)S->vocab * ((size_t)S->H + 12) : (size_t)S->vocab * S->H * 2;
   return per_layer * (size_t)S->n_layers + dense + head;
 }
 
@@ -1066,12 +1066,7 @@ static int stack_names(const ds_hip_stack_t *S, const char **names) {
       NM("down");
     }
   }
-  if (S->lm_fast && S->lm_cert) {
-    NM("lm_head.approx");
-    NM("lm_head.exact");
-  } else {
-    NM("lm_head.argmax");
-  }
+  NM("lm_head.argmax");
   NM(S->merged ? "lm_head.final+scores" : "lm_head.final");
   if (smp_active(S)) NM("sample");
 #undef NM
@@ -1218,17 +1213,20 @@ static hipError_t split_lm_enqueue(ds_hip_stack_t *S) {
 /* The step's final kernel: the token into tokens[step], the step counter advanced, the last copies
  * regions cleared (one-kernel layers) and, with the embedding feed and no sampling rules after it,
  * the next step's input row. */
+/* Keys the step's head writes: one per block of the kernel in use. */
+static int lm_keys(const ds_hip_stack_t *S) { return S->lm_fast && S->lm_cert ? dsh_lm_q8_blocks(S->vocab) : S->ncand; }
+
 static hipError_t final_enqueue(ds_hip_stack_t *S, int clear) {
   const int NL = S->n_layers, embed = S->emb && !smp_active(S);
   float *zp = clear ? xc_region(S, NL >= 2 ? NL - 2 : 0) : NULL;
   const int zn = clear ? (int)S->xc_region * (NL >= 2 ? 2 : 1) : 0;
   if (S->merged) {
     const ds_hip_layer_t *L0 = S->layers[0];
-    return dsh_launch_lm_final_scores(S->cand, S->ncand, S->tokens, S->step, zp, zn, embed ? S->emb : NULL,
+    return dsh_launch_lm_final_scores(S->cand, lm_keys(S), S->tokens, S->step, zp, zn, embed ? S->emb : NULL,
                                       S->emb_vocab, embed ? S->ebuf : NULL, S->xs, S->stride, S->rows,
                                       L0->d.router_f32_t, S->H, L0->E, S->partials[0], dsr_stream);
   }
-  return dsh_launch_lm_argmax_final(S->cand, S->ncand, S->tokens, S->step, zp, zn, embed ? S->emb : NULL,
+  return dsh_launch_lm_argmax_final(S->cand, lm_keys(S), S->tokens, S->step, zp, zn, embed ? S->emb : NULL,
                                     S->emb_vocab, S->H, embed ? S->ebuf : NULL, dsr_stream);
 }
 
@@ -1375,14 +1373,10 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
   const int lm_copies = S->split && S->lm_fast && !S->attn;
   const int clear_in_final = S->split && (S->lm_fast || S->attn); /* else copy_sum cleared them */
   if (S->lm_fast && S->lm_cert) {
-    /* pass 1 on the layer copies (its block 0 writes the plain output, the hidden state, which pass
-     * 2 reads) or on the head's input; then pass 2 */
-    e = dsh_launch_lm_q8_approx(&S->lmq, lm_copies ? xc_region(S, S->n_layers - 1) : lm_in(S),
-                                lm_copies ? dsh_layer_split_copies() : 0, lm_copies ? S->xbuf : NULL, dsr_stream);
-    if (e == hipSuccess) e = mark(ev, &n);
-    if (e == hipSuccess)
-      e = dsh_launch_lm_q8_exact(S->lm, &S->lmq, lm_copies ? S->xbuf : lm_in(S), S->cand,
-                                 lm_copies && S->merged ? S->step : NULL, dsr_stream);
+    /* on the layer copies (block 0 writes the plain output, the hidden state) or on the head's input */
+    e = dsh_launch_lm_q8(S->lm, &S->lmq, lm_copies ? xc_region(S, S->n_layers - 1) : lm_in(S),
+                         lm_copies ? dsh_layer_split_copies() : 0, lm_copies ? S->xbuf : NULL, S->cand,
+                         lm_copies && S->merged ? S->step : NULL, dsr_stream);
   } else if (lm_copies) {
     e = split_lm_enqueue(S);
   } else if (S->lm_fast) {
@@ -1636,10 +1630,9 @@ int ds_hip_time_lm_head(ds_hip_stack_t *S, int n, float *ms) {
   hipError_t e = hipEventRecord(a, dsr_stream);
   for (int i = 0; i < n && e == hipSuccess; i++) {
     if (S->lm_fast && S->lm_cert) {
-      /* both passes on the step's head input (the layer copies are cleared after a step; the last
-       * hidden state is the same vector, so the candidates are those of the last step) */
-      e = dsh_launch_lm_q8_approx(&S->lmq, lm_in(S), 0, NULL, dsr_stream);
-      if (e == hipSuccess) e = dsh_launch_lm_q8_exact(S->lm, &S->lmq, lm_in(S), S->cand, NULL, dsr_stream);
+      /* on the step's head input (the layer copies are cleared after a step; the last hidden state
+       * is the same vector, so the candidates are those of the last step) */
+      e = dsh_launch_lm_q8(S->lm, &S->lmq, lm_in(S), 0, NULL, S->cand, NULL, dsr_stream);
     } else if (S->split && S->lm_fast && !S->attn) {  /* the head kernel of the step (on the layer copies) */
       e = dsh_launch_dec_lm_argmax_copies(S->lm, xc_region(S, S->n_layers - 1), dsh_layer_split_copies(), S->H,
                                           S->vocab, S->cand, NULL, NULL, dsr_stream);

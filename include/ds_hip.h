@@ -248,16 +248,17 @@ int ds_hip_stack_set_dense(ds_hip_stack_t *S, ds_hip_dense_t *D);
 int ds_hip_stack_set_layer_kernels(ds_hip_stack_t *S, int one_kernel);
 /* Kernels per MoE layer of the bound stack (1 or 2). */
 int ds_hip_stack_layer_kernels(const ds_hip_stack_t *S);
-/* LM-head argmax in two passes (no counterpart in the reference; the tokens are the reference's,
- * ds_argmax_matvec_bf16's, ds_kernels_avx.c:162-245). Pass 1 streams an int8 per-row copy of the
- * head (half the bytes) and bounds every row's exact logit; pass 2 recomputes, in the reference's
- * order, only the rows whose upper bound reaches the largest lower bound, which always include the
- * argmax and every row tied with it. On by default where the one-pass head applies and hidden is a
- * multiple of 256 (<= 2048); ds_hip_stack_create builds the copy (vocab x hidden bytes + 20 bytes
- * per row) from the head's contents then. on = 1 rebuilds it (call after rewriting the head's
- * weights), 0 returns to the one-pass head. Call before ds_hip_stack_bind. */
+/* LM-head argmax over an int8 copy of the head (no counterpart in the reference; the tokens are
+ * the reference's, ds_argmax_matvec_bf16's, ds_kernels_avx.c:162-245). Each block of 256 rows
+ * streams the int8 rows (half the bytes) with a rigorous bound on every row's exact logit, then
+ * recomputes in the reference's order only its rows whose upper bound reaches the block's largest
+ * lower bound, which always include the block's argmax and every row tied with it. On by default
+ * where the one-pass head applies and hidden is a multiple of 256 (<= 2048); ds_hip_stack_create
+ * builds the copy (vocab x hidden bytes + 12 bytes per row) from the head's contents then. on = 1
+ * rebuilds it (call after rewriting the head's weights), 0 returns to the one-pass head. Call
+ * before ds_hip_stack_bind. */
 int ds_hip_stack_set_lm_certified(ds_hip_stack_t *S, int on);
-/* 1 if the stack's steps use the two-pass head. */
+/* 1 if the stack's steps use the int8 copy of the head. */
 int ds_hip_stack_lm_certified(const ds_hip_stack_t *S);
 void ds_hip_stack_destroy(ds_hip_stack_t *S);
 /* Autoregressive input (ds_ocr.c:2271-2278, the decode loop's "embedding for next token"): with a

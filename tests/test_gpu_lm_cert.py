@@ -1,6 +1,6 @@
-"""The decode stack's two-pass LM head (ds_hip_stack_set_lm_certified: an int8 copy of the head with
-per-row bounds on the exact logit, then the reference's order on the rows whose bound reaches the
-best lower bound) against the one-pass head and the oracle's argmax of the same hidden state
+"""The decode stack's bounded LM head (ds_hip_stack_set_lm_certified: an int8 copy of the head with
+per-row bounds on the exact logit, then the reference's order on each block's rows whose bound
+reaches the block's best lower bound) against the one-pass head and the oracle's argmax of the same hidden state
 (or_argmax_bf16, the reference's ds_argmax_matvec_bf16): tokens bit for bit. Heads: random, and
 planted with exact ties (the lowest index wins), one-ulp near ties (the exact order decides), rows
 that all bound together (every row a candidate), a NaN in the best row (never chosen), an all-zero
@@ -46,8 +46,6 @@ def run_stack(dev, hs, lm_w, vocab, xs, cert, kernels, rewrite=None):
             lm.write(rewrite)
         dev.check(L.ds_hip_stack_set_lm_certified(S, cert), "certified")
         assert L.ds_hip_stack_lm_certified(S) == cert
-        names = [L.ds_hip_stack_kernel_name(S, i).decode() for i in range(L.ds_hip_stack_kernel_count(S))]
-        assert ("lm_head.exact" in names) == bool(cert) and ("lm_head.argmax" in names) != bool(cert)
         dev.check(L.ds_hip_stack_bind(S, xd.ptr, H, n, td.ptr, n), "bind")
         hid = []
         for _ in range(n):
@@ -69,14 +67,14 @@ def check(B, lm_w, vocab, H, toks, hid, label):
 
 @pytest.mark.parametrize("kernels", [1, 2])
 @pytest.mark.parametrize("H,vocab", [(256, 3000), (512, 20480), (1280, 8192)])
-def test_two_pass_head_random(dev, B, H, vocab, kernels):
+def test_bounded_head_random(dev, B, H, vocab, kernels):
     L = dev.load()
     lays, hs = layers(dev, B, 700 + H, H)
     try:
         lm_w = B.normal_bf16(vocab * H, 710 + H, 0.02)
         xs = np.stack([B.normal_f32(H, 7200 + s) for s in range(6)])
         t1, h1 = run_stack(dev, hs, lm_w, vocab, xs, 1, kernels)
-        check(B, lm_w, vocab, H, t1, h1, f"two-pass H {H} vocab {vocab} kernels {kernels}")
+        check(B, lm_w, vocab, H, t1, h1, f"bounded H {H} vocab {vocab} kernels {kernels}")
         t0, h0 = run_stack(dev, hs, lm_w, vocab, xs, 0, kernels)
         check(B, lm_w, vocab, H, t0, h0, f"one-pass H {H} vocab {vocab} kernels {kernels}")
         if kernels == 2:  # deterministic layers: the same hidden states, so the same tokens
@@ -113,7 +111,7 @@ def planted_head(B, kind, h0, vocab, H, seed):
 
 
 @pytest.mark.parametrize("kind", ["ties", "near", "flat", "nan", "zero"])
-def test_two_pass_head_planted(dev, B, kind):
+def test_bounded_head_planted(dev, B, kind):
     L = dev.load()
     H, vocab = 256, 6000
     lays, hs = layers(dev, B, 760, H)
@@ -138,7 +136,7 @@ def test_two_pass_head_planted(dev, B, kind):
             L.ds_hip_layer_destroy(h)
 
 
-def test_two_pass_head_rebuilt_after_rewrite(dev, B):
+def test_bounded_head_rebuilt_after_rewrite(dev, B):
     """The copy is built from the head's contents: rewriting the head and calling
     ds_hip_stack_set_lm_certified(S, 1) again gives the new head's tokens."""
     L = dev.load()
