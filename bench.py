@@ -692,7 +692,12 @@ def main():
         "hbm": {"bytes_per_step": int(bytes_per_step), "achieved_gbs": round(step_gbs, 1),
                 "frac_of_peak": round(step_gbs / PEAK_HBM_GBS, 4), "peak_gbs": PEAK_HBM_GBS,
                 "frac_of_peak_median": round(bytes_per_step / (pct(each, 50) * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                "wall_s_timed_region": round(wall, 4)},
+                "wall_s_timed_region": round(wall, 4),
+                "bytes_per_step_note": "bytes this implementation reads per step" +
+                                       (" (the LM head as its int8 copy)" if cert else ""),
+                "one_pass_head_bytes_per_step": int(bytes_per_step - lm_bytes + VOCAB * H * 2),
+                "one_pass_head_equivalent_frac_of_peak": round((bytes_per_step - lm_bytes + VOCAB * H * 2) /
+                                                               (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
         "roofline": roofline,
         "roofline_lm_head": roofline_lm,
         "determinism": {"rerun_tokens_equal": rerun_equal, "of": max(0, hi - lo),
