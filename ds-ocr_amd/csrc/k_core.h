@@ -233,6 +233,12 @@ typedef struct {
   const float *z, *sz;      /* next router x down offsets: [E][64], [64] */
   const float *WrT_next;    /* [H][E_next]; NULL: last layer */
   int E_next;
+  /* the next layer's shared-expert data, read into the L2 of the XCDs whose blocks read it by extra
+   * blocks of this layer's kernel (pf_gu NULL: none): gate/up codes and their (scale, offset), down
+   * tiles, next-router products (may be NULL); pf_SI: its width */
+  const int8_t *pf_gu, *pf_dnT;
+  const float *pf_guso, *pf_M;
+  int pf_SI;
 } dsh_split_t;
 int dsh_layer_split_supported(const dsh_layer_t *L);
 int dsh_layer_split_blocks(const dsh_layer_t *L);

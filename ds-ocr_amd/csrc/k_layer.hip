@@ -24,6 +24,7 @@
 
 #define DL_UB 32  // intermediate units per block
 #define DL_REP 8  // copies of each accumulated output
+#define DL_PF 32  // blocks that read the next layer's shared-expert data into L2
 
 // The XCD this wave runs on: s_getreg_b32 hwreg(HW_REG_XCC_ID, 0, 4) (register id 20, 4 bits at
 // offset 0). It only picks which copy the block adds into (every copy is summed), so any value is
@@ -319,6 +320,41 @@ __device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t 
   }
 }
 
+// The extra blocks: their share of the region to clear, then the next layer's shared-expert data
+// (F.pf_*) read with ordinary loads, so it is in L2 when that layer's kernel reads it. Blocks are
+// dealt to the 8 XCDs in turn, the same way in every launch of the same grid, so shared block sl
+// of the next kernel runs on the XCD of residue sl % 8: prefetch block p (XCD residue p % 8) reads
+// the data of the shared blocks sl = p % 8 + 8 (p / 8 + 4 i). A block that lands elsewhere only
+// makes the data come from HBM, as without it. Nothing is written (the loaded words feed a
+// condition that never holds, which keeps the loads).
+template <int CPL>
+__device__ __forceinline__ void dl_prefetch(const dsh_split_t &F, int nwork, float *x_out, float *zero_p, int zero_n) {
+  constexpr int H = 256 * CPL;
+  const int t = threadIdx.x, blk = blockIdx.x;
+  for (int i = blk * 512 + t; i < zero_n; i += gridDim.x * 512) zero_p[i] = 0.0f;
+  const int p = blk - nwork, ns = F.pf_SI / DL_UB;
+  unsigned acc = 0;
+  for (int sl = (p & 7) + 8 * (p >> 3); sl < ns; sl += 8 * (DL_PF / 8)) {
+    const u32x4 *g = (const u32x4 *)(F.pf_gu + (size_t)sl * DL_UB * H);
+    const u32x4 *u = (const u32x4 *)(F.pf_gu + (size_t)(F.pf_SI + sl * DL_UB) * H);
+    const u32x4 *d = (const u32x4 *)(F.pf_dnT + (size_t)sl * DL_UB * H);
+    u32x4 v[3 * CPL + 2];
+#pragma unroll
+    for (int k = 0; k < CPL; k++) {  // each region DL_UB x H bytes: CPL 16-byte pieces per thread
+      v[k] = g[t + 512 * k];
+      v[CPL + k] = u[t + 512 * k];
+      v[2 * CPL + k] = d[t + 512 * k];
+    }
+    v[3 * CPL] = F.pf_M ? ((const u32x4 *)(F.pf_M + (size_t)sl * DL_UB * 64))[t] : u32x4{0, 0, 0, 0};
+    v[3 * CPL + 1] = u32x4{0, 0, 0, 0};
+    if (t < 16) v[3 * CPL + 1] = ((const u32x4 *)(F.pf_guso + 2 * (size_t)sl * DL_UB))[t];
+    else if (t < 32) v[3 * CPL + 1] = ((const u32x4 *)(F.pf_guso + 2 * (size_t)(F.pf_SI + sl * DL_UB)))[t - 16];
+#pragma unroll
+    for (int k = 0; k < 3 * CPL + 2; k++) acc ^= v[k][0] ^ v[k][1] ^ v[k][2] ^ v[k][3];
+  }
+  if (acc == 0x9E3779B9u && F.pf_SI < 0) x_out[0] = 0.0f;
+}
+
 // x_out copies [DL_REP][H] and lg_out copies [DL_REP][64] must be zero when the kernel starts
 // (the kernel of the layer after next, or the final sum, clears them: zero_p/zero_n).
 // NREP: copies of the input (1: a plain vector at x_in + step*stride); RB: router partial rows
@@ -330,6 +366,11 @@ __global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F,
                                                    const float *__restrict__ resid, float *x_out, float *lg_out,
                                                    float *zero_p, int zero_n) {
   __shared__ dl_smem<CPL> S;
+  const int nwork = (L.SI + L.K * L.I) / DL_UB;
+  if ((int)blockIdx.x >= nwork) {
+    dl_prefetch<CPL>(F, nwork, x_out, zero_p, zero_n);
+    return;
+  }
   if ((int)blockIdx.x < L.SI / DL_UB)
     dl_body<CPL, NREP, RB, true>(L, F, x_in, step, stride, partials, np, mode, resid, x_out, lg_out, zero_p, zero_n,
                                  S);
@@ -446,8 +487,9 @@ hipError_t dsh_launch_dec_layer(const dsh_layer_t *L, const dsh_split_t *F, cons
                                 int stride, int ncopies, const float *partials, int np, int route_mode,
                                 const float *resid, float *x_out, float *lg_out, float *zero_p, int zero_n,
                                 hipStream_t s) {
-  const int nb = dsh_layer_split_blocks(L);
+  const int nb = dsh_layer_split_blocks(L) + (F->pf_gu ? DL_PF : 0);
   if (ncopies != 1 && ncopies != DL_REP) return hipErrorInvalidValue;
+  if (F->pf_gu && (!F->pf_dnT || !F->pf_guso || F->pf_SI <= 0 || F->pf_SI % DL_UB)) return hipErrorInvalidValue;
   if (np < 1 || (ncopies == 1 ? np > 160 : np > 8)) return hipErrorInvalidValue;
   if (route_mode != DSH_ROUTE_CFG && (route_mode != DSH_ROUTE_DECODE || np != 1 || F->M)) return hipErrorInvalidValue;
 #define DLK(N)                                                                                                   \

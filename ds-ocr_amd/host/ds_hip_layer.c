@@ -1308,6 +1308,16 @@ static int split_build(ds_hip_stack_t *S) {
     e = dsh_launch_layer_build(d, F->WrT_next, F->E_next, tiles, tiles + routed, M, (float *)F->sM, z, (float *)F->sz,
                                dsr_stream);
   }
+  /* each layer's kernel reads the next layer's shared-expert data into L2 */
+  for (int l = 0; l + 1 < NL; l++) {
+    const dsh_layer_t *nd = &S->layers[l + 1]->d;
+    if (nd->H != S->layers[l]->d.H) continue;
+    S->sp[l].pf_gu = nd->sgu_q;
+    S->sp[l].pf_guso = nd->sgu_so;
+    S->sp[l].pf_dnT = S->sp[l + 1].sdnT;
+    S->sp[l].pf_M = S->sp[l + 1].sM;
+    S->sp[l].pf_SI = nd->SI;
+  }
   S->xc = (float *)b;
   if (e == hipSuccess) e = hipMemsetAsync(S->xc, 0, (size_t)NL * S->xc_region * 4, dsr_stream);
   if (e == hipSuccess) e = hipStreamSynchronize(dsr_stream);
