@@ -226,7 +226,35 @@ static int argmax_excluding(const float *x, const uint16_t *W_bf16, int in_dim, 
   if (!Wd || !xd || !cand || !res || (n_exclude && (!lg || !lg2 || !exd)) || dsr_h2d(xd, x, F4(in_dim))) return -1;
   int T = dsr_threads();
   hipError_t e;
-  if (!n_exclude) {
+  if (!n_exclude && dsh_dec_lm_eligible(Wd, in_dim, out_dim, T) && dsh_lm_q8_supported(in_dim, out_dim) &&
+      dsh_lm_q8_blocks(out_dim) <= nb) {
+    /* every row in the reference's 4-row-group order: the argmax over the head's int8 copy with
+     * exact bounds (k_lm.hip; the same index), the copy built at the first call and kept with the
+     * registered weights */
+    dsh_lm_q8_t Q;
+    void *aux = dsr_weight_aux(W_bf16);
+    if (!aux) {
+      if (hipMalloc(&aux, dsh_lm_q8_bytes(in_dim, out_dim)) != hipSuccess) {
+        (void)hipGetLastError();
+        aux = NULL;
+      } else {
+        dsh_lm_q8_carve(aux, in_dim, out_dim, &Q);
+        if (dsh_launch_lm_q8_build(Wd, &Q, dsr_stream) != hipSuccess || dsr_weight_set_aux(W_bf16, aux)) {
+          hipFree(aux);
+          aux = NULL;
+        }
+      }
+    }
+    if (aux) {
+      dsh_lm_q8_carve(aux, in_dim, out_dim, &Q);
+      e = dsh_launch_lm_q8(Wd, &Q, xd, 0, NULL, cand, NULL, dsr_stream);
+      if (e == hipSuccess)
+        e = dsh_launch_lm_argmax_final(cand, dsh_lm_q8_blocks(out_dim), res, NULL, NULL, 0, NULL, 0, in_dim, NULL,
+                                       dsr_stream);
+    } else {
+      e = dsh_launch_argmax_avx(Wd, xd, cand, NULL, in_dim, out_dim, T, res, NULL, dsr_stream);
+    }
+  } else if (!n_exclude) {
     e = dsh_launch_argmax_avx(Wd, xd, cand, NULL, in_dim, out_dim, T, res, NULL, dsr_stream);
   } else {
     if (dsr_h2d(exd, exclude_ids, sizeof(int) * (size_t)n_exclude)) return -1;

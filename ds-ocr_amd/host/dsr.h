@@ -51,6 +51,11 @@ void dsr_block_forget(const void *qweight);
 const void *dsr_weight_device(const void *host, size_t bytes);
 /* The device copy of a registered weight array of at least `bytes`, or NULL (no upload). */
 const void *dsr_weight_lookup(const void *host, size_t bytes);
+/* A device allocation derived from registered weights (e.g. the LM head's int8 copy): NULL until
+ * set; dsr_weight_set_aux hands it to the registry, which frees it with the weights' entry (when
+ * the weights change or are replaced). */
+void *dsr_weight_aux(const void *host);
+int dsr_weight_set_aux(const void *host, void *aux_dev);
 
 /* Emulated reference CPU thread count (ds_set_threads). */
 int dsr_threads(void);

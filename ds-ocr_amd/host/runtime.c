@@ -132,6 +132,7 @@ typedef struct {
   uint64_t fp;
   size_t bytes;
   void *dev; /* weights: the copy; blocks: q (scale, offset follow in sdev/odev) */
+  void *aux; /* weights: device data derived from them (dsr_weight_set_aux), freed with the entry */
   float *sdev, *odev;
   int out_dim, in_dim;
   int is_block;
@@ -149,6 +150,7 @@ static entry_t *find(const void *key, int is_block) {
 static void drop(entry_t *e) {
   hipStreamSynchronize(dsr_stream);
   if (e->dev) hipFree(e->dev);
+  if (e->aux) hipFree(e->aux);
   *e = g_ent[--g_nent];
 }
 
@@ -282,6 +284,19 @@ int ds_hip_weights_changed(const void *host_ptr) {
     }
   }
   return dropped;
+}
+
+void *dsr_weight_aux(const void *host) {
+  entry_t *e = find(host, 0);
+  return e ? e->aux : NULL;
+}
+
+int dsr_weight_set_aux(const void *host, void *aux_dev) {
+  entry_t *e = find(host, 0);
+  if (!e) return -1;
+  if (e->aux && e->aux != aux_dev) hipFree(e->aux);
+  e->aux = aux_dev;
+  return 0;
 }
 
 const void *dsr_weight_lookup(const void *host, size_t bytes) {
