@@ -66,7 +66,7 @@ def check(B, lm_w, vocab, H, toks, hid, label):
 
 
 @pytest.mark.parametrize("kernels", [1, 2])
-@pytest.mark.parametrize("H,vocab", [(256, 3000), (512, 20480), (1280, 8192)])
+@pytest.mark.parametrize("H,vocab", [(256, 3000), (512, 20480), (768, 5000), (1280, 8192), (2048, 4096)])
 def test_bounded_head_random(dev, B, H, vocab, kernels):
     L = dev.load()
     lays, hs = layers(dev, B, 700 + H, H)
