@@ -233,8 +233,8 @@ typedef struct {
   const float *z, *sz;      /* next router x down offsets: [E][64], [64] */
   const float *WrT_next;    /* [H][E_next]; NULL: last layer */
   int E_next;
-  /* the next layer's shared-expert data, read into the L2 of the XCDs whose blocks read it by extra
-   * blocks of this layer's kernel (pf_gu NULL: none): gate/up codes and their (scale, offset), down
+  /* the next layer's shared-expert data, read ahead by extra blocks of this layer's kernel on the
+   * XCDs whose blocks read it next (pf_gu NULL: none): gate/up codes and their (scale, offset), down
    * tiles, next-router products (may be NULL); pf_SI: its width */
   const int8_t *pf_gu, *pf_dnT;
   const float *pf_guso, *pf_M;

@@ -24,7 +24,7 @@
 
 #define DL_UB 32  // intermediate units per block
 #define DL_REP 8  // copies of each accumulated output
-#define DL_PF 32  // blocks that read the next layer's shared-expert data into L2
+#define DL_PF 32  // blocks that read the next layer's shared-expert data ahead
 
 // The XCD this wave runs on: s_getreg_b32 hwreg(HW_REG_XCC_ID, 0, 4) (register id 20, 4 bits at
 // offset 0). It only picks which copy the block adds into (every copy is summed), so any value is
@@ -321,12 +321,13 @@ __device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t 
 }
 
 // The extra blocks: their share of the region to clear, then the next layer's shared-expert data
-// (F.pf_*) read with ordinary loads, so it is in L2 when that layer's kernel reads it. Blocks are
-// dealt to the 8 XCDs in turn, the same way in every launch of the same grid, so shared block sl
-// of the next kernel runs on the XCD of residue sl % 8: prefetch block p (XCD residue p % 8) reads
-// the data of the shared blocks sl = p % 8 + 8 (p / 8 + 4 i). A block that lands elsewhere only
-// makes the data come from HBM, as without it. Nothing is written (the loaded words feed a
-// condition that never holds, which keeps the loads).
+// (F.pf_*) read with ordinary loads while this layer's routed blocks are still selecting, so that
+// layer's kernel reads it back faster (measured: its shared blocks finish ~1 us earlier; the L2
+// does not keep the lines across the kernel boundary, the cache behind it does) and leaves more of
+// HBM to its routed rows. Blocks are dealt to the 8 XCDs in turn, the same way in every launch of
+// the same grid, so prefetch block p (XCD residue p % 8) reads the data of the shared blocks
+// sl = p % 8 + 8 (p / 8 + 4 i), which run on that XCD in the next kernel. Nothing is written (the
+// loaded words feed a condition that never holds, which keeps the loads).
 template <int CPL>
 __device__ __forceinline__ void dl_prefetch(const dsh_split_t &F, int nwork, float *x_out, float *zero_p, int zero_n) {
   constexpr int H = 256 * CPL;

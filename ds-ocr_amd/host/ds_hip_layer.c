@@ -1308,7 +1308,7 @@ static int split_build(ds_hip_stack_t *S) {
     e = dsh_launch_layer_build(d, F->WrT_next, F->E_next, tiles, tiles + routed, M, (float *)F->sM, z, (float *)F->sz,
                                dsr_stream);
   }
-  /* each layer's kernel reads the next layer's shared-expert data into L2 */
+  /* each layer's kernel reads the next layer's shared-expert data ahead */
   for (int l = 0; l + 1 < NL; l++) {
     const dsh_layer_t *nd = &S->layers[l + 1]->d;
     if (nd->H != S->layers[l]->d.H) continue;
