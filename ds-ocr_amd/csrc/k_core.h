@@ -239,8 +239,15 @@ typedef struct {
   const int8_t *pf_gu, *pf_dnT;
   const float *pf_guso, *pf_M;
   int pf_SI;
+  /* DECODE routing: the router's bf16 rows [E][H], from which the routed blocks compute the exact
+   * scores of their input themselves (partials unused); NULL: the scores come in as partials.
+   * Only where dsh_layer_dec_scores_fusable holds. */
+  const uint16_t *Wr_dec;
 } dsh_split_t;
 int dsh_layer_split_supported(const dsh_layer_t *L);
+/* Whether the layer kernel can compute DECODE scores itself: H <= 1280 and every router row in a
+ * 4- or 2-row group of the reference's chunks of nthreads (no single-row path). */
+int dsh_layer_dec_scores_fusable(int H, int E, int nthreads);
 int dsh_layer_split_blocks(const dsh_layer_t *L);
 int dsh_layer_split_copies(void);
 size_t dsh_layer_split_tile_bytes(const dsh_layer_t *L); /* routed + shared down tiles */

@@ -19,6 +19,7 @@
 //
 // The sums differ from the reference's order by f32 rounding (the combine adds the experts' shares
 // in an order set by the atomics, so the low bits of the output may differ from run to run).
+#include "dsh_avx.h"
 #include "dsh_route.h"
 #include "k_core.h"
 
@@ -87,8 +88,11 @@ struct dl_smem {
 };
 
 // The block's work; SH: a shared-expert block (a compile-time split, so each kind of block runs
-// straight-line code and every wait for a load counts only that kind's own loads).
-template <int CPL, int NREP, int RB, bool SH>
+// straight-line code and every wait for a load counts only that kind's own loads). DS: DECODE routing
+// with the router's rows (F.Wr_dec): a routed block computes the exact scores of its input itself,
+// in the reference's order for rows in 4- and 2-row groups (avx_row_regs32, as k_dec_scores_bf16),
+// instead of reading them as partials.
+template <int CPL, int NREP, int RB, bool SH, bool DS>
 __device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t &F, const float *x_in,
                                         const int *__restrict__ step, int stride, const float *partials, int np,
                                         int mode, const float *__restrict__ resid, float *x_out, float *lg_out,
@@ -108,7 +112,7 @@ __device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t 
   // Loads in the order they are needed (a wave's loads complete in issue order): the router
   // partials, then the input copies, the residual rows and the next router's rows.
   float pv[RB];
-  if (!shared_blk && wave < 4) {
+  if (!shared_blk && !DS && wave < 4) {
 #pragma unroll
     for (int j = 0; j < RB; j++) pv[j] = partials[(size_t)min(wave + 4 * j, np - 1) * 64 + lane];
   }
@@ -119,6 +123,18 @@ __device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t 
 #pragma unroll
     for (int c = 0; c < NREP; c++) xr[j][c] = ((const f32x4 *)(x + (size_t)c * H))[min(max(t - XO, 0) + XT * j, NP - 1)];
   asm volatile("" ::: "memory");
+  // DS: waves 0-3 of a routed block load router row 16 * wave + lane / 4 (4 lanes a row; lane
+  // L = lane % 4 holds columns 32i + 8L .. 32i + 8L + 7 in piece i), used once x is in LDS
+  constexpr int N32 = DS ? 8 * CPL : 1;
+  u32x4 wv[N32];
+  if constexpr (DS && !SH) {
+    if (wave < 4) {
+      const u32x4 *row = (const u32x4 *)(F.Wr_dec + (size_t)min(16 * wave + (lane >> 2), L.E - 1) * H);
+#pragma unroll
+      for (int i = 0; i < N32; i++) wv[i] = row[4 * i + (lane & 3)];
+    }
+    asm volatile("" ::: "memory");
+  }
   float rv[CPL];  // block 0: the residual rows it adds (when it is not the input)
   if (blk == 0 && resid && !half) {
 #pragma unroll
@@ -150,11 +166,15 @@ __device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t 
     asm volatile("" ::: "memory");
   }
   if (!shared_blk && wave < 4) {
-    float acc = 0.0f;
+    if constexpr (DS) {  // the scores go to row 0 (below); rows 1-3 add zeros, as a single partial's do
+      if (wave > 0) S.s_red[wave][lane] = 0.0f;
+    } else {
+      float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < RB; j++)
-      if (wave + 4 * j < np) acc += pv[j];
-    S.s_red[wave][lane] = lane < L.E ? acc : 0.0f;
+      for (int j = 0; j < RB; j++)
+        if (wave + 4 * j < np) acc += pv[j];
+      S.s_red[wave][lane] = lane < L.E ? acc : 0.0f;
+    }
   }
   // x: the copies summed in copy order; max|x| and Σx per wave
   f32x4 xs[XV];
@@ -189,6 +209,13 @@ __device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t 
     xsum += S.s_stat[8 + w];
   }
   const int ex = __builtin_amdgcn_frexp_expf(xmax);  // xmax < 2^ex
+  if constexpr (DS && !SH) {  // the scores of x (s_x), row e into s_red[0][e]; read after the next barrier
+    if (wave < 4) {
+      const float v = avx_row_regs32<N32>(wv, S.s_x, lane & 3, true, 0.0f);
+      const int e = 16 * wave + (lane >> 2);
+      if ((lane & 3) == 0) S.s_red[0][e] = e < L.E ? v : 0.0f;
+    }
+  }
 
   // x → limbs, piece p (elements 4p..4p+3) into word p of each limb array
 #pragma unroll
@@ -373,11 +400,32 @@ __global__ void __launch_bounds__(512) k_dec_layer(dsh_layer_t L, dsh_split_t F,
     return;
   }
   if ((int)blockIdx.x < L.SI / DL_UB)
-    dl_body<CPL, NREP, RB, true>(L, F, x_in, step, stride, partials, np, mode, resid, x_out, lg_out, zero_p, zero_n,
-                                 S);
+    dl_body<CPL, NREP, RB, true, false>(L, F, x_in, step, stride, partials, np, mode, resid, x_out, lg_out, zero_p,
+                                        zero_n, S);
   else
-    dl_body<CPL, NREP, RB, false>(L, F, x_in, step, stride, partials, np, mode, resid, x_out, lg_out, zero_p,
-                                  zero_n, S);
+    dl_body<CPL, NREP, RB, false, false>(L, F, x_in, step, stride, partials, np, mode, resid, x_out, lg_out, zero_p,
+                                         zero_n, S);
+}
+
+// DECODE routing with the scores computed in the routed blocks (F.Wr_dec; CPL <= 5, so a lane's
+// router pieces fit in registers next to the input copies).
+template <int CPL, int NREP>
+__global__ void __launch_bounds__(512) k_dec_layer_ds(dsh_layer_t L, dsh_split_t F, const float *x_in,
+                                                      const int *__restrict__ step, int stride,
+                                                      const float *__restrict__ resid, float *x_out, float *lg_out,
+                                                      float *zero_p, int zero_n) {
+  __shared__ dl_smem<CPL> S;
+  const int nwork = (L.SI + L.K * L.I) / DL_UB;
+  if ((int)blockIdx.x >= nwork) {
+    dl_prefetch<CPL>(F, nwork, x_out, zero_p, zero_n);
+    return;
+  }
+  if ((int)blockIdx.x < L.SI / DL_UB)
+    dl_body<CPL, NREP, 1, true, true>(L, F, x_in, step, stride, nullptr, 1, DSH_ROUTE_DECODE, resid, x_out, lg_out,
+                                      zero_p, zero_n, S);
+  else
+    dl_body<CPL, NREP, 1, false, true>(L, F, x_in, step, stride, nullptr, 1, DSH_ROUTE_DECODE, resid, x_out, lg_out,
+                                       zero_p, zero_n, S);
 }
 
 // out[i] = Σ_c X[c][i] in copy order, then X is cleared; zero_p[0..zero_n) is cleared too.
@@ -466,6 +514,14 @@ int dsh_layer_split_blocks(const dsh_layer_t *L) { return (L->SI + L->K * L->I) 
 
 int dsh_layer_split_copies(void) { return DL_REP; }
 
+int dsh_layer_dec_scores_fusable(int H, int E, int nthreads) {
+  if (H <= 0 || H > 1280 || H % 256 || E <= 0 || E > 64) return 0;
+  const int chunk = dsh_chunk_len(E, nthreads);
+  for (int s0 = 0; s0 < E; s0 += chunk)
+    if (min(chunk, E - s0) % 2) return 0;  // an odd chunk ends in a single row
+  return 1;
+}
+
 size_t dsh_layer_split_tile_bytes(const dsh_layer_t *L) { return (size_t)(L->E * L->I + L->SI) * L->H; }
 
 size_t dsh_layer_split_m_floats(const dsh_layer_t *L) { return (size_t)(L->E * L->I + L->SI) * 64; }
@@ -491,6 +547,24 @@ hipError_t dsh_launch_dec_layer(const dsh_layer_t *L, const dsh_split_t *F, cons
   const int nb = dsh_layer_split_blocks(L) + (F->pf_gu ? DL_PF : 0);
   if (ncopies != 1 && ncopies != DL_REP) return hipErrorInvalidValue;
   if (F->pf_gu && (!F->pf_dnT || !F->pf_guso || F->pf_SI <= 0 || F->pf_SI % DL_UB)) return hipErrorInvalidValue;
+  if (F->Wr_dec) {  // the scores from the router rows: partials and np are not read
+    if (route_mode != DSH_ROUTE_DECODE || F->M || L->H > 1280 || L->E > 64) return hipErrorInvalidValue;
+#define DLS(N)                                                                                                   \
+  case N:                                                                                                        \
+    if (ncopies == 1)                                                                                            \
+      k_dec_layer_ds<N, 1><<<nb, 512, 0, s>>>(*L, *F, x_in, step, stride, resid, x_out, lg_out, zero_p, zero_n); \
+    else                                                                                                         \
+      k_dec_layer_ds<N, DL_REP><<<nb, 512, 0, s>>>(*L, *F, x_in, step, stride, resid, x_out, lg_out, zero_p,     \
+                                                   zero_n);                                                      \
+    break;
+    switch (L->H / 256) {
+      DLS(1) DLS(2) DLS(3) DLS(4) DLS(5)
+      default:
+        return hipErrorInvalidValue;
+    }
+#undef DLS
+    return hipGetLastError();
+  }
   if (np < 1 || (ncopies == 1 ? np > 160 : np > 8)) return hipErrorInvalidValue;
   if (route_mode != DSH_ROUTE_CFG && (route_mode != DSH_ROUTE_DECODE || np != 1 || F->M)) return hipErrorInvalidValue;
 #define DLK(N)                                                                                                   \

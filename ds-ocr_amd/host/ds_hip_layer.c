@@ -288,6 +288,15 @@ static hipError_t scores_enqueue(const ds_hip_layer_t *L, const float *x_in, con
                                     dsr_stream);
 }
 
+/* DECODE routing in the one-kernel layers: the router rows from which layer L's kernel computes its
+ * own exact scores, or NULL where the scores kernel runs before it (an odd chunk of the reference's
+ * threads puts a router row on the single-row path, or H is past the kernel's register budget). */
+static const uint16_t *dec_fused_router(const ds_hip_layer_t *L, int route_mode, int split) {
+  return split && route_mode == DS_HIP_ROUTE_DECODE && dsh_layer_dec_scores_fusable(L->H, L->E, dsr_threads())
+             ? L->d.router_bf16
+             : NULL;
+}
+
 /* One layer: [scores], gate_up, down. In CFG mode with next != NULL, down also writes the partial
  * scores of layer "next" and the next layer's scores kernel is skipped by the caller. */
 static hipError_t layer_enqueue(const ds_hip_layer_t *L, const dsh_layer_work_t *wk, float *partials,
@@ -1034,7 +1043,7 @@ static int stack_names(const ds_hip_stack_t *S, const char **names) {
     }
     for (int l = 0; l < S->n_layers; l++) {
       NM("attention");
-      if (!cfg || S->bf16sim) NM("scores");
+      if ((!cfg || S->bf16sim) && !dec_fused_router(S->layers[l], S->route_mode, S->split)) NM("scores");
       if (S->split) {
         NM("layer");
       } else {
@@ -1049,7 +1058,7 @@ static int stack_names(const ds_hip_stack_t *S, const char **names) {
       NM("dense.down");
     }
     for (int l = 0; l < S->n_layers; l++) {
-      if (!cfg || (l == 0 && !S->dense && !S->merged)) NM("scores");
+      if (cfg ? l == 0 && !S->dense && !S->merged : !dec_fused_router(S->layers[l], S->route_mode, 1)) NM("scores");
       NM("layer");
     }
     if (!S->lm_fast) NM("copy_sum");
@@ -1117,7 +1126,9 @@ static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *ne
                             S->nbuf,
                             cfgp ? L->d.router_f32_t : NULL, cfgp ? L->E : 0, cfgp ? pin : NULL);
     if (e == hipSuccess) e = mark(ev, nev);
-    if (e == hipSuccess && !cfgp) {
+    const uint16_t *wr_dec = dec_fused_router(L, S->route_mode, S->split);
+    if (S->split) S->sp[l].Wr_dec = wr_dec;
+    if (e == hipSuccess && !cfgp && !wr_dec) {
       e = scores_enqueue(L, S->nbuf, NULL, 0, S->route_mode, S->bf16sim, pin, &np);
       if (e == hipSuccess) e = mark(ev, nev);
     }
@@ -1164,7 +1175,8 @@ static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *n
   const int cfg = S->route_mode == DS_HIP_ROUTE_CFG, mode = cfg ? DSH_ROUTE_CFG : DSH_ROUTE_DECODE;
   const int zn = (int)S->xc_region;
   int np0 = S->layers[0]->np;
-  if ((!dense || !cfg) && !S->merged) {
+  for (int l = 0; l < NL; l++) S->sp[l].Wr_dec = dec_fused_router(S->layers[l], S->route_mode, 1);
+  if ((cfg ? !dense : !S->sp[0].Wr_dec) && !S->merged) {
     e = scores_enqueue(S->layers[0], dense ? S->xbuf : S->in, dense ? NULL : S->in_step, dense ? 0 : S->in_stride,
                        S->route_mode, S->bf16sim, S->partials[0], &np0);
     if (e == hipSuccess) e = mark(ev, nev);
@@ -1181,7 +1193,7 @@ static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *n
       float *in = xc_region(S, l - 1);
       const float *pin = in + (size_t)C * H;  /* CFG: the score copies the previous layer accumulated */
       int np = C;
-      if (!cfg) { /* DECODE: the exact scores of the summed input */
+      if (!cfg && !S->sp[l].Wr_dec) { /* DECODE: the exact scores of the summed input */
         e = dsh_launch_dec_scores_bf16_copies(L->d.router_bf16, in, NULL, 0, C, H, L->E, dsr_threads(),
                                               S->partials[l & 1], dsr_stream);
         if (e == hipSuccess) e = mark(ev, nev);
