@@ -235,10 +235,10 @@ def test_config2_layer_bf16sim_bit_exact(dev, B):
         L.ds_hip_layer_destroy(h)
 
 
-def run_stack(dev, layers, lm, vocab, xs, mode, graph=True, kernels=None, expect=None):
+def run_stack(dev, layers, lm, vocab, xs, mode, graph=True, kernels=None, expect=None, names=None):
     """Runs xs through a stack step by step; kernels = 1 or 2 picks the MoE layer kernels (default:
     the library's choice); expect: the kernels per layer the bound stack must report (default: the
-    ones picked)."""
+    ones picked); names (a list): receives the step's kernel group names."""
     L = dev.load()
     arr = (C.c_void_p * len(layers))(*layers)
     S = L.ds_hip_stack_create(arr, len(layers), lm.ptr, vocab, mode)
@@ -252,6 +252,8 @@ def run_stack(dev, layers, lm, vocab, xs, mode, graph=True, kernels=None, expect
         dev.check(L.ds_hip_stack_bind(S, xd.ptr, xs.shape[1], n, td.ptr, n), "bind")
         if kernels is not None:
             assert L.ds_hip_stack_layer_kernels(S) == (expect or (1 if kernels == 1 else 2))
+        if names is not None:
+            names += [L.ds_hip_stack_kernel_name(S, i).decode() for i in range(L.ds_hip_stack_kernel_count(S))]
         hidden = []
         for _ in range(n):
             dev.check(L.ds_hip_stack_run(S, 1) if graph else L.ds_hip_stack_run_eager(S, 1), "run")
@@ -263,19 +265,17 @@ def run_stack(dev, layers, lm, vocab, xs, mode, graph=True, kernels=None, expect
         L.ds_hip_stack_destroy(S)
 
 
-def oracle_decode(B, lays, lm_w, vocab, xs, mode):
+def oracle_decode(B, lays, lm_w, vocab, xs, mode, threads=1):
     toks, hid = [], []
     orls = [lay.or_layer() for lay in lays]
     for x in xs:
         h = x.copy()
         for orl, lay in zip(orls, lays):
             o = np.empty(lay.hidden, np.float32)
-            B.oracle().or_moe_layer_decode(o, h, C.byref(orl), mode, 0, 1, None, None)
+            B.oracle().or_moe_layer_decode(o, h, C.byref(orl), mode, 0, threads, None, None)
             h = h + o
         hid.append(h)
-        lg = np.empty(vocab, np.float32)
-        B.oracle().or_argmax_logits_avx512(lg, h, lm_w, h.size, vocab, 1)
-        toks.append(B.oracle().or_argmax_bf16(h, lm_w, h.size, vocab, 1, None))
+        toks.append(B.oracle().or_argmax_bf16(h, lm_w, h.size, vocab, threads, None))
     return np.array(toks), np.stack(hid)
 
 
@@ -370,6 +370,40 @@ def test_one_kernel_layers_vs_oracle(dev, B, n_layers, mode):
             assert toks1[s] == B.oracle().or_argmax_bf16(hid1[s], lm_w, 256, vocab, 1, None)
             assert toks1e[s] == B.oracle().or_argmax_bf16(hid1e[s], lm_w, 256, vocab, 1, None)
     finally:
+        for h in hs:
+            L.ds_hip_layer_destroy(h)
+
+
+@pytest.mark.parametrize("threads,fused", [(1, True), (3, True), (16, True), (6, False), (7, False)])
+def test_one_kernel_decode_scores_in_layer(dev, B, threads, fused):
+    """DECODE routing in one-kernel layers: where every router row of the reference's thread chunks
+    sits in a 4- or 2-row group (18 experts: chunks 18, 6, 2), the routed blocks compute the exact
+    scores themselves and no scores kernel runs; an odd chunk (3 rows; 6 and 7 threads) puts rows on
+    the single-row path and keeps the scores kernel. Hidden states against the oracle run with the
+    same thread count (its selection is the reference's), tokens against its argmax."""
+    L = dev.load()
+    H = 512
+    lays = [B.make_moe_layer(180 + i, hidden=H, inter=256, n_experts=18, top_k=6, n_shared=2) for i in range(3)]
+    hs = [upload_layer(dev, lay) for lay in lays]
+    vocab = 3000
+    lm_w = B.normal_bf16(vocab * H, 181, 0.02)
+    lm = dev.DeviceBuffer.from_array(lm_w)
+    xs = np.stack([B.normal_f32(H, 1800 + s) for s in range(4)])
+    try:
+        L.ds_set_threads(threads)
+        names = []
+        toks, hid = run_stack(dev, hs, lm, vocab, xs, 0, kernels=1, names=names)
+        toks_e, hid_e = run_stack(dev, hs, lm, vocab, xs, 0, graph=False, kernels=1)
+        rt, rh = oracle_decode(B, lays, lm_w, vocab, xs, 0, threads)
+        assert names.count("layer") == 3 and names.count("scores") == (0 if fused else 3), names
+        for s in range(len(xs)):
+            err, erre = rel_err(hid[s], rh[s]), rel_err(hid_e[s], hid[s])
+            print(f"DECODE threads {threads} ({'in-layer' if fused else 'kernel'} scores) step {s}: err {err:.2e}, "
+                  f"eager vs graph {erre:.2e}; token {toks[s]} vs {rt[s]}")
+            assert err < TOL and erre < 1e-4
+            assert toks[s] == B.oracle().or_argmax_bf16(hid[s], lm_w, H, vocab, threads, None)
+    finally:
+        L.ds_set_threads(1)
         for h in hs:
             L.ds_hip_layer_destroy(h)
 
