@@ -458,6 +458,8 @@ def main():
     # warmup, then exactly --steps timed steps (graph launches) between synchronisations
     dev.check(L.ds_hip_stack_run(S, args.warmup), "warmup")
     dev.check(L.ds_hip_sync(), "sync")
+    rstat = (C.c_ulonglong * 3)()
+    dev.check(L.ds_hip_route_stats(rstat, 1), "route counters")
     ms = C.c_float(0)
     t0 = time.perf_counter()
     dev.check(L.ds_hip_time_stack(S, args.steps, C.byref(ms)), "timed steps")
@@ -465,6 +467,16 @@ def main():
     wall = time.perf_counter() - t0
     gpu_tokens = toks.to_array(np.int32)[args.warmup:args.warmup + args.steps].copy()
     ms_per_step = ms.value / args.steps
+    dev.check(L.ds_hip_route_stats(rstat, 1), "route counters")
+    n_route = int(rstat[0])
+    route_cert = {"routings": n_route, "recomputed": int(rstat[1]), "corrected": int(rstat[2]),
+                  "fallback_rate": round(rstat[1] / n_route, 5) if n_route else None,
+                  "correction_rate": round(rstat[2] / n_route, 5) if n_route else None,
+                  "note": "the timed steps' CFG expert selections, every one certified against ds_linear's order: "
+                          "recomputed = the intervals did not separate the ranks, so the open experts' scores were "
+                          "recomputed in that order; corrected = the one-kernel layer's speculative selection "
+                          "differed from the certified one and its output was corrected (ms_per_step includes all "
+                          "of it)"} if route == dev.ROUTE_CFG else None
 
     # the step-time distribution: n_each graph launches with an event between consecutive ones
     dev.check(L.ds_hip_stack_reset(S), "reset")
@@ -702,6 +714,7 @@ def main():
                                                                (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
         "roofline": roofline,
         "roofline_lm_head": roofline_lm,
+        "route_cert": route_cert,
         "determinism": {"rerun_tokens_equal": rerun_equal, "of": max(0, hi - lo),
                         "note": "tokens of the timed steps against a second graph run of the same inputs; the "
                                 f"{'one-kernel' if layer_kernels == 1 else 'two-kernel'} layers produced both"},

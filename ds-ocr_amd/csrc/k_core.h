@@ -77,6 +77,21 @@ typedef struct {
   int H, I, E, K, SI;
 } dsh_layer_t;
 
+/* Certified CFG routing (dsh_cert.h): counters and an optional log of the routings. stats[0] counts
+ * the routings made, stats[1] those whose selection needed ds_linear's order recomputed (the bound
+ * could not separate the ranks). The log (a test aid) holds log[0] = entries written, then from word
+ * 64 entries of DSH_RLOG_STRIDE(H) words: idx[8], w[8] (f32 bits), flags (bit 0: recomputed in
+ * ds_linear's order; bit 1: the one-kernel layer's verdict replaced the speculative selection),
+ * tag, 14 spare words, then the H floats of the routed input. One entry per routing, written by one
+ * thread per layer launch. */
+typedef struct {
+  unsigned long long *stats;
+  int *log;
+  int log_cap;
+  int tag;
+} dsh_rcert_t;
+#define DSH_RLOG_STRIDE(H) (32 + (H))
+
 /* Work buffers of one decode layer. */
 typedef struct {
   float *scores; /* [E] router scores */
@@ -94,11 +109,19 @@ size_t dsh_pf_workspace_bytes(const dsh_layer_t *L, int T);
  * current choice. */
 hipError_t dsh_pf_init(int force);
 int dsh_pf_fused(void);
+/* 1 if a probe grid's blocks were dealt evenly over all 8 XCDs (runs the probe once, outside stream
+ * capture): the fused prefill GEMM and the one-kernel layers' per-XCD verifiers rely on it. */
+int dsh_xcd_even(void);
 /* 1 if a fused launch's bounded wait expired (its output is then not valid), 0 if not; synchronous. */
 int dsh_pf_wait_error(const void *ws, const dsh_layer_t *L, int T);
-/* out[T][H] = (residual ? X : 0) + MoE(X); ws: dsh_pf_workspace_bytes(L, T) device bytes. */
+/* out[T][H] = (residual ? X : 0) + MoE(X); ws: dsh_pf_workspace_bytes(L, T) device bytes. derr (may be
+ * NULL): a device word the fused kernel sets (and never clears) when a down tile's bounded wait for its
+ * gate_up tiles gives up, after spin_max sleeps (DSH_PF_SPIN_MAX normally; < 0: every such wait gives up
+ * at once, a test mode). */
+#define DSH_PF_SPIN_MAX (1 << 22)
 hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int route_mode, int nthreads, int residual,
-                              int bf16sim, float *out, void *ws, int *idx_out, float *w_out, hipStream_t s);
+                              int bf16sim, float *out, void *ws, int *idx_out, float *w_out, int *derr, int spin_max,
+                              hipStream_t s);
 /* The prefill SwiGLU against the correctly rounded division over every 32-bit gate value: counts[0]
  * = finite g with a zero or normal quotient whose results differ, counts[1] = those with a
  * subnormal quotient (2 device words, cleared here). */
@@ -188,7 +211,7 @@ hipError_t dsh_launch_dec_scores_f32_exact(const float *WrT, const float *x_in, 
                                           int E, float *partials, hipStream_t s);
 hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const int *step, int stride,
                                   const float *partials, int np, int route_mode, int bf16sim,
-                                  const dsh_layer_work_t *wk, hipStream_t s);
+                                  const dsh_layer_work_t *wk, const dsh_rcert_t *rc, hipStream_t s);
 /* x_out = (residual ? (resid ? resid : x) : 0) + MoE(x) rows. */
 hipError_t dsh_launch_dec_down(const dsh_layer_t *L, const float *x_in, const int *step, int stride, float *x_out,
                                int residual, const float *resid, int bf16sim, const dsh_layer_work_t *wk,
@@ -243,12 +266,27 @@ typedef struct {
    * scores of their input themselves (partials unused); NULL: the scores come in as partials.
    * Only where dsh_layer_dec_scores_fusable holds. */
   const uint16_t *Wr_dec;
+  /* CFG routing, certified (dsh_cert.h): the verdict area of this layer, DSH_SPLIT_VD_INTS ints that
+   * are zero when the kernel starts (they sit in the layer's output region). The routed blocks
+   * select from the scores as given and add their shares at once; 32 extra blocks compute the
+   * layer's exact router scores from its input (1/32 of the rows each, with the running-error bound
+   * of ds_linear's order); the last to finish certifies the selection (or recomputes the open
+   * experts in ds_linear's order) and, where the certified experts differ from the ones used, all of
+   * them add the difference. NULL: no certification (the selection from the scores as
+   * given). */
+  unsigned *vd;
+  int *derr;       /* set (system scope) when an extra block's wait for the verdict gives up */
+  dsh_rcert_t rc;  /* counters and log (recorded on XCD 0) */
 } dsh_split_t;
+#define DSH_SPLIT_VD_INTS (64 + 256 * 32)
 int dsh_layer_split_supported(const dsh_layer_t *L);
 /* Whether the layer kernel can compute DECODE scores itself: H <= 1280 and every router row in a
  * 4- or 2-row group of the reference's chunks of nthreads (no single-row path). */
 int dsh_layer_dec_scores_fusable(int H, int E, int nthreads);
 int dsh_layer_split_blocks(const dsh_layer_t *L);
+/* Whether the one-kernel layer can certify its CFG selection (dsh_split_t.vd): E % 4 == 0, K <= 8,
+ * both f32 router layouts present. */
+int dsh_layer_cert_supported(const dsh_layer_t *L);
 int dsh_layer_split_copies(void);
 size_t dsh_layer_split_tile_bytes(const dsh_layer_t *L); /* routed + shared down tiles */
 size_t dsh_layer_split_m_floats(const dsh_layer_t *L);   /* routed + shared M tiles */

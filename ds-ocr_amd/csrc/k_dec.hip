@@ -14,6 +14,7 @@
 // Every load phase is branch-free with all of its loads issued before the first use, so each
 // kernel costs one memory round trip plus its transfer time.
 #include "dsh_avx.h"
+#include "dsh_cert.h"
 #include "dsh_route.h"
 #include "k_core.h"
 
@@ -36,27 +37,42 @@ __device__ __forceinline__ void load_f16x(const float *p, float *o) {
 
 // ============================================================================ routing in a block
 // Routing of one MoE layer from the NP partial score vectors, done by every block that needs it:
-// route_load issues the ROUTE_BATCH partial loads of each wave (rows wave, wave+4, ...; at most
-// 4 * ROUTE_BATCH partials, checked by dsh_dec_supported), route_reduce sums them in that order
-// and stores the wave sums, and
-// route_select (every wave, for itself) adds the four wave sums in wave order and selects the experts
-// (same semantics as k_core.hip's top-k helpers). Results in s_idx/s_w (LDS), visible after the
-// next barrier.
+// route_load issues the ROUTE_BATCH partial loads of each wave (wave v: the contiguous range
+// v*P .. v*P + P - 1, P = ceil(NP / 4) <= ROUTE_BATCH, checked by dsh_dec_supported), route_reduce
+// sums them in that order from 0 and stores the wave sums, with (s_lam) the sum of |running sum|
+// before each partial, the prefix sizes the certified CFG selection bounds its rounding with
+// (dsh_cert.h). route_select (every wave, for itself) adds the four wave sums in wave order and
+// selects the experts (same semantics as k_core.hip's top-k helpers); in CFG routing from row
+// partials, route_select_cert certifies the selection against ds_linear's order first. Results in
+// s_idx/s_w (LDS), visible after the next barrier.
 #define ROUTE_BATCH 40
 
+__device__ __forceinline__ int route_span(int np) { return (np + 3) >> 2; }
+
 __device__ __forceinline__ void route_load(const float *partials, int np, float *v) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, b0 = wave * route_span(np);
 #pragma unroll
-  for (int j = 0; j < ROUTE_BATCH; j++) v[j] = partials[(size_t)min(wave + 4 * j, np - 1) * 64 + lane];
+  for (int j = 0; j < ROUTE_BATCH; j++) v[j] = partials[(size_t)min(b0 + j, np - 1) * 64 + lane];
 }
 
-__device__ __forceinline__ void route_reduce(int np, int E, const float *v, float (*s_red)[64]) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  float acc = 0.0f;
+__device__ __forceinline__ void route_reduce(int np, int E, const float *v, float (*s_red)[64], float (*s_lam)[64]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, P = route_span(np), b0 = wave * P;
+  float acc = 0.0f, lam = 0.0f;
 #pragma unroll
   for (int j = 0; j < ROUTE_BATCH; j++)
-    if (wave + 4 * j < np) acc += v[j];
+    if (j < P && b0 + j < np) {
+      lam += fabsf(acc);
+      acc += v[j];
+    }
   s_red[wave][lane] = lane < E ? acc : 0.0f;
+  if (s_lam) s_lam[wave][lane] = lane < E ? lam : 0.0f;
+}
+
+// partials per wave row of route_reduce
+__device__ __forceinline__ void route_counts(int np, int nb[4]) {
+  const int P = route_span(np);
+#pragma unroll
+  for (int v = 0; v < 4; v++) nb[v] = max(0, min(P, np - v * P));
 }
 
 // ============================================================================ partial scores
@@ -219,8 +235,9 @@ __global__ void __launch_bounds__(64) k_dec_scores_bf16(const uint16_t *__restri
 // the load groups (x and partials are not __restrict__ so that they cannot be moved across them).
 template <int CPL>
 __device__ __forceinline__ void gate_up_body(const dsh_layer_t &L, const float *x, const float *partials, int np,
-                                             int mode, int bf16sim, const dsh_layer_work_t &wk, int blk, int *s_idx,
-                                             float *s_w, float (*s_red)[64], float *s_stat,
+                                             int mode, int bf16sim, const dsh_layer_work_t &wk, const dsh_rcert_t &rc,
+                                             int blk, int *s_idx, float *s_w, float (*s_red)[64],
+                                             float (*s_lam)[64], float (*s_tmp)[4][64], float *s_stat,
                                              unsigned *s_lq) {
   constexpr int XV = (64 * CPL + 255) / 256;  // 16-byte pieces of x per thread
   constexpr int NP = 64 * CPL;                // pieces (4 elements) of x, = words per limb array
@@ -229,6 +246,9 @@ __device__ __forceinline__ void gate_up_body(const dsh_layer_t &L, const float *
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane & 15, grp = lane >> 4;
   const int KI = K * I;
   const bool shared_wave = wave == 0;
+  // CFG from row partials (not the bf16 simulation's exact scores): the selection is certified
+  // against ds_linear's order (dsh_cert.h)
+  const bool cert = mode == DSH_ROUTE_CFG && !bf16sim && np > 1 && H % np == 0;
 
   f32x4 xr[XV];
 #pragma unroll
@@ -236,6 +256,7 @@ __device__ __forceinline__ void gate_up_body(const dsh_layer_t &L, const float *
   asm volatile("" ::: "memory");  // keeps the issue order: x, partials, shared rows
   float pv[ROUTE_BATCH];
   route_load(partials, np, pv);
+  const float wn = cert && !shared_wave ? L.router_norm[min(lane, L.E - 1)] : 0.0f;
   asm volatile("" ::: "memory");
   const int su = blk * 4 + grp;
   const int suc = su < SI ? su : 0;
@@ -250,8 +271,8 @@ __device__ __forceinline__ void gate_up_body(const dsh_layer_t &L, const float *
     }
   }
   asm volatile("" ::: "memory");
-  {  // max|x| and Σx of the pieces this thread owns (clamped duplicates skipped), per wave
-    float mx = 0.0f, sx = 0.0f;
+  {  // max|x|, Σx and Σx² of the pieces this thread owns (clamped duplicates skipped), per wave
+    float mx = 0.0f, sx = 0.0f, ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < XV; j++) {
       const bool own = (int)threadIdx.x + 256 * j < NP;
@@ -259,25 +280,38 @@ __device__ __forceinline__ void gate_up_body(const dsh_layer_t &L, const float *
       for (int c = 0; c < 4; c++) {
         mx = own ? fmaxf(mx, fabsf(xr[j][c])) : mx;
         sx += own ? xr[j][c] : 0.0f;
+        ss = own ? __builtin_fmaf(xr[j][c], xr[j][c], ss) : ss;
       }
     }
     mx = dsh_wave_max(mx);
     sx = dsh_wave_sum(sx);
+    if (cert) ss = dsh_wave_sum(ss);
     if (lane == 0) {
       s_stat[wave] = mx;
       s_stat[4 + wave] = sx;
+      s_stat[8 + wave] = ss;
     }
   }
-  route_reduce(np, L.E, pv, s_red);
-  __syncthreads();  // s_red, s_stat
+  route_reduce(np, L.E, pv, s_red, cert ? s_lam : nullptr);
+  __syncthreads();  // s_red, s_lam, s_stat
   const float xmax = fmaxf(fmaxf(s_stat[0], s_stat[1]), fmaxf(s_stat[2], s_stat[3]));
   const float xsum = ((s_stat[4] + s_stat[5]) + s_stat[6]) + s_stat[7];
   const int ex = __builtin_amdgcn_frexp_expf(xmax);  // xmax < 2^ex
 
   int ru = 0, r = 0, e = 0;
   float2 sog, sou;
+  bool recomputed = false;
   if (!shared_wave) {
-    route_select(L.E, K, mode, s_idx + 64 * wave, s_w + 64 * wave, s_red);
+    if (cert) {
+      // ||x|| from the f32 sum of squares: relative error below (H + 3) u, which 2^-10 covers
+      const float xn = __builtin_sqrtf(((s_stat[8] + s_stat[9]) + s_stat[10]) + s_stat[11]) * (1.0f + 0x1p-10f);
+      int nb[4];
+      route_counts(np, nb);
+      recomputed = route_select_cert(L.E, K, s_idx + 64 * wave, s_w + 64 * wave, s_red, s_lam, nb, H / np, H, wn, xn,
+                                     L.router_f32, x, s_tmp[wave]);
+    } else {
+      route_select(L.E, K, mode, s_idx + 64 * wave, s_w + 64 * wave, s_red);
+    }
     s_idx += 64 * wave;
     s_w += 64 * wave;
     ru = blk * 12 + (wave - 1) * 4 + grp;
@@ -364,19 +398,22 @@ __device__ __forceinline__ void gate_up_body(const dsh_layer_t &L, const float *
     wk.idx[lane] = s_idx[lane];
     wk.w[lane] = s_w[lane];
   }
+  if (cert && blk == 0 && wave == 1 && lane == 0) cert_record(rc, s_idx, s_w, K, recomputed ? 1 : 0, x, H);
 }
 
 template <int CPL>
 __global__ void __launch_bounds__(256) k_dec_gate_up(dsh_layer_t L, const float *x_in, const int *__restrict__ step,
                                                      int stride, const float *partials, int np, int mode, int bf16sim,
-                                                     dsh_layer_work_t wk) {
+                                                     dsh_layer_work_t wk, dsh_rcert_t rc) {
   __shared__ int s_idx[4 * 64];
   __shared__ float s_w[4 * 64];
   __shared__ float s_red[4][64];
-  __shared__ float s_stat[8];
+  __shared__ float s_lam[4][64];
+  __shared__ float s_tmp[4][4][64];
+  __shared__ float s_stat[12];
   __shared__ __attribute__((aligned(16))) unsigned s_lq[4 * 64 * CPL];
-  gate_up_body<CPL>(L, at_step(x_in, step, stride), partials, np, mode, bf16sim, wk, blockIdx.x, s_idx, s_w, s_red,
-                    s_stat, s_lq);
+  gate_up_body<CPL>(L, at_step(x_in, step, stride), partials, np, mode, bf16sim, wk, rc, blockIdx.x, s_idx, s_w,
+                    s_red, s_lam, s_tmp, s_stat, s_lq);
 }
 
 // ============================================================================ down + combine
@@ -538,7 +575,7 @@ __global__ void __launch_bounds__(320) k_sim_gate_up(dsh_layer_t L, const float 
   if (wave < 4) {
     float pv[ROUTE_BATCH];
     route_load(partials, np, pv);
-    route_reduce(np, L.E, pv, s_red);
+    route_reduce(np, L.E, pv, s_red, nullptr);
   }
   __syncthreads();  // s_x, s_red
   const int u = blockIdx.x * 128 + (t & 127), part = (t >> 7) & 1;
@@ -1000,7 +1037,11 @@ hipError_t dsh_launch_dec_scores_f32_exact(const float *WrT, const float *x_in, 
 
 hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const int *step, int stride,
                                   const float *partials, int np, int route_mode, int bf16sim,
-                                  const dsh_layer_work_t *wk, hipStream_t s) {
+                                  const dsh_layer_work_t *wk, const dsh_rcert_t *rc, hipStream_t s) {
+  const dsh_rcert_t rc0 = {nullptr, nullptr, 0, 0};
+  if (!rc) rc = &rc0;
+  if (route_mode == DSH_ROUTE_CFG && !bf16sim && np > 1 && (!L->router_norm || !L->router_f32))
+    return hipErrorInvalidValue;
   if (bf16sim) {  // every rounded value in the reference's order
     if (L->H > 2048 || L->H % 16) return hipErrorInvalidValue;
     k_sim_gate_up<<<(L->K * L->I + L->SI + 127) / 128, 320, 0, s>>>(*L, x_in, step, stride, partials, np, route_mode,
@@ -1010,7 +1051,7 @@ hipError_t dsh_launch_dec_gate_up(const dsh_layer_t *L, const float *x_in, const
   const int blocks = dec_gate_up_blocks(L);
 #define GU(N)                                                                                                  \
   case N:                                                                                                      \
-    k_dec_gate_up<N><<<blocks, 256, 0, s>>>(*L, x_in, step, stride, partials, np, route_mode, bf16sim, *wk);   \
+    k_dec_gate_up<N><<<blocks, 256, 0, s>>>(*L, x_in, step, stride, partials, np, route_mode, bf16sim, *wk, *rc); \
     break;
   switch (L->H / 256) {
     GU(1) GU(2) GU(3) GU(4) GU(5) GU(6) GU(7) GU(8)

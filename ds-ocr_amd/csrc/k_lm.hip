@@ -5,11 +5,15 @@
 // The argmax needs every row's logit only to decide which row is largest. A per-row int8 copy of
 // the bf16 head (q = rint(w / s), s = max|w| / 127) gives an approximate logit A_r for half the
 // bytes, and a rigorous bound |L_r - A_r| <= B_r on the logit L_r the exact order computes:
-//   L_r - A_r = (L_r - Σ w x)                    rounding of the exact order: <= γ_64 ||w||_2 ||x||_2
+//   L_r - A_r = (L_r - Σ w x)                    rounding of the exact order: <= γ_n ||w||_2 ||x||_2
 //             + Σ (w - s q) x                     quantization:  <= ||w - s q||_2 ||x||_2
 //             + s Σ q (x - x~)                    the input on a 2^(e-14) grid: <= s ||q||_1 2^(e-15)
 //             + (s Σ q x~ - A_r)                  one rounding of A_r: <= 2^-22 |A_r| (generous)
-// with |x| < 2^e. Per row, α_r = γ_64 ||w||_2 + ||w - s q||_2 and β_r = s ||q||_1 are computed
+// with |x| < 2^e and γ_n = n u / (1 - n u), u = 2^-24, n = H/32 + 5: in the exact order each
+// product is rounded by its own fused multiply-add and by every later one of its chain (H/32 per
+// chain, H % 32 == 0), then by a0 + a1 and by the 4 levels of the 16-lane reduction tree, so no
+// term passes through more than H/32 + 5 roundings and |L_r - Σ w x| <= γ_n Σ|w x| (Cauchy-Schwarz
+// for the last step). Per row, α_r = γ_n ||w||_2 + ||w - s q||_2 and β_r = s ||q||_1 are computed
 // once (f64, rounded up to f32); per step B_r = α_r ||x||_2 + β_r 2^(e-15) + 2^-22 |A_r|.
 // k_lm_q8_argmax streams the int8 rows of its block of 512, computes A_r from exact integer dot
 // products of the codes with the input's two 8-bit limbs, and takes LB = the largest A_r - B_r
@@ -65,7 +69,10 @@ __device__ __forceinline__ float lm_f32_up(double d) {
   return f;
 }
 
-constexpr double LM_GAMMA64 = 64.0 * 0x1p-24 / (1.0 - 64.0 * 0x1p-24);
+// γ_n for the exact order's roundings at hidden size H (n = H/32 + 5, the count derived above)
+__host__ __device__ constexpr double lm_gamma(int H) {
+  return (H / 32 + 5) * 0x1p-24 / (1.0 - (H / 32 + 5) * 0x1p-24);
+}
 
 }  // namespace
 
@@ -102,7 +109,7 @@ __global__ void __launch_bounds__(256) k_lm_q8_build(const uint16_t *__restrict_
   w2 = lm_wave_sum_d(w2);
   q1 = lm_wave_sum_d(q1);
   if (lane == 0) {
-    const double a = (LM_GAMMA64 * sqrt(w2) + sqrt(r2)) * (1.0 + 1e-12);
+    const double a = (lm_gamma(H) * sqrt(w2) + sqrt(r2)) * (1.0 + 1e-12);
     const double b = (double)s * q1 * (1.0 + 1e-12);
     sab[3 * (size_t)row] = s;
     sab[3 * (size_t)row + 1] = bad ? __builtin_inff() : lm_f32_up(a);

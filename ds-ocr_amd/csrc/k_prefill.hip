@@ -24,6 +24,7 @@
 //   k_pf_moe     both GEMMs in one launch (per-XCD work queues), in place of the two above
 //   k_pf_combine out[t] = (residual ? x : 0) + (Σ_k w_k·Y_k in ascending expert order + Y_shared)
 #include "dsh_avx.h"
+#include "dsh_cert.h"
 #include "dsh_route.h"
 #include "k_core.h"
 #include <type_traits>
@@ -49,6 +50,8 @@ struct pf_queues {
   int *next;     // [PF_NQ] claim counters (zeroed by the plan)
   int *gu_done;  // [items] finished gate_up tiles per item (zeroed by the plan)
   int *err;      // set when a bounded wait expires (zeroed by the plan)
+  int *derr;     // the library's device error word for this failure (host memory; never cleared here)
+  int spin_max;  // sleeps before a wait gives up; < 0: every wait gives up at once (test mode)
   int cap;
   int ngu_r, ngu_s, ndn;      // n-tiles: gate_up routed / shared, down
   int nk_gu, nk_dr, nk_ds;    // 128-column stages: gate_up, routed down, shared down
@@ -70,17 +73,20 @@ struct pf_item {
 
 // ---------------------------------------------------------------------------------- routing
 // Router scores in the decode path's order, kept as four partial sums per token and expert:
-// ps[t][v][e] = Σ_jb p[v + 4·jb] added sequentially from 0, where p[b] = Σ_j WrT[R·b+j][e]·x[R·b+j]
-// is a chain of fused multiply-adds over j (the decode path's partials and per-wave sums, wave v
-// taking partials v, v+4, ...); k_pf_select adds them as ((ps0 + ps1) + ps2) + ps3 (route_select).
-// CFG (f32 router): block = (PF_SC_TOK tokens, residue v); the residue's router rows and the tokens'
+// ps[t][v][e] = Σ_jb p[v·P + jb] added sequentially from 0 (P = ceil(NB / 4), NB = H / R partials),
+// where p[b] = Σ_j WrT[R·b+j][e]·x[R·b+j] is a chain of fused multiply-adds over j (the decode path's
+// partials and per-wave sums, wave v taking the contiguous partials v·P ..); k_pf_select adds them
+// as ((ps0 + ps1) + ps2) + ps3 (route_select). pl[t][v][e] = Σ_jb |running sum before p[v·P + jb]|,
+// the prefix sizes that bound the rounding against ds_linear's order (dsh_cert.h).
+// CFG (f32 router): block = (PF_SC_TOK tokens, quarter v); the quarter's router rows and the tokens'
 // matching x values are staged in LDS PF_SC_JB partials at a time; wave w runs tokens 4w..4w+3,
 // lane = expert.
 #define PF_SC_TOK 16
 #define PF_SC_JB 20
 template <int R>
 __global__ void __launch_bounds__(256) k_pf_scores_cfg(const float *__restrict__ WrT, const float *__restrict__ X,
-                                                       int T, int H, int E, float *__restrict__ ps) {
+                                                       int T, int H, int E, float *__restrict__ ps,
+                                                       float *__restrict__ pl) {
   __shared__ __attribute__((aligned(16))) float wv[PF_SC_JB][R][64];
   __shared__ __attribute__((aligned(16))) float xv[PF_SC_TOK][PF_SC_JB][R];
   constexpr int NW = PF_SC_JB * R * 64 / 256;            // router values per thread per pass
@@ -88,8 +94,9 @@ __global__ void __launch_bounds__(256) k_pf_scores_cfg(const float *__restrict__
   constexpr int NXT = (NX + 255) / 256;
   const int v = blockIdx.y, t0 = blockIdx.x * PF_SC_TOK;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nbv = (H / R - v + 3) / 4;
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int NB = H / R, P = (NB + 3) / 4, bq = v * P;
+  const int nbv = max(0, min(P, NB - bq));
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, lam[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int jb0 = 0; jb0 < nbv; jb0 += PF_SC_JB) {
     const int nj = min(PF_SC_JB, nbv - jb0);
     // every load of the pass in flight at once (partials past the last repeat it, unused)
@@ -100,7 +107,7 @@ __global__ void __launch_bounds__(256) k_pf_scores_cfg(const float *__restrict__
       const int i = threadIdx.x + 256 * k;
       const int row = i >> 6, e = i & 63;
       const int jj = row / R, j = row - jj * R;
-      const int b = v + 4 * min(jb0 + jj, nbv - 1);
+      const int b = bq + min(jb0 + jj, max(nbv - 1, 0));
       const float val = WrT[(size_t)(R * b + j) * E + min(e, E - 1)];  // branch-free load
       wr_[k] = e < E ? val : 0.0f;
     }
@@ -110,7 +117,7 @@ __global__ void __launch_bounds__(256) k_pf_scores_cfg(const float *__restrict__
       const int tb = i / (PF_SC_JB * (R / 4)), rem = i - tb * (PF_SC_JB * (R / 4));
       const int jj = rem / (R / 4), q = rem - jj * (R / 4);
       const int t = min(t0 + tb, T - 1);
-      const int b = v + 4 * min(jb0 + jj, nbv - 1);
+      const int b = bq + min(jb0 + jj, max(nbv - 1, 0));
       xr_[k] = *(const f32x4 *)(X + (size_t)t * H + R * b + 4 * q);
     }
     __syncthreads();  // the previous pass's reads are done
@@ -139,6 +146,7 @@ __global__ void __launch_bounds__(256) k_pf_scores_cfg(const float *__restrict__
 #pragma unroll
           for (int i = 0; i < 4; i++) p = __builtin_fmaf(wr[4 * q + i], xq[i], p);
         }
+        lam[tk] += fabsf(acc[tk]);
         acc[tk] += p;
       }
     }
@@ -146,7 +154,10 @@ __global__ void __launch_bounds__(256) k_pf_scores_cfg(const float *__restrict__
 #pragma unroll
   for (int tk = 0; tk < 4; tk++) {
     const int t = t0 + 4 * wave + tk;
-    if (t < T) ps[((size_t)t * 4 + v) * 64 + lane] = lane < E ? acc[tk] : 0.0f;
+    if (t < T) {
+      ps[((size_t)t * 4 + v) * 64 + lane] = lane < E ? acc[tk] : 0.0f;
+      pl[((size_t)t * 4 + v) * 64 + lane] = lane < E ? lam[tk] : 0.0f;
+    }
   }
 }
 
@@ -183,23 +194,25 @@ __global__ void __launch_bounds__(256) k_pf_scores_bf16(const uint16_t *__restri
 // wave holds the whole row in registers.
 //
 // CFG: the partial-sum scores differ from ds_linear's sequential ones (ds_kernels.c:639-652) only
-// by rounding. Any order of the H products is within γ_{H+1}·Σ|w_i x_i| <= γ_{H+1}·||w_e||·||x|| of
-// the exact dot product (γ_n = n·u / (1 - n·u), u = 2^-24), so the two differ by at most
-// ε_e = 2·γ_{H+1}·||w_e||·||x||. The selection stands as it is when the intervals [s_e - ε_e,
-// s_e + ε_e] of the selected experts, taken in rank order, and of the best unselected one are
-// disjoint: then ds_moe_top_k on the sequential scores (ds_kernels.c:193-243) picks the same
-// experts in the same order. Otherwise the experts whose interval reaches the lowest selected
-// lower bound (the only ones that can be among the top K) are written as the token's candidate
-// mask, and k_pf_exact recomputes their scores in ds_linear's order and selects again.
+// by rounding, bounded per expert by cert_radius_partials (dsh_cert.h: the running-error bound of
+// ds_linear's chain from the partials' prefix sizes pl, plus this order's own rounding; R rows per
+// partial, ||x|| from the f32 sum of squares, the router row norms rounded up). The selection stands
+// as it is when cert_check finds the intervals of the selected experts, in rank order, and of the
+// best unselected one disjoint: then ds_moe_top_k on the sequential scores (ds_kernels.c:193-243)
+// picks the same experts in the same order. Otherwise the experts whose interval reaches the lowest
+// selected lower bound (the only ones that can be among the top K) are written as the token's
+// candidate mask, and k_pf_exact recomputes their scores in ds_linear's order and selects again.
 #define PF_SEL_U 8  // x float4 loads per lane
 template <int MODE>
 __global__ void __launch_bounds__(256) k_pf_select(const float *__restrict__ X, int T, int H, int E, int K,
-                                                   const float *__restrict__ ps, const float *__restrict__ wnorm,
+                                                   const float *__restrict__ ps, const float *__restrict__ pl, int R,
+                                                   const float *__restrict__ wnorm,
                                                    int8_t *__restrict__ X0, int8_t *__restrict__ X1,
                                                    float *__restrict__ xsc, float *__restrict__ xsum,
                                                    int *__restrict__ idx, float *__restrict__ w,
                                                    unsigned long long *__restrict__ cmask) {
   __shared__ float s_red[4][4][64];
+  __shared__ float s_lam[4][4][64];
   __shared__ int s_idx[4][64];
   __shared__ float s_w[4][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -207,6 +220,10 @@ __global__ void __launch_bounds__(256) k_pf_select(const float *__restrict__ X, 
   if (t >= T) return;  // no block-wide barriers below
 #pragma unroll
   for (int r = 0; r < 4; r++) s_red[wave][r][lane] = ps[((size_t)t * 4 + r) * 64 + lane];
+  if constexpr (MODE == DSH_ROUTE_CFG) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) s_lam[wave][r][lane] = pl[((size_t)t * 4 + r) * 64 + lane];
+  }
   const f32x4 *src = (const f32x4 *)(X + (size_t)t * H);
   const int nc = H / 4;
   f32x4 xv[PF_SEL_U];
@@ -248,37 +265,36 @@ __global__ void __launch_bounds__(256) k_pf_select(const float *__restrict__ X, 
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if constexpr (MODE == DSH_ROUTE_CFG) {
+    route_state st;
+    route_init(E, K, MODE, s_red[wave], st);
+    route_rounds(st, 0, st.ns);
+    // ||x|| from the f32 sum of squares: relative error below (H + 6) u, which 2^-10 covers
+    const float xn = __builtin_sqrtf(dsh_wave_sum(ss)) * (1.0f + 0x1p-10f);
+    const float r[4] = {s_red[wave][0][lane], s_red[wave][1][lane], s_red[wave][2][lane], s_red[wave][3][lane]};
+    const float lam[4] = {s_lam[wave][0][lane], s_lam[wave][1][lane], s_lam[wave][2][lane], s_lam[wave][3][lane]};
+    const int NB = H / R, P = (NB + 3) / 4;
+    int nb[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) nb[v] = max(0, min(P, NB - v * P));
+    const float c = ((r[0] + r[1]) + r[2]) + r[3];
+    const float eps = lane < E ? cert_radius_partials(r, lam, nb, R, H, wnorm[lane], xn) : 0.0f;
+    unsigned long long m;
+    cert_check(st, c, eps, E, K, m);
+    int id;
+    float wt;
+    route_finish(MODE, st, id, wt);
+    if (lane < K) {
+      idx[(size_t)t * K + lane] = id;
+      w[(size_t)t * K + lane] = wt;
+    }
+    if (lane == 0) cmask[t] = m;
+    return;
+  }
   route_select(E, K, MODE, s_idx[wave], s_w[wave], s_red[wave]);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if constexpr (MODE == DSH_ROUTE_CFG) {
-    // ||x|| from the f32 sum of squares (relative error below γ_H / 2 + u; 1e-4 covers it), the
-    // rounding margin of every expert, and the check of the selection in rank order
-    const float xn = __builtin_sqrtf(dsh_wave_sum(ss)) * 1.0001f;
-    const float un = 5.9604645e-8f * (float)(H + 1);
-    const float gam = 2.0f * un / (1.0f - un) * 1.0001f;
-    const float sc = ((s_red[wave][0][lane] + s_red[wave][1][lane]) + s_red[wave][2][lane]) + s_red[wave][3][lane];
-    const bool selectable = lane < E && sc > -1e30f;
-    const float eps = lane < E ? __builtin_fmaf(gam * xn, wnorm[lane], 1e-30f) : 0.0f;
-    const int ns = min(__popcll(__ballot(selectable)), K);
-    const int er = lane < ns ? s_idx[wave][lane] : 0;
-    const float vr = __shfl(sc, er), epr = __shfl(eps, er);
-    const float lo = vr - epr, hi = vr + epr;
-    const float hi_next = __shfl_down(hi, 1);
-    bool in_sel = false;
-    for (int r = 0; r < ns; r++) in_sel |= s_idx[wave][r] == lane;
-    const float hi_out = dsh_wave_max(selectable && !in_sel ? sc + eps : -__builtin_huge_valf());
-    const float lo_last = __shfl(lo, max(ns - 1, 0));
-    const bool bad = (lane < ns - 1 && !(lo > hi_next)) || (lane == 0 && ns > 0 && !(lo_last > hi_out));
-    unsigned long long m = 0ull;
-    if (__ballot(bad)) {  // not certain: the experts that can be in the top K
-      float lmin = lane < ns ? lo : __builtin_huge_valf();
-      lmin = -dsh_wave_max(-lmin);
-      m = __ballot(selectable && sc + eps >= lmin);
-    }
-    if (lane == 0) cmask[t] = m;
-  }
   if (lane < K) {
     idx[(size_t)t * K + lane] = s_idx[wave][lane];
     w[(size_t)t * K + lane] = s_w[wave][lane];
@@ -1105,7 +1121,6 @@ __global__ void __launch_bounds__(256, PF_OCC) k_pf_down(dsh_layer_t L, const pf
 // were written by this XCD (each 128-byte line by one block) and never read here before (the
 // per-row partials, which share lines across items, are read with L2 atomics). Claim counters and
 // item counters are zeroed by the plan kernel.
-#define PF_SPIN_MAX (1 << 22)
 #define PF_PROBE 4096  // blocks of the XCD placement check
 __global__ void __launch_bounds__(256, PF_OCC) k_pf_moe(dsh_layer_t L, const pf_item *__restrict__ items,
                                                     pf_queues Q, const int8_t *X0, const int8_t *X1,
@@ -1138,12 +1153,14 @@ __global__ void __launch_bounds__(256, PF_OCC) k_pf_moe(dsh_layer_t L, const pf_
     if (threadIdx.x == 0) {
       const int need = it.seg == L.E ? L.SI / PF_GU_N : L.I / PF_GU_N;
       int spins = 0;
-      while (__hip_atomic_load(Q.gu_done + item, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
-        if (++spins > PF_SPIN_MAX) {
-          __hip_atomic_store(Q.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(2);
+      bool gave_up = Q.spin_max < 0;
+      while (!gave_up && __hip_atomic_load(Q.gu_done + item, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
+        if (++spins > Q.spin_max) gave_up = true;
+        else __builtin_amdgcn_s_sleep(2);
+      }
+      if (gave_up) {  // the tile computes on h as it is; the call's output is reported as not valid
+        __hip_atomic_store(Q.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (Q.derr) __hip_atomic_store(Q.derr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       }
     }
     __syncthreads();
@@ -1157,6 +1174,13 @@ __global__ void __launch_bounds__(256, PF_OCC) k_pf_moe(dsh_layer_t L, const pf_
 // XCC id of each block, to check that a grid's blocks cover all PF_NQ XCDs before the fused kernel
 // is used.
 __global__ void __launch_bounds__(64) k_pf_xcc_probe(int *__restrict__ out) {
+  unsigned xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  if (threadIdx.x == 0) out[blockIdx.x] = (int)xcc;
+}
+
+// The same for a 512-thread grid (the one-kernel decode layers' block size).
+__global__ void __launch_bounds__(512) k_pf_xcc_probe512(int *__restrict__ out) {
   unsigned xcc;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
   if (threadIdx.x == 0) out[blockIdx.x] = (int)xcc;
@@ -1261,6 +1285,7 @@ struct pf_ws {
   pf_hq hq;         // SwiGLU outputs h as int8 limbs: routed [TK][I], shared [T][SI]
   float *Y, *Ysh;
   float *ps;        // [T][4][64] partial router scores
+  float *pl;        // [T][4][64] their prefix sizes (CFG)
   float *hpr, *hps; // Σh partials per (row, gate_up n-tile): routed [TK][I/128], shared [T][SI/128]
   float *hmr, *hms; // max |h| per (row, gate_up n-tile), same layout
   unsigned long long *cmask;  // CFG: per token, the experts whose scores are recomputed (0: none)
@@ -1317,6 +1342,7 @@ size_t pf_carve(const dsh_layer_t *L, int T, void *base, pf_ws *w) {
   TAKE(Y, float, TK * H);
   TAKE(Ysh, float, T * H);
   TAKE(ps, float, (size_t)T * 4 * 64);
+  TAKE(pl, float, (size_t)T * 4 * 64);
   TAKE(hpr, float, TK * (I / PF_GU_N));
   TAKE(hps, float, (size_t)T * (SI / PF_GU_N));
   TAKE(hmr, float, TK * (I / PF_GU_N));
@@ -1387,6 +1413,34 @@ hipError_t dsh_pf_init(int force) {
 
 int dsh_pf_fused(void) { return g_pf_fused == 1; }
 
+// 1 when a 512-thread grid's blocks are dealt to the 8 XCDs in turn (blocks 8 r .. 8 r + 7 on 8
+// different XCDs), as the one-kernel layers' verifier parts assume (they check it again on every
+// launch); probed once (outside stream capture).
+static int g_xcd_rr = -1;
+
+int dsh_xcd_even(void) {
+  if (g_pf_auto < 0 && dsh_pf_init(-2) != hipSuccess) return 0;
+  if (g_xcd_rr < 0) {
+    const int n = 256;
+    int *d = NULL;
+    int h[256];
+    g_xcd_rr = 0;
+    if (hipMalloc(&d, sizeof(int) * n) == hipSuccess) {
+      k_pf_xcc_probe512<<<n, 512>>>(d);
+      if (hipGetLastError() == hipSuccess && hipMemcpy(h, d, sizeof(int) * n, hipMemcpyDeviceToHost) == hipSuccess) {
+        g_xcd_rr = 1;
+        for (int r = 0; r < n / PF_NQ; r++) {
+          unsigned m = 0;
+          for (int i = 0; i < PF_NQ; i++) m |= 1u << (h[PF_NQ * r + i] & 31);
+          g_xcd_rr &= m == (1u << PF_NQ) - 1u;
+        }
+      }
+      (void)hipFree(d);
+    }
+  }
+  return g_pf_auto == 1 && g_xcd_rr == 1;
+}
+
 int dsh_pf_wait_error(const void *ws, const dsh_layer_t *L, int T) {
   pf_ws w;
   pf_carve(L, T, (void *)ws, &w);
@@ -1396,7 +1450,8 @@ int dsh_pf_wait_error(const void *ws, const dsh_layer_t *L, int T) {
 }
 
 hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int route_mode, int nthreads, int residual,
-                              int bf16sim, float *out, void *ws, int *idx_out, float *w_out, hipStream_t s) {
+                              int bf16sim, float *out, void *ws, int *idx_out, float *w_out, int *derr, int spin_max,
+                              hipStream_t s) {
   if (T <= 0 || !dsh_pf_supported(L)) return hipErrorInvalidValue;
   if (route_mode == DSH_ROUTE_CFG ? !L->router_f32_t : !L->router_bf16) return hipErrorInvalidValue;
   pf_ws w;
@@ -1407,10 +1462,10 @@ hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int r
   if (route_mode == DSH_ROUTE_CFG) {
     const dim3 g((T + PF_SC_TOK - 1) / PF_SC_TOK, 4);
     if (R == 16)
-      k_pf_scores_cfg<16><<<g, 256, 0, s>>>(L->router_f32_t, X, T, H, E, w.ps);
+      k_pf_scores_cfg<16><<<g, 256, 0, s>>>(L->router_f32_t, X, T, H, E, w.ps, w.pl);
     else
-      k_pf_scores_cfg<8><<<g, 256, 0, s>>>(L->router_f32_t, X, T, H, E, w.ps);
-    k_pf_select<DSH_ROUTE_CFG><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, L->router_norm, w.X0, w.X1, w.xsc,
+      k_pf_scores_cfg<8><<<g, 256, 0, s>>>(L->router_f32_t, X, T, H, E, w.ps, w.pl);
+    k_pf_select<DSH_ROUTE_CFG><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, w.pl, R, L->router_norm, w.X0, w.X1, w.xsc,
                                                             w.xsum, w.idx, w.w, w.cmask);
     const int G = min(PF_EX_G, (16384 - H) / (H + 4));  // H <= 2048: G >= 6
     k_pf_exact<<<T, 256, sizeof(float) * ((size_t)H + (size_t)G * (H + 4)), s>>>(X, L->router_f32, H, E, K, G,
@@ -1418,12 +1473,13 @@ hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int r
   } else {
     k_pf_scores_bf16<<<(T + PF_TB - 1) / PF_TB, 256, (size_t)PF_TB * H * sizeof(float), s>>>(
         L->router_bf16, X, T, H, E, nthreads, w.ps);
-    k_pf_select<DSH_ROUTE_DECODE><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, nullptr, w.X0, w.X1, w.xsc,
+    k_pf_select<DSH_ROUTE_DECODE><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, nullptr, R, nullptr, w.X0, w.X1, w.xsc,
                                                                 w.xsum, w.idx, w.w, nullptr);
   }
   const int n_items_max = pf_max_routed_items(L, T) + pf_shared_items(T);
   const bool fused = g_pf_fused == 1 && n_items_max < (1 << 22);
-  pf_queues Q{w.qtiles, w.qcount, w.qnext, w.gu_done, w.err, (int)pf_queue_cap(L, T), L->I / PF_GU_N, L->SI / PF_GU_N,
+  pf_queues Q{w.qtiles, w.qcount, w.qnext, w.gu_done, w.err, derr, spin_max, (int)pf_queue_cap(L, T),
+              L->I / PF_GU_N, L->SI / PF_GU_N,
               H / PF_DN_N, H / PF_KS, L->I / PF_KS, L->SI / PF_KS, fused ? 1 : 0};
   k_pf_plan<<<1, 1024, 0, s>>>(w.idx, T, K, E, L->I / PF_GU_N, H / PF_DN_N, w.seg_off, w.items, w.counts,
                                w.tiles_gu, w.tiles_dn, w.pair_tok, w.pos_of, Q);

@@ -159,11 +159,12 @@ int ds_hip_attn_load_kv(ds_hip_attn_t *A, const float *k_host, const float *v_ho
   return 0;
 }
 
-/* The launch sequence, also used inside captured decode steps. */
+/* The launch sequence, also used inside captured decode steps; threads: the reference thread count
+ * whose split of the QKV rows the kernels follow. */
 hipError_t ds_hip_attn_enqueue(const ds_hip_attn_t *A, const float *x_in, const int *step, int stride,
                                int ncopies, float *x_plain, const int *pos_ptr, int pos_add, float *h_out,
-                               float *n_out, const float *WrT_next, int E_next, float *partials_next) {
-  return dsh_launch_attn(&A->d, x_in, step, stride, ncopies, x_plain, pos_ptr, pos_add, A->prefill_len, A->window, dsr_threads(),
+                               float *n_out, const float *WrT_next, int E_next, float *partials_next, int threads) {
+  return dsh_launch_attn(&A->d, x_in, step, stride, ncopies, x_plain, pos_ptr, pos_add, A->prefill_len, A->window, threads,
                          h_out, n_out, WrT_next, E_next, partials_next, dsr_stream);
 }
 
@@ -178,6 +179,7 @@ size_t ds_hip_attn_weight_bytes(const ds_hip_attn_t *A) {
 int ds_hip_attn_forward(ds_hip_attn_t *A, float *h_dev, float *n_dev, const float *x_dev, int pos) {
   if (!A || !h_dev || !n_dev || !x_dev || pos < 0 || pos >= A->d.max_seq)
     return dsr_failf("ds_hip_attn_forward: invalid arguments (pos %d, max_seq %d)", pos, A ? A->d.max_seq : 0);
-  DSR_TRY(ds_hip_attn_enqueue(A, x_dev, NULL, 0, 1, NULL, NULL, pos, h_dev, n_dev, NULL, 0, NULL), "attention kernels");
+  DSR_TRY(ds_hip_attn_enqueue(A, x_dev, NULL, 0, 1, NULL, NULL, pos, h_dev, n_dev, NULL, 0, NULL, dsr_threads()),
+          "attention kernels");
   return 0;
 }

@@ -30,7 +30,7 @@ struct ds_hip_layer {
   hipGraphExec_t pf_exec;
   struct pf_key {
     const void *out, *x, *ws, *idx, *w;
-    int T, mode, residual, bf16sim, threads, fused;
+    int T, mode, residual, bf16sim, threads, fused, spin_max;
   } pf_key;
 };
 
@@ -274,7 +274,7 @@ static hipError_t mark(hipEvent_t *ev, int *n) {
  * exact full scores as one partial; DECODE: exact full scores as one partial). Returns the number of
  * partial rows through *np. */
 static hipError_t scores_enqueue(const ds_hip_layer_t *L, const float *x_in, const int *step, int stride,
-                                 int route_mode, int bf16sim, float *partials, int *np) {
+                                 int route_mode, int bf16sim, int threads, float *partials, int *np) {
   if (route_mode == DS_HIP_ROUTE_CFG && bf16sim) { /* exact: ds_linear's own order */
     *np = 1;
     return dsh_launch_dec_scores_f32_exact(L->d.router_f32_t, x_in, step, stride, L->H, L->E, partials, dsr_stream);
@@ -284,15 +284,15 @@ static hipError_t scores_enqueue(const ds_hip_layer_t *L, const float *x_in, con
     return dsh_launch_dec_partial_scores(L->d.router_f32_t, x_in, step, stride, L->H, L->E, partials, dsr_stream);
   }
   *np = 1;
-  return dsh_launch_dec_scores_bf16(L->d.router_bf16, x_in, step, stride, L->H, L->E, dsr_threads(), partials,
+  return dsh_launch_dec_scores_bf16(L->d.router_bf16, x_in, step, stride, L->H, L->E, threads, partials,
                                     dsr_stream);
 }
 
 /* DECODE routing in the one-kernel layers: the router rows from which layer L's kernel computes its
  * own exact scores, or NULL where the scores kernel runs before it (an odd chunk of the reference's
  * threads puts a router row on the single-row path, or H is past the kernel's register budget). */
-static const uint16_t *dec_fused_router(const ds_hip_layer_t *L, int route_mode, int split) {
-  return split && route_mode == DS_HIP_ROUTE_DECODE && dsh_layer_dec_scores_fusable(L->H, L->E, dsr_threads())
+static const uint16_t *dec_fused_router(const ds_hip_layer_t *L, int route_mode, int split, int threads) {
+  return split && route_mode == DS_HIP_ROUTE_DECODE && dsh_layer_dec_scores_fusable(L->H, L->E, threads)
              ? L->d.router_bf16
              : NULL;
 }
@@ -304,12 +304,13 @@ static hipError_t layer_enqueue(const ds_hip_layer_t *L, const dsh_layer_work_t 
                                 int route_mode, int residual, int bf16sim, const ds_hip_layer_t *next,
                                 hipEvent_t *ev, int *nev) {
   hipError_t e = hipSuccess;
+  const dsh_rcert_t rc = dsr_rcert(0);
   if (!have_scores) {
-    e = scores_enqueue(L, x_in, step, stride, route_mode, bf16sim, partials, &np);
+    e = scores_enqueue(L, x_in, step, stride, route_mode, bf16sim, dsr_threads(), partials, &np);
     if (e == hipSuccess) e = mark(ev, nev);
   }
   if (e == hipSuccess)
-    e = dsh_launch_dec_gate_up(&L->d, x_in, step, stride, partials, np, route_mode, bf16sim, wk, dsr_stream);
+    e = dsh_launch_dec_gate_up(&L->d, x_in, step, stride, partials, np, route_mode, bf16sim, wk, &rc, dsr_stream);
   if (e == hipSuccess) e = mark(ev, nev);
   int chain = next && route_mode == DS_HIP_ROUTE_CFG && !bf16sim;
   if (e == hipSuccess)
@@ -335,6 +336,14 @@ int ds_hip_layer_forward(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
   return 0;
 }
 
+/* Sleeps before a fused prefill tile's wait for its gate_up tiles gives up (ds_hip_prefill_set_wait_limit). */
+static int g_pf_spin_max = DSH_PF_SPIN_MAX;
+
+int ds_hip_prefill_set_wait_limit(int spins) {
+  g_pf_spin_max = spins == DS_HIP_PREFILL_WAIT_DEFAULT ? DSH_PF_SPIN_MAX : spins;
+  return 0;
+}
+
 /* Prefill MoE block (ds_moe_decoder.c:629-809) for T tokens already on the device. The workspace
  * (activations split to bf16, routing, the expert-sorted pair list, h and per-pair outputs; about
  * 65 KB per token at DeepSeek-OCR's shape) is a library staging buffer that grows to the largest T. */
@@ -342,6 +351,8 @@ int ds_hip_layer_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
                          int *idx_dev, float *w_dev) {
   if (!L || !out_dev || !x_dev || T <= 0) return dsr_failf("ds_hip_layer_prefill: invalid arguments");
   if (check_router(L, route_mode)) return -1;
+  /* a bounded wait that gave up in an earlier call (already finished) voids that call's output */
+  if (dsr_derr_check()) return -1;
   if (!dsh_pf_supported(&L->d))
     return dsr_failf("ds_hip_layer_prefill: shape H=%d I=%d SI=%d not supported (needs H %% 256 == 0, I and SI %% 128 == 0)",
                      L->H, L->I, L->SI);
@@ -361,6 +372,7 @@ int ds_hip_layer_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
   key.bf16sim = ds_bf16_simulate_python;
   key.threads = dsr_threads();
   key.fused = dsh_pf_fused();
+  key.spin_max = g_pf_spin_max;
   if (!L->pf_exec || memcmp(&key, &L->pf_key, sizeof key) != 0) {
     /* the seven kernels (and the idx/w copies) captured once, then one graph launch per call */
     if (L->pf_exec) {
@@ -369,7 +381,7 @@ int ds_hip_layer_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
     }
     DSR_TRY(hipStreamBeginCapture(dsr_stream, hipStreamCaptureModeThreadLocal), "prefill capture begin");
     hipError_t e = dsh_launch_prefill(&L->d, x_dev, T, route_mode, key.threads, residual, key.bf16sim, out_dev, ws,
-                                      idx_dev, w_dev, dsr_stream);
+                                      idx_dev, w_dev, dsr_derr_dev(DSR_DERR_PREFILL_WAIT), key.spin_max, dsr_stream);
     hipGraph_t g = NULL;
     hipError_t ec = hipStreamEndCapture(dsr_stream, &g);
     if (e != hipSuccess || ec != hipSuccess || !g) {
@@ -420,7 +432,9 @@ int ds_hip_prefill_wait_error(ds_hip_layer_t *L, int T) {
   DSR_TRY(hipStreamSynchronize(dsr_stream), "sync");
   void *ws = dsr_scratch(DSR_SLOT_PF, dsh_pf_workspace_bytes(&L->d, T));
   if (!ws) return -1;
-  return dsh_pf_wait_error(ws, &L->d, T);
+  const int v = dsh_pf_wait_error(ws, &L->d, T);
+  if (v == 1) (void)dsr_derr_check(); /* reported here: the caller asked */
+  return v;
 }
 
 /* Average device time of n back-to-back prefill calls (HIP events on the library stream). */
@@ -760,6 +774,10 @@ struct ds_hip_stack {
   const uint16_t *lm;
   int vocab, H;
   int route_mode, bf16sim;
+  /* the reference's thread count when the stack was created (ds_set_threads): the row chunks the
+   * stack's exact kernels emulate (DECODE scores, the head's row order, sampling) all follow it, so
+   * a later ds_set_threads does not change a created stack or its captured graph */
+  int threads;
   int lm_fast;
   /* the argmax over an int8 copy of the head with exact bounds (same tokens; lm_fast heads only) */
   void *lmq_mem;
@@ -893,7 +911,8 @@ ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers,
   S->H = H;
   S->route_mode = route_mode;
   S->bf16sim = ds_bf16_simulate_python;
-  S->lm_fast = dsh_dec_lm_eligible(lm_head_dev, H, vocab, dsr_threads());
+  S->threads = dsr_threads();
+  S->lm_fast = dsh_dec_lm_eligible(lm_head_dev, H, vocab, S->threads);
   S->ncand = S->lm_fast ? dsh_dec_lm_blocks(vocab) : dsh_argmax_avx_blocks(vocab);
   if (S->lm_fast && dsh_lm_q8_supported(H, vocab)) lm_cert_build(S);
   const size_t np_bytes = al((size_t)layers[0]->np * 64 * 4);
@@ -1043,7 +1062,7 @@ static int stack_names(const ds_hip_stack_t *S, const char **names) {
     }
     for (int l = 0; l < S->n_layers; l++) {
       NM("attention");
-      if ((!cfg || S->bf16sim) && !dec_fused_router(S->layers[l], S->route_mode, S->split)) NM("scores");
+      if ((!cfg || S->bf16sim) && !dec_fused_router(S->layers[l], S->route_mode, S->split, S->threads)) NM("scores");
       if (S->split) {
         NM("layer");
       } else {
@@ -1058,7 +1077,7 @@ static int stack_names(const ds_hip_stack_t *S, const char **names) {
       NM("dense.down");
     }
     for (int l = 0; l < S->n_layers; l++) {
-      if (cfg ? l == 0 && !S->dense && !S->merged : !dec_fused_router(S->layers[l], S->route_mode, 1)) NM("scores");
+      if (cfg ? l == 0 && !S->dense && !S->merged : !dec_fused_router(S->layers[l], S->route_mode, 1, S->threads)) NM("scores");
       NM("layer");
     }
     if (!S->lm_fast) NM("copy_sum");
@@ -1103,7 +1122,7 @@ static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *ne
   int stride = S->in_stride, a = 0, nc = 1; /* nc: copies of xin (one-kernel layers: the per-XCD copies) */
   if (S->dense) {
     e = ds_hip_attn_enqueue(S->attn[a++], xin, st, stride, 1, NULL, S->step, S->pos0, S->hbuf, S->nbuf, NULL, 0,
-                            NULL);
+                            NULL, S->threads);
     if (e == hipSuccess) e = mark(ev, nev);
     if (e == hipSuccess)
       e = dsh_launch_dense_gate_up(S->dense->wg, S->dense->wu, S->nbuf, NULL, 0, S->dense->H, S->dense->I,
@@ -1124,12 +1143,12 @@ static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *ne
     /* with the copies, the attention's first kernel also writes their sum to xbuf for its residual */
     e = ds_hip_attn_enqueue(S->attn[a++], xin, st, stride, nc, nc > 1 ? S->xbuf : NULL, S->step, S->pos0, S->hbuf,
                             S->nbuf,
-                            cfgp ? L->d.router_f32_t : NULL, cfgp ? L->E : 0, cfgp ? pin : NULL);
+                            cfgp ? L->d.router_f32_t : NULL, cfgp ? L->E : 0, cfgp ? pin : NULL, S->threads);
     if (e == hipSuccess) e = mark(ev, nev);
-    const uint16_t *wr_dec = dec_fused_router(L, S->route_mode, S->split);
+    const uint16_t *wr_dec = dec_fused_router(L, S->route_mode, S->split, S->threads);
     if (S->split) S->sp[l].Wr_dec = wr_dec;
     if (e == hipSuccess && !cfgp && !wr_dec) {
-      e = scores_enqueue(L, S->nbuf, NULL, 0, S->route_mode, S->bf16sim, pin, &np);
+      e = scores_enqueue(L, S->nbuf, NULL, 0, S->route_mode, S->bf16sim, S->threads, pin, &np);
       if (e == hipSuccess) e = mark(ev, nev);
     }
     if (S->split) { /* one kernel: MoE(n) + h into the copies region l, clearing region l - 2 */
@@ -1142,8 +1161,9 @@ static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *ne
       xin = out;
       nc = C;
     } else {
+      const dsh_rcert_t rc = dsr_rcert(l);
       if (e == hipSuccess)
-        e = dsh_launch_dec_gate_up(&L->d, S->nbuf, NULL, 0, pin, np, S->route_mode, S->bf16sim, wk, dsr_stream);
+        e = dsh_launch_dec_gate_up(&L->d, S->nbuf, NULL, 0, pin, np, S->route_mode, S->bf16sim, wk, &rc, dsr_stream);
       if (e == hipSuccess) e = mark(ev, nev);
       if (e == hipSuccess)
         e = dsh_launch_dec_down(&L->d, S->nbuf, NULL, 0, S->xbuf, 1, S->hbuf, S->bf16sim, wk, NULL, 0, NULL,
@@ -1175,10 +1195,10 @@ static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *n
   const int cfg = S->route_mode == DS_HIP_ROUTE_CFG, mode = cfg ? DSH_ROUTE_CFG : DSH_ROUTE_DECODE;
   const int zn = (int)S->xc_region;
   int np0 = S->layers[0]->np;
-  for (int l = 0; l < NL; l++) S->sp[l].Wr_dec = dec_fused_router(S->layers[l], S->route_mode, 1);
+  for (int l = 0; l < NL; l++) S->sp[l].Wr_dec = dec_fused_router(S->layers[l], S->route_mode, 1, S->threads);
   if ((cfg ? !dense : !S->sp[0].Wr_dec) && !S->merged) {
     e = scores_enqueue(S->layers[0], dense ? S->xbuf : S->in, dense ? NULL : S->in_step, dense ? 0 : S->in_stride,
-                       S->route_mode, S->bf16sim, S->partials[0], &np0);
+                       S->route_mode, S->bf16sim, S->threads, S->partials[0], &np0);
     if (e == hipSuccess) e = mark(ev, nev);
   }
   for (int l = 0; l < NL && e == hipSuccess; l++) {
@@ -1194,7 +1214,7 @@ static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *n
       const float *pin = in + (size_t)C * H;  /* CFG: the score copies the previous layer accumulated */
       int np = C;
       if (!cfg && !S->sp[l].Wr_dec) { /* DECODE: the exact scores of the summed input */
-        e = dsh_launch_dec_scores_bf16_copies(L->d.router_bf16, in, NULL, 0, C, H, L->E, dsr_threads(),
+        e = dsh_launch_dec_scores_bf16_copies(L->d.router_bf16, in, NULL, 0, C, H, L->E, S->threads,
                                               S->partials[l & 1], dsr_stream);
         if (e == hipSuccess) e = mark(ev, nev);
         pin = S->partials[l & 1];
@@ -1246,8 +1266,10 @@ static hipError_t final_enqueue(ds_hip_stack_t *S, int clear) {
  * DECODE routing each layer keeps its exact scores kernel before it). */
 static int split_eligible(const ds_hip_stack_t *S) {
   if (!S->split_want || S->bf16sim) return 0;
+  const int cfg = S->route_mode == DS_HIP_ROUTE_CFG;
   for (int l = 0; l < S->n_layers; l++)
-    if (!dsh_layer_split_supported(&S->layers[l]->d)) return 0;
+    if (!dsh_layer_split_supported(&S->layers[l]->d) || (cfg && !dsh_layer_cert_supported(&S->layers[l]->d)))
+      return 0;
   return 1;
 }
 
@@ -1268,6 +1290,9 @@ static int scores_refresh(ds_hip_stack_t *S) {
   return 0;
 }
 
+/* Sleeps after which a routed block of a one-kernel layer stops waiting for its rank's verdict (the
+ * verifier's work takes a few microseconds, its exact fallback some more). */
+
 /* Allocates and fills the per-layer tiles and products and the copies regions. */
 static int split_build(ds_hip_stack_t *S) {
   if (S->split_arena) {
@@ -1284,7 +1309,8 @@ static int split_build(ds_hip_stack_t *S) {
     if (l + 1 < NL && S->route_mode == DS_HIP_ROUTE_CFG && !S->attn)
       bytes += al(dsh_layer_split_m_floats(d) * 4) + al((size_t)(d->E + 1) * 64 * 4);
   }
-  S->xc_region = (size_t)C * S->H + (size_t)C * 64;
+  /* per layer: the output copies, the next router's score copies, the routing verdict area */
+  S->xc_region = (size_t)C * S->H + (size_t)C * 64 + DSH_SPLIT_VD_INTS;
   bytes += al((size_t)NL * S->xc_region * 4);
   S->sp = (dsh_split_t *)calloc((size_t)NL, sizeof(dsh_split_t));
   if (!S->sp) return dsr_failf("split layer tables: out of memory");
@@ -1294,6 +1320,8 @@ static int split_build(ds_hip_stack_t *S) {
     return dsr_fail("one-kernel layer arena allocation", e);
   }
   char *b = (char *)S->split_arena;
+  S->xc = (float *)b; /* the regions first (their verdict areas are 128-byte aligned) */
+  b += al((size_t)NL * S->xc_region * 4);
   for (int l = 0; l < NL && e == hipSuccess; l++) {
     const dsh_layer_t *d = &S->layers[l]->d;
     dsh_split_t *F = &S->sp[l];
@@ -1317,6 +1345,12 @@ static int split_build(ds_hip_stack_t *S) {
     F->sz = z ? z + (size_t)d->E * 64 : NULL;
     F->WrT_next = nx ? nx->router_f32_t : NULL;
     F->E_next = nx ? nx->E : 0;
+    /* CFG routing: the selection certified against ds_linear's order by a verifier block per XCD */
+    if (S->route_mode == DS_HIP_ROUTE_CFG) {
+      F->vd = (unsigned *)(S->xc + (size_t)l * S->xc_region + (size_t)C * S->H + (size_t)C * 64);
+      F->derr = dsr_derr_dev(DSR_DERR_ROUTE_WAIT);
+      F->rc = dsr_rcert(l);
+    }
     e = dsh_launch_layer_build(d, F->WrT_next, F->E_next, tiles, tiles + routed, M, (float *)F->sM, z, (float *)F->sz,
                                dsr_stream);
   }
@@ -1330,7 +1364,6 @@ static int split_build(ds_hip_stack_t *S) {
     S->sp[l].pf_M = S->sp[l + 1].sM;
     S->sp[l].pf_SI = nd->SI;
   }
-  S->xc = (float *)b;
   if (e == hipSuccess) e = hipMemsetAsync(S->xc, 0, (size_t)NL * S->xc_region * 4, dsr_stream);
   if (e == hipSuccess) e = hipStreamSynchronize(dsr_stream);
   if (e != hipSuccess) return dsr_fail("one-kernel layer tables", e);
@@ -1378,12 +1411,13 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
       float *pin = S->partials[l & 1], *pout = S->partials[(l + 1) & 1];
       int np = L->np;
       if (!cfgp || first) {
-        e = scores_enqueue(L, xin, st, stride, S->route_mode, S->bf16sim, pin, &np);
+        e = scores_enqueue(L, xin, st, stride, S->route_mode, S->bf16sim, S->threads, pin, &np);
         if (e == hipSuccess) e = mark(ev, &n);
         if (e != hipSuccess) break;
       }
       const ds_hip_layer_t *next = cfgp && l + 1 < S->n_layers ? S->layers[l + 1] : NULL;
-      e = dsh_launch_dec_gate_up(&L->d, xin, st, stride, pin, np, S->route_mode, S->bf16sim, wk, dsr_stream);
+      const dsh_rcert_t rc = dsr_rcert(l);
+      e = dsh_launch_dec_gate_up(&L->d, xin, st, stride, pin, np, S->route_mode, S->bf16sim, wk, &rc, dsr_stream);
       if (e == hipSuccess) e = mark(ev, &n);
       if (e == hipSuccess)
         e = dsh_launch_dec_down(&L->d, xin, st, stride, S->xbuf, 1, NULL, S->bf16sim, wk, next ? next->d.router_f32_t : NULL,
@@ -1404,7 +1438,7 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
   } else if (S->lm_fast) {
     e = dsh_launch_dec_lm_argmax(S->lm, lm_in(S), S->H, S->vocab, S->cand, dsr_stream);
   } else {
-    int T = dsr_threads();
+    int T = S->threads;
     e = dsh_launch_argmax_avx_partial(S->lm, lm_in(S), S->cand, NULL, S->H, S->vocab,
                                       T > 1 ? (S->vocab + T - 1) / T : S->vocab, dsr_stream);
   }
@@ -1414,7 +1448,7 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
   if (e == hipSuccess && smp_active(S)) {
     /* the repetition penalty and the n-gram ban over this stack's earlier tokens, then (embedding
      * feed) the final token's row; one event after all of these kernels */
-    e = dsh_launch_sample(S->lm, lm_in(S), S->H, S->vocab, dsr_threads(), S->rp, S->ngram, S->step, S->tokens, NULL,
+    e = dsh_launch_sample(S->lm, lm_in(S), S->H, S->vocab, S->threads, S->rp, S->ngram, S->step, S->tokens, NULL,
                           S->hist_cap, smp_vals(S), smp_logits(S), smp_flag(S), dsr_stream);
     if (e == hipSuccess && S->emb)
       e = dsh_launch_embed_next(S->tokens, S->step, S->emb, S->emb_vocab, S->H, S->ebuf, dsr_stream);
@@ -1661,7 +1695,7 @@ int ds_hip_time_lm_head(ds_hip_stack_t *S, int n, float *ms) {
     } else if (S->lm_fast) {
       e = dsh_launch_dec_lm_argmax(S->lm, lm_in(S), S->H, S->vocab, S->cand, dsr_stream);
     } else {
-      int T = dsr_threads();
+      int T = S->threads;
       e = dsh_launch_argmax_avx_partial(S->lm, lm_in(S), S->cand, NULL, S->H, S->vocab,
                                         T > 1 ? (S->vocab + T - 1) / T : S->vocab, dsr_stream);
     }

@@ -169,18 +169,17 @@ void ds_expert_forward_fused(float *out, const float *x, const uint16_t *gate_up
   dsr_d2h(out, od, F4(hidden));
 }
 
-/* ds_kernels.c:981-1011 (non-NEON branch). */
+/* ds_kernels.c:981-1011 (non-NEON branch). The row is staged from the caller's array at every call
+ * (2 bytes per column): a registered head is keyed by address, and a row read from it could belong
+ * to an older array at the same address. */
 float ds_bf16_dot_row(const float *x, const uint16_t *W_bf16, int in_dim, int tok_id) {
   if (!x || !W_bf16 || in_dim <= 0 || tok_id < 0) return 0.0f;
   if (dsr_init()) return 0.0f;
-  /* The reference's callers pass the LM head after the argmax has registered it
-   * (ds_moe_decoder.c:1041-1043): read the row from that device copy; otherwise stage this one row. */
   const size_t row_bytes = (size_t)in_dim * 2;
-  const uint16_t *head = (const uint16_t *)dsr_weight_lookup(W_bf16, row_bytes * ((size_t)tok_id + 1));
-  const uint16_t *Wd = head ? head + (size_t)tok_id * in_dim : (const uint16_t *)dsr_scratch(DSR_SLOT_D, row_bytes);
+  const uint16_t *Wd = (const uint16_t *)dsr_scratch(DSR_SLOT_D, row_bytes);
   float *xd = (float *)dsr_scratch(DSR_SLOT_X, F4(in_dim)), *od = (float *)dsr_scratch(DSR_SLOT_Y, F4(1));
   if (!Wd || !xd || !od || dsr_h2d(xd, x, F4(in_dim))) return 0.0f;
-  if (!head && dsr_h2d((void *)Wd, W_bf16 + (size_t)tok_id * in_dim, row_bytes)) return 0.0f;
+  if (dsr_h2d((void *)Wd, W_bf16 + (size_t)tok_id * in_dim, row_bytes)) return 0.0f;
   hipError_t e = dsh_launch_bf16_dot_row(Wd, xd, in_dim, 0, od, dsr_stream);
   if (e != hipSuccess) {
     dsr_fail("ds_bf16_dot_row", e);

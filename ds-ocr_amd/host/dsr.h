@@ -24,6 +24,20 @@ int dsr_failf(const char *fmt, ...);
     if (dsr_e_ != hipSuccess) return dsr_fail((what), dsr_e_); \
   } while (0)
 
+/* Errors that kernels report from the device: a word of mapped, coherent host memory per kind, which
+ * a kernel sets (a system-scope store) when one of its bounded waits gives up, and the host reads
+ * without a copy. dsr_derr_dev(kind) is the device address to pass to the kernel (NULL before
+ * dsr_init). dsr_derr_check() reports (and clears) any word that is set: -1 with ds_hip_last_error
+ * naming the failure, else 0. It runs after every synchronisation the library API offers
+ * (ds_hip_sync) and at the entry of the calls whose results such a failure voids. */
+enum { DSR_DERR_PREFILL_WAIT, DSR_DERR_ROUTE_WAIT, DSR_DERR_N };
+int *dsr_derr_dev(int kind);
+int dsr_derr_check(void);
+
+/* The certified CFG routing's counters and optional log (ds_hip_route_stats, ds_hip_set_route_log)
+ * for a launch: tag identifies the layer in the log entries. */
+dsh_rcert_t dsr_rcert(int tag);
+
 /* Grow-only device staging buffer per slot (not thread-safe, like the reference API). */
 enum { DSR_SLOT_X, DSR_SLOT_Y, DSR_SLOT_A, DSR_SLOT_B, DSR_SLOT_C, DSR_SLOT_D, DSR_SLOT_IDX, DSR_SLOT_PF, DSR_NSLOTS };
 void *dsr_scratch(int slot, size_t bytes);
@@ -49,8 +63,6 @@ void dsr_block_forget(const void *qweight);
 
 /* Device copy of a host weight array (bf16 / f32), uploaded on first use, same keying. */
 const void *dsr_weight_device(const void *host, size_t bytes);
-/* The device copy of a registered weight array of at least `bytes`, or NULL (no upload). */
-const void *dsr_weight_lookup(const void *host, size_t bytes);
 /* A device allocation derived from registered weights (e.g. the LM head's int8 copy): NULL until
  * set; dsr_weight_set_aux hands it to the registry, which frees it with the weights' entry (when
  * the weights change or are replaced). */
@@ -65,7 +77,7 @@ int dsr_threads(void);
 struct ds_hip_attn;
 hipError_t ds_hip_attn_enqueue(const struct ds_hip_attn *A, const float *x_in, const int *step, int stride,
                                int ncopies, float *x_plain, const int *pos_ptr, int pos_add, float *h_out, float *n_out,
-                               const float *WrT_next, int E_next, float *partials_next);
+                               const float *WrT_next, int E_next, float *partials_next, int threads);
 int ds_hip_attn_hidden(const struct ds_hip_attn *A);
 int ds_hip_attn_max_seq(const struct ds_hip_attn *A); /* KV positions the caches hold */
 size_t ds_hip_attn_weight_bytes(const struct ds_hip_attn *A); /* projections and norms read per token */

@@ -35,6 +35,64 @@ int dsr_fail(const char *what, hipError_t e) { return dsr_failf("%s: %s", what, 
 
 const char *ds_hip_last_error(void) { return g_err; }
 
+/* The device error words (DSR_DERR_*): one 64-byte line each of mapped, coherent pinned memory. */
+static int *g_derr_host = NULL, *g_derr_dev = NULL;
+#define DERR_STRIDE 16
+
+int *dsr_derr_dev(int kind) {
+  return g_derr_dev && kind >= 0 && kind < DSR_DERR_N ? g_derr_dev + DERR_STRIDE * kind : NULL;
+}
+
+/* Counters of the certified CFG routing ([0] routings, [1] recomputed in ds_linear's order, [2]
+ * one-kernel layers whose output was corrected to the certified selection) and the routing log
+ * (ds_hip_set_route_log). */
+static unsigned long long *g_rstat = NULL;
+static int *g_rlog = NULL, g_rlog_cap = 0;
+
+dsh_rcert_t dsr_rcert(int tag) {
+  dsh_rcert_t r;
+  r.stats = g_rstat;
+  r.log = g_rlog;
+  r.log_cap = g_rlog_cap;
+  r.tag = tag;
+  return r;
+}
+
+int ds_hip_route_stats(unsigned long long *counts, int reset) {
+  if (dsr_init()) return -1;
+  if (!counts) return dsr_failf("ds_hip_route_stats: NULL argument");
+  DSR_TRY(hipStreamSynchronize(dsr_stream), "synchronize");
+  DSR_TRY(hipMemcpy(counts, g_rstat, 3 * sizeof(unsigned long long), hipMemcpyDeviceToHost), "route counters");
+  if (reset) DSR_TRY(hipMemset(g_rstat, 0, 3 * sizeof(unsigned long long)), "route counters");
+  return 0;
+}
+
+int ds_hip_set_route_log(int *log_dev, int capacity) {
+  if (dsr_init()) return -1;
+  if ((log_dev == NULL) != (capacity == 0) || capacity < 0)
+    return dsr_failf("ds_hip_set_route_log: a buffer needs a capacity (NULL and 0 switch the log off)");
+  g_rlog = log_dev;
+  g_rlog_cap = capacity;
+  return 0;
+}
+
+int dsr_derr_check(void) {
+  static const char *what[DSR_DERR_N] = {
+      "prefill: a down tile's bounded wait for its gate_up tiles gave up; that call's output is not valid",
+      "decode: a certified layer's bounded wait for its verdict on the expert selection gave up; the "
+      "step's output is not valid",
+  };
+  if (!g_derr_host) return 0;
+  int rc = 0;
+  for (int k = 0; k < DSR_DERR_N; k++) {
+    if (__atomic_load_n(g_derr_host + DERR_STRIDE * k, __ATOMIC_ACQUIRE)) {
+      __atomic_store_n(g_derr_host + DERR_STRIDE * k, 0, __ATOMIC_RELEASE);
+      rc = dsr_failf("%s", what[k]);
+    }
+  }
+  return rc;
+}
+
 int dsr_init(void) {
   if (g_init == 1) return 0;
   if (g_init == -1) return dsr_failf("HIP device unavailable (initialisation failed earlier)");
@@ -49,6 +107,22 @@ int dsr_init(void) {
   if (e != hipSuccess) {
     g_init = -1;
     return dsr_fail("HIP init", e);
+  }
+  /* the device error words: host memory the kernels write directly */
+  if (e == hipSuccess)
+    e = hipHostMalloc((void **)&g_derr_host, (size_t)DSR_DERR_N * DERR_STRIDE * sizeof(int),
+                      hipHostMallocMapped | hipHostMallocCoherent);
+  if (e == hipSuccess) {
+    memset(g_derr_host, 0, (size_t)DSR_DERR_N * DERR_STRIDE * sizeof(int));
+    e = hipHostGetDevicePointer((void **)&g_derr_dev, g_derr_host, 0);
+  }
+  if (e != hipSuccess) {
+    g_init = -1;
+    return dsr_fail("HIP init (device error words)", e);
+  }
+  if (hipMalloc((void **)&g_rstat, 256) != hipSuccess || hipMemset(g_rstat, 0, 256) != hipSuccess) {
+    g_init = -1;
+    return dsr_failf("HIP init: routing counters");
   }
   /* the device address of the allocation-free entry points' scratch array (device 0 is current) */
   if (dsh_static_scratch_init()) {
@@ -299,11 +373,6 @@ int dsr_weight_set_aux(const void *host, void *aux_dev) {
   return 0;
 }
 
-const void *dsr_weight_lookup(const void *host, size_t bytes) {
-  entry_t *e = find(host, 0);
-  return e && e->bytes >= bytes ? e->dev : NULL;
-}
-
 const void *dsr_weight_device(const void *host, size_t bytes) {
   if (dsr_init()) return NULL;
   uint64_t fp = fingerprint(host, bytes);
@@ -420,5 +489,5 @@ int ds_hip_time_stream_read(const void *src_dev, size_t bytes, int n, float *ms)
 int ds_hip_sync(void) {
   if (dsr_init()) return -1;
   DSR_TRY(hipStreamSynchronize(dsr_stream), "synchronize");
-  return 0;
+  return dsr_derr_check();
 }

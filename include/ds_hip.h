@@ -36,7 +36,30 @@ int ds_hip_memcpy_d2d(void *dst_dev, const void *src_dev, size_t bytes);
 /* Average time of n back-to-back launches of a plain streaming read of bytes of src_dev (the
  * achievable-bandwidth reference for the HBM-bound kernels; no counterpart in the reference). */
 int ds_hip_time_stream_read(const void *src_dev, size_t bytes, int n, float *ms);
+/* Waits for the library stream. Returns -1 (message in ds_hip_last_error) if a kernel reported since
+ * the last check that one of its bounded waits gave up (the prefill's down tiles waiting for their
+ * gate_up tiles, the one-kernel decode layers' extra blocks waiting for the verdict on the expert
+ * selection): the output of that call or step is not valid. The report is given once. */
 int ds_hip_sync(void);
+/* Certified CFG routing (no counterpart in the reference; it makes the decode and prefill paths pick
+ * exactly the experts ds_moe_router + ds_moe_top_k pick, ds_kernels.c:181-243, on the same input):
+ * each MoE layer selects on router scores summed in its own order, checks the selection against a
+ * rigorous bound on the difference to ds_linear's sequential order, and recomputes the scores of
+ * the experts the bound leaves open in that order. In the stacks' one-kernel layers the routed
+ * blocks select from the accumulated scores and add their shares at once, while 32 extra blocks
+ * compute the exact scores' intervals and certify that selection, or add the difference to the one
+ * certified (rare: a near tie the accumulated scores ranked otherwise). counts[0] = decode routings made since the last
+ * reset, counts[1] = those that needed the recomputation, counts[2] = one-kernel layers whose output
+ * was corrected to the certified selection (their routed blocks had used another). Synchronises;
+ * reset = 1 zeroes them. */
+int ds_hip_route_stats(unsigned long long *counts, int reset);
+/* Test aid: a device buffer that receives one entry per decode routing (log_dev[0] = entries
+ * written, then from int 64 entries of 32 + hidden ints: idx[8], w[8] (f32 bits), flags (bit 0:
+ * recomputed in ds_linear's order; bit 1: a one-kernel layer's verdict replaced its speculative
+ * selection), the layer index, 14 spare ints, the routed input [hidden] (f32 bits)). Kernels record
+ * into the buffer set when they are launched or captured (ds_hip_stack_bind); NULL, 0 switches it
+ * off. The caller zeroes log_dev[0]. */
+int ds_hip_set_route_log(int *log_dev, int capacity);
 /* Seeded synthetic data generated on the device (counter-based SplitMix64 + Box–Muller). */
 int ds_hip_fill_normal_bf16(uint16_t *dst_dev, size_t n, uint64_t seed, float std_);
 int ds_hip_fill_normal_f32(float *dst_dev, size_t n, uint64_t seed, float mean, float std_);
@@ -104,7 +127,11 @@ int ds_hip_layer_forward(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
  * ds_hip_layer_forward (route_mode), experts as an expert-sorted grouped GEMM on the int8 MFMA
  * (each f32 activation row as two 8-bit limbs, exact integer sums), routed outputs added in
  * ascending expert order, then the shared expert. idx_dev/w_dev (optional,
- * [T][top_k]) receive the routing. Asynchronous; out_dev must not alias x_dev. */
+ * [T][top_k]) receive the routing. Asynchronous; out_dev must not alias x_dev. The reference's block
+ * is synchronous and always complete: if the persistent GEMM kernel's bounded wait gives up (its
+ * gate_up tiles not done after the wait limit), the next ds_hip_sync, ds_hip_prefill_wait_error or
+ * ds_hip_layer_prefill call returns -1 with ds_hip_last_error saying so, and that output is not
+ * valid. */
 int ds_hip_layer_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, int T, int route_mode, int residual,
                          int *idx_dev, float *w_dev);
 
@@ -119,6 +146,12 @@ int ds_hip_prefill_path(int mode);
 /* After a prefill call of T tokens on L: 1 if the persistent kernel's bounded wait for a gate_up
  * tile expired (that call's output is not valid), 0 if not, -1 on error. Synchronises. */
 int ds_hip_prefill_wait_error(ds_hip_layer_t *L, int T);
+/* Test hook (no counterpart in the reference): the sleeps after which a persistent prefill tile's
+ * wait for its gate_up tiles gives up. DS_HIP_PREFILL_WAIT_DEFAULT restores the default (2^22);
+ * spins < 0 makes every such wait give up at once (every kernel still runs to its end; the output is
+ * then not valid and the failure is reported as above). Takes effect at the next call. */
+#define DS_HIP_PREFILL_WAIT_DEFAULT (-2147483647 - 1)
+int ds_hip_prefill_set_wait_limit(int spins);
 
 /* Self-check of the prefill SwiGLU (no counterpart in the reference): the GEMM epilogue's
  * reciprocal-based (g / (1 + fast_exp(-g))) * u against the correctly rounded division of
@@ -228,7 +261,10 @@ int ds_hip_lm_head_sample(const float *x_dev, const uint16_t *lm_head_dev, int h
  * Before ds_hip_stack_bind; (NULL, 0, ...) returns to MoE layers only. Blocks are borrowed. */
 int ds_hip_stack_set_attention(ds_hip_stack_t *S, ds_hip_attn_t *const *attn, int n_attn, const float *final_norm,
                                float final_eps, int pos0, int trunc_final);
-/* lm_head_dev: bf16 [vocab, hidden] on the device (borrowed). Layers are borrowed. */
+/* lm_head_dev: bf16 [vocab, hidden] on the device (borrowed). Layers are borrowed. The reference
+ * thread count current here (ds_set_threads, ds_kernels.c:123-175) is the one the stack emulates for
+ * as long as it lives (the row chunks of the DECODE router, the LM head's row order, the attention's
+ * QKV split, the sampling rules); a later ds_set_threads does not change it. */
 ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers, const uint16_t *lm_head_dev,
                                     int vocab, int route_mode);
 /* Puts a dense FFN layer before the MoE layers (the decoder's layer 0): a step then runs
@@ -249,8 +285,9 @@ int ds_hip_stack_set_layer_kernels(ds_hip_stack_t *S, int one_kernel);
 /* Kernels per MoE layer of the bound stack (1 or 2). */
 int ds_hip_stack_layer_kernels(const ds_hip_stack_t *S);
 /* LM-head argmax over an int8 copy of the head (no counterpart in the reference; the tokens are
- * the reference's, ds_argmax_matvec_bf16's, ds_kernels_avx.c:162-245). Each block of 256 rows
- * streams the int8 rows (half the bytes) with a rigorous bound on every row's exact logit, then
+ * the reference's, ds_argmax_matvec_bf16's, ds_kernels_avx.c:162-245). Each block of 512 rows
+ * (one block per CU) streams the int8 rows (half the bytes) with a rigorous bound on every row's
+ * exact logit, then
  * recomputes in the reference's order only its rows whose upper bound reaches the block's largest
  * lower bound, which always include the block's argmax and every row tied with it. On by default
  * where the one-pass head applies and hidden is a multiple of 256 (<= 2048); ds_hip_stack_create

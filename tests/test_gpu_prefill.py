@@ -250,3 +250,47 @@ def test_prefill_swiglu_equals_division_on_every_gate_value(dev):
     dev.check(L.ds_hip_check_prefill_swiglu(n), "swiglu check")
     assert n[0] == 0, n[0]
     assert n[1] <= 2 ** 25, n[1]  # only among the g with |g| < 2^-125 (2^24 bit patterns per sign)
+
+
+def test_prefill_wait_expiry_reaches_the_caller(dev, B):
+    """The reference's block always returns a complete result (ds_moe_decoder.c:629-809). When the
+    persistent kernel's bounded wait for a down tile's gate_up tiles gives up, the caller is told:
+    with the wait limit forced from the host so that every such wait gives up at once (each kernel
+    still runs to its end), the next ds_hip_sync returns -1 naming the prefill, a later prefill call
+    reports a failure left unreported, and once the limit is restored the same call is valid and
+    equal to the normal result."""
+    L = dev.load()
+    if L.ds_hip_prefill_path(-1) != 1:
+        pytest.skip("persistent prefill kernel not available on this device")
+    lay = B.make_moe_layer(65, hidden=256, inter=128, n_experts=16)
+    h = upload_layer(dev, lay)
+    T = 64
+    X = np.stack([B.normal_f32(256, 9000 + t) for t in range(T)])
+    xd = dev.DeviceBuffer.from_array(X)
+    od = dev.DeviceBuffer(X.nbytes)
+    try:
+        assert L.ds_hip_prefill_path(1) == 1
+        good, _, _ = gpu_prefill(dev, h, X, 1)
+        assert L.ds_hip_prefill_set_wait_limit(-1) == 0
+        print("prefill with every wait giving up: ds_hip_sync", flush=True)
+        dev.check(L.ds_hip_layer_prefill(h, od.ptr, xd.ptr, T, 1, 0, None, None), "prefill")
+        assert L.ds_hip_sync() == -1
+        assert b"prefill" in L.ds_hip_last_error() and b"not valid" in L.ds_hip_last_error()
+        assert L.ds_hip_sync() == 0  # reported once
+        print("prefill with every wait giving up: the next prefill call", flush=True)
+        dev.check(L.ds_hip_layer_prefill(h, od.ptr, xd.ptr, T, 1, 0, None, None), "prefill")
+        od.to_array(np.float32)  # synchronises without checking the error words
+        assert L.ds_hip_prefill_set_wait_limit(L_DEFAULT) == 0
+        assert L.ds_hip_layer_prefill(h, od.ptr, xd.ptr, T, 1, 0, None, None) == -1
+        assert b"prefill" in L.ds_hip_last_error()
+        print("prefill with the default wait limit", flush=True)
+        again, _, _ = gpu_prefill(dev, h, X, 1)
+        assert L.ds_hip_sync() == 0
+        assert np.array_equal(good.view(np.uint32), again.view(np.uint32))
+    finally:
+        L.ds_hip_prefill_set_wait_limit(L_DEFAULT)
+        L.ds_hip_prefill_path(-1)
+        L.ds_hip_layer_destroy(h)
+
+
+L_DEFAULT = -2147483647 - 1  # DS_HIP_PREFILL_WAIT_DEFAULT
