@@ -98,6 +98,7 @@ SIGNATURES = {
     "ds_hip_stack_capacity": (C.c_int, [vp]),
     "ds_hip_argmax_bf16_noalloc": (C.c_int, [vp, vp, vp, C.c_int, C.c_int]),
     "ds_hip_weights_changed": (C.c_int, [vp]),
+    "ds_hip_argmax_int8_copy": (C.c_int, [vp]),
     "ds_hip_register_block": (C.c_int, [C.POINTER(Int4Block)]),
     "ds_hip_register_weights": (C.c_int, [vp, C.c_size_t]),
     "ds_hip_stack_steps_left": (C.c_int, [vp]),

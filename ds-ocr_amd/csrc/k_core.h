@@ -276,7 +276,7 @@ typedef struct {
    * given). */
   unsigned *vd;
   int *derr;       /* set (system scope) when an extra block's wait for the verdict gives up */
-  dsh_rcert_t rc;  /* counters and log (recorded on XCD 0) */
+  dsh_rcert_t rc;  /* counters and log (CFG: the verdict's block records; DECODE: the log only) */
 } dsh_split_t;
 #define DSH_SPLIT_VD_INTS (64 + 256 * 32)
 int dsh_layer_split_supported(const dsh_layer_t *L);

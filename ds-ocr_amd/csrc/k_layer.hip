@@ -266,6 +266,20 @@ __device__ __forceinline__ void dl_body(const dsh_layer_t &L, const dsh_split_t 
       route_finish(mode, st, idx, w);
       const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), slot));
       if (lane == 0) S.s_w[0] = slot < st.ns ? ws : 0.0f;  // DECODE: an empty slot adds with weight 0
+      if (mode == DSH_ROUTE_DECODE && F.rc.log && rb == 0) {  // the routing log (a test aid): one block
+        if (lane < 8) {
+          S.s_vi[lane] = lane < L.K ? idx : -1;
+          S.s_vw[lane] = lane < L.K ? w : 0.0f;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane == 0) {
+          dsh_rcert_t r = F.rc;
+          r.stats = nullptr;  // the counters count CFG routings only
+          cert_record(r, S.s_vi, S.s_vw, L.K, 0, S.s_x, H);
+        }
+      }
     }
   }
   {

@@ -1350,6 +1350,8 @@ static int split_build(ds_hip_stack_t *S) {
       F->vd = (unsigned *)(S->xc + (size_t)l * S->xc_region + (size_t)C * S->H + (size_t)C * 64);
       F->derr = dsr_derr_dev(DSR_DERR_ROUTE_WAIT);
       F->rc = dsr_rcert(l);
+    } else {
+      F->rc = dsr_rcert(l); /* DECODE: the routing log only (one routed block records each layer's selection) */
     }
     e = dsh_launch_layer_build(d, F->WrT_next, F->E_next, tiles, tiles + routed, M, (float *)F->sM, z, (float *)F->sz,
                                dsr_stream);

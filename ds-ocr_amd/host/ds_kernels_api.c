@@ -210,6 +210,8 @@ int ds_argmax_matvec_bf16_excluding(const float *x, const uint16_t *W_bf16, int 
   return idx >= 0 && idx < out_dim ? idx : 0;
 }
 
+int ds_hip_argmax_int8_copy(const uint16_t *W_bf16) { return W_bf16 && dsr_weight_aux(W_bf16) ? 1 : 0; }
+
 static int argmax_excluding(const float *x, const uint16_t *W_bf16, int in_dim, int out_dim, const int *exclude_ids,
                             int n_exclude) {
   if (!x || !W_bf16 || in_dim <= 0 || out_dim <= 0) return dsr_failf("ds_argmax_matvec_bf16: invalid arguments");

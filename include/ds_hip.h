@@ -53,7 +53,8 @@ int ds_hip_sync(void);
  * was corrected to the certified selection (their routed blocks had used another). Synchronises;
  * reset = 1 zeroes them. */
 int ds_hip_route_stats(unsigned long long *counts, int reset);
-/* Test aid: a device buffer that receives one entry per decode routing (log_dev[0] = entries
+/* Test aid: a device buffer that receives one entry per decode routing (CFG: every layer kind;
+ * DECODE: the stacks' one-kernel layers) (log_dev[0] = entries
  * written, then from int 64 entries of 32 + hidden ints: idx[8], w[8] (f32 bits), flags (bit 0:
  * recomputed in ds_linear's order; bit 1: a one-kernel layer's verdict replaced its speculative
  * selection), the layer index, 14 spare ints, the routed input [hidden] (f32 bits)). Kernels record
@@ -71,6 +72,11 @@ int ds_hip_fill_normal_f32(float *dst_dev, size_t n, uint64_t seed, float mean, 
  * uploaded again at the next use. Returns the number of copies dropped (0 if none), -1 on error.
  * No counterpart in the reference, whose weights are read-only mmaps (ds_ocr.c:611-622). */
 int ds_hip_weights_changed(const void *host_ptr);
+/* Diagnostic: 1 when ds_argmax_matvec_bf16 serves the registered head W_bf16 through its int8 copy
+ * with exact bounds (built at the first call when every row is in the reference's 4-row-group
+ * order for the current thread count and the head's shape is supported), 0 when it streams the bf16
+ * head. No counterpart in the reference. */
+int ds_hip_argmax_int8_copy(const uint16_t *W_bf16);
 /* Registers (uploads) a block or a weight array now rather than at its first use, e.g. at load time
  * so the first tokens do not pay for the uploads. 0 or -1. */
 int ds_hip_register_block(const ds_int4_block_t *block);

@@ -104,6 +104,28 @@ def test_config4_226_steps(dev, B):
     assert np.array_equal(got, want)
 
 
+def test_config4_226_steps_bounded_head(dev, B):
+    """Config 4 through the drop-in ds_argmax_matvec_bf16 (host pointers) at 16 threads, the path
+    that serves the head from its int8 copy with exact bounds (k_lm_q8_argmax, the kernel the bench
+    times): 226 steps on fresh seeded inputs, every index equal to or_argmax_bf16's."""
+    from concurrent.futures import ThreadPoolExecutor
+    L = dev.load()
+    V, H, N = 129280, 1280, 226
+    W = B.normal_bf16(V * H, 4343, 0.02)
+    xs = np.stack([B.normal_f32(H, 50000 + s) for s in range(N)])
+    try:
+        L.ds_set_threads(16)
+        got = np.array([L.ds_argmax_matvec_bf16(xs[s], W, H, V) for s in range(N)])
+        assert L.ds_hip_argmax_int8_copy(W.ctypes.data) == 1  # the bounded head served these calls
+    finally:
+        L.ds_hip_weights_changed(W.ctypes.data)
+        L.ds_set_threads(1)
+    with ThreadPoolExecutor(8) as ex:
+        want = np.array(list(ex.map(lambda s: B.oracle().or_argmax_bf16(xs[s], W, H, V, 16, None), range(N))))
+    print(f"config 4, bounded head: {int(np.sum(got == want))}/{N} indices equal")
+    assert np.array_equal(got, want)
+
+
 def test_lm_argmax_config5_head(dev, B):
     """The full 129280 x 1280 head of config 5, 16 reference threads (chunks of 8080 rows)."""
     L = dev.load()

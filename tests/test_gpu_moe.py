@@ -380,15 +380,30 @@ def test_one_kernel_decode_scores_in_layer(dev, B, threads, fused):
     sits in a 4- or 2-row group (18 experts: chunks 18, 6, 2), the routed blocks compute the exact
     scores themselves and no scores kernel runs; an odd chunk (3 rows; 6 and 7 threads) puts rows on
     the single-row path and keeps the scores kernel. Hidden states against the oracle run with the
-    same thread count (its selection is the reference's), tokens against its argmax."""
+    same thread count (its selection is the reference's), tokens against its argmax.
+
+    The routing itself is pinned too: every layer's bf16 router gets near ties (pairs of rows one
+    ulp apart at a coordinate where the first layer's inputs are tiny, so only the order of the sums
+    decides, and a pair of equal rows, where the lower index wins), and each layer's logged
+    selection (experts in rank order and weights) must equal or_moe_layer_decode's bit for bit on
+    the layer's own logged input."""
+    from test_gpu_route_cert import RouteLog
     L = dev.load()
-    H = 512
-    lays = [B.make_moe_layer(180 + i, hidden=H, inter=256, n_experts=18, top_k=6, n_shared=2) for i in range(3)]
+    H, K = 512, 6
+    lays = [B.make_moe_layer(180 + i, hidden=H, inter=256, n_experts=18, top_k=K, n_shared=2) for i in range(3)]
+    for lay in lays:
+        Wb = lay.router_bf16.reshape(18, H)
+        for a, col in ((0, 3), (2, 7), (4, 11)):
+            Wb[a + 1] = Wb[a]
+            Wb[a + 1, col] = Wb[a, col] + 1  # one bf16 ulp (same sign and exponent)
+        Wb[17] = Wb[16]
     hs = [upload_layer(dev, lay) for lay in lays]
     vocab = 3000
     lm_w = B.normal_bf16(vocab * H, 181, 0.02)
     lm = dev.DeviceBuffer.from_array(lm_w)
     xs = np.stack([B.normal_f32(H, 1800 + s) for s in range(4)])
+    xs[:, [3, 7, 11]] = np.float32(1e-6)
+    log = RouteLog(dev, 64, H)
     try:
         L.ds_set_threads(threads)
         names = []
@@ -402,7 +417,19 @@ def test_one_kernel_decode_scores_in_layer(dev, B, threads, fused):
                   f"eager vs graph {erre:.2e}; token {toks[s]} vs {rt[s]}")
             assert err < TOL and erre < 1e-4
             assert toks[s] == B.oracle().or_argmax_bf16(hid[s], lm_w, H, vocab, threads, None)
+        idx, w, flags, tags, xin = log.entries()
+        assert len(idx) == 2 * len(xs) * len(lays), len(idx)  # graph and eager runs
+        orls = [lay.or_layer() for lay in lays]
+        for j in range(len(idx)):
+            ri, rw = np.empty(K, np.int32), np.empty(K, np.float32)
+            o = np.empty(H, np.float32)
+            B.oracle().or_moe_layer_decode(o, np.ascontiguousarray(xin[j]), C.byref(orls[int(tags[j])]), 0, 0,
+                                           threads, ri, rw)
+            assert np.array_equal(idx[j, :K], ri) and np.array_equal(w[j, :K].view(np.int32), rw.view(np.int32)), \
+                (j, int(tags[j]), idx[j, :K], ri, w[j, :K], rw)
+        print(f"{len(idx)} DECODE routings equal to the reference's bit for bit")
     finally:
+        log.close()
         L.ds_set_threads(1)
         for h in hs:
             L.ds_hip_layer_destroy(h)
