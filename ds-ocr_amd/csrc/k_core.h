@@ -38,8 +38,32 @@ hipError_t dsh_launch_vec_add(float *dst, const float *a, const float *b, int n,
 hipError_t dsh_launch_expert_combine(float *out, const float *eo, const float *w, int top_k, int hidden,
                                      hipStream_t s);
 hipError_t dsh_launch_split_swiglu(float *h, const float *gu, int inter, int bf16sim, hipStream_t s);
+/* One expert (gate_up, SwiGLU, down) in the reference's per-row order in one launch: the gate
+ * blocks write h into hbuf (I device 64-bit words) tagged with epoch, which must differ from the
+ * previous launch's on the same hbuf; the down blocks wait (bounded by spin polls; *derr set on
+ * expiry) until every word carries it. xcache (optional, H device floats): receives x for later
+ * calls on the same input. done (optional): down block d stores epoch to done[d] (system scope,
+ * release) after its output rows. 0 blocks: shape not supported. */
+int dsh_expert_exact_blocks(int H, int I);
+hipError_t dsh_launch_expert_exact(const int8_t *gq, const float *gs, const float *go, const int8_t *dq, const float *dsc,
+                                   const float *dof, const float *x, float *xcache, unsigned long long *hbuf, float *y,
+                                   unsigned *done, int H, int I, unsigned epoch, int bf16sim, int spin, int *derr,
+                                   hipStream_t s);
+/* Down blocks of dsh_launch_expert_exact (one completion word each when done is given). */
+int dsh_expert_exact_down_blocks(int H);
 hipError_t dsh_launch_bf16_matvec_avx(const uint16_t *W, const float *x, const float *bias, float *y, int in_dim,
                                       int out_dim, int nthreads, hipStream_t s);
+/* The _done variants: block b stores epoch to done[b] (system scope, release) after its outputs, for
+ * a host polling those words (dsr_pin_out_done); _blocks gives the number of words. */
+int dsh_bf16_matvec_avx_blocks(int out_dim);
+hipError_t dsh_launch_bf16_matvec_avx_done(const uint16_t *W, const float *x, const float *bias, float *y, int in_dim,
+                                           int out_dim, int nthreads, unsigned *done, unsigned epoch, hipStream_t s);
+int dsh_vec_add_blocks(int n);
+hipError_t dsh_launch_vec_add_done(float *dst, const float *a, const float *b, int n, unsigned *done, unsigned epoch,
+                                   hipStream_t s);
+int dsh_expert_combine_blocks(int hidden);
+hipError_t dsh_launch_expert_combine_done(float *out, const float *eo, const float *w, int top_k, int hidden,
+                                          unsigned *done, unsigned epoch, hipStream_t s);
 int dsh_argmax_avx_blocks(int out_dim);
 /* Candidate keys in the file-scope device array of k_core.hip: DSH_STATIC_CAND entries (out_dim up
  * to 64 * DSH_STATIC_CAND rows). _init looks its address up for the current device (once per

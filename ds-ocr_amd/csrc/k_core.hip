@@ -179,6 +179,237 @@ __global__ void __launch_bounds__(256) k_int8_matvec_chain(const int8_t *__restr
   y[rr] = __builtin_fmaf(scale[r], dot, offset[r] * xs);
 }
 
+// The same order from LDS: a block stages its MV_RB rows as f32 codes u = q + 128 (coalesced
+// 16-byte loads, all in flight at once, converted on the way into LDS; row stride in_dim + 4
+// floats) and x; then wave 0 runs one row per lane, dot = fma(u_j, x_j, dot) in order (one LDS-fed
+// fused multiply-add per step), while wave 1 forms xs = Σ x_j in order once (it is the same for
+// every row: the reference adds it in the same loop, int8_matvec_generic, ds_quantize.c:154-170),
+// and y = fma(scale, dot, offset * xs). in_dim % 16 == 0, q 16-byte aligned, in_dim <= MV_MAX_DIM.
+#define MV_RB 16           // rows per block
+#define MV_PB 7            // 16-byte row chunks per thread (16 rows x 1792 bytes)
+#define MV_MAX_DIM 1792
+
+// Staged rows 0 .. na - 1 are rows a0 .., staged rows na .. na + nb - 1 are rows b0 .. of q (stride
+// in_dim), as f32 codes into s_rows (stride in_dim + 4 floats); PB * 256 >= (na + nb) * in_dim / 16.
+template <int PB>
+__device__ __forceinline__ void mv_stage_rows(float *s_rows, const int8_t *q, size_t a0, int na, size_t b0, int nb,
+                                              int in_dim) {
+  const int t = threadIdx.x, C = in_dim >> 4, n = (na + nb) * C, RS = in_dim + 4;
+  u32x4 v[PB];
+#pragma unroll
+  for (int j = 0; j < PB; j++) {
+    const int k = min(t + 256 * j, n - 1), r = k / C, c = k - r * C;
+    const size_t g = r < na ? a0 + r : b0 + (r - na);
+    v[j] = dsh_load_nt(q + g * in_dim + 16 * c);
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int j = 0; j < PB; j++) {
+    const int k = t + 256 * j, r = k / C, c = k - r * C;
+    if (k < n) {
+      float *d = s_rows + (size_t)r * RS + 16 * c;
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        float f0, f1, f2, f3;
+        dsh_u8x4_to_f32(v[j][w], f0, f1, f2, f3);
+        *(f32x4 *)(d + 4 * w) = f32x4{f0, f1, f2, f3};
+      }
+    }
+  }
+}
+
+// 16 steps of the chain (4 f32x4 of row values and inputs).
+__device__ __forceinline__ float mv_steps16(const f32x4 (&w)[4], const f32x4 (&x)[4], float dot) {
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    dot = __builtin_fmaf(w[k][0], x[k][0], dot);
+    dot = __builtin_fmaf(w[k][1], x[k][1], dot);
+    dot = __builtin_fmaf(w[k][2], x[k][2], dot);
+    dot = __builtin_fmaf(w[k][3], x[k][3], dot);
+  }
+  return dot;
+}
+
+__device__ __forceinline__ void mv_load16(const f32x4 *p, f32x4 (&v)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; k++) v[k] = p[k];
+}
+
+// Wave 0, lane l < nr: the chain of staged row l over s_x; wave 1 lane 0: xs into *s_xs. Returns dot.
+// The LDS reads of the next 16 steps go out before the current 16 run (two register sets), so the
+// chain waits only for its fused multiply-adds. in_dim % 16 == 0.
+__device__ __forceinline__ float mv_chain(const float *s_rows, const float *s_x, float *s_xs, int in_dim, int nr) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n16 = in_dim >> 4;
+  const f32x4 *x4 = (const f32x4 *)s_x;
+  float dot = 0.0f;
+  if (wave == 0 && lane < nr) {
+    const f32x4 *r4 = (const f32x4 *)(s_rows + (size_t)lane * (in_dim + 4));
+    f32x4 wa[4], xa[4], wb[4], xb[4];
+    mv_load16(r4, wa);
+    mv_load16(x4, xa);
+    int i = 0;
+    for (; i + 2 <= n16; i += 2) {  // the scheduling barriers keep each set's reads ahead of its use
+      mv_load16(r4 + 4 * (i + 1), wb);
+      mv_load16(x4 + 4 * (i + 1), xb);
+      __builtin_amdgcn_sched_barrier(0);
+      dot = mv_steps16(wa, xa, dot);
+      const int in = min(i + 2, n16 - 1);
+      mv_load16(r4 + 4 * in, wa);
+      mv_load16(x4 + 4 * in, xa);
+      __builtin_amdgcn_sched_barrier(0);
+      dot = mv_steps16(wb, xb, dot);
+    }
+    if (i < n16) dot = mv_steps16(wa, xa, dot);  // odd n16: the last 16
+  } else if (wave == 1 && lane == 0) {
+    f32x4 xa[4], xb[4];
+    mv_load16(x4, xa);
+    float xs = 0.0f;
+    int i = 0;
+    for (; i + 2 <= n16; i += 2) {
+      mv_load16(x4 + 4 * (i + 1), xb);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        xs += xa[k][0];
+        xs += xa[k][1];
+        xs += xa[k][2];
+        xs += xa[k][3];
+      }
+      mv_load16(x4 + 4 * min(i + 2, n16 - 1), xa);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        xs += xb[k][0];
+        xs += xb[k][1];
+        xs += xb[k][2];
+        xs += xb[k][3];
+      }
+    }
+    if (i < n16) {
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        xs += xa[k][0];
+        xs += xa[k][1];
+        xs += xa[k][2];
+        xs += xa[k][3];
+      }
+    }
+    *s_xs = xs;
+  }
+  return dot;
+}
+
+__global__ void __launch_bounds__(256) k_int8_mv_rows(const int8_t *__restrict__ q, const float *__restrict__ scale,
+                                                      const float *__restrict__ offset, const float *x,
+                                                      float *y, int in_dim, int row_start, int nrows) {
+  extern __shared__ __attribute__((aligned(16))) float mv_smem[];
+  float *s_rows = mv_smem, *s_x = mv_smem + (size_t)MV_RB * (in_dim + 4), *s_xs = s_x + in_dim;
+  const int t = threadIdx.x, lane = t & 63, r0 = blockIdx.x * MV_RB, nr = min(MV_RB, nrows - r0);
+  f32x4 xv[2];
+  const int NX = in_dim >> 2;
+#pragma unroll
+  for (int j = 0; j < 2; j++) xv[j] = ((const f32x4 *)x)[min(t + 256 * j, NX - 1)];
+  mv_stage_rows<MV_PB>(s_rows, q, (size_t)row_start + r0, nr, 0, 0, in_dim);
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+    if (t + 256 * j < NX) *(f32x4 *)(s_x + 4 * (t + 256 * j)) = xv[j];
+  __syncthreads();
+  const float dot = mv_chain(s_rows, s_x, s_xs, in_dim, nr);
+  __syncthreads();
+  if (t < nr) {
+    const int r = row_start + r0 + lane;
+    y[r0 + lane] = __builtin_fmaf(scale[r], dot, offset[r] * *s_xs);
+  }
+}
+
+// One expert of the per-function path (ds_expert_forward_fused_int4) in one launch. Gate blocks
+// (the first nG = I / 8) each take units i0 .. i0 + 7 (i0 = 8 b): gate rows i and up rows I + i (16
+// rows, staged as above), h_i = SwiGLU(gate_i, up_i) (bf16sim: inputs and h rounded to bf16, as
+// k_split_swiglu), written to hbuf as (epoch << 32 | bits of h_i) with one device-scope 64-bit
+// store each. Down blocks (16 output rows each) stage their rows, poll hbuf until every entry
+// carries this launch's epoch (the host's running count, different for every launch; a bounded wait
+// that sets *derr when it gives up) and run their rows over h (bf16sim: y rounded to bf16). Blocks
+// are dispatched in index order, so every gate block is running or done before a down block waits.
+// done (optional): down block d stores epoch to done[d] after its output rows (a system-scope
+// release store), so a host polling those words knows the outputs are there. xcache: when not NULL, gate block
+// 0 also writes x there (device memory) for a later call on the same input.
+__global__ void __launch_bounds__(256) k_expert_exact(const int8_t *__restrict__ gq, const float *__restrict__ gs,
+                                                      const float *__restrict__ go, const int8_t *__restrict__ dq,
+                                                      const float *__restrict__ dsc, const float *__restrict__ dof,
+                                                      const float *x, float *xcache,
+                                                      unsigned long long *hbuf, float *y, unsigned *done, int H,
+                                                      int I, int nG, unsigned epoch, int bf16sim, int spin,
+                                                      int *derr) {
+  extern __shared__ __attribute__((aligned(16))) float mv_smem[];
+  const int t = threadIdx.x, lane = t & 63, b = blockIdx.x;
+  const bool gate = b < nG;
+  const int in_dim = gate ? H : I;
+  float *s_rows = mv_smem, *s_x = mv_smem + (size_t)MV_RB * (in_dim + 4), *s_xs = s_x + in_dim;
+  __shared__ float s_g[MV_RB];
+  if (gate) {
+    const int i0 = 8 * b, NX = H >> 2;
+    f32x4 xv[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) xv[j] = ((const f32x4 *)x)[min(t + 256 * j, NX - 1)];
+    mv_stage_rows<MV_PB>(s_rows, gq, (size_t)i0, 8, (size_t)I + i0, 8, H);  // gate rows 0..7, up rows 8..15
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+      if (t + 256 * j < NX) {
+        *(f32x4 *)(s_x + 4 * (t + 256 * j)) = xv[j];
+        if (xcache && b == 0) *(f32x4 *)(xcache + 4 * (t + 256 * j)) = xv[j];
+      }
+    __syncthreads();
+    const float dot = mv_chain(s_rows, s_x, s_xs, H, MV_RB);
+    __syncthreads();
+    if (t < MV_RB) {
+      const int r = t < 8 ? i0 + t : I + i0 + (t - 8);
+      float v = __builtin_fmaf(gs[r], dot, go[r] * *s_xs);
+      if (bf16sim) v = dsh_bf16_round_half_up(v);
+      s_g[t] = v;
+    }
+    __syncthreads();
+    if (t < 8) {  // h out, each value with this launch's epoch
+      float hv = dsh_swiglu(s_g[t], s_g[8 + t]);
+      if (bf16sim) hv = dsh_bf16_round_half_up(hv);
+      __hip_atomic_store(hbuf + i0 + t, ((unsigned long long)epoch << 32) | __float_as_uint(hv), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
+  const int r0 = (b - nG) * MV_RB, nr = min(MV_RB, H - r0);
+  mv_stage_rows<MV_PB>(s_rows, dq, (size_t)r0, nr, 0, 0, I);
+  {  // h: poll this thread's entries (I <= 8 * 256 here) until every one of the block's carries the
+     // epoch; zeros when the wait gave up (the output is then reported invalid)
+    unsigned long long hv[8];
+    int ok = 0;
+    for (int n = 0; n < spin && !ok; n++) {
+      bool mine = true;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        hv[j] = __hip_atomic_load(hbuf + min(t + 256 * j, I - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        mine &= (unsigned)(hv[j] >> 32) == epoch;
+      }
+      ok = __syncthreads_and(mine);
+      if (!ok) __builtin_amdgcn_s_sleep(2);
+    }
+    if (!ok && t == 0 && derr) __hip_atomic_store(derr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      if (t + 256 * j < I) s_x[t + 256 * j] = ok ? __uint_as_float((unsigned)hv[j]) : 0.0f;
+  }
+  __syncthreads();
+  const float dot = mv_chain(s_rows, s_x, s_xs, I, nr);
+  __syncthreads();
+  if (t < 64) {
+    if (t < nr) {
+      const int r = r0 + lane;
+      const float v = __builtin_fmaf(dsc[r], dot, dof[r] * *s_xs);
+      y[r] = bf16sim ? dsh_bf16_round_half_up(v) : v;
+    }
+    if (done && t == 0) __hip_atomic_store(done + (b - nG), epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
 // ============================================================================ elementwise
 // ds_swiglu_direct (ds_kernels.c:1739-1789), fast-exp branch, for seq rows of inter.
 __global__ void k_swiglu(float *__restrict__ out, const float *__restrict__ g, const float *__restrict__ u, size_t n) {
@@ -191,18 +422,42 @@ __global__ void k_bf16_trunc(float *__restrict__ a, size_t n) {
     a[i] = dsh_bf16_round_half_up(a[i]);
 }
 
-__global__ void k_vec_add(float *__restrict__ dst, const float *__restrict__ a, const float *__restrict__ b, int n) {
+// done (optional): after the block's stores, thread 0 stores epoch to done[blockIdx.x] (system scope,
+// release), for a host that polls those words instead of synchronising.
+__device__ __forceinline__ void block_done(unsigned *done, unsigned epoch) {
+  if (!done) return;
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(done + blockIdx.x, epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__global__ void k_vec_add(float *__restrict__ dst, const float *__restrict__ a, const float *__restrict__ b, int n,
+                          unsigned *done, unsigned epoch) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) dst[i] = a[i] + b[i];
+  block_done(done, epoch);
 }
 
 // ds_expert_combine (ds_kernels.c:359-371): out = 0; out[i] = fma(w_k, e_k[i], out[i]) for k in order.
+// The expert outputs (which may sit in host memory) are loaded 8 at a time, all in flight at once;
+// the fused multiply-adds run in k order as before.
 __global__ void k_expert_combine(float *__restrict__ out, const float *__restrict__ eo, const float *__restrict__ w,
-                                 int top_k, int hidden) {
+                                 int top_k, int hidden, unsigned *done, unsigned epoch) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x) {
     float acc = 0.0f;
-    for (int k = 0; k < top_k; k++) acc = __builtin_fmaf(w[k], eo[(size_t)k * hidden + i], acc);
+    for (int k0 = 0; k0 < top_k; k0 += 8) {
+      float v[8], wk[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const int kk = min(k0 + k, top_k - 1);
+        v[k] = eo[(size_t)kk * hidden + i];
+        wk[k] = w[kk];
+      }
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+        if (k0 + k < top_k) acc = __builtin_fmaf(wk[k], v[k], acc);
+    }
     out[i] = acc;
   }
+  block_done(done, epoch);
 }
 
 // Split of a fused [2*inter] gate_up vector + optional truncation + SwiGLU (ds_quantize.c:308-318).
@@ -219,8 +474,23 @@ __global__ void k_split_swiglu(float *__restrict__ h, const float *__restrict__ 
 }
 
 // Stages x (in_dim floats) into LDS.
+// (x may sit in host memory: 16-byte loads, four per thread in flight at once when aligned.)
 __device__ __forceinline__ void stage_x(float *xs, const float *x, int in_dim) {
-  for (int i = threadIdx.x; i < in_dim; i += blockDim.x) xs[i] = x[i];
+  if ((in_dim & 3) == 0 && ((uintptr_t)x & 15) == 0) {
+    const int n4 = in_dim >> 2, nt = blockDim.x;
+    for (int base = 0; base < n4; base += 4 * nt) {
+      f32x4 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) v[j] = ((const f32x4 *)x)[min(base + (int)threadIdx.x + j * nt, n4 - 1)];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int i = base + threadIdx.x + j * nt;
+        if (i < n4) ((f32x4 *)xs)[i] = v[j];
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < in_dim; i += blockDim.x) xs[i] = x[i];
+  }
   __syncthreads();
 }
 
@@ -228,16 +498,19 @@ __device__ __forceinline__ void stage_x(float *xs, const float *x, int in_dim) {
 template <bool ALIGNED>
 __global__ void __launch_bounds__(256) k_bf16_matvec_avx(const uint16_t *__restrict__ W, const float *__restrict__ x,
                                                          const float *__restrict__ bias, float *__restrict__ y,
-                                                         int in_dim, int out_dim, int chunk) {
+                                                         int in_dim, int out_dim, int chunk, unsigned *done,
+                                                         unsigned epoch) {
   extern __shared__ float xs_lds[];
   stage_x(xs_lds, x, in_dim);
   const int L = threadIdx.x & 3;
   const int r = blockIdx.x * 64 + (threadIdx.x >> 2);
-  if (r >= out_dim) return;  // whole 4-lane groups exit together
-  int path = row_path(r, out_dim, chunk, false);
-  float v = avx_row<ALIGNED>(W + (size_t)r * in_dim, xs_lds, in_dim, L, path == DSH_ROW_SINGLE, true,
-                             bias ? bias[r] : 0.0f, path != DSH_ROW_GROUP4);
-  if (L == 0) y[r] = v;
+  if (r < out_dim) {  // whole 4-lane groups
+    int path = row_path(r, out_dim, chunk, false);
+    float v = avx_row<ALIGNED>(W + (size_t)r * in_dim, xs_lds, in_dim, L, path == DSH_ROW_SINGLE, true,
+                               bias ? bias[r] : 0.0f, path != DSH_ROW_GROUP4);
+    if (L == 0) y[r] = v;
+  }
+  block_done(done, epoch);
 }
 
 // Per-row logits in argmax order plus per-block (max, lowest index) candidates.
@@ -732,12 +1005,19 @@ hipError_t dsh_launch_dequantize(const int8_t *q, const float *scale, const floa
   return LAUNCH_CHECK();
 }
 
+static size_t mv_lds_host(int in_dim) { return ((size_t)MV_RB * (in_dim + 4) + (size_t)in_dim + 4) * 4; }
+
 hipError_t dsh_launch_int8_matvec_exact(const int8_t *q, const float *scale, const float *offset, const float *x,
                                         float *y, int in_dim, int row_start, int nrows, hipStream_t s) {
   if (nrows <= 0) return hipSuccess;
   const size_t lds = (size_t)in_dim * sizeof(float);
   if (in_dim <= 0 || lds > 64 * 1024) return hipErrorInvalidValue;
   const bool aligned = in_dim % 16 == 0 && ((uintptr_t)q & 15) == 0;
+  if (aligned && in_dim <= MV_MAX_DIM && ((uintptr_t)x & 15) == 0) {  // rows staged in LDS
+    k_int8_mv_rows<<<(nrows + MV_RB - 1) / MV_RB, 256, mv_lds_host(in_dim), s>>>(q, scale, offset, x, y, in_dim,
+                                                                               row_start, nrows);
+    return LAUNCH_CHECK();
+  }
   if (aligned)
     k_int8_matvec_chain<true><<<(nrows + 255) / 256, 256, lds, s>>>(q, scale, offset, x, y, in_dim, row_start, nrows);
   else
@@ -778,18 +1058,51 @@ hipError_t dsh_launch_bf16_trunc(float *a, size_t n, hipStream_t s) {
   return LAUNCH_CHECK();
 }
 
+int dsh_vec_add_blocks(int n) { return n <= 0 ? 0 : ((n + 255) / 256 > 4096 ? 4096 : (n + 255) / 256); }
+
 hipError_t dsh_launch_vec_add(float *dst, const float *a, const float *b, int n, hipStream_t s) {
+  return dsh_launch_vec_add_done(dst, a, b, n, NULL, 0, s);
+}
+
+hipError_t dsh_launch_vec_add_done(float *dst, const float *a, const float *b, int n, unsigned *done, unsigned epoch,
+                                   hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  int blocks = (n + 255) / 256;
-  if (blocks > 4096) blocks = 4096;
-  k_vec_add<<<blocks, 256, 0, s>>>(dst, a, b, n);
+  k_vec_add<<<dsh_vec_add_blocks(n), 256, 0, s>>>(dst, a, b, n, done, epoch);
   return LAUNCH_CHECK();
 }
 
+int dsh_expert_combine_blocks(int hidden) { return hidden <= 0 ? 0 : (hidden + 255) / 256; }
+
 hipError_t dsh_launch_expert_combine(float *out, const float *eo, const float *w, int top_k, int hidden,
                                      hipStream_t s) {
+  return dsh_launch_expert_combine_done(out, eo, w, top_k, hidden, NULL, 0, s);
+}
+
+hipError_t dsh_launch_expert_combine_done(float *out, const float *eo, const float *w, int top_k, int hidden,
+                                          unsigned *done, unsigned epoch, hipStream_t s) {
   if (hidden <= 0) return hipSuccess;
-  k_expert_combine<<<(hidden + 255) / 256, 256, 0, s>>>(out, eo, w, top_k, hidden);
+  k_expert_combine<<<dsh_expert_combine_blocks(hidden), 256, 0, s>>>(out, eo, w, top_k, hidden, done, epoch);
+  return LAUNCH_CHECK();
+}
+
+int dsh_expert_exact_down_blocks(int H) { return (H + MV_RB - 1) / MV_RB; }
+
+int dsh_expert_exact_blocks(int H, int I) {
+  if (H <= 0 || I <= 0 || H % 16 || I % 16 || H > MV_MAX_DIM || I > MV_MAX_DIM) return 0;
+  return I / 8 + (H + MV_RB - 1) / MV_RB;
+}
+
+hipError_t dsh_launch_expert_exact(const int8_t *gq, const float *gs, const float *go, const int8_t *dq, const float *dsc,
+                                   const float *dof, const float *x, float *xcache, unsigned long long *hbuf, float *y,
+                                   unsigned *done, int H, int I, unsigned epoch, int bf16sim, int spin, int *derr,
+                                   hipStream_t s) {
+  const int nb = dsh_expert_exact_blocks(H, I), nG = I / 8;
+  if (!nb || ((uintptr_t)gq & 15) || ((uintptr_t)dq & 15) || ((uintptr_t)x & 15) || ((uintptr_t)xcache & 15) ||
+      spin <= 0)
+    return hipErrorInvalidValue;
+  const size_t lds = mv_lds_host(H > I ? H : I);
+  k_expert_exact<<<nb, 256, lds, s>>>(gq, gs, go, dq, dsc, dof, x, xcache, hbuf, y, done, H, I, nG, epoch, bf16sim,
+                                      spin, derr);
   return LAUNCH_CHECK();
 }
 
@@ -803,15 +1116,22 @@ static bool bf16_aligned(const uint16_t *W, int in_dim) { return (in_dim % 8 == 
 
 hipError_t dsh_launch_bf16_matvec_avx(const uint16_t *W, const float *x, const float *bias, float *y, int in_dim,
                                       int out_dim, int nthreads, hipStream_t s) {
+  return dsh_launch_bf16_matvec_avx_done(W, x, bias, y, in_dim, out_dim, nthreads, NULL, 0, s);
+}
+
+int dsh_bf16_matvec_avx_blocks(int out_dim) { return out_dim <= 0 ? 0 : (out_dim + 63) / 64; }
+
+hipError_t dsh_launch_bf16_matvec_avx_done(const uint16_t *W, const float *x, const float *bias, float *y, int in_dim,
+                                           int out_dim, int nthreads, unsigned *done, unsigned epoch, hipStream_t s) {
   if (out_dim <= 0) return hipSuccess;
   size_t lds = (size_t)in_dim * sizeof(float);
   if (lds > 64 * 1024) return hipErrorInvalidValue;
   int blocks = (out_dim + 63) / 64;
   int chunk = dsh_chunk_len(out_dim, nthreads);
   if (bf16_aligned(W, in_dim))
-    k_bf16_matvec_avx<true><<<blocks, 256, lds, s>>>(W, x, bias, y, in_dim, out_dim, chunk);
+    k_bf16_matvec_avx<true><<<blocks, 256, lds, s>>>(W, x, bias, y, in_dim, out_dim, chunk, done, epoch);
   else
-    k_bf16_matvec_avx<false><<<blocks, 256, lds, s>>>(W, x, bias, y, in_dim, out_dim, chunk);
+    k_bf16_matvec_avx<false><<<blocks, 256, lds, s>>>(W, x, bias, y, in_dim, out_dim, chunk, done, epoch);
   return LAUNCH_CHECK();
 }
 

@@ -14,11 +14,26 @@ void ds_linear_nobias_bf16(float *y, const float *x, const uint16_t *W_bf16, int
   if (!y || !x || !W_bf16 || seq_len <= 0 || in_dim <= 0 || out_dim <= 0) return;
   const uint16_t *Wd = (const uint16_t *)dsr_weight_device(W_bf16, (size_t)out_dim * in_dim * 2);
   if (!Wd) return;
+  if (seq_len == 1) { /* the input and scores through pinned staging the kernel reads and writes */
+    const float *xp = (const float *)dsr_pin_in(DSR_PIN_X, x, F4(in_dim));
+    float *yp = (float *)dsr_pin_buf(DSR_PIN_Y, F4(out_dim));
+    const int nb = dsh_bf16_matvec_avx_blocks(out_dim);
+    unsigned *done = (unsigned *)dsr_pin_buf(DSR_PIN_DONE, sizeof(unsigned) * (size_t)nb);
+    if (!xp || !yp || !done) return;
+    const unsigned epoch = dsr_expert_epoch();
+    hipError_t e = dsh_launch_bf16_matvec_avx_done(Wd, xp, NULL, yp, in_dim, out_dim, dsr_threads(), done, epoch,
+                                                   dsr_stream);
+    if (e != hipSuccess) {
+      dsr_fail("ds_linear_nobias_bf16", e);
+      return;
+    }
+    dsr_pin_out_done(y, DSR_PIN_Y, F4(out_dim), nb, epoch);
+    return;
+  }
   float *xd = (float *)dsr_scratch(DSR_SLOT_X, F4((size_t)seq_len * in_dim));
   float *yd = (float *)dsr_scratch(DSR_SLOT_Y, F4((size_t)seq_len * out_dim));
   if (!xd || !yd || dsr_h2d(xd, x, F4((size_t)seq_len * in_dim))) return;
-  hipError_t e = seq_len == 1 ? dsh_launch_bf16_matvec_avx(Wd, xd, NULL, yd, in_dim, out_dim, dsr_threads(), dsr_stream)
-                              : dsh_launch_gemm_bf16w(xd, Wd, yd, seq_len, in_dim, out_dim, dsr_stream);
+  hipError_t e = dsh_launch_gemm_bf16w(xd, Wd, yd, seq_len, in_dim, out_dim, dsr_stream);
   if (e != hipSuccess) {
     dsr_fail("ds_linear_nobias_bf16", e);
     return;
@@ -46,14 +61,19 @@ void ds_bf16_matvec_pub(float *y, const float *x, const uint16_t *W_bf16, const 
 /* ds_kernels.c:1621-1642. */
 void ds_vec_add(float *dst, const float *a, const float *b, int n) {
   if (!dst || !a || !b || n <= 0) return;
-  float *ad = (float *)dsr_scratch(DSR_SLOT_A, F4(n)), *bd = (float *)dsr_scratch(DSR_SLOT_B, F4(n));
-  if (!ad || !bd || dsr_h2d(ad, a, F4(n)) || dsr_h2d(bd, b, F4(n))) return;
-  hipError_t e = dsh_launch_vec_add(ad, ad, bd, n, dsr_stream);
+  const float *ap = (const float *)dsr_pin_in(DSR_PIN_A, a, F4(n));
+  const float *bp = (const float *)dsr_pin_in(DSR_PIN_B, b, F4(n));
+  float *yp = (float *)dsr_pin_buf(DSR_PIN_Y, F4(n));
+  const int nb = dsh_vec_add_blocks(n);
+  unsigned *done = (unsigned *)dsr_pin_buf(DSR_PIN_DONE, sizeof(unsigned) * (size_t)nb);
+  if (!ap || !bp || !yp || !done) return;
+  const unsigned epoch = dsr_expert_epoch();
+  hipError_t e = dsh_launch_vec_add_done(yp, ap, bp, n, done, epoch, dsr_stream);
   if (e != hipSuccess) {
     dsr_fail("ds_vec_add", e);
     return;
   }
-  dsr_d2h(dst, ad, F4(n));
+  dsr_pin_out_done(dst, DSR_PIN_Y, F4(n), nb, epoch);
 }
 
 /* ds_kernels.c:1739-1789 (fast-exp branch): out[s*inter + j] = silu(g) * u. */
@@ -127,18 +147,19 @@ void ds_expert_combine(float *output, const float *expert_outputs, const int *to
                        int top_k, int hidden) {
   (void)top_indices;
   if (!output || !expert_outputs || !top_weights || top_k <= 0 || hidden <= 0) return;
-  float *eo = (float *)dsr_scratch(DSR_SLOT_A, F4((size_t)top_k * hidden));
-  float *wd = (float *)dsr_scratch(DSR_SLOT_B, F4(top_k));
-  float *od = (float *)dsr_scratch(DSR_SLOT_Y, F4(hidden));
-  if (!eo || !wd || !od || dsr_h2d(eo, expert_outputs, F4((size_t)top_k * hidden)) ||
-      dsr_h2d(wd, top_weights, F4(top_k)))
-    return;
-  hipError_t e = dsh_launch_expert_combine(od, eo, wd, top_k, hidden, dsr_stream);
+  const float *eo = (const float *)dsr_pin_in(DSR_PIN_A, expert_outputs, F4((size_t)top_k * hidden));
+  const float *wd = (const float *)dsr_pin_in(DSR_PIN_B, top_weights, F4(top_k));
+  float *od = (float *)dsr_pin_buf(DSR_PIN_Y, F4(hidden));
+  const int nb = dsh_expert_combine_blocks(hidden);
+  unsigned *done = (unsigned *)dsr_pin_buf(DSR_PIN_DONE, sizeof(unsigned) * (size_t)nb);
+  if (!eo || !wd || !od || !done) return;
+  const unsigned epoch = dsr_expert_epoch();
+  hipError_t e = dsh_launch_expert_combine_done(od, eo, wd, top_k, hidden, done, epoch, dsr_stream);
   if (e != hipSuccess) {
     dsr_fail("ds_expert_combine", e);
     return;
   }
-  dsr_d2h(output, od, F4(hidden));
+  dsr_pin_out_done(output, DSR_PIN_Y, F4(hidden), nb, epoch);
 }
 
 /* ds_kernels.c:322-357: BF16 fused expert; both matvecs in the AVX-512 order. */

@@ -123,12 +123,12 @@ static hipError_t int8_mv(const dsr_dblock_t *db, const float *xd, float *yd, in
 static int matvec_dev(float *y, const float *x, const ds_int4_block_t *block, int row_start, int nrows) {
   dsr_dblock_t db;
   if (dsr_block_device(block, &db)) return -1;
-  float *xd = (float *)dsr_scratch(DSR_SLOT_X, (size_t)block->in_dim * 4);
-  float *yd = (float *)dsr_scratch(DSR_SLOT_Y, (size_t)nrows * 4);
-  if (!xd || !yd || dsr_h2d(xd, x, (size_t)block->in_dim * 4)) return -1;
-  hipError_t e = int8_mv(&db, xd, yd, block->in_dim, row_start, nrows);
+  const float *xp = (const float *)dsr_pin_in(DSR_PIN_X, x, (size_t)block->in_dim * 4);
+  float *yp = (float *)dsr_pin_buf(DSR_PIN_Y, (size_t)nrows * 4);
+  if (!xp || !yp) return -1;
+  hipError_t e = int8_mv(&db, xp, yp, block->in_dim, row_start, nrows);
   if (e != hipSuccess) return dsr_fail("int8 matvec kernel", e);
-  return dsr_d2h(y, yd, (size_t)nrows * 4);
+  return dsr_pin_out(y, DSR_PIN_Y, (size_t)nrows * 4);
 }
 
 /* ds_quantize.c:260-274. */
@@ -167,11 +167,43 @@ void ds_expert_forward_fused_int4(float *out, const float *x, const ds_int4_bloc
   dsr_dblock_t g, d;
   if (dsr_block_device(gate_up_int4, &g) || dsr_block_device(down_int4, &d)) return;
   int bf16sim = ds_bf16_simulate_python;
-  float *xd = (float *)dsr_scratch(DSR_SLOT_X, (size_t)hidden * 4);
+  if (dsh_expert_exact_blocks(hidden, intermediate)) {
+    /* one launch (gate_up, SwiGLU, down) writing out to pinned staging; x from pinned staging, or from
+     * the device copy the previous call left when x is the same input (the routed experts and the
+     * shared expert of a layer share it) */
+    const size_t xb = (size_t)hidden * 4;
+    float *xc = (float *)dsr_scratch(DSR_SLOT_XC, xb);
+    unsigned long long *hb = (unsigned long long *)dsr_expert_hbuf((size_t)intermediate);
+    float *op = (float *)dsr_pin_buf(DSR_PIN_Y, xb);
+    if (!xc || !hb || !op) return;
+    const float *xsrc = xc;
+    float *xcache = NULL;
+    if (!dsr_input_cached(x, xb)) {
+      xsrc = (const float *)dsr_pin_in(DSR_PIN_X, x, xb);
+      xcache = xc;
+      if (!xsrc) return;
+    }
+    const int nd = dsh_expert_exact_down_blocks(hidden);
+    unsigned *done = (unsigned *)dsr_pin_buf(DSR_PIN_DONE, sizeof(unsigned) * (size_t)nd);
+    if (!done) return;
+    const unsigned epoch = dsr_expert_epoch();
+    hipError_t e = dsh_launch_expert_exact(g.q, g.scale, g.offset, d.q, d.scale, d.offset, xsrc, xcache, hb, op, done,
+                                           hidden, intermediate, epoch, bf16sim, 1 << 22,
+                                           dsr_derr_dev(DSR_DERR_EXPERT_WAIT), dsr_stream);
+    if (e != hipSuccess) {
+      dsr_input_forget();
+      dsr_fail("expert kernel", e);
+      return;
+    }
+    if (dsr_pin_out_done(out, DSR_PIN_Y, xb, nd, epoch) || dsr_derr_check()) dsr_input_forget();
+    return;
+  }
   float *gu = (float *)dsr_scratch(DSR_SLOT_A, (size_t)2 * intermediate * 4);
+  if (!gu) return;
+  float *xd = (float *)dsr_scratch(DSR_SLOT_X, (size_t)hidden * 4);
   float *hd = (float *)dsr_scratch(DSR_SLOT_B, (size_t)intermediate * 4);
   float *od = (float *)dsr_scratch(DSR_SLOT_Y, (size_t)hidden * 4);
-  if (!xd || !gu || !hd || !od || dsr_h2d(xd, x, (size_t)hidden * 4)) return;
+  if (!xd || !hd || !od || dsr_h2d(xd, x, (size_t)hidden * 4)) return;
   hipError_t e = int8_mv(&g, xd, gu, hidden, 0, 2 * intermediate);
   if (e == hipSuccess) e = dsh_launch_split_swiglu(hd, gu, intermediate, bf16sim, dsr_stream);
   if (e == hipSuccess) e = int8_mv(&d, hd, od, intermediate, 0, hidden);

@@ -30,7 +30,7 @@ int dsr_failf(const char *fmt, ...);
  * dsr_init). dsr_derr_check() reports (and clears) any word that is set: -1 with ds_hip_last_error
  * naming the failure, else 0. It runs after every synchronisation the library API offers
  * (ds_hip_sync) and at the entry of the calls whose results such a failure voids. */
-enum { DSR_DERR_PREFILL_WAIT, DSR_DERR_ROUTE_WAIT, DSR_DERR_N };
+enum { DSR_DERR_PREFILL_WAIT, DSR_DERR_ROUTE_WAIT, DSR_DERR_EXPERT_WAIT, DSR_DERR_N };
 int *dsr_derr_dev(int kind);
 int dsr_derr_check(void);
 
@@ -39,8 +39,33 @@ int dsr_derr_check(void);
 dsh_rcert_t dsr_rcert(int tag);
 
 /* Grow-only device staging buffer per slot (not thread-safe, like the reference API). */
-enum { DSR_SLOT_X, DSR_SLOT_Y, DSR_SLOT_A, DSR_SLOT_B, DSR_SLOT_C, DSR_SLOT_D, DSR_SLOT_IDX, DSR_SLOT_PF, DSR_NSLOTS };
+enum { DSR_SLOT_X, DSR_SLOT_Y, DSR_SLOT_A, DSR_SLOT_B, DSR_SLOT_C, DSR_SLOT_D, DSR_SLOT_IDX, DSR_SLOT_PF, DSR_SLOT_XC, DSR_NSLOTS };
 void *dsr_scratch(int slot, size_t bytes);
+
+/* The per-function path's one-launch expert kernels: the device buffer of epoch-tagged h words (at
+ * least n 64-bit words, zeroed when it is allocated). dsr_expert_epoch: the next launch epoch (never
+ * 0; a new one per launch), also for the completion words of DSR_PIN_DONE. */
+void *dsr_expert_hbuf(size_t n);
+unsigned dsr_expert_epoch(void);
+/* Whether the expert kernel's device copy of its input (DSR_SLOT_XC) holds these n bytes of host
+ * input from the previous call (compared by content); if not, remembers them as the copy the coming
+ * launch writes. dsr_input_forget() drops the record (any other use of the slot, a failed launch). */
+int dsr_input_cached(const void *x, size_t n);
+void dsr_input_forget(void);
+
+/* Pinned, mapped host staging per slot that kernels read and write directly (the per-function API's
+ * activations: a call copies its host inputs in, launches, synchronises and copies its outputs out,
+ * with no copy commands). dsr_pin_in copies n bytes of src into the slot and returns the device
+ * address; dsr_pin_buf returns a slot's device address (and its host address in *host); dsr_pin_out
+ * synchronises the stream and copies n bytes of a slot out. Grow-only, not thread-safe. */
+enum { DSR_PIN_X, DSR_PIN_A, DSR_PIN_B, DSR_PIN_Y, DSR_PIN_DONE, DSR_NPIN };
+const void *dsr_pin_in(int slot, const void *src, size_t n);
+void *dsr_pin_buf(int slot, size_t n);
+int dsr_pin_out(void *dst, int slot, size_t n);
+/* Like dsr_pin_out, for a launch whose blocks store epoch into the n_words completion words of
+ * DSR_PIN_DONE when their outputs are written: polls those words instead of synchronising the
+ * stream (after about a second without them, synchronises and reports failure). */
+int dsr_pin_out_done(void *dst, int slot, size_t n, int n_words, unsigned epoch);
 
 int dsr_h2d(void *dst, const void *src, size_t n);
 int dsr_d2h(void *dst, const void *src, size_t n); /* synchronises the stream */

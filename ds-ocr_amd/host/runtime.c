@@ -2,11 +2,13 @@
  * registry of libds_ocr_hip. The registry plays the role of the Metal backend's
  * ds_metal_register_expert_block (reference ds_metal.m:244-258): weights are uploaded once and
  * stay resident. */
+#define _GNU_SOURCE
 #include <pthread.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 #include <unistd.h>
 
 #include "dsr.h"
@@ -81,6 +83,7 @@ int dsr_derr_check(void) {
       "prefill: a down tile's bounded wait for its gate_up tiles gave up; that call's output is not valid",
       "decode: a certified layer's bounded wait for its verdict on the expert selection gave up; the "
       "step's output is not valid",
+      "expert: the down rows' bounded wait for the gate_up rows' h gave up; that call's output is not valid",
   };
   if (!g_derr_host) return 0;
   int rc = 0;
@@ -92,6 +95,55 @@ int dsr_derr_check(void) {
   }
   return rc;
 }
+
+static void *g_hbuf = NULL;
+static size_t g_hbuf_n = 0;
+static unsigned g_epoch = 0;
+
+void *dsr_expert_hbuf(size_t n) {
+  if (n <= g_hbuf_n) return g_hbuf;
+  if (g_hbuf) {
+    hipStreamSynchronize(dsr_stream);
+    hipFree(g_hbuf);
+    g_hbuf = NULL;
+    g_hbuf_n = 0;
+  }
+  const size_t cap = n < 4096 ? 4096 : n;
+  if (hipMalloc(&g_hbuf, cap * 8) != hipSuccess || hipMemset(g_hbuf, 0, cap * 8) != hipSuccess) {
+    dsr_failf("expert h buffer allocation failed");
+    if (g_hbuf) hipFree(g_hbuf);
+    g_hbuf = NULL;
+    return NULL;
+  }
+  g_hbuf_n = cap;
+  return g_hbuf;
+}
+
+unsigned dsr_expert_epoch(void) {
+  if (++g_epoch == 0) g_epoch = 1;
+  return g_epoch;
+}
+
+static unsigned char *g_xin = NULL;
+static size_t g_xin_n = 0, g_xin_cap = 0;
+static int g_xin_valid = 0;
+
+int dsr_input_cached(const void *x, size_t n) {
+  if (g_xin_valid && n == g_xin_n && memcmp(g_xin, x, n) == 0) return 1;
+  if (n > g_xin_cap) {
+    free(g_xin);
+    g_xin = (unsigned char *)malloc(n);
+    g_xin_cap = g_xin ? n : 0;
+  }
+  g_xin_valid = g_xin != NULL;
+  if (g_xin_valid) {
+    memcpy(g_xin, x, n);
+    g_xin_n = n;
+  }
+  return 0;
+}
+
+void dsr_input_forget(void) { g_xin_valid = 0; }
 
 int dsr_init(void) {
   if (g_init == 1) return 0;
@@ -163,6 +215,64 @@ void *dsr_scratch(int slot, size_t bytes) {
   return p;
 }
 
+static void *g_pin_host[DSR_NPIN], *g_pin_dev[DSR_NPIN];
+static size_t g_pin_cap[DSR_NPIN];
+
+static int pin_reserve(int slot, size_t n) {
+  if (slot < 0 || slot >= DSR_NPIN) return dsr_failf("pinned staging: bad slot");
+  if (n <= g_pin_cap[slot]) return 0;
+  if (g_pin_host[slot]) {
+    hipStreamSynchronize(dsr_stream);
+    hipHostFree(g_pin_host[slot]);
+    g_pin_host[slot] = g_pin_dev[slot] = NULL;
+    g_pin_cap[slot] = 0;
+  }
+  const size_t cap = n < 65536 ? 65536 : n + n / 4;
+  void *h = NULL, *d = NULL;
+  DSR_TRY(hipHostMalloc(&h, cap, hipHostMallocMapped | hipHostMallocCoherent), "pinned staging");
+  if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess) {
+    hipHostFree(h);
+    return dsr_failf("pinned staging: no device address");
+  }
+  g_pin_host[slot] = h;
+  g_pin_dev[slot] = d;
+  g_pin_cap[slot] = cap;
+  return 0;
+}
+
+const void *dsr_pin_in(int slot, const void *src, size_t n) {
+  if (pin_reserve(slot, n ? n : 16)) return NULL;
+  if (n) memcpy(g_pin_host[slot], src, n);
+  return g_pin_dev[slot];
+}
+
+void *dsr_pin_buf(int slot, size_t n) { return pin_reserve(slot, n ? n : 16) ? NULL : g_pin_dev[slot]; }
+
+int dsr_pin_out(void *dst, int slot, size_t n) {
+  DSR_TRY(hipStreamSynchronize(dsr_stream), "stream synchronize");
+  if (n) memcpy(dst, g_pin_host[slot], n);
+  return 0;
+}
+
+int dsr_pin_out_done(void *dst, int slot, size_t n, int n_words, unsigned epoch) {
+  const volatile unsigned *w = (const volatile unsigned *)g_pin_host[DSR_PIN_DONE];
+  struct timespec t0, t1;
+  clock_gettime(CLOCK_MONOTONIC, &t0);
+  for (int i = 0; i < n_words;) {
+    if (__atomic_load_n(&w[i], __ATOMIC_ACQUIRE) == epoch) {
+      i++;
+      continue;
+    }
+    clock_gettime(CLOCK_MONOTONIC, &t1);
+    if (t1.tv_sec - t0.tv_sec > 1) { /* not done: the launch failed or stalls; let the stream say why */
+      DSR_TRY(hipStreamSynchronize(dsr_stream), "stream synchronize");
+      return dsr_failf("a kernel did not report completion");
+    }
+  }
+  if (n) memcpy(dst, g_pin_host[slot], n);
+  return 0;
+}
+
 int dsr_h2d(void *dst, const void *src, size_t n) {
   if (n == 0) return 0;
   DSR_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, dsr_stream), "copy to device");
@@ -177,20 +287,34 @@ int dsr_d2h(void *dst, const void *src, size_t n) {
 
 /* ---------------------------------------------------------------- registry */
 
+/* 64-bit mixing hash, eight bytes per step (the tail zero-padded, the length mixed in). */
+static uint64_t mix64(uint64_t h, uint64_t v) {
+  h = (h ^ v) * 0x9E3779B97F4A7C15ull;
+  return h ^ (h >> 29);
+}
+
 static uint64_t fnv(uint64_t h, const void *p, size_t n) {
   const unsigned char *b = (const unsigned char *)p;
-  for (size_t i = 0; i < n; i++) h = (h ^ b[i]) * 1099511628211ull;
-  return h;
+  size_t i = 0;
+  for (; i + 8 <= n; i += 8) {
+    uint64_t v;
+    memcpy(&v, b + i, 8);
+    h = mix64(h, v);
+  }
+  uint64_t t = 0;
+  memcpy(&t, b + i, n - i);
+  return mix64(h, t ^ ((uint64_t)n << 56));
 }
 
 /* Weights are registered once: a host array is keyed by its address and size, like the reference's
  * read-only mmap'd weights and INT8 blocks that are never rewritten (ds_ocr.c:611-622; the Metal
  * backend registers expert blocks the same way, ds_metal.m:244-258). To notice a new array placed at
- * a freed one's address, each key also keeps a sampled fingerprint: 16 windows of 256 bytes spread
- * evenly over the array (the whole array when it is at most 4 KiB), about 4 KiB read per call
- * whatever the size. A caller that edits registered weights in place calls ds_hip_weights_changed. */
+ * a freed one's address, each key also keeps a sampled fingerprint: 16 windows of 64 bytes spread
+ * evenly over the array (the whole array when it is at most 1 KiB), about 1 KiB read per call
+ * whatever the size, hashed eight bytes at a time. Keys are found through a hash index on the
+ * address. A caller that edits registered weights in place calls ds_hip_weights_changed. */
 #define FP_WINDOWS 16
-#define FP_WINDOW 256
+#define FP_WINDOW 64
 
 static uint64_t fingerprint(const void *p, size_t n) {
   const unsigned char *b = (const unsigned char *)p;
@@ -214,11 +338,32 @@ typedef struct {
 
 static entry_t *g_ent = NULL;
 static int g_nent = 0, g_cap = 0;
+/* open-addressing index: slot -> entry index + 1 (0: empty), 4 slots per entry of capacity */
+static int *g_idx = NULL;
+static size_t g_idx_n = 0;
+
+static size_t idx_slot(const void *key, int is_block) {
+  return (size_t)(mix64((uint64_t)(uintptr_t)key, (uint64_t)is_block) & (g_idx_n - 1));
+}
+
+static void idx_insert(int i) {
+  size_t s = idx_slot(g_ent[i].key, g_ent[i].is_block);
+  while (g_idx[s]) s = (s + 1) & (g_idx_n - 1);
+  g_idx[s] = i + 1;
+}
+
+static void idx_rebuild(void) {
+  memset(g_idx, 0, g_idx_n * sizeof(int));
+  for (int i = 0; i < g_nent; i++) idx_insert(i);
+}
 
 static entry_t *find(const void *key, int is_block) {
-  for (int i = 0; i < g_nent; i++)
+  if (!g_idx) return NULL;
+  for (size_t s = idx_slot(key, is_block);; s = (s + 1) & (g_idx_n - 1)) {
+    const int i = g_idx[s] - 1;
+    if (i < 0) return NULL;
     if (g_ent[i].key == key && g_ent[i].is_block == is_block) return &g_ent[i];
-  return NULL;
+  }
 }
 
 static void drop(entry_t *e) {
@@ -226,20 +371,33 @@ static void drop(entry_t *e) {
   if (e->dev) hipFree(e->dev);
   if (e->aux) hipFree(e->aux);
   *e = g_ent[--g_nent];
+  idx_rebuild();
 }
 
+/* A new zeroed entry; the caller sets key and is_block, then calls add_done. */
 static entry_t *add(void) {
   if (g_nent == g_cap) {
     int nc = g_cap ? 2 * g_cap : 64;
     entry_t *ne = (entry_t *)realloc(g_ent, (size_t)nc * sizeof(entry_t));
-    if (!ne) return NULL;
+    int *ni = (int *)calloc((size_t)nc * 4, sizeof(int));
+    if (!ne || !ni) {
+      if (ne) g_ent = ne;
+      free(ni);
+      return NULL;
+    }
     g_ent = ne;
     g_cap = nc;
+    free(g_idx);
+    g_idx = ni;
+    g_idx_n = (size_t)nc * 4;
+    idx_rebuild();
   }
   entry_t *e = &g_ent[g_nent++];
   memset(e, 0, sizeof *e);
   return e;
 }
+
+static void add_done(entry_t *e) { idx_insert((int)(e - g_ent)); }
 
 static uint64_t block_fp(const ds_int4_block_t *b) {
   size_t nq = (size_t)b->out_dim * b->in_dim;
@@ -283,6 +441,7 @@ int dsr_block_device(const ds_int4_block_t *b, dsr_dblock_t *out) {
     }
     e->key = b->qweight;
     e->fp = fp;
+    add_done(e);
     if (dsr_h2d(e->dev, b->qweight, (size_t)b->out_dim * b->in_dim) ||
         dsr_h2d(e->sdev, b->scale, (size_t)b->out_dim * 4) || dsr_h2d(e->odev, b->offset, (size_t)b->out_dim * 4)) {
       drop(e);
@@ -309,6 +468,7 @@ int dsr_block_new(const ds_int4_block_t *b, dsr_dblock_t *out) {
     return -1;
   }
   e->key = b->qweight;
+  add_done(e);
   out->q = (int8_t *)e->dev;
   out->scale = e->sdev;
   out->offset = e->odev;
@@ -398,6 +558,7 @@ const void *dsr_weight_device(const void *host, size_t bytes) {
   e->fp = fp;
   e->bytes = bytes;
   e->dev = p;
+  add_done(e);
   if (dsr_h2d(p, host, bytes)) {
     drop(e);
     return NULL;
