@@ -14,8 +14,10 @@
 // scale·Σq·a + (offset + 128·scale)·Σa, with Σa of the f32 values.
 //
 // Kernels (one launch each, all sizes fixed by T, so a graph can hold them):
-//   k_pf_scores  router scores in the decode path's order, as four partial sums per token
-//   k_pf_select  per token: x → the two int8 limbs and their scale, Σx; expert selection → idx, w
+//   k_pf_route_cfg  CFG: per token, the router scores in ds_linear's order, x → the two int8 limbs
+//                and their scale, Σx; expert selection → idx, w
+//   k_pf_scores_bf16, k_pf_select_dec  DECODE: the bf16 router's scores in the reference's AVX-512
+//                order, then the limbs and the selection
 //   k_pf_plan    expert-sorted (token, slot) pairs (stable: tokens in increasing order per expert),
 //                per-expert offsets and the GEMM work items (expert, up-to-PF_MT-row chunk)
 //   k_pf_gate_up grouped GEMM + SwiGLU → h as limbs, its per-(row, n-tile) sums and maxima, for
@@ -24,7 +26,6 @@
 //   k_pf_moe     both GEMMs in one launch (per-XCD work queues), in place of the two above
 //   k_pf_combine out[t] = (residual ? x : 0) + (Σ_k w_k·Y_k in ascending expert order + Y_shared)
 #include "dsh_avx.h"
-#include "dsh_cert.h"
 #include "dsh_route.h"
 #include "k_core.h"
 #include <type_traits>
@@ -72,95 +73,221 @@ struct pf_item {
 };
 
 // ---------------------------------------------------------------------------------- routing
-// Router scores in the decode path's order, kept as four partial sums per token and expert:
-// ps[t][v][e] = Σ_jb p[v·P + jb] added sequentially from 0 (P = ceil(NB / 4), NB = H / R partials),
-// where p[b] = Σ_j WrT[R·b+j][e]·x[R·b+j] is a chain of fused multiply-adds over j (the decode path's
-// partials and per-wave sums, wave v taking the contiguous partials v·P ..); k_pf_select adds them
-// as ((ps0 + ps1) + ps2) + ps3 (route_select). pl[t][v][e] = Σ_jb |running sum before p[v·P + jb]|,
-// the prefix sizes that bound the rounding against ds_linear's order (dsh_cert.h).
-// CFG (f32 router): block = (PF_SC_TOK tokens, quarter v); the quarter's router rows and the tokens'
-// matching x values are staged in LDS PF_SC_JB partials at a time; wave w runs tokens 4w..4w+3,
-// lane = expert.
-#define PF_SC_TOK 16
-#define PF_SC_JB 20
-template <int R>
-__global__ void __launch_bounds__(256) k_pf_scores_cfg(const float *__restrict__ WrT, const float *__restrict__ X,
-                                                       int T, int H, int E, float *__restrict__ ps,
-                                                       float *__restrict__ pl) {
-  __shared__ __attribute__((aligned(16))) float wv[PF_SC_JB][R][64];
-  __shared__ __attribute__((aligned(16))) float xv[PF_SC_TOK][PF_SC_JB][R];
-  constexpr int NW = PF_SC_JB * R * 64 / 256;            // router values per thread per pass
-  constexpr int NX = PF_SC_TOK * PF_SC_JB * (R / 4);      // x float4s per pass
-  constexpr int NXT = (NX + 255) / 256;
-  const int v = blockIdx.y, t0 = blockIdx.x * PF_SC_TOK;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int NB = H / R, P = (NB + 3) / 4, bq = v * P;
-  const int nbv = max(0, min(P, NB - bq));
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, lam[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int jb0 = 0; jb0 < nbv; jb0 += PF_SC_JB) {
-    const int nj = min(PF_SC_JB, nbv - jb0);
-    // every load of the pass in flight at once (partials past the last repeat it, unused)
-    float wr_[NW];
-    f32x4 xr_[NXT];
+// One token's x as two int8 limbs (X0 low, X1 high) with their scale 2^(e-15) and Σx, for the
+// GEMM's activations: one wave, lane-strided float4s (H <= 256·PF_SEL_U, the whole row in
+// registers). xrow (optional, LDS) receives the row itself. Stores only when own.
+#define PF_SEL_U 8  // x float4 loads per lane
+__device__ __forceinline__ void pf_x_limbs(const float *__restrict__ X, int t, int H, bool own, int8_t *X0, int8_t *X1,
+                                           float *xsc, float *xsum, float *xrow) {
+  const int lane = threadIdx.x & 63;
+  const f32x4 *src = (const f32x4 *)(X + (size_t)t * H);
+  const int nc = H / 4;
+  f32x4 xv[PF_SEL_U];
 #pragma unroll
-    for (int k = 0; k < NW; k++) {
-      const int i = threadIdx.x + 256 * k;
-      const int row = i >> 6, e = i & 63;
-      const int jj = row / R, j = row - jj * R;
-      const int b = bq + min(jb0 + jj, max(nbv - 1, 0));
-      const float val = WrT[(size_t)(R * b + j) * E + min(e, E - 1)];  // branch-free load
-      wr_[k] = e < E ? val : 0.0f;
-    }
+  for (int u = 0; u < PF_SEL_U; u++) xv[u] = src[min(64 * u + lane, nc - 1)];
+  float s = 0.0f, mx = 0.0f;
 #pragma unroll
-    for (int k = 0; k < NXT; k++) {
-      const int i = min((int)threadIdx.x + 256 * k, NX - 1);
-      const int tb = i / (PF_SC_JB * (R / 4)), rem = i - tb * (PF_SC_JB * (R / 4));
-      const int jj = rem / (R / 4), q = rem - jj * (R / 4);
-      const int t = min(t0 + tb, T - 1);
-      const int b = bq + min(jb0 + jj, max(nbv - 1, 0));
-      xr_[k] = *(const f32x4 *)(X + (size_t)t * H + R * b + 4 * q);
-    }
-    __syncthreads();  // the previous pass's reads are done
-#pragma unroll
-    for (int k = 0; k < NW; k++) {
-      const int i = threadIdx.x + 256 * k;
-      (&wv[0][0][0])[i] = wr_[k];
-    }
-#pragma unroll
-    for (int k = 0; k < NXT; k++) {
-      const int i = threadIdx.x + 256 * k;
-      if (i < NX) ((f32x4 *)&xv[0][0][0])[i] = xr_[k];
-    }
-    __syncthreads();
-    for (int jj = 0; jj < nj; jj++) {
-      float wr[R];
-#pragma unroll
-      for (int j = 0; j < R; j++) wr[j] = wv[jj][j][lane];
-#pragma unroll
-      for (int tk = 0; tk < 4; tk++) {
-        const f32x4 *x4 = (const f32x4 *)xv[4 * wave + tk][jj];
-        float p = 0.0f;
-#pragma unroll
-        for (int q = 0; q < R / 4; q++) {
-          const f32x4 xq = x4[q];
-#pragma unroll
-          for (int i = 0; i < 4; i++) p = __builtin_fmaf(wr[4 * q + i], xq[i], p);
-        }
-        lam[tk] += fabsf(acc[tk]);
-        acc[tk] += p;
-      }
-    }
+  for (int u = 0; u < PF_SEL_U; u++) {
+    if (64 * u + lane >= nc) continue;
+    const f32x4 v = xv[u];
+    if (xrow) *(f32x4 *)(xrow + 4 * (64 * u + lane)) = v;
+    s += (v[0] + v[1]) + (v[2] + v[3]);
+    mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v[0]), fabsf(v[1]))), fmaxf(fabsf(v[2]), fabsf(v[3])));
   }
+  s = dsh_wave_sum(s);
+  mx = dsh_wave_max(mx);
+  if (!own) return;
+  const int ex = __builtin_amdgcn_frexp_expf(mx * 1.0078125f);  // 2^ex > max|x|·(1 + 2^-7)
 #pragma unroll
-  for (int tk = 0; tk < 4; tk++) {
-    const int t = t0 + 4 * wave + tk;
-    if (t < T) {
-      ps[((size_t)t * 4 + v) * 64 + lane] = lane < E ? acc[tk] : 0.0f;
-      pl[((size_t)t * 4 + v) * 64 + lane] = lane < E ? lam[tk] : 0.0f;
+  for (int u = 0; u < PF_SEL_U; u++) {
+    const int c = 64 * u + lane;
+    if (c >= nc) continue;
+    unsigned w0 = 0u, w1 = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int q = (int)__builtin_rintf(__builtin_ldexpf(xv[u][i], 15 - ex));  // |q| < 2^15 / (1 + 2^-7)
+      const int lo = __builtin_amdgcn_sbfe(q, 0, 8);                            // balanced low digit
+      const int hi = (q - lo) >> 8;                                              // |hi| <= 127
+      w0 |= ((unsigned)lo & 255u) << (8 * i);
+      w1 |= ((unsigned)hi & 255u) << (8 * i);
     }
+    *(unsigned *)(X0 + (size_t)t * H + 4 * c) = w0;
+    *(unsigned *)(X1 + (size_t)t * H + 4 * c) = w1;
+  }
+  if (lane == 0) {
+    xsum[t] = s;
+    xsc[t] = __builtin_ldexpf(1.0f, ex - 15);
   }
 }
 
+// CFG (f32 router: ds_moe_router → ds_linear_nobias → ds_linear, ds_kernels.c:181-185, :639-652):
+// every score in ds_linear's own order, so the selection is ds_moe_top_k's (:193-243) by
+// construction. ds_linear (no BLAS, seq 1, as GCC 11 compiles it) adds the rounded products
+// fl(x_k·w_ek) in index order from 0; the tail past the last multiple of 8 (16 when H >= 16) would be
+// fused, and H is a multiple of 256 here, so there is none. One wave per token, lane = expert: each
+// lane runs its own chain of H dependent adds, all T·E chains at once (one chain's latency for the
+// whole batch). The block's 4 tokens share the transposed router rows [H][E], staged in LDS
+// PF_RC_KC rows at a time with row stride 64 (double-buffered: the next chunk's loads are in flight
+// during the current chunk's chain, one barrier per chunk); each token's x stays in LDS, read as a
+// broadcast. The wave also writes its token's x limbs (pf_x_limbs), then selects and weights the
+// experts (route_select: top-k with strict >, softmax over the k).
+// Lane j of each row of 16 lanes, to every lane of the row (DPP row_newbcast:j); j must fold to a
+// constant (unrolled loops).
+template <int J>
+__device__ __forceinline__ float pf_row_bcast_c(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + J, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float pf_row_bcast(float v, int j) {
+  switch (j) {
+    case 0: return pf_row_bcast_c<0>(v);
+    case 1: return pf_row_bcast_c<1>(v);
+    case 2: return pf_row_bcast_c<2>(v);
+    case 3: return pf_row_bcast_c<3>(v);
+    case 4: return pf_row_bcast_c<4>(v);
+    case 5: return pf_row_bcast_c<5>(v);
+    case 6: return pf_row_bcast_c<6>(v);
+    case 7: return pf_row_bcast_c<7>(v);
+    case 8: return pf_row_bcast_c<8>(v);
+    case 9: return pf_row_bcast_c<9>(v);
+    case 10: return pf_row_bcast_c<10>(v);
+    case 11: return pf_row_bcast_c<11>(v);
+    case 12: return pf_row_bcast_c<12>(v);
+    case 13: return pf_row_bcast_c<13>(v);
+    case 14: return pf_row_bcast_c<14>(v);
+    default: return pf_row_bcast_c<15>(v);
+  }
+}
+
+#define PF_RC_KC 128
+#define PF_RC_WARM 2  // router lines a thread touches to fill its XCD's L2
+#define PF_RC_D 5     // groups of 4 chain steps whose LDS reads are in flight
+template <bool E64>
+__global__ void __launch_bounds__(256) k_pf_route_cfg(const float *__restrict__ WrT, const float *__restrict__ X,
+                                                      int T, int H, int E, int K, int8_t *__restrict__ X0,
+                                                      int8_t *__restrict__ X1, float *__restrict__ xsc,
+                                                      float *__restrict__ xsum, int *__restrict__ idx,
+                                                      float *__restrict__ w) {
+  __shared__ __attribute__((aligned(16))) float s_wr[2][PF_RC_KC * 64];
+  __shared__ __attribute__((aligned(16))) float s_x[4][256 * PF_SEL_U];
+  __shared__ float s_red[4][4][64];
+  __shared__ int s_idx[4][64];
+  __shared__ float s_w[4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const bool own = (int)blockIdx.x * 4 + wave < T;
+  const int t = min((int)blockIdx.x * 4 + wave, T - 1);  // past T: the last token again, nothing stored
+  const int nch = H / PF_RC_KC;
+  // Every XCD's L2 gets the whole router first: block b touches lines (b / 8) + n8·j (n8 = blocks per
+  // XCD when the grid is dealt to the 8 XCDs in turn; any other dealing only makes this prefetch
+  // partial). The loaded words feed a condition that never holds, which keeps the loads.
+  // At most PF_RC_WARM lines per thread, all loads issued before any is used (small grids warm part
+  // of the router; the chunk pipeline below covers the rest).
+  unsigned warm = 0;
+  {
+    const int lines = (H * E + 31) / 32, n8 = ((int)gridDim.x + 7) >> 3, r = (int)blockIdx.x >> 3;
+    unsigned v[PF_RC_WARM];
+#pragma unroll
+    for (int j = 0; j < PF_RC_WARM; j++)
+      v[j] = __float_as_uint(WrT[32 * (size_t)min(r + n8 * ((int)threadIdx.x + 256 * j), lines - 1)]);
+#pragma unroll
+    for (int j = 0; j < PF_RC_WARM; j++) warm ^= v[j];
+  }
+  // chunk c = router rows c·KC .. +KC-1 (KC·E contiguous floats) into LDS rows of 64 (zeros past E),
+  // through two register sets: a chunk's loads are issued two chunks before it is stored
+  constexpr int NQ = PF_RC_KC * 64 / 4 / 256;  // float4 slots per thread
+  f32x4 ra[NQ], rb[NQ];
+  auto load_chunk = [&](f32x4 (&r)[NQ], int c) {
+    const float *src = WrT + (size_t)min(c, nch - 1) * PF_RC_KC * E;
+#pragma unroll
+    for (int j = 0; j < NQ; j++) {
+      const int i = threadIdx.x + 256 * j;  // slot: row i / 16, experts 4 (i % 16) .. +3
+      if (E64) {
+        r[j] = ((const f32x4 *)src)[i];
+      } else {
+        const int row = i >> 4, e0 = 4 * (i & 15);
+#pragma unroll
+        for (int q = 0; q < 4; q++) r[j][q] = src[(size_t)row * E + min(e0 + q, E - 1)];
+      }
+    }
+  };
+  auto store_chunk = [&](const f32x4 (&r)[NQ], int buf) {
+#pragma unroll
+    for (int j = 0; j < NQ; j++) {
+      const int i = threadIdx.x + 256 * j;
+      f32x4 v = r[j];
+      if (!E64) {
+        const int e0 = 4 * (i & 15);
+#pragma unroll
+        for (int q = 0; q < 4; q++) v[q] = e0 + q < E ? v[q] : 0.0f;
+      }
+      ((f32x4 *)s_wr[buf])[i] = v;
+    }
+  };
+  load_chunk(ra, 0);
+  load_chunk(rb, 1);
+  asm volatile("" ::: "memory");
+  pf_x_limbs(X, t, H, own, X0, X1, xsc, xsum, s_x[wave]);
+  store_chunk(ra, 0);
+  load_chunk(ra, 2);
+  __syncthreads();
+  float s = 0.0f;
+  // chunk c from LDS buffer c & 1; then chunk c + 1 (in r) goes to the other buffer, which every wave
+  // finished before the last barrier, and r is reloaded with chunk c + 3. Unconditional (after the
+  // last chunk a copy of it goes to a buffer that is not read again), so the wait before the stores
+  // leaves the other register set's loads in flight.
+  // The chain reads the router values from LDS through a ring of PF_RC_D groups of 4 steps (two
+  // ds_read2st64 each), issued PF_RC_D groups ahead; the scheduling barriers keep the issue order, so
+  // each group waits only for its own reads. x comes from registers: xr[q] holds x values 16q .. 16q
+  // + 15 of the chunk in every row of 16 lanes (lane l: value 16q + l % 16), and a DPP row broadcast
+  // (row_newbcast) hands value k to all lanes as the multiply's operand.
+  auto step = [&](int c, f32x4 (&r)[NQ]) {
+    const float *wr = s_wr[c & 1] + lane;
+    const float *xs = s_x[wave] + c * PF_RC_KC + (lane & 15);
+    constexpr int G = PF_RC_KC / 4;
+    float xr[PF_RC_KC / 16];
+#pragma unroll
+    for (int q = 0; q < PF_RC_KC / 16; q++) xr[q] = xs[16 * q];
+    float wq[PF_RC_D][4];
+    auto ld = [&](int g, int slot) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) wq[slot][i] = wr[64 * (4 * g + i)];
+    };
+#pragma unroll
+    for (int g = 0; g < PF_RC_D; g++) ld(g, g);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      const int slot = g % PF_RC_D;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int k = 4 * g + i;
+        const float xb = pf_row_bcast(xr[k >> 4], k & 15);
+        s = __fadd_rn(s, __fmul_rn(xb, wq[slot][i]));
+      }
+      if (g + PF_RC_D < G) ld(g + PF_RC_D, slot);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    store_chunk(r, (c + 1) & 1);
+    load_chunk(r, c + 3);
+    __syncthreads();
+  };
+  for (int c = 0; c < nch; c += 2) {  // nch is even (H is a multiple of 256)
+    step(c, rb);
+    step(c + 1, ra);
+  }
+  if (warm == 0x9E3779B9u && T < 0) w[0] = 0.0f;
+  s_red[wave][0][lane] = lane < E ? s : 0.0f;
+  s_red[wave][1][lane] = 0.0f;
+  s_red[wave][2][lane] = 0.0f;
+  s_red[wave][3][lane] = 0.0f;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  route_select(E, K, DSH_ROUTE_CFG, s_idx[wave], s_w[wave], s_red[wave]);
+  if (own && lane < K) {
+    idx[(size_t)t * K + lane] = s_idx[wave][lane];
+    w[(size_t)t * K + lane] = s_w[wave][lane];
+  }
+}
 // DECODE (bf16 router in the reference's AVX-512 order, as k_dec_scores_bf16): one block per PF_TB
 // tokens, 64 groups of 4 lanes, group g computes expert g's score; the full score is partial 0, the
 // other three are zero (0 + ... keeps it).
@@ -188,31 +315,15 @@ __global__ void __launch_bounds__(256) k_pf_scores_bf16(const uint16_t *__restri
   }
 }
 
-// One wave per token: x's two int8 limbs (X0 low, X1 high) and their scale 2^(e-15), Σx, then the
-// expert selection from the four partial score rows (route_select: CFG top-k on raw scores +
-// softmax over the k; DECODE fast-exp softmax over all experts + top-k). H <= 256·PF_SEL_U: the
-// wave holds the whole row in registers.
-//
-// CFG: the partial-sum scores differ from ds_linear's sequential ones (ds_kernels.c:639-652) only
-// by rounding, bounded per expert by cert_radius_partials (dsh_cert.h: the running-error bound of
-// ds_linear's chain from the partials' prefix sizes pl, plus this order's own rounding; R rows per
-// partial, ||x|| from the f32 sum of squares, the router row norms rounded up). The selection stands
-// as it is when cert_check finds the intervals of the selected experts, in rank order, and of the
-// best unselected one disjoint: then ds_moe_top_k on the sequential scores (ds_kernels.c:193-243)
-// picks the same experts in the same order. Otherwise the experts whose interval reaches the lowest
-// selected lower bound (the only ones that can be among the top K) are written as the token's
-// candidate mask, and k_pf_exact recomputes their scores in ds_linear's order and selects again.
-#define PF_SEL_U 8  // x float4 loads per lane
-template <int MODE>
-__global__ void __launch_bounds__(256) k_pf_select(const float *__restrict__ X, int T, int H, int E, int K,
-                                                   const float *__restrict__ ps, const float *__restrict__ pl, int R,
-                                                   const float *__restrict__ wnorm,
-                                                   int8_t *__restrict__ X0, int8_t *__restrict__ X1,
-                                                   float *__restrict__ xsc, float *__restrict__ xsum,
-                                                   int *__restrict__ idx, float *__restrict__ w,
-                                                   unsigned long long *__restrict__ cmask) {
+
+// DECODE: one wave per token, x's limbs (pf_x_limbs), then the fast-exp softmax over all experts
+// and top-k (route_select) on the scores of k_pf_scores_bf16.
+__global__ void __launch_bounds__(256) k_pf_select_dec(const float *__restrict__ X, int T, int H, int E, int K,
+                                                       const float *__restrict__ ps, int8_t *__restrict__ X0,
+                                                       int8_t *__restrict__ X1, float *__restrict__ xsc,
+                                                       float *__restrict__ xsum, int *__restrict__ idx,
+                                                       float *__restrict__ w) {
   __shared__ float s_red[4][4][64];
-  __shared__ float s_lam[4][4][64];
   __shared__ int s_idx[4][64];
   __shared__ float s_w[4][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -220,205 +331,14 @@ __global__ void __launch_bounds__(256) k_pf_select(const float *__restrict__ X, 
   if (t >= T) return;  // no block-wide barriers below
 #pragma unroll
   for (int r = 0; r < 4; r++) s_red[wave][r][lane] = ps[((size_t)t * 4 + r) * 64 + lane];
-  if constexpr (MODE == DSH_ROUTE_CFG) {
-#pragma unroll
-    for (int r = 0; r < 4; r++) s_lam[wave][r][lane] = pl[((size_t)t * 4 + r) * 64 + lane];
-  }
-  const f32x4 *src = (const f32x4 *)(X + (size_t)t * H);
-  const int nc = H / 4;
-  f32x4 xv[PF_SEL_U];
-#pragma unroll
-  for (int u = 0; u < PF_SEL_U; u++) xv[u] = src[min(64 * u + lane, nc - 1)];
-  float s = 0.0f, mx = 0.0f, ss = 0.0f;
-#pragma unroll
-  for (int u = 0; u < PF_SEL_U; u++) {
-    if (64 * u + lane >= nc) continue;
-    const f32x4 v = xv[u];
-    s += (v[0] + v[1]) + (v[2] + v[3]);
-    mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v[0]), fabsf(v[1]))), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    if constexpr (MODE == DSH_ROUTE_CFG)
-      ss = __builtin_fmaf(v[3], v[3], __builtin_fmaf(v[2], v[2], __builtin_fmaf(v[1], v[1], __builtin_fmaf(v[0], v[0], ss))));
-  }
-  s = dsh_wave_sum(s);
-  mx = dsh_wave_max(mx);
-  const int ex = __builtin_amdgcn_frexp_expf(mx * 1.0078125f);  // 2^ex > max|x|·(1 + 2^-7)
-#pragma unroll
-  for (int u = 0; u < PF_SEL_U; u++) {
-    const int c = 64 * u + lane;
-    if (c >= nc) continue;
-    unsigned w0 = 0u, w1 = 0u;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int q = (int)__builtin_rintf(__builtin_ldexpf(xv[u][i], 15 - ex));  // |q| < 2^15 / (1 + 2^-7)
-      const int lo = __builtin_amdgcn_sbfe(q, 0, 8);                            // balanced low digit
-      const int hi = (q - lo) >> 8;                                              // |hi| <= 127
-      w0 |= ((unsigned)lo & 255u) << (8 * i);
-      w1 |= ((unsigned)hi & 255u) << (8 * i);
-    }
-    *(unsigned *)(X0 + (size_t)t * H + 4 * c) = w0;
-    *(unsigned *)(X1 + (size_t)t * H + 4 * c) = w1;
-  }
-  if (lane == 0) {
-    xsum[t] = s;
-    xsc[t] = __builtin_ldexpf(1.0f, ex - 15);
-  }
+  pf_x_limbs(X, t, H, true, X0, X1, xsc, xsum, nullptr);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if constexpr (MODE == DSH_ROUTE_CFG) {
-    route_state st;
-    route_init(E, K, MODE, s_red[wave], st);
-    route_rounds(st, 0, st.ns);
-    // ||x|| from the f32 sum of squares: relative error below (H + 6) u, which 2^-10 covers
-    const float xn = __builtin_sqrtf(dsh_wave_sum(ss)) * (1.0f + 0x1p-10f);
-    const float r[4] = {s_red[wave][0][lane], s_red[wave][1][lane], s_red[wave][2][lane], s_red[wave][3][lane]};
-    const float lam[4] = {s_lam[wave][0][lane], s_lam[wave][1][lane], s_lam[wave][2][lane], s_lam[wave][3][lane]};
-    const int NB = H / R, P = (NB + 3) / 4;
-    int nb[4];
-#pragma unroll
-    for (int v = 0; v < 4; v++) nb[v] = max(0, min(P, NB - v * P));
-    const float c = ((r[0] + r[1]) + r[2]) + r[3];
-    const float eps = lane < E ? cert_radius_partials(r, lam, nb, R, H, wnorm[lane], xn) : 0.0f;
-    unsigned long long m;
-    cert_check(st, c, eps, E, K, m);
-    int id;
-    float wt;
-    route_finish(MODE, st, id, wt);
-    if (lane < K) {
-      idx[(size_t)t * K + lane] = id;
-      w[(size_t)t * K + lane] = wt;
-    }
-    if (lane == 0) cmask[t] = m;
-    return;
-  }
-  route_select(E, K, MODE, s_idx[wave], s_w[wave], s_red[wave]);
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  route_select(E, K, DSH_ROUTE_DECODE, s_idx[wave], s_w[wave], s_red[wave]);
   if (lane < K) {
     idx[(size_t)t * K + lane] = s_idx[wave][lane];
     w[(size_t)t * K + lane] = s_w[wave][lane];
-  }
-}
-
-// CFG tokens whose selection the rounding bound could not confirm (cmask != 0): one block per
-// token; the candidates' router rows (up to G <= PF_EX_G at a time, G set so LDS stays within
-// 64 KB; rows H + 4 floats apart, so the lanes' 16-byte reads hit distinct banks) and x go to LDS,
-// all threads replace the rows' values by the rounded products x_k·r_k, and lane c of wave 0 adds
-// candidate c's products in ds_linear's order (ds_kernels.c:639-652 as GCC compiles it: rounded
-// products added in index order, the tail past the last multiple of 8 fused; the chain lane issues
-// only the dependent adds), the other experts are set aside, and the
-// selection and its softmax (route_select) run again: idx and w of the token are replaced.
-#define PF_EX_G 8
-#define PF_EX_LD ((PF_EX_G + 1) * 2048 / 4 / 256)  // f32x4 loads per thread for x and a group, H <= 2048
-__global__ void __launch_bounds__(256) k_pf_exact(const float *__restrict__ X, const float *__restrict__ Wr, int H,
-                                                  int E, int K, int G, const unsigned long long *__restrict__ cmask,
-                                                  int *__restrict__ idx, float *__restrict__ w) {
-  extern __shared__ __attribute__((aligned(16))) float s_dyn[];  // x [H], rows [G][H + 4]
-  __shared__ float s_red[4][64];
-  __shared__ int s_idx[64];
-  __shared__ float s_w[64];
-  const int t = blockIdx.x;
-  const unsigned long long mask = cmask[t];
-  if (!mask) return;
-  float *s_x = s_dyn, *s_rows = s_dyn + H;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q4 = H / 4;
-  bool first = true;
-  const int m = H >= 16 ? (H & ~15) + ((H - (H & ~15)) >= 8 ? 8 : 0) : (H >= 8 ? 8 : 0);
-  float mine = -1e30f;  // wave 0, lane e: the recomputed score of expert e (candidates only)
-  unsigned long long rest = mask;
-  while (rest) {
-    // the next PF_EX_G candidates (uniform), their rows into LDS
-    int ce[PF_EX_G], nc = 0;
-    while (rest && nc < G) {
-      ce[nc++] = __builtin_ctzll(rest);
-      rest &= rest - 1;
-    }
-    // every load of the group (and of x, with the first group) in flight before any store
-    const int n0 = first ? q4 : 0, tot = n0 + nc * q4;
-    f32x4 buf[PF_EX_LD];
-#pragma unroll
-    for (int j = 0; j < PF_EX_LD; j++) {
-      const int i = min((int)threadIdx.x + 256 * j, tot - 1);
-      const int c = (i - n0) / q4, o = i - n0 - c * q4;
-      buf[j] = i < n0 ? ((const f32x4 *)(X + (size_t)t * H))[i] : ((const f32x4 *)(Wr + (size_t)ce[min(c, nc - 1)] * H))[o];
-    }
-    __syncthreads();  // the previous group's reads are done
-#pragma unroll
-    for (int j = 0; j < PF_EX_LD; j++) {
-      const int i = threadIdx.x + 256 * j;
-      if (i >= tot) break;
-      const int c = (i - n0) / q4, o = i - n0 - c * q4;
-      if (i < n0)
-        ((f32x4 *)s_x)[i] = buf[j];
-      else
-        *(f32x4 *)(s_rows + (size_t)c * (H + 4) + 4 * o) = buf[j];
-    }
-    first = false;
-    __syncthreads();
-    // the rounded products x_k·r_k of the first m columns (contraction off: one rounding each),
-    // by all threads, in place of the rows' values
-    {
-      const int m4 = m / 4;
-      for (int i = threadIdx.x; i < nc * m4; i += 256) {
-        const int c = i / m4, q = i - c * m4;
-        f32x4 *r = (f32x4 *)(s_rows + (size_t)c * (H + 4)) + q;
-        *r = ((const f32x4 *)s_x)[q] * *r;
-      }
-    }
-    __syncthreads();
-    if (wave == 0) {
-      float a = 0.0f;
-      if (lane < nc) {
-        // the dependent adds of the products in index order, 16 values per step, EX_D steps of
-        // LDS reads in flight (a ring of registers), then the fused tail
-        constexpr int EX_D = 4;
-        const f32x4 *p4 = (const f32x4 *)(s_rows + lane * (H + 4));
-        const int m16 = m & ~15, nst = m16 / 16;
-        f32x4 pq[EX_D][4];
-#pragma unroll
-        for (int d = 0; d < EX_D; d++)
-#pragma unroll
-          for (int q = 0; q < 4; q++) pq[d][q] = p4[4 * min(d, max(nst - 1, 0)) + q];
-        asm volatile("" ::: "memory");
-        for (int s0 = 0; s0 < nst; s0 += EX_D) {
-#pragma unroll
-          for (int d = 0; d < EX_D; d++) {
-            if (s0 + d < nst) {
-#pragma unroll
-              for (int q = 0; q < 4; q++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) a = a + pq[d][q][i];
-            }
-            const int st = min(s0 + d + EX_D, max(nst - 1, 0));
-#pragma unroll
-            for (int q = 0; q < 4; q++) pq[d][q] = p4[4 * st + q];
-            asm volatile("" ::: "memory");
-          }
-        }
-        const float *rr = s_rows + lane * (H + 4);
-        for (int k = m16; k < m; k++) a = a + rr[k];
-        for (int k = m; k < H; k++) a = __builtin_fmaf(s_x[k], rr[k], a);
-      }
-      for (int c = 0; c < nc; c++) {
-        const float v = __shfl(a, c);
-        if (lane == ce[c]) mine = v;
-      }
-    }
-  }
-  if (wave == 0) {
-    s_red[0][lane] = lane < E ? mine : -1e30f;
-    s_red[1][lane] = 0.0f;
-    s_red[2][lane] = 0.0f;
-    s_red[3][lane] = 0.0f;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    route_select(E, K, DSH_ROUTE_CFG, s_idx, s_w, s_red);
-    if (lane < K) {
-      idx[(size_t)t * K + lane] = s_idx[lane];
-      w[(size_t)t * K + lane] = s_w[lane];
-    }
   }
 }
 
@@ -1284,11 +1204,9 @@ struct pf_ws {
   int *pair_tok, *pos_of;
   pf_hq hq;         // SwiGLU outputs h as int8 limbs: routed [TK][I], shared [T][SI]
   float *Y, *Ysh;
-  float *ps;        // [T][4][64] partial router scores
-  float *pl;        // [T][4][64] their prefix sizes (CFG)
+  float *ps;        // [T][4][64] router scores (DECODE: the full score in row 0, rows 1-3 zero)
   float *hpr, *hps; // Σh partials per (row, gate_up n-tile): routed [TK][I/128], shared [T][SI/128]
   float *hmr, *hms; // max |h| per (row, gate_up n-tile), same layout
-  unsigned long long *cmask;  // CFG: per token, the experts whose scores are recomputed (0: none)
   int *tiles_gu, *tiles_dn;  // routed GEMM tiles (item << 8 | n-tile) in launch order
   int *qtiles, *qcount, *qnext, *gu_done, *err;  // fused kernel: work queues, counters, wait error
 };
@@ -1342,12 +1260,10 @@ size_t pf_carve(const dsh_layer_t *L, int T, void *base, pf_ws *w) {
   TAKE(Y, float, TK * H);
   TAKE(Ysh, float, T * H);
   TAKE(ps, float, (size_t)T * 4 * 64);
-  TAKE(pl, float, (size_t)T * 4 * 64);
   TAKE(hpr, float, TK * (I / PF_GU_N));
   TAKE(hps, float, (size_t)T * (SI / PF_GU_N));
   TAKE(hmr, float, TK * (I / PF_GU_N));
   TAKE(hms, float, (size_t)T * (SI / PF_GU_N));
-  TAKE(cmask, unsigned long long, T);
   TAKE(tiles_gu, int, (size_t)pf_max_routed_items(L, T) * (I / PF_GU_N));
   TAKE(tiles_dn, int, (size_t)pf_max_routed_items(L, T) * (H / PF_DN_N));
   TAKE(qtiles, int, (size_t)PF_NQ * pf_queue_cap(L, T));
@@ -1367,7 +1283,7 @@ int dsh_pf_supported(const dsh_layer_t *L) {
   if (L->H % PF_KS || L->I % PF_KS || L->SI % PF_KS) return 0;
   if (L->E > 64 || L->K > 64 || L->K > L->E) return 0;
   if ((size_t)PF_TB * L->H * sizeof(float) > 96 * 1024) return 0;  // DECODE scores: x rows in LDS
-  if (L->H > 256 * PF_SEL_U) return 0;                              // k_pf_select holds a row per wave
+  if (L->H > 256 * PF_SEL_U) return 0;  // a wave holds a token's x row (pf_x_limbs, k_pf_route_cfg's LDS)
   if (L->I > PF_KS * PF_NT_MAX || L->SI > PF_KS * PF_NT_MAX) return 0;  // down: exponent table per row
   return 1;
 }
@@ -1457,24 +1373,17 @@ hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int r
   pf_ws w;
   pf_carve(L, T, ws, &w);
   const int H = L->H, K = L->K, E = L->E;
-  // CFG partial sums over the same row blocks as the decode path (8 rows, 16 past 1280 columns)
-  const int R = H / dsh_dec_partials(H);
   if (route_mode == DSH_ROUTE_CFG) {
-    const dim3 g((T + PF_SC_TOK - 1) / PF_SC_TOK, 4);
-    if (R == 16)
-      k_pf_scores_cfg<16><<<g, 256, 0, s>>>(L->router_f32_t, X, T, H, E, w.ps, w.pl);
+    if (E == 64)
+      k_pf_route_cfg<true><<<(T + 3) / 4, 256, 0, s>>>(L->router_f32_t, X, T, H, E, K, w.X0, w.X1, w.xsc, w.xsum,
+                                                        w.idx, w.w);
     else
-      k_pf_scores_cfg<8><<<g, 256, 0, s>>>(L->router_f32_t, X, T, H, E, w.ps, w.pl);
-    k_pf_select<DSH_ROUTE_CFG><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, w.pl, R, L->router_norm, w.X0, w.X1, w.xsc,
-                                                            w.xsum, w.idx, w.w, w.cmask);
-    const int G = min(PF_EX_G, (16384 - H) / (H + 4));  // H <= 2048: G >= 6
-    k_pf_exact<<<T, 256, sizeof(float) * ((size_t)H + (size_t)G * (H + 4)), s>>>(X, L->router_f32, H, E, K, G,
-                                                                                 w.cmask, w.idx, w.w);
+      k_pf_route_cfg<false><<<(T + 3) / 4, 256, 0, s>>>(L->router_f32_t, X, T, H, E, K, w.X0, w.X1, w.xsc, w.xsum,
+                                                         w.idx, w.w);
   } else {
     k_pf_scores_bf16<<<(T + PF_TB - 1) / PF_TB, 256, (size_t)PF_TB * H * sizeof(float), s>>>(
         L->router_bf16, X, T, H, E, nthreads, w.ps);
-    k_pf_select<DSH_ROUTE_DECODE><<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, nullptr, R, nullptr, w.X0, w.X1, w.xsc,
-                                                                w.xsum, w.idx, w.w, nullptr);
+    k_pf_select_dec<<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, w.X0, w.X1, w.xsc, w.xsum, w.idx, w.w);
   }
   const int n_items_max = pf_max_routed_items(L, T) + pf_shared_items(T);
   const bool fused = g_pf_fused == 1 && n_items_max < (1 << 22);

@@ -3,10 +3,10 @@ run on this layer's INT8 experts) against the oracle.
 
 Routing: DECODE mode (bf16 router) is compared bit for bit with the reference arithmetic of the
 decode router (the AVX-512-order bf16 scores, or_bf16_matvec_avx512, then the fast-exp softmax and
-top-k, or_softmax_topk_decode). CFG mode (f32 router) sums the scores in a different f32 order than
-or_linear_f32 and recomputes them in or_linear_f32's order whenever the rounding bound cannot
-separate the ranks: its expert indices (in rank order) equal or_prefill_route's on every token, its
-weights are within 1e-5 (2 ulp where the scores were recomputed).
+top-k, or_softmax_topk_decode). CFG mode (f32 router) computes every score in or_linear_f32's order
+(one chain per token and expert): its expert indices (in rank order) equal or_prefill_route's on every
+token, and its weights are within 2 ulp (the GPU's softmax uses a correctly rounded expf; glibc's is
+off by one ulp on a few arguments).
 Outputs: the GPU's own routing is fed to the f64 brute force (or_prefill_moe_f64) and the block
 output must be within max|a-b|/max|b| <= 1e-3.
 """
@@ -61,7 +61,8 @@ def check_routing(B, lay, X, idx, w, mode):
     B.oracle().or_prefill_route(ri, rw, X, T, C.byref(lay.or_layer()), mode)
     for t in range(T):
         assert np.array_equal(ri[t], idx[t]), (t, ri[t], idx[t])
-        assert np.allclose(rw[t], w[t], rtol=1e-5, atol=1e-7), t
+    ulp = np.abs(rw.view(np.int32).astype(np.int64) - w.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 2, (int(ulp.max()), int(np.argmax(ulp.max(axis=1))))
     return ri, rw
 
 
@@ -89,7 +90,9 @@ def test_prefill_one_token_equals_decode(dev, B, mode):
     """One token through the prefill block routes exactly like the decode layer and gives the same
     output within the two paths' rounding: the decode layer runs the reference's f32 chains, the
     prefill block puts x and h on a 16-bit grid (2^-15 of the row's largest value; h n-tiles at a
-    smaller exponent are rounded twice), about 1e-4 of the output's largest value."""
+    smaller exponent are rounded twice), about 1e-4 of the output's largest value. The weights are
+    the same bits in DECODE mode; in CFG mode the prefill block's come from scores in ds_linear's
+    order, the decode layer's from its certified partial sums (within 2e-5 unless it recomputed)."""
     from test_gpu_moe import layer_forward
     L = dev.load()
     lay = B.make_moe_layer(62, hidden=256, inter=128, n_experts=16)
@@ -98,7 +101,11 @@ def test_prefill_one_token_equals_decode(dev, B, mode):
         x = B.normal_f32(256, 6001)
         out, idx, w = gpu_prefill(dev, h, x[None, :], mode)
         dout, didx, dw = layer_forward(dev, h, x, mode)
-        assert np.array_equal(idx[0], didx) and np.array_equal(w[0].view(np.uint32), dw.view(np.uint32))
+        assert np.array_equal(idx[0], didx)
+        if mode == 0:
+            assert np.array_equal(w[0].view(np.uint32), dw.view(np.uint32))
+        else:
+            assert np.allclose(w[0], dw, rtol=2e-5, atol=1e-7)
         err = rel_err(out[0], dout)
         print(f"one-token prefill vs decode mode={mode}: {err:.2e}")
         assert err < 2e-4
@@ -213,11 +220,10 @@ def test_prefill_config3_outlier_channels(dev, B):
         L.ds_hip_layer_destroy(h)
 
 
-def test_prefill_cfg_near_ties_recomputed(dev, B):
+def test_prefill_cfg_near_ties(dev, B):
     """Router rows 3 and 5 differ by about 1e-6 of their size and are scaled up, so on every token
-    they rank next to each other in the top K with scores far closer than the rounding bound: the
-    selection is recomputed in or_linear_f32's order on every token: indices (in rank order) equal
-    or_prefill_route's, weights within 2 ulp."""
+    they rank next to each other in the top K with scores far closer than any other order's rounding
+    could separate: indices (in rank order) equal or_prefill_route's, weights within 2 ulp."""
     L = dev.load()
     lay = B.make_moe_layer(66, hidden=256, inter=128, n_experts=16)
     R = lay.router_f32.reshape(16, 256)
