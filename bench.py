@@ -212,6 +212,8 @@ def dropin_leg(dev, lays, lm_w, xs_host, n_steps):
     ex.dropin_register.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int]
     ex.dropin_decode_steps.restype = C.c_double
     ex.dropin_decode_steps.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p]
+    ex.dropin_call_times.restype = None
+    ex.dropin_call_times.argtypes = [C.c_void_p, C.c_void_p]
     keep = []
     arr = (DropinLayer * len(lays))()
     for l, lay in enumerate(lays):
@@ -235,9 +237,15 @@ def dropin_leg(dev, lays, lm_w, xs_host, n_steps):
                                   toks.ctypes.data)
     if secs <= 0:
         raise RuntimeError("drop-in leg failed")
+    ks, kc = (C.c_double * 6)(), (C.c_long * 6)()
+    ex.dropin_call_times(ks, kc)
+    kinds = ["ds_moe_router_bf16", "ds_expert_forward_fused_int4 (routed)", "ds_expert_combine",
+             "ds_expert_forward_fused_int4 (shared)", "ds_vec_add", "ds_argmax_matvec_bf16"]
+    per_call = {kinds[k]: {"calls_per_step": round(kc[k] / n, 2), "us_per_call": round(1e6 * ks[k] / max(kc[k], 1), 2),
+                           "us_per_step": round(1e6 * ks[k] / n, 1)} for k in range(6)}
     return {"value": round(n / secs, 3), "unit": "tok/s", "ms_per_step": round(1000 * secs / n, 3), "steps": n,
             "route": "decode (moe_forward's bf16 router, host softmax/top-k as the reference caller does it)",
-            "register_s": round(reg_s, 2), "tokens": toks[:n],
+            "register_s": round(reg_s, 2), "tokens": toks[:n], "per_call": per_call,
             "calls_per_step": LAYERS * (1 + K + 1 + 1 + 2) + 1,
             "method": "host wall clock around n steps of ds-ocr_amd/examples/moe_forward_dropin.c: per layer "
                       "ds_moe_router_bf16, 6 x ds_expert_forward_fused_int4, ds_expert_combine, the shared "
@@ -588,6 +596,43 @@ def main():
         xp.close()
         op.close()
 
+    # configs 1 and 2 on their own (BASELINE's GB/s rows): one expert through the per-function
+    # kernel, one MoE layer through ds_hip_layer_forward, inputs and outputs in device memory
+    singles = None
+    if not full:
+        gq, gs, go = np.empty((2 * I, H), np.int8), np.empty(2 * I, np.float32), np.empty(2 * I, np.float32)
+        dq, ds_, do = np.empty((H, I), np.int8), np.empty(H, np.float32), np.empty(H, np.float32)
+        dev.check(L.ds_hip_layer_export_expert(handles[0], 0, gq.ctypes.data, gs.ctypes.data, go.ctypes.data,
+                                               dq.ctypes.data, ds_.ctypes.data, do.ctypes.data), "export")
+        gb, db = dev.block_from_arrays(gq, gs, go), dev.block_from_arrays(dq, ds_, do)
+        x1 = np.random.default_rng(1).standard_normal(H).astype(np.float32)
+        te = C.c_float(0)
+        dev.check(L.ds_hip_time_expert(C.byref(gb), C.byref(db), H, I, x1.ctypes.data, 200, C.byref(te)),
+                  "expert timing")
+        e_bytes = 2 * I * H + 2 * I * 8 + H * I + H * 8
+        xl = dev.DeviceBuffer(H * 4)
+        dev.check(L.ds_hip_fill_normal_f32(xl.ptr, H, 4711, 0.0, 1.0), "fill")
+        ol = dev.DeviceBuffer(H * 4)
+        tl = C.c_float(0)
+        dev.check(L.ds_hip_time_layer(handles[0], ol.ptr, xl.ptr, route, 200, C.byref(tl)), "layer timing")
+        l_bytes = K * e_bytes + (2 * SI * H + 2 * SI * 8 + H * SI + H * 8) + E * H * 4
+        singles = {
+            "config1_expert": {"bytes": e_bytes, "us": round(te.value * 1e3, 2),
+                               "gbs": round(e_bytes / (te.value * 1e-3) / 1e9, 1),
+                               "frac": round(e_bytes / (te.value * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                               "kernel": "k_expert_exact (ds_expert_forward_fused_int4's one launch: every row "
+                                         "in the reference's sequential order, bit-identical)",
+                               "method": "200 back-to-back launches between HIP events, x and y in device memory"},
+            "config2_layer": {"bytes": l_bytes, "us": round(tl.value * 1e3, 2),
+                              "gbs": round(l_bytes / (tl.value * 1e-3) / 1e9, 1),
+                              "frac": round(l_bytes / (tl.value * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                              "kernel": "ds_hip_layer_forward: k_dec_gate_up + k_dec_down (the two-kernel layer, "
+                                        "certified CFG routing), one layer on its own",
+                              "method": "200 back-to-back calls between HIP events; in the stack the one-kernel "
+                                        "layer's time is roofline.avg_ms"}}
+        xl.close()
+        ol.close()
+
     # whole decoder steps (12 layers with their attention halves after kv cached positions), with
     # their own input rows and token slots
     decoder = None
@@ -720,6 +765,7 @@ def main():
                                 f"{'one-kernel' if layer_kernels == 1 else 'two-kernel'} layers produced both"},
         "kernels": kernel_ms,
         "prefill": prefill,
+        "single_configs": singles,
         "decoder_step": decoder,
         "cpu_baseline": cpu,
         "dropin_per_function": dropin,

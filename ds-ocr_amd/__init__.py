@@ -67,6 +67,8 @@ SIGNATURES = {
     "ds_hip_memcpy_h2d": (C.c_int, [vp, vp, C.c_size_t]),
     "ds_hip_memcpy_d2h": (C.c_int, [vp, vp, C.c_size_t]),
     "ds_hip_time_stream_read": (C.c_int, [vp, C.c_size_t, C.c_int, C.POINTER(C.c_float)]),
+    "ds_hip_time_expert": (C.c_int, [C.POINTER(Int4Block), C.POINTER(Int4Block), C.c_int, C.c_int, vp, C.c_int,
+                                     C.POINTER(C.c_float)]),
     "ds_hip_memcpy_d2d": (C.c_int, [vp, vp, C.c_size_t]),
     "ds_hip_sync": (C.c_int, []),
     "ds_hip_fill_normal_bf16": (C.c_int, [vp, C.c_size_t, C.c_uint64, C.c_float]),
@@ -85,6 +87,7 @@ SIGNATURES = {
     "ds_hip_layer_forward": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, vp, vp]),
     "ds_hip_layer_prefill": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp, vp]),
     "ds_hip_time_prefill": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float)]),
+    "ds_hip_time_layer": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.POINTER(C.c_float)]),
     "ds_hip_prefill_path": (C.c_int, [C.c_int]),
     "ds_hip_prefill_wait_error": (C.c_int, [vp, C.c_int]),
     "ds_hip_prefill_set_wait_limit": (C.c_int, [C.c_int]),

@@ -30,6 +30,34 @@ typedef struct {
   float *out, *experts, *shared, *gu, *g, *u, *h;
 } dropin_bufs_t;
 
+/* Host wall time and count of each kind of library call during the last dropin_decode_steps run
+ * (clock_gettime around every call; the caller's own routing on the host is in none of them). */
+enum { K_ROUTER, K_EXPERT, K_COMBINE, K_SHARED, K_VEC_ADD, K_ARGMAX, K_NKIND };
+static double g_secs[K_NKIND];
+static long g_calls[K_NKIND];
+
+static double now_s(void) {
+  struct timespec t;
+  clock_gettime(CLOCK_MONOTONIC, &t);
+  return (double)t.tv_sec + 1e-9 * (double)t.tv_nsec;
+}
+
+#define TIMED(kind, call)             \
+  do {                                \
+    const double t0_ = now_s();       \
+    call;                             \
+    g_secs[kind] += now_s() - t0_;    \
+    g_calls[kind]++;                  \
+  } while (0)
+
+/* secs[k], calls[k] for the kinds router, routed expert, combine, shared expert, vec_add, argmax. */
+void dropin_call_times(double *secs, long *calls) {
+  for (int k = 0; k < K_NKIND; k++) {
+    secs[k] = g_secs[k];
+    calls[k] = g_calls[k];
+  }
+}
+
 /* The caller's routing (ds_moe_decoder.c:157-183): softmax of all router scores with the bit-trick
  * exponent, then the top_k largest probabilities, the first of equal ones, unnormalised. */
 static void route(int *idx, float *w, float *scores, int n, int k) {
@@ -62,15 +90,15 @@ static void moe_block(const dropin_layer_t *ly, const float *x, dropin_bufs_t *b
   const int H = ly->hidden, I = ly->inter;
   float scores[DS_MAX_EXPERTS], w[DS_MAX_EXPERTS];
   int idx[DS_MAX_EXPERTS];
-  ds_moe_router_bf16(scores, x, ly->router_bf16, H, ly->n_experts);
+  TIMED(K_ROUTER, ds_moe_router_bf16(scores, x, ly->router_bf16, H, ly->n_experts));
   route(idx, w, scores, ly->n_experts, ly->top_k);
   for (int k = 0; k < ly->top_k; k++)
-    ds_expert_forward_fused_int4(b->experts + (size_t)k * H, x, &ly->gate_up[idx[k]], &ly->down[idx[k]], H, I, b->gu,
-                                 b->g, b->u, b->h);
-  ds_expert_combine(b->out, b->experts, idx, w, ly->top_k, H);
-  ds_expert_forward_fused_int4(b->shared, x, ly->shared_gate_up, ly->shared_down, H, ly->shared_inter, b->gu, b->g,
-                               b->u, b->h);
-  ds_vec_add(b->out, b->out, b->shared, H);
+    TIMED(K_EXPERT, ds_expert_forward_fused_int4(b->experts + (size_t)k * H, x, &ly->gate_up[idx[k]],
+                                                 &ly->down[idx[k]], H, I, b->gu, b->g, b->u, b->h));
+  TIMED(K_COMBINE, ds_expert_combine(b->out, b->experts, idx, w, ly->top_k, H));
+  TIMED(K_SHARED, ds_expert_forward_fused_int4(b->shared, x, ly->shared_gate_up, ly->shared_down, H,
+                                               ly->shared_inter, b->gu, b->g, b->u, b->h));
+  TIMED(K_VEC_ADD, ds_vec_add(b->out, b->out, b->shared, H));
 }
 
 /* Registers every block and the routers and the head with the device (one upload each), so the
@@ -109,14 +137,16 @@ double dropin_decode_steps(const dropin_layer_t *layers, int n_layers, const uin
   double secs = -1.0;
   if (x && b.out && b.shared && b.experts && b.gu && b.g && b.u && b.h) {
     struct timespec t0, t1;
+    memset(g_secs, 0, sizeof g_secs);
+    memset(g_calls, 0, sizeof g_calls);
     clock_gettime(CLOCK_MONOTONIC, &t0);
     for (int s = 0; s < n_steps; s++) {
       memcpy(x, xs + (size_t)s * H, sizeof(float) * (size_t)H);
       for (int l = 0; l < n_layers; l++) {
         moe_block(&layers[l], x, &b);
-        ds_vec_add(x, x, b.out, H);
+        TIMED(K_VEC_ADD, ds_vec_add(x, x, b.out, H));
       }
-      tokens[s] = ds_argmax_matvec_bf16(x, lm_w, H, vocab);
+      TIMED(K_ARGMAX, tokens[s] = ds_argmax_matvec_bf16(x, lm_w, H, vocab));
     }
     clock_gettime(CLOCK_MONOTONIC, &t1);
     secs = (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);

@@ -456,6 +456,24 @@ int ds_hip_time_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, i
   return rc;
 }
 
+int ds_hip_time_layer(ds_hip_layer_t *L, float *out_dev, const float *x_dev, int route_mode, int n, float *ms) {
+  if (!ms || n <= 0) return dsr_failf("ds_hip_time_layer: invalid arguments");
+  if (ds_hip_layer_forward(L, out_dev, x_dev, route_mode, 0, NULL, NULL)) return -1; /* warm-up */
+  hipEvent_t a, b;
+  DSR_TRY(hipEventCreate(&a), "event");
+  DSR_TRY(hipEventCreate(&b), "event");
+  int rc = 0;
+  if (hipEventRecord(a, dsr_stream) != hipSuccess) rc = -1;
+  for (int i = 0; i < n && rc == 0; i++) rc = ds_hip_layer_forward(L, out_dev, x_dev, route_mode, 0, NULL, NULL);
+  if (rc == 0 && (hipEventRecord(b, dsr_stream) != hipSuccess || hipEventSynchronize(b) != hipSuccess ||
+                  hipEventElapsedTime(ms, a, b) != hipSuccess))
+    rc = dsr_failf("ds_hip_time_layer: timing failed");
+  if (rc == 0) *ms /= (float)n;
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  return rc == 0 ? dsr_derr_check() : rc;
+}
+
 /* ================================================================ persisted arena
  * File (little-endian): a 256-byte header
  *   [0,8) magic "DSI8ARNA"  [8,12) version (1)  [12,16) n_layers  [16,36) hidden, inter, n_experts,

@@ -150,6 +150,52 @@ void ds_int4_matvec_rows(float *y, const float *x, const ds_int4_block_t *block,
 
 /* ds_quantize.c:301-321: gate_up matvec -> split -> [bf16] -> SwiGLU -> [bf16] -> down -> [bf16];
  * every step in the reference's order, so the output is bit-identical in both modes. */
+int ds_hip_time_expert(const ds_int4_block_t *gate_up_int4, const ds_int4_block_t *down_int4, int hidden,
+                       int intermediate, const float *x, int n, float *ms) {
+  if (dsr_init()) return -1;
+  if (!gate_up_int4 || !down_int4 || !x || n <= 0 || !ms) return dsr_failf("ds_hip_time_expert: invalid arguments");
+  if (gate_up_int4->out_dim != 2 * intermediate || down_int4->in_dim != intermediate ||
+      down_int4->out_dim != hidden || gate_up_int4->in_dim != hidden)
+    return dsr_failf("ds_hip_time_expert: block shapes do not match hidden=%d intermediate=%d", hidden, intermediate);
+  if (!dsh_expert_exact_blocks(hidden, intermediate))
+    return dsr_failf("ds_hip_time_expert: hidden=%d intermediate=%d has no one-launch expert kernel", hidden,
+                     intermediate);
+  dsr_dblock_t g, d;
+  if (dsr_block_device(gate_up_int4, &g) || dsr_block_device(down_int4, &d)) return -1;
+  const size_t xb = (size_t)hidden * 4;
+  const int nd = dsh_expert_exact_down_blocks(hidden);
+  unsigned long long *hb = (unsigned long long *)dsr_expert_hbuf((size_t)intermediate);
+  if (!hb) return -1;
+  float *xd = NULL, *yd = NULL;
+  unsigned *done = NULL;
+  hipEvent_t a = NULL, b = NULL;
+  int rc = 0;
+  if (hipMalloc((void **)&xd, xb) != hipSuccess || hipMalloc((void **)&yd, xb) != hipSuccess ||
+      hipMalloc((void **)&done, sizeof(unsigned) * (size_t)nd) != hipSuccess || hipEventCreate(&a) != hipSuccess ||
+      hipEventCreate(&b) != hipSuccess)
+    rc = dsr_failf("ds_hip_time_expert: allocation failed");
+  if (rc == 0 && dsr_h2d(xd, x, xb)) rc = -1;
+  for (int i = -1; i < n && rc == 0; i++) { /* i = -1: warm-up launch */
+    if (i == 0 && hipEventRecord(a, dsr_stream) != hipSuccess) rc = -1;
+    const hipError_t e = dsh_launch_expert_exact(g.q, g.scale, g.offset, d.q, d.scale, d.offset, xd, NULL, hb, yd,
+                                                 done, hidden, intermediate, dsr_expert_epoch(),
+                                                 ds_bf16_simulate_python, 1 << 22, dsr_derr_dev(DSR_DERR_EXPERT_WAIT),
+                                                 dsr_stream);
+    if (e != hipSuccess) rc = dsr_fail("expert kernel", e);
+  }
+  if (rc == 0 && (hipEventRecord(b, dsr_stream) != hipSuccess || hipEventSynchronize(b) != hipSuccess ||
+                  hipEventElapsedTime(ms, a, b) != hipSuccess))
+    rc = dsr_failf("ds_hip_time_expert: timing failed");
+  if (rc == 0) *ms /= (float)n;
+  (void)hipStreamSynchronize(dsr_stream);
+  if (a) hipEventDestroy(a);
+  if (b) hipEventDestroy(b);
+  hipFree(xd);
+  hipFree(yd);
+  hipFree(done);
+  return rc == 0 ? dsr_derr_check() : rc;
+}
+
 void ds_expert_forward_fused_int4(float *out, const float *x, const ds_int4_block_t *gate_up_int4,
                                   const ds_int4_block_t *down_int4, int hidden, int intermediate, float *gate_up_buf,
                                   float *gate_buf, float *up_buf, float *hidden_buf) {

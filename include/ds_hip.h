@@ -36,6 +36,13 @@ int ds_hip_memcpy_d2d(void *dst_dev, const void *src_dev, size_t bytes);
 /* Average time of n back-to-back launches of a plain streaming read of bytes of src_dev (the
  * achievable-bandwidth reference for the HBM-bound kernels; no counterpart in the reference). */
 int ds_hip_time_stream_read(const void *src_dev, size_t bytes, int n, float *ms);
+/* Average device time (ms) of n back-to-back launches of the kernel behind
+ * ds_expert_forward_fused_int4 (gate_up, SwiGLU and down in one launch, each row in the reference's
+ * order) with the input x (host, copied once) and the output in device memory: one expert on its own,
+ * without the per-call host transfers (a measurement hook, no counterpart in the reference). The
+ * blocks are registered like the per-function API's. */
+int ds_hip_time_expert(const ds_int4_block_t *gate_up_int4, const ds_int4_block_t *down_int4, int hidden,
+                       int intermediate, const float *x, int n, float *ms);
 /* Waits for the library stream. Returns -1 (message in ds_hip_last_error) if a kernel reported since
  * the last check that one of its bounded waits gave up (the prefill's down tiles waiting for their
  * gate_up tiles, the one-kernel decode layers' extra blocks waiting for the verdict on the expert
@@ -143,6 +150,9 @@ int ds_hip_layer_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
 
 /* Average device time (ms) of n back-to-back ds_hip_layer_prefill calls (no residual). */
 int ds_hip_time_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, int T, int route_mode, int n, float *ms);
+/* Average device time (ms) of n back-to-back ds_hip_layer_forward calls (no residual): one MoE layer
+ * on its own with its input in device memory (a measurement hook, no counterpart in the reference). */
+int ds_hip_time_layer(ds_hip_layer_t *L, float *out_dev, const float *x_dev, int route_mode, int n, float *ms);
 
 /* Prefill GEMM path (no counterpart in the reference): 1 = one persistent kernel with a work queue
  * per XCD, 0 = separate gate_up and down kernels, -1 = automatic (persistent when a grid's blocks

@@ -497,3 +497,32 @@ def test_config5_stack(dev, B, mode):
     finally:
         for h in hs:
             L.ds_hip_layer_destroy(h)
+
+
+def test_timing_hooks_config1_config2(dev, B):
+    """The measurement hooks behind the bench's config-1 and config-2 rows: one expert through the
+    per-function kernel and one layer through ds_hip_layer_forward, timed on the device; the expert
+    hook's kernel is the one ds_expert_forward_fused_int4 launches, whose output matches the oracle's
+    ds_expert_forward_fused_int4 bit for bit (checked here through that API on the same blocks)."""
+    L = dev.load()
+    h, rf, rb = make_device_layer(dev, 302)
+    try:
+        lay = export_layer(dev, B, h, rf, rb)
+        g, d = lay.gu[0], lay.dn[0]
+        gb, db = dev.block_from_arrays(g.q, g.scale, g.offset), dev.block_from_arrays(d.q, d.scale, d.offset)
+        x = B.normal_f32(1280, 4712)
+        ms = C.c_float(0)
+        dev.check(L.ds_hip_time_expert(C.byref(gb), C.byref(db), 1280, 896, x.ctypes.data, 5, C.byref(ms)), "expert")
+        assert 0.0 < ms.value < 1.0
+        y = np.empty(1280, np.float32)
+        L.ds_expert_forward_fused_int4(y, x, C.byref(gb), C.byref(db), 1280, 896, None, None, None, None)
+        ref = np.empty(1280, np.float32)
+        B.oracle().or_expert_int8(ref, x, C.byref(g.or_block()), C.byref(d.or_block()), 1280, 896, 0)
+        assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+        xd = dev.DeviceBuffer.from_array(x)
+        od = dev.DeviceBuffer(1280 * 4)
+        dev.check(L.ds_hip_time_layer(h, od.ptr, xd.ptr, dev.ROUTE_CFG, 5, C.byref(ms)), "layer")
+        assert 0.0 < ms.value < 1.0
+        print(f"timing hooks: expert {1e3 * ms.value:.2f} us per layer call")
+    finally:
+        L.ds_hip_layer_destroy(h)
