@@ -375,7 +375,8 @@ int ds_hip_layer_prefill(ds_hip_layer_t *L, float *out_dev, const float *x_dev, 
   key.spin_max = g_pf_spin_max;
   if (!L->pf_exec || memcmp(&key, &L->pf_key, sizeof key) != 0) {
     /* the seven kernels (and the idx/w copies) captured once, then one graph launch per call */
-    if (L->pf_exec) {
+    if (L->pf_exec) { /* an earlier call's launch of it may still run on the stream */
+      DSR_TRY(hipStreamSynchronize(dsr_stream), "prefill graph");
       hipGraphExecDestroy(L->pf_exec);
       L->pf_exec = NULL;
     }
@@ -1522,6 +1523,8 @@ int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int n_
   if (!S || !xs_dev || !tokens_dev || stride < 0 || n_rows < 1 || n_tokens < 1)
     return dsr_failf("ds_hip_stack_bind: invalid arguments (need xs_dev, tokens_dev, stride >= 0, n_rows >= 1, "
                      "n_tokens >= 1)");
+  /* an earlier launch of the old graph may still run on the stream: let it finish first */
+  DSR_TRY(hipStreamSynchronize(dsr_stream), "bind");
   if (S->exec) {
     hipGraphExecDestroy(S->exec);
     S->exec = NULL;
