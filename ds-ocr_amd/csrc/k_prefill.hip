@@ -316,6 +316,57 @@ __global__ void __launch_bounds__(256) k_pf_scores_bf16(const uint16_t *__restri
 }
 
 
+// The same scores with each lane's share of its router row held in registers, for H = 32·N32 when
+// every row takes the reference's 4- or 2-row group path (no single rows): a block loads its 64
+// rows once (group g of 4 lanes = expert g; lane L holds columns 32i + 8L .. + 7 for every i) and
+// runs its tpb tokens from LDS, one token row per pass (double-buffered: the next token's loads are
+// in flight during the current pass), with the chains, order and tree of avx_row
+// (avx_row_regs32). The rows stream from L2 once per block instead of once per token.
+template <int N32>
+__global__ void __launch_bounds__(256) k_pf_scores_bf16r(const uint16_t *__restrict__ Wr, const float *__restrict__ X,
+                                                         int T, int E, int tpb, float *__restrict__ ps) {
+  constexpr int H = 32 * N32, NX = H / 4, XL = (NX + 255) / 256;
+  __shared__ __attribute__((aligned(16))) float xs[2][H];
+  const int L = threadIdx.x & 3, g = threadIdx.x >> 2, e = min(g, E - 1);
+  const int t0 = blockIdx.x * tpb, nt = min(tpb, T - t0);
+  if (nt <= 0) return;  // uniform per block: no barrier is skipped by part of a block
+  u32x4 wv[N32];
+  const u32x4 *wrow = (const u32x4 *)(Wr + (size_t)e * H) + L;
+#pragma unroll
+  for (int i = 0; i < N32; i++) wv[i] = wrow[4 * i];
+  f32x4 xr[XL];
+  auto load_x = [&](int t) {
+#pragma unroll
+    for (int j = 0; j < XL; j++) xr[j] = ((const f32x4 *)(X + (size_t)t * H))[min((int)threadIdx.x + 256 * j, NX - 1)];
+  };
+  auto store_x = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < XL; j++) {
+      const int i = threadIdx.x + 256 * j;
+      if (i < NX) ((f32x4 *)xs[b])[i] = xr[j];
+    }
+  };
+  load_x(t0);
+  store_x(0);
+  if (nt > 1) load_x(t0 + 1);
+  __syncthreads();
+  for (int k = 0; k < nt; k++) {
+    const float v = avx_row_regs32<N32>(wv, xs[k & 1], L, true, 0.0f);
+    if (k + 1 < nt) {
+      store_x((k + 1) & 1);  // the buffer of token k - 1, which every wave finished before the last barrier
+      if (k + 2 < nt) load_x(t0 + k + 2);
+    }
+    if (L == 0) {
+      float *o = ps + (size_t)(t0 + k) * 4 * 64;
+      o[g] = g < E ? v : 0.0f;
+      o[64 + g] = 0.0f;
+      o[128 + g] = 0.0f;
+      o[192 + g] = 0.0f;
+    }
+    __syncthreads();
+  }
+}
+
 // DECODE: one wave per token, x's limbs (pf_x_limbs), then the fast-exp softmax over all experts
 // and top-k (route_select) on the scores of k_pf_scores_bf16.
 __global__ void __launch_bounds__(256) k_pf_select_dec(const float *__restrict__ X, int T, int H, int E, int K,
@@ -1381,8 +1432,22 @@ hipError_t dsh_launch_prefill(const dsh_layer_t *L, const float *X, int T, int r
       k_pf_route_cfg<false><<<(T + 3) / 4, 256, 0, s>>>(L->router_f32_t, X, T, H, E, K, w.X0, w.X1, w.xsc, w.xsum,
                                                          w.idx, w.w);
   } else {
-    k_pf_scores_bf16<<<(T + PF_TB - 1) / PF_TB, 256, (size_t)PF_TB * H * sizeof(float), s>>>(
-        L->router_bf16, X, T, H, E, nthreads, w.ps);
+    // every row on a group path: the chunks of the reference's threads all have an even length
+    const int chunk = dsh_chunk_len(E, nthreads);
+    bool grouped = true;
+    for (int s0 = 0; s0 < E; s0 += chunk) grouped = grouped && (min(chunk, E - s0) % 2 == 0);
+    const int tpb = (T + 255) / 256, nbr = (T + tpb - 1) / tpb;
+#define PFR(N)                                                                                                      \
+  case N:                                                                                                           \
+    k_pf_scores_bf16r<N><<<nbr, 256, 0, s>>>(L->router_bf16, X, T, E, tpb, w.ps);                                 \
+    break;
+    if (grouped && H % 256 == 0 && H <= 1280) {
+      switch (H / 32) { PFR(8) PFR(16) PFR(24) PFR(32) PFR(40) }
+    } else {
+      k_pf_scores_bf16<<<(T + PF_TB - 1) / PF_TB, 256, (size_t)PF_TB * H * sizeof(float), s>>>(
+          L->router_bf16, X, T, H, E, nthreads, w.ps);
+    }
+#undef PFR
     k_pf_select_dec<<<(T + 3) / 4, 256, 0, s>>>(X, T, H, E, K, w.ps, w.X0, w.X1, w.xsc, w.xsum, w.idx, w.w);
   }
   const int n_items_max = pf_max_routed_items(L, T) + pf_shared_items(T);

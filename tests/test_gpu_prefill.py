@@ -300,3 +300,54 @@ def test_prefill_wait_expiry_reaches_the_caller(dev, B):
 
 
 L_DEFAULT = -2147483647 - 1  # DS_HIP_PREFILL_WAIT_DEFAULT
+
+
+@pytest.mark.parametrize("threads", [8, 16])
+def test_prefill_decode_scores_both_kernels(dev, B, threads):
+    """DECODE routing's scores in the reference's bf16 AVX-512 order from both scores kernels: with
+    16 experts, 8 reference threads make chunks of 2 rows (every row on the 2-row group path: the
+    kernel that keeps each lane's router columns in registers) and 16 threads chunks of 1 (single
+    rows: the kernel that reads the rows per token). Indices and weights bit for bit."""
+    L = dev.load()
+    lay = B.make_moe_layer(67, hidden=256, inter=128, n_experts=16)
+    h = upload_layer(dev, lay)
+    old = L.ds_get_threads()
+    try:
+        L.ds_set_threads(threads)
+        T = 37
+        X = np.stack([B.normal_f32(256, 14000 + t) for t in range(T)])
+        out, idx, w = gpu_prefill(dev, h, X, 0)
+        for t in range(T):
+            sc = np.empty(16, np.float32)
+            B.oracle().or_bf16_matvec_avx512(sc, X[t], lay.router_bf16, 256, 16, threads)
+            ri, rw = np.empty(6, np.int32), np.empty(6, np.float32)
+            B.oracle().or_softmax_topk_decode(ri, rw, sc, 16, 6)
+            assert np.array_equal(ri, idx[t]), (t, ri, idx[t])
+            assert np.array_equal(rw.view(np.uint32), w[t].view(np.uint32)), t
+    finally:
+        L.ds_set_threads(old)
+        L.ds_hip_layer_destroy(h)
+
+
+def test_prefill_config3_decode_routing(dev, B):
+    """Config 3 in DECODE routing (the bf16 router in the reference's AVX-512 order; one reference
+    thread: all 64 rows in 4-row groups, the register-resident scores kernel): indices and weights
+    bit for bit on all 662 tokens, output within the tolerance of the f64 brute force on 24 sampled
+    tokens."""
+    L = dev.load()
+    T, H = 662, 1280
+    h, rf, rb = make_device_layer(dev, 303)
+    try:
+        X = np.stack([B.normal_f32(H, 15000 + t) for t in range(T)])
+        out, idx, w = gpu_prefill(dev, h, X, 0)
+        lay = export_layer(dev, B, h, rf, rb)
+        check_routing(B, lay, X, idx, w, 0)
+        rows = np.linspace(0, T - 1, 24).astype(int)
+        ref = np.empty((len(rows), H), np.float64)
+        B.oracle().or_prefill_moe_f64(ref, np.ascontiguousarray(X[rows]), len(rows), C.byref(lay.or_layer()),
+                                     np.ascontiguousarray(idx[rows]), np.ascontiguousarray(w[rows]))
+        err = rel_err(out[rows], ref)
+        print(f"config-3 prefill, DECODE routing: max rel err {err:.2e} on {len(rows)} tokens")
+        assert err < TOL
+    finally:
+        L.ds_hip_layer_destroy(h)
