@@ -351,3 +351,27 @@ def test_prefill_config3_decode_routing(dev, B):
         assert err < TOL
     finally:
         L.ds_hip_layer_destroy(h)
+
+
+@pytest.mark.parametrize("hidden", [512, 1024, 2048])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_prefill_hidden_sizes(dev, B, mode, hidden):
+    """The routing kernels at other hidden sizes: CFG scores in ds_linear's order (the router staged
+    in 128-row chunks: 4, 8 and 16 of them) and DECODE scores with the router columns in registers
+    (512, 1024) or streamed per token (2048); indices bit for bit, weights as check_routing asks;
+    the block output within the tolerance of the f64 brute force."""
+    L = dev.load()
+    lay = B.make_moe_layer(68 + hidden // 512, hidden=hidden, inter=128, n_experts=16)
+    h = upload_layer(dev, lay)
+    try:
+        T = 21
+        X = np.stack([B.normal_f32(hidden, 16000 + t) for t in range(T)])
+        out, idx, w = gpu_prefill(dev, h, X, mode)
+        check_routing(B, lay, X, idx, w, mode)
+        ref = np.empty((T, hidden), np.float64)
+        B.oracle().or_prefill_moe_f64(ref, X, T, C.byref(lay.or_layer()), idx, w)
+        err = rel_err(out, ref)
+        print(f"prefill hidden={hidden} mode={mode}: max rel err {err:.2e}")
+        assert err < TOL
+    finally:
+        L.ds_hip_layer_destroy(h)
