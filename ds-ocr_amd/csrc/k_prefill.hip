@@ -194,6 +194,7 @@ __global__ void __launch_bounds__(256) k_pf_route_cfg(const float *__restrict__ 
   // chunk c = router rows c·KC .. +KC-1 (KC·E contiguous floats) into LDS rows of 64 (zeros past E),
   // through two register sets: a chunk's loads are issued two chunks before it is stored
   constexpr int NQ = PF_RC_KC * 64 / 4 / 256;  // float4 slots per thread
+  static_assert(4 * NQ == PF_RC_KC / 4, "one piece per four groups of the chain");
   f32x4 ra[NQ], rb[NQ];
   auto load_chunk = [&](f32x4 (&r)[NQ], int c) {
     const float *src = WrT + (size_t)min(c, nch - 1) * PF_RC_KC * E;
@@ -222,6 +223,18 @@ __global__ void __launch_bounds__(256) k_pf_route_cfg(const float *__restrict__ 
       ((f32x4 *)s_wr[buf])[i] = v;
     }
   };
+  // piece j of a chunk (every thread's register slot j) into LDS buffer buf: the chain of one chunk
+  // stores the next chunk piece by piece between its groups, so the stores overlap the adds
+  auto store_piece = [&](const f32x4 (&r)[NQ], int buf, int j) {
+    const int i = threadIdx.x + 256 * j;
+    f32x4 v = r[j];
+    if (!E64) {
+      const int e0 = 4 * (i & 15);
+#pragma unroll
+      for (int q = 0; q < 4; q++) v[q] = e0 + q < E ? v[q] : 0.0f;
+    }
+    ((f32x4 *)s_wr[buf])[i] = v;
+  };
   load_chunk(ra, 0);
   load_chunk(rb, 1);
   asm volatile("" ::: "memory");
@@ -230,10 +243,10 @@ __global__ void __launch_bounds__(256) k_pf_route_cfg(const float *__restrict__ 
   load_chunk(ra, 2);
   __syncthreads();
   float s = 0.0f;
-  // chunk c from LDS buffer c & 1; then chunk c + 1 (in r) goes to the other buffer, which every wave
-  // finished before the last barrier, and r is reloaded with chunk c + 3. Unconditional (after the
-  // last chunk a copy of it goes to a buffer that is not read again), so the wait before the stores
-  // leaves the other register set's loads in flight.
+  // chunk c from LDS buffer c & 1; meanwhile chunk c + 1 (in r) goes to the other buffer, which every
+  // wave finished before the last barrier, one piece after every fourth group; then r is reloaded with
+  // chunk c + 3. Unconditional (after the last chunk a copy of it goes to a buffer that is not read
+  // again), so the waits before the stores leave the other register set's loads in flight.
   // The chain reads the router values from LDS through a ring of PF_RC_D groups of 4 steps (two
   // ds_read2st64 each), issued PF_RC_D groups ahead; the scheduling barriers keep the issue order, so
   // each group waits only for its own reads. x comes from registers: xr[q] holds x values 16q .. 16q
@@ -264,9 +277,9 @@ __global__ void __launch_bounds__(256) k_pf_route_cfg(const float *__restrict__ 
         s = __fadd_rn(s, __fmul_rn(xb, wq[slot][i]));
       }
       if (g + PF_RC_D < G) ld(g + PF_RC_D, slot);
+      if ((g & 3) == 3) store_piece(r, (c + 1) & 1, g >> 2);
       __builtin_amdgcn_sched_barrier(0);
     }
-    store_chunk(r, (c + 1) & 1);
     load_chunk(r, c + 3);
     __syncthreads();
   };
