@@ -137,6 +137,24 @@ def topk_tie_scores():
     return s
 
 
+def topk_nonfinite_cases():
+    """Score vectors (64 experts) for the selection's edge cases: NaN scores (never selected:
+    every comparison with NaN is false), -inf and +inf (+inf is selected; its softmax weight is
+    exp(inf - inf) = NaN), scores at or below the -1e30 floor (not selectable: the comparison is
+    strict), fewer selectable experts than K (the remaining slots are index 0, weight 0), all NaN,
+    and ties."""
+    base = B.normal_f32(64, 803, 1.0)
+    cases = []
+    s = base.copy(); s[[3, 17, 40]] = np.nan; cases.append(s)
+    s = base.copy(); s[[5, 9]] = -np.inf; cases.append(s)
+    s = base.copy(); s[11] = np.inf; s[12] = -np.inf; cases.append(s)
+    s = np.full(64, np.float32(-2e30)); s[[2, 30, 50]] = base[[2, 30, 50]]; cases.append(s)
+    s = base.copy(); s[::2] = np.float32(-1e30); cases.append(s)
+    s = np.full(64, np.float32(np.nan)); cases.append(s)
+    s = base.copy(); s[[1, 2, 7]] = s[0]; s[8] = np.nan; cases.append(s)
+    return [c.astype(np.float32) for c in cases]
+
+
 SMALL_LAYER = {"hidden": 256, "inter": 128, "n_experts": 16, "top_k": 6, "n_shared": 2, "seed": 9}
 
 

@@ -275,6 +275,24 @@ def test_topk_ties(dev):
     assert np.abs(w - GOLD["topk_ties.w"]).max() <= 2e-7
 
 
+def test_topk_nonfinite(dev, B):
+    """ds_moe_top_k on the device with NaN, infinite and floor scores, and with fewer selectable
+    experts than K (the oracle's restatement is pinned to the reference on the same cases on the
+    CPU): indices equal; weights NaN where the oracle's are, else within 2 ulp (the device's expf
+    is correctly rounded, glibc's is 1 ulp off on a few arguments)."""
+    L = dev.load()
+    for i, sc in enumerate(G.topk_nonfinite_cases()):
+        idx, w = np.empty(6, np.int32), np.empty(6, np.float32)
+        L.ds_moe_top_k(idx, w, sc, 64, 6)
+        io, wo = np.empty(6, np.int32), np.empty(6, np.float32)
+        B.oracle().or_moe_top_k(io, wo, sc, 64, 6)
+        assert np.array_equal(idx, io), (i, idx, io)
+        nan = np.isnan(wo)
+        assert np.array_equal(np.isnan(w), nan), (i, w, wo)
+        ulp = np.abs(w.view(np.int32).astype(np.int64) - wo.view(np.int32).astype(np.int64))[~nan]
+        assert ulp.max(initial=0) <= 2, (i, w, wo)
+
+
 def test_router_bf16_exact(dev, B):
     L = dev.load()
     Wr = B.normal_bf16(64 * 1280, 11, 0.02)

@@ -122,3 +122,17 @@ def test_excluding_matches_reference(B):
             res.append(R.ds_argmax_matvec_bf16_excluding(x, W, meta["in"], meta["out"], ea.ctypes.data, len(ex)))
         assert res == list(gold[f"excl_v20000.T{T}.idx"])
     R.ds_set_threads(1)
+
+
+def test_topk_nonfinite_matches_reference(B):
+    """ds_moe_top_k on NaN, infinite and floor scores, and with fewer selectable experts than K:
+    the oracle's restatement against the reference's own function, indices and weight bits."""
+    R = B.ref()
+    for i, sc in enumerate(G.topk_nonfinite_cases()):
+        ir, wr = np.empty(6, np.int32), np.empty(6, np.float32)
+        R.ds_moe_top_k(ir, wr, sc, 64, 6)
+        io, wo = np.empty(6, np.int32), np.empty(6, np.float32)
+        B.oracle().or_moe_top_k(io, wo, sc, 64, 6)
+        assert np.array_equal(ir, io), (i, ir, io)
+        assert np.array_equal(np.isnan(wr), np.isnan(wo)), i
+        assert np.array_equal(bits(wr)[~np.isnan(wr)], bits(wo)[~np.isnan(wo)]), i
