@@ -519,7 +519,7 @@ __device__ __forceinline__ void dl_verify_part(const dsh_layer_t &L, const float
 
 // The routed blocks' selection from the accumulated scores, restated by lane = expert of one wave
 // with the same loads, sums and rounds (so the same experts and weights bit for bit): idx/w of rank
-// lane < K. dl_spec_load issues the loads (partial rows v + 4 j, lane's column), dl_spec_finish
+// lane < K, idx -1 for an empty slot (fewer than K scores above -1e30). dl_spec_load issues the loads (partial rows v + 4 j, lane's column), dl_spec_finish
 // adds them in the routed blocks' order and selects.
 template <int RB>
 __device__ __forceinline__ void dl_spec_load(const float *partials, int np, float (&pv)[4][RB]) {
@@ -549,6 +549,7 @@ __device__ __forceinline__ void dl_spec_finish(int E, int K, int np, const float
   route_init(E, K, DSH_ROUTE_CFG, s_red, st);
   route_rounds(st, 0, st.ns);
   route_finish(DSH_ROUTE_CFG, st, idx, w);
+  if (lane >= st.ns) idx = -1;  // an empty slot (the routed blocks use expert 0 with weight 0 there)
 }
 
 // The parts' sums, gathered by the whole block of the last part to finish (wave w: parts PW w ..
@@ -656,7 +657,7 @@ __device__ __forceinline__ void dl_verdict_bounds(const dsh_layer_t &L, const dl
 }
 
 // Whether the intervals certify the routed blocks' own selection (S.s_si, ranks 0 .. K-1) as it
-// stands: its K experts distinct, their intervals strictly ordered in its rank order, the last one's
+// stands: its K experts distinct (no empty slot), their intervals strictly ordered in its rank order, the last one's
 // above every other expert's interval and above -1e30. Then the reference's selection is that one,
 // in that order (wave-uniform result). Interval ends rounded outward as in cert_check.
 template <int CPL>
@@ -681,7 +682,7 @@ __device__ __forceinline__ bool dl_spec_certified(int E, int K, float c, float e
 
 // The verdict, part 1, where dl_spec_certified does not hold (wave 0): the selection certified on
 // the intervals (route_rounds on c, cert_check) or recomputed in ds_linear's order: rank lane's
-// expert and weight (vi, vw); flags bit 0 when recomputed.
+// expert and weight (vi, vw; vi -1 for an empty slot); flags bit 0 when recomputed.
 template <int CPL, int NREP>
 __device__ __forceinline__ void dl_verdict_select(const dsh_layer_t &L, const float *x, bool need_x, float c,
                                                   float epsr, dl_smem<CPL> &S, int &vi, float &vw, int &flags) {
@@ -713,10 +714,11 @@ __device__ __forceinline__ void dl_verdict_select(const dsh_layer_t &L, const fl
     flags = 1;
   }
   route_finish(DSH_ROUTE_CFG, st, vi, vw);
+  if (lane >= st.ns) vi = -1;  // an empty slot: no expert (weight 0)
 }
 
 // The verdict, part 2 (wave 0; the routed blocks' own selection, restated by wave 1, in S.s_si /
-// S.s_sw): compared with the certified one. Returns the state word (1: it stands, 2: the experts in
+// S.s_sw): compared with the certified one, empty slots (-1) in neither set. Returns the state word (1: it stands, 2: the experts in
 // A[16..] need their Δw added; flags bit 1 then) and leaves the record in S.s_vi / S.s_vw: the
 // certified experts in rank order with the weights the layer's output carries.
 template <int CPL>
@@ -758,13 +760,17 @@ __device__ __forceinline__ int dl_verdict_compare(const dsh_layer_t &L, int *A, 
     state = 2;
     flags |= 2;
   }
-  // the record's weights: the routed blocks' for the same experts when the set stands
-  if (!differ && lane < K) {
+  // the record: the routed blocks' weights for the same experts when the set stands; an empty slot
+  // as ds_moe_top_k fills it (expert 0, weight 0)
+  if (lane < K) {
     const int a = S.s_vi[lane];
-    float w_used = 0.0f;
-    for (int k = 0; k < K; k++)
-      if (S.s_si[k] == a) w_used = S.s_sw[k];
-    S.s_vw[lane] = w_used;
+    if (!differ) {
+      float w_used = 0.0f;
+      for (int k = 0; k < K; k++)
+        if (a >= 0 && S.s_si[k] == a) w_used = S.s_sw[k];
+      S.s_vw[lane] = w_used;
+    }
+    S.s_vi[lane] = max(a, 0);
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();

@@ -16,7 +16,7 @@ import ctypes as C
 
 import numpy as np
 import pytest
-from test_gpu_moe import make_device_layer, upload_layer
+from test_gpu_moe import make_device_layer, run_stack, upload_layer
 
 pytestmark = pytest.mark.gpu
 
@@ -168,6 +168,71 @@ def test_config5_stack_routing_certified(dev, B, kernels, ties):
             assert n_re <= n // 10 and c[2] <= n // 10, c
     finally:
         L.ds_hip_stack_destroy(S)
+        log.close()
+        for h in hs:
+            L.ds_hip_layer_destroy(h)
+
+
+@pytest.mark.parametrize("path", ["layer_forward", "stack1", "stack2"])
+def test_nonfinite_inputs_route_like_reference(dev, B, path):
+    """Inputs with a +inf, a NaN or a -inf coordinate (CFG routing, whose reference selection is
+    defined for them: ds_moe_top_k never selects a NaN or floor score and fills empty slots with
+    expert 0, weight 0). Such scores or bounds are never certified, so every expert's score is
+    recomputed in ds_linear's order: an expert's score is ±inf by the sign of its router weight at the
+    +inf coordinate, the +inf scores tie (the lowest indices win) and their softmax weights are NaN as
+    in the reference; a NaN input selects nothing. One +inf coordinate is picked where fewer than K
+    experts, expert 0 among them, have a positive router weight: the empty slots then repeat expert 0,
+    which the one-kernel layers' verifier must not take for a selected expert. Every logged routing
+    (two-kernel layer, one- and two-kernel stacks, whose later layers see the non-finite outputs) must
+    give the oracle's indices, NaN weights where the oracle's are NaN, the rest within 2e-5."""
+    L = dev.load()
+    H, I, E, K, NS, nl = 256, 128, 16, 6, 2, 3
+    lays = [B.make_moe_layer(330 + l, hidden=H, inter=I, n_experts=E, top_k=K, n_shared=NS) for l in range(nl)]
+    hs = [upload_layer(dev, lay) for lay in lays]
+    routers = {l: np.ascontiguousarray(lays[l].router_f32.reshape(E, H)) for l in range(nl)}
+    pos = (routers[0] > 0).sum(axis=0)
+    few = [c for c in range(H) if routers[0][0, c] > 0 and 2 <= pos[c] <= K - 2]
+    many = [c for c in range(H) if pos[c] >= K + 2]
+    assert few and many
+    xs = np.stack([B.normal_f32(H, 3400 + s) for s in range(6)])
+    xs[1, few[0]] = np.inf
+    xs[2, 9] = np.nan
+    xs[4, 3] = -np.inf
+    xs[5, many[0]] = np.inf
+    steps = len(xs)
+    log = RouteLog(dev, 64, H)
+    try:
+        if path == "layer_forward":
+            xd, od = dev.DeviceBuffer(4 * H), dev.DeviceBuffer(4 * H)
+            for s in range(steps):
+                xd.write(xs[s])
+                dev.check(L.ds_hip_layer_forward(hs[0], od.ptr, xd.ptr, dev.ROUTE_CFG, 0, None, None), "forward")
+            dev.check(L.ds_hip_sync(), "sync")
+            expect = steps
+        else:
+            lm_w = B.normal_bf16(5000 * H, 3401, 0.02)
+            lm = dev.DeviceBuffer.from_array(lm_w)
+            run_stack(dev, hs, lm, 5000, xs, dev.ROUTE_CFG, kernels=1 if path == "stack1" else 2)
+            expect = nl * steps
+        idx, w, flags, tags, lx = log.entries()
+        assert len(idx) == expect, (len(idx), expect)
+        n_nan = n_empty = 0
+        for j in range(len(idx)):
+            W = routers[int(tags[j]) if path != "layer_forward" else 0]
+            sc = np.empty(E, np.float32)
+            B.oracle().or_linear_f32(sc, np.ascontiguousarray(lx[j]), W, H, E)
+            ri, rw = np.empty(K, np.int32), np.empty(K, np.float32)
+            B.oracle().or_moe_top_k(ri, rw, sc, E, K)
+            assert np.array_equal(idx[j, :K], ri), (path, j, idx[j, :K], ri, int(flags[j]))
+            nan = np.isnan(rw)
+            n_nan += int(nan.any())
+            n_empty += int(not np.isnan(sc).all() and (rw == 0).any() and ri[0] == 0)
+            assert np.array_equal(np.isnan(w[j, :K]), nan), (path, j, w[j, :K], rw)
+            assert np.allclose(w[j, :K][~nan], rw[~nan], rtol=2e-5, atol=1e-7), (path, j, w[j, :K], rw)
+        print(f"{path}: {len(idx)} routings with non-finite inputs equal to the reference's "
+              f"({n_nan} with NaN weights, {n_empty} with expert 0 selected and empty slots)")
+        assert n_nan >= 2 and n_empty >= 1
+    finally:
         log.close()
         for h in hs:
             L.ds_hip_layer_destroy(h)
