@@ -131,33 +131,6 @@ __device__ __forceinline__ void pf_x_limbs(const float *__restrict__ X, int t, i
 // during the current chunk's chain, one barrier per chunk); each token's x stays in LDS, read as a
 // broadcast. The wave also writes its token's x limbs (pf_x_limbs), then selects and weights the
 // experts (route_select: top-k with strict >, softmax over the k).
-// Lane j of each row of 16 lanes, to every lane of the row (DPP row_newbcast:j); j must fold to a
-// constant (unrolled loops).
-template <int J>
-__device__ __forceinline__ float pf_row_bcast_c(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + J, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float pf_row_bcast(float v, int j) {
-  switch (j) {
-    case 0: return pf_row_bcast_c<0>(v);
-    case 1: return pf_row_bcast_c<1>(v);
-    case 2: return pf_row_bcast_c<2>(v);
-    case 3: return pf_row_bcast_c<3>(v);
-    case 4: return pf_row_bcast_c<4>(v);
-    case 5: return pf_row_bcast_c<5>(v);
-    case 6: return pf_row_bcast_c<6>(v);
-    case 7: return pf_row_bcast_c<7>(v);
-    case 8: return pf_row_bcast_c<8>(v);
-    case 9: return pf_row_bcast_c<9>(v);
-    case 10: return pf_row_bcast_c<10>(v);
-    case 11: return pf_row_bcast_c<11>(v);
-    case 12: return pf_row_bcast_c<12>(v);
-    case 13: return pf_row_bcast_c<13>(v);
-    case 14: return pf_row_bcast_c<14>(v);
-    default: return pf_row_bcast_c<15>(v);
-  }
-}
-
 #define PF_RC_KC 128
 #define PF_RC_WARM 2  // router lines a thread touches to fill its XCD's L2
 #define PF_RC_D 5     // groups of 4 chain steps whose LDS reads are in flight
@@ -247,37 +220,42 @@ __global__ void __launch_bounds__(256) k_pf_route_cfg(const float *__restrict__ 
   // wave finished before the last barrier, one piece after every fourth group; then r is reloaded with
   // chunk c + 3. Unconditional (after the last chunk a copy of it goes to a buffer that is not read
   // again), so the waits before the stores leave the other register set's loads in flight.
-  // The chain reads the router values from LDS through a ring of PF_RC_D groups of 4 steps (two
-  // ds_read2st64 each), issued PF_RC_D groups ahead; the scheduling barriers keep the issue order, so
-  // each group waits only for its own reads. x comes from registers: xr[q] holds x values 16q .. 16q
-  // + 15 of the chunk in every row of 16 lanes (lane l: value 16q + l % 16), and a DPP row broadcast
-  // (row_newbcast) hands value k to all lanes as the multiply's operand.
+  // The chain reads its operands from LDS through a ring of PF_RC_D groups of 4 steps, issued PF_RC_D
+  // groups ahead: per group two ds_read2st64 for the router values (lane = expert) and one 16-byte
+  // read of the token's x values at one address for every lane (a broadcast; a DPP row broadcast
+  // per step instead cost ~3.7 ns a step more in a microbenchmark). The products run one group
+  // ahead of the adds, one between consecutive adds; the scheduling barriers keep that order, so
+  // each group waits only for its own reads.
   auto step = [&](int c, f32x4 (&r)[NQ]) {
     const float *wr = s_wr[c & 1] + lane;
-    const float *xs = s_x[wave] + c * PF_RC_KC + (lane & 15);
+    const float *xs = s_x[wave] + c * PF_RC_KC;
     constexpr int G = PF_RC_KC / 4;
-    float xr[PF_RC_KC / 16];
-#pragma unroll
-    for (int q = 0; q < PF_RC_KC / 16; q++) xr[q] = xs[16 * q];
     float wq[PF_RC_D][4];
+    f32x4 xq[PF_RC_D];
     auto ld = [&](int g, int slot) {
 #pragma unroll
       for (int i = 0; i < 4; i++) wq[slot][i] = wr[64 * (4 * g + i)];
+      xq[slot] = *(const f32x4 *)(xs + 4 * g);  // one address for every lane: a broadcast read
     };
 #pragma unroll
     for (int g = 0; g < PF_RC_D; g++) ld(g, g);
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) p[i] = __fmul_rn(xq[0][i], wq[0][i]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int g = 0; g < G; g++) {
-      const int slot = g % PF_RC_D;
+      float pn[4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int k = 4 * g + i;
-        const float xb = pf_row_bcast(xr[k >> 4], k & 15);
-        s = __fadd_rn(s, __fmul_rn(xb, wq[slot][i]));
+      for (int i = 0; i < 4; i++) {  // one product of the next group between consecutive adds
+        if (g + 1 < G) pn[i] = __fmul_rn(xq[(g + 1) % PF_RC_D][i], wq[(g + 1) % PF_RC_D][i]);
+        s = __fadd_rn(s, p[i]);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      if (g + PF_RC_D < G) ld(g + PF_RC_D, slot);
+      if (g + PF_RC_D < G) ld(g + PF_RC_D, g % PF_RC_D);  // group g's values were used by the last products
       if ((g & 3) == 3) store_piece(r, (c + 1) & 1, g >> 2);
+#pragma unroll
+      for (int i = 0; i < 4; i++) p[i] = pn[i];
       __builtin_amdgcn_sched_barrier(0);
     }
     load_chunk(r, c + 3);
