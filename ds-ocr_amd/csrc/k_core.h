@@ -167,6 +167,13 @@ hipError_t dsh_launch_lm_final_scores(const unsigned long long *cand, int n, int
                                       float *zero_p, int zero_n, const uint16_t *emb, int emb_vocab, float *emb_out,
                                       const float *x_in, int stride, int rows, const float *WrT, int H, int E,
                                       float *partials, hipStream_t s);
+/* After the last step of a run whose steps end with the LM head (dsh_split_t fin_cand / nx_partials):
+ * when *pending, the argmax of cand[0..n) into tokens[*step - 1] and *pending cleared; zero_p[0..zero_n)
+ * cleared (16-byte aligned, zero_n % 4 == 0). */
+hipError_t dsh_launch_lm_token_pending(const unsigned long long *cand, int n, int *tokens, const int *step,
+                                       int *pending, float *zero_p, int zero_n, hipStream_t s);
+/* Router partial rows per partial (dsh_launch_dec_partial_scores): 8 or 16. */
+int dsh_dec_partial_rows(int H);
 /* emb[tokens[*step - 1]][0..H) widened to f32 into out (a token outside [0, emb_vocab): unchanged). */
 hipError_t dsh_launch_embed_next(const int *tokens, const int *step, const uint16_t *emb, int emb_vocab, int H,
                                  float *out, hipStream_t s);
@@ -301,6 +308,22 @@ typedef struct {
   unsigned *vd;
   int *derr;       /* set (system scope) when an extra block's wait for the verdict gives up */
   dsh_rcert_t rc;  /* counters and log (CFG: the verdict's block records; DECODE: the log only) */
+  /* A step with no kernel after the LM head (bound input, no embedding feed). fin_cand (first
+   * layer): its last extra block turns the previous step's LM-head keys (fin_n of them) into that
+   * step's token, tokens[*fin_step - 1], when *fin_pending, and clears the flag. nx_partials (last
+   * layer): its extra blocks write the next step's router partials, from row *nx_step + 1 of nx_in
+   * (stride nx_stride) when that is below nx_rows, in k_dec_partial_scores' order (nx_R rows each
+   * of the transposed router nx_WrT, nx_E experts), and set *nx_pending. Both jobs run in the
+   * DL_PF extra blocks, which they add where the layer reads nothing ahead. */
+  const unsigned long long *fin_cand;
+  int *fin_tokens, *fin_pending;
+  const int *fin_step;
+  int fin_n;
+  const float *nx_in, *nx_WrT;
+  const int *nx_step;
+  float *nx_partials;
+  int *nx_pending;
+  int nx_stride, nx_rows, nx_R, nx_E;
 } dsh_split_t;
 #define DSH_SPLIT_VD_INTS (64 + 256 * 32)
 int dsh_layer_split_supported(const dsh_layer_t *L);

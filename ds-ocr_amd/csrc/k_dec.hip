@@ -964,6 +964,25 @@ __global__ void __launch_bounds__(64) k_lm_final_scores(const unsigned long long
   partials[(size_t)blockIdx.x * 64 + lane] = lane < E ? p : 0.0f;
 }
 
+// After the last step of a run whose steps end with the LM head: the pending token (the argmax of
+// the last step's keys; the LM head has advanced the step counter) and the last copies regions.
+__global__ void __launch_bounds__(256) k_lm_token_pending(const unsigned long long *__restrict__ cand, int n,
+                                                         int *__restrict__ tokens, const int *__restrict__ step,
+                                                         int *__restrict__ pending, float *__restrict__ zero_p,
+                                                         int zero_n) {
+  for (int i = 4 * (blockIdx.x * 256 + threadIdx.x); i < zero_n; i += 4 * 256 * (int)gridDim.x)
+    *(f32x4 *)(zero_p + i) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (blockIdx.x != 0 || threadIdx.x >= 64 || *pending == 0) return;
+  const int lane = threadIdx.x;
+  unsigned long long b = 0ull;
+  for (int i = lane; i < n; i += 64) b = dsh_umax64(b, cand[i]);
+  b = dsh_wave_max_u64(b);
+  if (lane == 0) {
+    tokens[*step - 1] = dsh_key_index(b);
+    *pending = 0;
+  }
+}
+
 // ============================================================================ launchers
 // Rows per down block (and per router partial): keeps the partial count within 4 * ROUTE_BATCH.
 static inline int dec_rows(int H) { return H <= 32 * ROUTE_BATCH ? 8 : 16; }
@@ -980,6 +999,17 @@ int dsh_dec_supported(int H, int I, int E, int K, int SI) {
 }
 
 int dsh_dec_partials(int H) { return H / dec_rows(H); }
+
+int dsh_dec_partial_rows(int H) { return dec_rows(H); }
+
+hipError_t dsh_launch_lm_token_pending(const unsigned long long *cand, int n, int *tokens, const int *step,
+                                       int *pending, float *zero_p, int zero_n, hipStream_t s) {
+  if (!cand || n <= 0 || !tokens || !step || !pending || ((uintptr_t)zero_p & 15) || zero_n % 4 || zero_n < 0)
+    return hipErrorInvalidValue;
+  k_lm_token_pending<<<max(1, min(16, (zero_n + 1023) / 1024)), 256, 0, s>>>(cand, n, tokens, step, pending, zero_p,
+                                                                            zero_n);
+  return hipGetLastError();
+}
 
 hipError_t dsh_launch_row_norms(const float *A, int rows, int cols, float *out, hipStream_t s) {
   if (rows <= 0 || cols <= 0) return hipErrorInvalidValue;

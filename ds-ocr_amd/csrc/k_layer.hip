@@ -426,12 +426,64 @@ __device__ __forceinline__ unsigned dl_pf_fold(const u32x4 (&v)[DL_PFV(CPL)]) {
   return acc;
 }
 
+// The next step's router partials (F.nx_partials; the last layer's extra block p): wave w of the
+// block takes partials 8 p + w, 8 p + w + 8 DL_PF, ... of R rows each, lane = expert, as
+// k_dec_partial_scores computes them (a fused multiply-add chain over the rows in order from 0).
+// The step counter is still this step's (the LM head advances it after this kernel).
+template <int CPL, int R>
+__device__ __forceinline__ void dl_next_partials_r(const dsh_split_t &F, int p, const float *x) {
+  constexpr int H = 256 * CPL;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, E = F.nx_E;
+  for (int g = 8 * p + wave; g < H / R; g += 8 * DL_PF) {
+    const int r0 = g * R;
+    float acc = 0.0f;
+    if (lane < E) {
+      float w[R], xv[R];
+#pragma unroll
+      for (int j = 0; j < R; j++) {
+        w[j] = F.nx_WrT[(size_t)(r0 + j) * E + lane];
+        xv[j] = x[r0 + j];
+      }
+#pragma unroll
+      for (int j = 0; j < R; j++) acc = __builtin_fmaf(w[j], xv[j], acc);
+    }
+    F.nx_partials[(size_t)g * 64 + lane] = lane < E ? acc : 0.0f;
+  }
+}
+template <int CPL>
+__device__ __forceinline__ void dl_next_partials(const dsh_split_t &F, int p) {
+  const int sn = *F.nx_step + 1;
+  if (p == 0 && threadIdx.x == 0) *F.nx_pending = 1;  // this step's token: the LM head's keys, turned later
+  if (sn >= F.nx_rows) return;                        // no next row in the bound input
+  const float *x = F.nx_in + (size_t)sn * F.nx_stride;
+  if (F.nx_R == 8)
+    dl_next_partials_r<CPL, 8>(F, p, x);
+  else
+    dl_next_partials_r<CPL, 16>(F, p, x);
+}
+
+// The previous step's token from its LM-head keys, when one is pending (F.fin_cand; one wave of
+// the first layer's last extra block).
+__device__ __forceinline__ void dl_finish_token(const dsh_split_t &F) {
+  const int lane = threadIdx.x & 63;
+  if (*F.fin_pending == 0) return;
+  unsigned long long b = 0ull;
+  for (int i = lane; i < F.fin_n; i += 64) b = dsh_umax64(b, F.fin_cand[i]);
+  b = dsh_wave_max_u64(b);
+  if (lane == 0) {
+    F.fin_tokens[*F.fin_step - 1] = dsh_key_index(b);
+    *F.fin_pending = 0;
+  }
+}
+
 // Extra block p's share (after clearing its share of the region to clear).
 template <int CPL>
 __device__ __forceinline__ void dl_prefetch(const dsh_split_t &F, int p, float *x_out, float *zero_p, int zero_n) {
   const int t = threadIdx.x;
   for (int i = blockIdx.x * 512 + t; i < zero_n; i += gridDim.x * 512) zero_p[i] = 0.0f;
-  const int ns = F.pf_SI / DL_UB;
+  if (F.nx_partials) dl_next_partials<CPL>(F, p);
+  if (F.fin_cand && p == DL_PF - 1 && t < 64) dl_finish_token(F);
+  const int ns = F.pf_gu ? F.pf_SI / DL_UB : 0;
   unsigned acc = 0;
   for (int sl = p; sl < ns; sl += DL_PF) {
     u32x4 v[DL_PFV(CPL)];
@@ -1117,8 +1169,14 @@ hipError_t dsh_launch_dec_layer(const dsh_layer_t *L, const dsh_split_t *F, cons
                                 const float *resid, float *x_out, float *lg_out, float *zero_p, int zero_n,
                                 hipStream_t s) {
   static_assert(DL_VX <= DSH_SPLIT_VD_INTS, "verdict area");
-  const int nb = dsh_layer_split_blocks(L) + (F->vd ? DL_NPART : 0) + (F->pf_gu ? DL_PF : 0);
+  const int extra = F->pf_gu || F->nx_partials || F->fin_cand;
+  const int nb = dsh_layer_split_blocks(L) + (F->vd ? DL_NPART : 0) + (extra ? DL_PF : 0);
   if (ncopies != 1 && ncopies != DL_REP) return hipErrorInvalidValue;
+  if (F->nx_partials && (!F->nx_in || !F->nx_WrT || !F->nx_step || !F->nx_pending || F->nx_stride < 0 ||
+                         (F->nx_R != 8 && F->nx_R != 16) || L->H % F->nx_R || L->H / F->nx_R > 8 * DL_PF ||
+                         F->nx_E <= 0 || F->nx_E > 64))
+    return hipErrorInvalidValue;
+  if (F->fin_cand && (!F->fin_tokens || !F->fin_step || !F->fin_pending || F->fin_n <= 0)) return hipErrorInvalidValue;
   if (F->vd && (route_mode != DSH_ROUTE_CFG || F->Wr_dec || !dsh_layer_cert_supported(L) ||
                 ((uintptr_t)F->vd & 127)))
     return hipErrorInvalidValue;

@@ -823,6 +823,13 @@ struct ds_hip_stack {
    * CFG routing, no dense layer, attention or sampling rules, the head on the layer copies): the
    * partials always belong to the current step's input (reset and every run call compute them) */
   int merged;
+  /* the step ends with the LM head (merged, the bound input without the embedding feed, at least 3
+   * layers): the first layer's extra block turns the previous step's LM-head keys into its token,
+   * the first two layers clear the last two copies regions, and the last layer's extra blocks
+   * compute the next step's router partials; one kernel after a run's steps (tail_enqueue) finishes
+   * its last token and clears those regions */
+  int tailed;
+  int *pending; /* the last step's token is still in the LM-head keys (in work, beside step) */
   /* autoregressive input (ds_hip_stack_set_embedding): step s >= 1 reads the widened embedding of
    * token s - 1, which the step before wrote into ebuf */
   const uint16_t *emb;
@@ -947,6 +954,7 @@ ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers,
   S->work_bytes = bytes;
   hipMemsetAsync(S->work, 0, bytes, dsr_stream);
   S->step = (int *)S->work;
+  S->pending = S->step + 1;
   S->xbuf = (float *)((char *)S->work + off_x);
   S->cand = (unsigned long long *)((char *)S->work + off_c);
   S->partials[0] = (float *)((char *)S->work + off_p);
@@ -1114,7 +1122,7 @@ static int stack_names(const ds_hip_stack_t *S, const char **names) {
     }
   }
   NM("lm_head.argmax");
-  NM(S->merged ? "lm_head.final+scores" : "lm_head.final");
+  if (!S->tailed) NM(S->merged ? "lm_head.final+scores" : "lm_head.final");
   if (smp_active(S)) NM("sample");
 #undef NM
   return n;
@@ -1207,6 +1215,7 @@ static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *ne
  * into region l; it also clears region l - 2, read by layer l - 2 (every region is zero at the
  * end of a step). The copy sum then writes the plain output for the LM head. */
 static float *xc_region(const ds_hip_stack_t *S, int l) { return S->xc + (size_t)l * S->xc_region; }
+static int lm_keys(const ds_hip_stack_t *S);
 
 static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *nev) {
   hipError_t e = hipSuccess;
@@ -1220,10 +1229,29 @@ static hipError_t split_layers_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *n
                        S->route_mode, S->bf16sim, S->threads, S->partials[0], &np0);
     if (e == hipSuccess) e = mark(ev, nev);
   }
+  /* a step that ends with the LM head: the first layer finishes the previous step's token, the last
+   * computes the next step's router partials (the step counter is still this step's there) */
+  dsh_split_t *F0 = &S->sp[0], *FL = &S->sp[NL - 1];
+  F0->fin_cand = S->tailed ? S->cand : NULL;
+  F0->fin_n = S->tailed ? lm_keys(S) : 0;
+  F0->fin_tokens = S->tailed ? S->tokens : NULL;
+  F0->fin_step = S->tailed ? S->step : NULL;
+  F0->fin_pending = S->tailed ? S->pending : NULL;
+  FL->nx_partials = S->tailed ? S->partials[0] : NULL;
+  FL->nx_in = S->tailed ? S->in : NULL;
+  FL->nx_step = S->tailed ? S->in_step : NULL;
+  FL->nx_stride = S->in_stride;
+  FL->nx_rows = S->rows;
+  FL->nx_R = dsh_dec_partial_rows(H);
+  FL->nx_E = S->layers[0]->E;
+  FL->nx_WrT = S->tailed ? S->layers[0]->d.router_f32_t : NULL;
+  FL->nx_pending = S->tailed ? S->pending : NULL;
   for (int l = 0; l < NL && e == hipSuccess; l++) {
     const ds_hip_layer_t *L = S->layers[l];
     float *out = xc_region(S, l);
-    float *zp = l >= 2 ? xc_region(S, l - 2) : NULL;
+    /* layer l clears region l - 2; with the step ending at the LM head, layers 0 and 1 clear the
+     * last two regions, which the final kernel clears otherwise */
+    float *zp = l >= 2 ? xc_region(S, l - 2) : S->tailed && l < 2 ? xc_region(S, NL - 2 + l) : NULL;
     if (l == 0) {
       e = dsh_launch_dec_layer(&L->d, &S->sp[l], dense ? S->xbuf : S->in, dense ? NULL : S->in_step,
                                dense ? 0 : S->in_stride, 1, S->partials[0], np0, mode, NULL, out, out + (size_t)C * H, zp,
@@ -1464,8 +1492,10 @@ static hipError_t step_enqueue(ds_hip_stack_t *S, hipEvent_t *ev) {
                                       T > 1 ? (S->vocab + T - 1) / T : S->vocab, dsr_stream);
   }
   if (e == hipSuccess) e = mark(ev, &n);
-  if (e == hipSuccess) e = final_enqueue(S, clear_in_final);
-  if (e == hipSuccess) e = mark(ev, &n);
+  if (!S->tailed) {
+    if (e == hipSuccess) e = final_enqueue(S, clear_in_final);
+    if (e == hipSuccess) e = mark(ev, &n);
+  }
   if (e == hipSuccess && smp_active(S)) {
     /* the repetition penalty and the n-gram ban over this stack's earlier tokens, then (embedding
      * feed) the final token's row; one event after all of these kernels */
@@ -1547,6 +1577,7 @@ int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int n_
   S->split = split_eligible(S);
   if (S->split && split_build(S)) return -1;
   S->merged = merged_eligible(S);
+  S->tailed = S->merged && !S->emb && S->n_layers >= 3;
   DSR_TRY(hipStreamBeginCapture(dsr_stream, hipStreamCaptureModeThreadLocal), "graph capture begin");
   hipError_t e = step_enqueue(S, NULL);
   hipGraph_t g = NULL;
@@ -1589,11 +1620,21 @@ static int steps_check(const ds_hip_stack_t *S, int n, const char *who) {
   return 0;
 }
 
+/* After a run's steps when they end with the LM head: the last step's token (if still pending) and
+ * the last two copies regions cleared. */
+static hipError_t tail_enqueue(ds_hip_stack_t *S) {
+  if (!S->tailed) return hipSuccess;
+  const int NL = S->n_layers;
+  return dsh_launch_lm_token_pending(S->cand, lm_keys(S), S->tokens, S->step, S->pending, xc_region(S, NL - 2),
+                                     (int)(2 * S->xc_region), dsr_stream);
+}
+
 static int graph_steps(ds_hip_stack_t *S, int n_steps) {
   for (int i = 0; i < n_steps; i++) {
     DSR_TRY(hipGraphLaunch(S->exec, dsr_stream), "graph launch");
     S->done++;
   }
+  DSR_TRY(tail_enqueue(S), "run tail");
   return 0;
 }
 
@@ -1609,6 +1650,7 @@ int ds_hip_stack_run_eager(ds_hip_stack_t *S, int n_steps) {
     S->done++;
     if (e != hipSuccess) return dsr_fail("decode step", e);
   }
+  DSR_TRY(tail_enqueue(S), "run tail");
   return 0;
 }
 
@@ -1662,6 +1704,7 @@ int ds_hip_time_stack_each(ds_hip_stack_t *S, int n_steps, float *ms_each) {
     S->done++;
     if (e == hipSuccess) e = hipEventRecord(ev[i + 1], dsr_stream);
   }
+  if (e == hipSuccess) e = tail_enqueue(S);
   if (e == hipSuccess) e = hipEventSynchronize(ev[n_steps]);
   for (int i = 0; i < n_steps && e == hipSuccess; i++) e = hipEventElapsedTime(&ms_each[i], ev[i], ev[i + 1]);
   events_destroy(ev, n_steps + 1);
@@ -1689,6 +1732,7 @@ int ds_hip_time_stack_span(ds_hip_stack_t *S, int n_steps, int k0, int k1, float
     e = step_enqueue(S, marks);
     S->done++;
   }
+  if (e == hipSuccess) e = tail_enqueue(S);
   if (e == hipSuccess) e = hipEventSynchronize(ev[2 * n_steps - 1]);
   for (int i = 0; i < n_steps && e == hipSuccess; i++) e = hipEventElapsedTime(&ms_each[i], ev[2 * i], ev[2 * i + 1]);
   events_destroy(ev, 2 * n_steps);
@@ -1767,6 +1811,7 @@ int ds_hip_profile_stack(ds_hip_stack_t *S, int n_steps, float *ms_out) {
       acc[i] += m;
     }
   }
+  if (rc == 0 && tail_enqueue(S) != hipSuccess) rc = -1;
   for (int i = 0; i < nk; i++) ms_out[i] = (float)(acc[i] / n_steps);
   for (int i = 0; i <= nk; i++)
     if (ev[i]) hipEventDestroy(ev[i]);
