@@ -211,3 +211,80 @@ def test_rewritten_input_rows_are_seen(dev, B):
     finally:
         for h in hs:
             L.ds_hip_layer_destroy(h)
+
+
+def test_step_ending_at_the_lm_head_across_runs(dev, B):
+    """Three one-kernel layers, CFG routing, bound input: the step ends with the LM head. The last
+    layer's extra blocks compute the next step's router partials, the next step's first layer turns
+    the previous step's keys into its token, and one kernel after each run finishes the last token.
+    Eight steps run in chunks (1, 0 and 3 graph steps, 2 eager steps, then 2 graph steps after rows 6
+    and 7 are rewritten) must give every token and the chunk-end hidden states of a stack bound to
+    the final rows and run one step per call, and the oracle's hidden states."""
+    L = dev.load()
+    H, vocab, n = 256, 3000, 8
+    lays, hs, lm_w = small_stack(dev, B, 580, n_layers=3)
+    lm = dev.DeviceBuffer.from_array(lm_w)
+    xs = np.stack([B.normal_f32(H, 5800 + s) for s in range(n)])
+    xs_new = xs.copy()
+    xs_new[6:] = np.stack([B.normal_f32(H, 5900 + s) for s in range(2)])
+    arr = (C.c_void_p * len(hs))(*hs)
+
+    def make(xd, td):
+        S = L.ds_hip_stack_create(arr, len(hs), lm.ptr, vocab, dev.ROUTE_CFG)
+        assert S, L.ds_hip_last_error()
+        dev.check(L.ds_hip_stack_set_layer_kernels(S, 1), "kernels")
+        dev.check(L.ds_hip_stack_bind(S, xd.ptr, H, n, td.ptr, n), "bind")
+        names = [L.ds_hip_stack_kernel_name(S, i).decode() for i in range(L.ds_hip_stack_kernel_count(S))]
+        assert names == ["layer"] * 3 + ["lm_head.argmax"], names
+        return S
+
+    def hidden(S):
+        hx = np.empty(H, np.float32)
+        dev.check(L.ds_hip_stack_hidden(S, hx), "hidden")
+        return hx
+
+    try:
+        # reference: bound to the final rows, one step per run call
+        xd_r, td_r = dev.DeviceBuffer.from_array(xs_new), dev.DeviceBuffer(4 * n)
+        S = make(xd_r, td_r)
+        try:
+            hid_ref = []
+            for s in range(n):
+                dev.check(L.ds_hip_stack_run(S, 1), "run")
+                hid_ref.append(hidden(S))
+            toks_ref = td_r.to_array(np.int32)
+        finally:
+            L.ds_hip_stack_destroy(S)
+        # chunked: the steps that end each chunk are 0, 3, 5 and 7
+        xd, td = dev.DeviceBuffer.from_array(xs), dev.DeviceBuffer(4 * n)
+        S = make(xd, td)
+        ends = {}
+        try:
+            dev.check(L.ds_hip_stack_run(S, 1), "run 1")
+            ends[0] = hidden(S)
+            dev.check(L.ds_hip_stack_run(S, 0), "run 0")
+            dev.check(L.ds_hip_stack_run(S, 3), "run 3")
+            ends[3] = hidden(S)
+            dev.check(L.ds_hip_stack_run_eager(S, 2), "eager 2")
+            ends[5] = hidden(S)
+            dev.check(L.ds_hip_sync(), "sync")
+            xd.write(xs_new)
+            dev.check(L.ds_hip_stack_run(S, 2), "run 2")
+            ends[7] = hidden(S)
+            toks = td.to_array(np.int32)
+        finally:
+            L.ds_hip_stack_destroy(S)
+        _, rh = oracle_decode(B, lays, lm_w, vocab, xs_new, dev.ROUTE_CFG)
+        for s in range(n):
+            err = rel_err(hid_ref[s], rh[s])
+            assert err < TOL, (s, err)
+            assert toks_ref[s] == B.oracle().or_argmax_bf16(hid_ref[s], lm_w, H, vocab, 1, None), s
+        for s, hx in ends.items():
+            err, err_ref = rel_err(hx, rh[s]), rel_err(hx, hid_ref[s])
+            print(f"chunked run, step {s}: vs oracle {err:.2e}, vs one step per call {err_ref:.2e}")
+            assert err < TOL and err_ref < 1e-5
+            assert toks[s] == B.oracle().or_argmax_bf16(hx, lm_w, H, vocab, 1, None), s
+        assert np.array_equal(toks, toks_ref), (toks, toks_ref)
+    finally:
+        for h in hs:
+            L.ds_hip_layer_destroy(h)
