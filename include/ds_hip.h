@@ -344,7 +344,10 @@ int ds_hip_steps_fit(int capacity, int steps_done, int n);
 /* Zeroes the step counter and the step's work buffers (with the embedding feed, row 0 of the bound
  * input becomes the next step's input). */
 int ds_hip_stack_reset(ds_hip_stack_t *S);
-/* Launches n_steps decode steps (one graph launch each), asynchronously. */
+/* Launches n_steps decode steps (one graph launch each), asynchronously. Every step's token is in
+ * tokens_dev once the launched work completes. (With one-kernel layers in CFG routing, at least 3
+ * layers and the bound input, a step ends with the LM head: the next step's first layer writes the
+ * previous step's token, and one kernel after the run's last step writes its token.) */
 int ds_hip_stack_run(ds_hip_stack_t *S, int n_steps);
 /* Same steps launched kernel by kernel, without the graph. */
 int ds_hip_stack_run_eager(ds_hip_stack_t *S, int n_steps);
@@ -366,8 +369,9 @@ int ds_hip_time_stack_span(ds_hip_stack_t *S, int n_steps, int k0, int k1, float
 /* Average time of the LM-head argmax kernel over n back-to-back launches on the stack's current
  * hidden state (no token written; includes the launch gaps). */
 int ds_hip_time_lm_head(ds_hip_stack_t *S, int n, float *ms);
-/* Kernels one decode step launches, and the kind of kernel i ("scores", "gate_up", "down",
- * "lm_head.argmax", "lm_head.final"). */
+/* Kernels one decode step launches, and the kind of kernel i ("scores", "gate_up", "down", "layer",
+ * "lm_head.argmax", "lm_head.final", "lm_head.final+scores"; no final kernel where the step ends with
+ * the LM head). */
 int ds_hip_stack_kernel_count(const ds_hip_stack_t *S);
 const char *ds_hip_stack_kernel_name(const ds_hip_stack_t *S, int i);
 /* Per-kernel durations over n_steps eager steps, HIP events around every kernel; ms_out receives
