@@ -242,7 +242,28 @@ __device__ __forceinline__ float mv_chain(const float *s_rows, const float *s_x,
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n16 = in_dim >> 4;
   const f32x4 *x4 = (const f32x4 *)s_x;
   float dot = 0.0f;
-  if (wave == 0 && lane < nr) {
+  if (wave == 0 && lane < nr && (n16 & 3) == 0) {
+    // a ring of four register sets: each set's LDS reads go out 48 steps before its fused
+    // multiply-adds (the loads past the row's end re-read its last 16 values, unused)
+    const f32x4 *r4 = (const f32x4 *)(s_rows + (size_t)lane * (in_dim + 4));
+    f32x4 w[4][4], xv[4][4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      mv_load16(r4 + 4 * k, w[k]);
+      mv_load16(x4 + 4 * k, xv[k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < n16; i += 4) {
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        dot = mv_steps16(w[k], xv[k], dot);
+        const int nx = min(i + k + 4, n16 - 1);
+        mv_load16(r4 + 4 * nx, w[k]);
+        mv_load16(x4 + 4 * nx, xv[k]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  } else if (wave == 0 && lane < nr) {
     const f32x4 *r4 = (const f32x4 *)(s_rows + (size_t)lane * (in_dim + 4));
     f32x4 wa[4], xa[4], wb[4], xb[4];
     mv_load16(r4, wa);
