@@ -1212,8 +1212,10 @@ static hipError_t layers_full_enqueue(ds_hip_stack_t *S, hipEvent_t *ev, int *ne
 
 /* The MoE layers as one kernel each (CFG routing): layer l reads its input (the step's input or the
  * dense layer's output for l = 0, else the copies region l - 1 with its router scores) and adds
- * into region l; it also clears region l - 2, read by layer l - 2 (every region is zero at the
- * end of a step). The copy sum then writes the plain output for the LM head. */
+ * into region l; it also clears region l - 2, read by layer l - 2. The last two regions are cleared
+ * by the step's final kernel, or, where the step ends with the LM head, by the next step's first
+ * two layers and after a run's last step by tail_enqueue; so every region is zero when a step
+ * writes it. The copy sum then writes the plain output for the LM head. */
 static float *xc_region(const ds_hip_stack_t *S, int l) { return S->xc + (size_t)l * S->xc_region; }
 static int lm_keys(const ds_hip_stack_t *S);
 
