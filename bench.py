@@ -28,10 +28,10 @@ PEAK_HBM_GBS = 8000.0
 # WRITE_SIZE x 1.0); profiles/lm_head_argmax_config5_hbm.md holds the runs. Re-measure when the
 # kernel changes.
 LM_TRAFFIC_BYTES = 331387295
-# k_dec_layer<5, 8, 2>, same runs: its own 28.0 MB, 7.4 MB of the next layer's shared experts read
-# ahead by its extra blocks (in layer 11 the next step's router partials), and the router its
-# verifier blocks read
-LAYER_TRAFFIC_BYTES = 39230832
+# k_dec_layer<5, 8, 2>, same runs: its own 28.0 MB, the router its verifier blocks read, the input
+# and score copies every block reads and its atomic adds (in layer 11 also the next step's router
+# partials)
+LAYER_TRAFFIC_BYTES = 32621834
 LM_CERT_TRAFFIC_BYTES = 170807173  # the bounded head, k_lm_q8_argmax<5, 8>, same method
 
 
