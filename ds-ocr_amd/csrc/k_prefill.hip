@@ -593,7 +593,13 @@ struct pf_smem {
 
 // Limb exponent of a set of values with max |v| = mx: 2^e > mx·(1 + 2^-7), so rint(v·2^(15-e)) + 128
 // stays within 16 bits and both limbs within 8.
-__device__ __forceinline__ int pf_limb_exp(float mx) { return __builtin_amdgcn_frexp_expf(mx * 1.0078125f); }
+// A set whose max |v| is at most 2^-101 (zero, in practice: a tile of zero h) takes e = -100: its
+// limbs are zero on that grid (or within 2^-116 of its values), so it neither raises the exponent
+// a down row aligns its n-tiles to (which would cost the other tiles' low bits) nor overflows the
+// factor 2^(15-e).
+__device__ __forceinline__ int pf_limb_exp(float mx) {
+  return mx > 0x1p-101f ? __builtin_amdgcn_frexp_expf(mx * 1.0078125f) : -100;
+}
 
 // Four values to limbs: fma(v, f, 1.5·2^23 + 128) rounds v·f to the nearest integer (ties to even)
 // and leaves t = rint(v·f) + 128 in the low 16 bits of the result's bits (|t| < 2^22); two byte

@@ -375,3 +375,71 @@ def test_prefill_hidden_sizes(dev, B, mode, hidden):
         assert err < TOL
     finally:
         L.ds_hip_layer_destroy(h)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_prefill_nonfinite_tokens(dev, B, mode, path):
+    """Tokens with a +inf, a NaN or a -inf coordinate among ordinary ones. Each token's row is
+    computed on its own (the GEMM's exact int32 sums, the per-row limb exponents and sums, the
+    per-token combine), so the ordinary tokens' outputs, indices and weights must be bit-identical
+    to those of a call where the three tokens are ordinary rows, and no wait may expire. CFG: every
+    token's expert indices must be the reference's (ds_moe_top_k never selects a NaN or floor score
+    and fills empty slots with expert 0, weight 0), with NaN weights where the oracle's are NaN and
+    the others within 2 ulp."""
+    L = dev.load()
+    T, H = 20, 256
+    lay = B.make_moe_layer(67, hidden=H, inter=128, n_experts=16)
+    h = upload_layer(dev, lay)
+    try:
+        X = np.stack([B.normal_f32(H, 6700 + t) for t in range(T)])
+        out_ok, idx_ok, w_ok = gpu_prefill(dev, h, X, mode, residual=1)
+        Xb = X.copy()
+        Xb[3, 17] = np.inf
+        Xb[7, 40] = np.nan
+        Xb[11, 5] = -np.inf
+        out, idx, w = gpu_prefill(dev, h, Xb, mode, residual=1)
+        bad = {3, 7, 11}
+        for t in range(T):
+            if t in bad:
+                assert not np.isfinite(out[t]).all(), t
+                continue
+            assert np.array_equal(out[t].view(np.uint32), out_ok[t].view(np.uint32)), t
+            assert np.array_equal(idx[t], idx_ok[t]) and np.array_equal(w[t].view(np.uint32), w_ok[t].view(np.uint32)), t
+        if mode == 1:
+            ri, rw = np.empty((T, lay.top_k), np.int32), np.empty((T, lay.top_k), np.float32)
+            B.oracle().or_prefill_route(ri, rw, Xb, T, C.byref(lay.or_layer()), mode)
+            assert np.array_equal(ri, idx), [(t, ri[t], idx[t]) for t in range(T) if not np.array_equal(ri[t], idx[t])]
+            nan = np.isnan(rw)
+            assert np.array_equal(np.isnan(w), nan)
+            assert nan[list(bad)].any()
+            ulp = np.abs(rw[~nan].view(np.int32).astype(np.int64) - w[~nan].view(np.int32).astype(np.int64))
+            assert ulp.max() <= 2, int(ulp.max())
+        print(f"mode {mode}: {T - len(bad)} ordinary tokens bit-identical next to tokens with +inf, NaN, -inf")
+    finally:
+        L.ds_hip_layer_destroy(h)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_prefill_zero_h_tile(dev, B, mode, path):
+    """The gate rows of units 0-127 of every expert are zero, so each row's h is zero over its first
+    128-unit n-tile and small (x scaled by 1/64) over the others. The zero tile must not set the
+    exponent to which the down GEMM aligns the row's n-tiles (exponent 0 would shift the small
+    tiles' limbs out entirely): the output must stay within 1e-3 of the f64 brute force."""
+    L = dev.load()
+    T, H, I = 40, 256, 256
+    lay = B.make_moe_layer(71, hidden=H, inter=I, n_experts=16)
+    for blk in list(lay.gu) + [lay.sgu]:
+        blk.q[:128] = -128  # stored code -128: u = 0
+        blk.scale[:128] = 0.0
+        blk.offset[:128] = 0.0
+    h = upload_layer(dev, lay)
+    try:
+        X = np.stack([B.normal_f32(H, 7100 + t) for t in range(T)]) / 64.0
+        out, idx, w = gpu_prefill(dev, h, X, mode)
+        ref = np.empty((T, H), np.float64)
+        B.oracle().or_prefill_moe_f64(ref, X, T, C.byref(lay.or_layer()), idx, w)
+        err = rel_err(out, ref)
+        print(f"mode {mode}: zero first h tile, rel err {err:.2e}")
+        assert err < TOL, err
+    finally:
+        L.ds_hip_layer_destroy(h)
