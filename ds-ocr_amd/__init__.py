@@ -230,11 +230,14 @@ class DeviceBuffer:
 
 
 def block_from_arrays(q, scale, offset):
-    """A ds_int4_block_t borrowing numpy arrays (keep them alive while the block is used)."""
+    """A ds_int4_block_t borrowing numpy arrays (keep them alive while the block is used). Converted
+    copies (non-contiguous or other dtypes) are held by the block itself."""
     q = np.ascontiguousarray(q, dtype=np.int8)
-    return Int4Block(q.ctypes.data, np.ascontiguousarray(scale, np.float32).ctypes.data,
-                     np.ascontiguousarray(offset, np.float32).ctypes.data, q.shape[0], q.shape[1],
-                     q.size + 8 * q.shape[0])
+    s = np.ascontiguousarray(scale, np.float32)
+    o = np.ascontiguousarray(offset, np.float32)
+    b = Int4Block(q.ctypes.data, s.ctypes.data, o.ctypes.data, q.shape[0], q.shape[1], q.size + 8 * q.shape[0])
+    b._arrays = (q, s, o)
+    return b
 
 
 def block_arrays(b):

@@ -136,7 +136,8 @@ def test_config5_stack_routing_certified(dev, B, kernels, ties):
             W = planted_router(320 + l, E, H, pairs=16)
         else:
             W = (np.random.default_rng(320 + l).standard_normal((E, H)) * 0.02).astype(np.float32)
-        dev.check(L.ds_hip_layer_set_router(h, W.ctypes.data, bf16_of(B, W).ctypes.data), "router")
+        Wb = bf16_of(B, W)  # held while the library reads it (a temporary's buffer is freed at once)
+        dev.check(L.ds_hip_layer_set_router(h, W.ctypes.data, Wb.ctypes.data), "router")
         routers[l] = W
     lm = dev.DeviceBuffer(vocab * H * 2)
     dev.check(L.ds_hip_fill_normal_bf16(lm.ptr, vocab * H, 4343, 0.02), "fill")

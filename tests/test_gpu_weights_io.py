@@ -62,9 +62,8 @@ def reference_layer(dev, B, seed, router_dtype):
     lay = B.make_moe_layer(seed, hidden=H, inter=I, n_experts=E, top_k=K, n_shared=NS)
     h = upload_layer(dev, lay)
     if router_dtype == "bf16":
-        rf = (lay.router_bf16.astype(np.uint32) << 16).view(np.float32).reshape(E, H)
-        dev.check(L.ds_hip_layer_set_router(h, np.ascontiguousarray(rf).ctypes.data, lay.router_bf16.ctypes.data),
-                  "router")
+        rf = np.ascontiguousarray((lay.router_bf16.astype(np.uint32) << 16).view(np.float32).reshape(E, H))
+        dev.check(L.ds_hip_layer_set_router(h, rf.ctypes.data, lay.router_bf16.ctypes.data), "router")
     return lay, h
 
 
