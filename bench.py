@@ -389,6 +389,8 @@ def main():
     ap.add_argument("--lm-head", choices=["bounded", "one-pass"], default="bounded",
                     help="LM-head argmax: an int8 copy with exact bounds, then each block's candidate rows in bf16 "
                          "(the same tokens), or the one-pass bf16 kernel")
+    ap.add_argument("--graph-steps", type=int, default=8,
+                    help="decode steps per graph launch in the timed runs (the same results for every value)")
     ap.add_argument("--layer-kernels", type=int, choices=[1, 2], default=1,
                     help="MoE layer kernels: 1 (down split over intermediate units, per-XCD output copies) or 2 "
                          "(gate_up, then down with the combine in top-k order)")
@@ -453,6 +455,7 @@ def main():
         dev.check(L.ds_hip_stack_set_attention(S, arr_a, len(attns), fnorm.ctypes.data, 1e-6, args.decoder_step, 0),
                   "set attention")
     dev.check(L.ds_hip_stack_set_layer_kernels(S, 1 if args.layer_kernels == 1 else 0), "layer kernels")
+    dev.check(L.ds_hip_stack_set_graph_steps(S, args.graph_steps), "graph steps")
     if args.lm_head == "one-pass":
         dev.check(L.ds_hip_stack_set_lm_certified(S, 0), "one-pass LM head")
     cert = L.ds_hip_stack_lm_certified(S) == 1

@@ -89,6 +89,7 @@ SIGNATURES = {
     "ds_hip_time_prefill": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float)]),
     "ds_hip_time_layer": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.POINTER(C.c_float)]),
     "ds_hip_prefill_path": (C.c_int, [C.c_int]),
+    "ds_hip_stack_set_graph_steps": (C.c_int, [C.c_void_p, C.c_int]),
     "ds_hip_prefill_wait_error": (C.c_int, [vp, C.c_int]),
     "ds_hip_prefill_set_wait_limit": (C.c_int, [C.c_int]),
     "ds_hip_route_stats": (C.c_int, [vp, C.c_int]),

@@ -837,6 +837,10 @@ struct ds_hip_stack {
   float *ebuf;
   hipGraph_t graph;
   hipGraphExec_t exec;
+  /* runs of several steps launch a graph of gk steps at a time (step_enqueue captured gk times:
+   * every step's kernels take the step from the device counter), then the 1-step graph */
+  hipGraphExec_t exec_k;
+  int gk;
   int bound;
   /* full decoder step (ds_hip_stack_set_attention): one attention block per decoder layer */
   ds_hip_attn_t **attn;
@@ -935,6 +939,7 @@ ds_hip_stack_t *ds_hip_stack_create(ds_hip_layer_t *const *layers, int n_layers,
   S->lm = lm_head_dev;
   S->vocab = vocab;
   S->H = H;
+  S->gk = DS_HIP_GRAPH_STEPS_DEFAULT;
   S->route_mode = route_mode;
   S->bf16sim = ds_bf16_simulate_python;
   S->threads = dsr_threads();
@@ -968,6 +973,7 @@ void ds_hip_stack_destroy(ds_hip_stack_t *S) {
   if (!S) return;
   hipStreamSynchronize(dsr_stream);
   if (S->exec) hipGraphExecDestroy(S->exec);
+  if (S->exec_k) hipGraphExecDestroy(S->exec_k);
   if (S->graph) hipGraphDestroy(S->graph);
   hipFree(S->work);
   if (S->lmq_mem) hipFree(S->lmq_mem);
@@ -1553,6 +1559,26 @@ int ds_hip_stack_set_embedding(ds_hip_stack_t *S, const uint16_t *tok_embeddings
   return 0;
 }
 
+/* One graph of k steps (step_enqueue captured k times), instantiated into *out. */
+static int capture_steps(ds_hip_stack_t *S, int k, hipGraphExec_t *out) {
+  DSR_TRY(hipStreamBeginCapture(dsr_stream, hipStreamCaptureModeThreadLocal), "graph capture begin");
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < k && e == hipSuccess; i++) e = step_enqueue(S, NULL);
+  hipGraph_t g = NULL;
+  hipError_t e2 = hipStreamEndCapture(dsr_stream, &g);
+  if (e != hipSuccess || e2 != hipSuccess || !g) {
+    if (g) hipGraphDestroy(g);
+    return dsr_fail("graph capture", e != hipSuccess ? e : e2);
+  }
+  e = hipGraphInstantiate(out, g, NULL, NULL, 0);
+  hipGraphDestroy(g);
+  if (e != hipSuccess) {
+    *out = NULL;
+    return dsr_fail("graph instantiate", e);
+  }
+  return 0;
+}
+
 int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int n_rows, int *tokens_dev,
                       int n_tokens) {
   if (!S || !xs_dev || !tokens_dev || stride < 0 || n_rows < 1 || n_tokens < 1)
@@ -1563,6 +1589,10 @@ int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int n_
   if (S->exec) {
     hipGraphExecDestroy(S->exec);
     S->exec = NULL;
+  }
+  if (S->exec_k) {
+    hipGraphExecDestroy(S->exec_k);
+    S->exec_k = NULL;
   }
   if (S->graph) {
     hipGraphDestroy(S->graph);
@@ -1594,8 +1624,22 @@ int ds_hip_stack_bind(ds_hip_stack_t *S, const float *xs_dev, int stride, int n_
   if (e2 != hipSuccess) return dsr_fail("graph capture end", e2);
   S->graph = g;
   DSR_TRY(hipGraphInstantiate(&S->exec, g, NULL, NULL, 0), "graph instantiate");
+  if (S->gk > 1 && capture_steps(S, S->gk, &S->exec_k)) return -1;
   S->bound = 1;
   return ds_hip_stack_reset(S);
+}
+
+int ds_hip_stack_set_graph_steps(ds_hip_stack_t *S, int k) {
+  if (!S || k < 1 || k > DS_HIP_GRAPH_STEPS_MAX)
+    return dsr_failf("ds_hip_stack_set_graph_steps: steps per graph must be 1..%d", DS_HIP_GRAPH_STEPS_MAX);
+  if (k == S->gk) return 0;
+  DSR_TRY(hipStreamSynchronize(dsr_stream), "graph steps"); /* a launch of the old graph may still run */
+  if (S->exec_k) {
+    hipGraphExecDestroy(S->exec_k);
+    S->exec_k = NULL;
+  }
+  S->gk = k;
+  return S->bound && k > 1 ? capture_steps(S, k, &S->exec_k) : 0;
 }
 
 int ds_hip_stack_capacity(const ds_hip_stack_t *S) { return S && S->bound ? S->cap : 0; }
@@ -1635,7 +1679,12 @@ static hipError_t tail_enqueue(ds_hip_stack_t *S) {
 }
 
 static int graph_steps(ds_hip_stack_t *S, int n_steps) {
-  for (int i = 0; i < n_steps; i++) {
+  int i = 0;
+  for (; S->exec_k && i + S->gk <= n_steps; i += S->gk) {
+    DSR_TRY(hipGraphLaunch(S->exec_k, dsr_stream), "graph launch");
+    S->done += S->gk;
+  }
+  for (; i < n_steps; i++) {
     DSR_TRY(hipGraphLaunch(S->exec, dsr_stream), "graph launch");
     S->done++;
   }

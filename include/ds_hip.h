@@ -268,6 +268,15 @@ int ds_hip_stack_set_sampling(ds_hip_stack_t *S, float repeat_penalty, int no_re
 int ds_hip_lm_head_sample(const float *x_dev, const uint16_t *lm_head_dev, int hidden, int vocab, const int *history_dev,
                           int history_len, float repeat_penalty, int no_repeat_ngram_size, int *token_dev);
 
+/* Steps per graph launch in ds_hip_stack_run and the timed runs (no counterpart in the reference; a
+ * launch setting): runs of several steps launch a graph of k steps at a time (the step's kernels
+ * captured k times; each step takes its index from the device step counter), then 1-step graphs
+ * for the rest. Results are the same for every k. Any time; 1..DS_HIP_GRAPH_STEPS_MAX. */
+#define DS_HIP_GRAPH_STEPS_MAX 16
+#define DS_HIP_GRAPH_STEPS_DEFAULT 8
+int ds_hip_stack_set_graph_steps(ds_hip_stack_t *S, int k);
+
+
 /* Makes each step a whole decoder step (ds_decoder_forward for one token, ds_moe_decoder.c:339-474
  * and :1000): attn[i] is decoder layer i's attention half (the dense layer's first when one is set,
  * then one per MoE layer; call after ds_hip_stack_set_dense), each followed by its MLP on the

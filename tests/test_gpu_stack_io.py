@@ -288,3 +288,60 @@ def test_step_ending_at_the_lm_head_across_runs(dev, B):
     finally:
         for h in hs:
             L.ds_hip_layer_destroy(h)
+
+
+@pytest.mark.parametrize("mode,kernels,feed", [(1, 1, False), (1, 2, False), (0, 1, False), (1, 1, True)])
+def test_steps_per_graph_launch(dev, B, mode, kernels, feed):
+    """Runs of several steps launch a graph of k steps at a time, then 1-step graphs: 11 steps with
+    k = 1 and with k = 4 (two 4-step launches and three single ones, and again through the timed
+    run) give the same tokens, and the same last hidden state (bit for bit with the two-kernel
+    layers; within the one-kernel layers' float-atomic order otherwise). Three layers, so the bound
+    input's steps end at the LM head (the last layer's extra blocks and the token of the next step's
+    first layer), and the embedding feed (each step's input from the token before)."""
+    L = dev.load()
+    H, vocab, n = 256, 3000, 11
+    lays, hs, lm_w = small_stack(dev, B, 540, n_layers=3)
+    lm = dev.DeviceBuffer.from_array(lm_w)
+    xs = np.stack([B.normal_f32(H, 5400 + s) for s in range(n)])
+    xd = dev.DeviceBuffer.from_array(xs)
+    emb = B.normal_bf16(vocab * H, 541, 0.5).reshape(vocab, H)
+    ed = dev.DeviceBuffer.from_array(emb)
+    td = dev.DeviceBuffer(4 * n)
+    arr = (C.c_void_p * len(hs))(*hs)
+    S = L.ds_hip_stack_create(arr, len(hs), lm.ptr, vocab, mode)
+    assert S, L.ds_hip_last_error()
+    try:
+        assert L.ds_hip_stack_set_graph_steps(S, 0) == -1 and L.ds_hip_stack_set_graph_steps(S, 17) == -1
+        dev.check(L.ds_hip_stack_set_layer_kernels(S, 1 if kernels == 1 else 0), "kernels")
+        if feed:
+            dev.check(L.ds_hip_stack_set_embedding(S, ed.ptr, vocab), "embedding")
+        dev.check(L.ds_hip_stack_bind(S, xd.ptr, H, 1 if feed else n, td.ptr, n), "bind")
+        runs = []
+        for k, timed in [(1, False), (4, False), (4, True), (1, True)]:
+            dev.check(L.ds_hip_stack_set_graph_steps(S, k), "graph steps")
+            dev.check(L.ds_hip_stack_reset(S), "reset")
+            td.write(np.full(n, -1, np.int32))
+            if timed:
+                ms = C.c_float(0)
+                dev.check(L.ds_hip_time_stack(S, n, C.byref(ms)), "timed run")
+            else:
+                dev.check(L.ds_hip_stack_run(S, n), "run")
+            hx = np.empty(H, np.float32)
+            dev.check(L.ds_hip_stack_hidden(S, hx), "hidden")
+            runs.append((k, timed, td.to_array(np.int32), hx))
+            assert L.ds_hip_stack_steps_left(S) == 0
+        k0, _, t0, h0 = runs[0]
+        assert (t0 >= 0).all() and (t0 < vocab).all()
+        for k, timed, t, hx in runs[1:]:
+            err = rel_err(hx, h0)
+            print(f"mode {mode} kernels {kernels} feed {feed}: k={k} timed={timed} tokens equal "
+                  f"{int((t == t0).sum())}/{n}, hidden err {err:.2e}")
+            assert np.array_equal(t, t0)
+            if kernels == 2:
+                assert np.array_equal(hx.view(np.uint32), h0.view(np.uint32))
+            else:
+                assert err < 1e-5
+    finally:
+        L.ds_hip_stack_destroy(S)
+        for h in hs:
+            L.ds_hip_layer_destroy(h)
